@@ -1,0 +1,198 @@
+/*
+ * relm_mp.h - C ABI of the MI355X (gfx950) relational message-passing library
+ * (librelm_mp_hip.so).
+ *
+ * Plain pointers, sizes and a HIP stream handle; no torch types.  All device
+ * pointers are HIP device memory on the device that is current on the calling
+ * thread.  Every entry point enqueues its kernels on `stream` (a hipStream_t
+ * passed as void*).  Entry points that build an index plan validate every
+ * index, and therefore synchronise `stream` once to read the validation status
+ * back; the compute-only entry points (relm_mp_plan_*) never synchronise.
+ *
+ * Return value: RELM_MP_OK (0) or one of the RELM_MP_ERR_* codes.  On error,
+ * relm_mp_last_error() returns a thread-local message that matches the
+ * reference library's wording where the reference defines one.
+ *
+ * Reference interface replaced (maichmueller/relmo, src/_ops/mp/mp_ops.cpp):
+ *   relm_mp_fanout_scatter                 <- relm::mp::fanout_scatter            mp_ops.cpp:3038-3101
+ *   relm_mp_fanout_scatter_backward        <- relm::mp::fanout_scatter_backward   mp_ops.cpp:3103-3166
+ *   relm_mp_fanin_reduce                   <- relm::mp::fanin_reduce (mode 0/1)   mp_ops.cpp:3327-3348,
+ *                                             fanin_reduce_sum 3168-3222, fanin_reduce_logsumexp 3005-3036
+ *   relm_mp_fanin_reduce_sum_backward      <- relm::mp::fanin_reduce_sum_backward mp_ops.cpp:3224-3284
+ *   relm_mp_fanin_reduce_logsumexp_backward<- relm::mp::fanin_reduce_logsumexp_backward mp_ops.cpp:3286-3325
+ *   relm_mp_build_info                     <- relm::mp::build_info                mp_ops.cpp:3745-3750
+ * The reference binds these through TORCH_LIBRARY(relm_mp) (mp_ops.cpp:3754-3838);
+ * this library's torch binding (relm_mp_ops.so) registers the same schemas
+ * and calls the functions below.
+ *
+ * Index plans (relm_mp_inv_plan_*, relm_mp_csr_plan_*, relm_mp_plan_*) have no
+ * counterpart in the reference: they expose the index preprocessing that the
+ * op-level entry points perform internally, so that a caller can build a plan
+ * once and reuse it while the index tensors stay unchanged.
+ */
+#ifndef RELM_MP_H
+#define RELM_MP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* relm_mp_stream_t; /* hipStream_t */
+
+enum relm_mp_status {
+    RELM_MP_OK = 0,
+    RELM_MP_ERR_INVALID_ARGUMENT = 1, /* negative size, size limit, mode */
+    RELM_MP_ERR_INDEX_OUT_OF_BOUNDS = 2,
+    RELM_MP_ERR_UNSUPPORTED_MODE = 3,
+    RELM_MP_ERR_WORKSPACE = 4, /* workspace missing or too small */
+    RELM_MP_ERR_HIP = 5        /* HIP runtime / launch error */
+};
+
+enum relm_mp_dtype { RELM_MP_F32 = 0, RELM_MP_F64 = 1 };
+
+enum relm_mp_mode { RELM_MP_MODE_SUM = 0, RELM_MP_MODE_LOGSUMEXP = 1 };
+
+/* Sizes accepted by the HIP path: every row count and edge count must be
+ * below 2^31 - 1 (indices are narrowed to int32 inside plans). */
+#define RELM_MP_MAX_ROWS 2147483646LL
+
+const char* relm_mp_last_error(void);
+/* "build_torch=...;build_cuda_tag=cpu;..." is produced by the torch binding;
+ * this returns the HIP-side part: "hip=<ver>;arch=gfx950;kernels=..." */
+const char* relm_mp_build_info(void);
+
+/* ------------------------------------------------------------------------ */
+/* Op-level entry points (one per reference op).  `workspace` is device      */
+/* memory of at least *_workspace_size(...) bytes, 256-byte aligned.  The    */
+/* output buffer is fully written (rows without messages become 0, or -inf   */
+/* for the logsumexp forward); the caller need not clear it.                 */
+/* ------------------------------------------------------------------------ */
+
+/* out[out_rows, emb]: out[flat_dst[e]] = x_cat[src_global_idx[e]], the last
+ * edge (largest e) wins on duplicate flat_dst, untouched rows are zero. */
+size_t relm_mp_fanout_scatter_workspace_size(int64_t num_edges, int64_t out_rows);
+int relm_mp_fanout_scatter(int dtype, const void* x_cat, int64_t x_rows, int64_t emb,
+                           const int64_t* src_global_idx, const int64_t* flat_dst,
+                           int64_t num_edges, int64_t out_rows, void* out,
+                           void* workspace, size_t workspace_bytes, relm_mp_stream_t stream);
+
+/* grad_x[x_rows, emb]: grad_x[src_global_idx[e]] += grad_out[flat_dst[e]]. */
+size_t relm_mp_fanout_scatter_backward_workspace_size(int64_t num_edges, int64_t x_rows,
+                                                      int64_t emb, int dtype);
+int relm_mp_fanout_scatter_backward(int dtype, const void* grad_out, int64_t grad_out_rows,
+                                    int64_t emb, const int64_t* src_global_idx,
+                                    const int64_t* flat_dst, int64_t num_edges, int64_t x_rows,
+                                    void* grad_x, void* workspace, size_t workspace_bytes,
+                                    relm_mp_stream_t stream);
+
+/* out[dim_size, emb]: mode 0: out[dst_idx[e]] += rel_flat[flat_src[e]];
+ * mode 1: out[d] = log(sum exp(rel - max)) + max over the messages of d,
+ * -inf for d without messages. */
+size_t relm_mp_fanin_reduce_workspace_size(int64_t num_edges, int64_t dim_size, int64_t emb,
+                                           int dtype);
+int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int64_t emb,
+                         const int64_t* flat_src, const int64_t* dst_idx, int64_t num_edges,
+                         int64_t dim_size, int64_t mode, void* out, void* workspace,
+                         size_t workspace_bytes, relm_mp_stream_t stream);
+
+/* grad_rel[rel_rows, emb]: grad_rel[flat_src[e]] += grad_out[dst_idx[e]]. */
+size_t relm_mp_fanin_reduce_sum_backward_workspace_size(int64_t num_edges, int64_t rel_rows,
+                                                        int64_t emb, int dtype);
+int relm_mp_fanin_reduce_sum_backward(int dtype, const void* grad_out, int64_t grad_out_rows,
+                                      int64_t emb, const int64_t* flat_src,
+                                      const int64_t* dst_idx, int64_t num_edges,
+                                      int64_t rel_rows, void* grad_rel, void* workspace,
+                                      size_t workspace_bytes, relm_mp_stream_t stream);
+
+/* grad_rel[rel_rows, emb]:
+ * grad_rel[flat_src[e]] += grad_out[d] * exp(rel_flat[flat_src[e]] - out[d]), d = dst_idx[e]. */
+size_t relm_mp_fanin_reduce_logsumexp_backward_workspace_size(int64_t num_edges, int64_t rel_rows,
+                                                              int64_t emb, int dtype);
+int relm_mp_fanin_reduce_logsumexp_backward(int dtype, const void* grad_out, int64_t dim_size,
+                                            int64_t emb, const void* rel_flat,
+                                            int64_t rel_flat_rows, const int64_t* flat_src,
+                                            const int64_t* dst_idx, int64_t num_edges,
+                                            const void* out, int64_t rel_rows, void* grad_rel,
+                                            void* workspace, size_t workspace_bytes,
+                                            relm_mp_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Index plans (no reference counterpart).                                   */
+/* ------------------------------------------------------------------------ */
+
+enum relm_mp_plan_kind { RELM_MP_PLAN_INVERSE = 1, RELM_MP_PLAN_CSR = 2 };
+
+/* Descriptor of a plan.  All pointers point into the caller's plan memory. */
+typedef struct relm_mp_plan {
+    int32_t kind;
+    int32_t hub_threshold;   /* CSR: segments longer than this use the hub path */
+    int32_t chunk_size;      /* CSR: edges per hub chunk                        */
+    int32_t reserved;
+    int64_t num_keys;        /* rows on the scatter (keyed) side               */
+    int64_t num_edges;
+    int64_t num_gather;      /* rows on the gathered side                      */
+    int64_t collisions;      /* inverse: edges whose key another edge also has */
+    int64_t max_degree;      /* CSR: longest segment                           */
+    int64_t num_hubs;        /* CSR: segments longer than hub_threshold        */
+    int64_t num_chunks;      /* CSR: hub chunks                                */
+    int32_t* inv;            /* inverse: [num_keys] largest edge id per key or -1 */
+    int32_t* offsets;        /* CSR: [num_keys + 1] segment offsets            */
+    int32_t* gather_sorted;  /* CSR: [num_edges] gathered row per edge, stable key order */
+    int32_t* keys_sorted;    /* CSR: [num_edges] key per edge, stable key order */
+    int32_t* hub_key;        /* CSR: [num_hubs] key of each hub                */
+    int32_t* hub_chunk_base; /* CSR: [num_hubs] first chunk of each hub        */
+    int32_t* chunk_hub;      /* CSR: [num_chunks] hub of each chunk            */
+} relm_mp_plan;
+
+/* Inverse plan: inv[k] = largest e with keys[e] == k, or -1.  Validates keys
+ * against key_bound and gathers (if non-NULL) against gather_bound; the first
+ * edge (in edge order) with a bad index is reported, `gather_checked_first`
+ * choosing which array the reference checks first within one edge.
+ * Synchronises `stream` once. */
+size_t relm_mp_inv_plan_bytes(int64_t num_keys);
+int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
+                           const int64_t* gathers, int64_t gather_bound, const char* gather_name,
+                           int gather_checked_first, int64_t num_edges, void* plan_mem,
+                           size_t plan_bytes, relm_mp_plan* plan, relm_mp_stream_t stream);
+
+/* CSR plan: stable counting order of the edges by key (edge order kept inside
+ * each segment), offsets, the gathered row of every edge in that order, and the
+ * list of hub segments.  Synchronises `stream` once. */
+size_t relm_mp_csr_plan_bytes(int64_t num_keys, int64_t num_edges);
+size_t relm_mp_csr_plan_scratch_bytes(int64_t num_keys, int64_t num_edges);
+int relm_mp_csr_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
+                           const int64_t* gathers, int64_t gather_bound, const char* gather_name,
+                           int gather_checked_first, int64_t num_edges, void* plan_mem,
+                           size_t plan_bytes, void* scratch, size_t scratch_bytes,
+                           relm_mp_plan* plan, relm_mp_stream_t stream);
+
+/* Scratch needed by the compute entry points below for hub partial results
+ * of a CSR plan (0 for inverse plans). */
+size_t relm_mp_plan_compute_scratch_bytes(const relm_mp_plan* plan, int64_t emb, int dtype,
+                                          int64_t mode);
+
+/* out[num_keys, emb] = per key: inverse plan -> table[gathers[inv[k]]] or 0;
+ * CSR plan -> last edge of the segment (fanout "last wins") or 0. */
+int relm_mp_plan_gather_last(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                             const void* table, int64_t emb, void* out,
+                             relm_mp_stream_t stream);
+/* out[num_keys, emb] = per key, sum over the segment of table[gathered row]
+ * (inverse plans require collisions == 0), or logsumexp (mode 1, CSR plans). */
+int relm_mp_plan_segment_reduce(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                                const void* table, int64_t emb, int64_t mode, void* out,
+                                void* scratch, size_t scratch_bytes, relm_mp_stream_t stream);
+/* grad_rel[num_keys, emb] = per key r, sum over its edges of
+ * grad_out[d] * exp(rel_flat[r] - out[d]) with d the gathered row. */
+int relm_mp_plan_logsumexp_backward(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                                    const void* grad_out, const void* out, const void* rel_flat,
+                                    int64_t emb, void* grad_rel, void* scratch,
+                                    size_t scratch_bytes, relm_mp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RELM_MP_H */

@@ -1,0 +1,113 @@
+"""Runs relmo's own CPU op library (``oracle/_ref/relm_mp_ops_ref.so``, built by
+``make -C oracle ref`` from the reference's ``src/_ops/mp/mp_ops.cpp``) in a
+child process.
+
+TEST INFRASTRUCTURE ONLY (golden fixtures, oracle pinning, bench.py's
+``cpu_baseline``).  The reference library registers the same
+``torch.ops.relm_mp`` namespace as the product library, so it always runs in
+its own process.  Arrays travel as ``.npz`` (no pickle), parameters as JSON.
+
+Parent side:  ``run_reference(calls, arrays)``
+Child side:   ``python oracle/ref_runner.py <request_dir>``
+"""
+
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+REF_LIB = HERE / "_ref" / "relm_mp_ops_ref.so"
+
+OPS = {
+    "fanout_scatter": 3,
+    "fanout_scatter_backward": 3,
+    "fanin_reduce": 3,
+    "fanin_reduce_sum_backward": 3,
+    "fanin_reduce_logsumexp_backward": 5,
+}
+
+
+def available() -> bool:
+    return REF_LIB.exists()
+
+
+def run_reference(calls: list[dict], arrays: dict[str, np.ndarray], timeout: float = 600.0) -> list[dict]:
+    """Each call: {"op", "tensors": [names], "ints": [...], optional "repeat",
+    "warmup", "threads"}.  Returns per call {"out": ndarray} or {"error": str},
+    plus "times" (seconds per repetition) when "repeat" is given."""
+
+    if not available():
+        raise FileNotFoundError(f"{REF_LIB} is missing; run `make -C oracle ref` where the reference is present")
+    with tempfile.TemporaryDirectory(prefix="relm_ref_") as tmp:
+        tmpd = Path(tmp)
+        np.savez(tmpd / "inputs.npz", **arrays)
+        (tmpd / "request.json").write_text(json.dumps(calls))
+        proc = subprocess.run(
+            [sys.executable, str(Path(__file__).resolve()), str(tmpd)],
+            capture_output=True, text=True, timeout=timeout,
+        )
+        if proc.returncode != 0:
+            raise RuntimeError(f"reference runner failed:\n{proc.stdout}\n{proc.stderr}")
+        meta = json.loads((tmpd / "result.json").read_text())
+        outs = np.load(tmpd / "outputs.npz", allow_pickle=False)
+        results = []
+        for i, m in enumerate(meta):
+            r = dict(m)
+            if f"out_{i}" in outs.files:
+                r["out"] = outs[f"out_{i}"]
+            results.append(r)
+        return results
+
+
+def _child(req_dir: Path) -> None:
+    import torch
+
+    torch.ops.load_library(str(REF_LIB))
+    ns = torch.ops.relm_mp
+    calls = json.loads((req_dir / "request.json").read_text())
+    arrays = np.load(req_dir / "inputs.npz", allow_pickle=False)
+    outputs: dict[str, np.ndarray] = {}
+    meta: list[dict] = []
+    for i, call in enumerate(calls):
+        op = call["op"]
+        if op not in OPS:
+            raise ValueError(f"unknown op {op}")
+        tensors = [torch.from_numpy(np.array(arrays[name])) for name in call["tensors"]]
+        ints = [int(v) for v in call.get("ints", [])]
+        threads = call.get("threads")
+        if threads:
+            torch.set_num_threads(int(threads))
+        entry: dict = {"op": op, "threads": torch.get_num_threads()}
+        fn = getattr(ns, op)
+        try:
+            out = fn(*tensors, *ints)
+        except Exception as exc:  # the reference's error is part of the result
+            entry["error"] = str(exc).splitlines()[0]
+            entry["error_type"] = type(exc).__name__
+            meta.append(entry)
+            continue
+        outputs[f"out_{i}"] = out.numpy()
+        repeat = int(call.get("repeat", 0))
+        if repeat:
+            for _ in range(int(call.get("warmup", 1))):
+                fn(*tensors, *ints)
+            times = []
+            for _ in range(repeat):
+                t0 = time.perf_counter()
+                fn(*tensors, *ints)
+                times.append(time.perf_counter() - t0)
+            entry["times"] = times
+        meta.append(entry)
+    np.savez(req_dir / "outputs.npz", **outputs)
+    (req_dir / "result.json").write_text(json.dumps(meta))
+
+
+if __name__ == "__main__":
+    _child(Path(sys.argv[1]))

@@ -1,0 +1,10 @@
+"""MI355X (gfx950) implementation of relmo's relational message-passing ops.
+
+``relmo_amd.mp`` mirrors ``relmo.ops.mp`` for ``fanout_scatter`` and
+``fanin_reduce``; the ops run on hand-written HIP kernels through
+``relm_mp_ops.so`` (torch binding) and ``librelm_mp_hip.so`` (C ABI).
+"""
+
+from . import mp
+
+__all__ = ["mp"]

@@ -1,0 +1,369 @@
+"""ctypes binding of ``librelm_mp_hip.so`` (declared in ``include/relm_mp.h``).
+
+Tensors are passed as raw device pointers; outputs and workspaces are
+allocated with torch on the tensors' device and every call is enqueued on
+torch's current stream.  torch is imported before the library is opened so
+that the process uses torch's HIP runtime (both carry the soname
+``libamdhip64.so.7``; loading ours first would map a second runtime).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "librelm_mp_hip.so"
+
+OK = 0
+ERR_INVALID_ARGUMENT = 1
+ERR_INDEX_OUT_OF_BOUNDS = 2
+ERR_UNSUPPORTED_MODE = 3
+ERR_WORKSPACE = 4
+ERR_HIP = 5
+
+F32 = 0
+F64 = 1
+PLAN_INVERSE = 1
+PLAN_CSR = 2
+
+EXPORTED_SYMBOLS = (
+    "relm_mp_last_error",
+    "relm_mp_build_info",
+    "relm_mp_fanout_scatter_workspace_size",
+    "relm_mp_fanout_scatter",
+    "relm_mp_fanout_scatter_backward_workspace_size",
+    "relm_mp_fanout_scatter_backward",
+    "relm_mp_fanin_reduce_workspace_size",
+    "relm_mp_fanin_reduce",
+    "relm_mp_fanin_reduce_sum_backward_workspace_size",
+    "relm_mp_fanin_reduce_sum_backward",
+    "relm_mp_fanin_reduce_logsumexp_backward_workspace_size",
+    "relm_mp_fanin_reduce_logsumexp_backward",
+    "relm_mp_inv_plan_bytes",
+    "relm_mp_inv_plan_build",
+    "relm_mp_csr_plan_bytes",
+    "relm_mp_csr_plan_scratch_bytes",
+    "relm_mp_csr_plan_build",
+    "relm_mp_plan_compute_scratch_bytes",
+    "relm_mp_plan_gather_last",
+    "relm_mp_plan_segment_reduce",
+    "relm_mp_plan_logsumexp_backward",
+)
+
+
+class Plan(ctypes.Structure):
+    """Mirror of ``struct relm_mp_plan``."""
+
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("hub_threshold", ctypes.c_int32),
+        ("chunk_size", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("num_keys", ctypes.c_int64),
+        ("num_edges", ctypes.c_int64),
+        ("num_gather", ctypes.c_int64),
+        ("collisions", ctypes.c_int64),
+        ("max_degree", ctypes.c_int64),
+        ("num_hubs", ctypes.c_int64),
+        ("num_chunks", ctypes.c_int64),
+        ("inv", ctypes.c_void_p),
+        ("offsets", ctypes.c_void_p),
+        ("gather_sorted", ctypes.c_void_p),
+        ("keys_sorted", ctypes.c_void_p),
+        ("hub_key", ctypes.c_void_p),
+        ("hub_chunk_base", ctypes.c_void_p),
+        ("chunk_hub", ctypes.c_void_p),
+    ]
+
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+_vp = ctypes.c_void_p
+_cp = ctypes.c_char_p
+_PP = ctypes.POINTER(Plan)
+
+_SIGNATURES = {
+    "relm_mp_last_error": (_cp, []),
+    "relm_mp_build_info": (_cp, []),
+    "relm_mp_fanout_scatter_workspace_size": (_sz, [_i64, _i64]),
+    "relm_mp_fanout_scatter": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_fanout_scatter_backward_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
+    "relm_mp_fanout_scatter_backward": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_fanin_reduce_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
+    "relm_mp_fanin_reduce": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_fanin_reduce_sum_backward_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
+    "relm_mp_fanin_reduce_sum_backward": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_fanin_reduce_logsumexp_backward_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
+    "relm_mp_fanin_reduce_logsumexp_backward": (
+        _int,
+        [_int, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _sz, _vp],
+    ),
+    "relm_mp_inv_plan_bytes": (_sz, [_i64]),
+    "relm_mp_inv_plan_build": (_int, [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _PP, _vp]),
+    "relm_mp_csr_plan_bytes": (_sz, [_i64, _i64]),
+    "relm_mp_csr_plan_scratch_bytes": (_sz, [_i64, _i64]),
+    "relm_mp_csr_plan_build": (
+        _int,
+        [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _vp, _sz, _PP, _vp],
+    ),
+    "relm_mp_plan_compute_scratch_bytes": (_sz, [_PP, _i64, _int, _i64]),
+    "relm_mp_plan_gather_last": (_int, [_int, _PP, _vp, _vp, _i64, _vp, _vp]),
+    "relm_mp_plan_segment_reduce": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_plan_logsumexp_backward": (_int, [_int, _PP, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Open the library once and declare every signature."""
+
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing; build it with `python -m relmo_amd.csrc.build`."
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = handle
+    return _LIB
+
+
+def last_error() -> str:
+    return lib().relm_mp_last_error().decode()
+
+
+def build_info() -> str:
+    return lib().relm_mp_build_info().decode()
+
+
+def check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = last_error()
+    if rc == ERR_UNSUPPORTED_MODE:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def _dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.float64:
+        return F64
+    raise TypeError(f"relm_mp C ABI supports float32 / float64, got {t.dtype}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    assert t.is_contiguous(), "C ABI tensors must be contiguous"
+    return t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _bytes(n: int, like: torch.Tensor) -> torch.Tensor:
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=like.device)
+
+
+def _check_index(t: torch.Tensor) -> None:
+    assert t.dtype == torch.int64 and t.dim() == 1 and t.is_contiguous()
+
+
+# ---- op-level entry points ----------------------------------------------------
+
+
+def fanout_scatter(x_cat: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, out_rows: int) -> torch.Tensor:
+    _check_index(src)
+    _check_index(dst)
+    emb = x_cat.size(1)
+    out = torch.empty(out_rows, emb, dtype=x_cat.dtype, device=x_cat.device)
+    ws_n = lib().relm_mp_fanout_scatter_workspace_size(src.numel(), out_rows)
+    ws = _bytes(ws_n, x_cat)
+    check(
+        lib().relm_mp_fanout_scatter(
+            _dtype(x_cat), _ptr(x_cat), x_cat.size(0), emb, _ptr(src), _ptr(dst), src.numel(),
+            out_rows, _ptr(out), _ptr(ws), ws.numel(), _stream(x_cat),
+        )
+    )
+    return out
+
+
+def fanout_scatter_backward(grad_out: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, x_rows: int) -> torch.Tensor:
+    _check_index(src)
+    _check_index(dst)
+    emb = grad_out.size(1)
+    grad_x = torch.empty(x_rows, emb, dtype=grad_out.dtype, device=grad_out.device)
+    ws_n = lib().relm_mp_fanout_scatter_backward_workspace_size(src.numel(), x_rows, emb, _dtype(grad_out))
+    ws = _bytes(ws_n, grad_out)
+    check(
+        lib().relm_mp_fanout_scatter_backward(
+            _dtype(grad_out), _ptr(grad_out), grad_out.size(0), emb, _ptr(src), _ptr(dst),
+            src.numel(), x_rows, _ptr(grad_x), _ptr(ws), ws.numel(), _stream(grad_out),
+        )
+    )
+    return grad_x
+
+
+def fanin_reduce(rel_flat: torch.Tensor, flat_src: torch.Tensor, dst_idx: torch.Tensor, dim_size: int, mode: int) -> torch.Tensor:
+    _check_index(flat_src)
+    _check_index(dst_idx)
+    emb = rel_flat.size(1)
+    out = torch.empty(dim_size, emb, dtype=rel_flat.dtype, device=rel_flat.device)
+    ws_n = lib().relm_mp_fanin_reduce_workspace_size(flat_src.numel(), dim_size, emb, _dtype(rel_flat))
+    ws = _bytes(ws_n, rel_flat)
+    check(
+        lib().relm_mp_fanin_reduce(
+            _dtype(rel_flat), _ptr(rel_flat), rel_flat.size(0), emb, _ptr(flat_src), _ptr(dst_idx),
+            flat_src.numel(), dim_size, mode, _ptr(out), _ptr(ws), ws.numel(), _stream(rel_flat),
+        )
+    )
+    return out
+
+
+def fanin_reduce_sum_backward(grad_out: torch.Tensor, flat_src: torch.Tensor, dst_idx: torch.Tensor, rel_rows: int) -> torch.Tensor:
+    _check_index(flat_src)
+    _check_index(dst_idx)
+    emb = grad_out.size(1)
+    grad_rel = torch.empty(rel_rows, emb, dtype=grad_out.dtype, device=grad_out.device)
+    ws_n = lib().relm_mp_fanin_reduce_sum_backward_workspace_size(flat_src.numel(), rel_rows, emb, _dtype(grad_out))
+    ws = _bytes(ws_n, grad_out)
+    check(
+        lib().relm_mp_fanin_reduce_sum_backward(
+            _dtype(grad_out), _ptr(grad_out), grad_out.size(0), emb, _ptr(flat_src), _ptr(dst_idx),
+            flat_src.numel(), rel_rows, _ptr(grad_rel), _ptr(ws), ws.numel(), _stream(grad_out),
+        )
+    )
+    return grad_rel
+
+
+def fanin_reduce_logsumexp_backward(
+    grad_out: torch.Tensor,
+    rel_flat: torch.Tensor,
+    flat_src: torch.Tensor,
+    dst_idx: torch.Tensor,
+    out: torch.Tensor,
+    rel_rows: int,
+) -> torch.Tensor:
+    _check_index(flat_src)
+    _check_index(dst_idx)
+    emb = grad_out.size(1)
+    grad_rel = torch.empty(rel_rows, emb, dtype=rel_flat.dtype, device=rel_flat.device)
+    ws_n = lib().relm_mp_fanin_reduce_logsumexp_backward_workspace_size(
+        flat_src.numel(), rel_rows, emb, _dtype(rel_flat)
+    )
+    ws = _bytes(ws_n, rel_flat)
+    check(
+        lib().relm_mp_fanin_reduce_logsumexp_backward(
+            _dtype(rel_flat), _ptr(grad_out), grad_out.size(0), emb, _ptr(rel_flat), rel_flat.size(0),
+            _ptr(flat_src), _ptr(dst_idx), flat_src.numel(), _ptr(out), rel_rows, _ptr(grad_rel),
+            _ptr(ws), ws.numel(), _stream(rel_flat),
+        )
+    )
+    return grad_rel
+
+
+# ---- plans -------------------------------------------------------------------------
+
+
+class BuiltPlan:
+    """A plan descriptor together with the device memory it points into."""
+
+    def __init__(self, plan: Plan, mem: torch.Tensor):
+        self.plan = plan
+        self.mem = mem
+
+    def _i32(self, ptr: int, n: int) -> torch.Tensor:
+        """View of ``n`` int32 values of the plan memory starting at ``ptr``."""
+
+        base = self.mem.data_ptr()
+        off = int(ptr) - base
+        assert 0 <= off and off + 4 * n <= self.mem.numel(), "pointer outside plan memory"
+        return self.mem[off : off + 4 * n].view(torch.int32)
+
+    @property
+    def inv(self) -> torch.Tensor:
+        return self._i32(self.plan.inv, self.plan.num_keys)
+
+    @property
+    def offsets(self) -> torch.Tensor:
+        return self._i32(self.plan.offsets, self.plan.num_keys + 1)
+
+    @property
+    def gather_sorted(self) -> torch.Tensor:
+        return self._i32(self.plan.gather_sorted, self.plan.num_edges)
+
+    @property
+    def keys_sorted(self) -> torch.Tensor:
+        return self._i32(self.plan.keys_sorted, self.plan.num_edges)
+
+
+def inv_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, gather_bound: int,
+             key_name: str = "key", gather_name: str = "gather", gather_first: bool = False) -> BuiltPlan:
+    _check_index(keys)
+    mem = _bytes(lib().relm_mp_inv_plan_bytes(key_bound), keys)
+    plan = Plan()
+    check(
+        lib().relm_mp_inv_plan_build(
+            _ptr(keys), key_bound, key_name.encode(), _ptr(gathers), gather_bound,
+            gather_name.encode(), int(gather_first), keys.numel(), _ptr(mem), mem.numel(),
+            ctypes.byref(plan), _stream(keys),
+        )
+    )
+    return BuiltPlan(plan, mem)
+
+
+def csr_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, gather_bound: int,
+             key_name: str = "key", gather_name: str = "gather", gather_first: bool = False) -> BuiltPlan:
+    _check_index(keys)
+    n = keys.numel()
+    mem = _bytes(lib().relm_mp_csr_plan_bytes(key_bound, n), keys)
+    scratch = _bytes(lib().relm_mp_csr_plan_scratch_bytes(key_bound, n), keys)
+    plan = Plan()
+    check(
+        lib().relm_mp_csr_plan_build(
+            _ptr(keys), key_bound, key_name.encode(), _ptr(gathers), gather_bound,
+            gather_name.encode(), int(gather_first), n, _ptr(mem), mem.numel(), _ptr(scratch),
+            scratch.numel(), ctypes.byref(plan), _stream(keys),
+        )
+    )
+    return BuiltPlan(plan, mem)
+
+
+def plan_segment_reduce(bp: BuiltPlan, table: torch.Tensor, mode: int, gathers: torch.Tensor | None = None) -> torch.Tensor:
+    emb = table.size(1)
+    out = torch.empty(bp.plan.num_keys, emb, dtype=table.dtype, device=table.device)
+    n = lib().relm_mp_plan_compute_scratch_bytes(ctypes.byref(bp.plan), emb, _dtype(table), mode)
+    scratch = _bytes(n, table)
+    check(
+        lib().relm_mp_plan_segment_reduce(
+            _dtype(table), ctypes.byref(bp.plan), _ptr(gathers), _ptr(table), emb, mode, _ptr(out),
+            _ptr(scratch), scratch.numel(), _stream(table),
+        )
+    )
+    return out
+
+
+def plan_gather_last(bp: BuiltPlan, table: torch.Tensor, gathers: torch.Tensor | None = None) -> torch.Tensor:
+    emb = table.size(1)
+    out = torch.empty(bp.plan.num_keys, emb, dtype=table.dtype, device=table.device)
+    check(
+        lib().relm_mp_plan_gather_last(
+            _dtype(table), ctypes.byref(bp.plan), _ptr(gathers), _ptr(table), emb, _ptr(out),
+            _stream(table),
+        )
+    )
+    return out
+
+
+__all__ = [name for name in dir() if not name.startswith("_")]

@@ -1,0 +1,535 @@
+// C ABI of librelm_mp_hip.so: index plans and the op-level entry points that
+// stand in for the reference's fanout_scatter / fanin_reduce ops
+// (maichmueller/relmo src/_ops/mp/mp_ops.cpp:3038-3348).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "internal.h"
+#include "relm_mp.h"
+
+namespace relm_mp {
+
+namespace {
+
+thread_local std::string g_last_error;
+
+// Bump allocator over caller memory; every piece is 256-byte aligned.
+struct Carver {
+    char* base;
+    size_t off = 0;
+    explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+    template <typename T>
+    T* take(size_t count) {
+        off = align_up(off, 256);
+        T* p = base != nullptr ? reinterpret_cast<T*>(base + off) : nullptr;
+        off += std::max<size_t>(count, 1) * sizeof(T);
+        return p;
+    }
+    size_t used() const { return align_up(off, 256); }
+};
+
+int check_rows(int64_t v, const char* name) {
+    if (v < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, std::string(name) + " must be >= 0.");
+    if (v > RELM_MP_MAX_ROWS)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         std::string("relm_mp HIP path: ") + name + " exceeds 2^31 - 2.");
+    return RELM_MP_OK;
+}
+
+int check_dtype(int dtype) {
+    if (dtype != RELM_MP_F32 && dtype != RELM_MP_F64)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp HIP path: dtype must be f32 or f64");
+    return RELM_MP_OK;
+}
+
+#define RELM_TRY(expr)                      \
+    do {                                    \
+        const int _rc = (expr);             \
+        if (_rc != RELM_MP_OK) return _rc;  \
+    } while (0)
+
+#define RELM_HIP(expr, what)                                  \
+    do {                                                      \
+        const hipError_t _e = (expr);                         \
+        if (_e != hipSuccess) return hip_error(_e, what);     \
+    } while (0)
+
+// Reads the status back (one stream synchronisation) and turns a bad index
+// into the reference's message "<name> index out of bounds: i not in [0, n)."
+// for the first offending edge in edge order.
+int finish_validation(const DevStatus* dst, DevStatus& host, const int64_t* keys, int64_t key_bound,
+                      const char* key_name, const int64_t* gathers, int64_t gather_bound,
+                      const char* gather_name, int gather_checked_first, hipStream_t s) {
+    RELM_HIP(hipMemcpyAsync(&host, dst, sizeof(DevStatus), hipMemcpyDeviceToHost, s),
+             "relm_mp status copy");
+    RELM_HIP(hipStreamSynchronize(s), "relm_mp status sync");
+    const unsigned long long ek = host.bad_key_edge;
+    const unsigned long long eg = gathers != nullptr ? host.bad_gather_edge : kNoEdge;
+    if (ek == kNoEdge && eg == kNoEdge) return RELM_MP_OK;
+    bool use_gather;
+    if (ek == eg) {
+        use_gather = gather_checked_first != 0;
+    } else {
+        use_gather = eg < ek;
+    }
+    const int64_t* arr = use_gather ? gathers : keys;
+    const unsigned long long e = use_gather ? eg : ek;
+    int64_t value = 0;
+    RELM_HIP(hipMemcpy(&value, arr + e, sizeof(int64_t), hipMemcpyDeviceToHost),
+             "relm_mp index copy");
+    const char* name = use_gather ? gather_name : key_name;
+    const int64_t bound = use_gather ? gather_bound : key_bound;
+    char buf[256];
+    std::snprintf(buf, sizeof(buf), "%s index out of bounds: %lld not in [0, %lld).",
+                  name != nullptr ? name : "index", static_cast<long long>(value),
+                  static_cast<long long>(bound));
+    return set_error(RELM_MP_ERR_INDEX_OUT_OF_BOUNDS, buf);
+}
+
+struct InvLayout {
+    DevStatus* status;
+    int32_t* inv;
+    size_t bytes;
+};
+
+InvLayout inv_layout(void* mem, int64_t num_keys) {
+    Carver c(mem);
+    InvLayout l;
+    l.status = c.take<DevStatus>(1);
+    l.inv = c.take<int32_t>(static_cast<size_t>(num_keys));
+    l.bytes = c.used();
+    return l;
+}
+
+int64_t max_hubs(int64_t num_edges) { return num_edges / (kHubThreshold + 1) + 1; }
+int64_t max_chunks(int64_t num_edges) {
+    return num_edges / kChunkSize + max_hubs(num_edges) + 1;
+}
+
+struct CsrLayout {
+    DevStatus* status;
+    int32_t* offsets;
+    int32_t* gather_sorted;
+    int32_t* keys_sorted;
+    int32_t* hub_key;
+    int32_t* hub_chunk_base;
+    int32_t* chunk_hub;
+    size_t bytes;
+};
+
+CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
+    Carver c(mem);
+    CsrLayout l;
+    l.status = c.take<DevStatus>(1);
+    l.offsets = c.take<int32_t>(static_cast<size_t>(num_keys) + 1);
+    l.gather_sorted = c.take<int32_t>(static_cast<size_t>(num_edges));
+    l.keys_sorted = c.take<int32_t>(static_cast<size_t>(num_edges));
+    l.hub_key = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
+    l.hub_chunk_base = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
+    l.chunk_hub = c.take<int32_t>(static_cast<size_t>(max_chunks(num_edges)));
+    l.bytes = c.used();
+    return l;
+}
+
+struct CsrScratch {
+    SortBuffers sort;
+    size_t bytes;
+};
+
+CsrScratch csr_scratch(void* mem, int64_t num_edges) {
+    Carver c(mem);
+    CsrScratch l;
+    const size_t n = static_cast<size_t>(num_edges);
+    l.sort.keys_a = c.take<uint32_t>(n);
+    l.sort.vals_a = c.take<uint32_t>(n);
+    l.sort.keys_b = c.take<uint32_t>(n);
+    l.sort.vals_b = c.take<uint32_t>(n);
+    const size_t hist = sort_hist_words(num_edges);
+    l.sort.hist = c.take<uint32_t>(hist);
+    l.sort.scan_tmp = c.take<uint32_t>(scan_tmp_words(static_cast<int64_t>(hist)));
+    l.bytes = c.used();
+    return l;
+}
+
+size_t hub_partial_upper_bound(int64_t num_edges, int64_t emb, int dtype, int64_t mode) {
+    const size_t elem = dtype == RELM_MP_F64 ? 8 : 4;
+    return align_up(static_cast<size_t>(max_chunks(num_edges)) * static_cast<size_t>(emb) * elem *
+                        (mode == RELM_MP_MODE_LOGSUMEXP ? 2 : 1),
+                    256);
+}
+
+int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, const int64_t* gathers,
+              int64_t gather_bound, const char* gather_name, int gather_checked_first,
+              int64_t num_edges, void* plan_mem, size_t plan_bytes, relm_mp_plan* plan,
+              hipStream_t s) {
+    RELM_TRY(check_rows(key_bound, "num_keys"));
+    RELM_TRY(check_rows(num_edges, "num_edges"));
+    if (gathers != nullptr) RELM_TRY(check_rows(gather_bound, "num_gather"));
+    const InvLayout l = inv_layout(plan_mem, key_bound);
+    if (plan_mem == nullptr || plan_bytes < l.bytes)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: inverse plan memory too small");
+    std::memset(plan, 0, sizeof(*plan));
+    plan->kind = RELM_MP_PLAN_INVERSE;
+    plan->num_keys = key_bound;
+    plan->num_edges = num_edges;
+    plan->num_gather = gather_bound;
+    plan->inv = l.inv;
+    RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
+    RELM_HIP(launch_fill_i32(l.inv, key_bound, -1, s), "relm_mp fill");
+    RELM_HIP(launch_inv_build(keys, key_bound, gathers, gather_bound, num_edges, l.inv, l.status, s),
+             "relm_mp inverse plan kernel");
+    DevStatus host{};
+    RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
+                               gather_name, gather_checked_first, s));
+    plan->collisions = static_cast<int64_t>(host.collisions);
+    return RELM_MP_OK;
+}
+
+int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, const int64_t* gathers,
+              int64_t gather_bound, const char* gather_name, int gather_checked_first,
+              int64_t num_edges, void* plan_mem, size_t plan_bytes, void* scratch,
+              size_t scratch_bytes, relm_mp_plan* plan, hipStream_t s) {
+    RELM_TRY(check_rows(key_bound, "num_keys"));
+    RELM_TRY(check_rows(num_edges, "num_edges"));
+    if (gathers != nullptr) RELM_TRY(check_rows(gather_bound, "num_gather"));
+    const CsrLayout l = csr_layout(plan_mem, key_bound, num_edges);
+    const CsrScratch sc = csr_scratch(scratch, num_edges);
+    if (plan_mem == nullptr || plan_bytes < l.bytes)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR plan memory too small");
+    if (scratch == nullptr || scratch_bytes < sc.bytes)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR scratch memory too small");
+    std::memset(plan, 0, sizeof(*plan));
+    plan->kind = RELM_MP_PLAN_CSR;
+    plan->hub_threshold = kHubThreshold;
+    plan->chunk_size = kChunkSize;
+    plan->num_keys = key_bound;
+    plan->num_edges = num_edges;
+    plan->num_gather = gathers != nullptr ? gather_bound : num_edges;
+    plan->offsets = l.offsets;
+    plan->gather_sorted = l.gather_sorted;
+    plan->keys_sorted = l.keys_sorted;
+    plan->hub_key = l.hub_key;
+    plan->hub_chunk_base = l.hub_chunk_base;
+    plan->chunk_hub = l.chunk_hub;
+    RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
+    if (num_edges > 0) {
+        RELM_HIP(sort_by_key(keys, key_bound, gathers, gather_bound, num_edges, sc.sort,
+                             reinterpret_cast<uint32_t*>(l.keys_sorted),
+                             reinterpret_cast<uint32_t*>(l.gather_sorted), l.status, s),
+                 "relm_mp radix sort");
+    }
+    RELM_HIP(launch_offsets_from_sorted(reinterpret_cast<const uint32_t*>(l.keys_sorted), num_edges,
+                                        key_bound, l.offsets, s),
+             "relm_mp offsets kernel");
+    RELM_HIP(launch_hub_list(l.offsets, key_bound, l.hub_key, l.hub_chunk_base,
+                             max_hubs(num_edges), l.status, s),
+             "relm_mp hub list kernel");
+    DevStatus host{};
+    RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
+                               gather_name, gather_checked_first, s));
+    plan->max_degree = static_cast<int64_t>(host.max_degree);
+    plan->num_hubs = static_cast<int64_t>(host.num_hubs);
+    plan->num_chunks = static_cast<int64_t>(host.num_chunks);
+    if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges))
+        return set_error(RELM_MP_ERR_HIP, "relm_mp: hub list overflow");
+    RELM_HIP(launch_chunk_map(l.offsets, l.hub_key, l.hub_chunk_base, plan->num_hubs,
+                              plan->num_chunks, l.chunk_hub, s),
+             "relm_mp chunk map kernel");
+    return RELM_MP_OK;
+}
+
+size_t csr_total(int64_t num_keys, int64_t num_edges) {
+    return csr_layout(nullptr, num_keys, num_edges).bytes + csr_scratch(nullptr, num_edges).bytes;
+}
+
+}  // namespace
+
+int set_error(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_error(hipError_t err, const char* what) {
+    if (err == hipSuccess) return RELM_MP_OK;
+    return set_error(RELM_MP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+}  // namespace relm_mp
+
+using namespace relm_mp;
+
+extern "C" {
+
+const char* relm_mp_last_error(void) { return g_last_error.c_str(); }
+
+const char* relm_mp_build_info(void) {
+    static const std::string info = [] {
+        char buf[160];
+        std::snprintf(buf, sizeof(buf), "hip=%d.%d;arch=gfx950;plans=inverse,csr;hub_threshold=%d;chunk=%d",
+                      HIP_VERSION_MAJOR, HIP_VERSION_MINOR, kHubThreshold, kChunkSize);
+        return std::string(buf);
+    }();
+    return info.c_str();
+}
+
+size_t relm_mp_inv_plan_bytes(int64_t num_keys) {
+    return inv_layout(nullptr, std::max<int64_t>(num_keys, 0)).bytes;
+}
+
+int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
+                           const int64_t* gathers, int64_t gather_bound, const char* gather_name,
+                           int gather_checked_first, int64_t num_edges, void* plan_mem,
+                           size_t plan_bytes, relm_mp_plan* plan, relm_mp_stream_t stream) {
+    return inv_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
+                     gather_checked_first, num_edges, plan_mem, plan_bytes, plan,
+                     static_cast<hipStream_t>(stream));
+}
+
+size_t relm_mp_csr_plan_bytes(int64_t num_keys, int64_t num_edges) {
+    return csr_layout(nullptr, std::max<int64_t>(num_keys, 0), std::max<int64_t>(num_edges, 0)).bytes;
+}
+
+size_t relm_mp_csr_plan_scratch_bytes(int64_t num_keys, int64_t num_edges) {
+    (void)num_keys;
+    return csr_scratch(nullptr, std::max<int64_t>(num_edges, 0)).bytes;
+}
+
+int relm_mp_csr_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
+                           const int64_t* gathers, int64_t gather_bound, const char* gather_name,
+                           int gather_checked_first, int64_t num_edges, void* plan_mem,
+                           size_t plan_bytes, void* scratch, size_t scratch_bytes,
+                           relm_mp_plan* plan, relm_mp_stream_t stream) {
+    return csr_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
+                     gather_checked_first, num_edges, plan_mem, plan_bytes, scratch, scratch_bytes,
+                     plan, static_cast<hipStream_t>(stream));
+}
+
+size_t relm_mp_plan_compute_scratch_bytes(const relm_mp_plan* plan, int64_t emb, int dtype,
+                                          int64_t mode) {
+    if (plan == nullptr) return 0;
+    return hub_partial_bytes(*plan, emb, dtype, mode);
+}
+
+int relm_mp_plan_gather_last(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                             const void* table, int64_t emb, void* out, relm_mp_stream_t stream) {
+    RELM_TRY(check_dtype(dtype));
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    return compute_gather_last(dtype, *plan, gathers, table, emb, out,
+                               static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_plan_segment_reduce(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                                const void* table, int64_t emb, int64_t mode, void* out,
+                                void* scratch, size_t scratch_bytes, relm_mp_stream_t stream) {
+    RELM_TRY(check_dtype(dtype));
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    return compute_segment_reduce(dtype, *plan, gathers, table, emb, mode, out, scratch,
+                                  scratch_bytes, static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_plan_logsumexp_backward(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                                    const void* grad_out, const void* out, const void* rel_flat,
+                                    int64_t emb, void* grad_rel, void* scratch,
+                                    size_t scratch_bytes, relm_mp_stream_t stream) {
+    RELM_TRY(check_dtype(dtype));
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    return compute_logsumexp_backward(dtype, *plan, gathers, grad_out, out, rel_flat, emb, grad_rel,
+                                      scratch, scratch_bytes, static_cast<hipStream_t>(stream));
+}
+
+/* ---- op-level entry points -------------------------------------------- */
+
+size_t relm_mp_fanout_scatter_workspace_size(int64_t num_edges, int64_t out_rows) {
+    (void)num_edges;
+    return relm_mp_inv_plan_bytes(out_rows);
+}
+
+// mp_ops.cpp:3038-3101 and the CPU loop 2815-2836: per edge the reference
+// checks src_global_idx before flat_dst.
+int relm_mp_fanout_scatter(int dtype, const void* x_cat, int64_t x_rows, int64_t emb,
+                           const int64_t* src_global_idx, const int64_t* flat_dst,
+                           int64_t num_edges, int64_t out_rows, void* out, void* workspace,
+                           size_t workspace_bytes, relm_mp_stream_t stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RELM_TRY(check_dtype(dtype));
+    RELM_TRY(check_rows(out_rows, "out_rows"));
+    RELM_TRY(check_rows(x_rows, "x_rows"));
+    RELM_TRY(check_rows(num_edges, "num_edges"));
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    if (num_edges == 0 || out_rows == 0)
+        return compute_fill(dtype, out, out_rows * emb, 0.0, s);
+    relm_mp_plan plan;
+    RELM_TRY(inv_build(flat_dst, out_rows, "flat_dst", src_global_idx, x_rows, "src_global_idx", 1,
+                       num_edges, workspace, workspace_bytes, &plan, s));
+    return compute_gather_last(dtype, plan, src_global_idx, x_cat, emb, out, s);
+}
+
+size_t relm_mp_fanout_scatter_backward_workspace_size(int64_t num_edges, int64_t x_rows,
+                                                      int64_t emb, int dtype) {
+    const size_t plan = relm_mp_csr_plan_bytes(x_rows, num_edges);
+    const size_t scratch = std::max(relm_mp_csr_plan_scratch_bytes(x_rows, num_edges),
+                                    hub_partial_upper_bound(num_edges, emb, dtype, RELM_MP_MODE_SUM));
+    return plan + scratch;
+}
+
+// mp_ops.cpp:3103-3166 and the CPU loop 2838-2861 (src checked first).
+int relm_mp_fanout_scatter_backward(int dtype, const void* grad_out, int64_t grad_out_rows,
+                                    int64_t emb, const int64_t* src_global_idx,
+                                    const int64_t* flat_dst, int64_t num_edges, int64_t x_rows,
+                                    void* grad_x, void* workspace, size_t workspace_bytes,
+                                    relm_mp_stream_t stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RELM_TRY(check_dtype(dtype));
+    RELM_TRY(check_rows(x_rows, "x_rows"));
+    RELM_TRY(check_rows(grad_out_rows, "grad_out_rows"));
+    RELM_TRY(check_rows(num_edges, "num_edges"));
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    if (num_edges == 0 || x_rows == 0) return compute_fill(dtype, grad_x, x_rows * emb, 0.0, s);
+    const size_t need = relm_mp_fanout_scatter_backward_workspace_size(num_edges, x_rows, emb, dtype);
+    if (workspace == nullptr || workspace_bytes < need)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: workspace too small");
+    const size_t plan_bytes = relm_mp_csr_plan_bytes(x_rows, num_edges);
+    char* scratch = static_cast<char*>(workspace) + plan_bytes;
+    relm_mp_plan plan;
+    RELM_TRY(csr_build(src_global_idx, x_rows, "src_global_idx", flat_dst, grad_out_rows, "flat_dst",
+                       0, num_edges, workspace, plan_bytes, scratch, workspace_bytes - plan_bytes,
+                       &plan, s));
+    return compute_segment_reduce(dtype, plan, nullptr, grad_out, emb, RELM_MP_MODE_SUM, grad_x,
+                                  scratch, workspace_bytes - plan_bytes, s);
+}
+
+size_t relm_mp_fanin_reduce_workspace_size(int64_t num_edges, int64_t dim_size, int64_t emb,
+                                           int dtype) {
+    const size_t plan = relm_mp_csr_plan_bytes(dim_size, num_edges);
+    const size_t scratch =
+        std::max(relm_mp_csr_plan_scratch_bytes(dim_size, num_edges),
+                 hub_partial_upper_bound(num_edges, emb, dtype, RELM_MP_MODE_LOGSUMEXP));
+    return plan + scratch;
+}
+
+// mp_ops.cpp:3327-3348 (mode router), 3168-3222 (sum), 3005-3036 (logsumexp);
+// the sum CPU loop 2863-2886 checks flat_src before dst_idx.
+int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int64_t emb,
+                         const int64_t* flat_src, const int64_t* dst_idx, int64_t num_edges,
+                         int64_t dim_size, int64_t mode, void* out, void* workspace,
+                         size_t workspace_bytes, relm_mp_stream_t stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RELM_TRY(check_dtype(dtype));
+    RELM_TRY(check_rows(dim_size, "dim_size"));
+    RELM_TRY(check_rows(rel_rows, "rel_rows"));
+    RELM_TRY(check_rows(num_edges, "num_edges"));
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    if (mode != RELM_MP_MODE_SUM && mode != RELM_MP_MODE_LOGSUMEXP)
+        return set_error(RELM_MP_ERR_UNSUPPORTED_MODE,
+                         "Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
+    const double empty = mode == RELM_MP_MODE_SUM ? 0.0 : -__builtin_huge_val();
+    if (num_edges == 0 || dim_size == 0) return compute_fill(dtype, out, dim_size * emb, empty, s);
+    const size_t need = relm_mp_fanin_reduce_workspace_size(num_edges, dim_size, emb, dtype);
+    if (workspace == nullptr || workspace_bytes < need)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: workspace too small");
+    const size_t plan_bytes = relm_mp_csr_plan_bytes(dim_size, num_edges);
+    char* scratch = static_cast<char*>(workspace) + plan_bytes;
+    relm_mp_plan plan;
+    RELM_TRY(csr_build(dst_idx, dim_size, "dst_idx", flat_src, rel_rows, "flat_src", 1, num_edges,
+                       workspace, plan_bytes, scratch, workspace_bytes - plan_bytes, &plan, s));
+    return compute_segment_reduce(dtype, plan, nullptr, rel_flat, emb, mode, out, scratch,
+                                  workspace_bytes - plan_bytes, s);
+}
+
+size_t relm_mp_fanin_reduce_sum_backward_workspace_size(int64_t num_edges, int64_t rel_rows,
+                                                        int64_t emb, int dtype) {
+    const size_t inv = relm_mp_inv_plan_bytes(rel_rows);
+    const size_t plan = relm_mp_csr_plan_bytes(rel_rows, num_edges);
+    const size_t scratch = std::max(relm_mp_csr_plan_scratch_bytes(rel_rows, num_edges),
+                                    hub_partial_upper_bound(num_edges, emb, dtype, RELM_MP_MODE_SUM));
+    return inv + plan + scratch;
+}
+
+// mp_ops.cpp:3224-3284 and the CPU loop 2888-2911 (flat_src checked first).
+int relm_mp_fanin_reduce_sum_backward(int dtype, const void* grad_out, int64_t grad_out_rows,
+                                      int64_t emb, const int64_t* flat_src,
+                                      const int64_t* dst_idx, int64_t num_edges,
+                                      int64_t rel_rows, void* grad_rel, void* workspace,
+                                      size_t workspace_bytes, relm_mp_stream_t stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RELM_TRY(check_dtype(dtype));
+    RELM_TRY(check_rows(rel_rows, "rel_rows"));
+    RELM_TRY(check_rows(grad_out_rows, "grad_out_rows"));
+    RELM_TRY(check_rows(num_edges, "num_edges"));
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    if (num_edges == 0 || rel_rows == 0) return compute_fill(dtype, grad_rel, rel_rows * emb, 0.0, s);
+    const size_t need = relm_mp_fanin_reduce_sum_backward_workspace_size(num_edges, rel_rows, emb, dtype);
+    if (workspace == nullptr || workspace_bytes < need)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: workspace too small");
+    const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows);
+    relm_mp_plan plan;
+    RELM_TRY(inv_build(flat_src, rel_rows, "flat_src", dst_idx, grad_out_rows, "dst_idx", 0,
+                       num_edges, workspace, inv_bytes, &plan, s));
+    if (plan.collisions == 0)
+        return compute_gather_last(dtype, plan, dst_idx, grad_out, emb, grad_rel, s);
+    char* csr_mem = static_cast<char*>(workspace) + inv_bytes;
+    const size_t plan_bytes = relm_mp_csr_plan_bytes(rel_rows, num_edges);
+    char* scratch = csr_mem + plan_bytes;
+    const size_t scratch_bytes = workspace_bytes - inv_bytes - plan_bytes;
+    RELM_TRY(csr_build(flat_src, rel_rows, "flat_src", dst_idx, grad_out_rows, "dst_idx", 0,
+                       num_edges, csr_mem, plan_bytes, scratch, scratch_bytes, &plan, s));
+    return compute_segment_reduce(dtype, plan, nullptr, grad_out, emb, RELM_MP_MODE_SUM, grad_rel,
+                                  scratch, scratch_bytes, s);
+}
+
+size_t relm_mp_fanin_reduce_logsumexp_backward_workspace_size(int64_t num_edges, int64_t rel_rows,
+                                                              int64_t emb, int dtype) {
+    return relm_mp_fanin_reduce_sum_backward_workspace_size(num_edges, rel_rows, emb, dtype);
+}
+
+// mp_ops.cpp:3286-3325 and the ATen sequence 2981-3003.
+int relm_mp_fanin_reduce_logsumexp_backward(int dtype, const void* grad_out, int64_t dim_size,
+                                            int64_t emb, const void* rel_flat,
+                                            int64_t rel_flat_rows, const int64_t* flat_src,
+                                            const int64_t* dst_idx, int64_t num_edges,
+                                            const void* out, int64_t rel_rows, void* grad_rel,
+                                            void* workspace, size_t workspace_bytes,
+                                            relm_mp_stream_t stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RELM_TRY(check_dtype(dtype));
+    RELM_TRY(check_rows(rel_rows, "rel_rows"));
+    RELM_TRY(check_rows(rel_flat_rows, "rel_flat rows"));
+    RELM_TRY(check_rows(dim_size, "dim_size"));
+    RELM_TRY(check_rows(num_edges, "num_edges"));
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    if (num_edges == 0 || rel_rows == 0) return compute_fill(dtype, grad_rel, rel_rows * emb, 0.0, s);
+    const size_t need =
+        relm_mp_fanin_reduce_logsumexp_backward_workspace_size(num_edges, rel_rows, emb, dtype);
+    if (workspace == nullptr || workspace_bytes < need)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: workspace too small");
+    // A message row is read from rel_flat and its gradient written to grad_rel,
+    // so flat_src must index both.
+    const int64_t key_bound = std::min(rel_rows, rel_flat_rows);
+    // Rows [key_bound, rel_rows) of grad_rel cannot receive messages.
+    const size_t elem = dtype == RELM_MP_F64 ? 8 : 4;
+    if (key_bound < rel_rows) {
+        RELM_TRY(compute_fill(dtype, static_cast<char*>(grad_rel) + key_bound * emb * elem,
+                              (rel_rows - key_bound) * emb, 0.0, s));
+    }
+    const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows);
+    relm_mp_plan plan;
+    RELM_TRY(inv_build(flat_src, key_bound, "flat_src", dst_idx, dim_size, "dst_idx", 1, num_edges,
+                       workspace, inv_bytes, &plan, s));
+    if (plan.collisions == 0)
+        return compute_logsumexp_backward(dtype, plan, dst_idx, grad_out, out, rel_flat, emb,
+                                          grad_rel, nullptr, 0, s);
+    char* csr_mem = static_cast<char*>(workspace) + inv_bytes;
+    const size_t plan_bytes = relm_mp_csr_plan_bytes(rel_rows, num_edges);
+    char* scratch = csr_mem + plan_bytes;
+    const size_t scratch_bytes = workspace_bytes - inv_bytes - plan_bytes;
+    RELM_TRY(csr_build(flat_src, key_bound, "flat_src", dst_idx, dim_size, "dst_idx", 1, num_edges,
+                       csr_mem, plan_bytes, scratch, scratch_bytes, &plan, s));
+    return compute_logsumexp_backward(dtype, plan, nullptr, grad_out, out, rel_flat, emb, grad_rel,
+                                      scratch, scratch_bytes, s);
+}
+
+}  // extern "C"

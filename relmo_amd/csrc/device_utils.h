@@ -1,0 +1,124 @@
+// Device helpers for gfx950 (wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace relm_mp {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+__device__ __forceinline__ unsigned long long lanemask_lt() {
+    return (1ull << lane_id()) - 1ull;
+}
+
+// Lanes of the wave whose `digit` (of `bits` bits) equals this lane's, among
+// the lanes in `active`.  One ballot per bit.
+__device__ __forceinline__ unsigned long long match_digit(uint32_t digit, int bits,
+                                                          unsigned long long active) {
+    unsigned long long peers = active;
+    for (int b = 0; b < bits; ++b) {
+        const bool set = (digit >> b) & 1u;
+        const unsigned long long m = __ballot(set);
+        peers &= set ? m : ~m;
+    }
+    return peers;
+}
+
+// Row-vector of V elements moved as one aligned load / store.
+template <typename T, int V>
+struct alignas(sizeof(T) * V) Pack {
+    T v[V];
+};
+
+template <typename T, int V>
+__device__ __forceinline__ Pack<T, V> pack_fill(T x) {
+    Pack<T, V> p;
+#pragma unroll
+    for (int i = 0; i < V; ++i) p.v[i] = x;
+    return p;
+}
+
+template <typename T, int V>
+__device__ __forceinline__ Pack<T, V> pack_load(const T* ptr) {
+    return *reinterpret_cast<const Pack<T, V>*>(ptr);
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void pack_store(T* ptr, const Pack<T, V>& p) {
+    *reinterpret_cast<Pack<T, V>*>(ptr) = p;
+}
+
+// Streaming store: the written rows are not re-read by this kernel.
+template <typename T, int V>
+__device__ __forceinline__ void pack_store_stream(T* ptr, const Pack<T, V>& p) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) __builtin_nontemporal_store(p.v[i], ptr + i);
+}
+
+// Maximum that propagates NaN like ATen's amax (a NaN operand wins).
+template <typename T>
+__device__ __forceinline__ T max_nan(T a, T b) {
+    return (b > a || b != b) ? b : a;
+}
+
+template <typename T>
+__device__ __forceinline__ T dev_exp(T x);
+template <>
+__device__ __forceinline__ float dev_exp<float>(float x) { return expf(x); }
+template <>
+__device__ __forceinline__ double dev_exp<double>(double x) { return exp(x); }
+
+template <typename T>
+__device__ __forceinline__ T dev_log(T x);
+template <>
+__device__ __forceinline__ float dev_log<float>(float x) { return logf(x); }
+template <>
+__device__ __forceinline__ double dev_log<double>(double x) { return log(x); }
+
+template <typename T>
+__device__ __forceinline__ T neg_inf() { return -__builtin_huge_val(); }
+template <>
+__device__ __forceinline__ float neg_inf<float>() { return -__builtin_huge_valf(); }
+
+template <typename T>
+__device__ __forceinline__ T quiet_nan() { return __builtin_nan(""); }
+template <>
+__device__ __forceinline__ float quiet_nan<float>() { return __builtin_nanf(""); }
+
+// Inclusive scan over one wave.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o, kWave);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+
+// Inclusive scan over a block of NT threads (NT a multiple of 64).  `lds` holds
+// NT/64 words.  Returns the inclusive prefix; `total` receives the block sum.
+template <int NT>
+__device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t x, uint32_t* lds,
+                                                         uint32_t& total) {
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    x = wave_inclusive_scan(x);
+    if (lane_id() == kWave - 1) lds[wave] = x;
+    __syncthreads();
+    uint32_t pre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NT / kWave; ++w) {
+        const uint32_t t = lds[w];
+        if (w < wave) pre += t;
+        tot += t;
+    }
+    __syncthreads();
+    total = tot;
+    return x + pre;
+}
+
+}  // namespace relm_mp

@@ -1,0 +1,99 @@
+// Internal declarations shared by the HIP translation units of librelm_mp_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "relm_mp.h"
+
+namespace relm_mp {
+
+// Validation / plan statistics written by the plan kernels and read back to
+// the host once per plan build (64 bytes).
+struct DevStatus {
+    unsigned long long bad_key_edge;     // smallest edge with a key out of range
+    unsigned long long bad_gather_edge;  // smallest edge with a gathered index out of range
+    unsigned long long collisions;       // inverse plans: edges whose key was already claimed
+    unsigned long long num_hubs;         // CSR plans: segments longer than the hub threshold
+    unsigned long long num_chunks;       // CSR plans: chunks over all hubs
+    unsigned long long max_degree;       // CSR plans: longest segment
+    unsigned long long reserved[2];
+};
+
+constexpr unsigned long long kNoEdge = ~0ull;
+
+// Hub geometry of CSR plans: segments with more than kHubThreshold edges are
+// cut into chunks of kChunkSize edges whose partial results are combined in
+// chunk order.
+constexpr int kHubThreshold = 64;
+constexpr int kChunkSize = 256;
+
+// Radix sort geometry (LSD, 8-bit digits at most).
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 16;
+constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys per block
+constexpr int kSortBins = 256;
+
+// Scan geometry.
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 16;
+constexpr int kScanTile = kScanThreads * kScanItems;
+
+int set_error(int code, const std::string& msg);
+int hip_error(hipError_t err, const char* what);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---- plan kernels (plan_kernels.hip) -------------------------------------
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
+hipError_t launch_status_init(DevStatus* st, hipStream_t s);
+hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
+                            int64_t gather_bound, int64_t n, int32_t* inv, DevStatus* st,
+                            hipStream_t s);
+
+// Exclusive scan of n uint32 values in place.  `tmp` holds scan_tmp_words(n) words.
+size_t scan_tmp_words(int64_t n);
+hipError_t launch_exclusive_scan_u32(uint32_t* data, int64_t n, uint32_t* tmp, hipStream_t s);
+
+// Stable LSD radix sort of (key, value) by key.  The first pass reads the
+// caller's int64 keys / gathers, validates them against the bounds (bad
+// entries are recorded in `st` and replaced by 0) and narrows them to 32 bit.
+struct SortBuffers {
+    uint32_t* keys_a;
+    uint32_t* vals_a;
+    uint32_t* keys_b;
+    uint32_t* vals_b;
+    uint32_t* hist;      // kSortBins * nblocks
+    uint32_t* scan_tmp;  // scan_tmp_words(kSortBins * nblocks)
+};
+size_t sort_hist_words(int64_t n);
+hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
+                       int64_t gather_bound, int64_t n, const SortBuffers& buf,
+                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s);
+
+hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
+                                      int32_t* offsets, hipStream_t s);
+hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
+                           int32_t* hub_chunk_base, int64_t hub_capacity, DevStatus* st,
+                           hipStream_t s);
+hipError_t launch_chunk_map(const int32_t* offsets, const int32_t* hub_key,
+                            const int32_t* hub_chunk_base, int64_t num_hubs, int64_t num_chunks,
+                            int32_t* chunk_hub, hipStream_t s);
+
+// ---- compute kernels (reduce_kernels.hip) --------------------------------
+int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
+                        const void* table, int64_t emb, void* out, hipStream_t s);
+int compute_segment_reduce(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
+                           const void* table, int64_t emb, int64_t mode, void* out,
+                           void* scratch, size_t scratch_bytes, hipStream_t s);
+int compute_logsumexp_backward(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
+                               const void* grad_out, const void* out, const void* rel_flat,
+                               int64_t emb, void* grad_rel, void* scratch, size_t scratch_bytes,
+                               hipStream_t s);
+int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t s);
+size_t hub_partial_bytes(const relm_mp_plan& plan, int64_t emb, int dtype, int64_t mode);
+
+}  // namespace relm_mp

@@ -1,0 +1,483 @@
+// Index-plan kernels: validation, inverse maps, device scan, stable LSD radix
+// sort by key, CSR offsets and hub lists.  All of these are integer work: the
+// bound is HBM traffic over the index arrays.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+
+#include "device_utils.h"
+#include "internal.h"
+
+namespace relm_mp {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+inline unsigned grid_1d(int64_t work, int per_block, int64_t cap = 1ll << 20) {
+    int64_t b = (work + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > cap) b = cap;
+    return static_cast<unsigned>(b);
+}
+
+__global__ __launch_bounds__(kThreads) void k_fill_i32(int32_t* __restrict__ p, int64_t n,
+                                                       int32_t value) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        p[i] = value;
+}
+
+__global__ void k_status_init(DevStatus* st) {
+    if (threadIdx.x == 0) {
+        st->bad_key_edge = kNoEdge;
+        st->bad_gather_edge = kNoEdge;
+        st->collisions = 0;
+        st->num_hubs = 0;
+        st->num_chunks = 0;
+        st->max_degree = 0;
+        st->reserved[0] = 0;
+        st->reserved[1] = 0;
+    }
+}
+
+// inv[k] = max e with keys[e] == k.  Every key and gathered index is checked;
+// the smallest offending edge of each array is recorded.
+__global__ __launch_bounds__(kThreads) void k_inv_build(const int64_t* __restrict__ keys,
+                                                        int64_t key_bound,
+                                                        const int64_t* __restrict__ gathers,
+                                                        int64_t gather_bound, int64_t n,
+                                                        int32_t* __restrict__ inv,
+                                                        DevStatus* __restrict__ st) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    unsigned long long collisions = 0;
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x; base < n; base += stride) {
+        const int64_t e = base + threadIdx.x;
+        bool coll = false;
+        if (e < n) {
+            const int64_t k = keys[e];
+            const bool bad_k = static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound);
+            if (bad_k) atomicMin(&st->bad_key_edge, static_cast<unsigned long long>(e));
+            if (gathers != nullptr) {
+                const int64_t g = gathers[e];
+                if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound))
+                    atomicMin(&st->bad_gather_edge, static_cast<unsigned long long>(e));
+            }
+            if (!bad_k) {
+                const int32_t old = atomicMax(inv + k, static_cast<int32_t>(e));
+                coll = old >= 0;
+            }
+        }
+        collisions += __popcll(__ballot(coll));
+    }
+    if (lane_id() == 0 && collisions != 0) atomicAdd(&st->collisions, collisions);
+}
+
+// ---- scan ----------------------------------------------------------------
+
+__global__ __launch_bounds__(kScanThreads) void k_scan_tile_sums(const uint32_t* __restrict__ in,
+                                                                 int64_t n,
+                                                                 uint32_t* __restrict__ sums) {
+    __shared__ uint32_t lds[kScanThreads / kWave];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
+        if (p < n) s += in[p];
+    }
+    uint32_t total;
+    block_inclusive_scan<kScanThreads>(s, lds, total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// Exclusive scan of one tile per block, in place, with a per-tile carry.
+__global__ __launch_bounds__(kScanThreads) void k_scan_tile_apply(uint32_t* __restrict__ data,
+                                                                  int64_t n,
+                                                                  const uint32_t* __restrict__ carry) {
+    __shared__ uint32_t tile[kScanTile];
+    __shared__ uint32_t lds[kScanThreads / kWave];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
+        tile[i * kScanThreads + threadIdx.x] = p < n ? data[p] : 0u;
+    }
+    __syncthreads();
+    uint32_t v[kScanItems];
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+        v[i] = tile[threadIdx.x * kScanItems + i];
+        s += v[i];
+    }
+    uint32_t total;
+    const uint32_t incl = block_inclusive_scan<kScanThreads>(s, lds, total);
+    uint32_t run = incl - s + (carry != nullptr ? carry[blockIdx.x] : 0u);
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+        tile[threadIdx.x * kScanItems + i] = run;
+        run += v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
+        if (p < n) data[p] = tile[i * kScanThreads + threadIdx.x];
+    }
+}
+
+// ---- radix sort ----------------------------------------------------------
+
+template <bool kFirst>
+__device__ __forceinline__ uint32_t load_key(const void* keys, int64_t pos, int64_t key_bound,
+                                             DevStatus* st) {
+    if constexpr (kFirst) {
+        const int64_t k = static_cast<const int64_t*>(keys)[pos];
+        if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound)) {
+            return 0u;
+        }
+        return static_cast<uint32_t>(k);
+    } else {
+        (void)key_bound;
+        (void)st;
+        return static_cast<const uint32_t*>(keys)[pos];
+    }
+}
+
+// Per-tile digit histogram, written digit-major: hist[d * nblocks + block].
+// The first pass also records the smallest edge with an out-of-range key.
+template <bool kFirst>
+__global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const void* __restrict__ keys,
+                                                                int64_t n, int shift, int bits,
+                                                                int64_t key_bound,
+                                                                uint32_t* __restrict__ hist,
+                                                                int64_t nblocks,
+                                                                DevStatus* __restrict__ st) {
+    __shared__ uint32_t h[kSortBins];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+    const uint32_t dmask = (1u << bits) - 1u;
+    unsigned long long bad = kNoEdge;
+    for (int i = 0; i < kSortItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+        const bool active = p < n;
+        uint32_t d = 0;
+        if (active) {
+            if constexpr (kFirst) {
+                const int64_t k = static_cast<const int64_t*>(keys)[p];
+                if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound)) {
+                    bad = min(bad, static_cast<unsigned long long>(p));
+                }
+            }
+            d = (load_key<kFirst>(keys, p, key_bound, st) >> shift) & dmask;
+        }
+        const unsigned long long peers = match_digit(d, bits, __ballot(active));
+        if (active && (peers & lanemask_lt()) == 0) atomicAdd(&h[d], __popcll(peers));
+    }
+    if constexpr (kFirst) {
+        if (bad != kNoEdge) atomicMin(&st->bad_key_edge, bad);
+    }
+    __syncthreads();
+    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = h[threadIdx.x];
+}
+
+// Stable scatter of one tile.  Wave w owns tile positions [w*1024, (w+1)*1024)
+// in 16 rounds of 64, so the order (wave, round, lane) is the edge order; each
+// key's rank is counted in that order, the tile is staged in LDS in digit order
+// and written out in runs per digit.
+template <bool kFirst>
+__global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
+    const void* __restrict__ keys, const void* __restrict__ vals, int64_t n, int shift, int bits,
+    int64_t key_bound, int64_t gather_bound, const uint32_t* __restrict__ hist_scanned,
+    int64_t nblocks, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
+    DevStatus* __restrict__ st) {
+    constexpr int kWaves = kSortThreads / kWave;
+    constexpr int kPerWave = kSortTile / kWaves;
+    __shared__ uint32_t wcnt[kWaves][kSortBins];
+    __shared__ uint32_t dstart[kSortBins];
+    __shared__ uint32_t gbase[kSortBins];
+    __shared__ uint32_t scan_lds[kSortThreads / kWave];
+    __shared__ uint32_t sk[kSortTile];
+    __shared__ uint32_t sv[kSortTile];
+
+    const int lane = lane_id();
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+    const uint32_t dmask = (1u << bits) - 1u;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) wcnt[w][threadIdx.x] = 0;
+    __syncthreads();
+
+    uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+    unsigned long long bad = kNoEdge;
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const int64_t p = tile_base + wave * kPerWave + r * kWave + lane;
+        const bool active = p < n;
+        uint32_t k = 0, v = 0;
+        if (active) {
+            k = load_key<kFirst>(keys, p, key_bound, st);
+            if constexpr (kFirst) {
+                if (vals != nullptr) {
+                    const int64_t g = static_cast<const int64_t*>(vals)[p];
+                    if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound)) {
+                        bad = min(bad, static_cast<unsigned long long>(p));
+                    } else {
+                        v = static_cast<uint32_t>(g);
+                    }
+                } else {
+                    v = static_cast<uint32_t>(p);
+                }
+            } else {
+                v = static_cast<const uint32_t*>(vals)[p];
+            }
+        }
+        key[r] = k;
+        val[r] = v;
+        const uint32_t d = (k >> shift) & dmask;
+        const unsigned long long peers = match_digit(d, bits, __ballot(active));
+        const uint32_t below = __popcll(peers & lanemask_lt());
+        uint32_t before = 0;
+        if (active) before = wcnt[wave][d];
+        rank[r] = before + below;
+        if (active && below == 0) wcnt[wave][d] = before + __popcll(peers);
+    }
+    if constexpr (kFirst) {
+        if (bad != kNoEdge) atomicMin(&st->bad_gather_edge, bad);
+    }
+    __syncthreads();
+
+    // Per digit (one thread per digit): exclusive prefix over waves, tile total.
+    const int dd = static_cast<int>(threadIdx.x);
+    uint32_t run = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const uint32_t c = wcnt[w][dd];
+        wcnt[w][dd] = run;
+        run += c;
+    }
+    uint32_t total;
+    const uint32_t incl = block_inclusive_scan<kSortThreads>(run, scan_lds, total);
+    dstart[dd] = incl - run;
+    gbase[dd] = hist_scanned[static_cast<int64_t>(dd) * nblocks + blockIdx.x];
+    __syncthreads();
+
+    const int64_t rem = n - tile_base;
+    const int count = rem < kSortTile ? static_cast<int>(rem) : kSortTile;
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const int local = wave * kPerWave + r * kWave + lane;
+        if (local < count) {
+            const uint32_t d = (key[r] >> shift) & dmask;
+            const uint32_t pos = dstart[d] + wcnt[wave][d] + rank[r];
+            if (pos < static_cast<uint32_t>(count)) {
+                sk[pos] = key[r];
+                sv[pos] = val[r];
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = static_cast<int>(threadIdx.x); i < count; i += kSortThreads) {
+        const uint32_t k = sk[i];
+        const uint32_t d = (k >> shift) & dmask;
+        const int64_t op = static_cast<int64_t>(gbase[d]) + (i - static_cast<int64_t>(dstart[d]));
+        if (op >= 0 && op < n) {
+            keys_out[op] = k;
+            vals_out[op] = sv[i];
+        }
+    }
+}
+
+// offsets[k] = first sorted position with key >= k; offsets[num_keys] = n.
+__global__ __launch_bounds__(kThreads) void k_offsets_from_sorted(const uint32_t* __restrict__ ks,
+                                                                  int64_t n, int64_t num_keys,
+                                                                  int32_t* __restrict__ offsets) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i <= n;
+         i += stride) {
+        const int64_t prev = i == 0 ? -1 : static_cast<int64_t>(ks[i - 1]);
+        int64_t cur = i == n ? num_keys : static_cast<int64_t>(ks[i]);
+        if (cur > num_keys) cur = num_keys;
+        for (int64_t k = prev + 1; k <= cur; ++k) offsets[k] = static_cast<int32_t>(i);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_hub_list(const int32_t* __restrict__ offsets,
+                                                       int64_t num_keys,
+                                                       int32_t* __restrict__ hub_key,
+                                                       int32_t* __restrict__ hub_chunk_base,
+                                                       int64_t hub_capacity,
+                                                       DevStatus* __restrict__ st) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    unsigned long long maxdeg = 0;
+    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k < num_keys;
+         k += stride) {
+        const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
+        if (deg > 0 && static_cast<unsigned long long>(deg) > maxdeg) maxdeg = deg;
+        if (deg > kHubThreshold) {
+            const unsigned long long slot = atomicAdd(&st->num_hubs, 1ull);
+            const unsigned long long nch = (deg + kChunkSize - 1) / kChunkSize;
+            const unsigned long long base = atomicAdd(&st->num_chunks, nch);
+            if (slot < static_cast<unsigned long long>(hub_capacity)) {
+                hub_key[slot] = static_cast<int32_t>(k);
+                hub_chunk_base[slot] = static_cast<int32_t>(base);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        const unsigned long long other = __shfl_xor(maxdeg, o, kWave);
+        maxdeg = other > maxdeg ? other : maxdeg;
+    }
+    if (lane_id() == 0 && maxdeg != 0) atomicMax(&st->max_degree, maxdeg);
+}
+
+// chunk_hub[hub_chunk_base[h] + j] = h for the chunks of hub h (one block per hub).
+__global__ __launch_bounds__(kThreads) void k_chunk_map(const int32_t* __restrict__ offsets,
+                                                        const int32_t* __restrict__ hub_key,
+                                                        const int32_t* __restrict__ hub_chunk_base,
+                                                        int64_t num_hubs, int64_t num_chunks,
+                                                        int32_t* __restrict__ chunk_hub) {
+    for (int64_t h = blockIdx.x; h < num_hubs; h += gridDim.x) {
+        const int64_t k = hub_key[h];
+        const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
+        const int64_t nch = (deg + kChunkSize - 1) / kChunkSize;
+        const int64_t base = hub_chunk_base[h];
+        for (int64_t j = threadIdx.x; j < nch; j += blockDim.x) {
+            if (base + j < num_chunks) chunk_hub[base + j] = static_cast<int32_t>(h);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid_1d(n, kThreads * 4)), dim3(kThreads), 0, s, p, n,
+                       value);
+    return hipGetLastError();
+}
+
+hipError_t launch_status_init(DevStatus* st, hipStream_t s) {
+    hipLaunchKernelGGL(k_status_init, dim3(1), dim3(64), 0, s, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
+                            int64_t gather_bound, int64_t n, int32_t* inv, DevStatus* st,
+                            hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_inv_build, dim3(grid_1d(n, kThreads * 4)), dim3(kThreads), 0, s, keys,
+                       key_bound, gathers, gather_bound, n, inv, st);
+    return hipGetLastError();
+}
+
+size_t scan_tmp_words(int64_t n) {
+    const int64_t tiles = (n + kScanTile - 1) / kScanTile;
+    if (tiles <= 1) return 0;
+    return align_up(static_cast<size_t>(tiles), 64) + scan_tmp_words(tiles);
+}
+
+hipError_t launch_exclusive_scan_u32(uint32_t* data, int64_t n, uint32_t* tmp, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int64_t tiles = (n + kScanTile - 1) / kScanTile;
+    if (tiles == 1) {
+        hipLaunchKernelGGL(k_scan_tile_apply, dim3(1), dim3(kScanThreads), 0, s, data, n,
+                           static_cast<const uint32_t*>(nullptr));
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_scan_tile_sums, dim3(static_cast<unsigned>(tiles)), dim3(kScanThreads), 0,
+                       s, data, n, tmp);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    err = launch_exclusive_scan_u32(tmp, tiles, tmp + align_up(static_cast<size_t>(tiles), 64), s);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_scan_tile_apply, dim3(static_cast<unsigned>(tiles)), dim3(kScanThreads), 0,
+                       s, data, n, static_cast<const uint32_t*>(tmp));
+    return hipGetLastError();
+}
+
+size_t sort_hist_words(int64_t n) {
+    const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
+    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks);
+}
+
+hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
+                       int64_t gather_bound, int64_t n, const SortBuffers& buf,
+                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    int bits = 0;
+    while (bits < 32 && (1ll << bits) < key_bound) ++bits;
+    const int passes = std::max(1, (bits + 7) / 8);
+    const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
+    const int64_t hist_n = static_cast<int64_t>(kSortBins) * nblocks;
+    const void* in_k = keys;
+    const void* in_v = gathers;
+    int shift = 0;
+    for (int p = 0; p < passes; ++p) {
+        const int width = bits / passes + (p < bits % passes ? 1 : 0);
+        const bool last = p == passes - 1;
+        uint32_t* out_k = last ? keys_out : (p % 2 == 0 ? buf.keys_a : buf.keys_b);
+        uint32_t* out_v = last ? vals_out : (p % 2 == 0 ? buf.vals_a : buf.vals_b);
+        if (p == 0) {
+            hipLaunchKernelGGL(k_radix_upsweep<true>, dim3(static_cast<unsigned>(nblocks)),
+                               dim3(kSortThreads), 0, s, in_k, n, shift, width, key_bound,
+                               buf.hist, nblocks, st);
+        } else {
+            hipLaunchKernelGGL(k_radix_upsweep<false>, dim3(static_cast<unsigned>(nblocks)),
+                               dim3(kSortThreads), 0, s, in_k, n, shift, width, key_bound,
+                               buf.hist, nblocks, st);
+        }
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        err = launch_exclusive_scan_u32(buf.hist, hist_n, buf.scan_tmp, s);
+        if (err != hipSuccess) return err;
+        if (p == 0) {
+            hipLaunchKernelGGL(k_radix_downsweep<true>, dim3(static_cast<unsigned>(nblocks)),
+                               dim3(kSortThreads), 0, s, in_k, in_v, n, shift, width, key_bound,
+                               gather_bound, buf.hist, nblocks, out_k, out_v, st);
+        } else {
+            hipLaunchKernelGGL(k_radix_downsweep<false>, dim3(static_cast<unsigned>(nblocks)),
+                               dim3(kSortThreads), 0, s, in_k, in_v, n, shift, width, key_bound,
+                               gather_bound, buf.hist, nblocks, out_k, out_v, st);
+        }
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        in_k = out_k;
+        in_v = out_v;
+        shift += width;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
+                                      int32_t* offsets, hipStream_t s) {
+    hipLaunchKernelGGL(k_offsets_from_sorted, dim3(grid_1d(n + 1, kThreads)), dim3(kThreads), 0, s,
+                       keys_sorted, n, num_keys, offsets);
+    return hipGetLastError();
+}
+
+hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
+                           int32_t* hub_chunk_base, int64_t hub_capacity, DevStatus* st,
+                           hipStream_t s) {
+    if (num_keys <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_hub_list, dim3(grid_1d(num_keys, kThreads * 4)), dim3(kThreads), 0, s,
+                       offsets, num_keys, hub_key, hub_chunk_base, hub_capacity, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_chunk_map(const int32_t* offsets, const int32_t* hub_key,
+                            const int32_t* hub_chunk_base, int64_t num_hubs, int64_t num_chunks,
+                            int32_t* chunk_hub, hipStream_t s) {
+    if (num_hubs <= 0) return hipSuccess;
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(num_hubs, 1 << 16));
+    hipLaunchKernelGGL(k_chunk_map, dim3(blocks), dim3(kThreads), 0, s, offsets, hub_key,
+                       hub_chunk_base, num_hubs, num_chunks, chunk_hub);
+    return hipGetLastError();
+}
+
+}  // namespace relm_mp

@@ -1,0 +1,667 @@
+// relm_mp_ops.so - torch.library binding of the relational message-passing ops.
+//
+// Registers TORCH_LIBRARY(relm_mp) with the reference's schema strings
+// (maichmueller/relmo src/_ops/mp/mp_ops.cpp:3754-3838) and the same
+// CompositeImplicitAutograd dispatch key (mp_ops.cpp:3840-3848).  Each op
+// validates its arguments with the reference's messages, then:
+//   * GPU tensors (float32 / float64): the HIP kernels of librelm_mp_hip.so,
+//     called through its C ABI (include/relm_mp.h) on the current stream;
+//   * CPU tensors (float32 / float64): sequential per-edge loops with the
+//     reference CPU lane's semantics (mp_ops.cpp:2815-2911) and its ATen
+//     logsumexp sequences (mp_ops.cpp:2981-3036);
+//   * other dtypes: the reference's ATen index_select / index_add_ sequences
+//     (mp_ops.cpp:2913-3003).
+// GPU tensors never take the CPU lane.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <c10/util/intrusive_ptr.h>
+#include <torch/library.h>
+
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "relm_mp.h"
+
+#ifndef RELM_MP_BUILD_TORCH_VERSION
+#define RELM_MP_BUILD_TORCH_VERSION "unknown"
+#endif
+
+namespace relm_amd {
+
+using at::Tensor;
+
+constexpr int64_t kModeSum = 0;
+constexpr int64_t kModeLogSumExp = 1;
+
+// ---- validation (mp_ops.cpp:28-72) ----------------------------------------
+
+bool is_fastpath_dtype(at::ScalarType dtype) {
+    return dtype == at::kFloat || dtype == at::kDouble;
+}
+
+void check_rank(const Tensor& t, int64_t expected, const char* name) {
+    TORCH_CHECK(t.dim() == expected, name, " must be rank ", expected, ", got rank ", t.dim(), ".");
+}
+
+void check_int64_index(const Tensor& t, const char* name) {
+    check_rank(t, 1, name);
+    TORCH_CHECK(t.scalar_type() == at::kLong, name, " must have dtype torch.int64.");
+}
+
+void check_in_bounds(int64_t idx, int64_t size, const char* name) {
+    TORCH_CHECK(idx >= 0 && idx < size, name, " index out of bounds: ", idx, " not in [0, ", size,
+                ").");
+}
+
+Tensor contiguous(const Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); }
+
+bool all_gpu(std::initializer_list<const Tensor*> ts) {
+    for (const Tensor* t : ts)
+        if (!t->is_cuda()) return false;
+    return true;
+}
+
+bool all_cpu(std::initializer_list<const Tensor*> ts) {
+    for (const Tensor* t : ts)
+        if (!t->is_cpu()) return false;
+    return true;
+}
+
+void check_same_gpu(const Tensor& a, const Tensor& b, const char* an, const char* bn) {
+    TORCH_CHECK(a.get_device() == b.get_device(), an, " and ", bn,
+                " must be on the same CUDA device.");
+}
+
+int dtype_code(const Tensor& t) { return t.scalar_type() == at::kDouble ? RELM_MP_F64 : RELM_MP_F32; }
+
+void raise_if(int rc) {
+    if (rc == RELM_MP_OK) return;
+    const std::string msg = relm_mp_last_error();
+    if (rc == RELM_MP_ERR_UNSUPPORTED_MODE) throw std::invalid_argument(msg);
+    TORCH_CHECK(false, msg);
+}
+
+hipStream_t current_stream(const Tensor& t) {
+    return c10::hip::getCurrentHIPStream(t.get_device()).stream();
+}
+
+Tensor byte_buffer(size_t bytes, const Tensor& like) {
+    return at::empty({static_cast<int64_t>(bytes == 0 ? 1 : bytes)},
+                     like.options().dtype(at::kByte));
+}
+
+// ---- plan cache -------------------------------------------------------------
+//
+// Plans depend only on the index tensors and bounds.  An entry is reused when
+// the same TensorImpl objects (held weakly, so a dead tensor's address cannot
+// be recycled while the entry exists) are passed again with unchanged version
+// counters.  RELM_MP_PLAN_CACHE=0 disables reuse; RELM_MP_PLAN_CACHE_MB bounds
+// the cached plan memory (default 4096).
+
+enum PlanRole : int {
+    kRoleInverse = 1,
+    kRoleCsr = 2,
+};
+
+struct PlanEntry {
+    PlanEntry(const Tensor& key, const Tensor& gather)
+        : key_w(key.getIntrusivePtr()), gather_w(gather.getIntrusivePtr()) {}
+    int role = 0;
+    c10::weak_intrusive_ptr<c10::TensorImpl> key_w;
+    c10::weak_intrusive_ptr<c10::TensorImpl> gather_w;
+    const c10::TensorImpl* key_impl = nullptr;
+    const c10::TensorImpl* gather_impl = nullptr;
+    uint32_t key_ver = 0;
+    uint32_t gather_ver = 0;
+    int64_t key_bound = 0;
+    int64_t gather_bound = 0;
+    int64_t num_edges = 0;
+    int device = -1;
+    Tensor mem;
+    relm_mp_plan plan{};
+    size_t bytes = 0;
+    uint64_t stamp = 0;
+};
+
+class PlanCache {
+   public:
+    static PlanCache& get() {
+        static PlanCache cache;
+        return cache;
+    }
+
+    bool enabled() const { return enabled_; }
+
+    bool lookup(int role, const Tensor& key, const Tensor& gather, int64_t key_bound,
+                int64_t gather_bound, relm_mp_plan* out) {
+        if (!enabled_ || !cacheable(key) || !cacheable(gather)) return false;
+        std::lock_guard<std::mutex> lock(mu_);
+        purge_dead_locked();
+        for (PlanEntry& e : entries_) {
+            if (e.role == role && e.key_impl == key.unsafeGetTensorImpl() &&
+                e.gather_impl == gather.unsafeGetTensorImpl() && e.key_ver == version(key) &&
+                e.gather_ver == version(gather) && e.key_bound == key_bound &&
+                e.gather_bound == gather_bound && e.num_edges == key.numel() &&
+                e.device == key.get_device()) {
+                e.stamp = ++clock_;
+                *out = e.plan;
+                return true;
+            }
+        }
+        return false;
+    }
+
+    void insert(int role, const Tensor& key, const Tensor& gather, int64_t key_bound,
+                int64_t gather_bound, const Tensor& mem, const relm_mp_plan& plan) {
+        if (!enabled_ || !cacheable(key) || !cacheable(gather)) return;
+        std::lock_guard<std::mutex> lock(mu_);
+        PlanEntry e(key, gather);
+        e.role = role;
+        e.key_impl = key.unsafeGetTensorImpl();
+        e.gather_impl = gather.unsafeGetTensorImpl();
+        e.key_ver = version(key);
+        e.gather_ver = version(gather);
+        e.key_bound = key_bound;
+        e.gather_bound = gather_bound;
+        e.num_edges = key.numel();
+        e.device = key.get_device();
+        e.mem = mem;
+        e.plan = plan;
+        e.bytes = static_cast<size_t>(mem.numel());
+        e.stamp = ++clock_;
+        total_ += e.bytes;
+        entries_.push_back(std::move(e));
+        while ((total_ > limit_ || entries_.size() > kMaxEntries) && entries_.size() > 1) {
+            size_t victim = 0;
+            for (size_t i = 1; i < entries_.size(); ++i)
+                if (entries_[i].stamp < entries_[victim].stamp) victim = i;
+            total_ -= entries_[victim].bytes;
+            entries_.erase(entries_.begin() + static_cast<std::ptrdiff_t>(victim));
+        }
+    }
+
+    void clear() {
+        std::lock_guard<std::mutex> lock(mu_);
+        entries_.clear();
+        total_ = 0;
+    }
+
+    int64_t size() {
+        std::lock_guard<std::mutex> lock(mu_);
+        purge_dead_locked();
+        return static_cast<int64_t>(entries_.size());
+    }
+
+   private:
+    static constexpr size_t kMaxEntries = 64;
+
+    PlanCache() {
+        const char* flag = std::getenv("RELM_MP_PLAN_CACHE");
+        if (flag != nullptr) {
+            std::string v(flag);
+            for (char& c : v) c = static_cast<char>(std::tolower(static_cast<unsigned char>(c)));
+            enabled_ = !(v == "0" || v == "false" || v == "no" || v == "off");
+        }
+        const char* mb = std::getenv("RELM_MP_PLAN_CACHE_MB");
+        if (mb != nullptr) limit_ = static_cast<size_t>(std::strtoull(mb, nullptr, 10)) << 20;
+    }
+
+    static bool cacheable(const Tensor& t) { return !t.is_inference(); }
+
+    static uint32_t version(const Tensor& t) {
+        return t.unsafeGetTensorImpl()->version_counter().current_version();
+    }
+
+    void purge_dead_locked() {
+        for (size_t i = 0; i < entries_.size();) {
+            if (entries_[i].key_w.expired() || entries_[i].gather_w.expired()) {
+                total_ -= entries_[i].bytes;
+                entries_.erase(entries_.begin() + static_cast<std::ptrdiff_t>(i));
+            } else {
+                ++i;
+            }
+        }
+    }
+
+    std::mutex mu_;
+    std::vector<PlanEntry> entries_;
+    size_t total_ = 0;
+    size_t limit_ = size_t(4096) << 20;
+    uint64_t clock_ = 0;
+    bool enabled_ = true;
+};
+
+struct GpuPlan {
+    relm_mp_plan plan{};
+    Tensor mem;  // keeps uncached plan memory alive for the call
+};
+
+GpuPlan inverse_plan(const Tensor& key, int64_t key_bound, const char* key_name,
+                     const Tensor& gather, int64_t gather_bound, const char* gather_name,
+                     bool gather_first, hipStream_t s) {
+    GpuPlan gp;
+    PlanCache& cache = PlanCache::get();
+    if (cache.lookup(kRoleInverse, key, gather, key_bound, gather_bound, &gp.plan)) return gp;
+    gp.mem = byte_buffer(relm_mp_inv_plan_bytes(key_bound), key);
+    raise_if(relm_mp_inv_plan_build(key.data_ptr<int64_t>(), key_bound, key_name,
+                                    gather.data_ptr<int64_t>(), gather_bound, gather_name,
+                                    gather_first ? 1 : 0, key.numel(), gp.mem.data_ptr(),
+                                    static_cast<size_t>(gp.mem.numel()), &gp.plan, s));
+    cache.insert(kRoleInverse, key, gather, key_bound, gather_bound, gp.mem, gp.plan);
+    return gp;
+}
+
+GpuPlan csr_plan(const Tensor& key, int64_t key_bound, const char* key_name, const Tensor& gather,
+                 int64_t gather_bound, const char* gather_name, bool gather_first, hipStream_t s) {
+    GpuPlan gp;
+    PlanCache& cache = PlanCache::get();
+    if (cache.lookup(kRoleCsr, key, gather, key_bound, gather_bound, &gp.plan)) return gp;
+    const int64_t n = key.numel();
+    gp.mem = byte_buffer(relm_mp_csr_plan_bytes(key_bound, n), key);
+    Tensor scratch = byte_buffer(relm_mp_csr_plan_scratch_bytes(key_bound, n), key);
+    raise_if(relm_mp_csr_plan_build(key.data_ptr<int64_t>(), key_bound, key_name,
+                                    gather.data_ptr<int64_t>(), gather_bound, gather_name,
+                                    gather_first ? 1 : 0, n, gp.mem.data_ptr(),
+                                    static_cast<size_t>(gp.mem.numel()), scratch.data_ptr(),
+                                    static_cast<size_t>(scratch.numel()), &gp.plan, s));
+    cache.insert(kRoleCsr, key, gather, key_bound, gather_bound, gp.mem, gp.plan);
+    return gp;
+}
+
+Tensor compute_scratch(const relm_mp_plan& plan, int64_t emb, int dtype, int64_t mode,
+                       const Tensor& like) {
+    const size_t bytes = relm_mp_plan_compute_scratch_bytes(&plan, emb, dtype, mode);
+    return byte_buffer(bytes, like);
+}
+
+// ---- GPU lane ----------------------------------------------------------------
+
+Tensor fanout_scatter_gpu(const Tensor& x_cat, const Tensor& src, const Tensor& dst,
+                          int64_t out_rows) {
+    c10::OptionalDeviceGuard guard(x_cat.device());
+    check_same_gpu(x_cat, src, "x_cat", "src_global_idx");
+    check_same_gpu(x_cat, dst, "x_cat", "flat_dst");
+    const int64_t emb = x_cat.size(1);
+    if (src.numel() == 0 || out_rows == 0 || emb == 0)
+        return at::zeros({out_rows, emb}, x_cat.options());
+    const Tensor x = contiguous(x_cat);
+    const Tensor s_idx = contiguous(src);
+    const Tensor d_idx = contiguous(dst);
+    hipStream_t stream = current_stream(x);
+    GpuPlan gp = inverse_plan(d_idx, out_rows, "flat_dst", s_idx, x.size(0), "src_global_idx",
+                              true, stream);
+    Tensor out = at::empty({out_rows, emb}, x_cat.options());
+    raise_if(relm_mp_plan_gather_last(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
+                                      x.data_ptr(), emb, out.data_ptr(), stream));
+    return out;
+}
+
+Tensor fanout_scatter_backward_gpu(const Tensor& grad_out, const Tensor& src, const Tensor& dst,
+                                   int64_t x_rows) {
+    c10::OptionalDeviceGuard guard(grad_out.device());
+    check_same_gpu(grad_out, src, "grad_out", "src_global_idx");
+    check_same_gpu(grad_out, dst, "grad_out", "flat_dst");
+    const int64_t emb = grad_out.size(1);
+    if (src.numel() == 0 || x_rows == 0 || emb == 0)
+        return at::zeros({x_rows, emb}, grad_out.options());
+    const Tensor g = contiguous(grad_out);
+    const Tensor s_idx = contiguous(src);
+    const Tensor d_idx = contiguous(dst);
+    hipStream_t stream = current_stream(g);
+    GpuPlan gp = csr_plan(s_idx, x_rows, "src_global_idx", d_idx, g.size(0), "flat_dst", false,
+                          stream);
+    Tensor grad_x = at::empty({x_rows, emb}, grad_out.options());
+    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(g), kModeSum, g);
+    raise_if(relm_mp_plan_segment_reduce(dtype_code(g), &gp.plan, nullptr, g.data_ptr(), emb,
+                                         kModeSum, grad_x.data_ptr(), scratch.data_ptr(),
+                                         static_cast<size_t>(scratch.numel()), stream));
+    return grad_x;
+}
+
+Tensor fanin_reduce_gpu(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
+                        int64_t dim_size, int64_t mode) {
+    c10::OptionalDeviceGuard guard(rel_flat.device());
+    check_same_gpu(rel_flat, flat_src, "rel_flat", "flat_src");
+    check_same_gpu(rel_flat, dst_idx, "rel_flat", "dst_idx");
+    const int64_t emb = rel_flat.size(1);
+    if (flat_src.numel() == 0 || dim_size == 0 || emb == 0) {
+        if (mode == kModeSum) return at::zeros({dim_size, emb}, rel_flat.options());
+        return at::full({dim_size, emb}, -std::numeric_limits<double>::infinity(),
+                        rel_flat.options());
+    }
+    const Tensor rel = contiguous(rel_flat);
+    const Tensor s_idx = contiguous(flat_src);
+    const Tensor d_idx = contiguous(dst_idx);
+    hipStream_t stream = current_stream(rel);
+    GpuPlan gp = csr_plan(d_idx, dim_size, "dst_idx", s_idx, rel.size(0), "flat_src", true, stream);
+    Tensor out = at::empty({dim_size, emb}, rel_flat.options());
+    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(rel), mode, rel);
+    raise_if(relm_mp_plan_segment_reduce(dtype_code(rel), &gp.plan, nullptr, rel.data_ptr(), emb,
+                                         mode, out.data_ptr(), scratch.data_ptr(),
+                                         static_cast<size_t>(scratch.numel()), stream));
+    return out;
+}
+
+Tensor fanin_reduce_sum_backward_gpu(const Tensor& grad_out, const Tensor& flat_src,
+                                     const Tensor& dst_idx, int64_t rel_rows) {
+    c10::OptionalDeviceGuard guard(grad_out.device());
+    check_same_gpu(grad_out, flat_src, "grad_out", "flat_src");
+    check_same_gpu(grad_out, dst_idx, "grad_out", "dst_idx");
+    const int64_t emb = grad_out.size(1);
+    if (flat_src.numel() == 0 || rel_rows == 0 || emb == 0)
+        return at::zeros({rel_rows, emb}, grad_out.options());
+    const Tensor g = contiguous(grad_out);
+    const Tensor s_idx = contiguous(flat_src);
+    const Tensor d_idx = contiguous(dst_idx);
+    hipStream_t stream = current_stream(g);
+    Tensor grad_rel = at::empty({rel_rows, emb}, grad_out.options());
+    GpuPlan inv = inverse_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false,
+                               stream);
+    if (inv.plan.collisions == 0) {
+        raise_if(relm_mp_plan_gather_last(dtype_code(g), &inv.plan, d_idx.data_ptr<int64_t>(),
+                                          g.data_ptr(), emb, grad_rel.data_ptr(), stream));
+        return grad_rel;
+    }
+    GpuPlan gp = csr_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false, stream);
+    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(g), kModeSum, g);
+    raise_if(relm_mp_plan_segment_reduce(dtype_code(g), &gp.plan, nullptr, g.data_ptr(), emb,
+                                         kModeSum, grad_rel.data_ptr(), scratch.data_ptr(),
+                                         static_cast<size_t>(scratch.numel()), stream));
+    return grad_rel;
+}
+
+Tensor fanin_reduce_logsumexp_backward_gpu(const Tensor& grad_out, const Tensor& rel_flat,
+                                           const Tensor& flat_src, const Tensor& dst_idx,
+                                           const Tensor& out, int64_t rel_rows) {
+    c10::OptionalDeviceGuard guard(grad_out.device());
+    check_same_gpu(grad_out, rel_flat, "grad_out", "rel_flat");
+    check_same_gpu(grad_out, flat_src, "grad_out", "flat_src");
+    check_same_gpu(grad_out, dst_idx, "grad_out", "dst_idx");
+    check_same_gpu(grad_out, out, "grad_out", "out");
+    TORCH_CHECK(grad_out.scalar_type() == rel_flat.scalar_type() &&
+                    grad_out.scalar_type() == out.scalar_type(),
+                "grad_out, rel_flat, and out must share dtype.");
+    const int64_t emb = grad_out.size(1);
+    Tensor grad_rel = at::zeros({0, emb}, rel_flat.options());
+    if (flat_src.numel() == 0 || rel_rows == 0 || emb == 0)
+        return at::zeros({rel_rows, emb}, rel_flat.options());
+    const Tensor g = contiguous(grad_out);
+    const Tensor rel = contiguous(rel_flat);
+    const Tensor o = contiguous(out);
+    const Tensor s_idx = contiguous(flat_src);
+    const Tensor d_idx = contiguous(dst_idx);
+    hipStream_t stream = current_stream(g);
+    // A message row is read from rel_flat and written to grad_rel, so flat_src
+    // must index both; rows beyond rel_flat cannot receive a gradient.
+    const int64_t key_bound = std::min<int64_t>(rel_rows, rel.size(0));
+    grad_rel = at::empty({rel_rows, emb}, rel_flat.options());
+    if (key_bound < rel_rows) grad_rel.narrow(0, key_bound, rel_rows - key_bound).zero_();
+    const int dt = dtype_code(rel);
+    GpuPlan inv = inverse_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true,
+                               stream);
+    if (inv.plan.collisions == 0) {
+        raise_if(relm_mp_plan_logsumexp_backward(dt, &inv.plan, d_idx.data_ptr<int64_t>(),
+                                                 g.data_ptr(), o.data_ptr(), rel.data_ptr(), emb,
+                                                 grad_rel.data_ptr(), nullptr, 0, stream));
+        return grad_rel;
+    }
+    GpuPlan gp = csr_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true, stream);
+    Tensor scratch = compute_scratch(gp.plan, emb, dt, kModeSum, g);
+    raise_if(relm_mp_plan_logsumexp_backward(dt, &gp.plan, nullptr, g.data_ptr(), o.data_ptr(),
+                                             rel.data_ptr(), emb, grad_rel.data_ptr(),
+                                             scratch.data_ptr(),
+                                             static_cast<size_t>(scratch.numel()), stream));
+    return grad_rel;
+}
+
+// ---- CPU lane (mp_ops.cpp:2815-2911) -------------------------------------------
+
+template <typename scalar_t>
+void cpu_scatter_rows(const scalar_t* in, const int64_t* read_idx, int64_t read_rows,
+                      const char* read_name, const int64_t* write_idx, int64_t write_rows,
+                      const char* write_name, bool read_checked_first, int64_t n, int64_t emb,
+                      scalar_t* out, bool accumulate) {
+    for (int64_t e = 0; e < n; ++e) {
+        const int64_t r = read_idx[e];
+        const int64_t w = write_idx[e];
+        if (read_checked_first) {
+            check_in_bounds(r, read_rows, read_name);
+            check_in_bounds(w, write_rows, write_name);
+        } else {
+            check_in_bounds(w, write_rows, write_name);
+            check_in_bounds(r, read_rows, read_name);
+        }
+        const scalar_t* src_row = in + r * emb;
+        scalar_t* dst_row = out + w * emb;
+        if (accumulate) {
+            for (int64_t k = 0; k < emb; ++k) dst_row[k] += src_row[k];
+        } else {
+            std::memcpy(dst_row, src_row, static_cast<size_t>(emb) * sizeof(scalar_t));
+        }
+    }
+}
+
+// Runs out[write[e]] (+)= in[read[e]] over all edges for f32 / f64 CPU tensors.
+void cpu_lane(const Tensor& in, const Tensor& read_idx, const char* read_name,
+              const Tensor& write_idx, const char* write_name, bool read_checked_first,
+              Tensor& out, bool accumulate) {
+    const Tensor x = contiguous(in);
+    const Tensor ri = contiguous(read_idx);
+    const Tensor wi = contiguous(write_idx);
+    const int64_t emb = out.size(1);
+    if (x.scalar_type() == at::kFloat) {
+        cpu_scatter_rows<float>(x.data_ptr<float>(), ri.data_ptr<int64_t>(), x.size(0), read_name,
+                                wi.data_ptr<int64_t>(), out.size(0), write_name,
+                                read_checked_first, ri.numel(), emb, out.data_ptr<float>(),
+                                accumulate);
+    } else {
+        cpu_scatter_rows<double>(x.data_ptr<double>(), ri.data_ptr<int64_t>(), x.size(0),
+                                 read_name, wi.data_ptr<int64_t>(), out.size(0), write_name,
+                                 read_checked_first, ri.numel(), emb, out.data_ptr<double>(),
+                                 accumulate);
+    }
+}
+
+// ---- ATen sequences (mp_ops.cpp:2913-3036) -------------------------------------
+
+Tensor fanin_logsumexp_aten(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
+                            int64_t dim_size) {
+    const int64_t emb = rel_flat.size(1);
+    Tensor max_vals =
+        at::full({dim_size, emb}, -std::numeric_limits<double>::infinity(), rel_flat.options());
+    if (flat_src.numel() == 0 || dim_size == 0) return max_vals;
+    Tensor msgs = rel_flat.index_select(0, flat_src);
+    Tensor index = dst_idx.unsqueeze(1).expand({dst_idx.size(0), emb});
+    max_vals.scatter_reduce_(0, index, msgs, "amax", true);
+    Tensor max_offsets = max_vals.index_select(0, dst_idx);
+    Tensor exps = (msgs - max_offsets).exp();
+    Tensor exps_sum = at::zeros({dim_size, emb}, rel_flat.options());
+    exps_sum.scatter_add_(0, index, exps);
+    return exps_sum.log() + max_vals;
+}
+
+Tensor fanin_logsumexp_backward_aten(const Tensor& grad_out, const Tensor& rel_flat,
+                                     const Tensor& flat_src, const Tensor& dst_idx,
+                                     const Tensor& out, int64_t rel_rows) {
+    const int64_t emb = grad_out.size(1);
+    Tensor grad_rel = at::zeros({rel_rows, emb}, rel_flat.options());
+    if (flat_src.numel() == 0 || rel_rows == 0) return grad_rel;
+    Tensor msgs = rel_flat.index_select(0, flat_src);
+    Tensor out_sel = out.index_select(0, dst_idx);
+    Tensor grad_sel = grad_out.index_select(0, dst_idx);
+    Tensor weights = (msgs - out_sel).exp();
+    grad_rel.index_add_(0, flat_src, grad_sel * weights);
+    return grad_rel;
+}
+
+// ---- ops -------------------------------------------------------------------------
+
+Tensor fanout_scatter(const Tensor& x_cat, const Tensor& src_global_idx, const Tensor& flat_dst,
+                      int64_t out_rows) {
+    check_rank(x_cat, 2, "x_cat");
+    check_int64_index(src_global_idx, "src_global_idx");
+    check_int64_index(flat_dst, "flat_dst");
+    TORCH_CHECK(src_global_idx.size(0) == flat_dst.size(0),
+                "src_global_idx and flat_dst must have equal length.");
+    TORCH_CHECK(out_rows >= 0, "out_rows must be >= 0.");
+    const int64_t emb = x_cat.size(1);
+    if (src_global_idx.numel() == 0 || out_rows == 0)
+        return at::zeros({out_rows, emb}, x_cat.options());
+    if (all_gpu({&x_cat, &src_global_idx, &flat_dst}) && is_fastpath_dtype(x_cat.scalar_type()))
+        return fanout_scatter_gpu(x_cat, src_global_idx, flat_dst, out_rows);
+    Tensor out = at::zeros({out_rows, emb}, x_cat.options());
+    if (all_cpu({&x_cat, &src_global_idx, &flat_dst}) && is_fastpath_dtype(x_cat.scalar_type())) {
+        cpu_lane(x_cat, src_global_idx, "src_global_idx", flat_dst, "flat_dst", true, out, false);
+        return out;
+    }
+    out.index_copy_(0, flat_dst, x_cat.index_select(0, src_global_idx));
+    return out;
+}
+
+Tensor fanout_scatter_backward(const Tensor& grad_out, const Tensor& src_global_idx,
+                               const Tensor& flat_dst, int64_t x_rows) {
+    check_rank(grad_out, 2, "grad_out");
+    check_int64_index(src_global_idx, "src_global_idx");
+    check_int64_index(flat_dst, "flat_dst");
+    TORCH_CHECK(src_global_idx.size(0) == flat_dst.size(0),
+                "src_global_idx and flat_dst must have equal length.");
+    TORCH_CHECK(x_rows >= 0, "x_rows must be >= 0.");
+    const int64_t emb = grad_out.size(1);
+    if (src_global_idx.numel() == 0 || x_rows == 0)
+        return at::zeros({x_rows, emb}, grad_out.options());
+    if (all_gpu({&grad_out, &src_global_idx, &flat_dst}) &&
+        is_fastpath_dtype(grad_out.scalar_type()))
+        return fanout_scatter_backward_gpu(grad_out, src_global_idx, flat_dst, x_rows);
+    Tensor grad_x = at::zeros({x_rows, emb}, grad_out.options());
+    if (all_cpu({&grad_out, &src_global_idx, &flat_dst}) &&
+        is_fastpath_dtype(grad_out.scalar_type())) {
+        // mp_ops.cpp:2838-2861: src (write side) is checked before flat_dst.
+        cpu_lane(grad_out, flat_dst, "flat_dst", src_global_idx, "src_global_idx", false, grad_x,
+                 true);
+        return grad_x;
+    }
+    grad_x.index_add_(0, src_global_idx, grad_out.index_select(0, flat_dst));
+    return grad_x;
+}
+
+Tensor fanin_reduce_sum(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
+                        int64_t dim_size) {
+    const int64_t emb = rel_flat.size(1);
+    if (flat_src.numel() == 0 || dim_size == 0)
+        return at::zeros({dim_size, emb}, rel_flat.options());
+    if (all_gpu({&rel_flat, &flat_src, &dst_idx}) && is_fastpath_dtype(rel_flat.scalar_type()))
+        return fanin_reduce_gpu(rel_flat, flat_src, dst_idx, dim_size, kModeSum);
+    Tensor out = at::zeros({dim_size, emb}, rel_flat.options());
+    if (all_cpu({&rel_flat, &flat_src, &dst_idx}) && is_fastpath_dtype(rel_flat.scalar_type())) {
+        cpu_lane(rel_flat, flat_src, "flat_src", dst_idx, "dst_idx", true, out, true);
+        return out;
+    }
+    out.index_add_(0, dst_idx, rel_flat.index_select(0, flat_src));
+    return out;
+}
+
+Tensor fanin_reduce_logsumexp(const Tensor& rel_flat, const Tensor& flat_src,
+                              const Tensor& dst_idx, int64_t dim_size) {
+    if (all_gpu({&rel_flat, &flat_src, &dst_idx}) && is_fastpath_dtype(rel_flat.scalar_type()))
+        return fanin_reduce_gpu(rel_flat, flat_src, dst_idx, dim_size, kModeLogSumExp);
+    return fanin_logsumexp_aten(rel_flat, flat_src, dst_idx, dim_size);
+}
+
+Tensor fanin_reduce(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
+                    int64_t dim_size, int64_t mode) {
+    check_rank(rel_flat, 2, "rel_flat");
+    check_int64_index(flat_src, "flat_src");
+    check_int64_index(dst_idx, "dst_idx");
+    TORCH_CHECK(flat_src.size(0) == dst_idx.size(0), "flat_src and dst_idx must have equal length.");
+    TORCH_CHECK(dim_size >= 0, "dim_size must be >= 0.");
+    if (mode == kModeSum) return fanin_reduce_sum(rel_flat, flat_src, dst_idx, dim_size);
+    if (mode == kModeLogSumExp) return fanin_reduce_logsumexp(rel_flat, flat_src, dst_idx, dim_size);
+    throw std::invalid_argument("Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
+}
+
+Tensor fanin_reduce_sum_backward(const Tensor& grad_out, const Tensor& flat_src,
+                                 const Tensor& dst_idx, int64_t rel_rows) {
+    check_rank(grad_out, 2, "grad_out");
+    check_int64_index(flat_src, "flat_src");
+    check_int64_index(dst_idx, "dst_idx");
+    TORCH_CHECK(flat_src.size(0) == dst_idx.size(0), "flat_src and dst_idx must have equal length.");
+    TORCH_CHECK(rel_rows >= 0, "rel_rows must be >= 0.");
+    const int64_t emb = grad_out.size(1);
+    if (flat_src.numel() == 0 || rel_rows == 0)
+        return at::zeros({rel_rows, emb}, grad_out.options());
+    if (all_gpu({&grad_out, &flat_src, &dst_idx}) && is_fastpath_dtype(grad_out.scalar_type()))
+        return fanin_reduce_sum_backward_gpu(grad_out, flat_src, dst_idx, rel_rows);
+    Tensor grad_rel = at::zeros({rel_rows, emb}, grad_out.options());
+    if (all_cpu({&grad_out, &flat_src, &dst_idx}) && is_fastpath_dtype(grad_out.scalar_type())) {
+        // mp_ops.cpp:2888-2911: flat_src (write side) is checked before dst_idx.
+        cpu_lane(grad_out, dst_idx, "dst_idx", flat_src, "flat_src", false, grad_rel, true);
+        return grad_rel;
+    }
+    grad_rel.index_add_(0, flat_src, grad_out.index_select(0, dst_idx));
+    return grad_rel;
+}
+
+Tensor fanin_reduce_logsumexp_backward(const Tensor& grad_out, const Tensor& rel_flat,
+                                       const Tensor& flat_src, const Tensor& dst_idx,
+                                       const Tensor& out, int64_t rel_rows) {
+    check_rank(grad_out, 2, "grad_out");
+    check_rank(rel_flat, 2, "rel_flat");
+    check_int64_index(flat_src, "flat_src");
+    check_int64_index(dst_idx, "dst_idx");
+    check_rank(out, 2, "out");
+    TORCH_CHECK(flat_src.size(0) == dst_idx.size(0), "flat_src and dst_idx must have equal length.");
+    TORCH_CHECK(rel_flat.size(1) == grad_out.size(1),
+                "rel_flat and grad_out must share embedding dim.");
+    TORCH_CHECK(out.size(0) == grad_out.size(0), "out and grad_out must share dim_size.");
+    TORCH_CHECK(out.size(1) == grad_out.size(1), "out and grad_out must share embedding dim.");
+    TORCH_CHECK(rel_rows >= 0, "rel_rows must be >= 0.");
+    const int64_t emb = grad_out.size(1);
+    if (flat_src.numel() == 0 || rel_rows == 0)
+        return at::zeros({rel_rows, emb}, rel_flat.options());
+    if (all_gpu({&grad_out, &rel_flat, &flat_src, &dst_idx, &out}) &&
+        is_fastpath_dtype(grad_out.scalar_type()))
+        return fanin_reduce_logsumexp_backward_gpu(grad_out, rel_flat, flat_src, dst_idx, out,
+                                                   rel_rows);
+    return fanin_logsumexp_backward_aten(grad_out, rel_flat, flat_src, dst_idx, out, rel_rows);
+}
+
+std::string build_info() {
+    return std::string("build_torch=") + RELM_MP_BUILD_TORCH_VERSION +
+           ";build_cuda_tag=cpu;abi_target=rocm-gfx950;abi_lane=nonstable;" + relm_mp_build_info();
+}
+
+void plan_cache_clear() { PlanCache::get().clear(); }
+
+int64_t plan_cache_size() { return PlanCache::get().size(); }
+
+}  // namespace relm_amd
+
+TORCH_LIBRARY(relm_mp, m) {
+    m.def("fanout_scatter(Tensor x_cat, Tensor src_global_idx, Tensor flat_dst, int out_rows) -> Tensor");
+    m.def("fanout_scatter_backward(Tensor grad_out, Tensor src_global_idx, Tensor flat_dst, int x_rows) -> Tensor");
+    m.def("fanin_reduce(Tensor rel_flat, Tensor flat_src, Tensor dst_idx, int dim_size, int mode) -> Tensor");
+    m.def("fanin_reduce_sum_backward(Tensor grad_out, Tensor flat_src, Tensor dst_idx, int rel_rows) -> Tensor");
+    m.def("fanin_reduce_logsumexp_backward(Tensor grad_out, Tensor rel_flat, Tensor flat_src, Tensor dst_idx, Tensor out, int rel_rows) -> Tensor");
+    m.def("build_info() -> str");
+    // No reference counterpart: control of the index-plan cache.
+    m.def("plan_cache_clear() -> ()");
+    m.def("plan_cache_size() -> int");
+}
+
+TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
+    m.impl("fanout_scatter", relm_amd::fanout_scatter);
+    m.impl("fanout_scatter_backward", relm_amd::fanout_scatter_backward);
+    m.impl("fanin_reduce", relm_amd::fanin_reduce);
+    m.impl("fanin_reduce_sum_backward", relm_amd::fanin_reduce_sum_backward);
+    m.impl("fanin_reduce_logsumexp_backward", relm_amd::fanin_reduce_logsumexp_backward);
+    m.impl("build_info", relm_amd::build_info);
+    m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
+    m.impl("plan_cache_size", relm_amd::plan_cache_size);
+}

@@ -1,0 +1,352 @@
+"""GPU parity of the HIP path against the oracle and the reference's golden
+fixtures.  Every test calls the kernels through the C ABI (relmo_amd.capi) or
+through the torch binding, never through a CPU path.
+
+Bars: fanout copies and sums over segments of at most 64 messages are
+bit-exact (the kernels add in edge order like the reference's CPU loop);
+longer segments are compared with the float64 truth within
+4 * eps32 * sum|terms|; logsumexp within rtol 1e-4 (exp/log differ by ulps).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests.conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+EPS32 = float(np.finfo(np.float32).eps)
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    os.environ["RELM_MP_FALLBACK"] = "error"
+    from relmo_amd import capi, mp
+
+    assert mp.available(), "relm_mp_ops.so failed to load"
+    capi.lib()
+    yield
+
+
+def _t(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _is_lse(case: dict) -> bool:
+    return case["op"] == "fanin_reduce_logsumexp_backward" or (
+        case["op"] == "fanin_reduce" and case["ints"][1] == 1
+    )
+
+
+def _assert_lse_close(got: np.ndarray, want: np.ndarray, name: str) -> None:
+    assert np.array_equal(np.isnan(got), np.isnan(want)), name
+    assert np.array_equal(np.isneginf(got), np.isneginf(want)), name
+    assert np.array_equal(np.isposinf(got), np.isposinf(want)), name
+    fin = np.isfinite(want)
+    np.testing.assert_allclose(got[fin], want[fin], rtol=1e-4, atol=1e-6, err_msg=name)
+
+
+# (table, read index, write index) positions in each summing op's arguments
+_SUM_OPS = {
+    "fanout_scatter_backward": (0, 2, 1),
+    "fanin_reduce": (0, 1, 2),
+    "fanin_reduce_sum_backward": (0, 2, 1),
+}
+
+
+def _assert_sum_parity(op: str, args: list, got: np.ndarray, want: np.ndarray, name: str) -> None:
+    """Rows with at most 64 messages: bit-exact.  Longer (hub) rows: within
+    4 * eps32 * sum|terms| of the float64 truth, a bound the reference's own
+    sequential sum also meets."""
+
+    t, r, w = _SUM_OPS[op]
+    table, read, write = args[t], args[r], args[w]
+    deg = np.bincount(write, minlength=got.shape[0])
+    short = deg <= 64
+    assert np.array_equal(got[short], want[short], equal_nan=True), name
+    if (~short).any():
+        truth, absum = oracle.segment_sum_truth(table, read, write, got.shape[0])
+        bound = 4 * EPS32 * absum[~short] + 1e-30
+        assert np.all(np.abs(got[~short] - truth[~short]) <= bound), name
+        assert np.all(np.abs(want[~short] - truth[~short]) <= bound), name
+
+
+def test_product_libraries_are_the_in_tree_builds() -> None:
+    from relmo_amd import capi, mp_runtime
+
+    lib = mp_runtime.loaded_library()
+    assert lib is not None and lib.parent == capi.LIB_PATH.parent
+    maps = open("/proc/self/maps").read()
+    assert "relmo_amd/relm_mp_ops.so" in maps and "relmo_amd/librelm_mp_hip.so" in maps
+    assert len({line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}) == 1
+
+
+@pytest.mark.parametrize("via", ["capi", "torch"])
+def test_golden_cases(golden, via: str) -> None:
+    from relmo_amd import capi
+
+    ns = torch.ops.relm_mp
+    fns = {
+        "capi": {
+            "fanout_scatter": capi.fanout_scatter,
+            "fanout_scatter_backward": capi.fanout_scatter_backward,
+            "fanin_reduce": capi.fanin_reduce,
+            "fanin_reduce_sum_backward": capi.fanin_reduce_sum_backward,
+            "fanin_reduce_logsumexp_backward": capi.fanin_reduce_logsumexp_backward,
+        },
+        "torch": {op: getattr(ns, op) for op in (
+            "fanout_scatter", "fanout_scatter_backward", "fanin_reduce",
+            "fanin_reduce_sum_backward", "fanin_reduce_logsumexp_backward")},
+    }[via]
+    cases, arrays = golden
+    for case in cases:
+        _log(f"golden[{via}] {case['name']}")
+        args = [_t(arrays[n]) for n in case["tensors"]] + list(case["ints"])
+        if "error" in case:
+            with pytest.raises((RuntimeError, ValueError)) as info:
+                fns[case["op"]](*args)
+                torch.cuda.synchronize()
+            assert str(info.value).splitlines()[0] == case["error"], case["name"]
+            continue
+        got = _np(fns[case["op"]](*args))
+        want = arrays[case["expected"]]
+        assert got.shape == want.shape and got.dtype == want.dtype, case["name"]
+        if _is_lse(case):
+            _assert_lse_close(got, want, case["name"])
+        elif case["op"] in _SUM_OPS and not (case["op"] == "fanin_reduce" and case["ints"][1] != 0):
+            np_args = [arrays[n] for n in case["tensors"]]
+            _assert_sum_parity(case["op"], np_args, got, want, case["name"])
+        else:
+            assert np.array_equal(got, want, equal_nan=True), case["name"]
+
+
+def test_c1_outputs_match_reference_digests() -> None:
+    from relmo_amd import capi
+    from tests.golden.c1_config import c1_inputs
+
+    a = {k: _t(v) for k, v in c1_inputs().items()}
+    digests = json.loads((GOLDEN / "c1_digests.json").read_text())
+    outs = {
+        "fanout_scatter": capi.fanout_scatter(a["x"], a["src"], a["flat_dst"], a["src"].numel()),
+        "fanout_scatter_backward": capi.fanout_scatter_backward(a["grad_slots"], a["src"], a["flat_dst"], a["x"].size(0)),
+        "fanin_reduce": capi.fanin_reduce(a["rel"], a["flat_src"], a["dst"], a["x"].size(0), 0),
+        "fanin_reduce_sum_backward": capi.fanin_reduce_sum_backward(a["grad_obj"], a["flat_src"], a["dst"], a["rel"].size(0)),
+    }
+    for op, out in outs.items():
+        _log(f"C1 {op}")
+        assert hashlib.sha256(_np(out).tobytes()).hexdigest() == digests[op], op
+
+
+@pytest.mark.parametrize(
+    "num_keys,num_edges,skew",
+    [(1, 1000, False), (2, 5000, False), (300, 1, False), (4096, 98304, False),
+     (50_000, 400_000, True), ((1 << 20) + 3, 300_000, False), (70_000, 4096 * 3 + 17, True)],
+)
+def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, skew: bool) -> None:
+    from relmo_amd import capi
+
+    _log(f"csr plan keys={num_keys} edges={num_edges} skew={skew}")
+    rng = np.random.default_rng(num_keys + num_edges)
+    if skew:
+        keys = np.minimum((rng.pareto(0.6, num_edges)).astype(np.int64), num_keys - 1)
+    else:
+        keys = rng.integers(0, num_keys, num_edges)
+    bp = capi.csr_plan(_t(keys), num_keys, None, num_edges)
+    offsets, perm = oracle.csr_build(keys, num_keys)
+    assert np.array_equal(_np(bp.offsets), offsets)
+    assert np.array_equal(_np(bp.gather_sorted), perm)
+    assert np.array_equal(_np(bp.keys_sorted), keys[perm])
+    deg = np.diff(offsets)
+    assert bp.plan.max_degree == deg.max()
+    assert bp.plan.num_hubs == int((deg > 64).sum())
+    assert bp.plan.num_chunks == int(((deg[deg > 64] + 255) // 256).sum())
+
+
+def test_inverse_plan_matches_oracle() -> None:
+    from relmo_amd import capi
+
+    rng = np.random.default_rng(11)
+    for n, k in [(1000, 5000), (100_000, 100_000), (300_000, 50_000)]:
+        keys = rng.permutation(k)[:n] if n <= k else rng.integers(0, k, n)
+        bp = capi.inv_plan(_t(keys), k, None, 0)
+        inv, coll = oracle.inverse_build(keys, k)
+        assert np.array_equal(_np(bp.inv), inv)
+        assert bp.plan.collisions == coll
+
+
+def _segments_bounded(keys: np.ndarray, bound: int = 64) -> bool:
+    return keys.size == 0 or np.bincount(keys).max() <= bound
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("emb", [1, 3, 4, 5, 32, 64, 128, 200, 300])
+def test_random_parity_all_ops(dtype, emb: int) -> None:
+    from relmo_amd import capi
+
+    _log(f"random parity dtype={dtype.__name__} emb={emb}")
+    rng = np.random.default_rng(emb * 7 + (dtype == np.float64))
+    x_rows, slots, objs = 900, 5000, 700
+    x = rng.standard_normal((x_rows, emb)).astype(dtype)
+    src = rng.integers(0, x_rows, slots)
+    flat_dst = rng.permutation(slots + 300)[:slots]  # injective with untouched rows
+    out_rows = slots + 300
+    g_slots = rng.standard_normal((out_rows, emb)).astype(dtype)
+    rel = rng.standard_normal((slots, emb)).astype(dtype)
+    flat_src = rng.permutation(slots)
+    dst = rng.integers(0, objs, slots)
+    g_obj = rng.standard_normal((objs, emb)).astype(dtype)
+
+    got = _np(capi.fanout_scatter(_t(x), _t(src), _t(flat_dst), out_rows))
+    assert np.array_equal(got, oracle.fanout_scatter(x, src, flat_dst, out_rows))
+    got = _np(capi.fanout_scatter_backward(_t(g_slots), _t(src), _t(flat_dst), x_rows))
+    assert _segments_bounded(src)
+    assert np.array_equal(got, oracle.fanout_scatter_backward(g_slots, src, flat_dst, x_rows))
+    got = _np(capi.fanin_reduce(_t(rel), _t(flat_src), _t(dst), objs, 0))
+    assert np.array_equal(got, oracle.fanin_reduce_sum(rel, flat_src, dst, objs))
+    got = _np(capi.fanin_reduce_sum_backward(_t(g_obj), _t(flat_src), _t(dst), slots))
+    assert np.array_equal(got, oracle.fanin_reduce_sum_backward(g_obj, flat_src, dst, slots))
+    lse = _np(capi.fanin_reduce(_t(rel), _t(flat_src), _t(dst), objs, 1))
+    want = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, objs)
+    _assert_lse_close(lse, want, "lse fwd")
+    got = _np(capi.fanin_reduce_logsumexp_backward(_t(g_obj), _t(rel), _t(flat_src), _t(dst), _t(want), slots))
+    ref = oracle.fanin_reduce_logsumexp_backward(g_obj, rel, flat_src, dst, want, slots)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-6)
+    # duplicated flat_src: the backward ops take the CSR (sorted) lane
+    flat_dup = rng.integers(0, slots // 2, slots)
+    got = _np(capi.fanin_reduce_sum_backward(_t(g_obj), _t(flat_dup), _t(dst), slots))
+    assert np.array_equal(got, oracle.fanin_reduce_sum_backward(g_obj, flat_dup, dst, slots))
+    got = _np(capi.fanin_reduce_logsumexp_backward(_t(g_obj), _t(rel), _t(flat_dup), _t(dst), _t(want), slots))
+    ref = oracle.fanin_reduce_logsumexp_backward(g_obj, rel, flat_dup, dst, want, slots)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-6)
+
+
+def _zipf_keys(rng, num_keys: int, n: int, s: float = 1.1) -> np.ndarray:
+    ranks = np.arange(1, num_keys + 1, dtype=np.float64)
+    cdf = np.cumsum(ranks ** -s)
+    cdf /= cdf[-1]
+    r = np.searchsorted(cdf, rng.random(n), side="right")
+    return rng.permutation(num_keys)[np.minimum(r, num_keys - 1)]
+
+
+def test_hub_segments_against_float64_truth() -> None:
+    from relmo_amd import capi
+
+    rng = np.random.default_rng(12)
+    num_keys, n, emb = 20_000, 600_000, 32
+    dst = _zipf_keys(rng, num_keys, n)
+    rel = (2.0 * rng.standard_normal((n, emb))).astype(np.float32)
+    flat_src = rng.permutation(n)
+    deg = np.bincount(dst, minlength=num_keys)
+    assert deg.max() > 10_000
+    short = deg <= 64
+    got = _np(capi.fanin_reduce(_t(rel), _t(flat_src), _t(dst), num_keys, 0))
+    want = oracle.fanin_reduce_sum(rel, flat_src, dst, num_keys)
+    truth, absum = oracle.segment_sum_truth(rel, flat_src, dst, num_keys)
+    assert np.array_equal(got[short], want[short])
+    assert np.all(np.abs(got - truth) <= 4 * EPS32 * absum + 1e-30)
+    lse = _np(capi.fanin_reduce(_t(rel), _t(flat_src), _t(dst), num_keys, 1))
+    lse_truth = oracle.fanin_logsumexp_truth(rel, flat_src, dst, num_keys)
+    _assert_lse_close(lse, lse_truth.astype(np.float32), "lse vs truth")
+    _assert_lse_close(lse, oracle.fanin_reduce_logsumexp(rel, flat_src, dst, num_keys), "lse vs oracle")
+    # fanout backward with hub rows on the source side
+    src = _zipf_keys(rng, 5000, n)
+    g = rng.standard_normal((n, emb)).astype(np.float32)
+    slots = np.arange(n)
+    got = _np(capi.fanout_scatter_backward(_t(g), _t(src), _t(slots), 5000))
+    truth, absum = oracle.segment_sum_truth(g, slots, src, 5000)
+    assert np.all(np.abs(got - truth) <= 4 * EPS32 * absum + 1e-30)
+
+
+def test_results_are_deterministic() -> None:
+    from relmo_amd import capi
+
+    rng = np.random.default_rng(13)
+    num_keys, n, emb = 10_000, 400_000, 64
+    dst = _t(_zipf_keys(rng, num_keys, n))
+    rel = _t(rng.standard_normal((n, emb)).astype(np.float32))
+    flat_src = _t(rng.permutation(n))
+    for mode in (0, 1):
+        a = capi.fanin_reduce(rel, flat_src, dst, num_keys, mode)
+        b = capi.fanin_reduce(rel, flat_src, dst, num_keys, mode)
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), mode
+
+
+def test_autograd_facade_on_gpu(mp_env) -> None:
+    from relmo_amd import mp
+
+    rng = np.random.default_rng(14)
+    x = torch.tensor(rng.standard_normal((50, 8)), dtype=torch.float32, device=DEV, requires_grad=True)
+    src = _t(rng.integers(0, 50, 300))
+    flat_dst = _t(rng.permutation(300))
+    slots = mp.fanout_scatter(x, src, flat_dst, 300)
+    dst = _t(rng.integers(0, 50, 300))
+    agg = mp.fanin_reduce(slots, flat_dst, dst, 50, 1) + mp.fanin_reduce(slots, flat_dst, dst, 50, 0)
+    loss = torch.where(torch.isfinite(agg), agg, torch.zeros_like(agg)).sum()
+    loss.backward()
+    x_ref = x.detach().cpu().double().requires_grad_(True)
+    from relmo_amd.mp_pack import fanin_reduce_python, fanout_scatter_python
+
+    s = fanout_scatter_python(x_ref, src.cpu(), flat_dst.cpu(), 300)
+    a = fanin_reduce_python(s, flat_dst.cpu(), dst.cpu(), 50, 1) + fanin_reduce_python(s, flat_dst.cpu(), dst.cpu(), 50, 0)
+    torch.where(torch.isfinite(a), a, torch.zeros_like(a)).sum().backward()
+    np.testing.assert_allclose(_np(x.grad), x_ref.grad.numpy(), rtol=1e-4, atol=1e-5)
+
+
+def test_gradcheck_float64_on_gpu(mp_env) -> None:
+    from relmo_amd import mp
+
+    x = torch.randn(6, 3, dtype=torch.float64, device=DEV, requires_grad=True)
+    src = torch.tensor([0, 5, 2, 1], device=DEV)
+    flat_dst = torch.tensor([1, 0, 3, 2], device=DEV)
+    assert torch.autograd.gradcheck(lambda t: mp.fanout_scatter(t, src, flat_dst, 5), (x,), eps=1e-6, atol=1e-4, rtol=1e-3)
+    rel = torch.randn(8, 4, dtype=torch.float64, device=DEV, requires_grad=True)
+    fs = torch.tensor([0, 2, 5, 7, 1, 3], device=DEV)
+    di = torch.tensor([1, 0, 3, 2, 0, 1], device=DEV)
+    assert torch.autograd.gradcheck(lambda t: mp.fanin_reduce(t, fs, di, 4, 1), (rel,), eps=1e-6, atol=1e-4, rtol=1e-3)
+    assert torch.autograd.gradcheck(lambda t: mp.fanin_reduce(t, fs[:5], di[:5], 5, 0), (rel,), eps=1e-6, atol=1e-4, rtol=1e-3)
+
+
+def test_noncontiguous_and_plan_cache_reuse(mp_env) -> None:
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    base = torch.randn(4, 6, device=DEV)
+    x = base.transpose(0, 1)
+    src = torch.tensor([0, 4, 2, 5], device=DEV)
+    flat_dst = torch.tensor([2, 1, 0, 3], device=DEV)
+    out = mp.fanout_scatter(x, src, flat_dst, 5)
+    want = oracle.fanout_scatter(x.cpu().numpy(), src.cpu().numpy(), flat_dst.cpu().numpy(), 5)
+    assert np.array_equal(_np(out), want)
+    # the cached plan must not survive an in-place change of the index tensor
+    ns.plan_cache_clear()
+    rel = torch.randn(10, 4, device=DEV)
+    fs = torch.tensor([0, 2, 7, 5, 2, 1], device=DEV)
+    di = torch.tensor([1, 0, 2, 2, 1, 0], device=DEV)
+    a = ns.fanin_reduce(rel, fs, di, 4, 0)
+    assert ns.plan_cache_size() >= 1
+    di[0] = 3
+    b = ns.fanin_reduce(rel, fs, di, 4, 0)
+    want = oracle.fanin_reduce_sum(rel.cpu().numpy(), fs.cpu().numpy(), di.cpu().numpy(), 4)
+    assert np.array_equal(_np(b), want)
+    assert not torch.equal(a, b)

@@ -1,0 +1,218 @@
+"""Pins the C oracle: golden fixtures of the reference library, the reference
+library itself where it is built, numpy brute force, closed forms and
+invariants chosen so that a dropped term, a wrong index or a transposed
+operand fails one of them."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle, ref_runner
+
+ORACLE_OPS = {
+    "fanout_scatter": oracle.fanout_scatter,
+    "fanout_scatter_backward": oracle.fanout_scatter_backward,
+    "fanin_reduce": oracle.fanin_reduce,
+    "fanin_reduce_sum_backward": oracle.fanin_reduce_sum_backward,
+    "fanin_reduce_logsumexp_backward": oracle.fanin_reduce_logsumexp_backward,
+}
+
+
+def _is_logsumexp(case: dict) -> bool:
+    return case["op"] == "fanin_reduce_logsumexp_backward" or (
+        case["op"] == "fanin_reduce" and case["ints"][1] == 1
+    )
+
+
+def test_oracle_matches_every_golden_case(golden) -> None:
+    cases, arrays = golden
+    for case in cases:
+        args = [arrays[n] for n in case["tensors"]] + list(case["ints"])
+        fn = ORACLE_OPS[case["op"]]
+        if "error" in case:
+            with pytest.raises((RuntimeError, ValueError)) as info:
+                fn(*args)
+            assert str(info.value) == case["error"], case["name"]
+            continue
+        got = fn(*args)
+        want = arrays[case["expected"]]
+        assert got.dtype == want.dtype and got.shape == want.shape, case["name"]
+        if _is_logsumexp(case):
+            # The reference computes exp/log with ATen's vectorised kernels,
+            # the oracle with libm: agreement to a few ulp.
+            np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-6, equal_nan=True, err_msg=case["name"])
+            assert np.array_equal(np.isnan(got), np.isnan(want)), case["name"]
+            assert np.array_equal(np.isneginf(got), np.isneginf(want)), case["name"]
+        else:
+            assert np.array_equal(got, want, equal_nan=True), case["name"]
+
+
+def test_oracle_c1_digests() -> None:
+    import hashlib
+    import json
+
+    from tests.conftest import GOLDEN
+    from tests.golden.c1_config import c1_inputs
+
+    a = c1_inputs()
+    digests = json.loads((GOLDEN / "c1_digests.json").read_text())
+    outs = {
+        "fanout_scatter": oracle.fanout_scatter(a["x"], a["src"], a["flat_dst"], a["src"].size),
+        "fanout_scatter_backward": oracle.fanout_scatter_backward(a["grad_slots"], a["src"], a["flat_dst"], a["x"].shape[0]),
+        "fanin_reduce": oracle.fanin_reduce_sum(a["rel"], a["flat_src"], a["dst"], a["x"].shape[0]),
+        "fanin_reduce_sum_backward": oracle.fanin_reduce_sum_backward(a["grad_obj"], a["flat_src"], a["dst"], a["rel"].shape[0]),
+    }
+    for op, out in outs.items():
+        assert hashlib.sha256(np.ascontiguousarray(out).tobytes()).hexdigest() == digests[op], op
+
+
+def test_fanout_matches_brute_force_with_duplicates() -> None:
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((30, 7)).astype(np.float32)
+    src = rng.integers(0, 30, 200)
+    dst = rng.integers(0, 50, 200)
+    want = np.zeros((50, 7), np.float32)
+    for e in range(200):
+        want[dst[e]] = x[src[e]]
+    assert np.array_equal(oracle.fanout_scatter(x, src, dst, 50), want)
+
+
+def test_sums_match_float64_truth_and_conserve_mass() -> None:
+    rng = np.random.default_rng(2)
+    rel = rng.standard_normal((400, 5)).astype(np.float32)
+    src = rng.integers(0, 400, 1000)
+    dst = rng.integers(0, 37, 1000)
+    out = oracle.fanin_reduce_sum(rel, src, dst, 37)
+    truth, absum = oracle.segment_sum_truth(rel, src, dst, 37)
+    assert np.all(np.abs(out - truth) <= 1e-6 * absum + 1e-30)
+    # conservation: the total over all rows equals the total over all messages
+    np.testing.assert_allclose(out.astype(np.float64).sum(0), rel[src].astype(np.float64).sum(0), rtol=1e-5)
+    # linearity: f(2a + b) == 2 f(a) + f(b) in float64
+    rel64 = rel.astype(np.float64)
+    b64 = rng.standard_normal(rel64.shape)
+    lhs = oracle.fanin_reduce_sum(2 * rel64 + b64, src, dst, 37)
+    rhs = 2 * oracle.fanin_reduce_sum(rel64, src, dst, 37) + oracle.fanin_reduce_sum(b64, src, dst, 37)
+    np.testing.assert_allclose(lhs, rhs, rtol=1e-12, atol=1e-12)
+    # fanout backward is the adjoint of fanout: <fanout(x), g> == <x, fanout_bwd(g)>
+    x = rng.standard_normal((400, 5))
+    g = rng.standard_normal((1000, 5))
+    slot = np.arange(1000)
+    lhs = np.sum(oracle.fanout_scatter(x, src, slot, 1000) * g)
+    rhs = np.sum(x * oracle.fanout_scatter_backward(g, src, slot, 400))
+    assert abs(lhs - rhs) < 1e-9 * max(1.0, abs(lhs))
+
+
+def test_sum_backward_is_adjoint_of_sum() -> None:
+    rng = np.random.default_rng(3)
+    rel = rng.standard_normal((60, 4))
+    src = rng.integers(0, 60, 150)  # duplicates on purpose
+    dst = rng.integers(0, 9, 150)
+    g = rng.standard_normal((9, 4))
+    lhs = np.sum(oracle.fanin_reduce_sum(rel, src, dst, 9) * g)
+    rhs = np.sum(rel * oracle.fanin_reduce_sum_backward(g, src, dst, 60))
+    assert abs(lhs - rhs) < 1e-10 * max(1.0, abs(lhs))
+
+
+def test_logsumexp_closed_forms() -> None:
+    rng = np.random.default_rng(4)
+    rel = rng.standard_normal((10, 3)).astype(np.float64)
+    # single message: log(exp(x - x)) + x == x exactly
+    out = oracle.fanin_reduce_logsumexp(rel, [7], [2], 4)
+    assert np.array_equal(out[2], rel[7])
+    assert np.all(np.isneginf(out[[0, 1, 3]]))
+    # n equal values c -> c + log n
+    c = np.full((5, 3), 1.25)
+    out = oracle.fanin_reduce_logsumexp(c, np.arange(5), np.zeros(5, np.int64), 1)
+    np.testing.assert_allclose(out[0], 1.25 + np.log(5.0), rtol=1e-15)
+    # shift invariance and bounds max <= lse <= max + log n
+    src = rng.integers(0, 10, 40)
+    dst = rng.integers(0, 6, 40)
+    a = oracle.fanin_reduce_logsumexp(rel, src, dst, 6)
+    b = oracle.fanin_reduce_logsumexp(rel + 3.5, src, dst, 6)
+    np.testing.assert_allclose(b, a + 3.5, rtol=1e-13)
+    for d in range(6):
+        sel = rel[src[dst == d]]
+        if len(sel):
+            assert np.all(sel.max(0) <= a[d] + 1e-12) and np.all(a[d] <= sel.max(0) + np.log(len(sel)) + 1e-12)
+            np.testing.assert_allclose(a[d], np.log(np.exp(sel).sum(0)), rtol=1e-13)
+    # all -inf row -> NaN (exp(-inf - -inf)); +inf -> NaN; NaN propagates
+    v = np.array([[-np.inf, 0.0, np.nan], [-np.inf, np.inf, 1.0]])
+    out = oracle.fanin_reduce_logsumexp(v, [0, 1], [0, 0], 1)
+    assert np.isnan(out[0]).all()
+
+
+def test_logsumexp_backward_weights_sum_to_one_and_match_finite_differences() -> None:
+    rng = np.random.default_rng(5)
+    rel = rng.standard_normal((30, 4))
+    src = rng.permutation(30)[:25]
+    dst = rng.integers(0, 7, 25)
+    out = oracle.fanin_reduce_logsumexp(rel, src, dst, 7)
+    ones = np.ones((7, 4))
+    g = oracle.fanin_reduce_logsumexp_backward(ones, rel, src, dst, out, 30)
+    for d in range(7):
+        if (dst == d).any():
+            np.testing.assert_allclose(g[src[dst == d]].sum(0), 1.0, rtol=1e-12)
+    gout = rng.standard_normal((7, 4))
+    gout[np.bincount(dst, minlength=7) == 0] = 0.0  # rows without messages hold -inf
+    grad = oracle.fanin_reduce_logsumexp_backward(gout, rel, src, dst, out, 30)
+    live = np.bincount(dst, minlength=7) > 0
+    eps = 1e-6
+    for r, k in [(src[0], 0), (src[3], 2), (src[10], 3)]:
+        plus, minus = rel.copy(), rel.copy()
+        plus[r, k] += eps
+        minus[r, k] -= eps
+        fd = (np.sum((gout * oracle.fanin_reduce_logsumexp(plus, src, dst, 7))[live])
+              - np.sum((gout * oracle.fanin_reduce_logsumexp(minus, src, dst, 7))[live])) / (2 * eps)
+        assert abs(fd - grad[r, k]) < 1e-6
+
+
+def test_csr_and_inverse_builders_match_numpy() -> None:
+    rng = np.random.default_rng(6)
+    keys = rng.integers(0, 300, 5000)
+    offsets, perm = oracle.csr_build(keys, 300)
+    assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(np.bincount(keys, minlength=300))]))
+    assert np.array_equal(perm, np.argsort(keys, kind="stable"))
+    inv, coll = oracle.inverse_build(keys, 300)
+    want = np.full(300, -1)
+    for e, k in enumerate(keys):
+        want[k] = e
+    assert np.array_equal(inv, want)
+    assert coll == 5000 - len(np.unique(keys))
+
+
+@pytest.mark.skipif(not ref_runner.available(), reason="oracle/_ref not built")
+def test_oracle_matches_reference_library_on_random_inputs() -> None:
+    rng = np.random.default_rng(7)
+    arrays = {
+        "x": rng.standard_normal((500, 16)).astype(np.float32),
+        "src": rng.integers(0, 500, 3000),
+        "dst": rng.integers(0, 900, 3000),
+        "g": rng.standard_normal((900, 16)).astype(np.float32),
+        "rel": (2 * rng.standard_normal((3000, 16))).astype(np.float32),
+        "fsrc": rng.permutation(3000),
+        "fdst": rng.integers(0, 64, 3000),
+        "gk": rng.standard_normal((64, 16)).astype(np.float32),
+    }
+    lse = oracle.fanin_reduce_logsumexp(arrays["rel"], arrays["fsrc"], arrays["fdst"], 64)
+    arrays["lse"] = lse
+    calls = [
+        {"op": "fanout_scatter", "tensors": ["x", "src", "dst"], "ints": [900]},
+        {"op": "fanout_scatter_backward", "tensors": ["g", "src", "dst"], "ints": [500]},
+        {"op": "fanin_reduce", "tensors": ["rel", "fsrc", "fdst"], "ints": [64, 0]},
+        {"op": "fanin_reduce", "tensors": ["rel", "fsrc", "fdst"], "ints": [64, 1]},
+        {"op": "fanin_reduce_sum_backward", "tensors": ["gk", "fsrc", "fdst"], "ints": [3000]},
+        {"op": "fanin_reduce_logsumexp_backward", "tensors": ["gk", "rel", "fsrc", "fdst", "lse"], "ints": [3000]},
+    ]
+    res = ref_runner.run_reference(calls, arrays)
+    a = arrays
+    assert np.array_equal(res[0]["out"], oracle.fanout_scatter(a["x"], a["src"], a["dst"], 900))
+    assert np.array_equal(res[1]["out"], oracle.fanout_scatter_backward(a["g"], a["src"], a["dst"], 500))
+    assert np.array_equal(res[2]["out"], oracle.fanin_reduce_sum(a["rel"], a["fsrc"], a["fdst"], 64))
+    np.testing.assert_allclose(res[3]["out"], lse, rtol=2e-6)
+    assert np.array_equal(res[4]["out"], oracle.fanin_reduce_sum_backward(a["gk"], a["fsrc"], a["fdst"], 3000))
+    np.testing.assert_allclose(
+        res[5]["out"],
+        oracle.fanin_reduce_logsumexp_backward(a["gk"], a["rel"], a["fsrc"], a["fdst"], lse, 3000),
+        rtol=2e-6, atol=1e-7,
+    )
