@@ -1,0 +1,336 @@
+#!/usr/bin/env python3
+"""Benchmark of the relational message-passing hot path on one MI355X.
+
+Headline ("C2"): fanin_reduce logsumexp forward +
+backward through the public API (relmo_amd.mp + autograd) - 1,048,576
+objects, D = 32, 16,777,216 messages ~ N(0, 2^2), Zipf(1.1) destinations.
+One step = forward + backward over the whole batch, with the index plans
+rebuilt in every step (the plan cache is cleared first), so the figure covers
+the whole op call.  value = algorithmic bytes per step / time per step.
+
+The JSON line also carries
+  roofline      - the dominant kernel (logsumexp backward over the inverse
+                  plan, one launch) timed with HIP events on its stream;
+  cpu_baseline  - the reference's own CPU op library (oracle/_ref) on a
+                  bounded 1/8-scale sample of C2, on the host's cores;
+  extra         - kernel-only rates with cached plans, C2 with sum, C3 fanout
+                  forward + backward, C1 latencies.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "fanout/fanin fwd+bwd HBM GB/s (% of peak); RelationalGNN graphs/sec, 1 GPU"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gbs(nbytes: float, seconds: float) -> float:
+    return nbytes / seconds / 1e9
+
+
+def timed(fn, steps: int, warmup: int, sync) -> float:
+    """Average seconds per call of fn over `steps` calls after `warmup` calls,
+    bracketed by device synchronisation."""
+
+    for _ in range(warmup):
+        fn()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    sync()
+    return (time.perf_counter() - t0) / steps
+
+
+def event_time(fn, reps: int, torch) -> float:
+    """Average seconds per launch measured with HIP events on the current stream
+    (the stream the library enqueues on)."""
+
+    stream = torch.cuda.current_stream()
+    fn()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / reps
+
+
+def load_traffic(name: str) -> dict | None:
+    path = REPO / "profiles" / f"{name}.json"
+    if path.exists():
+        return json.loads(path.read_text())
+    return None
+
+
+def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
+    dev = torch.device("cuda", 0)
+    d = syn.c2_fanin(dev)
+    rel, flat_src, dst, grad_out, K = d["rel"], d["flat_src"], d["dst"], d["grad_out"], d["dim_size"]
+    E, D = rel.shape
+    ns = torch.ops.relm_mp
+    rel.requires_grad_(True)
+    deg = torch.bincount(dst, minlength=K)
+    info = {"max_degree": int(deg.max()), "empty_objects": int((deg == 0).sum()),
+            "objects_over_64": int((deg > 64).sum())}
+    if mode == 1:
+        b_fwd, b_bwd = syn.bytes_fanin_fwd(E, D, K), syn.bytes_fanin_lse_bwd(E, D, K, E)
+    else:
+        b_fwd, b_bwd = syn.bytes_fanin_fwd(E, D, K), syn.bytes_fanin_sum_bwd(E, D, K, E)
+
+    def step_uncached():
+        ns.plan_cache_clear()
+        out = mp.fanin_reduce(rel, flat_src, dst, K, mode)
+        torch.autograd.grad(out, rel, grad_out)
+
+    def step_cached():
+        out = mp.fanin_reduce(rel, flat_src, dst, K, mode)
+        torch.autograd.grad(out, rel, grad_out)
+
+    sync = torch.cuda.synchronize
+    t_step = timed(step_uncached, steps, warmup, sync)
+    t_cached = timed(step_cached, steps, warmup, sync)
+    ns.plan_cache_clear()
+
+    # Kernel-only timings with prebuilt plans, HIP events on the launch stream.
+    r = rel.detach()
+    fwd_plan = capi.csr_plan(dst, K, flat_src, E, "dst_idx", "flat_src", True)
+    bwd_plan = capi.inv_plan(flat_src, E, dst, K, "flat_src", "dst_idx", True)
+    out = capi.plan_segment_reduce(fwd_plan, r, mode)
+    reps = max(steps, 10)
+    t_fwd = event_time(lambda: capi.plan_segment_reduce(fwd_plan, r, mode), reps, torch)
+    if mode == 1:
+        t_bwd = event_time(lambda: capi.plan_logsumexp_backward(bwd_plan, grad_out, out, r, dst), reps, torch)
+    else:
+        t_bwd = event_time(lambda: capi.plan_gather_last(bwd_plan, grad_out, dst), reps, torch)
+    t_plan_fwd = timed(lambda: capi.csr_plan(dst, K, flat_src, E), 3, 1, sync)
+    t_plan_bwd = timed(lambda: capi.inv_plan(flat_src, E, dst, K), 3, 1, sync)
+    del fwd_plan, bwd_plan, out
+    res = {
+        "bytes_fwd": b_fwd, "bytes_bwd": b_bwd,
+        "ms_step": t_step * 1e3, "gbs_step": gbs(b_fwd + b_bwd, t_step),
+        "ms_step_cached_plans": t_cached * 1e3, "gbs_step_cached_plans": gbs(b_fwd + b_bwd, t_cached),
+        "ms_fwd_kernels": t_fwd * 1e3, "gbs_fwd_kernels": gbs(b_fwd, t_fwd),
+        "ms_bwd_kernel": t_bwd * 1e3, "gbs_bwd_kernel": gbs(b_bwd, t_bwd),
+        "ms_plan_fwd_csr": t_plan_fwd * 1e3, "ms_plan_bwd_inverse": t_plan_bwd * 1e3,
+        **info,
+    }
+    del d, rel, grad_out
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_c3(torch, mp, capi, syn, steps: int, warmup: int) -> dict:
+    dev = torch.device("cuda", 0)
+    d = syn.c3_fanout(dev)
+    x, src, flat_dst, grad_out, out_rows = d["x"], d["src"], d["flat_dst"], d["grad_out"], d["out_rows"]
+    R, D = x.shape
+    E = src.numel()
+    ns = torch.ops.relm_mp
+    x.requires_grad_(True)
+    b_fwd, b_bwd = syn.bytes_fanout_fwd(E, D, out_rows), syn.bytes_fanout_bwd(E, D, R)
+
+    def step_uncached():
+        ns.plan_cache_clear()
+        out = mp.fanout_scatter(x, src, flat_dst, out_rows)
+        torch.autograd.grad(out, x, grad_out)
+
+    def step_cached():
+        out = mp.fanout_scatter(x, src, flat_dst, out_rows)
+        torch.autograd.grad(out, x, grad_out)
+
+    sync = torch.cuda.synchronize
+    t_step = timed(step_uncached, steps, warmup, sync)
+    t_cached = timed(step_cached, steps, warmup, sync)
+    ns.plan_cache_clear()
+    xd = x.detach()
+    fwd_plan = capi.inv_plan(flat_dst, out_rows, src, R, "flat_dst", "src_global_idx", True)
+    bwd_plan = capi.csr_plan(src, R, flat_dst, out_rows, "src_global_idx", "flat_dst", False)
+    reps = max(steps, 10)
+    t_fwd = event_time(lambda: capi.plan_gather_last(fwd_plan, xd, src), reps, torch)
+    t_bwd = event_time(lambda: capi.plan_segment_reduce(bwd_plan, grad_out, 0), reps, torch)
+    del fwd_plan, bwd_plan
+    res = {
+        "bytes_fwd": b_fwd, "bytes_bwd": b_bwd,
+        "ms_step": t_step * 1e3, "gbs_step": gbs(b_fwd + b_bwd, t_step),
+        "ms_step_cached_plans": t_cached * 1e3, "gbs_step_cached_plans": gbs(b_fwd + b_bwd, t_cached),
+        "ms_fwd_kernel": t_fwd * 1e3, "gbs_fwd_kernel": gbs(b_fwd, t_fwd),
+        "ms_bwd_kernels": t_bwd * 1e3, "gbs_bwd_kernels": gbs(b_bwd, t_bwd),
+    }
+    del d, x, grad_out
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_c1(torch, mp, syn) -> dict:
+    dev = torch.device("cuda", 0)
+    d = syn.c1_ops(dev)
+    ns = torch.ops.relm_mp
+    calls = {
+        "fanout_scatter": lambda: ns.fanout_scatter(d["x"], d["src"], d["flat_dst"], d["slots"]),
+        "fanout_scatter_backward": lambda: ns.fanout_scatter_backward(d["grad_slots"], d["src"], d["flat_dst"], d["objects"]),
+        "fanin_reduce_sum": lambda: ns.fanin_reduce(d["rel"], d["flat_src"], d["dst"], d["objects"], 0),
+        "fanin_reduce_sum_backward": lambda: ns.fanin_reduce_sum_backward(d["grad_obj"], d["flat_src"], d["dst"], d["slots"]),
+    }
+    out = {}
+    for name, fn in calls.items():
+        ns.plan_cache_clear()
+        out[f"us_{name}_uncached"] = timed(lambda: (ns.plan_cache_clear(), fn()), 20, 5, torch.cuda.synchronize) * 1e6
+        out[f"us_{name}_cached"] = timed(fn, 50, 5, torch.cuda.synchronize) * 1e6
+    ns.plan_cache_clear()
+    return out
+
+
+def cpu_baseline(syn) -> dict:
+    """The reference's CPU op library on a 1/8-scale C2 sample (same generator,
+    131,072 objects, 2,097,152 messages), logsumexp forward + backward, on all
+    host cores; falls back to the C oracle (1 core) where oracle/_ref is absent."""
+
+    import numpy as np
+
+    from oracle import oracle, ref_runner
+
+    K, E, D = 1 << 17, 1 << 21, 32
+    rng = np.random.default_rng(0)
+    ranks = np.arange(1, K + 1, dtype=np.float64)
+    cdf = np.cumsum(ranks ** -1.1)
+    cdf /= cdf[-1]
+    dst = rng.permutation(K)[np.minimum(np.searchsorted(cdf, rng.random(E), side="right"), K - 1)]
+    rel = (2.0 * rng.standard_normal((E, D))).astype(np.float32)
+    flat_src = np.arange(E, dtype=np.int64)
+    g = rng.standard_normal((K, D)).astype(np.float32)
+    nbytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_lse_bwd(E, D, K, E)
+    sample = f"C2 at 1/8 scale: K={K}, E={E}, D={D}, Zipf(1.1) dst, logsumexp fwd+bwd"
+    cores = os.cpu_count() or 1
+    if ref_runner.available():
+        out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, K)
+        arrays = {"rel": rel, "src": flat_src, "dst": dst, "g": g, "out": out}
+        calls = [
+            {"op": "fanin_reduce", "tensors": ["rel", "src", "dst"], "ints": [K, 1], "repeat": 3, "warmup": 1, "threads": cores},
+            {"op": "fanin_reduce_logsumexp_backward", "tensors": ["g", "rel", "src", "dst", "out"], "ints": [E], "repeat": 3, "warmup": 1, "threads": cores},
+        ]
+        res = ref_runner.run_reference(calls, arrays)
+        t = statistics.median(res[0]["times"]) + statistics.median(res[1]["times"])
+        threads = res[0]["threads"]
+        return {"value": round(gbs(nbytes, t), 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+                "sample": sample + f"; reference CPU lane (ATen sequences, mp_ops.cpp:2981-3036), "
+                                   f"{threads} threads, median of 3, {t:.3f} s per fwd+bwd"}
+    t0 = time.perf_counter()
+    out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, K)
+    oracle.fanin_reduce_logsumexp_backward(g, rel, flat_src, dst, out, E)
+    t = time.perf_counter() - t0
+    return {"value": round(gbs(nbytes, t), 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": sample + f"; C oracle, 1 thread, {t:.3f} s per fwd+bwd"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1"], default=None,
+                    help="run one workload only and print its figures (for profiling)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the op library has no multi-GPU path: see DESIGN.md for how it would shard).", file=sys.stderr)
+        return 2
+
+    os.environ["RELM_MP_FALLBACK"] = "error"
+    import torch
+
+    from relmo_amd import capi, mp
+    from relmo_amd import synthetic as syn
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    if not mp.available():
+        raise RuntimeError("relm_mp_ops.so failed to load")
+
+    if args.only:
+        fn = {"c2": lambda: bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 1),
+              "c2sum": lambda: bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 0),
+              "c3": lambda: bench_c3(torch, mp, capi, syn, args.steps, args.warmup),
+              "c1": lambda: bench_c1(torch, mp, syn)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
+        return 0
+
+    log("C2 logsumexp fwd+bwd ...")
+    c2 = bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 1)
+    log(f"  {c2['gbs_step']:.0f} GB/s per step; dominant kernel {c2['gbs_bwd_kernel']:.0f} GB/s")
+    extra = {"c2_logsumexp": c2}
+    log("C2 sum fwd+bwd ...")
+    extra["c2_sum"] = bench_c2(torch, mp, capi, syn, max(5, args.steps // 2), 2, 0)
+    log("C3 fanout fwd+bwd ...")
+    extra["c3_fanout"] = bench_c3(torch, mp, capi, syn, max(5, args.steps // 2), 2)
+    log("C1 latencies ...")
+    extra["c1_latency_us"] = bench_c1(torch, mp, syn)
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline ...")
+        baseline = cpu_baseline(syn)
+
+    traffic = load_traffic("lse_bwd_inverse_c2_traffic")
+    bwd_bytes = c2["bytes_bwd"]
+    achieved = gbs(bwd_bytes, c2["ms_bwd_kernel"] / 1e3)
+    roofline = {
+        "bound": "hbm",
+        "kernel": "k_lse_bwd_inv (fanin_reduce_logsumexp_backward, inverse plan)",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": traffic.get("bytes_per_launch") if traffic else None,
+    }
+    ms = c2["ms_step"]
+    line = {
+        "metric": METRIC,
+        "value": round(c2["gbs_step"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: fanin_reduce logsumexp fwd+bwd, 1,048,576 objects, D=32, 16,777,216 messages "
+                        "~N(0,2^2), Zipf(1.1) destinations (unsorted), plans rebuilt every step",
+            "objects": 1 << 20, "messages": 1 << 24, "emb": 32,
+            "bytes_per_step": c2["bytes_fwd"] + c2["bytes_bwd"],
+            "frac_of_peak": round(c2["gbs_step"] / PEAK_HBM_GBS, 4),
+        },
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -59,6 +59,17 @@ enum relm_mp_mode { RELM_MP_MODE_SUM = 0, RELM_MP_MODE_LOGSUMEXP = 1 };
  * below 2^31 - 1 (indices are narrowed to int32 inside plans). */
 #define RELM_MP_MAX_ROWS 2147483646LL
 
+/* CSR plans: segments with more messages than RELM_MP_HUB_THRESHOLD are hubs,
+ * reduced in chunks of RELM_MP_CHUNK_SIZE messages (one workgroup per chunk);
+ * hubs spanning more than RELM_MP_BIG_HUB_CHUNKS chunks combine their chunk
+ * results with a whole workgroup.  The other segments are walked in items:
+ * item j holds the keys whose segment starts in positions
+ * [j * RELM_MP_ITEM_SIZE, (j + 1) * RELM_MP_ITEM_SIZE). */
+#define RELM_MP_HUB_THRESHOLD 64
+#define RELM_MP_CHUNK_SIZE 2048
+#define RELM_MP_BIG_HUB_CHUNKS 64
+#define RELM_MP_ITEM_SIZE 64
+
 const char* relm_mp_last_error(void);
 /* "build_torch=...;build_cuda_tag=cpu;..." is produced by the torch binding;
  * this returns the HIP-side part: "hip=<ver>;arch=gfx950;kernels=..." */
@@ -138,6 +149,8 @@ typedef struct relm_mp_plan {
     int64_t max_degree;      /* CSR: longest segment                           */
     int64_t num_hubs;        /* CSR: segments longer than hub_threshold        */
     int64_t num_chunks;      /* CSR: hub chunks                                */
+    int64_t num_big_hubs;    /* CSR: hubs with more than RELM_MP_BIG_HUB_CHUNKS chunks */
+    int64_t num_items;       /* CSR: walk items (see RELM_MP_ITEM_SIZE)        */
     int32_t* inv;            /* inverse: [num_keys] largest edge id per key or -1 */
     int32_t* offsets;        /* CSR: [num_keys + 1] segment offsets            */
     int32_t* gather_sorted;  /* CSR: [num_edges] gathered row per edge, stable key order */
@@ -145,6 +158,8 @@ typedef struct relm_mp_plan {
     int32_t* hub_key;        /* CSR: [num_hubs] key of each hub                */
     int32_t* hub_chunk_base; /* CSR: [num_hubs] first chunk of each hub        */
     int32_t* chunk_hub;      /* CSR: [num_chunks] hub of each chunk            */
+    int32_t* big_hubs;       /* CSR: [num_big_hubs] hub slots of the big hubs  */
+    int32_t* item_first;     /* CSR: [num_items + 1] first key of each item    */
 } relm_mp_plan;
 
 /* Inverse plan: inv[k] = largest e with keys[e] == k, or -1.  Validates keys

@@ -68,6 +68,8 @@ class Plan(ctypes.Structure):
         ("max_degree", ctypes.c_int64),
         ("num_hubs", ctypes.c_int64),
         ("num_chunks", ctypes.c_int64),
+        ("num_big_hubs", ctypes.c_int64),
+        ("num_items", ctypes.c_int64),
         ("inv", ctypes.c_void_p),
         ("offsets", ctypes.c_void_p),
         ("gather_sorted", ctypes.c_void_p),
@@ -75,6 +77,8 @@ class Plan(ctypes.Structure):
         ("hub_key", ctypes.c_void_p),
         ("hub_chunk_base", ctypes.c_void_p),
         ("chunk_hub", ctypes.c_void_p),
+        ("big_hubs", ctypes.c_void_p),
+        ("item_first", ctypes.c_void_p),
     ]
 
 
@@ -352,6 +356,21 @@ def plan_segment_reduce(bp: BuiltPlan, table: torch.Tensor, mode: int, gathers: 
         )
     )
     return out
+
+
+def plan_logsumexp_backward(bp: BuiltPlan, grad_out: torch.Tensor, out: torch.Tensor, rel_flat: torch.Tensor,
+                            gathers: torch.Tensor | None = None) -> torch.Tensor:
+    emb = grad_out.size(1)
+    grad_rel = torch.empty(bp.plan.num_keys, emb, dtype=rel_flat.dtype, device=rel_flat.device)
+    n = lib().relm_mp_plan_compute_scratch_bytes(ctypes.byref(bp.plan), emb, _dtype(rel_flat), 0)
+    scratch = _bytes(n, rel_flat)
+    check(
+        lib().relm_mp_plan_logsumexp_backward(
+            _dtype(rel_flat), ctypes.byref(bp.plan), _ptr(gathers), _ptr(grad_out), _ptr(out),
+            _ptr(rel_flat), emb, _ptr(grad_rel), _ptr(scratch), scratch.numel(), _stream(rel_flat),
+        )
+    )
+    return grad_rel
 
 
 def plan_gather_last(bp: BuiltPlan, table: torch.Tensor, gathers: torch.Tensor | None = None) -> torch.Tensor:

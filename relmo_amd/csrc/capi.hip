@@ -118,6 +118,9 @@ struct CsrLayout {
     int32_t* hub_key;
     int32_t* hub_chunk_base;
     int32_t* chunk_hub;
+    int32_t* big_hubs;
+    int32_t* item_first;
+    int64_t num_items;
     size_t bytes;
 };
 
@@ -131,16 +134,23 @@ CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
     l.hub_key = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.hub_chunk_base = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.chunk_hub = c.take<int32_t>(static_cast<size_t>(max_chunks(num_edges)));
+    l.big_hubs = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
+    l.num_items = item_capacity_for(num_keys);
+    l.item_first = c.take<int32_t>(static_cast<size_t>(l.num_items) + 1);
     l.bytes = c.used();
     return l;
 }
 
 struct CsrScratch {
     SortBuffers sort;
+    uint32_t* hub_counts;
+    uint32_t* hub_scan_tmp;
+    uint32_t* weights;
+    uint32_t* weight_scan_tmp;
     size_t bytes;
 };
 
-CsrScratch csr_scratch(void* mem, int64_t num_edges) {
+CsrScratch csr_scratch(void* mem, int64_t num_keys, int64_t num_edges) {
     Carver c(mem);
     CsrScratch l;
     const size_t n = static_cast<size_t>(num_edges);
@@ -151,6 +161,11 @@ CsrScratch csr_scratch(void* mem, int64_t num_edges) {
     const size_t hist = sort_hist_words(num_edges);
     l.sort.hist = c.take<uint32_t>(hist);
     l.sort.scan_tmp = c.take<uint32_t>(scan_tmp_words(static_cast<int64_t>(hist)));
+    const size_t hw = hub_list_words(num_keys);
+    l.hub_counts = c.take<uint32_t>(hw);
+    l.hub_scan_tmp = c.take<uint32_t>(scan_tmp_words(static_cast<int64_t>(hw / 4)));
+    l.weights = c.take<uint32_t>(static_cast<size_t>(num_keys) + 1);
+    l.weight_scan_tmp = c.take<uint32_t>(scan_tmp_words(num_keys + 1));
     l.bytes = c.used();
     return l;
 }
@@ -197,7 +212,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_TRY(check_rows(num_edges, "num_edges"));
     if (gathers != nullptr) RELM_TRY(check_rows(gather_bound, "num_gather"));
     const CsrLayout l = csr_layout(plan_mem, key_bound, num_edges);
-    const CsrScratch sc = csr_scratch(scratch, num_edges);
+    const CsrScratch sc = csr_scratch(scratch, key_bound, num_edges);
     if (plan_mem == nullptr || plan_bytes < l.bytes)
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR plan memory too small");
     if (scratch == nullptr || scratch_bytes < sc.bytes)
@@ -215,6 +230,9 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->hub_key = l.hub_key;
     plan->hub_chunk_base = l.hub_chunk_base;
     plan->chunk_hub = l.chunk_hub;
+    plan->big_hubs = l.big_hubs;
+    plan->item_first = l.item_first;
+    plan->num_items = l.num_items;
     RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
     if (num_edges > 0) {
         RELM_HIP(sort_by_key(keys, key_bound, gathers, gather_bound, num_edges, sc.sort,
@@ -225,16 +243,23 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_HIP(launch_offsets_from_sorted(reinterpret_cast<const uint32_t*>(l.keys_sorted), num_edges,
                                         key_bound, l.offsets, s),
              "relm_mp offsets kernel");
-    RELM_HIP(launch_hub_list(l.offsets, key_bound, l.hub_key, l.hub_chunk_base,
-                             max_hubs(num_edges), l.status, s),
-             "relm_mp hub list kernel");
+    RELM_HIP(launch_hub_list(l.offsets, key_bound, l.hub_key, l.hub_chunk_base, l.big_hubs,
+                             max_hubs(num_edges), sc.hub_counts, sc.hub_scan_tmp, l.status, s),
+             "relm_mp hub list kernels");
+    RELM_HIP(launch_item_first(l.offsets, key_bound, sc.weights, sc.weight_scan_tmp, l.item_first,
+                               l.num_items, l.status, s),
+             "relm_mp item kernels");
     DevStatus host{};
     RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
                                gather_name, gather_checked_first, s));
     plan->max_degree = static_cast<int64_t>(host.max_degree);
     plan->num_hubs = static_cast<int64_t>(host.num_hubs);
     plan->num_chunks = static_cast<int64_t>(host.num_chunks);
-    if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges))
+    plan->num_big_hubs = static_cast<int64_t>(host.num_big_hubs);
+    plan->num_items = std::min<int64_t>(static_cast<int64_t>(host.total_weight) / kItemSize + 1,
+                                        l.num_items);
+    if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges) ||
+        plan->num_big_hubs > plan->num_hubs)
         return set_error(RELM_MP_ERR_HIP, "relm_mp: hub list overflow");
     RELM_HIP(launch_chunk_map(l.offsets, l.hub_key, l.hub_chunk_base, plan->num_hubs,
                               plan->num_chunks, l.chunk_hub, s),
@@ -243,7 +268,8 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
 }
 
 size_t csr_total(int64_t num_keys, int64_t num_edges) {
-    return csr_layout(nullptr, num_keys, num_edges).bytes + csr_scratch(nullptr, num_edges).bytes;
+    return csr_layout(nullptr, num_keys, num_edges).bytes +
+           csr_scratch(nullptr, num_keys, num_edges).bytes;
 }
 
 }  // namespace
@@ -269,8 +295,9 @@ const char* relm_mp_last_error(void) { return g_last_error.c_str(); }
 const char* relm_mp_build_info(void) {
     static const std::string info = [] {
         char buf[160];
-        std::snprintf(buf, sizeof(buf), "hip=%d.%d;arch=gfx950;plans=inverse,csr;hub_threshold=%d;chunk=%d",
-                      HIP_VERSION_MAJOR, HIP_VERSION_MINOR, kHubThreshold, kChunkSize);
+        std::snprintf(buf, sizeof(buf),
+                      "hip=%d.%d;arch=gfx950;plans=inverse,csr;hub_threshold=%d;chunk=%d;item=%d",
+                      HIP_VERSION_MAJOR, HIP_VERSION_MINOR, kHubThreshold, kChunkSize, kItemSize);
         return std::string(buf);
     }();
     return info.c_str();
@@ -294,8 +321,7 @@ size_t relm_mp_csr_plan_bytes(int64_t num_keys, int64_t num_edges) {
 }
 
 size_t relm_mp_csr_plan_scratch_bytes(int64_t num_keys, int64_t num_edges) {
-    (void)num_keys;
-    return csr_scratch(nullptr, std::max<int64_t>(num_edges, 0)).bytes;
+    return csr_scratch(nullptr, std::max<int64_t>(num_keys, 0), std::max<int64_t>(num_edges, 0)).bytes;
 }
 
 int relm_mp_csr_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,

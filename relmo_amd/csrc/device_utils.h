@@ -72,6 +72,20 @@ __device__ __forceinline__ float dev_exp<float>(float x) { return expf(x); }
 template <>
 __device__ __forceinline__ double dev_exp<double>(double x) { return exp(x); }
 
+// exp on the hardware exp2 unit (v_exp_f32 of x * log2(e)); relative error
+// grows like |x| * 2^-24, far inside the logsumexp tolerance.  The double
+// version stays the accurate libm-equivalent exp.
+template <typename T>
+__device__ __forceinline__ T fast_exp(T x);
+template <>
+__device__ __forceinline__ float fast_exp<float>(float x) { return __expf(x); }
+template <>
+__device__ __forceinline__ double fast_exp<double>(double x) { return exp(x); }
+
+// Maximum that ignores NaN operands (v_max_f32); NaN is tracked separately.
+template <typename T>
+__device__ __forceinline__ T max_num(T a, T b) { return fmax(a, b); }
+
 template <typename T>
 __device__ __forceinline__ T dev_log(T x);
 template <>

@@ -20,16 +20,19 @@ struct DevStatus {
     unsigned long long num_hubs;         // CSR plans: segments longer than the hub threshold
     unsigned long long num_chunks;       // CSR plans: chunks over all hubs
     unsigned long long max_degree;       // CSR plans: longest segment
-    unsigned long long reserved[2];
+    unsigned long long num_big_hubs;     // CSR plans: hubs over RELM_MP_BIG_HUB_CHUNKS chunks
+    unsigned long long total_weight;     // CSR plans: sum of the walk weights of all keys
 };
 
 constexpr unsigned long long kNoEdge = ~0ull;
 
-// Hub geometry of CSR plans: segments with more than kHubThreshold edges are
-// cut into chunks of kChunkSize edges whose partial results are combined in
-// chunk order.
-constexpr int kHubThreshold = 64;
-constexpr int kChunkSize = 256;
+// Geometry of CSR plans (see relm_mp.h): segments with more than
+// kHubThreshold messages are hubs, reduced in chunks of kChunkSize messages;
+// the others are walked in items of kItemSize positions.
+constexpr int kHubThreshold = RELM_MP_HUB_THRESHOLD;
+constexpr int kChunkSize = RELM_MP_CHUNK_SIZE;
+constexpr int kBigHubChunks = RELM_MP_BIG_HUB_CHUNKS;
+constexpr int kItemSize = RELM_MP_ITEM_SIZE;
 
 // Radix sort geometry (LSD, 8-bit digits at most).
 constexpr int kSortThreads = 256;
@@ -76,9 +79,20 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
 
 hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
                                       int32_t* offsets, hipStream_t s);
+// Hub list (deterministic: hubs in key order) and walk items.  `counts` holds
+// hub_list_words(num_keys) words of scratch, `scan_tmp` scan_tmp_words() of
+// the same length.
+size_t hub_list_words(int64_t num_keys);
 hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
-                           int32_t* hub_chunk_base, int64_t hub_capacity, DevStatus* st,
-                           hipStream_t s);
+                           int32_t* hub_chunk_base, int32_t* big_hubs, int64_t hub_capacity,
+                           uint32_t* counts, uint32_t* scan_tmp, DevStatus* st, hipStream_t s);
+// Walk items balanced by key weight (1 + messages of non-hub keys).
+// `weights` and `scan_tmp` are scratch of num_keys + 1 and scan_tmp_words(num_keys + 1)
+// words; item_first has item_capacity + 1 entries (item_capacity_for(num_keys)).
+int64_t item_capacity_for(int64_t num_keys);
+hipError_t launch_item_first(const int32_t* offsets, int64_t num_keys, uint32_t* weights,
+                             uint32_t* scan_tmp, int32_t* item_first, int64_t item_capacity,
+                             DevStatus* st, hipStream_t s);
 hipError_t launch_chunk_map(const int32_t* offsets, const int32_t* hub_key,
                             const int32_t* hub_chunk_base, int64_t num_hubs, int64_t num_chunks,
                             int32_t* chunk_hub, hipStream_t s);

@@ -38,8 +38,8 @@ __global__ void k_status_init(DevStatus* st) {
         st->num_hubs = 0;
         st->num_chunks = 0;
         st->max_degree = 0;
-        st->reserved[0] = 0;
-        st->reserved[1] = 0;
+        st->num_big_hubs = 0;
+        st->total_weight = 0;
     }
 }
 
@@ -162,19 +162,28 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const void* __re
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
     const uint32_t dmask = (1u << bits) - 1u;
     unsigned long long bad = kNoEdge;
+    uint32_t key[kSortItems];
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+        key[i] = 0;
+        if (p < n) {
+            if constexpr (kFirst) {
+                const int64_t k = static_cast<const int64_t*>(keys)[p];
+                if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound))
+                    bad = min(bad, static_cast<unsigned long long>(p));
+                else
+                    key[i] = static_cast<uint32_t>(k);
+            } else {
+                key[i] = static_cast<const uint32_t*>(keys)[p];
+            }
+        }
+    }
+#pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
         const bool active = p < n;
-        uint32_t d = 0;
-        if (active) {
-            if constexpr (kFirst) {
-                const int64_t k = static_cast<const int64_t*>(keys)[p];
-                if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound)) {
-                    bad = min(bad, static_cast<unsigned long long>(p));
-                }
-            }
-            d = (load_key<kFirst>(keys, p, key_bound, st) >> shift) & dmask;
-        }
+        const uint32_t d = (key[i] >> shift) & dmask;
         const unsigned long long peers = match_digit(d, bits, __ballot(active));
         if (active && (peers & lanemask_lt()) == 0) atomicAdd(&h[d], __popcll(peers));
     }
@@ -214,21 +223,20 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
     unsigned long long bad = kNoEdge;
+    const int64_t wave_base = tile_base + wave * kPerWave + lane;
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
-        const int64_t p = tile_base + wave * kPerWave + r * kWave + lane;
-        const bool active = p < n;
+        const int64_t p = wave_base + r * kWave;
         uint32_t k = 0, v = 0;
-        if (active) {
+        if (p < n) {
             k = load_key<kFirst>(keys, p, key_bound, st);
             if constexpr (kFirst) {
                 if (vals != nullptr) {
                     const int64_t g = static_cast<const int64_t*>(vals)[p];
-                    if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound)) {
+                    if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound))
                         bad = min(bad, static_cast<unsigned long long>(p));
-                    } else {
+                    else
                         v = static_cast<uint32_t>(g);
-                    }
                 } else {
                     v = static_cast<uint32_t>(p);
                 }
@@ -238,7 +246,11 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
         }
         key[r] = k;
         val[r] = v;
-        const uint32_t d = (k >> shift) & dmask;
+    }
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const bool active = wave_base + r * kWave < n;
+        const uint32_t d = (key[r] >> shift) & dmask;
         const unsigned long long peers = match_digit(d, bits, __ballot(active));
         const uint32_t below = __popcll(peers & lanemask_lt());
         uint32_t before = 0;
@@ -306,34 +318,156 @@ __global__ __launch_bounds__(kThreads) void k_offsets_from_sorted(const uint32_t
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_hub_list(const int32_t* __restrict__ offsets,
-                                                       int64_t num_keys,
-                                                       int32_t* __restrict__ hub_key,
-                                                       int32_t* __restrict__ hub_chunk_base,
-                                                       int64_t hub_capacity,
-                                                       DevStatus* __restrict__ st) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    unsigned long long maxdeg = 0;
-    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k < num_keys;
-         k += stride) {
-        const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
-        if (deg > 0 && static_cast<unsigned long long>(deg) > maxdeg) maxdeg = deg;
-        if (deg > kHubThreshold) {
-            const unsigned long long slot = atomicAdd(&st->num_hubs, 1ull);
-            const unsigned long long nch = (deg + kChunkSize - 1) / kChunkSize;
-            const unsigned long long base = atomicAdd(&st->num_chunks, nch);
-            if (slot < static_cast<unsigned long long>(hub_capacity)) {
-                hub_key[slot] = static_cast<int32_t>(k);
-                hub_chunk_base[slot] = static_cast<int32_t>(base);
-            }
+// Hub list in two passes over the segment sizes, without global atomics:
+// k_hub_count writes per-block counts (hubs, chunks, big hubs) and the block's
+// longest segment; the counts are scanned; k_hub_write gives every hub its
+// slot (hubs in key order) and chunk range.
+struct HubFlags {
+    uint32_t hub;
+    uint32_t chunks;
+    uint32_t big;
+    int64_t deg;
+};
+
+__device__ __forceinline__ HubFlags hub_flags(const int32_t* __restrict__ offsets, int64_t k,
+                                              int64_t num_keys) {
+    HubFlags f{0u, 0u, 0u, 0};
+    if (k < num_keys) f.deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
+    if (f.deg > kHubThreshold) {
+        f.hub = 1u;
+        f.chunks = static_cast<uint32_t>((f.deg + kChunkSize - 1) / kChunkSize);
+        f.big = f.chunks > static_cast<uint32_t>(kBigHubChunks) ? 1u : 0u;
+    }
+    return f;
+}
+
+__global__ __launch_bounds__(kThreads) void k_hub_count(const int32_t* __restrict__ offsets,
+                                                        int64_t num_keys, int64_t nblk,
+                                                        uint32_t* __restrict__ counts) {
+    __shared__ uint32_t lds[kThreads / kWave];
+    __shared__ uint32_t wmax[kThreads / kWave];
+    const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const HubFlags f = hub_flags(offsets, k, num_keys);
+    uint32_t th, tc, tb;
+    block_inclusive_scan<kThreads>(f.hub, lds, th);
+    block_inclusive_scan<kThreads>(f.chunks, lds, tc);
+    block_inclusive_scan<kThreads>(f.big, lds, tb);
+    uint32_t m = f.deg > 0 ? static_cast<uint32_t>(f.deg) : 0u;
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        const uint32_t other = __shfl_xor(m, o, kWave);
+        m = other > m ? other : m;
+    }
+    if (lane_id() == 0) wmax[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t mm = 0;
+        for (int w = 0; w < kThreads / kWave; ++w) mm = wmax[w] > mm ? wmax[w] : mm;
+        const int64_t stride = nblk + 1;
+        counts[blockIdx.x] = th;
+        counts[stride + blockIdx.x] = tc;
+        counts[2 * stride + blockIdx.x] = tb;
+        counts[3 * stride + blockIdx.x] = mm;
+        if (blockIdx.x == 0) {
+            counts[nblk] = 0;
+            counts[stride + nblk] = 0;
+            counts[2 * stride + nblk] = 0;
         }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_hub_write(const int32_t* __restrict__ offsets,
+                                                        int64_t num_keys, int64_t nblk,
+                                                        const uint32_t* __restrict__ counts,
+                                                        int32_t* __restrict__ hub_key,
+                                                        int32_t* __restrict__ hub_chunk_base,
+                                                        int32_t* __restrict__ big_hubs,
+                                                        int64_t hub_capacity) {
+    __shared__ uint32_t lds[kThreads / kWave];
+    const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const HubFlags f = hub_flags(offsets, k, num_keys);
+    uint32_t th, tc, tb;
+    const uint32_t ih = block_inclusive_scan<kThreads>(f.hub, lds, th);
+    const uint32_t ic = block_inclusive_scan<kThreads>(f.chunks, lds, tc);
+    const uint32_t ib = block_inclusive_scan<kThreads>(f.big, lds, tb);
+    if (!f.hub) return;
+    const int64_t stride = nblk + 1;
+    const int64_t slot = static_cast<int64_t>(counts[blockIdx.x]) + ih - 1;
+    if (slot < 0 || slot >= hub_capacity) return;
+    hub_key[slot] = static_cast<int32_t>(k);
+    hub_chunk_base[slot] = static_cast<int32_t>(counts[stride + blockIdx.x] + ic - f.chunks);
+    if (f.big) {
+        const int64_t b = static_cast<int64_t>(counts[2 * stride + blockIdx.x]) + ib - 1;
+        if (b >= 0 && b < hub_capacity) big_hubs[b] = static_cast<int32_t>(slot);
+    }
+}
+
+// Totals of the scanned counts and the longest segment into the status.
+__global__ __launch_bounds__(kThreads) void k_hub_totals(const uint32_t* __restrict__ counts,
+                                                         int64_t nblk, DevStatus* __restrict__ st) {
+    const int64_t stride = nblk + 1;
+    uint32_t m = 0;
+    for (int64_t b = threadIdx.x; b < nblk; b += kThreads) {
+        const uint32_t v = counts[3 * stride + b];
+        m = v > m ? v : m;
     }
 #pragma unroll
     for (int o = kWave / 2; o > 0; o >>= 1) {
-        const unsigned long long other = __shfl_xor(maxdeg, o, kWave);
-        maxdeg = other > maxdeg ? other : maxdeg;
+        const uint32_t other = __shfl_xor(m, o, kWave);
+        m = other > m ? other : m;
     }
-    if (lane_id() == 0 && maxdeg != 0) atomicMax(&st->max_degree, maxdeg);
+    __shared__ uint32_t wmax[kThreads / kWave];
+    if (lane_id() == 0) wmax[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t mm = 0;
+        for (int w = 0; w < kThreads / kWave; ++w) mm = wmax[w] > mm ? wmax[w] : mm;
+        st->max_degree = mm;
+        st->num_hubs = counts[nblk];
+        st->num_chunks = counts[stride + nblk];
+        st->num_big_hubs = counts[2 * stride + nblk];
+    }
+}
+
+// Walk items are balanced by a per-key weight: 1 (the key's output row) plus
+// its messages for non-hub keys (hub messages are reduced elsewhere).  With
+// W the exclusive scan of the weights (W[num_keys] = total),
+// item_first[j] = first key k with W[k] >= j * kItemSize, and
+// item_first[num_items] = num_keys.
+__global__ __launch_bounds__(kThreads) void k_item_weights(const int32_t* __restrict__ offsets,
+                                                           int64_t num_keys,
+                                                           uint32_t* __restrict__ w) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k <= num_keys;
+         k += stride) {
+        uint32_t v = 0;
+        if (k < num_keys) {
+            const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
+            v = 1u + (deg > 0 && deg <= kHubThreshold ? static_cast<uint32_t>(deg) : 0u);
+        }
+        w[k] = v;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_item_first(const uint32_t* __restrict__ W,
+                                                         int64_t num_keys,
+                                                         int32_t* __restrict__ item_first,
+                                                         int64_t num_items,
+                                                         DevStatus* __restrict__ st) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k <= num_keys;
+         k += stride) {
+        const int64_t o = W[k];
+        const int64_t op = k == 0 ? -1 : static_cast<int64_t>(W[k - 1]);
+        // items j with op < j * kItemSize <= o (weights are at most kHubThreshold + 1,
+        // so a key covers at most two items)
+        const int64_t j0 = op < 0 ? 0 : op / kItemSize + 1;
+        // the key past the end also closes the last used item (j = total / kItemSize + 1)
+        int64_t j1 = k == num_keys ? o / kItemSize + 1 : o / kItemSize;
+        if (j1 > num_items) j1 = num_items;
+        for (int64_t j = j0; j <= j1; ++j) item_first[j] = static_cast<int32_t>(k);
+        if (k == num_keys) st->total_weight = static_cast<unsigned long long>(o);
+    }
 }
 
 // chunk_hub[hub_chunk_base[h] + j] = h for the chunks of hub h (one block per hub).
@@ -348,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_map(const int32_t* __restric
         const int64_t nch = (deg + kChunkSize - 1) / kChunkSize;
         const int64_t base = hub_chunk_base[h];
         for (int64_t j = threadIdx.x; j < nch; j += blockDim.x) {
-            if (base + j < num_chunks) chunk_hub[base + j] = static_cast<int32_t>(h);
+            if (base + j >= 0 && base + j < num_chunks) chunk_hub[base + j] = static_cast<int32_t>(h);
         }
     }
 }
@@ -461,12 +595,50 @@ hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, in
     return hipGetLastError();
 }
 
+size_t hub_list_words(int64_t num_keys) {
+    const int64_t nblk = std::max<int64_t>(1, (num_keys + kThreads - 1) / kThreads);
+    return static_cast<size_t>(4 * (nblk + 1));
+}
+
 hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
-                           int32_t* hub_chunk_base, int64_t hub_capacity, DevStatus* st,
-                           hipStream_t s) {
+                           int32_t* hub_chunk_base, int32_t* big_hubs, int64_t hub_capacity,
+                           uint32_t* counts, uint32_t* scan_tmp, DevStatus* st, hipStream_t s) {
     if (num_keys <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_hub_list, dim3(grid_1d(num_keys, kThreads * 4)), dim3(kThreads), 0, s,
-                       offsets, num_keys, hub_key, hub_chunk_base, hub_capacity, st);
+    const int64_t nblk = (num_keys + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(k_hub_count, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
+                       num_keys, nblk, counts);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    for (int a = 0; a < 3; ++a) {
+        err = launch_exclusive_scan_u32(counts + a * (nblk + 1), nblk + 1, scan_tmp, s);
+        if (err != hipSuccess) return err;
+    }
+    hipLaunchKernelGGL(k_hub_write, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
+                       num_keys, nblk, static_cast<const uint32_t*>(counts), hub_key, hub_chunk_base,
+                       big_hubs, hub_capacity);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_hub_totals, dim3(1), dim3(kThreads), 0, s, static_cast<const uint32_t*>(counts),
+                       nblk, st);
+    return hipGetLastError();
+}
+
+int64_t item_capacity_for(int64_t num_keys) {
+    return num_keys * (kHubThreshold + 1) / kItemSize + 1;
+}
+
+hipError_t launch_item_first(const int32_t* offsets, int64_t num_keys, uint32_t* weights,
+                             uint32_t* scan_tmp, int32_t* item_first, int64_t item_capacity,
+                             DevStatus* st, hipStream_t s) {
+    hipLaunchKernelGGL(k_item_weights, dim3(grid_1d(num_keys + 1, kThreads * 4)), dim3(kThreads), 0,
+                       s, offsets, num_keys, weights);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    err = launch_exclusive_scan_u32(weights, num_keys + 1, scan_tmp, s);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_item_first, dim3(grid_1d(num_keys + 1, kThreads)), dim3(kThreads), 0, s,
+                       static_cast<const uint32_t*>(weights), num_keys, item_first, item_capacity,
+                       st);
     return hipGetLastError();
 }
 

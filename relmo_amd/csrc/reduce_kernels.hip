@@ -1,13 +1,24 @@
 // Row kernels of the relational message-passing ops.
 //
-// Every output row is written exactly once by one "row group" of G lanes
-// (G = 4..64, a divisor of the wave), each lane moving V contiguous elements
-// (float4 / double2 when the rows allow it).  Rows wider than G*V are split
-// over blockIdx.y slices.  No atomics: a key's messages are visited in the
-// stable (edge) order of the plan, so results are deterministic and, for
-// segments up to kHubThreshold messages, the fp32 sums are bit-identical to a
-// sequential loop in edge order.  Longer segments ("hubs") are cut into chunks
-// of kChunkSize messages; chunk partials are combined in chunk order.
+// Every output row is owned by exactly one "row group" of G lanes (G = 4..64,
+// a divisor of the wave), each lane moving V contiguous elements (float4 /
+// double2 when the rows allow it); rows wider than G*V are split over
+// blockIdx.y slices.  No atomics anywhere: the messages of a key are visited
+// in the stable (edge) order of the plan, so every result is deterministic.
+//
+// CSR plans are reduced in two parts:
+//  * segments of at most kHubThreshold messages: k_walk_items.  Item j holds
+//    the keys whose segment starts in positions [j*kItemSize, (j+1)*kItemSize),
+//    so every row group gets a similar number of messages; the group walks its
+//    keys in order, each key's messages sequentially in edge order, which makes
+//    the fp32 sums bit-identical to the reference's sequential CPU loop.  The
+//    item's offsets and gathered indices are prefetched G at a time and handed
+//    out with group shuffles, leaving one memory round trip per batch of rows.
+//  * hubs: k_hub_chunks, one workgroup per chunk of kChunkSize messages; each
+//    row group folds a contiguous slice, the slices are folded in slice order.
+//    Single-chunk hubs are finished there; the others leave chunk partials that
+//    k_hub_combine_small (one row group per hub) or k_hub_combine_big (one
+//    1024-thread workgroup per hub) fold in chunk order.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -21,168 +32,244 @@ namespace relm_mp {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int64_t kMaxBlocksX = 1 << 22;  // keeps blocks * 256 threads below 2^32
+constexpr int kBigThreads = 1024;
+constexpr int kRowsInFlight = 4;          // rows per row group per iteration (inverse plans)
+constexpr int64_t kMaxBlocksX = 1 << 22;  // keeps blocks * 1024 threads below 2^32
 
 template <int G>
 constexpr int batch_rows() {
     return G < 8 ? G : 8;
 }
 
-struct Span {
-    int64_t beg;
-    int64_t end;
-};
-
-__device__ __forceinline__ Span segment(const int32_t* __restrict__ offsets, int64_t key,
-                                        int64_t num_edges) {
-    int64_t b = offsets[key];
-    int64_t e = offsets[key + 1];
-    b = b < 0 ? 0 : (b > num_edges ? num_edges : b);
-    e = e < b ? b : (e > num_edges ? num_edges : e);
-    return {b, e};
+template <typename T, int V>
+__device__ __forceinline__ void pack_add(Pack<T, V>& a, const Pack<T, V>& b) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) a.v[i] = a.v[i] + b.v[i];
 }
 
-// ---- accumulators --------------------------------------------------------
+// ---- partial results -----------------------------------------------------
 
 template <typename T, int V>
-struct SumAcc {
-    Pack<T, V> acc;
-    __device__ __forceinline__ void init() { acc = pack_fill<T, V>(T(0)); }
-    template <int U>
-    __device__ __forceinline__ void batch(const Pack<T, V> (&x)[U], int valid) {
+struct SumPartial {
+    Pack<T, V> a;
+    static constexpr int kWords = 1;  // Packs per stored partial
+    __device__ __forceinline__ static SumPartial identity() { return {pack_fill<T, V>(T(0))}; }
+    __device__ __forceinline__ void merge(const SumPartial& o) { pack_add(a, o.a); }
+    __device__ __forceinline__ void store(T* p, int64_t D, int64_t col) const { pack_store<T, V>(p + col, a); }
+    __device__ __forceinline__ static SumPartial load(const T* p, int64_t D, int64_t col) {
+        return {pack_load<T, V>(p + col)};
+    }
+    __device__ __forceinline__ Pack<T, V> value() const { return a; }
+};
+
+// (m, s): maximum of the messages and the sum of exp(x - m); s is NaN when a
+// message was NaN.  Merging rescales both sums to the larger maximum.
+template <typename T, int V>
+struct LsePartial {
+    Pack<T, V> m;
+    Pack<T, V> s;
+    static constexpr int kWords = 2;
+    __device__ __forceinline__ static LsePartial identity() {
+        return {pack_fill<T, V>(neg_inf<T>()), pack_fill<T, V>(T(0))};
+    }
+    __device__ __forceinline__ void merge(const LsePartial& o) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (u < valid) {
-#pragma unroll
-                for (int i = 0; i < V; ++i) acc.v[i] = acc.v[i] + x[u].v[i];
+        for (int i = 0; i < V; ++i) {
+            const T M = max_num(m.v[i], o.m.v[i]);
+            if (M == neg_inf<T>()) {
+                s.v[i] = (s.v[i] != s.v[i]) ? s.v[i] : (o.s.v[i] != o.s.v[i] ? o.s.v[i] : T(0));
+            } else {
+                s.v[i] = s.v[i] * fast_exp<T>(m.v[i] - M) + o.s.v[i] * fast_exp<T>(o.m.v[i] - M);
             }
+            m.v[i] = M;
         }
+    }
+    __device__ __forceinline__ void store(T* p, int64_t D, int64_t col) const {
+        pack_store<T, V>(p + col, m);
+        pack_store<T, V>(p + D + col, s);
+    }
+    __device__ __forceinline__ static LsePartial load(const T* p, int64_t D, int64_t col) {
+        return {pack_load<T, V>(p + col), pack_load<T, V>(p + D + col)};
+    }
+    // Result of a non-empty segment.
+    __device__ __forceinline__ Pack<T, V> value() const {
+        Pack<T, V> r;
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+            r.v[i] = m.v[i] == neg_inf<T>() ? quiet_nan<T>() : dev_log<T>(s.v[i]) + m.v[i];
+        return r;
     }
 };
 
-// Blocked max-then-sum: per batch of rows, the batch maximum first, then the
-// exponentials against the running maximum.  s is kept relative to m; while
-// m is -inf, s stays 0.
-template <typename T, int V>
-struct LseAcc {
-    Pack<T, V> m;
-    Pack<T, V> s;
-    __device__ __forceinline__ void init() {
+// ---- ops: what is accumulated per message ----------------------------------
+
+// Sum of table rows.
+template <typename T, int V, int U>
+struct SumOp {
+    using Partial = SumPartial<T, V>;
+    const T* __restrict__ table;
+    int64_t D;
+    int64_t col;
+    bool colok;
+    Pack<T, V> x[U];
+    Pack<T, V> acc;
+
+    __device__ __forceinline__ void begin(int64_t, bool) { acc = pack_fill<T, V>(T(0)); }
+    __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + static_cast<int64_t>(idx[u]) * D + col)
+                                      : pack_fill<T, V>(T(0));
+    }
+    __device__ __forceinline__ void consume(int cnt) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (u < cnt) pack_add(acc, x[u]);
+    }
+    __device__ __forceinline__ Pack<T, V> result(bool) const { return acc; }
+    __device__ __forceinline__ Partial partial() const { return {acc}; }
+};
+
+// Logsumexp of table rows as a blocked max-then-sum: per batch the batch
+// maximum first, then exp(x - max) summed against the running maximum (s is
+// kept relative to m and rescaled when m grows).  Semantics of the reference's
+// amax / exp / sum / log sequence: a NaN message makes the result NaN (tracked
+// in `nan`, because the maximum ignores NaN), messages that are all -inf give
+// NaN, an empty segment -inf.
+template <typename T, int V, int U>
+struct LseOp {
+    using Partial = LsePartial<T, V>;
+    const T* __restrict__ table;
+    int64_t D;
+    int64_t col;
+    bool colok;
+    Pack<T, V> x[U];
+    Pack<T, V> m, s, nan;
+
+    __device__ __forceinline__ void begin(int64_t, bool) {
         m = pack_fill<T, V>(neg_inf<T>());
         s = pack_fill<T, V>(T(0));
+        nan = pack_fill<T, V>(T(0));
     }
-    template <int U>
-    __device__ __forceinline__ void batch(const Pack<T, V> (&x)[U], int valid) {
+    __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + static_cast<int64_t>(idx[u]) * D + col)
+                                      : pack_fill<T, V>(neg_inf<T>());
+    }
+    __device__ __forceinline__ void consume(int cnt) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             T mb = neg_inf<T>();
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                if (u < valid) mb = max_nan(mb, x[u].v[i]);
-            const T nm = max_nan(m.v[i], mb);
+                if (u < cnt) mb = max_num(mb, x[u].v[i]);
+            const T nm = max_num(m.v[i], mb);
             if (nm != neg_inf<T>()) {
-                T acc = s.v[i] * dev_exp<T>(m.v[i] - nm);
+                T acc = s.v[i] * fast_exp<T>(m.v[i] - nm);
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    if (u < valid) acc = acc + dev_exp<T>(x[u].v[i] - nm);
+                    if (u < cnt) acc = acc + fast_exp<T>(x[u].v[i] - nm);
                 s.v[i] = acc;
                 m.v[i] = nm;
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (u < cnt && x[u].v[i] != x[u].v[i]) nan.v[i] = T(1);
             }
         }
     }
+    __device__ __forceinline__ Pack<T, V> result(bool nonempty) const {
+        Pack<T, V> r;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            if (!nonempty)
+                r.v[i] = neg_inf<T>();
+            else if (nan.v[i] != T(0) || m.v[i] == neg_inf<T>())
+                r.v[i] = quiet_nan<T>();
+            else
+                r.v[i] = dev_log<T>(s.v[i]) + m.v[i];
+        }
+        return r;
+    }
+    __device__ __forceinline__ Partial partial() const {
+        Partial p{m, s};
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+            if (nan.v[i] != T(0)) p.s.v[i] = quiet_nan<T>();
+        return p;
+    }
 };
 
-// grad_out[d] * exp(x_r - out[d]) accumulated in edge order.
-template <typename T, int V>
-struct LseBwdAcc {
-    Pack<T, V> acc;
-    Pack<T, V> xr;
-    __device__ __forceinline__ void init() { acc = pack_fill<T, V>(T(0)); }
-    template <int U>
-    __device__ __forceinline__ void batch2(const Pack<T, V> (&g)[U], const Pack<T, V> (&o)[U],
-                                           int valid) {
+// Logsumexp backward of key r (= a rel row): sum over its messages of
+// grad_out[d] * exp(rel[r] - out[d]), d the gathered row, in edge order.
+template <typename T, int V, int U>
+struct LseBwdOp {
+    using Partial = SumPartial<T, V>;
+    const T* __restrict__ grad_out;
+    const T* __restrict__ out;
+    const T* __restrict__ rel;
+    int64_t D;
+    int64_t col;
+    bool colok;
+    Pack<T, V> g[U], o[U];
+    Pack<T, V> xr, acc;
+
+    __device__ __forceinline__ void begin(int64_t key, bool nonempty) {
+        acc = pack_fill<T, V>(T(0));
+        xr = (colok && nonempty) ? pack_load<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
+    }
+    __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (u < valid) {
+            const bool ok = u < cnt && colok;
+            const int64_t off = static_cast<int64_t>(idx[u]) * D + col;
+            g[u] = ok ? pack_load<T, V>(grad_out + off) : pack_fill<T, V>(T(0));
+            o[u] = ok ? pack_load<T, V>(out + off) : pack_fill<T, V>(T(0));
+        }
+    }
+    __device__ __forceinline__ void consume(int cnt) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (u < cnt) {
 #pragma unroll
                 for (int i = 0; i < V; ++i) {
-                    const T w = dev_exp<T>(xr.v[i] - o[u].v[i]);
+                    const T w = fast_exp<T>(xr.v[i] - o[u].v[i]);
                     const T c = g[u].v[i] * w;
                     acc.v[i] = acc.v[i] + c;
                 }
             }
         }
     }
+    __device__ __forceinline__ Pack<T, V> result(bool) const { return acc; }
+    __device__ __forceinline__ Partial partial() const { return {acc}; }
 };
 
-template <typename T, int V>
-__device__ __forceinline__ Pack<T, V> lse_finish(const LseAcc<T, V>& a, bool nonempty) {
-    Pack<T, V> r;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-        if (!nonempty) {
-            r.v[i] = neg_inf<T>();
-        } else if (a.m.v[i] == neg_inf<T>()) {
-            r.v[i] = quiet_nan<T>();  // every message is -inf: exp(-inf - -inf) is NaN
-        } else {
-            r.v[i] = dev_log<T>(a.s.v[i]) + a.m.v[i];
-        }
-    }
-    return r;
+// ---- shared walking helpers -------------------------------------------------
+
+__device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// Visits positions [beg, end) of `gs` in order, in batches of U rows of
-// `table` (row index = gs[pos]); lanes of the group load the batch's indices
-// cooperatively and broadcast them with a group shuffle.
-template <typename T, int V, int G, typename Acc>
-__device__ __forceinline__ void reduce_rows(Acc& acc, const int32_t* __restrict__ gs, int64_t beg,
-                                            int64_t end, const T* __restrict__ table, int64_t D,
-                                            int64_t col, bool colok, int gl) {
-    constexpr int U = batch_rows<G>();
-    for (int64_t i = beg; i < end; i += G) {
-        const int cnt = static_cast<int>(end - i < G ? end - i : G);
-        const int32_t my = gl < cnt ? gs[i + gl] : 0;
-        for (int t0 = 0; t0 < cnt; t0 += U) {
-            Pack<T, V> x[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int32_t g = __shfl(my, t0 + u, G);
-                if (t0 + u < cnt && colok)
-                    x[u] = pack_load<T, V>(table + static_cast<int64_t>(g) * D + col);
-                else
-                    x[u] = pack_fill<T, V>(T(0));
-            }
-            if (colok) acc.template batch<U>(x, cnt - t0);
+// Feeds positions [beg, end) of `gs` to `op` in batches of U, in order.  The
+// gathered indices are fetched G at a time into a register window that
+// survives across calls (`gbase`, `gwin`).
+template <int G, int U, class Op>
+__device__ __forceinline__ void feed(Op& op, const int32_t* __restrict__ gs, int64_t num_edges,
+                                     int64_t beg, int64_t end, int64_t& gbase, int32_t& gwin,
+                                     int gl) {
+    for (int64_t p = beg; p < end; p += U) {
+        const int cnt = static_cast<int>(end - p < U ? end - p : U);
+        if (p < gbase || p + cnt > gbase + G) {
+            gbase = p;
+            gwin = gbase + gl < num_edges ? gs[gbase + gl] : 0;
         }
-    }
-}
-
-template <typename T, int V, int G>
-__device__ __forceinline__ void reduce_rows_lse_bwd(LseBwdAcc<T, V>& acc,
-                                                    const int32_t* __restrict__ gs, int64_t beg,
-                                                    int64_t end, const T* __restrict__ grad_out,
-                                                    const T* __restrict__ out, int64_t D,
-                                                    int64_t col, bool colok, int gl) {
-    constexpr int U = batch_rows<G>();
-    for (int64_t i = beg; i < end; i += G) {
-        const int cnt = static_cast<int>(end - i < G ? end - i : G);
-        const int32_t my = gl < cnt ? gs[i + gl] : 0;
-        for (int t0 = 0; t0 < cnt; t0 += U) {
-            Pack<T, V> g[U], o[U];
+        int32_t idx[U];
+        const int off = static_cast<int>(p - gbase);
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int32_t d = __shfl(my, t0 + u, G);
-                if (t0 + u < cnt && colok) {
-                    const int64_t off = static_cast<int64_t>(d) * D + col;
-                    g[u] = pack_load<T, V>(grad_out + off);
-                    o[u] = pack_load<T, V>(out + off);
-                } else {
-                    g[u] = pack_fill<T, V>(T(0));
-                    o[u] = pack_fill<T, V>(T(0));
-                }
-            }
-            if (colok) acc.template batch2<U>(g, o, cnt - t0);
-        }
+        for (int u = 0; u < U; ++u) idx[u] = __shfl(gwin, off + u < G ? off + u : G - 1, G);
+        op.load(idx, cnt);
+        op.consume(cnt);
     }
 }
 
@@ -196,8 +283,197 @@ __global__ __launch_bounds__(kThreads) void k_fill(T* __restrict__ p, int64_t n,
         p[i] = value;
 }
 
+// Keys with at most kHubThreshold messages, walked item by item.
+template <typename T, int V, int G, class Op>
+__global__ __launch_bounds__(kThreads) void k_walk_items(
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs,
+    const int32_t* __restrict__ item_first, int64_t num_items, int64_t num_keys,
+    int64_t num_edges, T* __restrict__ out, Op op) {
+    constexpr int R = kThreads / G;
+    constexpr int U = batch_rows<G>();
+    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
+    op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
+    op.colok = op.col < op.D;
+    const int64_t D = op.D;
+    for (int64_t item = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; item < num_items;
+         item += static_cast<int64_t>(gridDim.x) * R) {
+        const int64_t kb = clamp64(item_first[item], 0, num_keys);
+        const int64_t ke = clamp64(item_first[item + 1], kb, num_keys);
+        if (kb >= ke) continue;
+        int64_t wbase = kb;
+        int32_t woff = offsets[wbase + gl < num_keys ? wbase + gl : num_keys];
+        int64_t beg = clamp64(__shfl(woff, 0, G), 0, num_edges);
+        int64_t gbase = beg;
+        int32_t gwin = gbase + gl < num_edges ? gs[gbase + gl] : 0;
+        for (int64_t k = kb; k < ke; ++k) {
+            if (k + 1 - wbase >= G) {
+                wbase = k;
+                woff = offsets[wbase + gl < num_keys ? wbase + gl : num_keys];
+            }
+            const int64_t end = clamp64(__shfl(woff, static_cast<int>(k + 1 - wbase), G), beg, num_edges);
+            if (end - beg <= kHubThreshold) {
+                op.begin(k, end > beg);
+                feed<G, U>(op, gs, num_edges, beg, end, gbase, gwin, gl);
+                if (op.colok) pack_store_stream<T, V>(out + k * D + op.col, op.result(end > beg));
+            }
+            beg = end;
+        }
+    }
+}
+
+struct HubChunk {
+    int64_t key;
+    int64_t beg;
+    int64_t end;
+    int64_t nch;
+    bool ok;
+};
+
+__device__ __forceinline__ HubChunk hub_chunk(int64_t c, const int32_t* __restrict__ offsets,
+                                              const int32_t* __restrict__ hub_key,
+                                              const int32_t* __restrict__ hub_chunk_base,
+                                              const int32_t* __restrict__ chunk_hub,
+                                              int64_t num_hubs, int64_t num_edges) {
+    HubChunk hc{0, 0, 0, 0, false};
+    const int64_t h = chunk_hub[c];
+    if (h < 0 || h >= num_hubs) return hc;
+    hc.key = hub_key[h];
+    const int64_t j = c - hub_chunk_base[h];
+    const int64_t sb = clamp64(offsets[hc.key], 0, num_edges);
+    const int64_t se = clamp64(offsets[hc.key + 1], sb, num_edges);
+    hc.nch = (se - sb + kChunkSize - 1) / kChunkSize;
+    hc.beg = clamp64(sb + j * kChunkSize, sb, se);
+    hc.end = clamp64(hc.beg + kChunkSize, hc.beg, se);
+    hc.ok = true;
+    return hc;
+}
+
+// One workgroup per hub chunk: row group g folds slice g of the chunk, the
+// slices are folded in order by group 0; a single-chunk hub is finished here.
+template <typename T, int V, int G, class Op>
+__global__ __launch_bounds__(kThreads) void k_hub_chunks(
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_edges,
+    const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
+    const int32_t* __restrict__ chunk_hub, int64_t num_hubs, int64_t num_chunks,
+    T* __restrict__ partial, T* __restrict__ out, Op op) {
+    using Partial = typename Op::Partial;
+    constexpr int NG = kThreads / G;
+    constexpr int U = batch_rows<G>();
+    __shared__ Partial red[kThreads];
+    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
+    const int grp = static_cast<int>(threadIdx.x) / G;
+    op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
+    op.colok = op.col < op.D;
+    const int64_t D = op.D;
+    constexpr int64_t kPer = (kChunkSize + NG - 1) / NG;
+    for (int64_t c = blockIdx.x; c < num_chunks; c += gridDim.x) {
+        const HubChunk hc =
+            hub_chunk(c, offsets, hub_key, hub_chunk_base, chunk_hub, num_hubs, num_edges);
+        const int64_t lo = hc.ok ? clamp64(hc.beg + grp * kPer, hc.beg, hc.end) : 0;
+        const int64_t hi = hc.ok ? clamp64(lo + kPer, lo, hc.end) : 0;
+        op.begin(hc.key, hc.ok && hi > lo);
+        int64_t gbase = lo;
+        int32_t gwin = gbase + gl < num_edges ? gs[gbase + gl] : 0;
+        feed<G, U>(op, gs, num_edges, lo, hi, gbase, gwin, gl);
+        red[threadIdx.x] = hi > lo ? op.partial() : Partial::identity();
+        __syncthreads();
+        if (grp == 0 && hc.ok && op.colok) {
+            const int active = static_cast<int>((hc.end - hc.beg + kPer - 1) / kPer);
+            Partial acc = red[gl];
+            for (int g = 1; g < active && g < NG; ++g) acc.merge(red[g * G + gl]);
+            if (hc.nch == 1)
+                pack_store<T, V>(out + hc.key * D + op.col, acc.value());
+            else
+                acc.store(partial + c * Partial::kWords * D, D, op.col);
+        }
+        __syncthreads();
+    }
+}
+
+template <class Partial, typename T, int U>
+__device__ __forceinline__ Partial fold_partials(const T* __restrict__ partial, int64_t lo,
+                                                 int64_t hi, int64_t D, int64_t col) {
+    Partial acc = Partial::identity();
+    for (int64_t c0 = lo; c0 < hi; c0 += U) {
+        Partial x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            x[u] = c0 + u < hi ? Partial::load(partial + (c0 + u) * Partial::kWords * D, D, col)
+                               : Partial::identity();
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (c0 + u < hi) acc.merge(x[u]);
+    }
+    return acc;
+}
+
+// Hubs of 2..kBigHubChunks chunks: one row group per hub, chunks in order.
+template <typename T, int V, int G, class Partial>
+__global__ __launch_bounds__(kThreads) void k_hub_combine_small(
+    const int32_t* __restrict__ offsets, int64_t num_edges, int64_t D,
+    const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
+    int64_t num_hubs, int64_t num_chunks, const T* __restrict__ partial, T* __restrict__ out) {
+    constexpr int R = kThreads / G;
+    constexpr int U = batch_rows<G>();
+    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
+    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
+    if (col >= D) return;
+    for (int64_t h = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; h < num_hubs;
+         h += static_cast<int64_t>(gridDim.x) * R) {
+        const int64_t key = hub_key[h];
+        const int64_t sb = clamp64(offsets[key], 0, num_edges);
+        const int64_t se = clamp64(offsets[key + 1], sb, num_edges);
+        const int64_t nch = (se - sb + kChunkSize - 1) / kChunkSize;
+        if (nch < 2 || nch > kBigHubChunks) continue;
+        const int64_t base = hub_chunk_base[h];
+        if (base < 0 || base + nch > num_chunks) continue;
+        const Partial acc = fold_partials<Partial, T, U>(partial, base, base + nch, D, col);
+        pack_store<T, V>(out + key * D + col, acc.value());
+    }
+}
+
+// Hubs of more than kBigHubChunks chunks: one 1024-thread workgroup per hub;
+// group g folds a contiguous range of chunks, group results in group order.
+template <typename T, int V, int G, class Partial>
+__global__ __launch_bounds__(kBigThreads) void k_hub_combine_big(
+    const int32_t* __restrict__ offsets, int64_t num_edges, int64_t D,
+    const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
+    const int32_t* __restrict__ big_hubs, int64_t num_hubs, int64_t num_big_hubs,
+    int64_t num_chunks, const T* __restrict__ partial, T* __restrict__ out) {
+    constexpr int NG = kBigThreads / G;
+    constexpr int U = batch_rows<G>();
+    __shared__ Partial red[kBigThreads];
+    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
+    const int grp = static_cast<int>(threadIdx.x) / G;
+    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
+    const bool colok = col < D;
+    for (int64_t bi = blockIdx.x; bi < num_big_hubs; bi += gridDim.x) {
+        const int64_t h = big_hubs[bi];
+        const bool hok = h >= 0 && h < num_hubs;
+        const int64_t key = hok ? hub_key[h] : 0;
+        const int64_t sb = hok ? clamp64(offsets[key], 0, num_edges) : 0;
+        const int64_t se = hok ? clamp64(offsets[key + 1], sb, num_edges) : 0;
+        int64_t nch = (se - sb + kChunkSize - 1) / kChunkSize;
+        const int64_t base = hok ? hub_chunk_base[h] : 0;
+        if (base < 0 || base + nch > num_chunks) nch = 0;
+        const int64_t per = (nch + NG - 1) / NG;
+        const int64_t lo = clamp64(grp * per, 0, nch);
+        const int64_t hi = clamp64(lo + per, lo, nch);
+        red[threadIdx.x] = colok ? fold_partials<Partial, T, U>(partial, base + lo, base + hi, D, col)
+                                 : Partial::identity();
+        __syncthreads();
+        if (grp == 0 && colok && hok && nch > 0) {
+            Partial acc = red[gl];
+            for (int g = 1; g < NG; ++g) acc.merge(red[g * G + gl]);
+            pack_store<T, V>(out + key * D + col, acc.value());
+        }
+        __syncthreads();
+    }
+}
+
 // out[r] = table[gathers[inv[r]]] or 0 (inverse plans: fanout forward and
-// injective sum backward).
+// injective sum backward).  Each row group keeps kRowsInFlight rows in flight:
+// rows key0 + j * ngroups, so neighbouring groups touch neighbouring rows.
 template <typename T, int V, int G>
 __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restrict__ inv,
                                                          const int64_t* __restrict__ gathers,
@@ -206,19 +482,34 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
                                                          int64_t num_keys, int64_t D,
                                                          T* __restrict__ out) {
     constexpr int R = kThreads / G;
+    constexpr int RU = kRowsInFlight;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
-    for (int64_t key = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key < num_keys;
-         key += static_cast<int64_t>(gridDim.x) * R) {
-        const int32_t e = inv[key];
-        Pack<T, V> v = pack_fill<T, V>(T(0));
-        if (e >= 0) {
-            const int64_t g = gathers[e];
-            if (static_cast<uint64_t>(g) < static_cast<uint64_t>(num_gather))
-                v = pack_load<T, V>(table + g * D + col);
+    const int64_t ngroups = static_cast<int64_t>(gridDim.x) * R;
+    for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key0 < num_keys;
+         key0 += ngroups * RU) {
+        int32_t e[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            const int64_t key = key0 + j * ngroups;
+            e[j] = key < num_keys ? inv[key] : -1;
         }
-        pack_store_stream<T, V>(out + key * D + col, v);
+        int64_t g[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) g[j] = e[j] >= 0 ? gathers[e[j]] : -1;
+        Pack<T, V> v[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            v[j] = pack_fill<T, V>(T(0));
+            if (static_cast<uint64_t>(g[j]) < static_cast<uint64_t>(num_gather))
+                v[j] = pack_load<T, V>(table + g[j] * D + col);
+        }
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            const int64_t key = key0 + j * ngroups;
+            if (key < num_keys) pack_store_stream<T, V>(out + key * D + col, v[j]);
+        }
     }
 }
 
@@ -236,201 +527,11 @@ __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __r
     if (col >= D) return;
     for (int64_t key = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key < num_keys;
          key += static_cast<int64_t>(gridDim.x) * R) {
-        const Span sp = segment(offsets, key, num_edges);
+        const int64_t b = clamp64(offsets[key], 0, num_edges);
+        const int64_t e = clamp64(offsets[key + 1], b, num_edges);
         Pack<T, V> v = pack_fill<T, V>(T(0));
-        if (sp.end > sp.beg) v = pack_load<T, V>(table + static_cast<int64_t>(gs[sp.end - 1]) * D + col);
+        if (e > b) v = pack_load<T, V>(table + static_cast<int64_t>(gs[e - 1]) * D + col);
         pack_store_stream<T, V>(out + key * D + col, v);
-    }
-}
-
-// Segments with at most kHubThreshold messages: one row group per key, the
-// messages in edge order.
-template <typename T, int V, int G, int MODE>
-__global__ __launch_bounds__(kThreads) void k_segment_short(const int32_t* __restrict__ offsets,
-                                                            const int32_t* __restrict__ gs,
-                                                            int64_t num_edges,
-                                                            const T* __restrict__ table,
-                                                            int64_t num_keys, int64_t D,
-                                                            T* __restrict__ out) {
-    constexpr int R = kThreads / G;
-    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
-    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
-    const bool colok = col < D;
-    for (int64_t key = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key < num_keys;
-         key += static_cast<int64_t>(gridDim.x) * R) {
-        const Span sp = segment(offsets, key, num_edges);
-        if (sp.end - sp.beg > kHubThreshold) continue;
-        if constexpr (MODE == RELM_MP_MODE_SUM) {
-            SumAcc<T, V> acc;
-            acc.init();
-            reduce_rows<T, V, G>(acc, gs, sp.beg, sp.end, table, D, col, colok, gl);
-            if (colok) pack_store_stream<T, V>(out + key * D + col, acc.acc);
-        } else {
-            LseAcc<T, V> acc;
-            acc.init();
-            reduce_rows<T, V, G>(acc, gs, sp.beg, sp.end, table, D, col, colok, gl);
-            if (colok)
-                pack_store_stream<T, V>(out + key * D + col, lse_finish<T, V>(acc, sp.end > sp.beg));
-        }
-    }
-}
-
-struct HubChunk {
-    int64_t key;
-    int64_t beg;
-    int64_t end;
-    bool ok;
-};
-
-__device__ __forceinline__ HubChunk hub_chunk(int64_t c, const int32_t* __restrict__ offsets,
-                                              const int32_t* __restrict__ hub_key,
-                                              const int32_t* __restrict__ hub_chunk_base,
-                                              const int32_t* __restrict__ chunk_hub,
-                                              int64_t num_hubs, int64_t num_edges) {
-    HubChunk hc{0, 0, 0, false};
-    const int64_t h = chunk_hub[c];
-    if (h < 0 || h >= num_hubs) return hc;
-    hc.key = hub_key[h];
-    const int64_t j = c - hub_chunk_base[h];
-    const Span sp = segment(offsets, hc.key, num_edges);
-    hc.beg = sp.beg + j * kChunkSize;
-    if (hc.beg < sp.beg) hc.beg = sp.beg;
-    if (hc.beg > sp.end) hc.beg = sp.end;
-    hc.end = hc.beg + kChunkSize < sp.end ? hc.beg + kChunkSize : sp.end;
-    hc.ok = true;
-    return hc;
-}
-
-// Hub chunk partials: sum -> partial[c][D]; logsumexp -> (m, s) in
-// partial[c][0:D], partial[c][D:2D]; logsumexp backward -> sum.
-template <typename T, int V, int G, int MODE>
-__global__ __launch_bounds__(kThreads) void k_hub_partial(
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_edges,
-    const T* __restrict__ table, int64_t D, const int32_t* __restrict__ hub_key,
-    const int32_t* __restrict__ hub_chunk_base, const int32_t* __restrict__ chunk_hub,
-    int64_t num_hubs, int64_t num_chunks, T* __restrict__ partial) {
-    constexpr int R = kThreads / G;
-    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
-    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
-    const bool colok = col < D;
-    for (int64_t c = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; c < num_chunks;
-         c += static_cast<int64_t>(gridDim.x) * R) {
-        const HubChunk hc =
-            hub_chunk(c, offsets, hub_key, hub_chunk_base, chunk_hub, num_hubs, num_edges);
-        const int64_t beg = hc.ok ? hc.beg : 0;
-        const int64_t end = hc.ok ? hc.end : 0;
-        if constexpr (MODE == RELM_MP_MODE_SUM) {
-            SumAcc<T, V> acc;
-            acc.init();
-            reduce_rows<T, V, G>(acc, gs, beg, end, table, D, col, colok, gl);
-            if (colok) pack_store<T, V>(partial + c * D + col, acc.acc);
-        } else {
-            LseAcc<T, V> acc;
-            acc.init();
-            reduce_rows<T, V, G>(acc, gs, beg, end, table, D, col, colok, gl);
-            if (colok) {
-                pack_store<T, V>(partial + c * 2 * D + col, acc.m);
-                pack_store<T, V>(partial + c * 2 * D + D + col, acc.s);
-            }
-        }
-    }
-}
-
-// Combines the chunk partials of one hub per block, in chunk order: group g
-// folds a contiguous range of chunks, then group results are folded in group
-// order.
-template <typename T, int V, int G, int MODE>
-__global__ __launch_bounds__(kThreads) void k_hub_combine(const int32_t* __restrict__ offsets,
-                                                          int64_t num_edges, int64_t D,
-                                                          const int32_t* __restrict__ hub_key,
-                                                          const int32_t* __restrict__ hub_chunk_base,
-                                                          int64_t num_hubs, int64_t num_chunks,
-                                                          const T* __restrict__ partial,
-                                                          T* __restrict__ out) {
-    constexpr int NG = kThreads / G;
-    __shared__ Pack<T, V> red_a[kThreads];
-    __shared__ Pack<T, V> red_b[kThreads];
-    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
-    const int grp = static_cast<int>(threadIdx.x) / G;
-    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
-    const bool colok = col < D;
-    for (int64_t h = blockIdx.x; h < num_hubs; h += gridDim.x) {
-        const int64_t key = hub_key[h];
-        const Span sp = segment(offsets, key, num_edges);
-        const int64_t nch_all = (sp.end - sp.beg + kChunkSize - 1) / kChunkSize;
-        int64_t base = hub_chunk_base[h];
-        int64_t nch = nch_all;
-        if (base < 0) base = 0;
-        if (base + nch > num_chunks) nch = num_chunks - base > 0 ? num_chunks - base : 0;
-        const int64_t per = (nch + NG - 1) / NG;
-        const int64_t lo = grp * per < nch ? grp * per : nch;
-        const int64_t hi = lo + per < nch ? lo + per : nch;
-        if constexpr (MODE == RELM_MP_MODE_SUM) {
-            Pack<T, V> acc = pack_fill<T, V>(T(0));
-            if (colok) {
-                for (int64_t c = lo; c < hi; ++c) {
-                    const Pack<T, V> x = pack_load<T, V>(partial + (base + c) * D + col);
-#pragma unroll
-                    for (int i = 0; i < V; ++i) acc.v[i] = acc.v[i] + x.v[i];
-                }
-            }
-            red_a[threadIdx.x] = acc;
-            __syncthreads();
-            if (grp == 0 && colok) {
-                Pack<T, V> tot = pack_fill<T, V>(T(0));
-                for (int g = 0; g < NG; ++g) {
-                    const Pack<T, V> x = red_a[g * G + gl];
-#pragma unroll
-                    for (int i = 0; i < V; ++i) tot.v[i] = tot.v[i] + x.v[i];
-                }
-                pack_store<T, V>(out + key * D + col, tot);
-            }
-            __syncthreads();
-        } else {
-            Pack<T, V> M = pack_fill<T, V>(neg_inf<T>());
-            Pack<T, V> S = pack_fill<T, V>(T(0));
-            if (colok) {
-                for (int64_t c = lo; c < hi; ++c) {
-                    const Pack<T, V> m = pack_load<T, V>(partial + (base + c) * 2 * D + col);
-#pragma unroll
-                    for (int i = 0; i < V; ++i) M.v[i] = max_nan(M.v[i], m.v[i]);
-                }
-                for (int64_t c = lo; c < hi; ++c) {
-                    const Pack<T, V> m = pack_load<T, V>(partial + (base + c) * 2 * D + col);
-                    const Pack<T, V> s = pack_load<T, V>(partial + (base + c) * 2 * D + D + col);
-#pragma unroll
-                    for (int i = 0; i < V; ++i)
-                        if (M.v[i] != neg_inf<T>())
-                            S.v[i] = S.v[i] + s.v[i] * dev_exp<T>(m.v[i] - M.v[i]);
-                }
-            }
-            red_a[threadIdx.x] = M;
-            red_b[threadIdx.x] = S;
-            __syncthreads();
-            if (grp == 0 && colok) {
-                Pack<T, V> MM = pack_fill<T, V>(neg_inf<T>());
-                for (int g = 0; g < NG; ++g) {
-                    const Pack<T, V> m = red_a[g * G + gl];
-#pragma unroll
-                    for (int i = 0; i < V; ++i) MM.v[i] = max_nan(MM.v[i], m.v[i]);
-                }
-                Pack<T, V> SS = pack_fill<T, V>(T(0));
-                for (int g = 0; g < NG; ++g) {
-                    const Pack<T, V> m = red_a[g * G + gl];
-                    const Pack<T, V> s = red_b[g * G + gl];
-#pragma unroll
-                    for (int i = 0; i < V; ++i)
-                        if (MM.v[i] != neg_inf<T>())
-                            SS.v[i] = SS.v[i] + s.v[i] * dev_exp<T>(m.v[i] - MM.v[i]);
-                }
-                Pack<T, V> r;
-#pragma unroll
-                for (int i = 0; i < V; ++i)
-                    r.v[i] = MM.v[i] == neg_inf<T>() ? quiet_nan<T>() : dev_log<T>(SS.v[i]) + MM.v[i];
-                pack_store<T, V>(out + key * D + col, r);
-            }
-            __syncthreads();
-        }
     }
 }
 
@@ -442,76 +543,47 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
     const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
     int64_t num_keys, int64_t D, T* __restrict__ grad_rel) {
     constexpr int R = kThreads / G;
+    constexpr int RU = kRowsInFlight;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
-    for (int64_t key = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key < num_keys;
-         key += static_cast<int64_t>(gridDim.x) * R) {
-        const int32_t e = inv[key];
-        Pack<T, V> r = pack_fill<T, V>(T(0));
-        if (e >= 0) {
-            const int64_t d = gathers[e];
-            if (static_cast<uint64_t>(d) < static_cast<uint64_t>(num_gather)) {
-                const Pack<T, V> x = pack_load<T, V>(rel + key * D + col);
-                const Pack<T, V> g = pack_load<T, V>(grad_out + d * D + col);
-                const Pack<T, V> o = pack_load<T, V>(out + d * D + col);
+    const int64_t ngroups = static_cast<int64_t>(gridDim.x) * R;
+    for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key0 < num_keys;
+         key0 += ngroups * RU) {
+        int32_t e[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            const int64_t key = key0 + j * ngroups;
+            e[j] = key < num_keys ? inv[key] : -1;
+        }
+        int64_t d[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) d[j] = e[j] >= 0 ? gathers[e[j]] : -1;
+        Pack<T, V> x[RU], g[RU], o[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
+            const int64_t key = key0 + j * ngroups;
+            x[j] = ok ? pack_load<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
+            g[j] = ok ? pack_load<T, V>(grad_out + d[j] * D + col) : pack_fill<T, V>(T(0));
+            o[j] = ok ? pack_load<T, V>(out + d[j] * D + col) : pack_fill<T, V>(T(0));
+        }
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            const int64_t key = key0 + j * ngroups;
+            if (key >= num_keys) continue;
+            const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
+            Pack<T, V> r = pack_fill<T, V>(T(0));
+            if (ok) {
 #pragma unroll
                 for (int i = 0; i < V; ++i) {
-                    const T w = dev_exp<T>(x.v[i] - o.v[i]);
-                    const T c = g.v[i] * w;
+                    const T w = fast_exp<T>(x[j].v[i] - o[j].v[i]);
+                    const T c = g[j].v[i] * w;
                     r.v[i] = T(0) + c;
                 }
             }
+            pack_store_stream<T, V>(grad_rel + key * D + col, r);
         }
-        pack_store_stream<T, V>(grad_rel + key * D + col, r);
-    }
-}
-
-// Logsumexp backward with a CSR plan keyed by flat_src: short segments.
-template <typename T, int V, int G>
-__global__ __launch_bounds__(kThreads) void k_lse_bwd_short(
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_edges,
-    const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
-    int64_t num_keys, int64_t D, T* __restrict__ grad_rel) {
-    constexpr int R = kThreads / G;
-    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
-    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
-    const bool colok = col < D;
-    for (int64_t key = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key < num_keys;
-         key += static_cast<int64_t>(gridDim.x) * R) {
-        const Span sp = segment(offsets, key, num_edges);
-        if (sp.end - sp.beg > kHubThreshold) continue;
-        LseBwdAcc<T, V> acc;
-        acc.init();
-        acc.xr = pack_fill<T, V>(T(0));
-        if (colok && sp.end > sp.beg) acc.xr = pack_load<T, V>(rel + key * D + col);
-        reduce_rows_lse_bwd<T, V, G>(acc, gs, sp.beg, sp.end, grad_out, out, D, col, colok, gl);
-        if (colok) pack_store_stream<T, V>(grad_rel + key * D + col, acc.acc);
-    }
-}
-
-template <typename T, int V, int G>
-__global__ __launch_bounds__(kThreads) void k_lse_bwd_hub_partial(
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_edges,
-    const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
-    int64_t D, const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
-    const int32_t* __restrict__ chunk_hub, int64_t num_hubs, int64_t num_chunks,
-    T* __restrict__ partial) {
-    constexpr int R = kThreads / G;
-    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
-    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
-    const bool colok = col < D;
-    for (int64_t c = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; c < num_chunks;
-         c += static_cast<int64_t>(gridDim.x) * R) {
-        const HubChunk hc =
-            hub_chunk(c, offsets, hub_key, hub_chunk_base, chunk_hub, num_hubs, num_edges);
-        LseBwdAcc<T, V> acc;
-        acc.init();
-        acc.xr = pack_fill<T, V>(T(0));
-        if (colok && hc.ok) acc.xr = pack_load<T, V>(rel + hc.key * D + col);
-        reduce_rows_lse_bwd<T, V, G>(acc, gs, hc.ok ? hc.beg : 0, hc.ok ? hc.end : 0, grad_out,
-                                     out, D, col, colok, gl);
-        if (colok) pack_store<T, V>(partial + c * D + col, acc.acc);
     }
 }
 
@@ -556,12 +628,47 @@ int with_geometry(const Geometry& geo, F&& f) {
     return by_g(std::integral_constant<int, 1>{});
 }
 
-dim3 row_grid(int64_t rows, int G, int64_t slices) {
-    const int64_t per = kThreads / G;
+dim3 row_grid(int64_t rows, int G, int64_t slices, int rows_per_group = 1) {
+    const int64_t per = static_cast<int64_t>(kThreads / G) * rows_per_group;
     int64_t bx = (rows + per - 1) / per;
     if (bx < 1) bx = 1;
     if (bx > kMaxBlocksX) bx = kMaxBlocksX;
     return dim3(static_cast<unsigned>(bx), static_cast<unsigned>(slices));
+}
+
+dim3 block_grid(int64_t blocks, int64_t slices) {
+    int64_t bx = blocks < 1 ? 1 : (blocks > kMaxBlocksX ? kMaxBlocksX : blocks);
+    return dim3(static_cast<unsigned>(bx), static_cast<unsigned>(slices));
+}
+
+// Runs the CSR reduction of `op` (items, hub chunks, hub combines) into out.
+template <typename T, int V, int G, class Op>
+int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, T* out,
+            hipStream_t s) {
+    using Partial = typename Op::Partial;
+    const int64_t emb = op.D;
+    hipLaunchKernelGGL((k_walk_items<T, V, G, Op>), row_grid(plan.num_items, G, slices),
+                       dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.item_first,
+                       plan.num_items, plan.num_keys, plan.num_edges, out, op);
+    int rc = hip_error(hipGetLastError(), "relm_mp item kernel");
+    if (rc != RELM_MP_OK || plan.num_hubs == 0) return rc;
+    hipLaunchKernelGGL((k_hub_chunks<T, V, G, Op>), block_grid(plan.num_chunks, slices),
+                       dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.num_edges,
+                       plan.hub_key, plan.hub_chunk_base, plan.chunk_hub, plan.num_hubs,
+                       plan.num_chunks, partial, out, op);
+    rc = hip_error(hipGetLastError(), "relm_mp hub chunk kernel");
+    if (rc != RELM_MP_OK || plan.num_chunks == plan.num_hubs) return rc;  // single-chunk hubs only
+    hipLaunchKernelGGL((k_hub_combine_small<T, V, G, Partial>), row_grid(plan.num_hubs, G, slices),
+                       dim3(kThreads), 0, s, plan.offsets, plan.num_edges, emb, plan.hub_key,
+                       plan.hub_chunk_base, plan.num_hubs, plan.num_chunks,
+                       static_cast<const T*>(partial), out);
+    rc = hip_error(hipGetLastError(), "relm_mp hub combine kernel");
+    if (rc != RELM_MP_OK || plan.num_big_hubs == 0) return rc;
+    hipLaunchKernelGGL((k_hub_combine_big<T, V, G, Partial>), block_grid(plan.num_big_hubs, slices),
+                       dim3(kBigThreads), 0, s, plan.offsets, plan.num_edges, emb, plan.hub_key,
+                       plan.hub_chunk_base, plan.big_hubs, plan.num_hubs, plan.num_big_hubs,
+                       plan.num_chunks, static_cast<const T*>(partial), out);
+    return hip_error(hipGetLastError(), "relm_mp big hub combine kernel");
 }
 
 template <typename T>
@@ -573,14 +680,15 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
     return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
         constexpr int V = decltype(vt)::value;
         constexpr int G = decltype(gt)::value;
-        const dim3 grid = row_grid(plan.num_keys, G, geo.slices);
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
-            hipLaunchKernelGGL((k_gather_inv<T, V, G>), grid, dim3(kThreads), 0, s, plan.inv,
-                               gathers, plan.num_gather, table, plan.num_keys, emb, out);
-        } else {
-            hipLaunchKernelGGL((k_gather_last_csr<T, V, G>), grid, dim3(kThreads), 0, s,
-                               plan.offsets, plan.gather_sorted, plan.num_edges, table,
+            hipLaunchKernelGGL((k_gather_inv<T, V, G>),
+                               row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
+                               dim3(kThreads), 0, s, plan.inv, gathers, plan.num_gather, table,
                                plan.num_keys, emb, out);
+        } else {
+            hipLaunchKernelGGL((k_gather_last_csr<T, V, G>), row_grid(plan.num_keys, G, geo.slices),
+                               dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted,
+                               plan.num_edges, table, plan.num_keys, emb, out);
         }
         return hip_error(hipGetLastError(), "relm_mp gather kernel");
     });
@@ -596,23 +704,18 @@ int segment_reduce_t(const relm_mp_plan& plan, const void* table_v, int64_t emb,
     return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
         constexpr int V = decltype(vt)::value;
         constexpr int G = decltype(gt)::value;
-        hipLaunchKernelGGL((k_segment_short<T, V, G, MODE>), row_grid(plan.num_keys, G, geo.slices),
-                           dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.num_edges,
-                           table, plan.num_keys, emb, out);
-        int rc = hip_error(hipGetLastError(), "relm_mp segment kernel");
-        if (rc != RELM_MP_OK || plan.num_hubs == 0) return rc;
-        hipLaunchKernelGGL((k_hub_partial<T, V, G, MODE>), row_grid(plan.num_chunks, G, geo.slices),
-                           dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.num_edges,
-                           table, emb, plan.hub_key, plan.hub_chunk_base, plan.chunk_hub,
-                           plan.num_hubs, plan.num_chunks, partial);
-        rc = hip_error(hipGetLastError(), "relm_mp hub partial kernel");
-        if (rc != RELM_MP_OK) return rc;
-        const unsigned hb = static_cast<unsigned>(std::min<int64_t>(plan.num_hubs, kMaxBlocksX));
-        hipLaunchKernelGGL((k_hub_combine<T, V, G, MODE>), dim3(hb, static_cast<unsigned>(geo.slices)),
-                           dim3(kThreads), 0, s, plan.offsets, plan.num_edges, emb, plan.hub_key,
-                           plan.hub_chunk_base, plan.num_hubs, plan.num_chunks,
-                           static_cast<const T*>(partial), out);
-        return hip_error(hipGetLastError(), "relm_mp hub combine kernel");
+        constexpr int U = batch_rows<G>();
+        if constexpr (MODE == RELM_MP_MODE_SUM) {
+            SumOp<T, V, U> op{};
+            op.table = table;
+            op.D = emb;
+            return run_csr<T, V, G>(plan, op, geo.slices, partial, out, s);
+        } else {
+            LseOp<T, V, U> op{};
+            op.table = table;
+            op.D = emb;
+            return run_csr<T, V, G>(plan, op, geo.slices, partial, out, s);
+        }
     });
 }
 
@@ -629,31 +732,20 @@ int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void*
     return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
         constexpr int V = decltype(vt)::value;
         constexpr int G = decltype(gt)::value;
-        const dim3 grid = row_grid(plan.num_keys, G, geo.slices);
+        constexpr int U = batch_rows<G>();
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
-            hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G>), grid, dim3(kThreads), 0, s, plan.inv,
-                               gathers, plan.num_gather, grad_out, out, rel, plan.num_keys, emb,
-                               grad_rel);
+            hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G>),
+                               row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
+                               dim3(kThreads), 0, s, plan.inv, gathers, plan.num_gather, grad_out,
+                               out, rel, plan.num_keys, emb, grad_rel);
             return hip_error(hipGetLastError(), "relm_mp logsumexp backward kernel");
         }
-        hipLaunchKernelGGL((k_lse_bwd_short<T, V, G>), grid, dim3(kThreads), 0, s, plan.offsets,
-                           plan.gather_sorted, plan.num_edges, grad_out, out, rel, plan.num_keys,
-                           emb, grad_rel);
-        int rc = hip_error(hipGetLastError(), "relm_mp logsumexp backward kernel");
-        if (rc != RELM_MP_OK || plan.num_hubs == 0) return rc;
-        hipLaunchKernelGGL((k_lse_bwd_hub_partial<T, V, G>), row_grid(plan.num_chunks, G, geo.slices),
-                           dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.num_edges,
-                           grad_out, out, rel, emb, plan.hub_key, plan.hub_chunk_base,
-                           plan.chunk_hub, plan.num_hubs, plan.num_chunks, partial);
-        rc = hip_error(hipGetLastError(), "relm_mp logsumexp backward hub kernel");
-        if (rc != RELM_MP_OK) return rc;
-        const unsigned hb = static_cast<unsigned>(std::min<int64_t>(plan.num_hubs, kMaxBlocksX));
-        hipLaunchKernelGGL((k_hub_combine<T, V, G, RELM_MP_MODE_SUM>),
-                           dim3(hb, static_cast<unsigned>(geo.slices)), dim3(kThreads), 0, s,
-                           plan.offsets, plan.num_edges, emb, plan.hub_key, plan.hub_chunk_base,
-                           plan.num_hubs, plan.num_chunks, static_cast<const T*>(partial),
-                           grad_rel);
-        return hip_error(hipGetLastError(), "relm_mp logsumexp backward combine kernel");
+        LseBwdOp<T, V, U> op{};
+        op.grad_out = grad_out;
+        op.out = out;
+        op.rel = rel;
+        op.D = emb;
+        return run_csr<T, V, G>(plan, op, geo.slices, partial, grad_rel, s);
     });
 }
 

@@ -159,6 +159,24 @@ def add_edge_cases(b: Builder) -> None:
     b.idx("e4_dst", [0, 0, 1, 1, 2, 2, 3, 3, 3])
     b.case("e4_lse_special", "fanin_reduce", ["e4_rel", "e4_src", "e4_dst"], [5, 1])
     b.case("e4_sum_special", "fanin_reduce", ["e4_rel", "e4_src", "e4_dst"], [5, 0])
+    # NaN or -inf in the leading messages of a segment, finite ones after them
+    # (a NaN anywhere makes the logsumexp NaN; -inf messages add nothing)
+    lead = b.rng.standard_normal((20, 4)).astype(np.float32)
+    lead[0:4, :] = -np.inf
+    lead[0, 0] = np.nan
+    lead[2, 2] = np.nan
+    b.arr("e9_rel", lead)
+    b.idx("e9_src", np.arange(20))
+    b.idx("e9_dst", np.zeros(20, dtype=np.int64))
+    b.case("e9_lse_nan_lead", "fanin_reduce", ["e9_rel", "e9_src", "e9_dst"], [1, 1])
+    hub = b.rng.standard_normal((300, 32)).astype(np.float32)
+    hub[:256, :] = -np.inf
+    hub[17, 3] = np.nan
+    hub[299, 5] = np.nan
+    b.arr("e9_hub", hub)
+    b.idx("e9_hsrc", np.arange(300))
+    b.idx("e9_hdst", np.zeros(300, dtype=np.int64))
+    b.case("e9_lse_nan_hub", "fanin_reduce", ["e9_hub", "e9_hsrc", "e9_hdst"], [2, 1])
     # widths that are not multiples of the vector width
     for d in (1, 3, 7, 65):
         b.randn(f"e5_x{d}", (13, d))

@@ -178,9 +178,24 @@ def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, sk
     assert np.array_equal(_np(bp.gather_sorted), perm)
     assert np.array_equal(_np(bp.keys_sorted), keys[perm])
     deg = np.diff(offsets)
+    hub, chunk = bp.plan.hub_threshold, bp.plan.chunk_size
     assert bp.plan.max_degree == deg.max()
-    assert bp.plan.num_hubs == int((deg > 64).sum())
-    assert bp.plan.num_chunks == int(((deg[deg > 64] + 255) // 256).sum())
+    assert bp.plan.num_hubs == int((deg > hub).sum())
+    nch = (deg[deg > hub] + chunk - 1) // chunk
+    assert bp.plan.num_chunks == int(nch.sum())
+    assert bp.plan.num_big_hubs == int((nch > 64).sum())
+    # hubs are listed in key order; items start at the first key of their position range
+    hub_keys = np.flatnonzero(deg > hub)
+    got_hubs = bp.mem[bp.plan.hub_key - bp.mem.data_ptr():][: 4 * hub_keys.size].view(torch.int32)
+    assert np.array_equal(_np(got_hubs), hub_keys)
+    # walk items: balanced by weight 1 + messages of non-hub keys, 64 units each
+    item = 64
+    weight = 1 + np.where((deg > 0) & (deg <= hub), deg, 0)
+    W = np.concatenate([[0], np.cumsum(weight)])
+    assert bp.plan.num_items == W[-1] // item + 1
+    items = np.searchsorted(W[:-1], np.arange(bp.plan.num_items) * item, side="left")
+    got_items = bp.mem[bp.plan.item_first - bp.mem.data_ptr():][: 4 * (items.size + 1)].view(torch.int32)
+    assert np.array_equal(_np(got_items), np.append(items, num_keys))
 
 
 def test_inverse_plan_matches_oracle() -> None:
