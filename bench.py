@@ -16,7 +16,7 @@ The JSON line also carries
   extra         - kernel-only rates with cached plans, C2 with sum, C3 fanout
                   forward + backward, C1 latencies.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1|copy]
 """
 
 from __future__ import annotations
@@ -199,6 +199,17 @@ def bench_c1(torch, mp, syn) -> dict:
     return out
 
 
+def bench_copy(torch, steps: int) -> dict:
+    """A plain 1 GiB device-to-device copy: the calibration kernel for the HBM
+    byte counters (FETCH_SIZE / WRITE_SIZE per dispatch against 1 GiB)."""
+
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    sec = timed(lambda: b.copy_(a), max(steps, 3), 1, torch.cuda.synchronize)
+    return {"bytes_read": 4 * n, "bytes_written": 4 * n, "ms": sec * 1e3, "gbs": gbs(8 * n, sec)}
+
+
 def cpu_baseline(syn) -> dict:
     """The reference's CPU op library on a 1/8-scale C2 sample (same generator,
     131,072 objects, 2,097,152 messages), logsumexp forward + backward, on all
@@ -246,7 +257,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1"], default=None,
+    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "copy"], default=None,
                     help="run one workload only and print its figures (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -271,7 +282,8 @@ def main() -> int:
         fn = {"c2": lambda: bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 1),
               "c2sum": lambda: bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 0),
               "c3": lambda: bench_c3(torch, mp, capi, syn, args.steps, args.warmup),
-              "c1": lambda: bench_c1(torch, mp, syn)}[args.only]
+              "c1": lambda: bench_c1(torch, mp, syn),
+              "copy": lambda: bench_copy(torch, args.steps)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
 

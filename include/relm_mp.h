@@ -63,8 +63,9 @@ enum relm_mp_mode { RELM_MP_MODE_SUM = 0, RELM_MP_MODE_LOGSUMEXP = 1 };
  * reduced in chunks of RELM_MP_CHUNK_SIZE messages (one workgroup per chunk);
  * hubs spanning more than RELM_MP_BIG_HUB_CHUNKS chunks combine their chunk
  * results with a whole workgroup.  The other segments are walked in items:
- * item j holds the keys whose segment starts in positions
- * [j * RELM_MP_ITEM_SIZE, (j + 1) * RELM_MP_ITEM_SIZE). */
+ * key k weighs 1 plus its message count (1 for a hub), W[k] is the sum of
+ * the weights of the keys before k, and item j holds the keys with
+ * W[k] in [j * RELM_MP_ITEM_SIZE, (j + 1) * RELM_MP_ITEM_SIZE). */
 #define RELM_MP_HUB_THRESHOLD 64
 #define RELM_MP_CHUNK_SIZE 2048
 #define RELM_MP_BIG_HUB_CHUNKS 64
@@ -151,6 +152,7 @@ typedef struct relm_mp_plan {
     int64_t num_chunks;      /* CSR: hub chunks                                */
     int64_t num_big_hubs;    /* CSR: hubs with more than RELM_MP_BIG_HUB_CHUNKS chunks */
     int64_t num_items;       /* CSR: walk items (see RELM_MP_ITEM_SIZE)        */
+    int64_t num_short;       /* CSR: edges of the segments of at most hub_threshold */
     int32_t* inv;            /* inverse: [num_keys] largest edge id per key or -1 */
     int32_t* offsets;        /* CSR: [num_keys + 1] segment offsets            */
     int32_t* gather_sorted;  /* CSR: [num_edges] gathered row per edge, stable key order */
@@ -160,6 +162,9 @@ typedef struct relm_mp_plan {
     int32_t* chunk_hub;      /* CSR: [num_chunks] hub of each chunk            */
     int32_t* big_hubs;       /* CSR: [num_big_hubs] hub slots of the big hubs  */
     int32_t* item_first;     /* CSR: [num_items + 1] first key of each item    */
+    int32_t* item_short;     /* CSR: [num_items + 1] short_off[item_first[j]]  */
+    int32_t* short_off;      /* CSR: [num_keys + 1] edges of non-hub segments before each key */
+    int32_t* short_gather;   /* CSR: [num_short] gather_sorted without the hub segments */
 } relm_mp_plan;
 
 /* Inverse plan: inv[k] = largest e with keys[e] == k, or -1.  Validates keys

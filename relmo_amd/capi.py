@@ -70,6 +70,7 @@ class Plan(ctypes.Structure):
         ("num_chunks", ctypes.c_int64),
         ("num_big_hubs", ctypes.c_int64),
         ("num_items", ctypes.c_int64),
+        ("num_short", ctypes.c_int64),
         ("inv", ctypes.c_void_p),
         ("offsets", ctypes.c_void_p),
         ("gather_sorted", ctypes.c_void_p),
@@ -79,6 +80,9 @@ class Plan(ctypes.Structure):
         ("chunk_hub", ctypes.c_void_p),
         ("big_hubs", ctypes.c_void_p),
         ("item_first", ctypes.c_void_p),
+        ("item_short", ctypes.c_void_p),
+        ("short_off", ctypes.c_void_p),
+        ("short_gather", ctypes.c_void_p),
     ]
 
 
@@ -310,6 +314,22 @@ class BuiltPlan:
     @property
     def keys_sorted(self) -> torch.Tensor:
         return self._i32(self.plan.keys_sorted, self.plan.num_edges)
+
+    @property
+    def item_first(self) -> torch.Tensor:
+        return self._i32(self.plan.item_first, self.plan.num_items + 1)
+
+    @property
+    def item_short(self) -> torch.Tensor:
+        return self._i32(self.plan.item_short, self.plan.num_items + 1)
+
+    @property
+    def short_off(self) -> torch.Tensor:
+        return self._i32(self.plan.short_off, self.plan.num_keys + 1)
+
+    @property
+    def short_gather(self) -> torch.Tensor:
+        return self._i32(self.plan.short_gather, self.plan.num_short)
 
 
 def inv_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, gather_bound: int,

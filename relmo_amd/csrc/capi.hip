@@ -120,6 +120,9 @@ struct CsrLayout {
     int32_t* chunk_hub;
     int32_t* big_hubs;
     int32_t* item_first;
+    int32_t* item_short;
+    int32_t* short_off;
+    int32_t* short_gather;
     int64_t num_items;
     size_t bytes;
 };
@@ -137,6 +140,9 @@ CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
     l.big_hubs = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.num_items = item_capacity_for(num_keys);
     l.item_first = c.take<int32_t>(static_cast<size_t>(l.num_items) + 1);
+    l.item_short = c.take<int32_t>(static_cast<size_t>(l.num_items) + 1);
+    l.short_off = c.take<int32_t>(static_cast<size_t>(num_keys) + 1);
+    l.short_gather = c.take<int32_t>(static_cast<size_t>(num_edges));
     l.bytes = c.used();
     return l;
 }
@@ -232,6 +238,9 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->chunk_hub = l.chunk_hub;
     plan->big_hubs = l.big_hubs;
     plan->item_first = l.item_first;
+    plan->item_short = l.item_short;
+    plan->short_off = l.short_off;
+    plan->short_gather = l.short_gather;
     plan->num_items = l.num_items;
     RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
     if (num_edges > 0) {
@@ -246,8 +255,9 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_HIP(launch_hub_list(l.offsets, key_bound, l.hub_key, l.hub_chunk_base, l.big_hubs,
                              max_hubs(num_edges), sc.hub_counts, sc.hub_scan_tmp, l.status, s),
              "relm_mp hub list kernels");
-    RELM_HIP(launch_item_first(l.offsets, key_bound, sc.weights, sc.weight_scan_tmp, l.item_first,
-                               l.num_items, l.status, s),
+    RELM_HIP(launch_item_first(l.offsets, l.gather_sorted, key_bound, sc.weights,
+                               sc.weight_scan_tmp, l.item_first, l.item_short, l.num_items,
+                               l.short_off, l.short_gather, l.status, s),
              "relm_mp item kernels");
     DevStatus host{};
     RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
@@ -258,6 +268,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->num_big_hubs = static_cast<int64_t>(host.num_big_hubs);
     plan->num_items = std::min<int64_t>(static_cast<int64_t>(host.total_weight) / kItemSize + 1,
                                         l.num_items);
+    plan->num_short = static_cast<int64_t>(host.total_weight) - key_bound;
     if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges) ||
         plan->num_big_hubs > plan->num_hubs)
         return set_error(RELM_MP_ERR_HIP, "relm_mp: hub list overflow");

@@ -86,13 +86,19 @@ size_t hub_list_words(int64_t num_keys);
 hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
                            int32_t* hub_chunk_base, int32_t* big_hubs, int64_t hub_capacity,
                            uint32_t* counts, uint32_t* scan_tmp, DevStatus* st, hipStream_t s);
-// Walk items balanced by key weight (1 + messages of non-hub keys).
+// Walk items balanced by key weight (1 + messages of non-hub keys), and the
+// short-segment index: short_off[k] = messages of non-hub keys before key k
+// (num_keys + 1 entries), short_gather = gather_sorted with the hub segments
+// left out, item_short[j] = short_off[item_first[j]].
 // `weights` and `scan_tmp` are scratch of num_keys + 1 and scan_tmp_words(num_keys + 1)
-// words; item_first has item_capacity + 1 entries (item_capacity_for(num_keys)).
+// words; item_first and item_short have item_capacity + 1 entries
+// (item_capacity_for(num_keys)).
 int64_t item_capacity_for(int64_t num_keys);
-hipError_t launch_item_first(const int32_t* offsets, int64_t num_keys, uint32_t* weights,
-                             uint32_t* scan_tmp, int32_t* item_first, int64_t item_capacity,
-                             DevStatus* st, hipStream_t s);
+hipError_t launch_item_first(const int32_t* offsets, const int32_t* gather_sorted,
+                             int64_t num_keys, uint32_t* weights, uint32_t* scan_tmp,
+                             int32_t* item_first, int32_t* item_short, int64_t item_capacity,
+                             int32_t* short_off, int32_t* short_gather, DevStatus* st,
+                             hipStream_t s);
 hipError_t launch_chunk_map(const int32_t* offsets, const int32_t* hub_key,
                             const int32_t* hub_chunk_base, int64_t num_hubs, int64_t num_chunks,
                             int32_t* chunk_hub, hipStream_t s);

@@ -452,6 +452,7 @@ __global__ __launch_bounds__(kThreads) void k_item_weights(const int32_t* __rest
 __global__ __launch_bounds__(kThreads) void k_item_first(const uint32_t* __restrict__ W,
                                                          int64_t num_keys,
                                                          int32_t* __restrict__ item_first,
+                                                         int32_t* __restrict__ item_short,
                                                          int64_t num_items,
                                                          DevStatus* __restrict__ st) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -465,8 +466,43 @@ __global__ __launch_bounds__(kThreads) void k_item_first(const uint32_t* __restr
         // the key past the end also closes the last used item (j = total / kItemSize + 1)
         int64_t j1 = k == num_keys ? o / kItemSize + 1 : o / kItemSize;
         if (j1 > num_items) j1 = num_items;
-        for (int64_t j = j0; j <= j1; ++j) item_first[j] = static_cast<int32_t>(k);
+        // W[k] counts one per key before k plus their short messages
+        const int32_t so = static_cast<int32_t>(o - k);
+        for (int64_t j = j0; j <= j1; ++j) {
+            item_first[j] = static_cast<int32_t>(k);
+            item_short[j] = so;
+        }
         if (k == num_keys) st->total_weight = static_cast<unsigned long long>(o);
+    }
+}
+
+// short_off[k] = W[k] - k; the gathered rows of each non-hub segment are
+// copied to short_gather[short_off[k] ...], so the short segments lie back to
+// back in key order.
+__global__ __launch_bounds__(kThreads) void k_short_index(const int32_t* __restrict__ offsets,
+                                                          const int32_t* __restrict__ gs,
+                                                          const uint32_t* __restrict__ W,
+                                                          int64_t num_keys,
+                                                          int32_t* __restrict__ short_off,
+                                                          int32_t* __restrict__ short_gather) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k <= num_keys;
+         k += stride) {
+        const int64_t so = static_cast<int64_t>(W[k]) - k;
+        short_off[k] = static_cast<int32_t>(so);
+        if (k == num_keys) continue;
+        const int64_t b = offsets[k];
+        const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - b;
+        if (deg <= 0 || deg > kHubThreshold) continue;
+        int64_t j = 0;
+        for (; j + 4 <= deg; j += 4) {
+            const int32_t a0 = gs[b + j], a1 = gs[b + j + 1], a2 = gs[b + j + 2], a3 = gs[b + j + 3];
+            short_gather[so + j] = a0;
+            short_gather[so + j + 1] = a1;
+            short_gather[so + j + 2] = a2;
+            short_gather[so + j + 3] = a3;
+        }
+        for (; j < deg; ++j) short_gather[so + j] = gs[b + j];
     }
 }
 
@@ -627,9 +663,11 @@ int64_t item_capacity_for(int64_t num_keys) {
     return num_keys * (kHubThreshold + 1) / kItemSize + 1;
 }
 
-hipError_t launch_item_first(const int32_t* offsets, int64_t num_keys, uint32_t* weights,
-                             uint32_t* scan_tmp, int32_t* item_first, int64_t item_capacity,
-                             DevStatus* st, hipStream_t s) {
+hipError_t launch_item_first(const int32_t* offsets, const int32_t* gather_sorted,
+                             int64_t num_keys, uint32_t* weights, uint32_t* scan_tmp,
+                             int32_t* item_first, int32_t* item_short, int64_t item_capacity,
+                             int32_t* short_off, int32_t* short_gather, DevStatus* st,
+                             hipStream_t s) {
     hipLaunchKernelGGL(k_item_weights, dim3(grid_1d(num_keys + 1, kThreads * 4)), dim3(kThreads), 0,
                        s, offsets, num_keys, weights);
     hipError_t err = hipGetLastError();
@@ -637,8 +675,13 @@ hipError_t launch_item_first(const int32_t* offsets, int64_t num_keys, uint32_t*
     err = launch_exclusive_scan_u32(weights, num_keys + 1, scan_tmp, s);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_item_first, dim3(grid_1d(num_keys + 1, kThreads)), dim3(kThreads), 0, s,
-                       static_cast<const uint32_t*>(weights), num_keys, item_first, item_capacity,
-                       st);
+                       static_cast<const uint32_t*>(weights), num_keys, item_first, item_short,
+                       item_capacity, st);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_short_index, dim3(grid_1d(num_keys + 1, kThreads)), dim3(kThreads), 0, s,
+                       offsets, gather_sorted, static_cast<const uint32_t*>(weights), num_keys,
+                       short_off, short_gather);
     return hipGetLastError();
 }
 

@@ -7,13 +7,14 @@
 // in the stable (edge) order of the plan, so every result is deterministic.
 //
 // CSR plans are reduced in two parts:
-//  * segments of at most kHubThreshold messages: k_walk_items.  Item j holds
-//    the keys whose segment starts in positions [j*kItemSize, (j+1)*kItemSize),
-//    so every row group gets a similar number of messages; the group walks its
-//    keys in order, each key's messages sequentially in edge order, which makes
-//    the fp32 sums bit-identical to the reference's sequential CPU loop.  The
-//    item's offsets and gathered indices are prefetched G at a time and handed
-//    out with group shuffles, leaving one memory round trip per batch of rows.
+//  * segments of at most kHubThreshold messages: k_walk_items.  Key k weighs
+//    1 + its short message count and item j holds the keys whose prefix weight
+//    lies in [j*kItemSize, (j+1)*kItemSize), so every row group gets a similar
+//    amount of work; the group walks its keys in order, each key's messages
+//    sequentially in edge order, which makes the fp32 sums bit-identical to the
+//    reference's sequential CPU loop.  A workgroup stages the short offsets and
+//    gathered indices of its items in LDS first, leaving one memory round trip
+//    per batch of message rows.
 //  * hubs: k_hub_chunks, one workgroup per chunk of kChunkSize messages; each
 //    row group folds a contiguous slice, the slices are folded in slice order.
 //    Single-chunk hubs are finished there; the others leave chunk partials that
@@ -60,6 +61,12 @@ struct SumPartial {
         return {pack_load<T, V>(p + col)};
     }
     __device__ __forceinline__ Pack<T, V> value() const { return a; }
+    __device__ __forceinline__ SumPartial shfl_down(int d) const {
+        SumPartial r;
+#pragma unroll
+        for (int i = 0; i < V; ++i) r.a.v[i] = __shfl_down(a.v[i], d, kWave);
+        return r;
+    }
 };
 
 // (m, s): maximum of the messages and the sum of exp(x - m); s is NaN when a
@@ -99,6 +106,15 @@ struct LsePartial {
             r.v[i] = m.v[i] == neg_inf<T>() ? quiet_nan<T>() : dev_log<T>(s.v[i]) + m.v[i];
         return r;
     }
+    __device__ __forceinline__ LsePartial shfl_down(int d) const {
+        LsePartial r;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            r.m.v[i] = __shfl_down(m.v[i], d, kWave);
+            r.s.v[i] = __shfl_down(s.v[i], d, kWave);
+        }
+        return r;
+    }
 };
 
 // ---- ops: what is accumulated per message ----------------------------------
@@ -126,7 +142,9 @@ struct SumOp {
         for (int u = 0; u < U; ++u)
             if (u < cnt) pack_add(acc, x[u]);
     }
+    __device__ __forceinline__ void add(int u) { pack_add(acc, x[u]); }
     __device__ __forceinline__ Pack<T, V> result(bool) const { return acc; }
+    __device__ __forceinline__ Pack<T, V> empty() const { return pack_fill<T, V>(T(0)); }
     __device__ __forceinline__ Partial partial() const { return {acc}; }
 };
 
@@ -179,19 +197,34 @@ struct LseOp {
             }
         }
     }
+    // One message at a time (segments whose batches mix keys): the running
+    // maximum only moves up, so each message costs one exp.
+    __device__ __forceinline__ void add(int u) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const T xv = x[u].v[i];
+            const bool up = xv > m.v[i];
+            const T e = xv == neg_inf<T>() ? T(0) : fast_exp<T>(up ? m.v[i] - xv : xv - m.v[i]);
+            s.v[i] = up ? s.v[i] * e + T(1) : s.v[i] + e;
+            m.v[i] = up ? xv : m.v[i];
+        }
+    }
+    // A +inf message makes the reference's exp(x - max) NaN; so does a NaN
+    // message or a segment of -inf only.
     __device__ __forceinline__ Pack<T, V> result(bool nonempty) const {
         Pack<T, V> r;
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             if (!nonempty)
                 r.v[i] = neg_inf<T>();
-            else if (nan.v[i] != T(0) || m.v[i] == neg_inf<T>())
+            else if (nan.v[i] != T(0) || m.v[i] == neg_inf<T>() || m.v[i] == -neg_inf<T>())
                 r.v[i] = quiet_nan<T>();
             else
                 r.v[i] = dev_log<T>(s.v[i]) + m.v[i];
         }
         return r;
     }
+    __device__ __forceinline__ Pack<T, V> empty() const { return pack_fill<T, V>(neg_inf<T>()); }
     __device__ __forceinline__ Partial partial() const {
         Partial p{m, s};
 #pragma unroll
@@ -241,7 +274,16 @@ struct LseBwdOp {
             }
         }
     }
+    __device__ __forceinline__ void add(int u) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const T w = fast_exp<T>(xr.v[i] - o[u].v[i]);
+            const T c = g[u].v[i] * w;
+            acc.v[i] = acc.v[i] + c;
+        }
+    }
     __device__ __forceinline__ Pack<T, V> result(bool) const { return acc; }
+    __device__ __forceinline__ Pack<T, V> empty() const { return pack_fill<T, V>(T(0)); }
     __device__ __forceinline__ Partial partial() const { return {acc}; }
 };
 
@@ -251,23 +293,46 @@ __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// Feeds positions [beg, end) of `gs` to `op` in batches of U, in order.  The
-// gathered indices are fetched G at a time into a register window that
-// survives across calls (`gbase`, `gwin`).
+// W*G consecutive int32 values starting at `base`; lane l of the group holds
+// elements base + w*G + l.  get() must be called by the whole group with the
+// same index.
+template <int G, int W>
+struct Window {
+    int64_t base;
+    int32_t v[W];
+    __device__ __forceinline__ void fill(const int32_t* __restrict__ src, int64_t b, int64_t n,
+                                         int32_t pad, int gl) {
+        base = b;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const int64_t i = b + w * G + gl;
+            v[w] = i < n ? src[i] : pad;
+        }
+    }
+    __device__ __forceinline__ bool covers(int64_t i, int64_t cnt) const {
+        return i >= base && i + cnt <= base + W * G;
+    }
+    __device__ __forceinline__ int32_t get(int64_t i) const {
+        const int sidx = static_cast<int>(i - base);
+        const int w = sidx / G;
+        int32_t x = v[0];
+#pragma unroll
+        for (int ww = 1; ww < W; ++ww) x = w == ww ? v[ww] : x;
+        return __shfl(x, sidx & (G - 1), G);
+    }
+};
+
+// Feeds positions [beg, end) of `gs` to `op` in batches of U, in order
+// (single-key batches: op.consume).
 template <int G, int U, class Op>
 __device__ __forceinline__ void feed(Op& op, const int32_t* __restrict__ gs, int64_t num_edges,
-                                     int64_t beg, int64_t end, int64_t& gbase, int32_t& gwin,
-                                     int gl) {
+                                     int64_t beg, int64_t end, Window<G, 4>& gw, int gl) {
     for (int64_t p = beg; p < end; p += U) {
         const int cnt = static_cast<int>(end - p < U ? end - p : U);
-        if (p < gbase || p + cnt > gbase + G) {
-            gbase = p;
-            gwin = gbase + gl < num_edges ? gs[gbase + gl] : 0;
-        }
+        if (!gw.covers(p, cnt)) gw.fill(gs, p, num_edges, 0, gl);
         int32_t idx[U];
-        const int off = static_cast<int>(p - gbase);
 #pragma unroll
-        for (int u = 0; u < U; ++u) idx[u] = __shfl(gwin, off + u < G ? off + u : G - 1, G);
+        for (int u = 0; u < U; ++u) idx[u] = gw.get(p + (u < cnt ? u : cnt - 1));
         op.load(idx, cnt);
         op.consume(cnt);
     }
@@ -283,40 +348,119 @@ __global__ __launch_bounds__(kThreads) void k_fill(T* __restrict__ p, int64_t n,
         p[i] = value;
 }
 
-// Keys with at most kHubThreshold messages, walked item by item.
+// Keys with at most kHubThreshold messages, walked item by item.  A workgroup
+// takes R consecutive items, one per row group.  Their keys are consecutive and
+// so are their short segments (short_gather leaves the hub segments out), so
+// the workgroup first stages its short offsets and gathered row indices in LDS
+// with coalesced loads; after that the only global loads of a group are its
+// message rows.  Each group feeds its messages in batches of U that may span
+// several keys, adds every message to its key in edge order and stores a key
+// once its last message is in.  Keys without short messages (empty segments
+// and hubs) get the empty-segment result: hub rows are written again by the
+// hub kernels, which run after this one on the same stream.
 template <typename T, int V, int G, class Op>
 __global__ __launch_bounds__(kThreads) void k_walk_items(
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs,
-    const int32_t* __restrict__ item_first, int64_t num_items, int64_t num_keys,
-    int64_t num_edges, T* __restrict__ out, Op op) {
+    const int32_t* __restrict__ short_off, const int32_t* __restrict__ short_gather,
+    const int32_t* __restrict__ item_first, const int32_t* __restrict__ item_short,
+    int64_t num_items, int64_t num_keys, int64_t num_short, T* __restrict__ out, Op op) {
     constexpr int R = kThreads / G;
     constexpr int U = batch_rows<G>();
+    // an item holds at most kItemSize keys and 2 * kItemSize - 1 short messages
+    constexpr int kKeyCap = R * kItemSize + 2;
+    constexpr int kPosCap = R * kItemSize + kItemSize;
+    __shared__ int32_t s_off[kKeyCap];
+    __shared__ int32_t s_idx[kPosCap];
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
+    const int grp = static_cast<int>(threadIdx.x) / G;
     op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     op.colok = op.col < op.D;
     const int64_t D = op.D;
-    for (int64_t item = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; item < num_items;
-         item += static_cast<int64_t>(gridDim.x) * R) {
-        const int64_t kb = clamp64(item_first[item], 0, num_keys);
-        const int64_t ke = clamp64(item_first[item + 1], kb, num_keys);
+    // block-uniform loop: every thread reaches the barriers below
+    for (int64_t ib = static_cast<int64_t>(blockIdx.x) * R; ib < num_items;
+         ib += static_cast<int64_t>(gridDim.x) * R) {
+        const int64_t ie = ib + R < num_items ? ib + R : num_items;
+        const int64_t bk0 = clamp64(item_first[ib], 0, num_keys);
+        const int64_t bk1 = clamp64(item_first[ie], bk0, num_keys);
+        const int64_t bs0 = clamp64(item_short[ib], 0, num_short);
+        const int64_t bs1 = clamp64(item_short[ie], bs0, num_short);
+        const int64_t item = ib + grp;
+        int64_t kb = bk1, ke = bk1, sb = bs1, se = bs1;
+        if (item < ie) {
+            kb = clamp64(item_first[item], bk0, bk1);
+            ke = clamp64(item_first[item + 1], kb, bk1);
+            sb = clamp64(item_short[item], bs0, bs1);
+            se = clamp64(item_short[item + 1], sb, bs1);
+        }
+        // The item construction bounds the workgroup's keys by R * kItemSize and
+        // its short messages by (R + 1) * kItemSize; the clamps only keep a
+        // corrupt plan inside LDS.  All loads are issued before the first write.
+        const int nk = static_cast<int>(bk1 - bk0 + 1 < kKeyCap ? bk1 - bk0 + 1 : kKeyCap);
+        const int np = static_cast<int>(bs1 - bs0 < kPosCap ? bs1 - bs0 : kPosCap);
+        constexpr int KI = (kKeyCap + kThreads - 1) / kThreads;
+        constexpr int PI = (kPosCap + kThreads - 1) / kThreads;
+        int32_t tk[KI], tp[PI];
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + j * kThreads;
+            tk[j] = i < nk ? short_off[bk0 + i] : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < PI; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + j * kThreads;
+            tp[j] = i < np ? short_gather[bs0 + i] : 0;
+        }
+        __syncthreads();  // the previous round's LDS reads are done
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + j * kThreads;
+            if (i < nk) s_off[i] = tk[j];
+        }
+#pragma unroll
+        for (int j = 0; j < PI; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + j * kThreads;
+            if (i < np) s_idx[i] = tp[j];
+        }
+        __syncthreads();
         if (kb >= ke) continue;
-        int64_t wbase = kb;
-        int32_t woff = offsets[wbase + gl < num_keys ? wbase + gl : num_keys];
-        int64_t beg = clamp64(__shfl(woff, 0, G), 0, num_edges);
-        int64_t gbase = beg;
-        int32_t gwin = gbase + gl < num_edges ? gs[gbase + gl] : 0;
-        for (int64_t k = kb; k < ke; ++k) {
-            if (k + 1 - wbase >= G) {
-                wbase = k;
-                woff = offsets[wbase + gl < num_keys ? wbase + gl : num_keys];
+        auto soff = [&](int64_t k) -> int64_t {
+            const int64_t i = k - bk0;
+            return s_off[i < kKeyCap ? i : kKeyCap - 1];
+        };
+        auto sidx = [&](int64_t p) -> int32_t {
+            const int64_t i = p - bs0;
+            return s_idx[i < kPosCap ? i : kPosCap - 1];
+        };
+        int64_t cur = kb;
+        int64_t cur_beg = sb;
+        int64_t cur_end = clamp64(soff(kb + 1), sb, se);
+        op.begin(cur, cur_end > cur_beg);
+        for (int64_t q = sb; q < se; q += U) {
+            const int cnt = static_cast<int>(se - q < U ? se - q : U);
+            int32_t idx[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) idx[u] = sidx(q + (u < cnt ? u : cnt - 1));
+            op.load(idx, cnt);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (u < cnt) {
+                    while (q + u >= cur_end && cur + 1 < ke) {
+                        if (op.colok) pack_store_stream<T, V>(out + cur * D + op.col, op.result(cur_end > cur_beg));
+                        ++cur;
+                        cur_beg = cur_end;
+                        cur_end = clamp64(soff(cur + 1), cur_beg, se);
+                        op.begin(cur, cur_end > cur_beg);
+                    }
+                    op.add(u);
+                }
             }
-            const int64_t end = clamp64(__shfl(woff, static_cast<int>(k + 1 - wbase), G), beg, num_edges);
-            if (end - beg <= kHubThreshold) {
-                op.begin(k, end > beg);
-                feed<G, U>(op, gs, num_edges, beg, end, gbase, gwin, gl);
-                if (op.colok) pack_store_stream<T, V>(out + k * D + op.col, op.result(end > beg));
-            }
-            beg = end;
+        }
+        // the key of the last message and the keys after it
+        for (;;) {
+            if (op.colok) pack_store_stream<T, V>(out + cur * D + op.col, op.result(cur_end > cur_beg));
+            if (++cur >= ke) break;
+            cur_beg = cur_end;
+            cur_end = clamp64(soff(cur + 1), cur_beg, se);
+            op.begin(cur, cur_end > cur_beg);
         }
     }
 }
@@ -372,15 +516,23 @@ __global__ __launch_bounds__(kThreads) void k_hub_chunks(
         const int64_t lo = hc.ok ? clamp64(hc.beg + grp * kPer, hc.beg, hc.end) : 0;
         const int64_t hi = hc.ok ? clamp64(lo + kPer, lo, hc.end) : 0;
         op.begin(hc.key, hc.ok && hi > lo);
-        int64_t gbase = lo;
-        int32_t gwin = gbase + gl < num_edges ? gs[gbase + gl] : 0;
-        feed<G, U>(op, gs, num_edges, lo, hi, gbase, gwin, gl);
-        red[threadIdx.x] = hi > lo ? op.partial() : Partial::identity();
+        Window<G, 4> gw;
+        gw.base = -(int64_t(1) << 40);
+        feed<G, U>(op, gs, num_edges, lo, hi, gw, gl);
+        // Fold the slices: a shuffle tree over the groups of each wave, then
+        // the waves in order.
+        Partial pg = hi > lo ? op.partial() : Partial::identity();
+        const int gw_idx = (static_cast<int>(threadIdx.x) & (kWave - 1)) / G;
+#pragma unroll
+        for (int sgrp = 1; sgrp < kWave / G; sgrp <<= 1) {
+            const Partial other = pg.shfl_down(sgrp * G);
+            if ((gw_idx & (2 * sgrp - 1)) == 0) pg.merge(other);
+        }
+        if (gw_idx == 0) red[(threadIdx.x / kWave) * G + gl] = pg;
         __syncthreads();
         if (grp == 0 && hc.ok && op.colok) {
-            const int active = static_cast<int>((hc.end - hc.beg + kPer - 1) / kPer);
             Partial acc = red[gl];
-            for (int g = 1; g < active && g < NG; ++g) acc.merge(red[g * G + gl]);
+            for (int wv = 1; wv < kThreads / kWave; ++wv) acc.merge(red[wv * G + gl]);
             if (hc.nch == 1)
                 pack_store<T, V>(out + hc.key * D + op.col, acc.value());
             else
@@ -648,8 +800,8 @@ int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, 
     using Partial = typename Op::Partial;
     const int64_t emb = op.D;
     hipLaunchKernelGGL((k_walk_items<T, V, G, Op>), row_grid(plan.num_items, G, slices),
-                       dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.item_first,
-                       plan.num_items, plan.num_keys, plan.num_edges, out, op);
+                       dim3(kThreads), 0, s, plan.short_off, plan.short_gather, plan.item_first,
+                       plan.item_short, plan.num_items, plan.num_keys, plan.num_short, out, op);
     int rc = hip_error(hipGetLastError(), "relm_mp item kernel");
     if (rc != RELM_MP_OK || plan.num_hubs == 0) return rc;
     hipLaunchKernelGGL((k_hub_chunks<T, V, G, Op>), block_grid(plan.num_chunks, slices),

@@ -194,8 +194,16 @@ def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, sk
     W = np.concatenate([[0], np.cumsum(weight)])
     assert bp.plan.num_items == W[-1] // item + 1
     items = np.searchsorted(W[:-1], np.arange(bp.plan.num_items) * item, side="left")
-    got_items = bp.mem[bp.plan.item_first - bp.mem.data_ptr():][: 4 * (items.size + 1)].view(torch.int32)
-    assert np.array_equal(_np(got_items), np.append(items, num_keys))
+    items = np.append(items, num_keys)
+    assert np.array_equal(_np(bp.item_first), items)
+    # short-segment index: the non-hub segments back to back in key order
+    short = (deg > 0) & (deg <= hub)
+    short_off = W - np.arange(num_keys + 1)
+    assert np.array_equal(_np(bp.short_off), short_off)
+    assert bp.plan.num_short == int(deg[short].sum())
+    mask = np.repeat(short, deg)
+    assert np.array_equal(_np(bp.short_gather), perm[mask])
+    assert np.array_equal(_np(bp.item_short), short_off[items])
 
 
 def test_inverse_plan_matches_oracle() -> None:
