@@ -1,0 +1,309 @@
+"""Host-side checks that run without a GPU: the C ABI library loads and exports
+exactly what include/relm_mp.h declares, the ctypes plan mirror matches the C
+struct, the torch binding's CPU lane and the python_only path reproduce the
+reference's golden fixtures, the runtime / dispatch policy follows relmo's
+mp_runtime.py / mp_dispatch.py, and the autograd facade differentiates
+correctly (CPU lane, float64 gradcheck).  No kernel is launched here.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests.conftest import REPO
+
+HEADER = REPO / "include" / "relm_mp.h"
+EPS32 = float(np.finfo(np.float32).eps)
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^(?:size_t|int|const char\*)\s+(relm_mp_\w+)\s*\(", text, re.M))
+
+
+def _hip_library():
+    from relmo_amd import capi
+
+    if not capi.LIB_PATH.exists():
+        pytest.skip("librelm_mp_hip.so is not built (run __graft_entry__.build())")
+    return capi
+
+
+def test_header_declares_the_reference_ops() -> None:
+    names = _declared_functions()
+    for op in ("fanout_scatter", "fanout_scatter_backward", "fanin_reduce",
+               "fanin_reduce_sum_backward", "fanin_reduce_logsumexp_backward"):
+        assert f"relm_mp_{op}" in names and f"relm_mp_{op}_workspace_size" in names
+    assert {"relm_mp_last_error", "relm_mp_build_info"} <= names
+
+
+def test_library_exports_exactly_the_header_symbols() -> None:
+    capi = _hip_library()
+    declared = _declared_functions()
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(capi.LIB_PATH)], capture_output=True,
+                        text=True, check=True).stdout
+    exported = {line.split()[-1] for line in nm.splitlines() if " T relm_mp_" in line}
+    assert exported == declared
+    assert set(capi.EXPORTED_SYMBOLS) == declared
+    lib = ctypes.CDLL(str(capi.LIB_PATH))
+    for name in declared:
+        assert getattr(lib, name) is not None
+
+
+def test_plan_struct_layout_matches_header(tmp_path) -> None:
+    from relmo_amd import capi
+
+    fields = [name for name, _ in capi.Plan._fields_]
+    prog = tmp_path / "layout.c"
+    body = "\n".join(f'    printf("{f} %zu\\n", offsetof(relm_mp_plan, {f}));' for f in fields)
+    prog.write_text(
+        "#include <stddef.h>\n#include <stdio.h>\n#include \"relm_mp.h\"\n"
+        f"int main(void) {{\n    printf(\"sizeof %zu\\n\", sizeof(relm_mp_plan));\n{body}\n    return 0;\n}}\n"
+    )
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{HEADER.parent}", str(prog), "-o", str(exe)], check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                        check=True).stdout.splitlines())
+    assert int(out["sizeof"]) == ctypes.sizeof(capi.Plan)
+    for f in fields:
+        assert int(out[f]) == getattr(capi.Plan, f).offset, f
+
+
+# ---- torch binding, CPU lane -------------------------------------------------------------
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from relmo_amd import mp_runtime
+
+    mp_runtime.ensure_loaded()
+    return torch.ops.relm_mp
+
+
+def _cpu_sum_parity(op: str, args: list, got: np.ndarray, want: np.ndarray, name: str) -> None:
+    positions = {"fanout_scatter_backward": (0, 2, 1), "fanin_reduce": (0, 1, 2),
+                 "fanin_reduce_sum_backward": (0, 2, 1)}
+    t, r, w = positions[op]
+    truth, absum = oracle.segment_sum_truth(args[t], args[r], args[w], got.shape[0])
+    special = ~np.isfinite(want) | ~np.isfinite(truth)
+    assert np.array_equal(got[special], want[special], equal_nan=True), name
+    bound = 4 * EPS32 * absum[~special] + 1e-30
+    assert np.all(np.abs(got[~special] - truth[~special]) <= bound), name
+    assert np.all(np.abs(want[~special] - truth[~special]) <= bound), name
+
+
+def _check_case(fn, case: dict, arrays: dict, exact: bool) -> None:
+    args = [torch.from_numpy(arrays[n]) for n in case["tensors"]] + list(case["ints"])
+    if "error" in case:
+        with pytest.raises((RuntimeError, ValueError)) as info:
+            fn(*args)
+        assert str(info.value).splitlines()[0] == case["error"], case["name"]
+        return
+    got = fn(*args).numpy()
+    want = arrays[case["expected"]]
+    assert got.shape == want.shape and got.dtype == want.dtype, case["name"]
+    lse = case["op"] == "fanin_reduce_logsumexp_backward" or (
+        case["op"] == "fanin_reduce" and case["ints"][1] == 1)
+    if exact and not lse:
+        assert np.array_equal(got, want, equal_nan=True), case["name"]
+    elif lse:
+        assert np.array_equal(np.isnan(got), np.isnan(want)), case["name"]
+        assert np.array_equal(np.isinf(got), np.isinf(want)), case["name"]
+        fin = np.isfinite(want)
+        np.testing.assert_allclose(got[fin], want[fin], rtol=1e-5, atol=1e-6, err_msg=case["name"])
+    elif case["op"] == "fanout_scatter":
+        assert np.array_equal(got, want), case["name"]
+    else:
+        np_args = [arrays[n] for n in case["tensors"]]
+        _cpu_sum_parity(case["op"], np_args, got, want, case["name"])
+
+
+def test_cpu_lane_reproduces_golden_bit_exact(ops, golden) -> None:
+    """The CPU lane is the reference's sequential loops: identical bits for
+    copies and sums, the same ATen sequence for logsumexp."""
+
+    cases, arrays = golden
+    for case in cases:
+        _check_case(getattr(ops, case["op"]), case, arrays, exact=True)
+
+
+def test_python_only_path_reproduces_golden(monkeypatch, golden) -> None:
+    from relmo_amd import mp_pack
+
+    cases, arrays = golden
+    fns = {
+        "fanout_scatter": mp_pack.fanout_scatter_python,
+        "fanin_reduce": mp_pack.fanin_reduce_python,
+    }
+    checked = 0
+    for case in cases:
+        if case["op"] not in fns or "error" in case:
+            continue
+        _check_case(fns[case["op"]], case, arrays, exact=False)
+        checked += 1
+    assert checked > 10
+
+
+def test_cpu_lane_rejects_bad_arguments(ops) -> None:
+    x = torch.randn(4, 3)
+    idx = torch.tensor([0, 1, 2])
+    with pytest.raises(RuntimeError, match="must have equal length"):
+        ops.fanout_scatter(x, idx, idx[:2], 3)
+    with pytest.raises(RuntimeError, match="must have dtype torch.int64"):
+        ops.fanout_scatter(x, idx.int(), idx, 3)
+    # std::invalid_argument, as in the reference (torch surfaces it as ValueError)
+    with pytest.raises((RuntimeError, ValueError), match="Unsupported fanin_reduce mode"):
+        ops.fanin_reduce(x, idx, idx, 4, 2)
+    with pytest.raises(RuntimeError, match=r"src_global_idx index out of bounds: 4 not in \[0, 4\)\."):
+        ops.fanout_scatter(x, torch.tensor([0, 4]), torch.tensor([0, 1]), 2)
+
+
+def test_cpu_lane_empty_inputs(ops) -> None:
+    rel = torch.randn(0, 5)
+    empty = torch.zeros(0, dtype=torch.long)
+    assert torch.equal(ops.fanin_reduce(rel, empty, empty, 3, 0), torch.zeros(3, 5))
+    assert torch.equal(ops.fanin_reduce(rel, empty, empty, 3, 1), torch.full((3, 5), float("-inf")))
+    assert ops.fanout_scatter(torch.randn(2, 4), empty, empty, 0).shape == (0, 4)
+
+
+def test_build_info_is_rocm_compatible(ops) -> None:
+    from relmo_amd import mp_runtime
+
+    info = mp_runtime.parse_build_info(ops.build_info())
+    assert info["build_cuda_tag"] == "cpu"
+    assert mp_runtime.major_minor(info["build_torch"]) == mp_runtime.major_minor(torch.__version__)
+    assert info["arch"] == "gfx950" and "hip" in info
+    assert mp_runtime.assert_runtime_compat()["build_cuda_tag"] == "cpu"
+
+
+# ---- runtime / dispatch policy (mirrors relmo's test_mp_runtime.py) -------------------------
+
+
+def test_parse_build_info_and_versions() -> None:
+    from relmo_amd import mp_runtime
+
+    assert mp_runtime.parse_build_info("a=1; b = x ;junk;c=") == {"a": "1", "b": "x", "c": ""}
+    assert mp_runtime.major_minor("2.10.0+rocm7.0") == (2, 10)
+    with pytest.raises(RuntimeError):
+        mp_runtime.major_minor("nightly")
+    assert mp_runtime.runtime_cuda_tag() == ("cpu" if torch.version.cuda is None else
+                                             "cu" + torch.version.cuda.replace(".", ""))
+
+
+def test_env_policies(monkeypatch) -> None:
+    from relmo_amd import mp_runtime
+
+    monkeypatch.delenv("RELM_MP_FALLBACK", raising=False)
+    assert mp_runtime.fallback_mode() == "error"
+    monkeypatch.setenv("RELM_MP_FALLBACK", "PYTHON")
+    assert mp_runtime.fallback_mode() == "python"
+    monkeypatch.setenv("RELM_MP_TORCH_VERSION_POLICY", "strict")
+    assert mp_runtime.torch_version_policy() == "strict"
+    # unknown values fall back to the default, as in relmo's mp_runtime.py:60-69
+    monkeypatch.setenv("RELM_MP_TORCH_VERSION_POLICY", "bogus")
+    assert mp_runtime.torch_version_policy() == "forward"
+    monkeypatch.setenv("RELM_MP_FALLBACK", "bogus")
+    assert mp_runtime.fallback_mode() == "error"
+
+
+def _fake_build(monkeypatch, info: str) -> None:
+    from relmo_amd import mp_runtime
+
+    class _NS:
+        @staticmethod
+        def build_info() -> str:
+            return info
+
+    monkeypatch.setattr(mp_runtime, "_BUILD_INFO_CACHE", None)
+    monkeypatch.setattr(mp_runtime, "ensure_loaded", lambda: None)
+    monkeypatch.setattr(mp_runtime, "ops_namespace", lambda: _NS)
+
+
+def test_compat_rejects_mismatched_builds(monkeypatch) -> None:
+    from relmo_amd import mp_runtime
+
+    major, minor = mp_runtime.major_minor(torch.__version__)
+    _fake_build(monkeypatch, "build_cuda_tag=cpu")
+    with pytest.raises(RuntimeError, match="missing build_torch"):
+        mp_runtime.assert_runtime_compat()
+    _fake_build(monkeypatch, f"build_torch={major + 1}.0.0;build_cuda_tag=cpu")
+    with pytest.raises(RuntimeError, match="major version mismatch"):
+        mp_runtime.assert_runtime_compat()
+    _fake_build(monkeypatch, f"build_torch={major}.{minor + 1}.0;build_cuda_tag=cpu")
+    with pytest.raises(RuntimeError, match="older than the build torch"):
+        mp_runtime.assert_runtime_compat()
+    _fake_build(monkeypatch, f"build_torch={major}.{minor}.0;build_cuda_tag=cu999")
+    with pytest.raises(RuntimeError, match="CUDA tag mismatch"):
+        mp_runtime.assert_runtime_compat()
+    if minor > 0:
+        _fake_build(monkeypatch, f"build_torch={major}.{minor - 1}.0;build_cuda_tag=cpu")
+        with pytest.warns(RuntimeWarning, match="version drift"):
+            mp_runtime.assert_runtime_compat()
+        monkeypatch.setenv("RELM_MP_TORCH_VERSION_POLICY", "strict")
+        _fake_build(monkeypatch, f"build_torch={major}.{minor - 1}.0;build_cuda_tag=cpu")
+        with pytest.raises(RuntimeError, match="Expected matching major.minor"):
+            mp_runtime.assert_runtime_compat()
+
+
+def test_dispatch_policy(monkeypatch) -> None:
+    from relmo_amd import mp_dispatch, mp_runtime
+
+    monkeypatch.setenv("RELM_MP_ENABLE", "0")
+    assert mp_dispatch.should_use_custom("fanin_reduce") is False
+
+    def broken() -> None:
+        raise RuntimeError("library missing")
+
+    monkeypatch.setenv("RELM_MP_ENABLE", "1")
+    monkeypatch.setattr(mp_dispatch, "ensure_runtime_compat_once", broken)
+    monkeypatch.setenv("RELM_MP_FALLBACK", "error")
+    with pytest.raises(RuntimeError, match="Custom mp op fanin_reduce is unavailable"):
+        mp_dispatch.should_use_custom("fanin_reduce")
+    monkeypatch.setenv("RELM_MP_FALLBACK", "python")
+    assert mp_dispatch.should_use_custom("fanin_reduce") is False
+    assert mp_runtime.candidate_libraries()[0].name.startswith("relm_mp_ops")
+
+
+def test_facade_public_names() -> None:
+    from relmo_amd import mp
+
+    for name in mp.__all__:
+        assert hasattr(mp, name), name
+    assert (mp.MODE_SUM, mp.MODE_LOGSUMEXP, mp.MODE_MEAN) == (0, 1, 2)
+    with pytest.raises(ValueError):
+        mp.fanin_reduce(torch.randn(2, 3), torch.tensor([0, 1]), torch.tensor([0, 0]), 1, mode=2)
+
+
+# ---- autograd facade on the CPU lane -----------------------------------------------------
+
+
+def test_autograd_matches_aten_on_cpu(mp_env) -> None:
+    from relmo_amd import mp
+
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(6, 4, dtype=torch.float64, generator=gen, requires_grad=True)
+    src = torch.tensor([0, 2, 2, 5, 1, 0, 3])
+    flat = torch.tensor([3, 0, 6, 1, 2, 5, 4])
+    assert torch.autograd.gradcheck(lambda t: mp.fanout_scatter(t, src, flat, 7), (x,))
+    rel = torch.randn(7, 4, dtype=torch.float64, generator=gen, requires_grad=True)
+    fs = torch.tensor([0, 1, 2, 3, 4, 5, 6])
+    di = torch.tensor([1, 1, 0, 3, 1, 0, 3])
+    assert torch.autograd.gradcheck(lambda t: mp.fanin_reduce(t, fs, di, 4, 0), (rel,))
+    assert torch.autograd.gradcheck(lambda t: mp.fanin_reduce(t, fs, di, 4, 1)[[0, 1, 3]], (rel,))
+    out = mp.fanin_reduce(rel, fs, di, 4, 1)
+    ref = torch.full((4, 4), float("-inf"), dtype=torch.float64).index_reduce(
+        0, di, rel, "amax", include_self=True)
+    ref = torch.zeros(4, 4, dtype=torch.float64).index_add(0, di, (rel - ref[di]).exp()).log() + ref
+    torch.testing.assert_close(out, ref)
+
+
+if __name__ == "__main__":  # pragma: no cover
+    sys.exit(pytest.main([__file__, "-q"]))
