@@ -9,8 +9,9 @@ rebuilt in every step (the plan cache is cleared first), so the figure covers
 the whole op call.  value = algorithmic bytes per step / time per step.
 
 The JSON line also carries
-  roofline      - the dominant kernel (logsumexp backward over the inverse
-                  plan, one launch) timed with HIP events on its stream;
+  roofline      - the dominant kernel (logsumexp backward in edge order: flat_src
+                  is the identity, so no index plan; one launch) timed with HIP
+                  events on its stream;
   cpu_baseline  - the reference's own CPU op library (oracle/_ref) on a
                   bounded 1/8-scale sample of C2, on the host's cores;
   extra         - kernel-only rates with cached plans, C2 with sum, C3 fanout
@@ -117,10 +118,18 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
     out = capi.plan_segment_reduce(fwd_plan, r, mode)
     reps = max(steps, 10)
     t_fwd = event_time(lambda: capi.plan_segment_reduce(fwd_plan, r, mode), reps, torch)
+    # what the step's backward runs: flat_src is the identity, so the backward
+    # op reuses the forward's CSR plan (no inverse plan)
+    assert fwd_plan.plan.gather_identity == 1
+    t_bwd = event_time(lambda: capi.plan_fanin_backward_by_dst(fwd_plan, dst, mode, grad_out, E, out, r),
+                       reps, torch)
+    ident = capi.identity_inv_plan(E, E, K)
     if mode == 1:
-        t_bwd = event_time(lambda: capi.plan_logsumexp_backward(bwd_plan, grad_out, out, r, dst), reps, torch)
+        t_bwd_inv = event_time(lambda: capi.plan_logsumexp_backward(bwd_plan, grad_out, out, r, dst), reps, torch)
+        t_bwd_ident = event_time(lambda: capi.plan_logsumexp_backward(ident, grad_out, out, r, dst), reps, torch)
     else:
-        t_bwd = event_time(lambda: capi.plan_gather_last(bwd_plan, grad_out, dst), reps, torch)
+        t_bwd_inv = event_time(lambda: capi.plan_gather_last(bwd_plan, grad_out, dst), reps, torch)
+        t_bwd_ident = event_time(lambda: capi.plan_gather_last(ident, grad_out, dst), reps, torch)
     t_plan_fwd = timed(lambda: capi.csr_plan(dst, K, flat_src, E), 3, 1, sync)
     t_plan_bwd = timed(lambda: capi.inv_plan(flat_src, E, dst, K), 3, 1, sync)
     del fwd_plan, bwd_plan, out
@@ -130,6 +139,7 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         "ms_step_cached_plans": t_cached * 1e3, "gbs_step_cached_plans": gbs(b_fwd + b_bwd, t_cached),
         "ms_fwd_kernels": t_fwd * 1e3, "gbs_fwd_kernels": gbs(b_fwd, t_fwd),
         "ms_bwd_kernel": t_bwd * 1e3, "gbs_bwd_kernel": gbs(b_bwd, t_bwd),
+        "ms_bwd_kernel_inverse_plan": t_bwd_inv * 1e3, "ms_bwd_kernel_edge_order": t_bwd_ident * 1e3,
         "ms_plan_fwd_csr": t_plan_fwd * 1e3, "ms_plan_bwd_inverse": t_plan_bwd * 1e3,
         **info,
     }
@@ -303,12 +313,15 @@ def main() -> int:
         log("CPU baseline ...")
         baseline = cpu_baseline(syn)
 
-    traffic = load_traffic("lse_bwd_inverse_c2_traffic")
+    kernel = "k_lse_bwd_inv"
+    traffic = load_traffic("c2_logsumexp_backward_traffic")
+    if traffic is not None and not traffic.get("kernel", "").startswith(kernel):
+        traffic = None
     bwd_bytes = c2["bytes_bwd"]
     achieved = gbs(bwd_bytes, c2["ms_bwd_kernel"] / 1e3)
     roofline = {
         "bound": "hbm",
-        "kernel": "k_lse_bwd_inv (fanin_reduce_logsumexp_backward, inverse plan)",
+        "kernel": f"{kernel} (fanin_reduce_logsumexp_backward, identity flat_src: edge order, no plan)",
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",

@@ -142,7 +142,7 @@ typedef struct relm_mp_plan {
     int32_t kind;
     int32_t hub_threshold;   /* CSR: segments longer than this use the hub path */
     int32_t chunk_size;      /* CSR: edges per hub chunk                        */
-    int32_t reserved;
+    int32_t gather_identity; /* CSR: 1 if gathers[e] == e for every edge (or no gathers) */
     int64_t num_keys;        /* rows on the scatter (keyed) side               */
     int64_t num_edges;
     int64_t num_gather;      /* rows on the gathered side                      */
@@ -153,7 +153,8 @@ typedef struct relm_mp_plan {
     int64_t num_big_hubs;    /* CSR: hubs with more than RELM_MP_BIG_HUB_CHUNKS chunks */
     int64_t num_items;       /* CSR: walk items (see RELM_MP_ITEM_SIZE)        */
     int64_t num_short;       /* CSR: edges of the segments of at most hub_threshold */
-    int32_t* inv;            /* inverse: [num_keys] largest edge id per key or -1 */
+    int32_t* inv;            /* inverse: [num_keys] largest edge id per key or -1;
+                                NULL = identity (key k <-> edge k for k < num_edges) */
     int32_t* offsets;        /* CSR: [num_keys + 1] segment offsets            */
     int32_t* gather_sorted;  /* CSR: [num_edges] gathered row per edge, stable key order */
     int32_t* keys_sorted;    /* CSR: [num_edges] key per edge, stable key order */
@@ -167,7 +168,8 @@ typedef struct relm_mp_plan {
     int32_t* short_gather;   /* CSR: [num_short] gather_sorted without the hub segments */
 } relm_mp_plan;
 
-/* Inverse plan: inv[k] = largest e with keys[e] == k, or -1.  Validates keys
+/* Inverse plan: inv[k] = largest e with keys[e] == k, or -1 (plan->inv is
+ * set to NULL when keys[e] == e for every edge: the identity).  Validates keys
  * against key_bound and gathers (if non-NULL) against gather_bound; the first
  * edge (in edge order) with a bad index is reported, `gather_checked_first`
  * choosing which array the reference checks first within one edge.
@@ -210,6 +212,21 @@ int relm_mp_plan_logsumexp_backward(int dtype, const relm_mp_plan* plan, const i
                                     const void* grad_out, const void* out, const void* rel_flat,
                                     int64_t emb, void* grad_rel, void* scratch,
                                     size_t scratch_bytes, relm_mp_stream_t stream);
+/* Backward of fanin_reduce over the FORWARD's CSR plan (keys = dst_idx,
+ * gathers = flat_src) when flat_src is the identity (dst_plan->gather_identity,
+ * which also makes every message row distinct).  dst_idx is the int64 array the
+ * plan was built from (validated by that build).  For every edge e:
+ * mode 0: grad_rel[e] = grad_out[dst_idx[e]];
+ * mode 1: grad_rel[e] = grad_out[d] * exp(rel_flat[e] - out[d]), d = dst_idx[e];
+ * rows [num_edges, rel_rows) become 0.  Requires num_edges <= rel_rows.  The
+ * result equals relm_mp_fanin_reduce_sum_backward / _logsumexp_backward for
+ * the same tensors, without building the inverse plan; rel_flat and out are
+ * read in mode 1 only. */
+int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
+                                       const int64_t* dst_idx, int64_t mode,
+                                       const void* grad_out, const void* out,
+                                       const void* rel_flat, int64_t emb, void* grad_rel,
+                                       int64_t rel_rows, relm_mp_stream_t stream);
 
 #ifdef __cplusplus
 }

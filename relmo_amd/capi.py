@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "relm_mp_plan_gather_last",
     "relm_mp_plan_segment_reduce",
     "relm_mp_plan_logsumexp_backward",
+    "relm_mp_plan_fanin_backward_by_dst",
 )
 
 
@@ -60,7 +61,7 @@ class Plan(ctypes.Structure):
         ("kind", ctypes.c_int32),
         ("hub_threshold", ctypes.c_int32),
         ("chunk_size", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("gather_identity", ctypes.c_int32),
         ("num_keys", ctypes.c_int64),
         ("num_edges", ctypes.c_int64),
         ("num_gather", ctypes.c_int64),
@@ -121,6 +122,7 @@ _SIGNATURES = {
     "relm_mp_plan_gather_last": (_int, [_int, _PP, _vp, _vp, _i64, _vp, _vp]),
     "relm_mp_plan_segment_reduce": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_logsumexp_backward": (_int, [_int, _PP, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_plan_fanin_backward_by_dst": (_int, [_int, _PP, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -301,6 +303,9 @@ class BuiltPlan:
 
     @property
     def inv(self) -> torch.Tensor:
+        if not self.plan.inv:  # identity plan: key k <-> edge k
+            k = torch.arange(self.plan.num_keys, dtype=torch.int32, device=self.mem.device)
+            return torch.where(k < self.plan.num_edges, k, torch.full_like(k, -1))
         return self._i32(self.plan.inv, self.plan.num_keys)
 
     @property
@@ -391,6 +396,33 @@ def plan_logsumexp_backward(bp: BuiltPlan, grad_out: torch.Tensor, out: torch.Te
         )
     )
     return grad_rel
+
+
+def plan_fanin_backward_by_dst(bp: BuiltPlan, dst_idx: torch.Tensor, mode: int, grad_out: torch.Tensor,
+                               rel_rows: int, out: torch.Tensor | None = None,
+                               rel_flat: torch.Tensor | None = None) -> torch.Tensor:
+    """Backward of fanin_reduce over the forward's CSR plan (keys = dst_idx,
+    gathers = flat_src) when flat_src is the identity."""
+
+    _check_index(dst_idx)
+    emb = grad_out.size(1)
+    grad_rel = torch.empty(rel_rows, emb, dtype=grad_out.dtype, device=grad_out.device)
+    check(
+        lib().relm_mp_plan_fanin_backward_by_dst(
+            _dtype(grad_out), ctypes.byref(bp.plan), _ptr(dst_idx), mode, _ptr(grad_out), _ptr(out),
+            _ptr(rel_flat), emb, _ptr(grad_rel), rel_rows, _stream(grad_out),
+        )
+    )
+    return grad_rel
+
+
+def identity_inv_plan(num_keys: int, num_edges: int, num_gather: int) -> BuiltPlan:
+    """Inverse plan that maps key k to edge k (k < num_edges): ``inv`` is NULL."""
+
+    plan = Plan()
+    plan.kind = PLAN_INVERSE
+    plan.num_keys, plan.num_edges, plan.num_gather = num_keys, num_edges, num_gather
+    return BuiltPlan(plan, torch.empty(0, dtype=torch.uint8))
 
 
 def plan_gather_last(bp: BuiltPlan, table: torch.Tensor, gathers: torch.Tensor | None = None) -> torch.Tensor:

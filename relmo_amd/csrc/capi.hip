@@ -207,6 +207,9 @@ int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
                                gather_name, gather_checked_first, s));
     plan->collisions = static_cast<int64_t>(host.collisions);
+    // keys[e] == e for every edge: the map is the identity, which the compute
+    // kernels apply without reading inv (one dependent load less per row)
+    if (host.key_mismatch == 0) plan->inv = nullptr;
     return RELM_MP_OK;
 }
 
@@ -269,6 +272,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->num_items = std::min<int64_t>(static_cast<int64_t>(host.total_weight) / kItemSize + 1,
                                         l.num_items);
     plan->num_short = static_cast<int64_t>(host.total_weight) - key_bound;
+    plan->gather_identity = gathers == nullptr || host.gather_mismatch == 0 ? 1 : 0;
     if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges) ||
         plan->num_big_hubs > plan->num_hubs)
         return set_error(RELM_MP_ERR_HIP, "relm_mp: hub list overflow");
@@ -376,6 +380,19 @@ int relm_mp_plan_logsumexp_backward(int dtype, const relm_mp_plan* plan, const i
     if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
     return compute_logsumexp_backward(dtype, *plan, gathers, grad_out, out, rel_flat, emb, grad_rel,
                                       scratch, scratch_bytes, static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
+                                       const int64_t* dst_idx, int64_t mode,
+                                       const void* grad_out, const void* out,
+                                       const void* rel_flat, int64_t emb, void* grad_rel,
+                                       int64_t rel_rows, relm_mp_stream_t stream) {
+    RELM_TRY(check_dtype(dtype));
+    RELM_TRY(check_rows(rel_rows, "rel_rows"));
+    if (dst_plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    return compute_backward_by_key(dtype, *dst_plan, dst_idx, mode, grad_out, out, rel_flat, emb,
+                                   grad_rel, rel_rows, static_cast<hipStream_t>(stream));
 }
 
 /* ---- op-level entry points -------------------------------------------- */

@@ -52,6 +52,15 @@ __device__ __forceinline__ void pack_store(T* ptr, const Pack<T, V>& p) {
     *reinterpret_cast<Pack<T, V>*>(ptr) = p;
 }
 
+// Streaming load: rows read once, kept out of the way of reused rows in L2.
+template <typename T, int V>
+__device__ __forceinline__ Pack<T, V> pack_load_stream(const T* ptr) {
+    Pack<T, V> p;
+#pragma unroll
+    for (int i = 0; i < V; ++i) p.v[i] = __builtin_nontemporal_load(ptr + i);
+    return p;
+}
+
 // Streaming store: the written rows are not re-read by this kernel.
 template <typename T, int V>
 __device__ __forceinline__ void pack_store_stream(T* ptr, const Pack<T, V>& p) {

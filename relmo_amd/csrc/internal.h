@@ -22,6 +22,8 @@ struct DevStatus {
     unsigned long long max_degree;       // CSR plans: longest segment
     unsigned long long num_big_hubs;     // CSR plans: hubs over RELM_MP_BIG_HUB_CHUNKS chunks
     unsigned long long total_weight;     // CSR plans: sum of the walk weights of all keys
+    unsigned long long gather_mismatch;  // CSR plans: nonzero if gathers[e] != e for some edge
+    unsigned long long key_mismatch;     // inverse plans: nonzero if keys[e] != e for some edge
 };
 
 constexpr unsigned long long kNoEdge = ~0ull;
@@ -114,6 +116,13 @@ int compute_logsumexp_backward(int dtype, const relm_mp_plan& plan, const int64_
                                int64_t emb, void* grad_rel, void* scratch, size_t scratch_bytes,
                                hipStream_t s);
 int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t s);
+// Backward of fanin_reduce (mode 0 / 1) over a CSR plan keyed by destination
+// whose gathered rows are the identity (plan.gather_identity); rows
+// [num_edges, rel_rows) of grad_rel become zero.
+int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* dst_idx,
+                            int64_t mode, const void* grad_out, const void* out,
+                            const void* rel_flat, int64_t emb, void* grad_rel, int64_t rel_rows,
+                            hipStream_t s);
 size_t hub_partial_bytes(const relm_mp_plan& plan, int64_t emb, int dtype, int64_t mode);
 
 }  // namespace relm_mp

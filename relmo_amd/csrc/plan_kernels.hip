@@ -40,6 +40,8 @@ __global__ void k_status_init(DevStatus* st) {
         st->max_degree = 0;
         st->num_big_hubs = 0;
         st->total_weight = 0;
+        st->gather_mismatch = 0;
+        st->key_mismatch = 0;
     }
 }
 
@@ -53,11 +55,13 @@ __global__ __launch_bounds__(kThreads) void k_inv_build(const int64_t* __restric
                                                         DevStatus* __restrict__ st) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     unsigned long long collisions = 0;
+    bool mismatch = false;
     for (int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x; base < n; base += stride) {
         const int64_t e = base + threadIdx.x;
         bool coll = false;
         if (e < n) {
             const int64_t k = keys[e];
+            mismatch = mismatch || k != e;
             const bool bad_k = static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound);
             if (bad_k) atomicMin(&st->bad_key_edge, static_cast<unsigned long long>(e));
             if (gathers != nullptr) {
@@ -73,6 +77,7 @@ __global__ __launch_bounds__(kThreads) void k_inv_build(const int64_t* __restric
         collisions += __popcll(__ballot(coll));
     }
     if (lane_id() == 0 && collisions != 0) atomicAdd(&st->collisions, collisions);
+    if (__ballot(mismatch) != 0 && lane_id() == 0) atomicOr(&st->key_mismatch, 1ull);
 }
 
 // ---- scan ----------------------------------------------------------------
@@ -223,6 +228,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
     unsigned long long bad = kNoEdge;
+    bool mismatch = false;
     const int64_t wave_base = tile_base + wave * kPerWave + lane;
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
@@ -237,6 +243,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
                         bad = min(bad, static_cast<unsigned long long>(p));
                     else
                         v = static_cast<uint32_t>(g);
+                    mismatch = mismatch || g != p;
                 } else {
                     v = static_cast<uint32_t>(p);
                 }
@@ -260,6 +267,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     }
     if constexpr (kFirst) {
         if (bad != kNoEdge) atomicMin(&st->bad_gather_edge, bad);
+        if (__ballot(mismatch) != 0 && lane == 0) atomicOr(&st->gather_mismatch, 1ull);
     }
     __syncthreads();
 

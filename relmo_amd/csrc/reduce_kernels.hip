@@ -623,11 +623,21 @@ __global__ __launch_bounds__(kBigThreads) void k_hub_combine_big(
     }
 }
 
+// Edge of key k under an inverse plan: inv[k], or k itself (k < num_edges)
+// when the plan is the identity (inv == nullptr).
+__device__ __forceinline__ int32_t inverse_edge(const int32_t* __restrict__ inv, int64_t key,
+                                                int64_t num_keys, int64_t num_edges) {
+    if (key >= num_keys) return -1;
+    if (inv != nullptr) return inv[key];
+    return key < num_edges ? static_cast<int32_t>(key) : -1;
+}
+
 // out[r] = table[gathers[inv[r]]] or 0 (inverse plans: fanout forward and
 // injective sum backward).  Each row group keeps kRowsInFlight rows in flight:
 // rows key0 + j * ngroups, so neighbouring groups touch neighbouring rows.
 template <typename T, int V, int G>
 __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restrict__ inv,
+                                                         int64_t num_edges,
                                                          const int64_t* __restrict__ gathers,
                                                          int64_t num_gather,
                                                          const T* __restrict__ table,
@@ -643,10 +653,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
          key0 += ngroups * RU) {
         int32_t e[RU];
 #pragma unroll
-        for (int j = 0; j < RU; ++j) {
-            const int64_t key = key0 + j * ngroups;
-            e[j] = key < num_keys ? inv[key] : -1;
-        }
+        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * ngroups, num_keys, num_edges);
         int64_t g[RU];
 #pragma unroll
         for (int j = 0; j < RU; ++j) g[j] = e[j] >= 0 ? gathers[e[j]] : -1;
@@ -691,7 +698,8 @@ __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __r
 // grad_rel[r] = grad_out[d] * exp(rel[r] - out[d]), d = gathers[inv[r]], or 0.
 template <typename T, int V, int G>
 __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
-    const int32_t* __restrict__ inv, const int64_t* __restrict__ gathers, int64_t num_gather,
+    const int32_t* __restrict__ inv, int64_t num_edges, const int64_t* __restrict__ gathers,
+    int64_t num_gather,
     const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
     int64_t num_keys, int64_t D, T* __restrict__ grad_rel) {
     constexpr int R = kThreads / G;
@@ -704,10 +712,7 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
          key0 += ngroups * RU) {
         int32_t e[RU];
 #pragma unroll
-        for (int j = 0; j < RU; ++j) {
-            const int64_t key = key0 + j * ngroups;
-            e[j] = key < num_keys ? inv[key] : -1;
-        }
+        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * ngroups, num_keys, num_edges);
         int64_t d[RU];
 #pragma unroll
         for (int j = 0; j < RU; ++j) d[j] = e[j] >= 0 ? gathers[e[j]] : -1;
@@ -716,7 +721,7 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
         for (int j = 0; j < RU; ++j) {
             const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
             const int64_t key = key0 + j * ngroups;
-            x[j] = ok ? pack_load<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
+            x[j] = ok ? pack_load_stream<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
             g[j] = ok ? pack_load<T, V>(grad_out + d[j] * D + col) : pack_fill<T, V>(T(0));
             o[j] = ok ? pack_load<T, V>(out + d[j] * D + col) : pack_fill<T, V>(T(0));
         }
@@ -835,8 +840,8 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
             hipLaunchKernelGGL((k_gather_inv<T, V, G>),
                                row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
-                               dim3(kThreads), 0, s, plan.inv, gathers, plan.num_gather, table,
-                               plan.num_keys, emb, out);
+                               dim3(kThreads), 0, s, plan.inv, plan.num_edges, gathers,
+                               plan.num_gather, table, plan.num_keys, emb, out);
         } else {
             hipLaunchKernelGGL((k_gather_last_csr<T, V, G>), row_grid(plan.num_keys, G, geo.slices),
                                dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted,
@@ -888,8 +893,8 @@ int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void*
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
             hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G>),
                                row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
-                               dim3(kThreads), 0, s, plan.inv, gathers, plan.num_gather, grad_out,
-                               out, rel, plan.num_keys, emb, grad_rel);
+                               dim3(kThreads), 0, s, plan.inv, plan.num_edges, gathers,
+                               plan.num_gather, grad_out, out, rel, plan.num_keys, emb, grad_rel);
             return hip_error(hipGetLastError(), "relm_mp logsumexp backward kernel");
         }
         LseBwdOp<T, V, U> op{};
@@ -976,6 +981,36 @@ int compute_logsumexp_backward(int dtype, const relm_mp_plan& plan, const int64_
     return dtype == RELM_MP_F64
                ? lse_backward_t<double>(plan, gathers, grad_out, out, rel_flat, emb, grad_rel, scratch, s)
                : lse_backward_t<float>(plan, gathers, grad_out, out, rel_flat, emb, grad_rel, scratch, s);
+}
+
+int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* dst_idx,
+                            int64_t mode, const void* grad_out, const void* out,
+                            const void* rel_flat, int64_t emb, void* grad_rel, int64_t rel_rows,
+                            hipStream_t s) {
+    if (plan.kind != RELM_MP_PLAN_CSR || plan.gather_identity == 0)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: backward by key needs a CSR plan whose gathered rows are the identity");
+    if (mode != RELM_MP_MODE_SUM && mode != RELM_MP_MODE_LOGSUMEXP)
+        return set_error(RELM_MP_ERR_UNSUPPORTED_MODE,
+                         "Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
+    if (plan.num_edges > rel_rows)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: backward by key needs num_edges <= rel_rows");
+    if (dst_idx == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: dst_idx is NULL");
+    // Message row e belongs to edge e alone, so the backward runs in edge
+    // order over the identity inverse plan: rel_flat / grad_rel stream through
+    // in order, the destination rows are gathered (rows >= num_edges get 0).
+    // This beat walking the plan's segments, whose row writes scatter.
+    relm_mp_plan ident{};
+    ident.kind = RELM_MP_PLAN_INVERSE;
+    ident.num_keys = rel_rows;
+    ident.num_edges = plan.num_edges;
+    ident.num_gather = plan.num_keys;
+    if (mode == RELM_MP_MODE_SUM)
+        return compute_gather_last(dtype, ident, dst_idx, grad_out, emb, grad_rel, s);
+    return compute_logsumexp_backward(dtype, ident, dst_idx, grad_out, out, rel_flat, emb, grad_rel,
+                                      nullptr, 0, s);
 }
 
 }  // namespace relm_mp

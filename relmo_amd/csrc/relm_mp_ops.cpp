@@ -158,6 +158,27 @@ class PlanCache {
         return false;
     }
 
+    // A cached CSR plan for (key, gather) with any gather bound: the forward's
+    // plan, looked up by a backward op whose own bound for the gathered rows
+    // may differ.
+    bool lookup_csr_any_gather_bound(const Tensor& key, const Tensor& gather, int64_t key_bound,
+                                     relm_mp_plan* out) {
+        if (!enabled_ || !cacheable(key) || !cacheable(gather)) return false;
+        std::lock_guard<std::mutex> lock(mu_);
+        purge_dead_locked();
+        for (PlanEntry& e : entries_) {
+            if (e.role == kRoleCsr && e.key_impl == key.unsafeGetTensorImpl() &&
+                e.gather_impl == gather.unsafeGetTensorImpl() && e.key_ver == version(key) &&
+                e.gather_ver == version(gather) && e.key_bound == key_bound &&
+                e.num_edges == key.numel() && e.device == key.get_device()) {
+                e.stamp = ++clock_;
+                *out = e.plan;
+                return true;
+            }
+        }
+        return false;
+    }
+
     void insert(int role, const Tensor& key, const Tensor& gather, int64_t key_bound,
                 int64_t gather_bound, const Tensor& mem, const relm_mp_plan& plan) {
         if (!enabled_ || !cacheable(key) || !cacheable(gather)) return;
@@ -362,6 +383,17 @@ Tensor fanin_reduce_sum_backward_gpu(const Tensor& grad_out, const Tensor& flat_
     const Tensor d_idx = contiguous(dst_idx);
     hipStream_t stream = current_stream(g);
     Tensor grad_rel = at::empty({rel_rows, emb}, grad_out.options());
+    // The forward's plan (keys dst_idx, gathers flat_src, validated) serves
+    // directly when flat_src is the identity.
+    relm_mp_plan fwd{};
+    if (PlanCache::get().lookup_csr_any_gather_bound(d_idx, s_idx, g.size(0), &fwd) &&
+        fwd.gather_identity != 0 && fwd.num_edges <= rel_rows) {
+        raise_if(relm_mp_plan_fanin_backward_by_dst(dtype_code(g), &fwd, d_idx.data_ptr<int64_t>(),
+                                                    kModeSum, g.data_ptr(),
+                                                    nullptr, nullptr, emb, grad_rel.data_ptr(),
+                                                    rel_rows, stream));
+        return grad_rel;
+    }
     GpuPlan inv = inverse_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false,
                                stream);
     if (inv.plan.collisions == 0) {
@@ -402,8 +434,17 @@ Tensor fanin_reduce_logsumexp_backward_gpu(const Tensor& grad_out, const Tensor&
     // must index both; rows beyond rel_flat cannot receive a gradient.
     const int64_t key_bound = std::min<int64_t>(rel_rows, rel.size(0));
     grad_rel = at::empty({rel_rows, emb}, rel_flat.options());
-    if (key_bound < rel_rows) grad_rel.narrow(0, key_bound, rel_rows - key_bound).zero_();
     const int dt = dtype_code(rel);
+    relm_mp_plan fwd{};
+    if (PlanCache::get().lookup_csr_any_gather_bound(d_idx, s_idx, g.size(0), &fwd) &&
+        fwd.gather_identity != 0 && fwd.num_edges <= key_bound) {
+        raise_if(relm_mp_plan_fanin_backward_by_dst(dt, &fwd, d_idx.data_ptr<int64_t>(),
+                                                    kModeLogSumExp, g.data_ptr(), o.data_ptr(),
+                                                    rel.data_ptr(), emb, grad_rel.data_ptr(),
+                                                    rel_rows, stream));
+        return grad_rel;
+    }
+    if (key_bound < rel_rows) grad_rel.narrow(0, key_bound, rel_rows - key_bound).zero_();
     GpuPlan inv = inverse_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true,
                                stream);
     if (inv.plan.collisions == 0) {

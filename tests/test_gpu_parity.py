@@ -216,6 +216,12 @@ def test_inverse_plan_matches_oracle() -> None:
         inv, coll = oracle.inverse_build(keys, k)
         assert np.array_equal(_np(bp.inv), inv)
         assert bp.plan.collisions == coll
+        assert bool(bp.plan.inv)
+    # identity keys: the plan is marked as the identity (no inv array)
+    for n, k in [(5000, 5000), (4000, 6000)]:
+        bp = capi.inv_plan(_t(np.arange(n)), k, None, 0)
+        assert not bp.plan.inv and bp.plan.collisions == 0
+        assert np.array_equal(_np(bp.inv), oracle.inverse_build(np.arange(n), k)[0])
 
 
 def _segments_bounded(keys: np.ndarray, bound: int = 64) -> bool:
@@ -373,3 +379,68 @@ def test_noncontiguous_and_plan_cache_reuse(mp_env) -> None:
     want = oracle.fanin_reduce_sum(rel.cpu().numpy(), fs.cpu().numpy(), di.cpu().numpy(), 4)
     assert np.array_equal(_np(b), want)
     assert not torch.equal(a, b)
+
+
+@pytest.mark.parametrize("emb", [3, 32, 64])
+def test_backward_by_dst_over_the_forward_plan(emb: int) -> None:
+    """With flat_src = arange, the fanin backward runs over the forward's CSR
+    plan: identical to the oracle (sum: exact copies) and to the inverse-plan
+    lane; rows past the messages are zero."""
+
+    from relmo_amd import capi
+
+    _log(f"backward by dst emb={emb}")
+    rng = np.random.default_rng(40 + emb)
+    num_keys, n = 3000, 50_000
+    dst = _zipf_keys(rng, num_keys, n)
+    flat_src = np.arange(n)
+    rel_rows = n + 17
+    rel = (2.0 * rng.standard_normal((rel_rows, emb))).astype(np.float32)
+    g = rng.standard_normal((num_keys, emb)).astype(np.float32)
+    bp = capi.csr_plan(_t(dst), num_keys, _t(flat_src), rel_rows, "dst_idx", "flat_src", True)
+    assert bp.plan.gather_identity == 1
+    got = _np(capi.plan_fanin_backward_by_dst(bp, _t(dst), 0, _t(g), rel_rows))
+    assert np.array_equal(got, oracle.fanin_reduce_sum_backward(g, flat_src, dst, rel_rows))
+    out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, num_keys)
+    got = _np(capi.plan_fanin_backward_by_dst(bp, _t(dst), 1, _t(g), rel_rows, _t(out), _t(rel)))
+    ref = oracle.fanin_reduce_logsumexp_backward(g, rel, flat_src, dst, out, rel_rows)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-6)
+    inv_lane = _np(capi.fanin_reduce_logsumexp_backward(_t(g), _t(rel), _t(flat_src), _t(dst), _t(out), rel_rows))
+    assert np.array_equal(got, inv_lane)
+    ident = capi.identity_inv_plan(rel_rows, n, num_keys)
+    got = _np(capi.plan_logsumexp_backward(ident, _t(g), _t(out), _t(rel), _t(dst)))
+    assert np.array_equal(got, inv_lane)
+    # a permuted flat_src is not the identity: the plan says so and the entry point refuses
+    bp2 = capi.csr_plan(_t(dst), num_keys, _t(rng.permutation(n)), rel_rows, "dst_idx", "flat_src", True)
+    assert bp2.plan.gather_identity == 0
+    with pytest.raises(RuntimeError, match="identity"):
+        capi.plan_fanin_backward_by_dst(bp2, _t(dst), 0, _t(g), rel_rows)
+
+
+def test_facade_backward_reuses_forward_plan(mp_env) -> None:
+    """Autograd through the facade with flat_src = arange: the backward finds the
+    forward's plan in the cache; results equal those computed without it."""
+
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    rng = np.random.default_rng(41)
+    num_keys, n, emb = 2000, 40_000, 32
+    dst = _t(_zipf_keys(rng, num_keys, n))
+    flat_src = torch.arange(n, device=DEV)
+    g = _t(rng.standard_normal((num_keys, emb)).astype(np.float32))
+    for mode in (0, 1):
+        rel = _t((2.0 * rng.standard_normal((n, emb))).astype(np.float32)).requires_grad_(True)
+        ns.plan_cache_clear()
+        out = mp.fanin_reduce(rel, flat_src, dst, num_keys, mode)
+        (cached,) = torch.autograd.grad(out, rel, g)
+        ns.plan_cache_clear()
+        if mode == 0:
+            fresh = ns.fanin_reduce_sum_backward(g, flat_src, dst, n)
+        else:
+            fresh = ns.fanin_reduce_logsumexp_backward(g, rel.detach(), flat_src, dst, out.detach(), n)
+        assert torch.equal(cached, fresh), mode
+        want = (oracle.fanin_reduce_sum_backward(_np(g), _np(flat_src), _np(dst), n) if mode == 0 else
+                oracle.fanin_reduce_logsumexp_backward(_np(g), _np(rel.detach()), _np(flat_src), _np(dst),
+                                                       _np(out.detach()), n))
+        np.testing.assert_allclose(_np(cached), want, rtol=1e-4, atol=1e-6)
