@@ -61,14 +61,13 @@ enum relm_mp_mode { RELM_MP_MODE_SUM = 0, RELM_MP_MODE_LOGSUMEXP = 1 };
 
 /* CSR plans: segments with more messages than RELM_MP_HUB_THRESHOLD are hubs,
  * reduced in chunks of RELM_MP_CHUNK_SIZE messages (one workgroup per chunk);
- * hubs spanning more than RELM_MP_BIG_HUB_CHUNKS chunks combine their chunk
- * results with a whole workgroup.  The other segments are walked in items:
+ * hubs spanning more than one chunk combine their chunk results in chunk
+ * order with one workgroup per hub.  The other segments are walked in items:
  * key k weighs 1 plus its message count (1 for a hub), W[k] is the sum of
  * the weights of the keys before k, and item j holds the keys with
  * W[k] in [j * RELM_MP_ITEM_SIZE, (j + 1) * RELM_MP_ITEM_SIZE). */
 #define RELM_MP_HUB_THRESHOLD 64
 #define RELM_MP_CHUNK_SIZE 2048
-#define RELM_MP_BIG_HUB_CHUNKS 64
 #define RELM_MP_ITEM_SIZE 64
 
 const char* relm_mp_last_error(void);
@@ -150,7 +149,7 @@ typedef struct relm_mp_plan {
     int64_t max_degree;      /* CSR: longest segment                           */
     int64_t num_hubs;        /* CSR: segments longer than hub_threshold        */
     int64_t num_chunks;      /* CSR: hub chunks                                */
-    int64_t num_big_hubs;    /* CSR: hubs with more than RELM_MP_BIG_HUB_CHUNKS chunks */
+    int64_t num_multi_hubs;  /* CSR: hubs with more than one chunk             */
     int64_t num_items;       /* CSR: walk items (see RELM_MP_ITEM_SIZE)        */
     int64_t num_short;       /* CSR: edges of the segments of at most hub_threshold */
     int32_t* inv;            /* inverse: [num_keys] largest edge id per key or -1;
@@ -161,7 +160,7 @@ typedef struct relm_mp_plan {
     int32_t* hub_key;        /* CSR: [num_hubs] key of each hub                */
     int32_t* hub_chunk_base; /* CSR: [num_hubs] first chunk of each hub        */
     int32_t* chunk_hub;      /* CSR: [num_chunks] hub of each chunk            */
-    int32_t* big_hubs;       /* CSR: [num_big_hubs] hub slots of the big hubs  */
+    int32_t* multi_hubs;     /* CSR: [num_multi_hubs] hub slots of those hubs  */
     int32_t* item_first;     /* CSR: [num_items + 1] first key of each item    */
     int32_t* item_short;     /* CSR: [num_items + 1] short_off[item_first[j]]  */
     int32_t* short_off;      /* CSR: [num_keys + 1] edges of non-hub segments before each key */

@@ -69,7 +69,7 @@ class Plan(ctypes.Structure):
         ("max_degree", ctypes.c_int64),
         ("num_hubs", ctypes.c_int64),
         ("num_chunks", ctypes.c_int64),
-        ("num_big_hubs", ctypes.c_int64),
+        ("num_multi_hubs", ctypes.c_int64),
         ("num_items", ctypes.c_int64),
         ("num_short", ctypes.c_int64),
         ("inv", ctypes.c_void_p),
@@ -79,7 +79,7 @@ class Plan(ctypes.Structure):
         ("hub_key", ctypes.c_void_p),
         ("hub_chunk_base", ctypes.c_void_p),
         ("chunk_hub", ctypes.c_void_p),
-        ("big_hubs", ctypes.c_void_p),
+        ("multi_hubs", ctypes.c_void_p),
         ("item_first", ctypes.c_void_p),
         ("item_short", ctypes.c_void_p),
         ("short_off", ctypes.c_void_p),

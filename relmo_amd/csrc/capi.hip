@@ -118,7 +118,7 @@ struct CsrLayout {
     int32_t* hub_key;
     int32_t* hub_chunk_base;
     int32_t* chunk_hub;
-    int32_t* big_hubs;
+    int32_t* multi_hubs;
     int32_t* item_first;
     int32_t* item_short;
     int32_t* short_off;
@@ -137,7 +137,7 @@ CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
     l.hub_key = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.hub_chunk_base = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.chunk_hub = c.take<int32_t>(static_cast<size_t>(max_chunks(num_edges)));
-    l.big_hubs = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
+    l.multi_hubs = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.num_items = item_capacity_for(num_keys);
     l.item_first = c.take<int32_t>(static_cast<size_t>(l.num_items) + 1);
     l.item_short = c.take<int32_t>(static_cast<size_t>(l.num_items) + 1);
@@ -169,7 +169,7 @@ CsrScratch csr_scratch(void* mem, int64_t num_keys, int64_t num_edges) {
     l.sort.scan_tmp = c.take<uint32_t>(scan_tmp_words(static_cast<int64_t>(hist)));
     const size_t hw = hub_list_words(num_keys);
     l.hub_counts = c.take<uint32_t>(hw);
-    l.hub_scan_tmp = c.take<uint32_t>(scan_tmp_words(static_cast<int64_t>(hw / 4)));
+    l.hub_scan_tmp = c.take<uint32_t>(64);  // row totals of the hub count scan
     l.weights = c.take<uint32_t>(static_cast<size_t>(num_keys) + 1);
     l.weight_scan_tmp = c.take<uint32_t>(scan_tmp_words(num_keys + 1));
     l.bytes = c.used();
@@ -239,7 +239,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->hub_key = l.hub_key;
     plan->hub_chunk_base = l.hub_chunk_base;
     plan->chunk_hub = l.chunk_hub;
-    plan->big_hubs = l.big_hubs;
+    plan->multi_hubs = l.multi_hubs;
     plan->item_first = l.item_first;
     plan->item_short = l.item_short;
     plan->short_off = l.short_off;
@@ -255,7 +255,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_HIP(launch_offsets_from_sorted(reinterpret_cast<const uint32_t*>(l.keys_sorted), num_edges,
                                         key_bound, l.offsets, s),
              "relm_mp offsets kernel");
-    RELM_HIP(launch_hub_list(l.offsets, key_bound, l.hub_key, l.hub_chunk_base, l.big_hubs,
+    RELM_HIP(launch_hub_list(l.offsets, key_bound, l.hub_key, l.hub_chunk_base, l.multi_hubs,
                              max_hubs(num_edges), sc.hub_counts, sc.hub_scan_tmp, l.status, s),
              "relm_mp hub list kernels");
     RELM_HIP(launch_item_first(l.offsets, l.gather_sorted, key_bound, sc.weights,
@@ -268,13 +268,13 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->max_degree = static_cast<int64_t>(host.max_degree);
     plan->num_hubs = static_cast<int64_t>(host.num_hubs);
     plan->num_chunks = static_cast<int64_t>(host.num_chunks);
-    plan->num_big_hubs = static_cast<int64_t>(host.num_big_hubs);
+    plan->num_multi_hubs = static_cast<int64_t>(host.num_multi_hubs);
     plan->num_items = std::min<int64_t>(static_cast<int64_t>(host.total_weight) / kItemSize + 1,
                                         l.num_items);
     plan->num_short = static_cast<int64_t>(host.total_weight) - key_bound;
     plan->gather_identity = gathers == nullptr || host.gather_mismatch == 0 ? 1 : 0;
     if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges) ||
-        plan->num_big_hubs > plan->num_hubs)
+        plan->num_multi_hubs > plan->num_hubs)
         return set_error(RELM_MP_ERR_HIP, "relm_mp: hub list overflow");
     RELM_HIP(launch_chunk_map(l.offsets, l.hub_key, l.hub_chunk_base, plan->num_hubs,
                               plan->num_chunks, l.chunk_hub, s),

@@ -20,7 +20,7 @@ struct DevStatus {
     unsigned long long num_hubs;         // CSR plans: segments longer than the hub threshold
     unsigned long long num_chunks;       // CSR plans: chunks over all hubs
     unsigned long long max_degree;       // CSR plans: longest segment
-    unsigned long long num_big_hubs;     // CSR plans: hubs over RELM_MP_BIG_HUB_CHUNKS chunks
+    unsigned long long num_multi_hubs;   // CSR plans: hubs of more than one chunk
     unsigned long long total_weight;     // CSR plans: sum of the walk weights of all keys
     unsigned long long gather_mismatch;  // CSR plans: nonzero if gathers[e] != e for some edge
     unsigned long long key_mismatch;     // inverse plans: nonzero if keys[e] != e for some edge
@@ -33,7 +33,6 @@ constexpr unsigned long long kNoEdge = ~0ull;
 // the others are walked in items of kItemSize positions.
 constexpr int kHubThreshold = RELM_MP_HUB_THRESHOLD;
 constexpr int kChunkSize = RELM_MP_CHUNK_SIZE;
-constexpr int kBigHubChunks = RELM_MP_BIG_HUB_CHUNKS;
 constexpr int kItemSize = RELM_MP_ITEM_SIZE;
 
 // Radix sort geometry (LSD, 8-bit digits at most).
@@ -86,7 +85,7 @@ hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, in
 // the same length.
 size_t hub_list_words(int64_t num_keys);
 hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
-                           int32_t* hub_chunk_base, int32_t* big_hubs, int64_t hub_capacity,
+                           int32_t* hub_chunk_base, int32_t* multi_hubs, int64_t hub_capacity,
                            uint32_t* counts, uint32_t* scan_tmp, DevStatus* st, hipStream_t s);
 // Walk items balanced by key weight (1 + messages of non-hub keys), and the
 // short-segment index: short_off[k] = messages of non-hub keys before key k

@@ -38,7 +38,7 @@ __global__ void k_status_init(DevStatus* st) {
         st->num_hubs = 0;
         st->num_chunks = 0;
         st->max_degree = 0;
-        st->num_big_hubs = 0;
+        st->num_multi_hubs = 0;
         st->total_weight = 0;
         st->gather_mismatch = 0;
         st->key_mismatch = 0;
@@ -99,6 +99,53 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_tile_sums(const uint32_t*
 }
 
 // Exclusive scan of one tile per block, in place, with a per-tile carry.
+// Exclusive scan of every row of a [gridDim.x, len] array in place (one
+// workgroup per row, kScanTile values per step with a running carry);
+// tot[row] receives the row's sum.
+__global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict__ data,
+                                                            int64_t len,
+                                                            uint32_t* __restrict__ tot) {
+    __shared__ uint32_t tile[kScanTile];
+    __shared__ uint32_t lds[kScanThreads / kWave];
+    uint32_t* row = data + static_cast<int64_t>(blockIdx.x) * len;
+    uint32_t carry = 0;
+    for (int64_t base = 0; base < len; base += kScanTile) {
+        uint32_t in[kScanItems];
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
+            in[i] = p < len ? row[p] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) tile[i * kScanThreads + threadIdx.x] = in[i];
+        __syncthreads();
+        uint32_t v[kScanItems];
+        uint32_t sum = 0;
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            v[i] = tile[threadIdx.x * kScanItems + i];
+            sum += v[i];
+        }
+        uint32_t total;
+        const uint32_t incl = block_inclusive_scan<kScanThreads>(sum, lds, total);
+        uint32_t run = incl - sum + carry;
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            tile[threadIdx.x * kScanItems + i] = run;
+            run += v[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
+            if (p < len) row[p] = tile[i * kScanThreads + threadIdx.x];
+        }
+        carry += total;
+        __syncthreads();  // tile is rewritten by the next step
+    }
+    if (threadIdx.x == 0) tot[blockIdx.x] = carry;
+}
+
 __global__ __launch_bounds__(kScanThreads) void k_scan_tile_apply(uint32_t* __restrict__ data,
                                                                   int64_t n,
                                                                   const uint32_t* __restrict__ carry) {
@@ -184,6 +231,8 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const void* __re
             }
         }
     }
+    // one LDS atomic per distinct digit of a wave: hub keys repeat a digit
+    // across many lanes, and same-address atomics serialise
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
@@ -207,8 +256,8 @@ template <bool kFirst>
 __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     const void* __restrict__ keys, const void* __restrict__ vals, int64_t n, int shift, int bits,
     int64_t key_bound, int64_t gather_bound, const uint32_t* __restrict__ hist_scanned,
-    int64_t nblocks, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
-    DevStatus* __restrict__ st) {
+    const uint32_t* __restrict__ digit_tot, int64_t nblocks, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, DevStatus* __restrict__ st) {
     constexpr int kWaves = kSortThreads / kWave;
     constexpr int kPerWave = kSortTile / kWaves;
     __shared__ uint32_t wcnt[kWaves][kSortBins];
@@ -283,7 +332,12 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     uint32_t total;
     const uint32_t incl = block_inclusive_scan<kSortThreads>(run, scan_lds, total);
     dstart[dd] = incl - run;
-    gbase[dd] = hist_scanned[static_cast<int64_t>(dd) * nblocks + blockIdx.x];
+    // global start of digit dd: all smaller digits of every tile, then this
+    // digit in the tiles before this one (rows of hist_scanned)
+    const uint32_t dt = digit_tot[dd];
+    uint32_t all;
+    const uint32_t dincl = block_inclusive_scan<kSortThreads>(dt, scan_lds, all);
+    gbase[dd] = (dincl - dt) + hist_scanned[static_cast<int64_t>(dd) * nblocks + blockIdx.x];
     __syncthreads();
 
     const int64_t rem = n - tile_base;
@@ -316,13 +370,29 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
 __global__ __launch_bounds__(kThreads) void k_offsets_from_sorted(const uint32_t* __restrict__ ks,
                                                                   int64_t n, int64_t num_keys,
                                                                   int32_t* __restrict__ offsets) {
+    // thread t covers positions [4t, 4t + 4) (one 16-byte load) and writes
+    // offsets[k] = i for every key k in (ks[i - 1], ks[i]]; position n closes
+    // the keys after the last edge.
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i <= n;
-         i += stride) {
-        const int64_t prev = i == 0 ? -1 : static_cast<int64_t>(ks[i - 1]);
-        int64_t cur = i == n ? num_keys : static_cast<int64_t>(ks[i]);
-        if (cur > num_keys) cur = num_keys;
-        for (int64_t k = prev + 1; k <= cur; ++k) offsets[k] = static_cast<int32_t>(i);
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; 4 * t <= n;
+         t += stride) {
+        const int64_t i0 = 4 * t;
+        int64_t cur[4];
+        if (i0 + 4 <= n) {
+            const uint4 v = *reinterpret_cast<const uint4*>(ks + i0);
+            cur[0] = v.x; cur[1] = v.y; cur[2] = v.z; cur[3] = v.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cur[j] = i0 + j < n ? static_cast<int64_t>(ks[i0 + j]) : num_keys;
+        }
+        int64_t prev = i0 == 0 ? -1 : static_cast<int64_t>(ks[i0 - 1]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i0 + j > n) break;
+            const int64_t c = cur[j] > num_keys ? num_keys : cur[j];
+            for (int64_t k = prev + 1; k <= c; ++k) offsets[k] = static_cast<int32_t>(i0 + j);
+            prev = c > prev ? c : prev;
+        }
     }
 }
 
@@ -333,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void k_offsets_from_sorted(const uint32_t
 struct HubFlags {
     uint32_t hub;
     uint32_t chunks;
-    uint32_t big;
+    uint32_t multi;
     int64_t deg;
 };
 
@@ -344,7 +414,7 @@ __device__ __forceinline__ HubFlags hub_flags(const int32_t* __restrict__ offset
     if (f.deg > kHubThreshold) {
         f.hub = 1u;
         f.chunks = static_cast<uint32_t>((f.deg + kChunkSize - 1) / kChunkSize);
-        f.big = f.chunks > static_cast<uint32_t>(kBigHubChunks) ? 1u : 0u;
+        f.multi = f.chunks > 1u ? 1u : 0u;
     }
     return f;
 }
@@ -359,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void k_hub_count(const int32_t* __restric
     uint32_t th, tc, tb;
     block_inclusive_scan<kThreads>(f.hub, lds, th);
     block_inclusive_scan<kThreads>(f.chunks, lds, tc);
-    block_inclusive_scan<kThreads>(f.big, lds, tb);
+    block_inclusive_scan<kThreads>(f.multi, lds, tb);
     uint32_t m = f.deg > 0 ? static_cast<uint32_t>(f.deg) : 0u;
 #pragma unroll
     for (int o = kWave / 2; o > 0; o >>= 1) {
@@ -389,7 +459,7 @@ __global__ __launch_bounds__(kThreads) void k_hub_write(const int32_t* __restric
                                                         const uint32_t* __restrict__ counts,
                                                         int32_t* __restrict__ hub_key,
                                                         int32_t* __restrict__ hub_chunk_base,
-                                                        int32_t* __restrict__ big_hubs,
+                                                        int32_t* __restrict__ multi_hubs,
                                                         int64_t hub_capacity) {
     __shared__ uint32_t lds[kThreads / kWave];
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -397,16 +467,16 @@ __global__ __launch_bounds__(kThreads) void k_hub_write(const int32_t* __restric
     uint32_t th, tc, tb;
     const uint32_t ih = block_inclusive_scan<kThreads>(f.hub, lds, th);
     const uint32_t ic = block_inclusive_scan<kThreads>(f.chunks, lds, tc);
-    const uint32_t ib = block_inclusive_scan<kThreads>(f.big, lds, tb);
+    const uint32_t ib = block_inclusive_scan<kThreads>(f.multi, lds, tb);
     if (!f.hub) return;
     const int64_t stride = nblk + 1;
     const int64_t slot = static_cast<int64_t>(counts[blockIdx.x]) + ih - 1;
     if (slot < 0 || slot >= hub_capacity) return;
     hub_key[slot] = static_cast<int32_t>(k);
     hub_chunk_base[slot] = static_cast<int32_t>(counts[stride + blockIdx.x] + ic - f.chunks);
-    if (f.big) {
+    if (f.multi) {
         const int64_t b = static_cast<int64_t>(counts[2 * stride + blockIdx.x]) + ib - 1;
-        if (b >= 0 && b < hub_capacity) big_hubs[b] = static_cast<int32_t>(slot);
+        if (b >= 0 && b < hub_capacity) multi_hubs[b] = static_cast<int32_t>(slot);
     }
 }
 
@@ -433,7 +503,7 @@ __global__ __launch_bounds__(kThreads) void k_hub_totals(const uint32_t* __restr
         st->max_degree = mm;
         st->num_hubs = counts[nblk];
         st->num_chunks = counts[stride + nblk];
-        st->num_big_hubs = counts[2 * stride + nblk];
+        st->num_multi_hubs = counts[2 * stride + nblk];
     }
 }
 
@@ -581,7 +651,8 @@ hipError_t launch_exclusive_scan_u32(uint32_t* data, int64_t n, uint32_t* tmp, h
 
 size_t sort_hist_words(int64_t n) {
     const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
-    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks);
+    // per-tile digit counts, then the digit totals
+    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks + 1);
 }
 
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
@@ -612,16 +683,21 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         }
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
-        err = launch_exclusive_scan_u32(buf.hist, hist_n, buf.scan_tmp, s);
+        uint32_t* digit_tot = buf.hist + hist_n;
+        hipLaunchKernelGGL(k_scan_rows, dim3(kSortBins), dim3(kScanThreads), 0, s, buf.hist, nblocks,
+                           digit_tot);
+        err = hipGetLastError();
         if (err != hipSuccess) return err;
         if (p == 0) {
             hipLaunchKernelGGL(k_radix_downsweep<true>, dim3(static_cast<unsigned>(nblocks)),
                                dim3(kSortThreads), 0, s, in_k, in_v, n, shift, width, key_bound,
-                               gather_bound, buf.hist, nblocks, out_k, out_v, st);
+                               gather_bound, buf.hist, static_cast<const uint32_t*>(digit_tot),
+                               nblocks, out_k, out_v, st);
         } else {
             hipLaunchKernelGGL(k_radix_downsweep<false>, dim3(static_cast<unsigned>(nblocks)),
                                dim3(kSortThreads), 0, s, in_k, in_v, n, shift, width, key_bound,
-                               gather_bound, buf.hist, nblocks, out_k, out_v, st);
+                               gather_bound, buf.hist, static_cast<const uint32_t*>(digit_tot),
+                               nblocks, out_k, out_v, st);
         }
         err = hipGetLastError();
         if (err != hipSuccess) return err;
@@ -634,8 +710,8 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
 
 hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
                                       int32_t* offsets, hipStream_t s) {
-    hipLaunchKernelGGL(k_offsets_from_sorted, dim3(grid_1d(n + 1, kThreads)), dim3(kThreads), 0, s,
-                       keys_sorted, n, num_keys, offsets);
+    hipLaunchKernelGGL(k_offsets_from_sorted, dim3(grid_1d(n / 4 + 1, kThreads)), dim3(kThreads), 0,
+                       s, keys_sorted, n, num_keys, offsets);
     return hipGetLastError();
 }
 
@@ -645,7 +721,7 @@ size_t hub_list_words(int64_t num_keys) {
 }
 
 hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
-                           int32_t* hub_chunk_base, int32_t* big_hubs, int64_t hub_capacity,
+                           int32_t* hub_chunk_base, int32_t* multi_hubs, int64_t hub_capacity,
                            uint32_t* counts, uint32_t* scan_tmp, DevStatus* st, hipStream_t s) {
     if (num_keys <= 0) return hipSuccess;
     const int64_t nblk = (num_keys + kThreads - 1) / kThreads;
@@ -653,13 +729,13 @@ hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hu
                        num_keys, nblk, counts);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    for (int a = 0; a < 3; ++a) {
-        err = launch_exclusive_scan_u32(counts + a * (nblk + 1), nblk + 1, scan_tmp, s);
-        if (err != hipSuccess) return err;
-    }
+    // the three count arrays are consecutive rows of nblk + 1 values
+    hipLaunchKernelGGL(k_scan_rows, dim3(3), dim3(kScanThreads), 0, s, counts, nblk + 1, scan_tmp);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_hub_write, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
                        num_keys, nblk, static_cast<const uint32_t*>(counts), hub_key, hub_chunk_base,
-                       big_hubs, hub_capacity);
+                       multi_hubs, hub_capacity);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_hub_totals, dim3(1), dim3(kThreads), 0, s, static_cast<const uint32_t*>(counts),

@@ -16,10 +16,9 @@
 //    gathered indices of its items in LDS first, leaving one memory round trip
 //    per batch of message rows.
 //  * hubs: k_hub_chunks, one workgroup per chunk of kChunkSize messages; each
-//    row group folds a contiguous slice, the slices are folded in slice order.
+//    row group folds a contiguous slice, the slices are folded as a fixed tree.
 //    Single-chunk hubs are finished there; the others leave chunk partials that
-//    k_hub_combine_small (one row group per hub) or k_hub_combine_big (one
-//    1024-thread workgroup per hub) fold in chunk order.
+//    k_hub_combine (one workgroup per hub) folds the same way.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -33,13 +32,19 @@ namespace relm_mp {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBigThreads = 1024;
 constexpr int kRowsInFlight = 4;          // rows per row group per iteration (inverse plans)
 constexpr int64_t kMaxBlocksX = 1 << 22;  // keeps blocks * 1024 threads below 2^32
 
 template <int G>
 constexpr int batch_rows() {
     return G < 8 ? G : 8;
+}
+
+// Element offset of row `row` (a valid row index, below 2^31) of a table of
+// D columns: one unsigned 32 x 32 -> 64 multiply instead of a signed 64-bit one.
+__device__ __forceinline__ uint64_t row_offset(int64_t row, int64_t D) {
+    return static_cast<uint64_t>(static_cast<uint32_t>(row)) *
+           static_cast<uint64_t>(static_cast<uint32_t>(D));
 }
 
 template <typename T, int V>
@@ -134,7 +139,7 @@ struct SumOp {
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + static_cast<int64_t>(idx[u]) * D + col)
+            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + row_offset(idx[u], D) + col)
                                       : pack_fill<T, V>(T(0));
     }
     __device__ __forceinline__ void consume(int cnt) {
@@ -151,9 +156,10 @@ struct SumOp {
 // Logsumexp of table rows as a blocked max-then-sum: per batch the batch
 // maximum first, then exp(x - max) summed against the running maximum (s is
 // kept relative to m and rescaled when m grows).  Semantics of the reference's
-// amax / exp / sum / log sequence: a NaN message makes the result NaN (tracked
-// in `nan`, because the maximum ignores NaN), messages that are all -inf give
-// NaN, an empty segment -inf.
+// amax / exp / sum / log sequence: a NaN message makes the result NaN (s
+// becomes NaN: through exp(NaN - m), or explicitly while m is still -inf,
+// because the maximum ignores NaN), messages that are all -inf give NaN, an
+// empty segment -inf.
 template <typename T, int V, int U>
 struct LseOp {
     using Partial = LsePartial<T, V>;
@@ -162,17 +168,16 @@ struct LseOp {
     int64_t col;
     bool colok;
     Pack<T, V> x[U];
-    Pack<T, V> m, s, nan;
+    Pack<T, V> m, s;
 
     __device__ __forceinline__ void begin(int64_t, bool) {
         m = pack_fill<T, V>(neg_inf<T>());
         s = pack_fill<T, V>(T(0));
-        nan = pack_fill<T, V>(T(0));
     }
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + static_cast<int64_t>(idx[u]) * D + col)
+            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + row_offset(idx[u], D) + col)
                                       : pack_fill<T, V>(neg_inf<T>());
     }
     __device__ __forceinline__ void consume(int cnt) {
@@ -193,7 +198,7 @@ struct LseOp {
             } else {
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    if (u < cnt && x[u].v[i] != x[u].v[i]) nan.v[i] = T(1);
+                    if (u < cnt && x[u].v[i] != x[u].v[i]) s.v[i] = quiet_nan<T>();
             }
         }
     }
@@ -217,7 +222,7 @@ struct LseOp {
         for (int i = 0; i < V; ++i) {
             if (!nonempty)
                 r.v[i] = neg_inf<T>();
-            else if (nan.v[i] != T(0) || m.v[i] == neg_inf<T>() || m.v[i] == -neg_inf<T>())
+            else if (m.v[i] == neg_inf<T>() || m.v[i] == -neg_inf<T>())
                 r.v[i] = quiet_nan<T>();
             else
                 r.v[i] = dev_log<T>(s.v[i]) + m.v[i];
@@ -225,13 +230,7 @@ struct LseOp {
         return r;
     }
     __device__ __forceinline__ Pack<T, V> empty() const { return pack_fill<T, V>(neg_inf<T>()); }
-    __device__ __forceinline__ Partial partial() const {
-        Partial p{m, s};
-#pragma unroll
-        for (int i = 0; i < V; ++i)
-            if (nan.v[i] != T(0)) p.s.v[i] = quiet_nan<T>();
-        return p;
-    }
+    __device__ __forceinline__ Partial partial() const { return Partial{m, s}; }
 };
 
 // Logsumexp backward of key r (= a rel row): sum over its messages of
@@ -256,7 +255,7 @@ struct LseBwdOp {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const bool ok = u < cnt && colok;
-            const int64_t off = static_cast<int64_t>(idx[u]) * D + col;
+            const uint64_t off = row_offset(idx[u], D) + col;
             g[u] = ok ? pack_load<T, V>(grad_out + off) : pack_fill<T, V>(T(0));
             o[u] = ok ? pack_load<T, V>(out + off) : pack_fill<T, V>(T(0));
         }
@@ -559,48 +558,25 @@ __device__ __forceinline__ Partial fold_partials(const T* __restrict__ partial, 
     return acc;
 }
 
-// Hubs of 2..kBigHubChunks chunks: one row group per hub, chunks in order.
+// Hubs of more than one chunk: one workgroup per hub.  Row group g folds a
+// contiguous range of the hub's chunk partials in chunk order; the group
+// results are folded as a fixed tree (shuffles inside a wave, then the waves in
+// order), so the result is deterministic.
 template <typename T, int V, int G, class Partial>
-__global__ __launch_bounds__(kThreads) void k_hub_combine_small(
+__global__ __launch_bounds__(kThreads) void k_hub_combine(
     const int32_t* __restrict__ offsets, int64_t num_edges, int64_t D,
     const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
-    int64_t num_hubs, int64_t num_chunks, const T* __restrict__ partial, T* __restrict__ out) {
-    constexpr int R = kThreads / G;
-    constexpr int U = batch_rows<G>();
-    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
-    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
-    if (col >= D) return;
-    for (int64_t h = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; h < num_hubs;
-         h += static_cast<int64_t>(gridDim.x) * R) {
-        const int64_t key = hub_key[h];
-        const int64_t sb = clamp64(offsets[key], 0, num_edges);
-        const int64_t se = clamp64(offsets[key + 1], sb, num_edges);
-        const int64_t nch = (se - sb + kChunkSize - 1) / kChunkSize;
-        if (nch < 2 || nch > kBigHubChunks) continue;
-        const int64_t base = hub_chunk_base[h];
-        if (base < 0 || base + nch > num_chunks) continue;
-        const Partial acc = fold_partials<Partial, T, U>(partial, base, base + nch, D, col);
-        pack_store<T, V>(out + key * D + col, acc.value());
-    }
-}
-
-// Hubs of more than kBigHubChunks chunks: one 1024-thread workgroup per hub;
-// group g folds a contiguous range of chunks, group results in group order.
-template <typename T, int V, int G, class Partial>
-__global__ __launch_bounds__(kBigThreads) void k_hub_combine_big(
-    const int32_t* __restrict__ offsets, int64_t num_edges, int64_t D,
-    const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
-    const int32_t* __restrict__ big_hubs, int64_t num_hubs, int64_t num_big_hubs,
+    const int32_t* __restrict__ multi_hubs, int64_t num_hubs, int64_t num_multi_hubs,
     int64_t num_chunks, const T* __restrict__ partial, T* __restrict__ out) {
-    constexpr int NG = kBigThreads / G;
+    constexpr int NG = kThreads / G;
     constexpr int U = batch_rows<G>();
-    __shared__ Partial red[kBigThreads];
+    __shared__ Partial red[kThreads / kWave * G];
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int grp = static_cast<int>(threadIdx.x) / G;
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     const bool colok = col < D;
-    for (int64_t bi = blockIdx.x; bi < num_big_hubs; bi += gridDim.x) {
-        const int64_t h = big_hubs[bi];
+    for (int64_t bi = blockIdx.x; bi < num_multi_hubs; bi += gridDim.x) {
+        const int64_t h = multi_hubs[bi];
         const bool hok = h >= 0 && h < num_hubs;
         const int64_t key = hok ? hub_key[h] : 0;
         const int64_t sb = hok ? clamp64(offsets[key], 0, num_edges) : 0;
@@ -611,12 +587,19 @@ __global__ __launch_bounds__(kBigThreads) void k_hub_combine_big(
         const int64_t per = (nch + NG - 1) / NG;
         const int64_t lo = clamp64(grp * per, 0, nch);
         const int64_t hi = clamp64(lo + per, lo, nch);
-        red[threadIdx.x] = colok ? fold_partials<Partial, T, U>(partial, base + lo, base + hi, D, col)
-                                 : Partial::identity();
+        Partial pg = colok ? fold_partials<Partial, T, U>(partial, base + lo, base + hi, D, col)
+                           : Partial::identity();
+        const int gw_idx = (static_cast<int>(threadIdx.x) & (kWave - 1)) / G;
+#pragma unroll
+        for (int sgrp = 1; sgrp < kWave / G; sgrp <<= 1) {
+            const Partial other = pg.shfl_down(sgrp * G);
+            if ((gw_idx & (2 * sgrp - 1)) == 0) pg.merge(other);
+        }
+        if (gw_idx == 0) red[(threadIdx.x / kWave) * G + gl] = pg;
         __syncthreads();
         if (grp == 0 && colok && hok && nch > 0) {
             Partial acc = red[gl];
-            for (int g = 1; g < NG; ++g) acc.merge(red[g * G + gl]);
+            for (int wv = 1; wv < kThreads / kWave; ++wv) acc.merge(red[wv * G + gl]);
             pack_store<T, V>(out + key * D + col, acc.value());
         }
         __syncthreads();
@@ -662,7 +645,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
         for (int j = 0; j < RU; ++j) {
             v[j] = pack_fill<T, V>(T(0));
             if (static_cast<uint64_t>(g[j]) < static_cast<uint64_t>(num_gather))
-                v[j] = pack_load<T, V>(table + g[j] * D + col);
+                v[j] = pack_load<T, V>(table + row_offset(g[j], D) + col);
         }
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
@@ -689,7 +672,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __r
         const int64_t b = clamp64(offsets[key], 0, num_edges);
         const int64_t e = clamp64(offsets[key + 1], b, num_edges);
         Pack<T, V> v = pack_fill<T, V>(T(0));
-        if (e > b) v = pack_load<T, V>(table + static_cast<int64_t>(gs[e - 1]) * D + col);
+        if (e > b) v = pack_load<T, V>(table + row_offset(gs[e - 1], D) + col);
         pack_store_stream<T, V>(out + key * D + col, v);
     }
 }
@@ -722,8 +705,8 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
             const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
             const int64_t key = key0 + j * ngroups;
             x[j] = ok ? pack_load_stream<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
-            g[j] = ok ? pack_load<T, V>(grad_out + d[j] * D + col) : pack_fill<T, V>(T(0));
-            o[j] = ok ? pack_load<T, V>(out + d[j] * D + col) : pack_fill<T, V>(T(0));
+            g[j] = ok ? pack_load<T, V>(grad_out + row_offset(d[j], D) + col) : pack_fill<T, V>(T(0));
+            o[j] = ok ? pack_load<T, V>(out + row_offset(d[j], D) + col) : pack_fill<T, V>(T(0));
         }
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
@@ -815,17 +798,11 @@ int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, 
                        plan.num_chunks, partial, out, op);
     rc = hip_error(hipGetLastError(), "relm_mp hub chunk kernel");
     if (rc != RELM_MP_OK || plan.num_chunks == plan.num_hubs) return rc;  // single-chunk hubs only
-    hipLaunchKernelGGL((k_hub_combine_small<T, V, G, Partial>), row_grid(plan.num_hubs, G, slices),
+    hipLaunchKernelGGL((k_hub_combine<T, V, G, Partial>), block_grid(plan.num_multi_hubs, slices),
                        dim3(kThreads), 0, s, plan.offsets, plan.num_edges, emb, plan.hub_key,
-                       plan.hub_chunk_base, plan.num_hubs, plan.num_chunks,
-                       static_cast<const T*>(partial), out);
-    rc = hip_error(hipGetLastError(), "relm_mp hub combine kernel");
-    if (rc != RELM_MP_OK || plan.num_big_hubs == 0) return rc;
-    hipLaunchKernelGGL((k_hub_combine_big<T, V, G, Partial>), block_grid(plan.num_big_hubs, slices),
-                       dim3(kBigThreads), 0, s, plan.offsets, plan.num_edges, emb, plan.hub_key,
-                       plan.hub_chunk_base, plan.big_hubs, plan.num_hubs, plan.num_big_hubs,
+                       plan.hub_chunk_base, plan.multi_hubs, plan.num_hubs, plan.num_multi_hubs,
                        plan.num_chunks, static_cast<const T*>(partial), out);
-    return hip_error(hipGetLastError(), "relm_mp big hub combine kernel");
+    return hip_error(hipGetLastError(), "relm_mp hub combine kernel");
 }
 
 template <typename T>

@@ -183,7 +183,10 @@ def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, sk
     assert bp.plan.num_hubs == int((deg > hub).sum())
     nch = (deg[deg > hub] + chunk - 1) // chunk
     assert bp.plan.num_chunks == int(nch.sum())
-    assert bp.plan.num_big_hubs == int((nch > 64).sum())
+    assert bp.plan.num_multi_hubs == int((nch > 1).sum())
+    got_multi = bp.mem[bp.plan.multi_hubs - bp.mem.data_ptr():][: 4 * int((nch > 1).sum())].view(torch.int32) \
+        if (nch > 1).any() else torch.zeros(0, dtype=torch.int32)
+    assert np.array_equal(_np(got_multi), np.flatnonzero(nch > 1))
     # hubs are listed in key order; items start at the first key of their position range
     hub_keys = np.flatnonzero(deg > hub)
     got_hubs = bp.mem[bp.plan.hub_key - bp.mem.data_ptr():][: 4 * hub_keys.size].view(torch.int32)
