@@ -271,6 +271,10 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kSortTile;
     const uint32_t dmask = (1u << bits) - 1u;
+    // this tile's start within each digit does not depend on the keys: fetch
+    // it together with them
+    const uint32_t tile_prefix = hist_scanned[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x];
+    const uint32_t dt = digit_tot[threadIdx.x];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][threadIdx.x] = 0;
     __syncthreads();
@@ -334,10 +338,9 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     dstart[dd] = incl - run;
     // global start of digit dd: all smaller digits of every tile, then this
     // digit in the tiles before this one (rows of hist_scanned)
-    const uint32_t dt = digit_tot[dd];
     uint32_t all;
     const uint32_t dincl = block_inclusive_scan<kSortThreads>(dt, scan_lds, all);
-    gbase[dd] = (dincl - dt) + hist_scanned[static_cast<int64_t>(dd) * nblocks + blockIdx.x];
+    gbase[dd] = (dincl - dt) + tile_prefix;
     __syncthreads();
 
     const int64_t rem = n - tile_base;
