@@ -15,9 +15,10 @@ The JSON line also carries
   cpu_baseline  - the reference's own CPU op library (oracle/_ref) on a
                   bounded 1/8-scale sample of C2, on the host's cores;
   extra         - kernel-only rates with cached plans, C2 with sum, C3 fanout
-                  forward + backward, C1 latencies.
+                  forward + backward, C1 latencies, C4 / C5 model training
+                  steps (graphs/sec).
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1|copy]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1|c4|c5|copy]
 """
 
 from __future__ import annotations
@@ -209,6 +210,43 @@ def bench_c1(torch, mp, syn) -> dict:
     return out
 
 
+def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
+    """C4 (RelationalGNN, fast fused relation layer) and C5
+    (CentralizedRelationalGNN, fused central layer): fp32 training step =
+    forward + backward of mean(out^2) through relmo_amd.mp (HIP ops), index
+    routing built once per batch as in the reference layers; graphs/sec =
+    graphs / time per step.  C5 runs 512 of its 2048 graphs: ten layers of
+    saved activations for 2048 graphs (about 40 GB per layer) exceed one
+    GPU's 288 GB."""
+
+    from relmo_amd import consumers as C
+
+    dev = torch.device("cuda", 0)
+    if which == "c4":
+        batch = C.synthetic_c4(dev)
+        make = lambda mode: C.RelationalGNN(32, 10, batch.relations, mode).to(dev)
+        cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects, "emb": 32, "layers": 10}
+    else:
+        batch = C.synthetic_c5(dev, num_graphs=512)
+        make = lambda mode: C.CentralizedRelationalGNN(128, 10, batch.relations, mode).to(dev)
+        cfg = {"graphs": batch.num_graphs, "graphs_in_config": 2048, "objects": batch.num_objects,
+               "emb": 128, "layers": 10}
+    res = {"config": cfg}
+    for mode, name in ((0, "sum"), (1, "logsumexp")):
+        torch.manual_seed(0)
+        model = make(mode)
+        routing = model.routing(batch)
+        torch.cuda.reset_peak_memory_stats()
+        t = timed(lambda: C.train_step(model, batch, routing), steps, warmup, torch.cuda.synchronize)
+        res[name] = {"ms_step": t * 1e3, "graphs_per_sec": batch.num_graphs / t,
+                     "peak_gb": torch.cuda.max_memory_allocated() / 1e9}
+        del model, routing
+        torch.cuda.empty_cache()
+    if which == "c4":
+        res["slots"] = int(sum(a.numel() for a in batch.atoms.values()))
+    return res
+
+
 def bench_copy(torch, steps: int) -> dict:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the HBM
     byte counters (FETCH_SIZE / WRITE_SIZE per dispatch against 1 GiB)."""
@@ -220,14 +258,28 @@ def bench_copy(torch, steps: int) -> dict:
     return {"bytes_read": 4 * n, "bytes_written": 4 * n, "ms": sec * 1e3, "gbs": gbs(8 * n, sec)}
 
 
-def cpu_baseline(syn) -> dict:
-    """The reference's CPU op library on a 1/8-scale C2 sample (same generator,
-    131,072 objects, 2,097,152 messages), logsumexp forward + backward, on all
-    host cores; falls back to the C oracle (1 core) where oracle/_ref is absent."""
+def host_threads() -> int:
+    """Host threads this job may use: the box's CPU share (OMP_NUM_THREADS),
+    not every core the OS reports."""
+
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(os.cpu_count() or 1, share))
+
+
+def cpu_baseline(syn, torch) -> dict:
+    """CPU baselines on a 1/8-scale C2 sample (same generator: 131,072 objects,
+    2,097,152 messages), logsumexp forward + backward, on the host's cores:
+      * the reference's own CPU op library (oracle/_ref, built from mp_ops.cpp),
+        at 1 thread and at the job's thread share - the headline baseline;
+      * relmo's python_only path (ATen index_select / scatter_reduce / exp /
+        scatter_add / log and autograd, mirrored by relmo_amd.mp_pack) at the
+        same two thread counts.
+    Falls back to the C oracle (1 thread) where oracle/_ref is absent."""
 
     import numpy as np
 
     from oracle import oracle, ref_runner
+    from relmo_amd import mp_pack
 
     K, E, D = 1 << 17, 1 << 21, 32
     rng = np.random.default_rng(0)
@@ -240,26 +292,57 @@ def cpu_baseline(syn) -> dict:
     g = rng.standard_normal((K, D)).astype(np.float32)
     nbytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_lse_bwd(E, D, K, E)
     sample = f"C2 at 1/8 scale: K={K}, E={E}, D={D}, Zipf(1.1) dst, logsumexp fwd+bwd"
-    cores = os.cpu_count() or 1
+    full = host_threads()
+    variants = []
+
+    # python_only: ATen forward + autograd backward, in this process on CPU tensors
+    rel_t = torch.from_numpy(rel)
+    src_t, dst_t, g_t = torch.from_numpy(flat_src), torch.from_numpy(dst), torch.from_numpy(g)
+
+    def aten_step():
+        r = rel_t.clone().requires_grad_(True)
+        out = mp_pack.fanin_reduce_python(r, src_t, dst_t, K, 1)
+        torch.autograd.grad(out, r, g_t)
+
+    saved = torch.get_num_threads()
+    for th in (1, full):
+        torch.set_num_threads(th)
+        if th != 1:  # the 1-thread run is long enough to go unwarmed
+            aten_step()
+        t0 = time.perf_counter()
+        aten_step()
+        t = time.perf_counter() - t0
+        variants.append({"kind": "python_only (ATen)", "threads": th, "seconds": round(t, 4),
+                         "value": round(gbs(nbytes, t), 3)})
+    torch.set_num_threads(saved)
+
     if ref_runner.available():
         out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, K)
         arrays = {"rel": rel, "src": flat_src, "dst": dst, "g": g, "out": out}
-        calls = [
-            {"op": "fanin_reduce", "tensors": ["rel", "src", "dst"], "ints": [K, 1], "repeat": 3, "warmup": 1, "threads": cores},
-            {"op": "fanin_reduce_logsumexp_backward", "tensors": ["g", "rel", "src", "dst", "out"], "ints": [E], "repeat": 3, "warmup": 1, "threads": cores},
-        ]
-        res = ref_runner.run_reference(calls, arrays)
-        t = statistics.median(res[0]["times"]) + statistics.median(res[1]["times"])
-        threads = res[0]["threads"]
-        return {"value": round(gbs(nbytes, t), 3), "unit": "GB/s", "cores": threads, "kind": "reference",
-                "sample": sample + f"; reference CPU lane (ATen sequences, mp_ops.cpp:2981-3036), "
-                                   f"{threads} threads, median of 3, {t:.3f} s per fwd+bwd"}
+        headline = None
+        for th, reps, warm in ((1, 1, 0), (full, 3, 1)):
+            calls = [
+                {"op": "fanin_reduce", "tensors": ["rel", "src", "dst"], "ints": [K, 1], "repeat": reps,
+                 "warmup": warm, "threads": th},
+                {"op": "fanin_reduce_logsumexp_backward", "tensors": ["g", "rel", "src", "dst", "out"],
+                 "ints": [E], "repeat": reps, "warmup": warm, "threads": th},
+            ]
+            res = ref_runner.run_reference(calls, arrays)
+            t = statistics.median(res[0]["times"]) + statistics.median(res[1]["times"])
+            threads = res[0]["threads"]
+            variants.append({"kind": "reference relm_mp_ops CPU lane", "threads": threads,
+                             "seconds": round(t, 4), "value": round(gbs(nbytes, t), 3)})
+            headline = {"value": round(gbs(nbytes, t), 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+                        "sample": sample + f"; reference CPU lane (ATen sequences, mp_ops.cpp:2981-3036), "
+                                           f"{threads} threads, median of {reps}, {t:.3f} s per fwd+bwd"}
+        headline["variants"] = variants
+        return headline
     t0 = time.perf_counter()
     out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, K)
     oracle.fanin_reduce_logsumexp_backward(g, rel, flat_src, dst, out, E)
     t = time.perf_counter() - t0
     return {"value": round(gbs(nbytes, t), 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": sample + f"; C oracle, 1 thread, {t:.3f} s per fwd+bwd"}
+            "sample": sample + f"; C oracle, 1 thread, {t:.3f} s per fwd+bwd", "variants": variants}
 
 
 def main() -> int:
@@ -267,7 +350,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "copy"], default=None,
                     help="run one workload only and print its figures (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -293,6 +376,8 @@ def main() -> int:
               "c2sum": lambda: bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 0),
               "c3": lambda: bench_c3(torch, mp, capi, syn, args.steps, args.warmup),
               "c1": lambda: bench_c1(torch, mp, syn),
+              "c4": lambda: bench_models(torch, "c4", args.steps, args.warmup),
+              "c5": lambda: bench_models(torch, "c5", args.steps, args.warmup),
               "copy": lambda: bench_copy(torch, args.steps)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
@@ -307,11 +392,15 @@ def main() -> int:
     extra["c3_fanout"] = bench_c3(torch, mp, capi, syn, max(5, args.steps // 2), 2)
     log("C1 latencies ...")
     extra["c1_latency_us"] = bench_c1(torch, mp, syn)
+    log("C4 RelationalGNN training step ...")
+    extra["c4_relational_gnn"] = bench_models(torch, "c4", 5, 2)
+    log("C5 CentralizedRelationalGNN training step ...")
+    extra["c5_centralized_gnn"] = bench_models(torch, "c5", 3, 1)
 
     baseline = None
     if not args.no_cpu_baseline:
         log("CPU baseline ...")
-        baseline = cpu_baseline(syn)
+        baseline = cpu_baseline(syn, torch)
 
     kernel = "k_lse_bwd_inv"
     traffic = load_traffic("c2_logsumexp_backward_traffic")

@@ -87,7 +87,9 @@ def _child(req_dir: Path) -> None:
         entry: dict = {"op": op, "threads": torch.get_num_threads()}
         fn = getattr(ns, op)
         try:
+            t0 = time.perf_counter()
             out = fn(*tensors, *ints)
+            first = time.perf_counter() - t0
         except Exception as exc:  # the reference's error is part of the result
             entry["error"] = str(exc).splitlines()[0]
             entry["error_type"] = type(exc).__name__
@@ -96,10 +98,12 @@ def _child(req_dir: Path) -> None:
         outputs[f"out_{i}"] = out.numpy()
         repeat = int(call.get("repeat", 0))
         if repeat:
-            for _ in range(int(call.get("warmup", 1))):
+            warmup = int(call.get("warmup", 1))
+            for _ in range(warmup):
                 fn(*tensors, *ints)
-            times = []
-            for _ in range(repeat):
+            # without warmup the output-producing call is the first timed one
+            times = [] if warmup else [first]
+            while len(times) < repeat:
                 t0 = time.perf_counter()
                 fn(*tensors, *ints)
                 times.append(time.perf_counter() - t0)

@@ -1,0 +1,306 @@
+"""The reference's model-level callers of the ops, restated in plain torch.
+
+relmo's RelationalGNN (``rel_layer_mode="fast_fused"``,
+src/relmo/models/relational_gnn.py:124-535 with
+src/relmo/models/hetero_mp/fast_fused.py:26-300) and CentralizedRelationalGNN
+(``central_layer_mode="fused"``, relational_gnn.py:552-846 with
+hetero_mp/fused.py:121-406) are built on torch_geometric, which is not
+available here.  This module keeps their computation on the hot path - the
+slot layout that feeds ``fanout_scatter`` / ``fanin_reduce``, the relation and
+central MLPs, the embedding update - over a plain batch description, so that a
+training step of either model can be timed (graphs/sec) and compared between
+the HIP op lane and the ATen lane.
+
+Batch: one object node type; ``relations`` maps predicate -> arity; ``atoms``
+maps predicate -> int64 [n, arity] global object ids (arity-0 predicates are
+skipped, as in relational_gnn.py:322-326).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor, nn
+
+from . import mp
+
+
+@dataclass
+class RelationalBatch:
+    num_graphs: int
+    num_objects: int
+    relations: dict[str, int]
+    atoms: dict[str, Tensor]
+
+
+def _graph_atoms(gen: torch.Generator, obj_offsets: Tensor, obj_counts: Tensor, n_per_graph: Tensor,
+                 arity: int) -> Tensor:
+    """Arguments uniform within each graph: [sum(n_per_graph), arity] global ids."""
+
+    graph_of_atom = torch.repeat_interleave(torch.arange(n_per_graph.numel()), n_per_graph)
+    u = torch.rand(int(graph_of_atom.numel()), arity, generator=gen, dtype=torch.float64)
+    local = (u * obj_counts[graph_of_atom].unsqueeze(1).double()).long()
+    local = torch.minimum(local, (obj_counts[graph_of_atom] - 1).unsqueeze(1))
+    return obj_offsets[graph_of_atom].unsqueeze(1) + local
+
+
+def synthetic_c4(device, seed: int = 0, num_graphs: int = 512) -> RelationalBatch:
+    """200 objects per graph, predicates of arity
+    0, 1, 2, 2, 3 with 400 atoms each per graph, uniform arguments."""
+
+    gen = torch.Generator().manual_seed(seed)
+    objs = torch.full((num_graphs,), 200, dtype=torch.long)
+    offsets = torch.cumsum(objs, 0) - objs
+    relations = {"p0": 0, "p1": 1, "p2": 2, "p3": 2, "p4": 3}
+    atoms = {}
+    for name, arity in relations.items():
+        if arity == 0:
+            continue
+        per = torch.full((num_graphs,), 400, dtype=torch.long)
+        atoms[name] = _graph_atoms(gen, offsets, objs, per, arity).to(device)
+    return RelationalBatch(num_graphs, int(objs.sum()), relations, atoms)
+
+
+def synthetic_c5(device, seed: int = 0, num_graphs: int = 2048) -> RelationalBatch:
+    """64-512 objects per graph, 8 predicates of arity
+    1-3, 1000-4000 atoms per graph split uniformly at random over the
+    predicates, uniform arguments within each graph."""
+
+    gen = torch.Generator().manual_seed(seed)
+    objs = torch.randint(64, 513, (num_graphs,), generator=gen)
+    offsets = torch.cumsum(objs, 0) - objs
+    relations = {f"r{i}": int(torch.randint(1, 4, (1,), generator=gen)) for i in range(8)}
+    total_atoms = torch.randint(1000, 4001, (num_graphs,), generator=gen)
+    # split every graph's atoms over the predicates (multinomial, uniform)
+    pick = torch.multinomial(torch.full((8,), 1.0 / 8), int(total_atoms.sum()), replacement=True,
+                             generator=gen)
+    graph_of = torch.repeat_interleave(torch.arange(num_graphs), total_atoms)
+    counts = torch.zeros(num_graphs, 8, dtype=torch.long)
+    counts.index_put_((graph_of, pick), torch.ones_like(pick), accumulate=True)
+    atoms = {}
+    for i, (name, arity) in enumerate(relations.items()):
+        atoms[name] = _graph_atoms(gen, offsets, objs, counts[:, i], arity).to(device)
+    return RelationalBatch(num_graphs, int(objs.sum()), relations, atoms)
+
+
+# ---- modules (relmo/models/mlp.py, residual.py, film.py) ---------------------------------
+
+
+class Residual(nn.Module):
+    """x[..., -width:] + f(x) (residual.py:4-31 with truncate_right=False)."""
+
+    def __init__(self, module: nn.Module, width: int | None = None):
+        super().__init__()
+        self.module = module
+        self.width = width
+
+    def forward(self, x: Tensor) -> Tensor:
+        base = x if self.width is None or x.size(-1) == self.width else x[..., -self.width:]
+        return base + self.module(x)
+
+
+def arity_mlp(feature: int, arity: int, layers: int) -> nn.Module:
+    """ArityMLPFactory(feature_size, residual=True, layers=L)(arity)
+    (mlp.py:127-246): Linear + Mish per hidden layer of width arity * feature."""
+
+    width = feature * arity
+    mods: list[nn.Module] = []
+    dims = [width] * (layers + 1) + [width]
+    for i in range(len(dims) - 1):
+        mods.append(nn.Linear(dims[i], dims[i + 1]))
+        if i < len(dims) - 2:
+            mods.append(nn.Mish())
+    return Residual(nn.Sequential(*mods), width)
+
+
+def simple_mlp(in_size: int, hidden: int, out_size: int) -> nn.Module:
+    """SimpleMLP (mlp.py:50-79): Linear, Mish, Linear."""
+
+    return nn.Sequential(nn.Linear(in_size, hidden), nn.Mish(), nn.Linear(hidden, out_size))
+
+
+class FiLMConcatMLP(nn.Module):
+    """FiLM-conditioned MLP on [cond | features] (film.py:10-195): each hidden
+    layer is Linear -> gamma(c) * h + beta(c) -> Mish, then an output Linear."""
+
+    def __init__(self, in_dim: int, cond_dim: int, hidden: list[int], out_dim: int):
+        super().__init__()
+        self.cond_dim = cond_dim
+        self.lins = nn.ModuleList()
+        self.gammas = nn.ModuleList()
+        self.betas = nn.ModuleList()
+        prev = in_dim
+        for h in hidden:
+            self.lins.append(nn.Linear(prev, h))
+            self.gammas.append(nn.Linear(cond_dim, h))
+            self.betas.append(nn.Linear(cond_dim, h))
+            prev = h
+        self.out = nn.Linear(prev, out_dim)
+        self.act = nn.Mish()
+
+    def forward(self, x: Tensor) -> Tensor:
+        cond, h = x[..., : self.cond_dim], x[..., self.cond_dim:]
+        for lin, g, b in zip(self.lins, self.gammas, self.betas):
+            h = self.act(g(cond) * lin(h) + b(cond))
+        return self.out(h)
+
+
+# ---- RelationalGNN, fast fused relation layer ------------------------------------------
+
+
+class RelationalGNN(nn.Module):
+    """RelationalGNN with the fast fused relation layer: per layer, gather the
+    argument embeddings of every atom into slots (fanout_scatter), apply the
+    predicate's residual MLP, reduce the slot outputs back to objects
+    (fanin_reduce: sum or logsumexp), update X <- X + updater([X, m])."""
+
+    def __init__(self, embedding_size: int, num_layers: int, relations: dict[str, int], mode: int,
+                 mlp_layers: int = 2):
+        super().__init__()
+        self.d = embedding_size
+        self.num_layers = num_layers
+        self.mode = mode
+        self.relations = {p: a for p, a in relations.items() if a > 0}
+        self.rel_mlps = nn.ModuleDict({p: arity_mlp(embedding_size, a, mlp_layers)
+                                       for p, a in self.relations.items()})
+        self.updater = simple_mlp(2 * embedding_size, 2 * embedding_size, embedding_size)
+
+    def routing(self, batch: RelationalBatch) -> dict:
+        """fast_fused.py:79-177: slots ordered by predicate name, slot of
+        (atom, pos) = offset + atom * arity + pos; fanout edges listed per
+        predicate then position, fanin edges the same way."""
+
+        meta, flat, obj = [], [], []
+        total = 0
+        for pred in sorted(self.relations):
+            args = batch.atoms.get(pred)
+            if args is None or args.numel() == 0:
+                continue
+            n, arity = int(args.size(0)), self.relations[pred]
+            meta.append((pred, n, arity, total))
+            atom = torch.arange(n, device=args.device)
+            for pos in range(arity):
+                flat.append(total + atom * arity + pos)
+                obj.append(args[:, pos])
+            total += n * arity
+        flat_t = torch.cat(flat) if flat else torch.zeros(0, dtype=torch.long)
+        obj_t = torch.cat(obj) if obj else torch.zeros(0, dtype=torch.long)
+        # the fanin pair (flat_src, dst) is the same edge list as the fanout pair
+        return {"meta": meta, "total": total, "flat": flat_t, "obj": obj_t}
+
+    def forward(self, batch: RelationalBatch, routing: dict | None = None) -> Tensor:
+        r = routing or self.routing(batch)
+        ref = next(iter(self.updater.parameters()))
+        x = ref.new_zeros(batch.num_objects, self.d)
+        for _ in range(self.num_layers):
+            args = mp.fanout_scatter(x, r["obj"], r["flat"], r["total"])
+            outs = []
+            for pred, n, arity, off in r["meta"]:
+                feat = args[off: off + n * arity].view(n, arity * self.d)
+                outs.append(self.rel_mlps[pred](feat).view(n * arity, self.d))
+            rel_flat = torch.cat(outs) if len(outs) > 1 else outs[0]
+            msgs = mp.fanin_reduce(rel_flat, r["flat"], r["obj"], batch.num_objects, self.mode)
+            if self.mode == mp.MODE_LOGSUMEXP:
+                # objects without atoms receive -inf; the reference's PyG
+                # aggregators give 0 there
+                msgs = torch.where(torch.isfinite(msgs), msgs, torch.zeros_like(msgs))
+            x = x + self.updater(torch.cat([x, msgs], dim=1))
+        return x
+
+
+# ---- CentralizedRelationalGNN, fused central layer -------------------------------------
+
+
+class CentralizedRelationalGNN(nn.Module):
+    """CentralizedRelationalGNN with the fused central layer: every atom's
+    arguments in max_arity padded slots, one central FiLM MLP conditioned on a
+    learned relation embedding plus the slot mask, fanin over the padded slot
+    layout, the same object update as RelationalGNN."""
+
+    def __init__(self, embedding_size: int, num_layers: int, relations: dict[str, int], mode: int,
+                 condition_dim: int | None = None, slot_mask: bool = True):
+        super().__init__()
+        self.d = embedding_size
+        self.num_layers = num_layers
+        self.mode = mode
+        self.relations = dict(relations)
+        self.cond_index = {p: i for i, p in enumerate(self.relations)}
+        self.max_arity = max(self.relations.values(), default=0)
+        self.cond_dim = condition_dim or max(1, int(math.sqrt(embedding_size)))
+        self.mask_dim = self.max_arity if slot_mask else 0
+        self.cond = nn.Embedding(len(self.relations), self.cond_dim)
+        feat_in = self.max_arity * embedding_size + self.mask_dim
+        out = self.max_arity * embedding_size
+        hidden = max(feat_in + self.cond_dim, out)
+        # relational_gnn.py:757-787: residual FiLM MLP, condition first ("pre")
+        self.central = Residual(FiLMConcatMLP(feat_in, self.cond_dim, [hidden], out), out)
+        mask = torch.zeros(len(self.relations), self.max_arity)
+        for p, a in self.relations.items():
+            mask[self.cond_index[p], :a] = 1.0
+        self.register_buffer("slot_mask", mask, persistent=False)
+        self.updater = simple_mlp(2 * embedding_size, 2 * embedding_size, embedding_size)
+
+    def routing(self, batch: RelationalBatch) -> dict:
+        """fused.py:133-232: relation nodes ordered by predicate name; slot of
+        (node, pos) = node * max_arity + pos."""
+
+        meta, flat, obj = [], [], []
+        start = 0
+        for pred in sorted(self.relations):
+            args = batch.atoms.get(pred)
+            if args is None or args.numel() == 0 or self.relations[pred] == 0:
+                continue
+            n, arity = int(args.size(0)), self.relations[pred]
+            meta.append((pred, start, n, arity, self.cond_index[pred]))
+            node = torch.arange(n, device=args.device) + start
+            for pos in range(arity):
+                flat.append(node * self.max_arity + pos)
+                obj.append(args[:, pos])
+            start += n
+        return {"meta": meta, "nodes": start, "flat": torch.cat(flat), "obj": torch.cat(obj)}
+
+    def forward(self, batch: RelationalBatch, routing: dict | None = None) -> Tensor:
+        r = routing or self.routing(batch)
+        ref = self.cond.weight
+        x = ref.new_zeros(batch.num_objects, self.d)
+        nodes, ma, d = r["nodes"], self.max_arity, self.d
+        # context columns [cond | slot mask] per relation node, built once per
+        # forward and shared by the layers (fused.py:311-340)
+        cond_rows = torch.cat([torch.full((n,), ci, dtype=torch.long, device=ref.device)
+                               for _p, _s, n, _a, ci in r["meta"]])
+        ctx = [self.cond(cond_rows)]
+        if self.mask_dim:
+            ctx.append(self.slot_mask[cond_rows])
+        context = torch.cat(ctx, dim=1)
+        for _ in range(self.num_layers):
+            args = mp.fanout_scatter(x, r["obj"], r["flat"], nodes * ma)
+            outputs = self.central(torch.cat([context, args.view(nodes, ma * d)], dim=1))
+            out_flat = outputs.reshape(nodes * ma, d)
+            msgs = mp.fanin_reduce(out_flat, r["flat"], r["obj"], batch.num_objects, self.mode)
+            if self.mode == mp.MODE_LOGSUMEXP:
+                msgs = torch.where(torch.isfinite(msgs), msgs, torch.zeros_like(msgs))
+            x = x + self.updater(torch.cat([x, msgs], dim=1))
+        return x
+
+
+def train_step(model: nn.Module, batch: RelationalBatch, routing: dict) -> Tensor:
+    """Forward + backward of loss = mean(out^2), as the reference's benchmark
+    (scripts/benchmark_relational_models.py:287-295)."""
+
+    model.zero_grad(set_to_none=True)
+    out = model(batch, routing)
+    loss = out.square().mean()
+    loss.backward()
+    return loss.detach()
+
+
+__all__ = [
+    "CentralizedRelationalGNN",
+    "RelationalBatch",
+    "RelationalGNN",
+    "synthetic_c4",
+    "synthetic_c5",
+    "train_step",
+]

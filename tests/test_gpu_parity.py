@@ -447,3 +447,34 @@ def test_facade_backward_reuses_forward_plan(mp_env) -> None:
                 oracle.fanin_reduce_logsumexp_backward(_np(g), _np(rel.detach()), _np(flat_src), _np(dst),
                                                        _np(out.detach()), n))
         np.testing.assert_allclose(_np(cached), want, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("model", ["relational", "centralized"])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_model_training_step_matches_aten_lane(model: str, mode: int, monkeypatch) -> None:
+    """The reference's model-level callers (C4 / C5 structure, small batch):
+    the HIP op lane and the ATen lane give the same loss, output and
+    parameter gradients."""
+
+    from relmo_amd import consumers as C
+
+    _log(f"model {model} mode={mode}")
+    if model == "relational":
+        batch = C.synthetic_c4(DEV, seed=3, num_graphs=6)
+        make = lambda: C.RelationalGNN(32, 3, batch.relations, mode).to(DEV)
+    else:
+        batch = C.synthetic_c5(DEV, seed=3, num_graphs=4)
+        make = lambda: C.CentralizedRelationalGNN(16, 3, batch.relations, mode).to(DEV)
+    torch.manual_seed(0)
+    m = make()
+    routing = m.routing(batch)
+    monkeypatch.setenv("RELM_MP_ENABLE", "1")
+    loss = C.train_step(m, batch, routing)
+    grads = {k: p.grad.clone() for k, p in m.named_parameters() if p.grad is not None}
+    monkeypatch.setenv("RELM_MP_ENABLE", "0")
+    loss_ref = C.train_step(m, batch, routing)
+    assert torch.allclose(loss, loss_ref, rtol=1e-4, atol=1e-6)
+    for k, p in m.named_parameters():
+        if p.grad is None:
+            continue
+        torch.testing.assert_close(grads[k], p.grad, rtol=2e-3, atol=1e-5, msg=k)

@@ -307,3 +307,27 @@ def test_autograd_matches_aten_on_cpu(mp_env) -> None:
 
 if __name__ == "__main__":  # pragma: no cover
     sys.exit(pytest.main([__file__, "-q"]))
+
+
+def test_model_consumers_cpu_lane_matches_aten(monkeypatch) -> None:
+    """The C4 / C5 model structure on CPU tensors: the torch binding's CPU
+    lane and the ATen (python_only) lane give the same loss."""
+
+    from relmo_amd import consumers as C
+
+    for make_batch, make_model in (
+        (lambda: C.synthetic_c4("cpu", seed=1, num_graphs=3),
+         lambda b, mode: C.RelationalGNN(16, 2, b.relations, mode)),
+        (lambda: C.synthetic_c5("cpu", seed=1, num_graphs=2),
+         lambda b, mode: C.CentralizedRelationalGNN(8, 2, b.relations, mode)),
+    ):
+        batch = make_batch()
+        for mode in (0, 1):
+            torch.manual_seed(0)
+            model = make_model(batch, mode)
+            routing = model.routing(batch)
+            monkeypatch.setenv("RELM_MP_ENABLE", "1")
+            a = C.train_step(model, batch, routing)
+            monkeypatch.setenv("RELM_MP_ENABLE", "0")
+            b = C.train_step(model, batch, routing)
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-7), (mode, float(a), float(b))
