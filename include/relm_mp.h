@@ -68,7 +68,7 @@ enum relm_mp_mode { RELM_MP_MODE_SUM = 0, RELM_MP_MODE_LOGSUMEXP = 1 };
  * W[k] in [j * RELM_MP_ITEM_SIZE, (j + 1) * RELM_MP_ITEM_SIZE). */
 #define RELM_MP_HUB_THRESHOLD 64
 #define RELM_MP_CHUNK_SIZE 2048
-#define RELM_MP_ITEM_SIZE 64
+#define RELM_MP_ITEM_SIZE 32
 
 const char* relm_mp_last_error(void);
 /* "build_torch=...;build_cuda_tag=cpu;..." is produced by the torch binding;

@@ -364,9 +364,10 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
     int64_t num_items, int64_t num_keys, int64_t num_short, T* __restrict__ out, Op op) {
     constexpr int R = kThreads / G;
     constexpr int U = batch_rows<G>();
-    // an item holds at most kItemSize keys and 2 * kItemSize - 1 short messages
+    // R items hold at most R * kItemSize keys and R * kItemSize + kHubThreshold
+    // short messages (the last key may weigh up to kHubThreshold + 1)
     constexpr int kKeyCap = R * kItemSize + 2;
-    constexpr int kPosCap = R * kItemSize + kItemSize;
+    constexpr int kPosCap = R * kItemSize + kHubThreshold + 1;
     __shared__ int32_t s_off[kKeyCap];
     __shared__ int32_t s_idx[kPosCap];
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
@@ -391,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
             se = clamp64(item_short[item + 1], sb, bs1);
         }
         // The item construction bounds the workgroup's keys by R * kItemSize and
-        // its short messages by (R + 1) * kItemSize; the clamps only keep a
+        // its short messages by R * kItemSize + kHubThreshold; the clamps keep a
         // corrupt plan inside LDS.  All loads are issued before the first write.
         const int nk = static_cast<int>(bk1 - bk0 + 1 < kKeyCap ? bk1 - bk0 + 1 : kKeyCap);
         const int np = static_cast<int>(bs1 - bs0 < kPosCap ? bs1 - bs0 : kPosCap);

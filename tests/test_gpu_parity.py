@@ -13,6 +13,7 @@ from __future__ import annotations
 import hashlib
 import json
 import os
+import re
 import sys
 
 import numpy as np
@@ -20,7 +21,7 @@ import pytest
 import torch
 
 from oracle import oracle
-from tests.conftest import GOLDEN
+from tests.conftest import GOLDEN, REPO
 
 pytestmark = pytest.mark.gpu
 
@@ -191,8 +192,8 @@ def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, sk
     hub_keys = np.flatnonzero(deg > hub)
     got_hubs = bp.mem[bp.plan.hub_key - bp.mem.data_ptr():][: 4 * hub_keys.size].view(torch.int32)
     assert np.array_equal(_np(got_hubs), hub_keys)
-    # walk items: balanced by weight 1 + messages of non-hub keys, 64 units each
-    item = 64
+    # walk items: balanced by weight 1 + messages of non-hub keys, RELM_MP_ITEM_SIZE units each
+    item = int(re.search(r"#define RELM_MP_ITEM_SIZE (\d+)", (REPO / "include" / "relm_mp.h").read_text()).group(1))
     weight = 1 + np.where((deg > 0) & (deg <= hub), deg, 0)
     W = np.concatenate([[0], np.cumsum(weight)])
     assert bp.plan.num_items == W[-1] // item + 1
