@@ -166,7 +166,7 @@ CsrScratch csr_scratch(void* mem, int64_t num_keys, int64_t num_edges) {
     l.sort.vals_b = c.take<uint32_t>(n);
     const size_t hist = sort_hist_words(num_edges);
     l.sort.hist = c.take<uint32_t>(hist);
-    l.sort.scan_tmp = c.take<uint32_t>(scan_tmp_words(static_cast<int64_t>(hist)));
+    l.sort.tile_plain = c.take<uint32_t>(static_cast<size_t>(sort_tiles(num_edges)));
     const size_t hw = hub_list_words(num_keys);
     l.hub_counts = c.take<uint32_t>(hw);
     l.hub_scan_tmp = c.take<uint32_t>(64);  // row totals of the hub count scan

@@ -70,9 +70,10 @@ struct SortBuffers {
     uint32_t* vals_a;
     uint32_t* keys_b;
     uint32_t* vals_b;
-    uint32_t* hist;      // kSortBins * nblocks
-    uint32_t* scan_tmp;  // scan_tmp_words(kSortBins * nblocks)
+    uint32_t* hist;        // sort_hist_words(n): per-tile digit counts, digit totals
+    uint32_t* tile_plain;  // sort_tiles(n): first-pass tiles whose values are the edge ids
 };
+int64_t sort_tiles(int64_t n);
 size_t sort_hist_words(int64_t n);
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,

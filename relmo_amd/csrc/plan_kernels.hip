@@ -183,81 +183,131 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_tile_apply(uint32_t* __re
 
 // ---- radix sort ----------------------------------------------------------
 
-template <bool kFirst>
-__device__ __forceinline__ uint32_t load_key(const void* keys, int64_t pos, int64_t key_bound,
-                                             DevStatus* st) {
-    if constexpr (kFirst) {
-        const int64_t k = static_cast<const int64_t*>(keys)[pos];
-        if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound)) {
-            return 0u;
-        }
-        return static_cast<uint32_t>(k);
-    } else {
-        (void)key_bound;
-        (void)st;
-        return static_cast<const uint32_t*>(keys)[pos];
-    }
+// Tile digit histogram in LDS: kSubHists copies per wave (lane & 3), so that
+// lanes holding the same digit - frequent for hub keys - rarely hit the same
+// address; plain LDS atomics, no cross-lane matching.
+constexpr int kSubHists = 4;
+
+__device__ __forceinline__ void hist_clear(uint32_t* h) {
+    for (int i = static_cast<int>(threadIdx.x); i < (kSortThreads / kWave) * kSubHists * kSortBins;
+         i += kSortThreads)
+        h[i] = 0;
 }
 
-// Per-tile digit histogram, written digit-major: hist[d * nblocks + block].
-// The first pass also records the smallest edge with an out-of-range key.
-template <bool kFirst>
-__global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const void* __restrict__ keys,
-                                                                int64_t n, int shift, int bits,
-                                                                int64_t key_bound,
-                                                                uint32_t* __restrict__ hist,
-                                                                int64_t nblocks,
-                                                                DevStatus* __restrict__ st) {
-    __shared__ uint32_t h[kSortBins];
-    h[threadIdx.x] = 0;
-    __syncthreads();
+__device__ __forceinline__ void hist_add(uint32_t* h, uint32_t d) {
+    const int copy = (static_cast<int>(threadIdx.x) / kWave) * kSubHists + (lane_id() & (kSubHists - 1));
+    atomicAdd(&h[copy * kSortBins + d], 1u);
+}
+
+// Sum of the copies for digit threadIdx.x (call after a barrier).
+__device__ __forceinline__ uint32_t hist_total(const uint32_t* h) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int c = 0; c < (kSortThreads / kWave) * kSubHists; ++c) t += h[c * kSortBins + threadIdx.x];
+    return t;
+}
+
+// First pass over the caller's int64 arrays: validates every key (and
+// gathered index), narrows both to int32 for the sort passes and counts the
+// tile's digits of the first pass (hist[d * nblocks + tile]).  Gathered
+// indices equal to their edge ids (or no gathers) are common; a tile made of
+// those only is flagged in tile_plain instead of written, and the first
+// scatter generates its values.
+__global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
+    const int64_t* __restrict__ keys, const int64_t* __restrict__ gathers, int64_t n, int shift,
+    int bits, int64_t key_bound, int64_t gather_bound, uint32_t* __restrict__ keys32,
+    uint32_t* __restrict__ vals32, uint32_t* __restrict__ tile_plain, uint32_t* __restrict__ hist,
+    int64_t nblocks, DevStatus* __restrict__ st) {
+    __shared__ uint32_t h[(kSortThreads / kWave) * kSubHists * kSortBins];
+    hist_clear(h);
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
     const uint32_t dmask = (1u << bits) - 1u;
-    unsigned long long bad = kNoEdge;
-    uint32_t key[kSortItems];
+    unsigned long long bad_k = kNoEdge, bad_g = kNoEdge;
+    uint32_t key[kSortItems], val[kSortItems];
+    int mismatch = 0;
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
         key[i] = 0;
+        val[i] = 0;
         if (p < n) {
-            if constexpr (kFirst) {
-                const int64_t k = static_cast<const int64_t*>(keys)[p];
-                if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound))
-                    bad = min(bad, static_cast<unsigned long long>(p));
+            const int64_t k = keys[p];
+            if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound))
+                bad_k = min(bad_k, static_cast<unsigned long long>(p));
+            else
+                key[i] = static_cast<uint32_t>(k);
+            if (gathers != nullptr) {
+                const int64_t g = gathers[p];
+                if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound))
+                    bad_g = min(bad_g, static_cast<unsigned long long>(p));
                 else
-                    key[i] = static_cast<uint32_t>(k);
-            } else {
-                key[i] = static_cast<const uint32_t*>(keys)[p];
+                    val[i] = static_cast<uint32_t>(g);
+                mismatch |= g != p ? 1 : 0;
             }
         }
     }
-    // one LDS atomic per distinct digit of a wave: hub keys repeat a digit
-    // across many lanes, and same-address atomics serialise
+    // block-wide: does any gathered index differ from its edge id?  (also the
+    // barrier after clearing h)
+    const int any = __syncthreads_or(mismatch);
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
-        const bool active = p < n;
-        const uint32_t d = (key[i] >> shift) & dmask;
-        const unsigned long long peers = match_digit(d, bits, __ballot(active));
-        if (active && (peers & lanemask_lt()) == 0) atomicAdd(&h[d], __popcll(peers));
+        if (p < n) {
+            keys32[p] = key[i];
+            if (any) vals32[p] = val[i];
+        }
     }
-    if constexpr (kFirst) {
-        if (bad != kNoEdge) atomicMin(&st->bad_key_edge, bad);
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+        if (p < n) hist_add(h, (key[i] >> shift) & dmask);
+    }
+    if (bad_k != kNoEdge) atomicMin(&st->bad_key_edge, bad_k);
+    if (bad_g != kNoEdge) atomicMin(&st->bad_gather_edge, bad_g);
+    if (threadIdx.x == 0) {
+        tile_plain[blockIdx.x] = any ? 0u : 1u;
+        if (any) atomicOr(&st->gather_mismatch, 1ull);
     }
     __syncthreads();
-    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = h[threadIdx.x];
+    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = hist_total(h);
+}
+
+// Per-tile digit histogram of the narrowed keys, written digit-major:
+// hist[d * nblocks + tile].
+__global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* __restrict__ keys,
+                                                                int64_t n, int shift, int bits,
+                                                                uint32_t* __restrict__ hist,
+                                                                int64_t nblocks) {
+    __shared__ uint32_t h[(kSortThreads / kWave) * kSubHists * kSortBins];
+    hist_clear(h);
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+    const uint32_t dmask = (1u << bits) - 1u;
+    uint32_t key[kSortItems];
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+        key[i] = p < n ? keys[p] : 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+        if (p < n) hist_add(h, (key[i] >> shift) & dmask);
+    }
+    __syncthreads();
+    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = hist_total(h);
 }
 
 // Stable scatter of one tile.  Wave w owns tile positions [w*1024, (w+1)*1024)
 // in 16 rounds of 64, so the order (wave, round, lane) is the edge order; each
 // key's rank is counted in that order, the tile is staged in LDS in digit order
-// and written out in runs per digit.
-template <bool kFirst>
+// and written out in runs per digit.  In the first pass a tile flagged in
+// tile_plain takes the edge ids as its values.
 __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
-    const void* __restrict__ keys, const void* __restrict__ vals, int64_t n, int shift, int bits,
-    int64_t key_bound, int64_t gather_bound, const uint32_t* __restrict__ hist_scanned,
-    const uint32_t* __restrict__ digit_tot, int64_t nblocks, uint32_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out, DevStatus* __restrict__ st) {
+    const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+    const uint32_t* __restrict__ tile_plain, int64_t n, int shift, int bits,
+    const uint32_t* __restrict__ hist_scanned, const uint32_t* __restrict__ digit_tot,
+    int64_t nblocks, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
     constexpr int kWaves = kSortThreads / kWave;
     constexpr int kPerWave = kSortTile / kWaves;
     __shared__ uint32_t wcnt[kWaves][kSortBins];
@@ -280,29 +330,15 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     __syncthreads();
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
-    unsigned long long bad = kNoEdge;
-    bool mismatch = false;
+    const bool plain = tile_plain != nullptr && tile_plain[blockIdx.x] != 0u;
     const int64_t wave_base = tile_base + wave * kPerWave + lane;
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         const int64_t p = wave_base + r * kWave;
         uint32_t k = 0, v = 0;
         if (p < n) {
-            k = load_key<kFirst>(keys, p, key_bound, st);
-            if constexpr (kFirst) {
-                if (vals != nullptr) {
-                    const int64_t g = static_cast<const int64_t*>(vals)[p];
-                    if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound))
-                        bad = min(bad, static_cast<unsigned long long>(p));
-                    else
-                        v = static_cast<uint32_t>(g);
-                    mismatch = mismatch || g != p;
-                } else {
-                    v = static_cast<uint32_t>(p);
-                }
-            } else {
-                v = static_cast<const uint32_t*>(vals)[p];
-            }
+            k = keys[p];
+            v = plain ? static_cast<uint32_t>(p) : vals[p];
         }
         key[r] = k;
         val[r] = v;
@@ -318,10 +354,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
         rank[r] = before + below;
         if (active && below == 0) wcnt[wave][d] = before + __popcll(peers);
     }
-    if constexpr (kFirst) {
-        if (bad != kNoEdge) atomicMin(&st->bad_gather_edge, bad);
-        if (__ballot(mismatch) != 0 && lane == 0) atomicOr(&st->gather_mismatch, 1ull);
-    }
+
     __syncthreads();
 
     // Per digit (one thread per digit): exclusive prefix over waves, tile total.
@@ -652,6 +685,8 @@ hipError_t launch_exclusive_scan_u32(uint32_t* data, int64_t n, uint32_t* tmp, h
     return hipGetLastError();
 }
 
+int64_t sort_tiles(int64_t n) { return std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile); }
+
 size_t sort_hist_words(int64_t n) {
     const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
     // per-tile digit counts, then the digit totals
@@ -667,8 +702,11 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
     const int passes = std::max(1, (bits + 7) / 8);
     const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
     const int64_t hist_n = static_cast<int64_t>(kSortBins) * nblocks;
-    const void* in_k = keys;
-    const void* in_v = gathers;
+    uint32_t* digit_tot = buf.hist + hist_n;
+    // the narrowed input goes to the b buffers; pass p writes a, b, a, ... and
+    // the last pass the plan arrays
+    const uint32_t* in_k = buf.keys_b;
+    const uint32_t* in_v = buf.vals_b;
     int shift = 0;
     for (int p = 0; p < passes; ++p) {
         const int width = bits / passes + (p < bits % passes ? 1 : 0);
@@ -676,32 +714,24 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         uint32_t* out_k = last ? keys_out : (p % 2 == 0 ? buf.keys_a : buf.keys_b);
         uint32_t* out_v = last ? vals_out : (p % 2 == 0 ? buf.vals_a : buf.vals_b);
         if (p == 0) {
-            hipLaunchKernelGGL(k_radix_upsweep<true>, dim3(static_cast<unsigned>(nblocks)),
-                               dim3(kSortThreads), 0, s, in_k, n, shift, width, key_bound,
-                               buf.hist, nblocks, st);
+            hipLaunchKernelGGL(k_radix_narrow, dim3(static_cast<unsigned>(nblocks)), dim3(kSortThreads),
+                               0, s, keys, gathers, n, shift, width, key_bound, gather_bound,
+                               buf.keys_b, buf.vals_b, buf.tile_plain, buf.hist, nblocks, st);
         } else {
-            hipLaunchKernelGGL(k_radix_upsweep<false>, dim3(static_cast<unsigned>(nblocks)),
-                               dim3(kSortThreads), 0, s, in_k, n, shift, width, key_bound,
-                               buf.hist, nblocks, st);
+            hipLaunchKernelGGL(k_radix_upsweep, dim3(static_cast<unsigned>(nblocks)), dim3(kSortThreads),
+                               0, s, in_k, n, shift, width, buf.hist, nblocks);
         }
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
-        uint32_t* digit_tot = buf.hist + hist_n;
         hipLaunchKernelGGL(k_scan_rows, dim3(kSortBins), dim3(kScanThreads), 0, s, buf.hist, nblocks,
                            digit_tot);
         err = hipGetLastError();
         if (err != hipSuccess) return err;
-        if (p == 0) {
-            hipLaunchKernelGGL(k_radix_downsweep<true>, dim3(static_cast<unsigned>(nblocks)),
-                               dim3(kSortThreads), 0, s, in_k, in_v, n, shift, width, key_bound,
-                               gather_bound, buf.hist, static_cast<const uint32_t*>(digit_tot),
-                               nblocks, out_k, out_v, st);
-        } else {
-            hipLaunchKernelGGL(k_radix_downsweep<false>, dim3(static_cast<unsigned>(nblocks)),
-                               dim3(kSortThreads), 0, s, in_k, in_v, n, shift, width, key_bound,
-                               gather_bound, buf.hist, static_cast<const uint32_t*>(digit_tot),
-                               nblocks, out_k, out_v, st);
-        }
+        hipLaunchKernelGGL(k_radix_downsweep, dim3(static_cast<unsigned>(nblocks)), dim3(kSortThreads),
+                           0, s, in_k, in_v,
+                           p == 0 ? static_cast<const uint32_t*>(buf.tile_plain) : nullptr, n, shift,
+                           width, static_cast<const uint32_t*>(buf.hist),
+                           static_cast<const uint32_t*>(digit_tot), nblocks, out_k, out_v);
         err = hipGetLastError();
         if (err != hipSuccess) return err;
         in_k = out_k;
