@@ -149,10 +149,7 @@ CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
 
 struct CsrScratch {
     SortBuffers sort;
-    uint32_t* hub_counts;
-    uint32_t* hub_scan_tmp;
-    uint32_t* weights;
-    uint32_t* weight_scan_tmp;
+    uint32_t* key_index;
     size_t bytes;
 };
 
@@ -167,11 +164,7 @@ CsrScratch csr_scratch(void* mem, int64_t num_keys, int64_t num_edges) {
     const size_t hist = sort_hist_words(num_edges);
     l.sort.hist = c.take<uint32_t>(hist);
     l.sort.tile_plain = c.take<uint32_t>(static_cast<size_t>(sort_tiles(num_edges)));
-    const size_t hw = hub_list_words(num_keys);
-    l.hub_counts = c.take<uint32_t>(hw);
-    l.hub_scan_tmp = c.take<uint32_t>(64);  // row totals of the hub count scan
-    l.weights = c.take<uint32_t>(static_cast<size_t>(num_keys) + 1);
-    l.weight_scan_tmp = c.take<uint32_t>(scan_tmp_words(num_keys + 1));
+    l.key_index = c.take<uint32_t>(key_index_words(num_keys));
     l.bytes = c.used();
     return l;
 }
@@ -255,13 +248,11 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_HIP(launch_offsets_from_sorted(reinterpret_cast<const uint32_t*>(l.keys_sorted), num_edges,
                                         key_bound, l.offsets, s),
              "relm_mp offsets kernel");
-    RELM_HIP(launch_hub_list(l.offsets, key_bound, l.hub_key, l.hub_chunk_base, l.multi_hubs,
-                             max_hubs(num_edges), sc.hub_counts, sc.hub_scan_tmp, l.status, s),
-             "relm_mp hub list kernels");
-    RELM_HIP(launch_item_first(l.offsets, l.gather_sorted, key_bound, sc.weights,
-                               sc.weight_scan_tmp, l.item_first, l.item_short, l.num_items,
-                               l.short_off, l.short_gather, l.status, s),
-             "relm_mp item kernels");
+    RELM_HIP(launch_key_index(l.offsets, l.gather_sorted, key_bound, sc.key_index, l.hub_key,
+                              l.hub_chunk_base, l.multi_hubs, l.chunk_hub, max_hubs(num_edges),
+                              max_chunks(num_edges), l.item_first, l.item_short, l.num_items,
+                              l.short_off, l.short_gather, l.status, s),
+             "relm_mp key index kernels");
     DevStatus host{};
     RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
                                gather_name, gather_checked_first, s));
@@ -276,9 +267,6 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges) ||
         plan->num_multi_hubs > plan->num_hubs)
         return set_error(RELM_MP_ERR_HIP, "relm_mp: hub list overflow");
-    RELM_HIP(launch_chunk_map(l.offsets, l.hub_key, l.hub_chunk_base, plan->num_hubs,
-                              plan->num_chunks, l.chunk_hub, s),
-             "relm_mp chunk map kernel");
     return RELM_MP_OK;
 }
 

@@ -58,9 +58,6 @@ hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_
                             int64_t gather_bound, int64_t n, int32_t* inv, DevStatus* st,
                             hipStream_t s);
 
-// Exclusive scan of n uint32 values in place.  `tmp` holds scan_tmp_words(n) words.
-size_t scan_tmp_words(int64_t n);
-hipError_t launch_exclusive_scan_u32(uint32_t* data, int64_t n, uint32_t* tmp, hipStream_t s);
 
 // Stable LSD radix sort of (key, value) by key.  The first pass reads the
 // caller's int64 keys / gathers, validates them against the bounds (bad
@@ -81,29 +78,22 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
 
 hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
                                       int32_t* offsets, hipStream_t s);
-// Hub list (deterministic: hubs in key order) and walk items.  `counts` holds
-// hub_list_words(num_keys) words of scratch, `scan_tmp` scan_tmp_words() of
-// the same length.
-size_t hub_list_words(int64_t num_keys);
-hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
-                           int32_t* hub_chunk_base, int32_t* multi_hubs, int64_t hub_capacity,
-                           uint32_t* counts, uint32_t* scan_tmp, DevStatus* st, hipStream_t s);
-// Walk items balanced by key weight (1 + messages of non-hub keys), and the
-// short-segment index: short_off[k] = messages of non-hub keys before key k
-// (num_keys + 1 entries), short_gather = gather_sorted with the hub segments
-// left out, item_short[j] = short_off[item_first[j]].
-// `weights` and `scan_tmp` are scratch of num_keys + 1 and scan_tmp_words(num_keys + 1)
-// words; item_first and item_short have item_capacity + 1 entries
+// Per-key index of a CSR plan (deterministic, hubs in key order): hub list,
+// chunk ranges and chunk -> hub map, walk items (balanced by weight: 1 plus the
+// messages of a non-hub key), the short-segment index (short_off[k] = messages
+// of non-hub keys before key k, num_keys + 1 entries; short_gather =
+// gather_sorted without the hub segments; item_short[j] =
+// short_off[item_first[j]]).  `scratch` holds key_index_words(num_keys) words;
+// item_first and item_short have item_capacity + 1 entries
 // (item_capacity_for(num_keys)).
+size_t key_index_words(int64_t num_keys);
 int64_t item_capacity_for(int64_t num_keys);
-hipError_t launch_item_first(const int32_t* offsets, const int32_t* gather_sorted,
-                             int64_t num_keys, uint32_t* weights, uint32_t* scan_tmp,
-                             int32_t* item_first, int32_t* item_short, int64_t item_capacity,
-                             int32_t* short_off, int32_t* short_gather, DevStatus* st,
-                             hipStream_t s);
-hipError_t launch_chunk_map(const int32_t* offsets, const int32_t* hub_key,
-                            const int32_t* hub_chunk_base, int64_t num_hubs, int64_t num_chunks,
-                            int32_t* chunk_hub, hipStream_t s);
+hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted, int64_t num_keys,
+                            uint32_t* scratch, int32_t* hub_key, int32_t* hub_chunk_base,
+                            int32_t* multi_hubs, int32_t* chunk_hub, int64_t hub_capacity,
+                            int64_t chunk_capacity, int32_t* item_first, int32_t* item_short,
+                            int64_t item_capacity, int32_t* short_off, int32_t* short_gather,
+                            DevStatus* st, hipStream_t s);
 
 // ---- compute kernels (reduce_kernels.hip) --------------------------------
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,

@@ -82,23 +82,6 @@ __global__ __launch_bounds__(kThreads) void k_inv_build(const int64_t* __restric
 
 // ---- scan ----------------------------------------------------------------
 
-__global__ __launch_bounds__(kScanThreads) void k_scan_tile_sums(const uint32_t* __restrict__ in,
-                                                                 int64_t n,
-                                                                 uint32_t* __restrict__ sums) {
-    __shared__ uint32_t lds[kScanThreads / kWave];
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
-    uint32_t s = 0;
-#pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
-        if (p < n) s += in[p];
-    }
-    uint32_t total;
-    block_inclusive_scan<kScanThreads>(s, lds, total);
-    if (threadIdx.x == 0) sums[blockIdx.x] = total;
-}
-
-// Exclusive scan of one tile per block, in place, with a per-tile carry.
 // Exclusive scan of every row of a [gridDim.x, len] array in place (one
 // workgroup per row, kScanTile values per step with a running carry);
 // tot[row] receives the row's sum.
@@ -144,41 +127,6 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict
         __syncthreads();  // tile is rewritten by the next step
     }
     if (threadIdx.x == 0) tot[blockIdx.x] = carry;
-}
-
-__global__ __launch_bounds__(kScanThreads) void k_scan_tile_apply(uint32_t* __restrict__ data,
-                                                                  int64_t n,
-                                                                  const uint32_t* __restrict__ carry) {
-    __shared__ uint32_t tile[kScanTile];
-    __shared__ uint32_t lds[kScanThreads / kWave];
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
-#pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
-        tile[i * kScanThreads + threadIdx.x] = p < n ? data[p] : 0u;
-    }
-    __syncthreads();
-    uint32_t v[kScanItems];
-    uint32_t s = 0;
-#pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
-        v[i] = tile[threadIdx.x * kScanItems + i];
-        s += v[i];
-    }
-    uint32_t total;
-    const uint32_t incl = block_inclusive_scan<kScanThreads>(s, lds, total);
-    uint32_t run = incl - s + (carry != nullptr ? carry[blockIdx.x] : 0u);
-#pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
-        tile[threadIdx.x * kScanItems + i] = run;
-        run += v[i];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
-        if (p < n) data[p] = tile[i * kScanThreads + threadIdx.x];
-    }
 }
 
 // ---- radix sort ----------------------------------------------------------
@@ -432,40 +380,53 @@ __global__ __launch_bounds__(kThreads) void k_offsets_from_sorted(const uint32_t
     }
 }
 
-// Hub list in two passes over the segment sizes, without global atomics:
-// k_hub_count writes per-block counts (hubs, chunks, big hubs) and the block's
-// longest segment; the counts are scanned; k_hub_write gives every hub its
-// slot (hubs in key order) and chunk range.
-struct HubFlags {
+// Per-key index of a CSR plan in two passes over the keys k = 0..num_keys,
+// without global atomics beyond one maximum per workgroup:
+//  * k_key_stats: per workgroup of kThreads keys the number of hubs (segments
+//    longer than kHubThreshold), their chunks, the hubs of more than one chunk
+//    and the hub messages;
+//  * these four rows are scanned (k_scan_rows);
+//  * k_key_write: every hub gets its slot in key order, its chunk range and the
+//    chunk -> hub map; with S[k] = short messages before key k (= offsets[k]
+//    minus the hub messages before k) and the walk weight W[k] = k + S[k], the
+//    walk items, short_off = S and the short-segment gather copy.
+struct KeyFlags {
     uint32_t hub;
     uint32_t chunks;
     uint32_t multi;
+    uint32_t hub_edges;
     int64_t deg;
 };
 
-__device__ __forceinline__ HubFlags hub_flags(const int32_t* __restrict__ offsets, int64_t k,
+__device__ __forceinline__ KeyFlags key_flags(const int32_t* __restrict__ offsets, int64_t k,
                                               int64_t num_keys) {
-    HubFlags f{0u, 0u, 0u, 0};
+    KeyFlags f{0u, 0u, 0u, 0u, 0};
     if (k < num_keys) f.deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
     if (f.deg > kHubThreshold) {
         f.hub = 1u;
         f.chunks = static_cast<uint32_t>((f.deg + kChunkSize - 1) / kChunkSize);
         f.multi = f.chunks > 1u ? 1u : 0u;
+        f.hub_edges = static_cast<uint32_t>(f.deg);
     }
     return f;
 }
 
-__global__ __launch_bounds__(kThreads) void k_hub_count(const int32_t* __restrict__ offsets,
+constexpr int kKeyRows = 4;  // scanned rows: hubs, chunks, multi-chunk hubs, hub messages;
+                             // a fifth row holds each workgroup's longest segment
+
+__global__ __launch_bounds__(kThreads) void k_key_stats(const int32_t* __restrict__ offsets,
                                                         int64_t num_keys, int64_t nblk,
-                                                        uint32_t* __restrict__ counts) {
+                                                        uint32_t* __restrict__ counts,
+                                                        DevStatus* __restrict__ st) {
     __shared__ uint32_t lds[kThreads / kWave];
-    __shared__ uint32_t wmax[kThreads / kWave];
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    const HubFlags f = hub_flags(offsets, k, num_keys);
-    uint32_t th, tc, tb;
+    const KeyFlags f = key_flags(offsets, k, num_keys);
+    uint32_t th, tc, tm, te;
     block_inclusive_scan<kThreads>(f.hub, lds, th);
     block_inclusive_scan<kThreads>(f.chunks, lds, tc);
-    block_inclusive_scan<kThreads>(f.multi, lds, tb);
+    block_inclusive_scan<kThreads>(f.multi, lds, tm);
+    block_inclusive_scan<kThreads>(f.hub_edges, lds, te);
+    __shared__ uint32_t wmax[kThreads / kWave];
     uint32_t m = f.deg > 0 ? static_cast<uint32_t>(f.deg) : 0u;
 #pragma unroll
     for (int o = kWave / 2; o > 0; o >>= 1) {
@@ -480,160 +441,117 @@ __global__ __launch_bounds__(kThreads) void k_hub_count(const int32_t* __restric
         const int64_t stride = nblk + 1;
         counts[blockIdx.x] = th;
         counts[stride + blockIdx.x] = tc;
-        counts[2 * stride + blockIdx.x] = tb;
-        counts[3 * stride + blockIdx.x] = mm;
+        counts[2 * stride + blockIdx.x] = tm;
+        counts[3 * stride + blockIdx.x] = te;
+        counts[4 * stride + blockIdx.x] = mm;
         if (blockIdx.x == 0) {
-            counts[nblk] = 0;
-            counts[stride + nblk] = 0;
-            counts[2 * stride + nblk] = 0;
+            for (int r = 0; r < kKeyRows; ++r) counts[r * stride + nblk] = 0;
         }
     }
+    (void)st;
 }
 
-__global__ __launch_bounds__(kThreads) void k_hub_write(const int32_t* __restrict__ offsets,
-                                                        int64_t num_keys, int64_t nblk,
-                                                        const uint32_t* __restrict__ counts,
-                                                        int32_t* __restrict__ hub_key,
-                                                        int32_t* __restrict__ hub_chunk_base,
-                                                        int32_t* __restrict__ multi_hubs,
-                                                        int64_t hub_capacity) {
+__global__ __launch_bounds__(kThreads) void k_key_write(
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_keys,
+    int64_t nblk, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ totals,
+    int32_t* __restrict__ hub_key, int32_t* __restrict__ hub_chunk_base,
+    int32_t* __restrict__ multi_hubs, int32_t* __restrict__ chunk_hub, int64_t hub_capacity,
+    int64_t chunk_capacity, int32_t* __restrict__ item_first, int32_t* __restrict__ item_short,
+    int64_t item_capacity, int32_t* __restrict__ short_off, int32_t* __restrict__ short_gather,
+    DevStatus* __restrict__ st) {
     __shared__ uint32_t lds[kThreads / kWave];
+    __shared__ int32_t blk_slot[kThreads];
+    __shared__ int64_t blk_cbase[kThreads];
+    __shared__ uint32_t blk_chunks[kThreads];
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    const HubFlags f = hub_flags(offsets, k, num_keys);
-    uint32_t th, tc, tb;
+    const KeyFlags f = key_flags(offsets, k, num_keys);
+    uint32_t th, tc, tm, te;
     const uint32_t ih = block_inclusive_scan<kThreads>(f.hub, lds, th);
     const uint32_t ic = block_inclusive_scan<kThreads>(f.chunks, lds, tc);
-    const uint32_t ib = block_inclusive_scan<kThreads>(f.multi, lds, tb);
-    if (!f.hub) return;
+    const uint32_t im = block_inclusive_scan<kThreads>(f.multi, lds, tm);
+    const uint32_t ie = block_inclusive_scan<kThreads>(f.hub_edges, lds, te);
     const int64_t stride = nblk + 1;
-    const int64_t slot = static_cast<int64_t>(counts[blockIdx.x]) + ih - 1;
-    if (slot < 0 || slot >= hub_capacity) return;
-    hub_key[slot] = static_cast<int32_t>(k);
-    hub_chunk_base[slot] = static_cast<int32_t>(counts[stride + blockIdx.x] + ic - f.chunks);
-    if (f.multi) {
-        const int64_t b = static_cast<int64_t>(counts[2 * stride + blockIdx.x]) + ib - 1;
-        if (b >= 0 && b < hub_capacity) multi_hubs[b] = static_cast<int32_t>(slot);
-    }
-}
-
-// Totals of the scanned counts and the longest segment into the status.
-__global__ __launch_bounds__(kThreads) void k_hub_totals(const uint32_t* __restrict__ counts,
-                                                         int64_t nblk, DevStatus* __restrict__ st) {
-    const int64_t stride = nblk + 1;
-    uint32_t m = 0;
-    for (int64_t b = threadIdx.x; b < nblk; b += kThreads) {
-        const uint32_t v = counts[3 * stride + b];
-        m = v > m ? v : m;
-    }
+    if (blockIdx.x == 0) {
+        // totals and the longest segment into the status
+        uint32_t m = 0;
+        for (int64_t b = threadIdx.x; b < nblk; b += kThreads) {
+            const uint32_t v = counts[4 * stride + b];
+            m = v > m ? v : m;
+        }
 #pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-        const uint32_t other = __shfl_xor(m, o, kWave);
-        m = other > m ? other : m;
+        for (int o = kWave / 2; o > 0; o >>= 1) {
+            const uint32_t other = __shfl_xor(m, o, kWave);
+            m = other > m ? other : m;
+        }
+        if (lane_id() == 0) atomicMax(&st->max_degree, static_cast<unsigned long long>(m));
+        if (threadIdx.x == 0) {
+            st->num_hubs = totals[0];
+            st->num_chunks = totals[1];
+            st->num_multi_hubs = totals[2];
+        }
     }
-    __shared__ uint32_t wmax[kThreads / kWave];
-    if (lane_id() == 0) wmax[threadIdx.x / kWave] = m;
+    // hub slot, chunk range; the workgroup fills the chunk -> hub map of its
+    // hubs together (a hub can have hundreds of chunks)
+    if (f.hub) {
+        const int64_t slot = static_cast<int64_t>(counts[blockIdx.x]) + ih - 1;
+        const int64_t cbase = static_cast<int64_t>(counts[stride + blockIdx.x]) + ic - f.chunks;
+        blk_slot[ih - 1] = static_cast<int32_t>(slot);
+        blk_cbase[ih - 1] = cbase;
+        blk_chunks[ih - 1] = f.chunks;
+        if (slot >= 0 && slot < hub_capacity) {
+            hub_key[slot] = static_cast<int32_t>(k);
+            hub_chunk_base[slot] = static_cast<int32_t>(cbase);
+            if (f.multi) {
+                const int64_t mslot = static_cast<int64_t>(counts[2 * stride + blockIdx.x]) + im - 1;
+                if (mslot >= 0 && mslot < hub_capacity) multi_hubs[mslot] = static_cast<int32_t>(slot);
+            }
+        }
+    }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t mm = 0;
-        for (int w = 0; w < kThreads / kWave; ++w) mm = wmax[w] > mm ? wmax[w] : mm;
-        st->max_degree = mm;
-        st->num_hubs = counts[nblk];
-        st->num_chunks = counts[stride + nblk];
-        st->num_multi_hubs = counts[2 * stride + nblk];
-    }
-}
-
-// Walk items are balanced by a per-key weight: 1 (the key's output row) plus
-// its messages for non-hub keys (hub messages are reduced elsewhere).  With
-// W the exclusive scan of the weights (W[num_keys] = total),
-// item_first[j] = first key k with W[k] >= j * kItemSize, and
-// item_first[num_items] = num_keys.
-__global__ __launch_bounds__(kThreads) void k_item_weights(const int32_t* __restrict__ offsets,
-                                                           int64_t num_keys,
-                                                           uint32_t* __restrict__ w) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k <= num_keys;
-         k += stride) {
-        uint32_t v = 0;
-        if (k < num_keys) {
-            const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
-            v = 1u + (deg > 0 && deg <= kHubThreshold ? static_cast<uint32_t>(deg) : 0u);
+    for (uint32_t h = 0; h < th; ++h) {
+        const int64_t slot = blk_slot[h];
+        if (slot < 0 || slot >= hub_capacity) continue;
+        for (int64_t c = threadIdx.x; c < blk_chunks[h]; c += kThreads) {
+            const int64_t at = blk_cbase[h] + c;
+            if (at >= 0 && at < chunk_capacity) chunk_hub[at] = static_cast<int32_t>(slot);
         }
-        w[k] = v;
     }
-}
-
-__global__ __launch_bounds__(kThreads) void k_item_first(const uint32_t* __restrict__ W,
-                                                         int64_t num_keys,
-                                                         int32_t* __restrict__ item_first,
-                                                         int32_t* __restrict__ item_short,
-                                                         int64_t num_items,
-                                                         DevStatus* __restrict__ st) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k <= num_keys;
-         k += stride) {
-        const int64_t o = W[k];
-        const int64_t op = k == 0 ? -1 : static_cast<int64_t>(W[k - 1]);
-        // items j with op < j * kItemSize <= o (weights are at most kHubThreshold + 1,
-        // so a key covers at most two items)
-        const int64_t j0 = op < 0 ? 0 : op / kItemSize + 1;
-        // the key past the end also closes the last used item (j = total / kItemSize + 1)
-        int64_t j1 = k == num_keys ? o / kItemSize + 1 : o / kItemSize;
-        if (j1 > num_items) j1 = num_items;
-        // W[k] counts one per key before k plus their short messages
-        const int32_t so = static_cast<int32_t>(o - k);
-        for (int64_t j = j0; j <= j1; ++j) {
-            item_first[j] = static_cast<int32_t>(k);
-            item_short[j] = so;
-        }
-        if (k == num_keys) st->total_weight = static_cast<unsigned long long>(o);
+    if (k > num_keys) return;
+    // S[k]: short messages before k; W[k] = k + S[k]
+    const int64_t hub_before = static_cast<int64_t>(counts[3 * stride + blockIdx.x]) + ie - f.hub_edges;
+    const int64_t S = static_cast<int64_t>(offsets[k]) - hub_before;
+    const int64_t W = k + S;
+    int64_t Wprev = -1;
+    if (k > 0) {
+        const int64_t dprev = static_cast<int64_t>(offsets[k]) - offsets[k - 1];
+        Wprev = W - 1 - (dprev > 0 && dprev <= kHubThreshold ? dprev : 0);
     }
-}
-
-// short_off[k] = W[k] - k; the gathered rows of each non-hub segment are
-// copied to short_gather[short_off[k] ...], so the short segments lie back to
-// back in key order.
-__global__ __launch_bounds__(kThreads) void k_short_index(const int32_t* __restrict__ offsets,
-                                                          const int32_t* __restrict__ gs,
-                                                          const uint32_t* __restrict__ W,
-                                                          int64_t num_keys,
-                                                          int32_t* __restrict__ short_off,
-                                                          int32_t* __restrict__ short_gather) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; k <= num_keys;
-         k += stride) {
-        const int64_t so = static_cast<int64_t>(W[k]) - k;
-        short_off[k] = static_cast<int32_t>(so);
-        if (k == num_keys) continue;
+    short_off[k] = static_cast<int32_t>(S);
+    // items j with Wprev < j * kItemSize <= W; the key past the end also closes
+    // the last used item (j = W / kItemSize + 1)
+    const int64_t j0 = Wprev < 0 ? 0 : Wprev / kItemSize + 1;
+    int64_t j1 = k == num_keys ? W / kItemSize + 1 : W / kItemSize;
+    if (j1 > item_capacity) j1 = item_capacity;
+    for (int64_t j = j0; j <= j1; ++j) {
+        item_first[j] = static_cast<int32_t>(k);
+        item_short[j] = static_cast<int32_t>(S);
+    }
+    if (k == num_keys) {
+        st->total_weight = static_cast<unsigned long long>(W);
+        return;
+    }
+    // the short segment's gathered rows, back to back in key order
+    if (f.deg > 0 && f.deg <= kHubThreshold) {
         const int64_t b = offsets[k];
-        const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - b;
-        if (deg <= 0 || deg > kHubThreshold) continue;
         int64_t j = 0;
-        for (; j + 4 <= deg; j += 4) {
+        for (; j + 4 <= f.deg; j += 4) {
             const int32_t a0 = gs[b + j], a1 = gs[b + j + 1], a2 = gs[b + j + 2], a3 = gs[b + j + 3];
-            short_gather[so + j] = a0;
-            short_gather[so + j + 1] = a1;
-            short_gather[so + j + 2] = a2;
-            short_gather[so + j + 3] = a3;
+            short_gather[S + j] = a0;
+            short_gather[S + j + 1] = a1;
+            short_gather[S + j + 2] = a2;
+            short_gather[S + j + 3] = a3;
         }
-        for (; j < deg; ++j) short_gather[so + j] = gs[b + j];
-    }
-}
-
-// chunk_hub[hub_chunk_base[h] + j] = h for the chunks of hub h (one block per hub).
-__global__ __launch_bounds__(kThreads) void k_chunk_map(const int32_t* __restrict__ offsets,
-                                                        const int32_t* __restrict__ hub_key,
-                                                        const int32_t* __restrict__ hub_chunk_base,
-                                                        int64_t num_hubs, int64_t num_chunks,
-                                                        int32_t* __restrict__ chunk_hub) {
-    for (int64_t h = blockIdx.x; h < num_hubs; h += gridDim.x) {
-        const int64_t k = hub_key[h];
-        const int64_t deg = static_cast<int64_t>(offsets[k + 1]) - offsets[k];
-        const int64_t nch = (deg + kChunkSize - 1) / kChunkSize;
-        const int64_t base = hub_chunk_base[h];
-        for (int64_t j = threadIdx.x; j < nch; j += blockDim.x) {
-            if (base + j >= 0 && base + j < num_chunks) chunk_hub[base + j] = static_cast<int32_t>(h);
-        }
+        for (; j < f.deg; ++j) short_gather[S + j] = gs[b + j];
     }
 }
 
@@ -657,31 +575,6 @@ hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_inv_build, dim3(grid_1d(n, kThreads * 4)), dim3(kThreads), 0, s, keys,
                        key_bound, gathers, gather_bound, n, inv, st);
-    return hipGetLastError();
-}
-
-size_t scan_tmp_words(int64_t n) {
-    const int64_t tiles = (n + kScanTile - 1) / kScanTile;
-    if (tiles <= 1) return 0;
-    return align_up(static_cast<size_t>(tiles), 64) + scan_tmp_words(tiles);
-}
-
-hipError_t launch_exclusive_scan_u32(uint32_t* data, int64_t n, uint32_t* tmp, hipStream_t s) {
-    if (n <= 0) return hipSuccess;
-    const int64_t tiles = (n + kScanTile - 1) / kScanTile;
-    if (tiles == 1) {
-        hipLaunchKernelGGL(k_scan_tile_apply, dim3(1), dim3(kScanThreads), 0, s, data, n,
-                           static_cast<const uint32_t*>(nullptr));
-        return hipGetLastError();
-    }
-    hipLaunchKernelGGL(k_scan_tile_sums, dim3(static_cast<unsigned>(tiles)), dim3(kScanThreads), 0,
-                       s, data, n, tmp);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    err = launch_exclusive_scan_u32(tmp, tiles, tmp + align_up(static_cast<size_t>(tiles), 64), s);
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_scan_tile_apply, dim3(static_cast<unsigned>(tiles)), dim3(kScanThreads), 0,
-                       s, data, n, static_cast<const uint32_t*>(tmp));
     return hipGetLastError();
 }
 
@@ -748,67 +641,37 @@ hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, in
     return hipGetLastError();
 }
 
-size_t hub_list_words(int64_t num_keys) {
-    const int64_t nblk = std::max<int64_t>(1, (num_keys + kThreads - 1) / kThreads);
-    return static_cast<size_t>(4 * (nblk + 1));
-}
-
-hipError_t launch_hub_list(const int32_t* offsets, int64_t num_keys, int32_t* hub_key,
-                           int32_t* hub_chunk_base, int32_t* multi_hubs, int64_t hub_capacity,
-                           uint32_t* counts, uint32_t* scan_tmp, DevStatus* st, hipStream_t s) {
-    if (num_keys <= 0) return hipSuccess;
-    const int64_t nblk = (num_keys + kThreads - 1) / kThreads;
-    hipLaunchKernelGGL(k_hub_count, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
-                       num_keys, nblk, counts);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    // the three count arrays are consecutive rows of nblk + 1 values
-    hipLaunchKernelGGL(k_scan_rows, dim3(3), dim3(kScanThreads), 0, s, counts, nblk + 1, scan_tmp);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_hub_write, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
-                       num_keys, nblk, static_cast<const uint32_t*>(counts), hub_key, hub_chunk_base,
-                       multi_hubs, hub_capacity);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_hub_totals, dim3(1), dim3(kThreads), 0, s, static_cast<const uint32_t*>(counts),
-                       nblk, st);
-    return hipGetLastError();
+size_t key_index_words(int64_t num_keys) {
+    const int64_t nblk = (num_keys + 1 + kThreads - 1) / kThreads;
+    return static_cast<size_t>((kKeyRows + 1) * (nblk + 1) + 64);
 }
 
 int64_t item_capacity_for(int64_t num_keys) {
     return num_keys * (kHubThreshold + 1) / kItemSize + 1;
 }
 
-hipError_t launch_item_first(const int32_t* offsets, const int32_t* gather_sorted,
-                             int64_t num_keys, uint32_t* weights, uint32_t* scan_tmp,
-                             int32_t* item_first, int32_t* item_short, int64_t item_capacity,
-                             int32_t* short_off, int32_t* short_gather, DevStatus* st,
-                             hipStream_t s) {
-    hipLaunchKernelGGL(k_item_weights, dim3(grid_1d(num_keys + 1, kThreads * 4)), dim3(kThreads), 0,
-                       s, offsets, num_keys, weights);
+hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted, int64_t num_keys,
+                            uint32_t* scratch, int32_t* hub_key, int32_t* hub_chunk_base,
+                            int32_t* multi_hubs, int32_t* chunk_hub, int64_t hub_capacity,
+                            int64_t chunk_capacity, int32_t* item_first, int32_t* item_short,
+                            int64_t item_capacity, int32_t* short_off, int32_t* short_gather,
+                            DevStatus* st, hipStream_t s) {
+    const int64_t nblk = (num_keys + 1 + kThreads - 1) / kThreads;
+    uint32_t* counts = scratch;
+    uint32_t* totals = scratch + (kKeyRows + 1) * (nblk + 1);
+    hipLaunchKernelGGL(k_key_stats, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
+                       num_keys, nblk, counts, st);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    err = launch_exclusive_scan_u32(weights, num_keys + 1, scan_tmp, s);
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_item_first, dim3(grid_1d(num_keys + 1, kThreads)), dim3(kThreads), 0, s,
-                       static_cast<const uint32_t*>(weights), num_keys, item_first, item_short,
-                       item_capacity, st);
+    hipLaunchKernelGGL(k_scan_rows, dim3(kKeyRows), dim3(kScanThreads), 0, s, counts, nblk + 1,
+                       totals);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_short_index, dim3(grid_1d(num_keys + 1, kThreads)), dim3(kThreads), 0, s,
-                       offsets, gather_sorted, static_cast<const uint32_t*>(weights), num_keys,
-                       short_off, short_gather);
-    return hipGetLastError();
-}
-
-hipError_t launch_chunk_map(const int32_t* offsets, const int32_t* hub_key,
-                            const int32_t* hub_chunk_base, int64_t num_hubs, int64_t num_chunks,
-                            int32_t* chunk_hub, hipStream_t s) {
-    if (num_hubs <= 0) return hipSuccess;
-    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(num_hubs, 1 << 16));
-    hipLaunchKernelGGL(k_chunk_map, dim3(blocks), dim3(kThreads), 0, s, offsets, hub_key,
-                       hub_chunk_base, num_hubs, num_chunks, chunk_hub);
+    hipLaunchKernelGGL(k_key_write, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
+                       gather_sorted, num_keys, nblk, static_cast<const uint32_t*>(counts),
+                       static_cast<const uint32_t*>(totals), hub_key, hub_chunk_base, multi_hubs,
+                       chunk_hub, hub_capacity, chunk_capacity, item_first, item_short,
+                       item_capacity, short_off, short_gather, st);
     return hipGetLastError();
 }
 
