@@ -15,17 +15,27 @@ __device__ __forceinline__ unsigned long long lanemask_lt() {
     return (1ull << lane_id()) - 1ull;
 }
 
-// Lanes of the wave whose `digit` (of `bits` bits) equals this lane's, among
-// the lanes in `active`.  One ballot per bit.
-__device__ __forceinline__ unsigned long long match_digit(uint32_t digit, int bits,
+// Lanes of the wave whose `digit` (of BITS bits) equals this lane's, among
+// the lanes in `active`.  One ballot per bit; each bit keeps the lanes whose
+// ballot bit agrees with this lane's digit bit, peers &= ~(ballot ^ bitmask):
+// a sign-extending bit extract, a compare and one v_bitop3 per 32-bit half.
+// v_bitop3's table is indexed by (src0, src1, src2) bits; with src0 = 0xF0,
+// src1 = 0xCC, src2 = 0xAA, src0 & ~(src1 ^ src2) = 0x90.
+template <int BITS>
+__device__ __forceinline__ unsigned long long match_digit(uint32_t digit,
                                                           unsigned long long active) {
-    unsigned long long peers = active;
-    for (int b = 0; b < bits; ++b) {
-        const bool set = (digit >> b) & 1u;
-        const unsigned long long m = __ballot(set);
-        peers &= set ? m : ~m;
+    uint32_t lo = static_cast<uint32_t>(active);
+    uint32_t hi = static_cast<uint32_t>(active >> 32);
+#pragma unroll
+    for (int b = 0; b < BITS; ++b) {
+        // all ones if bit b of the digit is set, else zero
+        const int32_t sm = __builtin_amdgcn_sbfe(static_cast<int32_t>(digit), b, 1);
+        const unsigned long long m = __ballot(sm < 0);
+        lo = __builtin_amdgcn_bitop3_b32(lo, static_cast<uint32_t>(m), static_cast<uint32_t>(sm), 0x90);
+        hi = __builtin_amdgcn_bitop3_b32(hi, static_cast<uint32_t>(m >> 32), static_cast<uint32_t>(sm),
+                                         0x90);
     }
-    return peers;
+    return (static_cast<unsigned long long>(hi) << 32) | lo;
 }
 
 // Row-vector of V elements moved as one aligned load / store.

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "device_utils.h"
 #include "internal.h"
@@ -221,15 +222,20 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
 }
 
 // Per-tile digit histogram of the narrowed keys, written digit-major:
-// hist[d * nblocks + tile].
+// hist[d * nblocks + tile].  Lanes holding the same digit are matched and the
+// lowest of them adds their number to the wave's own histogram, so runs of
+// one key (hub messages, already grouped by the earlier passes) cost one LDS
+// update per wave instead of a chain of conflicting atomics.
+template <int BITS>
 __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* __restrict__ keys,
-                                                                int64_t n, int shift, int bits,
+                                                                int64_t n, int shift,
                                                                 uint32_t* __restrict__ hist,
                                                                 int64_t nblocks) {
-    __shared__ uint32_t h[(kSortThreads / kWave) * kSubHists * kSortBins];
-    hist_clear(h);
+    constexpr int kWaves = kSortThreads / kWave;
+    __shared__ uint32_t h[kWaves * kSortBins];
+    for (int i = static_cast<int>(threadIdx.x); i < kWaves * kSortBins; i += kSortThreads) h[i] = 0;
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
-    const uint32_t dmask = (1u << bits) - 1u;
+    constexpr uint32_t dmask = (1u << BITS) - 1u;
     uint32_t key[kSortItems];
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
@@ -237,13 +243,19 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
         key[i] = p < n ? keys[p] : 0u;
     }
     __syncthreads();
+    uint32_t* wh = h + (static_cast<int>(threadIdx.x) / kWave) * kSortBins;
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
-        if (p < n) hist_add(h, (key[i] >> shift) & dmask);
+        const bool active = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x < n;
+        const uint32_t d = (key[i] >> shift) & dmask;
+        const unsigned long long peers = match_digit<BITS>(d, __ballot(active));
+        if (active && (peers & lanemask_lt()) == 0) wh[d] += static_cast<uint32_t>(__popcll(peers));
     }
     __syncthreads();
-    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = hist_total(h);
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t += h[w * kSortBins + threadIdx.x];
+    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = t;
 }
 
 // Stable scatter of one tile.  Wave w owns tile positions [w*1024, (w+1)*1024)
@@ -251,9 +263,10 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
 // key's rank is counted in that order, the tile is staged in LDS in digit order
 // and written out in runs per digit.  In the first pass a tile flagged in
 // tile_plain takes the edge ids as its values.
+template <int BITS>
 __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
-    const uint32_t* __restrict__ tile_plain, int64_t n, int shift, int bits,
+    const uint32_t* __restrict__ tile_plain, int64_t n, int shift,
     const uint32_t* __restrict__ hist_scanned, const uint32_t* __restrict__ digit_tot,
     int64_t nblocks, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
     constexpr int kWaves = kSortThreads / kWave;
@@ -268,7 +281,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     const int lane = lane_id();
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kSortTile;
-    const uint32_t dmask = (1u << bits) - 1u;
+    constexpr uint32_t dmask = (1u << BITS) - 1u;
     // this tile's start within each digit does not depend on the keys: fetch
     // it together with them
     const uint32_t tile_prefix = hist_scanned[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x];
@@ -295,7 +308,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     for (int r = 0; r < kSortItems; ++r) {
         const bool active = wave_base + r * kWave < n;
         const uint32_t d = (key[r] >> shift) & dmask;
-        const unsigned long long peers = match_digit(d, bits, __ballot(active));
+        const unsigned long long peers = match_digit<BITS>(d, __ballot(active));
         const uint32_t below = __popcll(peers & lanemask_lt());
         uint32_t before = 0;
         if (active) before = wcnt[wave][d];
@@ -586,6 +599,26 @@ size_t sort_hist_words(int64_t n) {
     return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks + 1);
 }
 
+namespace {
+
+// Calls f(std::integral_constant<int, bits>) for a digit width of 0..8 bits.
+template <class F>
+void with_digit_bits(int bits, F&& f) {
+    switch (bits) {
+        case 0: f(std::integral_constant<int, 0>{}); break;
+        case 1: f(std::integral_constant<int, 1>{}); break;
+        case 2: f(std::integral_constant<int, 2>{}); break;
+        case 3: f(std::integral_constant<int, 3>{}); break;
+        case 4: f(std::integral_constant<int, 4>{}); break;
+        case 5: f(std::integral_constant<int, 5>{}); break;
+        case 6: f(std::integral_constant<int, 6>{}); break;
+        case 7: f(std::integral_constant<int, 7>{}); break;
+        default: f(std::integral_constant<int, 8>{}); break;
+    }
+}
+
+}  // namespace
+
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,
                        uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s) {
@@ -606,13 +639,16 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         const bool last = p == passes - 1;
         uint32_t* out_k = last ? keys_out : (p % 2 == 0 ? buf.keys_a : buf.keys_b);
         uint32_t* out_v = last ? vals_out : (p % 2 == 0 ? buf.vals_a : buf.vals_b);
+        const dim3 grid(static_cast<unsigned>(nblocks)), block(kSortThreads);
         if (p == 0) {
-            hipLaunchKernelGGL(k_radix_narrow, dim3(static_cast<unsigned>(nblocks)), dim3(kSortThreads),
-                               0, s, keys, gathers, n, shift, width, key_bound, gather_bound,
-                               buf.keys_b, buf.vals_b, buf.tile_plain, buf.hist, nblocks, st);
+            hipLaunchKernelGGL(k_radix_narrow, grid, block, 0, s, keys, gathers, n, shift, width,
+                               key_bound, gather_bound, buf.keys_b, buf.vals_b, buf.tile_plain,
+                               buf.hist, nblocks, st);
         } else {
-            hipLaunchKernelGGL(k_radix_upsweep, dim3(static_cast<unsigned>(nblocks)), dim3(kSortThreads),
-                               0, s, in_k, n, shift, width, buf.hist, nblocks);
+            with_digit_bits(width, [&](auto bt) {
+                hipLaunchKernelGGL((k_radix_upsweep<decltype(bt)::value>), grid, block, 0, s, in_k, n,
+                                   shift, buf.hist, nblocks);
+            });
         }
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
@@ -620,11 +656,12 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
                            digit_tot);
         err = hipGetLastError();
         if (err != hipSuccess) return err;
-        hipLaunchKernelGGL(k_radix_downsweep, dim3(static_cast<unsigned>(nblocks)), dim3(kSortThreads),
-                           0, s, in_k, in_v,
-                           p == 0 ? static_cast<const uint32_t*>(buf.tile_plain) : nullptr, n, shift,
-                           width, static_cast<const uint32_t*>(buf.hist),
-                           static_cast<const uint32_t*>(digit_tot), nblocks, out_k, out_v);
+        const uint32_t* plain = p == 0 ? static_cast<const uint32_t*>(buf.tile_plain) : nullptr;
+        with_digit_bits(width, [&](auto bt) {
+            hipLaunchKernelGGL((k_radix_downsweep<decltype(bt)::value>), grid, block, 0, s, in_k, in_v,
+                               plain, n, shift, static_cast<const uint32_t*>(buf.hist),
+                               static_cast<const uint32_t*>(digit_tot), nblocks, out_k, out_v);
+        });
         err = hipGetLastError();
         if (err != hipSuccess) return err;
         in_k = out_k;

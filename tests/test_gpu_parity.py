@@ -162,7 +162,9 @@ def test_c1_outputs_match_reference_digests() -> None:
 @pytest.mark.parametrize(
     "num_keys,num_edges,skew",
     [(1, 1000, False), (2, 5000, False), (300, 1, False), (4096, 98304, False),
-     (50_000, 400_000, True), ((1 << 20) + 3, 300_000, False), (70_000, 4096 * 3 + 17, True)],
+     (50_000, 400_000, True), ((1 << 20) + 3, 300_000, False), (70_000, 4096 * 3 + 17, True),
+     # three sort passes; several tiles per sort chunk (more tiles than resident workgroups)
+     ((1 << 23) + 1, 200_000, False), (1 << 20, 5_000_003, True), ((1 << 21) - 7, 4_000_000, False)],
 )
 def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, skew: bool) -> None:
     from relmo_amd import capi
