@@ -136,7 +136,21 @@ int relm_mp_fanin_reduce_logsumexp_backward(int dtype, const void* grad_out, int
 
 enum relm_mp_plan_kind { RELM_MP_PLAN_INVERSE = 1, RELM_MP_PLAN_CSR = 2 };
 
-/* Descriptor of a plan.  All pointers point into the caller's plan memory. */
+/* Statistics of a CSR plan as the build's kernels write them into plan
+ * memory.  They are valid in stream order after the build, so compute entry
+ * points read them there and a plan is usable before the host has them. */
+typedef struct relm_mp_plan_counts {
+    int64_t max_degree;
+    int64_t num_hubs;
+    int64_t num_chunks;
+    int64_t num_multi_hubs;
+    int64_t num_items;
+    int64_t num_short;
+} relm_mp_plan_counts;
+
+/* Descriptor of a plan.  All pointers point into the caller's plan memory.
+ * The CSR statistics max_degree .. num_short are -1 after
+ * relm_mp_csr_plan_build_async until relm_mp_plan_read_counts fills them. */
 typedef struct relm_mp_plan {
     int32_t kind;
     int32_t hub_threshold;   /* CSR: segments longer than this use the hub path */
@@ -165,6 +179,7 @@ typedef struct relm_mp_plan {
     int32_t* item_short;     /* CSR: [num_items + 1] short_off[item_first[j]]  */
     int32_t* short_off;      /* CSR: [num_keys + 1] edges of non-hub segments before each key */
     int32_t* short_gather;   /* CSR: [num_short] gather_sorted without the hub segments */
+    const relm_mp_plan_counts* counts; /* CSR: the statistics, in device memory */
 } relm_mp_plan;
 
 /* Inverse plan: inv[k] = largest e with keys[e] == k, or -1 (plan->inv is
@@ -181,7 +196,8 @@ int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* k
 
 /* CSR plan: stable counting order of the edges by key (edge order kept inside
  * each segment), offsets, the gathered row of every edge in that order, and the
- * list of hub segments.  Synchronises `stream` once. */
+ * list of hub segments.  Validates like relm_mp_inv_plan_build.  Waits for
+ * `stream` to finish the build and fills the statistics. */
 size_t relm_mp_csr_plan_bytes(int64_t num_keys, int64_t num_edges);
 size_t relm_mp_csr_plan_scratch_bytes(int64_t num_keys, int64_t num_edges);
 int relm_mp_csr_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
@@ -189,6 +205,20 @@ int relm_mp_csr_plan_build(const int64_t* keys, int64_t key_bound, const char* k
                            int gather_checked_first, int64_t num_edges, void* plan_mem,
                            size_t plan_bytes, void* scratch, size_t scratch_bytes,
                            relm_mp_plan* plan, relm_mp_stream_t stream);
+/* The same build, returning as soon as the indices are validated (after the
+ * first sort pass; the rest of the build stays queued on `stream`): the
+ * host-side statistics are -1 and gather_identity is set.  No counterpart in
+ * the reference: callers that go on to enqueue compute work on the plan use
+ * it so that the device does not idle while the host waits. */
+int relm_mp_csr_plan_build_async(const int64_t* keys, int64_t key_bound, const char* key_name,
+                                 const int64_t* gathers, int64_t gather_bound,
+                                 const char* gather_name, int gather_checked_first,
+                                 int64_t num_edges, void* plan_mem, size_t plan_bytes,
+                                 void* scratch, size_t scratch_bytes, relm_mp_plan* plan,
+                                 relm_mp_stream_t stream);
+/* Copies plan->counts into the host-side statistics of a CSR plan
+ * (synchronises `stream`). */
+int relm_mp_plan_read_counts(relm_mp_plan* plan, relm_mp_stream_t stream);
 
 /* Scratch needed by the compute entry points below for hub partial results
  * of a CSR plan (0 for inverse plans). */

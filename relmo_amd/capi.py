@@ -46,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "relm_mp_csr_plan_bytes",
     "relm_mp_csr_plan_scratch_bytes",
     "relm_mp_csr_plan_build",
+    "relm_mp_csr_plan_build_async",
+    "relm_mp_plan_read_counts",
     "relm_mp_plan_compute_scratch_bytes",
     "relm_mp_plan_gather_last",
     "relm_mp_plan_segment_reduce",
@@ -84,6 +86,7 @@ class Plan(ctypes.Structure):
         ("item_short", ctypes.c_void_p),
         ("short_off", ctypes.c_void_p),
         ("short_gather", ctypes.c_void_p),
+        ("counts", ctypes.c_void_p),
     ]
 
 
@@ -118,6 +121,11 @@ _SIGNATURES = {
         _int,
         [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _vp, _sz, _PP, _vp],
     ),
+    "relm_mp_csr_plan_build_async": (
+        _int,
+        [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _vp, _sz, _PP, _vp],
+    ),
+    "relm_mp_plan_read_counts": (_int, [_PP, _vp]),
     "relm_mp_plan_compute_scratch_bytes": (_sz, [_PP, _i64, _int, _i64]),
     "relm_mp_plan_gather_last": (_int, [_int, _PP, _vp, _vp, _i64, _vp, _vp]),
     "relm_mp_plan_segment_reduce": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
@@ -353,20 +361,31 @@ def inv_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, g
 
 
 def csr_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, gather_bound: int,
-             key_name: str = "key", gather_name: str = "gather", gather_first: bool = False) -> BuiltPlan:
+             key_name: str = "key", gather_name: str = "gather", gather_first: bool = False,
+             wait_counts: bool = True) -> BuiltPlan:
+    """CSR plan; with wait_counts=False the build returns after validation and the
+    host-side statistics stay -1 until read_counts()."""
+
     _check_index(keys)
     n = keys.numel()
     mem = _bytes(lib().relm_mp_csr_plan_bytes(key_bound, n), keys)
     scratch = _bytes(lib().relm_mp_csr_plan_scratch_bytes(key_bound, n), keys)
     plan = Plan()
+    build = lib().relm_mp_csr_plan_build if wait_counts else lib().relm_mp_csr_plan_build_async
     check(
-        lib().relm_mp_csr_plan_build(
+        build(
             _ptr(keys), key_bound, key_name.encode(), _ptr(gathers), gather_bound,
             gather_name.encode(), int(gather_first), n, _ptr(mem), mem.numel(), _ptr(scratch),
             scratch.numel(), ctypes.byref(plan), _stream(keys),
         )
     )
-    return BuiltPlan(plan, mem)
+    bp = BuiltPlan(plan, mem)
+    bp.scratch = scratch  # the queued build kernels still use it
+    return bp
+
+
+def read_counts(bp: BuiltPlan, like: torch.Tensor) -> None:
+    check(lib().relm_mp_plan_read_counts(ctypes.byref(bp.plan), _stream(like)))
 
 
 def plan_segment_reduce(bp: BuiltPlan, table: torch.Tensor, mode: int, gathers: torch.Tensor | None = None) -> torch.Tensor:

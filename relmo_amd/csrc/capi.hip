@@ -58,15 +58,12 @@ int check_dtype(int dtype) {
         if (_e != hipSuccess) return hip_error(_e, what);     \
     } while (0)
 
-// Reads the status back (one stream synchronisation) and turns a bad index
-// into the reference's message "<name> index out of bounds: i not in [0, n)."
-// for the first offending edge in edge order.
-int finish_validation(const DevStatus* dst, DevStatus& host, const int64_t* keys, int64_t key_bound,
-                      const char* key_name, const int64_t* gathers, int64_t gather_bound,
-                      const char* gather_name, int gather_checked_first, hipStream_t s) {
-    RELM_HIP(hipMemcpyAsync(&host, dst, sizeof(DevStatus), hipMemcpyDeviceToHost, s),
-             "relm_mp status copy");
-    RELM_HIP(hipStreamSynchronize(s), "relm_mp status sync");
+// Turns a bad index recorded in a status read back to the host into the
+// reference's message "<name> index out of bounds: i not in [0, n)." for the
+// first offending edge in edge order.
+int check_validation(const DevStatus& host, const int64_t* keys, int64_t key_bound,
+                     const char* key_name, const int64_t* gathers, int64_t gather_bound,
+                     const char* gather_name, int gather_checked_first) {
     const unsigned long long ek = host.bad_key_edge;
     const unsigned long long eg = gathers != nullptr ? host.bad_gather_edge : kNoEdge;
     if (ek == kNoEdge && eg == kNoEdge) return RELM_MP_OK;
@@ -90,6 +87,78 @@ int finish_validation(const DevStatus* dst, DevStatus& host, const int64_t* keys
     return set_error(RELM_MP_ERR_INDEX_OUT_OF_BOUNDS, buf);
 }
 
+// Reads the status back (one stream synchronisation) and checks it.
+int finish_validation(const DevStatus* dst, DevStatus& host, const int64_t* keys, int64_t key_bound,
+                      const char* key_name, const int64_t* gathers, int64_t gather_bound,
+                      const char* gather_name, int gather_checked_first, hipStream_t s) {
+    RELM_HIP(hipMemcpyAsync(&host, dst, sizeof(DevStatus), hipMemcpyDeviceToHost, s),
+             "relm_mp status copy");
+    RELM_HIP(hipStreamSynchronize(s), "relm_mp status sync");
+    return check_validation(host, keys, key_bound, key_name, gathers, gather_bound, gather_name,
+                            gather_checked_first);
+}
+
+// Per host thread and device: pinned host copies of a plan status and plan
+// counts, and an event marking when the status copy has landed.  A build
+// waits for its own event before returning, so one slot per thread suffices.
+struct HostSlot {
+    int device = -1;
+    hipEvent_t ready = nullptr;
+    DevStatus* status = nullptr;         // host address
+    DevStatus* status_mapped = nullptr;  // the same memory as the device addresses it
+    relm_mp_plan_counts* counts = nullptr;
+};
+
+int host_slot(HostSlot** out) {
+    thread_local HostSlot slots[16];
+    int dev = 0;
+    RELM_HIP(hipGetDevice(&dev), "relm_mp device query");
+    for (HostSlot& h : slots) {
+        if (h.device == dev) {
+            *out = &h;
+            return RELM_MP_OK;
+        }
+    }
+    for (HostSlot& h : slots) {
+        if (h.device < 0) {
+            // default system-scope release on record: the status stores of
+            // the kernel before it are visible once the event has completed
+            RELM_HIP(hipEventCreateWithFlags(&h.ready, hipEventDisableTiming), "relm_mp event");
+            void* mem = nullptr;
+            RELM_HIP(hipHostMalloc(&mem, sizeof(DevStatus) + sizeof(relm_mp_plan_counts),
+                                   hipHostMallocDefault),
+                     "relm_mp pinned status");
+            h.status = static_cast<DevStatus*>(mem);
+            h.counts = reinterpret_cast<relm_mp_plan_counts*>(static_cast<char*>(mem) + sizeof(DevStatus));
+            void* mapped = nullptr;
+            RELM_HIP(hipHostGetDevicePointer(&mapped, mem, 0), "relm_mp pinned status mapping");
+            h.status_mapped = static_cast<DevStatus*>(mapped);
+            h.device = dev;
+            *out = &h;
+            return RELM_MP_OK;
+        }
+    }
+    return set_error(RELM_MP_ERR_HIP, "relm_mp: too many devices for one host thread");
+}
+
+int read_counts(relm_mp_plan* plan, hipStream_t s) {
+    if (plan->kind != RELM_MP_PLAN_CSR || plan->counts == nullptr) return RELM_MP_OK;
+    HostSlot* hs = nullptr;
+    RELM_TRY(host_slot(&hs));
+    RELM_HIP(hipMemcpyAsync(hs->counts, plan->counts, sizeof(relm_mp_plan_counts),
+                            hipMemcpyDeviceToHost, s),
+             "relm_mp counts copy");
+    RELM_HIP(hipStreamSynchronize(s), "relm_mp counts sync");
+    const relm_mp_plan_counts c = *hs->counts;
+    plan->max_degree = c.max_degree;
+    plan->num_hubs = c.num_hubs;
+    plan->num_chunks = c.num_chunks;
+    plan->num_multi_hubs = c.num_multi_hubs;
+    plan->num_items = c.num_items;
+    plan->num_short = c.num_short;
+    return RELM_MP_OK;
+}
+
 struct InvLayout {
     DevStatus* status;
     int32_t* inv;
@@ -105,13 +174,10 @@ InvLayout inv_layout(void* mem, int64_t num_keys) {
     return l;
 }
 
-int64_t max_hubs(int64_t num_edges) { return num_edges / (kHubThreshold + 1) + 1; }
-int64_t max_chunks(int64_t num_edges) {
-    return num_edges / kChunkSize + max_hubs(num_edges) + 1;
-}
 
 struct CsrLayout {
     DevStatus* status;
+    relm_mp_plan_counts* counts;
     int32_t* offsets;
     int32_t* gather_sorted;
     int32_t* keys_sorted;
@@ -131,6 +197,7 @@ CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
     Carver c(mem);
     CsrLayout l;
     l.status = c.take<DevStatus>(1);
+    l.counts = c.take<relm_mp_plan_counts>(1);
     l.offsets = c.take<int32_t>(static_cast<size_t>(num_keys) + 1);
     l.gather_sorted = c.take<int32_t>(static_cast<size_t>(num_edges));
     l.keys_sorted = c.take<int32_t>(static_cast<size_t>(num_edges));
@@ -209,7 +276,7 @@ int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
 int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, const int64_t* gathers,
               int64_t gather_bound, const char* gather_name, int gather_checked_first,
               int64_t num_edges, void* plan_mem, size_t plan_bytes, void* scratch,
-              size_t scratch_bytes, relm_mp_plan* plan, hipStream_t s) {
+              size_t scratch_bytes, relm_mp_plan* plan, bool wait_counts, hipStream_t s) {
     RELM_TRY(check_rows(key_bound, "num_keys"));
     RELM_TRY(check_rows(num_edges, "num_edges"));
     if (gathers != nullptr) RELM_TRY(check_rows(gather_bound, "num_gather"));
@@ -219,6 +286,8 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR plan memory too small");
     if (scratch == nullptr || scratch_bytes < sc.bytes)
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR scratch memory too small");
+    HostSlot* hs = nullptr;
+    RELM_TRY(host_slot(&hs));
     std::memset(plan, 0, sizeof(*plan));
     plan->kind = RELM_MP_PLAN_CSR;
     plan->hub_threshold = kHubThreshold;
@@ -237,13 +306,24 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->item_short = l.item_short;
     plan->short_off = l.short_off;
     plan->short_gather = l.short_gather;
-    plan->num_items = l.num_items;
+    plan->counts = l.counts;
+    plan->max_degree = plan->num_hubs = plan->num_chunks = plan->num_multi_hubs = -1;
+    plan->num_items = plan->num_short = -1;
     RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
+    // The validation result is final after the first sort pass: copy it to
+    // the host and mark the point, then enqueue the rest of the build.
+    auto mark_validation = [&]() -> hipError_t {
+        hipError_t e = launch_status_publish(l.status, hs->status_mapped, s);
+        return e != hipSuccess ? e : hipEventRecord(hs->ready, s);
+    };
     if (num_edges > 0) {
         RELM_HIP(sort_by_key(keys, key_bound, gathers, gather_bound, num_edges, sc.sort,
                              reinterpret_cast<uint32_t*>(l.keys_sorted),
-                             reinterpret_cast<uint32_t*>(l.gather_sorted), l.status, s),
+                             reinterpret_cast<uint32_t*>(l.gather_sorted), l.status, s,
+                             mark_validation),
                  "relm_mp radix sort");
+    } else {
+        RELM_HIP(mark_validation(), "relm_mp status copy");
     }
     RELM_HIP(launch_offsets_from_sorted(reinterpret_cast<const uint32_t*>(l.keys_sorted), num_edges,
                                         key_bound, l.offsets, s),
@@ -251,22 +331,14 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_HIP(launch_key_index(l.offsets, l.gather_sorted, key_bound, sc.key_index, l.hub_key,
                               l.hub_chunk_base, l.multi_hubs, l.chunk_hub, max_hubs(num_edges),
                               max_chunks(num_edges), l.item_first, l.item_short, l.num_items,
-                              l.short_off, l.short_gather, l.status, s),
+                              l.short_off, l.short_gather, l.counts, l.status, s),
              "relm_mp key index kernels");
-    DevStatus host{};
-    RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
-                               gather_name, gather_checked_first, s));
-    plan->max_degree = static_cast<int64_t>(host.max_degree);
-    plan->num_hubs = static_cast<int64_t>(host.num_hubs);
-    plan->num_chunks = static_cast<int64_t>(host.num_chunks);
-    plan->num_multi_hubs = static_cast<int64_t>(host.num_multi_hubs);
-    plan->num_items = std::min<int64_t>(static_cast<int64_t>(host.total_weight) / kItemSize + 1,
-                                        l.num_items);
-    plan->num_short = static_cast<int64_t>(host.total_weight) - key_bound;
+    RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
+    const DevStatus host = *hs->status;
+    RELM_TRY(check_validation(host, keys, key_bound, key_name, gathers, gather_bound, gather_name,
+                              gather_checked_first));
     plan->gather_identity = gathers == nullptr || host.gather_mismatch == 0 ? 1 : 0;
-    if (plan->num_hubs > max_hubs(num_edges) || plan->num_chunks > max_chunks(num_edges) ||
-        plan->num_multi_hubs > plan->num_hubs)
-        return set_error(RELM_MP_ERR_HIP, "relm_mp: hub list overflow");
+    if (wait_counts) RELM_TRY(read_counts(plan, s));
     return RELM_MP_OK;
 }
 
@@ -334,7 +406,23 @@ int relm_mp_csr_plan_build(const int64_t* keys, int64_t key_bound, const char* k
                            relm_mp_plan* plan, relm_mp_stream_t stream) {
     return csr_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
                      gather_checked_first, num_edges, plan_mem, plan_bytes, scratch, scratch_bytes,
-                     plan, static_cast<hipStream_t>(stream));
+                     plan, true, static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_csr_plan_build_async(const int64_t* keys, int64_t key_bound, const char* key_name,
+                                 const int64_t* gathers, int64_t gather_bound,
+                                 const char* gather_name, int gather_checked_first,
+                                 int64_t num_edges, void* plan_mem, size_t plan_bytes,
+                                 void* scratch, size_t scratch_bytes, relm_mp_plan* plan,
+                                 relm_mp_stream_t stream) {
+    return csr_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
+                     gather_checked_first, num_edges, plan_mem, plan_bytes, scratch, scratch_bytes,
+                     plan, false, static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_plan_read_counts(relm_mp_plan* plan, relm_mp_stream_t stream) {
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    return read_counts(plan, static_cast<hipStream_t>(stream));
 }
 
 size_t relm_mp_plan_compute_scratch_bytes(const relm_mp_plan* plan, int64_t emb, int dtype,
@@ -439,7 +527,7 @@ int relm_mp_fanout_scatter_backward(int dtype, const void* grad_out, int64_t gra
     relm_mp_plan plan;
     RELM_TRY(csr_build(src_global_idx, x_rows, "src_global_idx", flat_dst, grad_out_rows, "flat_dst",
                        0, num_edges, workspace, plan_bytes, scratch, workspace_bytes - plan_bytes,
-                       &plan, s));
+                       &plan, false, s));
     return compute_segment_reduce(dtype, plan, nullptr, grad_out, emb, RELM_MP_MODE_SUM, grad_x,
                                   scratch, workspace_bytes - plan_bytes, s);
 }
@@ -477,7 +565,7 @@ int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int6
     char* scratch = static_cast<char*>(workspace) + plan_bytes;
     relm_mp_plan plan;
     RELM_TRY(csr_build(dst_idx, dim_size, "dst_idx", flat_src, rel_rows, "flat_src", 1, num_edges,
-                       workspace, plan_bytes, scratch, workspace_bytes - plan_bytes, &plan, s));
+                       workspace, plan_bytes, scratch, workspace_bytes - plan_bytes, &plan, false, s));
     return compute_segment_reduce(dtype, plan, nullptr, rel_flat, emb, mode, out, scratch,
                                   workspace_bytes - plan_bytes, s);
 }
@@ -518,7 +606,7 @@ int relm_mp_fanin_reduce_sum_backward(int dtype, const void* grad_out, int64_t g
     char* scratch = csr_mem + plan_bytes;
     const size_t scratch_bytes = workspace_bytes - inv_bytes - plan_bytes;
     RELM_TRY(csr_build(flat_src, rel_rows, "flat_src", dst_idx, grad_out_rows, "dst_idx", 0,
-                       num_edges, csr_mem, plan_bytes, scratch, scratch_bytes, &plan, s));
+                       num_edges, csr_mem, plan_bytes, scratch, scratch_bytes, &plan, false, s));
     return compute_segment_reduce(dtype, plan, nullptr, grad_out, emb, RELM_MP_MODE_SUM, grad_rel,
                                   scratch, scratch_bytes, s);
 }
@@ -569,7 +657,7 @@ int relm_mp_fanin_reduce_logsumexp_backward(int dtype, const void* grad_out, int
     char* scratch = csr_mem + plan_bytes;
     const size_t scratch_bytes = workspace_bytes - inv_bytes - plan_bytes;
     RELM_TRY(csr_build(flat_src, key_bound, "flat_src", dst_idx, dim_size, "dst_idx", 1, num_edges,
-                       csr_mem, plan_bytes, scratch, scratch_bytes, &plan, s));
+                       csr_mem, plan_bytes, scratch, scratch_bytes, &plan, false, s));
     return compute_logsumexp_backward(dtype, plan, nullptr, grad_out, out, rel_flat, emb, grad_rel,
                                       scratch, scratch_bytes, s);
 }

@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <string>
 
 #include "relm_mp.h"
@@ -25,6 +26,9 @@ struct DevStatus {
     unsigned long long gather_mismatch;  // CSR plans: nonzero if gathers[e] != e for some edge
     unsigned long long key_mismatch;     // inverse plans: nonzero if keys[e] != e for some edge
 };
+static_assert(sizeof(DevStatus) % sizeof(unsigned long long) == 0 &&
+                  sizeof(DevStatus) / sizeof(unsigned long long) <= 64,
+              "status words fit one wave");
 
 constexpr unsigned long long kNoEdge = ~0ull;
 
@@ -54,6 +58,8 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // ---- plan kernels (plan_kernels.hip) -------------------------------------
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
 hipError_t launch_status_init(DevStatus* st, hipStream_t s);
+// Copies *st to pinned host memory through its device mapping.
+hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped, hipStream_t s);
 hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                             int64_t gather_bound, int64_t n, int32_t* inv, DevStatus* st,
                             hipStream_t s);
@@ -72,9 +78,12 @@ struct SortBuffers {
 };
 int64_t sort_tiles(int64_t n);
 size_t sort_hist_words(int64_t n);
+// after_validation (may be null) is called once the first pass is enqueued:
+// from then on, in stream order, `st` holds the validation result.
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,
-                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s);
+                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s,
+                       const std::function<hipError_t()>& after_validation);
 
 hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
                                       int32_t* offsets, hipStream_t s);
@@ -93,7 +102,13 @@ hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted
                             int32_t* multi_hubs, int32_t* chunk_hub, int64_t hub_capacity,
                             int64_t chunk_capacity, int32_t* item_first, int32_t* item_short,
                             int64_t item_capacity, int32_t* short_off, int32_t* short_gather,
-                            DevStatus* st, hipStream_t s);
+                            relm_mp_plan_counts* counts, DevStatus* st, hipStream_t s);
+
+// Capacities of the hub arrays of a CSR plan over num_edges edges.
+inline int64_t max_hubs(int64_t num_edges) { return num_edges / (kHubThreshold + 1) + 1; }
+inline int64_t max_chunks(int64_t num_edges) {
+    return num_edges / kChunkSize + max_hubs(num_edges) + 1;
+}
 
 // ---- compute kernels (reduce_kernels.hip) --------------------------------
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,

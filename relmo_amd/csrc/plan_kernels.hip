@@ -46,6 +46,16 @@ __global__ void k_status_init(DevStatus* st) {
     }
 }
 
+// Copies the status to host memory mapped for the device (vector stores).
+// The host reads it after an event recorded behind this kernel has
+// completed; the event's system-scope release makes the stores visible.
+__global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __restrict__ host) {
+    constexpr int kWords = static_cast<int>(sizeof(DevStatus) / sizeof(unsigned long long));
+    const int i = static_cast<int>(threadIdx.x);
+    if (i < kWords)
+        reinterpret_cast<unsigned long long*>(host)[i] = reinterpret_cast<const unsigned long long*>(st)[i];
+}
+
 // inv[k] = max e with keys[e] == k.  Every key and gathered index is checked;
 // the smallest offending edge of each array is recorded.
 __global__ __launch_bounds__(kThreads) void k_inv_build(const int64_t* __restrict__ keys,
@@ -471,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     int32_t* __restrict__ multi_hubs, int32_t* __restrict__ chunk_hub, int64_t hub_capacity,
     int64_t chunk_capacity, int32_t* __restrict__ item_first, int32_t* __restrict__ item_short,
     int64_t item_capacity, int32_t* __restrict__ short_off, int32_t* __restrict__ short_gather,
-    DevStatus* __restrict__ st) {
+    relm_mp_plan_counts* __restrict__ pc, DevStatus* __restrict__ st) {
     __shared__ uint32_t lds[kThreads / kWave];
     __shared__ int32_t blk_slot[kThreads];
     __shared__ int64_t blk_cbase[kThreads];
@@ -485,7 +495,8 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     const uint32_t ie = block_inclusive_scan<kThreads>(f.hub_edges, lds, te);
     const int64_t stride = nblk + 1;
     if (blockIdx.x == 0) {
-        // totals and the longest segment into the status
+        // totals (within the capacities the plan arrays were sized for) and
+        // the longest segment into the plan's counts and the status
         uint32_t m = 0;
         for (int64_t b = threadIdx.x; b < nblk; b += kThreads) {
             const uint32_t v = counts[4 * stride + b];
@@ -496,8 +507,18 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
             const uint32_t other = __shfl_xor(m, o, kWave);
             m = other > m ? other : m;
         }
-        if (lane_id() == 0) atomicMax(&st->max_degree, static_cast<unsigned long long>(m));
+        if (lane_id() == 0) lds[threadIdx.x / kWave] = m;
+        __syncthreads();
         if (threadIdx.x == 0) {
+            for (int w = 1; w < kThreads / kWave; ++w) m = lds[w] > m ? lds[w] : m;
+            const int64_t hubs = min(static_cast<int64_t>(totals[0]), hub_capacity);
+            const int64_t chunks = min(static_cast<int64_t>(totals[1]), chunk_capacity);
+            const int64_t multi = min(static_cast<int64_t>(totals[2]), hubs);
+            pc->max_degree = m;
+            pc->num_hubs = hubs;
+            pc->num_chunks = chunks;
+            pc->num_multi_hubs = multi;
+            st->max_degree = m;
             st->num_hubs = totals[0];
             st->num_chunks = totals[1];
             st->num_multi_hubs = totals[2];
@@ -551,6 +572,8 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     }
     if (k == num_keys) {
         st->total_weight = static_cast<unsigned long long>(W);
+        pc->num_items = min(W / kItemSize + 1, item_capacity);
+        pc->num_short = W - num_keys;
         return;
     }
     // the short segment's gathered rows, back to back in key order
@@ -579,6 +602,11 @@ hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s) 
 
 hipError_t launch_status_init(DevStatus* st, hipStream_t s) {
     hipLaunchKernelGGL(k_status_init, dim3(1), dim3(64), 0, s, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped, hipStream_t s) {
+    hipLaunchKernelGGL(k_status_publish, dim3(1), dim3(64), 0, s, st, host_mapped);
     return hipGetLastError();
 }
 
@@ -621,7 +649,8 @@ void with_digit_bits(int bits, F&& f) {
 
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,
-                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s) {
+                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s,
+                       const std::function<hipError_t()>& after_validation) {
     if (n <= 0) return hipSuccess;
     int bits = 0;
     while (bits < 32 && (1ll << bits) < key_bound) ++bits;
@@ -652,6 +681,10 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         }
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
+        if (p == 0 && after_validation) {
+            err = after_validation();
+            if (err != hipSuccess) return err;
+        }
         hipLaunchKernelGGL(k_scan_rows, dim3(kSortBins), dim3(kScanThreads), 0, s, buf.hist, nblocks,
                            digit_tot);
         err = hipGetLastError();
@@ -692,7 +725,7 @@ hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted
                             int32_t* multi_hubs, int32_t* chunk_hub, int64_t hub_capacity,
                             int64_t chunk_capacity, int32_t* item_first, int32_t* item_short,
                             int64_t item_capacity, int32_t* short_off, int32_t* short_gather,
-                            DevStatus* st, hipStream_t s) {
+                            relm_mp_plan_counts* pc, DevStatus* st, hipStream_t s) {
     const int64_t nblk = (num_keys + 1 + kThreads - 1) / kThreads;
     uint32_t* counts = scratch;
     uint32_t* totals = scratch + (kKeyRows + 1) * (nblk + 1);
@@ -708,7 +741,7 @@ hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted
                        gather_sorted, num_keys, nblk, static_cast<const uint32_t*>(counts),
                        static_cast<const uint32_t*>(totals), hub_key, hub_chunk_base, multi_hubs,
                        chunk_hub, hub_capacity, chunk_capacity, item_first, item_short,
-                       item_capacity, short_off, short_gather, st);
+                       item_capacity, short_off, short_gather, pc, st);
     return hipGetLastError();
 }
 

@@ -22,7 +22,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "device_utils.h"
 #include "internal.h"
@@ -361,7 +364,7 @@ template <typename T, int V, int G, class Op>
 __global__ __launch_bounds__(kThreads) void k_walk_items(
     const int32_t* __restrict__ short_off, const int32_t* __restrict__ short_gather,
     const int32_t* __restrict__ item_first, const int32_t* __restrict__ item_short,
-    int64_t num_items, int64_t num_keys, int64_t num_short, T* __restrict__ out, Op op) {
+    const relm_mp_plan_counts* __restrict__ pc, int64_t num_keys, T* __restrict__ out, Op op) {
     constexpr int R = kThreads / G;
     constexpr int U = batch_rows<G>();
     // R items hold at most R * kItemSize keys and R * kItemSize + kHubThreshold
@@ -375,6 +378,8 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
     op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     op.colok = op.col < op.D;
     const int64_t D = op.D;
+    const int64_t num_items = pc->num_items;
+    const int64_t num_short = pc->num_short;
     // block-uniform loop: every thread reaches the barriers below
     for (int64_t ib = static_cast<int64_t>(blockIdx.x) * R; ib < num_items;
          ib += static_cast<int64_t>(gridDim.x) * R) {
@@ -498,7 +503,7 @@ template <typename T, int V, int G, class Op>
 __global__ __launch_bounds__(kThreads) void k_hub_chunks(
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_edges,
     const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
-    const int32_t* __restrict__ chunk_hub, int64_t num_hubs, int64_t num_chunks,
+    const int32_t* __restrict__ chunk_hub, const relm_mp_plan_counts* __restrict__ pc,
     T* __restrict__ partial, T* __restrict__ out, Op op) {
     using Partial = typename Op::Partial;
     constexpr int NG = kThreads / G;
@@ -510,6 +515,8 @@ __global__ __launch_bounds__(kThreads) void k_hub_chunks(
     op.colok = op.col < op.D;
     const int64_t D = op.D;
     constexpr int64_t kPer = (kChunkSize + NG - 1) / NG;
+    const int64_t num_hubs = pc->num_hubs;
+    const int64_t num_chunks = pc->num_chunks;
     for (int64_t c = blockIdx.x; c < num_chunks; c += gridDim.x) {
         const HubChunk hc =
             hub_chunk(c, offsets, hub_key, hub_chunk_base, chunk_hub, num_hubs, num_edges);
@@ -567,8 +574,8 @@ template <typename T, int V, int G, class Partial>
 __global__ __launch_bounds__(kThreads) void k_hub_combine(
     const int32_t* __restrict__ offsets, int64_t num_edges, int64_t D,
     const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
-    const int32_t* __restrict__ multi_hubs, int64_t num_hubs, int64_t num_multi_hubs,
-    int64_t num_chunks, const T* __restrict__ partial, T* __restrict__ out) {
+    const int32_t* __restrict__ multi_hubs, const relm_mp_plan_counts* __restrict__ pc,
+    const T* __restrict__ partial, T* __restrict__ out) {
     constexpr int NG = kThreads / G;
     constexpr int U = batch_rows<G>();
     __shared__ Partial red[kThreads / kWave * G];
@@ -576,6 +583,9 @@ __global__ __launch_bounds__(kThreads) void k_hub_combine(
     const int grp = static_cast<int>(threadIdx.x) / G;
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     const bool colok = col < D;
+    const int64_t num_hubs = pc->num_hubs;
+    const int64_t num_multi_hubs = pc->num_multi_hubs;
+    const int64_t num_chunks = pc->num_chunks;
     for (int64_t bi = blockIdx.x; bi < num_multi_hubs; bi += gridDim.x) {
         const int64_t h = multi_hubs[bi];
         const bool hok = h >= 0 && h < num_hubs;
@@ -782,27 +792,81 @@ dim3 block_grid(int64_t blocks, int64_t slices) {
     return dim3(static_cast<unsigned>(bx), static_cast<unsigned>(slices));
 }
 
+// Workgroups of `kernel` (kThreads each) resident on the current device at
+// once; persistent launches size their grids with it.
+int64_t resident_blocks(const void* kernel) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, int64_t> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return 2048;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(kernel, dev);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int cus = 0, per_cu = 0;
+    int64_t r = 2048;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) == hipSuccess &&
+        cus > 0 && per_cu > 0)
+        r = static_cast<int64_t>(cus) * per_cu;
+    else
+        (void)hipGetLastError();
+    cache.emplace(key, r);
+    return r;
+}
+
+// Grid of a grid-stride launch over `work` units of `per_block` each, times
+// `slices` column slices: one workgroup per unit, at most `rounds` times what
+// is resident at once.  Unit costs vary (hub chunks of 65..2048 messages), so
+// several rounds of workgroups let the hardware scheduler balance them; the
+// workgroups past the actual count (read on the device) exit at once, which
+// costs about 1.5 ns each.
+dim3 persistent_grid(const void* kernel, int64_t work, int64_t per_block, int64_t slices,
+                     int64_t rounds) {
+    int64_t bx = (work + per_block - 1) / per_block;
+    const int64_t cap =
+        std::max<int64_t>(1, rounds * resident_blocks(kernel) / std::max<int64_t>(1, slices));
+    bx = std::max<int64_t>(1, std::min(bx, cap));
+    return dim3(static_cast<unsigned>(bx), static_cast<unsigned>(slices));
+}
+
 // Runs the CSR reduction of `op` (items, hub chunks, hub combines) into out.
+// The item, hub and chunk counts are read from plan.counts on the device:
+// grids are sized by the host-side counts where the plan has them (>= 0),
+// else by the plan's capacities, and capped (persistent_grid).
 template <typename T, int V, int G, class Op>
 int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, T* out,
             hipStream_t s) {
     using Partial = typename Op::Partial;
-    const int64_t emb = op.D;
-    hipLaunchKernelGGL((k_walk_items<T, V, G, Op>), row_grid(plan.num_items, G, slices),
+    if (plan.counts == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: CSR plan without counts");
+    const int64_t E = plan.num_edges;
+    const int64_t items = plan.num_items >= 0 ? plan.num_items : item_capacity_for(plan.num_keys);
+    const void* walk = reinterpret_cast<const void*>(&k_walk_items<T, V, G, Op>);
+    hipLaunchKernelGGL((k_walk_items<T, V, G, Op>), persistent_grid(walk, items, kThreads / G, slices, 4),
                        dim3(kThreads), 0, s, plan.short_off, plan.short_gather, plan.item_first,
-                       plan.item_short, plan.num_items, plan.num_keys, plan.num_short, out, op);
+                       plan.item_short, plan.counts, plan.num_keys, out, op);
     int rc = hip_error(hipGetLastError(), "relm_mp item kernel");
-    if (rc != RELM_MP_OK || plan.num_hubs == 0) return rc;
-    hipLaunchKernelGGL((k_hub_chunks<T, V, G, Op>), block_grid(plan.num_chunks, slices),
+    // no hub when the counts say so, or when no segment can be longer than the threshold
+    if (rc != RELM_MP_OK || plan.num_hubs == 0 || E <= kHubThreshold) return rc;
+    const int64_t chunks = plan.num_chunks >= 0 ? plan.num_chunks : max_chunks(E);
+    const void* hub = reinterpret_cast<const void*>(&k_hub_chunks<T, V, G, Op>);
+    hipLaunchKernelGGL((k_hub_chunks<T, V, G, Op>), persistent_grid(hub, chunks, 1, slices, 8),
                        dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.num_edges,
-                       plan.hub_key, plan.hub_chunk_base, plan.chunk_hub, plan.num_hubs,
-                       plan.num_chunks, partial, out, op);
+                       plan.hub_key, plan.hub_chunk_base, plan.chunk_hub, plan.counts, partial, out,
+                       op);
     rc = hip_error(hipGetLastError(), "relm_mp hub chunk kernel");
-    if (rc != RELM_MP_OK || plan.num_chunks == plan.num_hubs) return rc;  // single-chunk hubs only
-    hipLaunchKernelGGL((k_hub_combine<T, V, G, Partial>), block_grid(plan.num_multi_hubs, slices),
-                       dim3(kThreads), 0, s, plan.offsets, plan.num_edges, emb, plan.hub_key,
-                       plan.hub_chunk_base, plan.multi_hubs, plan.num_hubs, plan.num_multi_hubs,
-                       plan.num_chunks, static_cast<const T*>(partial), out);
+    // no hub of more than one chunk when the counts say so, or when none fits
+    if (rc != RELM_MP_OK || plan.num_multi_hubs == 0 || E <= kChunkSize) return rc;
+    const int64_t multi = plan.num_multi_hubs >= 0 ? plan.num_multi_hubs : E / (kChunkSize + 1) + 1;
+    const void* comb = reinterpret_cast<const void*>(&k_hub_combine<T, V, G, Partial>);
+    hipLaunchKernelGGL((k_hub_combine<T, V, G, Partial>), persistent_grid(comb, multi, 1, slices, 8),
+                       dim3(kThreads), 0, s, plan.offsets, plan.num_edges, op.D, plan.hub_key,
+                       plan.hub_chunk_base, plan.multi_hubs, plan.counts,
+                       static_cast<const T*>(partial), out);
     return hip_error(hipGetLastError(), "relm_mp hub combine kernel");
 }
 
@@ -887,10 +951,13 @@ int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void*
 }  // namespace
 
 size_t hub_partial_bytes(const relm_mp_plan& plan, int64_t emb, int dtype, int64_t mode) {
-    if (plan.kind != RELM_MP_PLAN_CSR || plan.num_chunks == 0) return 0;
+    if (plan.kind != RELM_MP_PLAN_CSR || plan.num_chunks == 0 || plan.num_edges <= kHubThreshold)
+        return 0;
     const size_t elem = dtype == RELM_MP_F64 ? 8 : 4;
     const size_t per = static_cast<size_t>(emb) * elem * (mode == RELM_MP_MODE_LOGSUMEXP ? 2 : 1);
-    return static_cast<size_t>(plan.num_chunks) * per;
+    // counts not read back yet: the capacity of the chunk list
+    const int64_t chunks = plan.num_chunks >= 0 ? plan.num_chunks : max_chunks(plan.num_edges);
+    return static_cast<size_t>(chunks) * per;
 }
 
 int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t s) {

@@ -287,11 +287,13 @@ GpuPlan csr_plan(const Tensor& key, int64_t key_bound, const char* key_name, con
     const int64_t n = key.numel();
     gp.mem = byte_buffer(relm_mp_csr_plan_bytes(key_bound, n), key);
     Tensor scratch = byte_buffer(relm_mp_csr_plan_scratch_bytes(key_bound, n), key);
-    raise_if(relm_mp_csr_plan_build(key.data_ptr<int64_t>(), key_bound, key_name,
-                                    gather.data_ptr<int64_t>(), gather_bound, gather_name,
-                                    gather_first ? 1 : 0, n, gp.mem.data_ptr(),
-                                    static_cast<size_t>(gp.mem.numel()), scratch.data_ptr(),
-                                    static_cast<size_t>(scratch.numel()), &gp.plan, s));
+    // returns once the indices are validated; the build's remaining kernels
+    // and the caller's compute stay queued on the stream
+    raise_if(relm_mp_csr_plan_build_async(key.data_ptr<int64_t>(), key_bound, key_name,
+                                          gather.data_ptr<int64_t>(), gather_bound, gather_name,
+                                          gather_first ? 1 : 0, n, gp.mem.data_ptr(),
+                                          static_cast<size_t>(gp.mem.numel()), scratch.data_ptr(),
+                                          static_cast<size_t>(scratch.numel()), &gp.plan, s));
     cache.insert(kRoleCsr, key, gather, key_bound, gather_bound, gp.mem, gp.plan);
     return gp;
 }

@@ -212,6 +212,38 @@ def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, sk
     assert np.array_equal(_np(bp.item_short), short_off[items])
 
 
+@pytest.mark.parametrize("num_keys,num_edges", [(4096, 98304), (50_000, 1_000_000), (7, 5)])
+def test_async_csr_plan_computes_before_its_counts_are_read(num_keys: int, num_edges: int) -> None:
+    """A plan whose build returned after validation (statistics still on the
+    device) gives the same results as a fully built one; reading the counts
+    afterwards gives the same statistics."""
+
+    from relmo_amd import capi
+
+    _log(f"async csr plan keys={num_keys} edges={num_edges}")
+    rng = np.random.default_rng(num_keys)
+    keys = np.minimum(rng.pareto(0.7, num_edges).astype(np.int64), num_keys - 1)
+    table = _t(rng.standard_normal((num_edges, 32)).astype(np.float32))
+    kt = _t(keys)
+    sync = capi.csr_plan(kt, num_keys, None, num_edges)
+    fast = capi.csr_plan(kt, num_keys, None, num_edges, wait_counts=False)
+    p = fast.plan
+    assert (p.max_degree, p.num_hubs, p.num_chunks, p.num_multi_hubs, p.num_items, p.num_short) == (-1,) * 6
+    assert p.gather_identity == 1 and p.counts
+    for mode in (0, 1):
+        want = capi.plan_segment_reduce(sync, table, mode)
+        got = capi.plan_segment_reduce(fast, table, mode)
+        assert np.array_equal(_np(got), _np(want), equal_nan=True), mode
+    capi.read_counts(fast, kt)
+    q = sync.plan
+    assert (p.max_degree, p.num_hubs, p.num_chunks, p.num_multi_hubs, p.num_items, p.num_short) == \
+        (q.max_degree, q.num_hubs, q.num_chunks, q.num_multi_hubs, q.num_items, q.num_short)
+    bad = keys.copy()
+    bad[num_edges // 2] = num_keys
+    with pytest.raises((RuntimeError, ValueError), match=rf"key index out of bounds: {num_keys} not in"):
+        capi.csr_plan(_t(bad), num_keys, None, num_edges, wait_counts=False)
+
+
 def test_inverse_plan_matches_oracle() -> None:
     from relmo_amd import capi
 
