@@ -172,6 +172,18 @@ __device__ __forceinline__ uint32_t hist_total(const uint32_t* h) {
 // indices equal to their edge ids (or no gathers) are common; a tile made of
 // those only is flagged in tile_plain instead of written, and the first
 // scatter generates its values.
+using i64x2 = int64_t __attribute__((ext_vector_type(2)));
+using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+
+// One index checked against its bound: the narrowed value (0 if bad), the
+// smallest bad edge so far.
+__device__ __forceinline__ uint32_t narrow_index(int64_t v, int64_t bound, int64_t p,
+                                                 unsigned long long& bad) {
+    const bool ok = static_cast<uint64_t>(v) < static_cast<uint64_t>(bound);
+    bad = ok ? bad : min(bad, static_cast<unsigned long long>(p));
+    return ok ? static_cast<uint32_t>(v) : 0u;
+}
+
 __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
     const int64_t* __restrict__ keys, const int64_t* __restrict__ gathers, int64_t n, int shift,
     int bits, int64_t key_bound, int64_t gather_bound, uint32_t* __restrict__ keys32,
@@ -184,42 +196,71 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
     unsigned long long bad_k = kNoEdge, bad_g = kNoEdge;
     uint32_t key[kSortItems], val[kSortItems];
     int mismatch = 0;
+    // Full tiles of 16-byte aligned arrays: thread t owns the element pairs
+    // 2 * (i * 256 + t) + {0, 1}, read as 16-byte streaming loads and written
+    // as 8-byte stores.  The last, partial tile (or unaligned arrays) go
+    // element by element.
+    const bool full = base + kSortTile <= n &&
+                      ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(gathers)) & 15u) == 0;
+    constexpr int kPairs = kSortItems / 2;
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
-        key[i] = 0;
-        val[i] = 0;
-        if (p < n) {
-            const int64_t k = keys[p];
-            if (static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound))
-                bad_k = min(bad_k, static_cast<unsigned long long>(p));
-            else
-                key[i] = static_cast<uint32_t>(k);
-            if (gathers != nullptr) {
-                const int64_t g = gathers[p];
-                if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound))
-                    bad_g = min(bad_g, static_cast<unsigned long long>(p));
-                else
-                    val[i] = static_cast<uint32_t>(g);
-                mismatch |= g != p ? 1 : 0;
+        for (int i = 0; i < kPairs; ++i) {
+            const int64_t p = base + 2 * (static_cast<int64_t>(i) * kSortThreads + threadIdx.x);
+            const i64x2 k2 = __builtin_nontemporal_load(reinterpret_cast<const i64x2*>(keys + p));
+            key[2 * i] = narrow_index(k2.x, key_bound, p, bad_k);
+            key[2 * i + 1] = narrow_index(k2.y, key_bound, p + 1, bad_k);
+            val[2 * i] = val[2 * i + 1] = 0;
+        }
+        if (gathers != nullptr) {
+#pragma unroll
+            for (int i = 0; i < kPairs; ++i) {
+                const int64_t p = base + 2 * (static_cast<int64_t>(i) * kSortThreads + threadIdx.x);
+                const i64x2 g2 =
+                    __builtin_nontemporal_load(reinterpret_cast<const i64x2*>(gathers + p));
+                val[2 * i] = narrow_index(g2.x, gather_bound, p, bad_g);
+                val[2 * i + 1] = narrow_index(g2.y, gather_bound, p + 1, bad_g);
+                mismatch |= (g2.x != p) | (g2.y != p + 1);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kSortItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+            key[i] = 0;
+            val[i] = 0;
+            if (p < n) {
+                key[i] = narrow_index(keys[p], key_bound, p, bad_k);
+                if (gathers != nullptr) {
+                    const int64_t g = gathers[p];
+                    val[i] = narrow_index(g, gather_bound, p, bad_g);
+                    mismatch |= g != p ? 1 : 0;
+                }
             }
         }
     }
     // block-wide: does any gathered index differ from its edge id?  (also the
     // barrier after clearing h)
     const int any = __syncthreads_or(mismatch);
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
-        if (p < n) {
-            keys32[p] = key[i];
-            if (any) vals32[p] = val[i];
+        for (int i = 0; i < kPairs; ++i) {
+            const int64_t p = base + 2 * (static_cast<int64_t>(i) * kSortThreads + threadIdx.x);
+            *reinterpret_cast<u32x2*>(keys32 + p) = u32x2{key[2 * i], key[2 * i + 1]};
+            if (any) *reinterpret_cast<u32x2*>(vals32 + p) = u32x2{val[2 * i], val[2 * i + 1]};
         }
-    }
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
-        if (p < n) hist_add(h, (key[i] >> shift) & dmask);
+        for (int i = 0; i < kSortItems; ++i) hist_add(h, (key[i] >> shift) & dmask);
+    } else {
+#pragma unroll
+        for (int i = 0; i < kSortItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+            if (p < n) {
+                keys32[p] = key[i];
+                if (any) vals32[p] = val[i];
+                hist_add(h, (key[i] >> shift) & dmask);
+            }
+        }
     }
     if (bad_k != kNoEdge) atomicMin(&st->bad_key_edge, bad_k);
     if (bad_g != kNoEdge) atomicMin(&st->bad_gather_edge, bad_g);
