@@ -139,6 +139,11 @@ struct SumOp {
     Pack<T, V> acc;
 
     __device__ __forceinline__ void begin(int64_t, bool) { acc = pack_fill<T, V>(T(0)); }
+    // Starts a new segment when `head` (branch-free).
+    __device__ __forceinline__ void restart(bool head, int64_t) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc.v[i] = head ? T(0) : acc.v[i];
+    }
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -177,6 +182,13 @@ struct LseOp {
         m = pack_fill<T, V>(neg_inf<T>());
         s = pack_fill<T, V>(T(0));
     }
+    __device__ __forceinline__ void restart(bool head, int64_t) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            m.v[i] = head ? neg_inf<T>() : m.v[i];
+            s.v[i] = head ? T(0) : s.v[i];
+        }
+    }
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -210,9 +222,12 @@ struct LseOp {
     __device__ __forceinline__ void add(int u) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
+            // exp(-|x - m|) is exp(m - x) when x raises the maximum, exp(x - m)
+            // otherwise; a -inf message adds 0 (its difference may be NaN)
             const T xv = x[u].v[i];
             const bool up = xv > m.v[i];
-            const T e = xv == neg_inf<T>() ? T(0) : fast_exp<T>(up ? m.v[i] - xv : xv - m.v[i]);
+            const T d = xv - m.v[i];
+            const T e = xv == neg_inf<T>() ? T(0) : fast_exp<T>(-fabs(d));
             s.v[i] = up ? s.v[i] * e + T(1) : s.v[i] + e;
             m.v[i] = up ? xv : m.v[i];
         }
@@ -253,6 +268,9 @@ struct LseBwdOp {
     __device__ __forceinline__ void begin(int64_t key, bool nonempty) {
         acc = pack_fill<T, V>(T(0));
         xr = (colok && nonempty) ? pack_load<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
+    }
+    __device__ __forceinline__ void restart(bool head, int64_t key) {
+        if (head) begin(key, true);
     }
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
 #pragma unroll
@@ -354,12 +372,15 @@ __global__ __launch_bounds__(kThreads) void k_fill(T* __restrict__ p, int64_t n,
 // takes R consecutive items, one per row group.  Their keys are consecutive and
 // so are their short segments (short_gather leaves the hub segments out), so
 // the workgroup first stages its short offsets and gathered row indices in LDS
-// with coalesced loads; after that the only global loads of a group are its
-// message rows.  Each group feeds its messages in batches of U that may span
-// several keys, adds every message to its key in edge order and stores a key
-// once its last message is in.  Keys without short messages (empty segments
-// and hubs) get the empty-segment result: hub rows are written again by the
-// hub kernels, which run after this one on the same stream.
+// with coalesced loads, and labels every staged message with its key (the
+// segment heads are marked, then a block-wide running maximum fills the
+// labels in).  Keys without short messages (empty segments and hubs) get the
+// empty-segment result from a block-wide pass: hub rows are written again by
+// the hub kernels, which run after this one on the same stream.  Each group
+// then feeds its item's messages in batches of U in edge order; a message
+// whose label differs from the previous one restarts the accumulator and one
+// whose label differs from the next one stores its key's result - no
+// per-key loop, so the row groups of a wave stay in step.
 template <typename T, int V, int G, class Op>
 __global__ __launch_bounds__(kThreads) void k_walk_items(
     const int32_t* __restrict__ short_off, const int32_t* __restrict__ short_gather,
@@ -371,8 +392,12 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
     // short messages (the last key may weigh up to kHubThreshold + 1)
     constexpr int kKeyCap = R * kItemSize + 2;
     constexpr int kPosCap = R * kItemSize + kHubThreshold + 1;
+    constexpr int PI = (kPosCap + kThreads - 1) / kThreads;  // staged positions per thread
+    constexpr int KI = (kKeyCap + kThreads - 1) / kThreads;
     __shared__ int32_t s_off[kKeyCap];
     __shared__ int32_t s_idx[kPosCap];
+    __shared__ uint16_t s_key[kThreads * PI];  // labels; thread t scans [t * PI, t * PI + PI)
+    __shared__ uint32_t s_scan[kThreads / kWave];
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int grp = static_cast<int>(threadIdx.x) / G;
     op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
@@ -389,10 +414,8 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
         const int64_t bs0 = clamp64(item_short[ib], 0, num_short);
         const int64_t bs1 = clamp64(item_short[ie], bs0, num_short);
         const int64_t item = ib + grp;
-        int64_t kb = bk1, ke = bk1, sb = bs1, se = bs1;
+        int64_t sb = bs1, se = bs1;
         if (item < ie) {
-            kb = clamp64(item_first[item], bk0, bk1);
-            ke = clamp64(item_first[item + 1], kb, bk1);
             sb = clamp64(item_short[item], bs0, bs1);
             se = clamp64(item_short[item + 1], sb, bs1);
         }
@@ -401,8 +424,6 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
         // corrupt plan inside LDS.  All loads are issued before the first write.
         const int nk = static_cast<int>(bk1 - bk0 + 1 < kKeyCap ? bk1 - bk0 + 1 : kKeyCap);
         const int np = static_cast<int>(bs1 - bs0 < kPosCap ? bs1 - bs0 : kPosCap);
-        constexpr int KI = (kKeyCap + kThreads - 1) / kThreads;
-        constexpr int PI = (kPosCap + kThreads - 1) / kThreads;
         int32_t tk[KI], tp[PI];
 #pragma unroll
         for (int j = 0; j < KI; ++j) {
@@ -420,52 +441,95 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
             const int i = static_cast<int>(threadIdx.x) + j * kThreads;
             if (i < nk) s_off[i] = tk[j];
         }
+        // labels start at 0; thread t owns positions [t * PI, t * PI + PI)
 #pragma unroll
         for (int j = 0; j < PI; ++j) {
             const int i = static_cast<int>(threadIdx.x) + j * kThreads;
             if (i < np) s_idx[i] = tp[j];
+            s_key[static_cast<int>(threadIdx.x) * PI + j] = 0;
         }
         __syncthreads();
-        if (kb >= ke) continue;
-        auto soff = [&](int64_t k) -> int64_t {
-            const int64_t i = k - bk0;
-            return s_off[i < kKeyCap ? i : kKeyCap - 1];
-        };
-        auto sidx = [&](int64_t p) -> int32_t {
-            const int64_t i = p - bs0;
-            return s_idx[i < kPosCap ? i : kPosCap - 1];
-        };
-        int64_t cur = kb;
-        int64_t cur_beg = sb;
-        int64_t cur_end = clamp64(soff(kb + 1), sb, se);
-        op.begin(cur, cur_end > cur_beg);
-        for (int64_t q = sb; q < se; q += U) {
-            const int cnt = static_cast<int>(se - q < U ? se - q : U);
-            int32_t idx[U];
+        // segment heads: the first staged position of each key with short
+        // messages carries the key's offset from bk0 (keys with several
+        // heads at one position cannot occur: a head needs a message)
 #pragma unroll
-            for (int u = 0; u < U; ++u) idx[u] = sidx(q + (u < cnt ? u : cnt - 1));
+        for (int j = 0; j < KI; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + j * kThreads;
+            if (i + 1 < nk) {
+                const int64_t a = static_cast<int64_t>(s_off[i]) - bs0;
+                const int64_t b = static_cast<int64_t>(s_off[i + 1]) - bs0;
+                if (b > a && a >= 0 && a < np) s_key[a] = static_cast<uint16_t>(i);
+            }
+        }
+        __syncthreads();
+        // running maximum over positions: each position gets its key's label
+        {
+            uint32_t v[PI];
+            uint32_t run = 0;
+#pragma unroll
+            for (int j = 0; j < PI; ++j) {
+                v[j] = s_key[static_cast<int>(threadIdx.x) * PI + j];
+                run = v[j] > run ? v[j] : run;
+            }
+            // exclusive block maximum of the per-thread maxima
+            const int lane = lane_id();
+            uint32_t x = run;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const uint32_t y = __shfl_up(x, o, kWave);
+                if (lane >= o) x = y > x ? y : x;
+            }
+            if (lane == kWave - 1) s_scan[threadIdx.x / kWave] = x;
+            uint32_t before = __shfl_up(x, 1, kWave);
+            if (lane == 0) before = 0;
+            __syncthreads();
+            const int wave = static_cast<int>(threadIdx.x) / kWave;
+#pragma unroll
+            for (int w = 0; w < kThreads / kWave; ++w) {
+                const uint32_t t = s_scan[w];
+                if (w < wave) before = t > before ? t : before;
+            }
+            uint32_t cur = before;
+#pragma unroll
+            for (int j = 0; j < PI; ++j) {
+                cur = v[j] > cur ? v[j] : cur;
+                s_key[static_cast<int>(threadIdx.x) * PI + j] = static_cast<uint16_t>(cur);
+            }
+        }
+        __syncthreads();
+        // keys without short messages: the empty-segment result
+        for (int64_t k = bk0 + grp; k < bk1; k += R) {
+            const int i = static_cast<int>(k - bk0 < kKeyCap - 1 ? k - bk0 : kKeyCap - 2);
+            if (s_off[i + 1] == s_off[i] && op.colok) pack_store_stream<T, V>(out + k * D + op.col, op.empty());
+        }
+        // the item's messages [sb, se), as staged positions [lb, le)
+        const int lb = static_cast<int>(sb - bs0 < np ? sb - bs0 : np);
+        const int le = static_cast<int>(se - bs0 < np ? se - bs0 : np);
+        int prev = -1;
+        for (int q = lb; q < le; q += U) {
+            const int cnt = le - q < U ? le - q : U;
+            int32_t idx[U];
+            int lab[U + 1];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int at = q + (u < cnt ? u : cnt - 1);
+                idx[u] = s_idx[at];
+                lab[u] = s_key[at];
+            }
+            lab[U] = q + cnt < le ? static_cast<int>(s_key[q + cnt]) : -1;
             op.load(idx, cnt);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (u < cnt) {
-                    while (q + u >= cur_end && cur + 1 < ke) {
-                        if (op.colok) pack_store_stream<T, V>(out + cur * D + op.col, op.result(cur_end > cur_beg));
-                        ++cur;
-                        cur_beg = cur_end;
-                        cur_end = clamp64(soff(cur + 1), cur_beg, se);
-                        op.begin(cur, cur_end > cur_beg);
-                    }
+                    const int next = u + 1 < cnt ? lab[u + 1] : lab[U];
+                    const int64_t key = bk0 + lab[u];
+                    op.restart(lab[u] != prev, key);
                     op.add(u);
+                    if (next != lab[u] && op.colok)
+                        pack_store_stream<T, V>(out + key * D + op.col, op.result(true));
+                    prev = lab[u];
                 }
             }
-        }
-        // the key of the last message and the keys after it
-        for (;;) {
-            if (op.colok) pack_store_stream<T, V>(out + cur * D + op.col, op.result(cur_end > cur_beg));
-            if (++cur >= ke) break;
-            cur_beg = cur_end;
-            cur_end = clamp64(soff(cur + 1), cur_beg, se);
-            op.begin(cur, cur_end > cur_beg);
         }
     }
 }
