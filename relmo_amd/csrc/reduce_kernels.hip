@@ -228,7 +228,7 @@ struct LseOp {
             const bool up = xv > m.v[i];
             const T d = xv - m.v[i];
             const T e = xv == neg_inf<T>() ? T(0) : fast_exp<T>(-fabs(d));
-            s.v[i] = up ? s.v[i] * e + T(1) : s.v[i] + e;
+            s.v[i] = up ? fma(s.v[i], e, T(1)) : s.v[i] + e;
             m.v[i] = up ? xv : m.v[i];
         }
     }
@@ -240,7 +240,7 @@ struct LseOp {
         for (int i = 0; i < V; ++i) {
             if (!nonempty)
                 r.v[i] = neg_inf<T>();
-            else if (m.v[i] == neg_inf<T>() || m.v[i] == -neg_inf<T>())
+            else if (__builtin_isinf(m.v[i]))
                 r.v[i] = quiet_nan<T>();
             else
                 r.v[i] = dev_log<T>(s.v[i]) + m.v[i];
