@@ -578,14 +578,17 @@ __global__ __launch_bounds__(kThreads) void k_hub_chunks(
     op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     op.colok = op.col < op.D;
     const int64_t D = op.D;
-    constexpr int64_t kPer = (kChunkSize + NG - 1) / NG;
     const int64_t num_hubs = pc->num_hubs;
     const int64_t num_chunks = pc->num_chunks;
     for (int64_t c = blockIdx.x; c < num_chunks; c += gridDim.x) {
         const HubChunk hc =
             hub_chunk(c, offsets, hub_key, hub_chunk_base, chunk_hub, num_hubs, num_edges);
-        const int64_t lo = hc.ok ? clamp64(hc.beg + grp * kPer, hc.beg, hc.end) : 0;
-        const int64_t hi = hc.ok ? clamp64(lo + kPer, lo, hc.end) : 0;
+        // the chunk's messages split evenly over the row groups in whole
+        // batches (a hub of one short chunk still uses every group)
+        const int64_t len = hc.ok ? hc.end - hc.beg : 0;
+        const int64_t per = ((len + NG * U - 1) / (NG * U)) * U;
+        const int64_t lo = hc.ok ? clamp64(hc.beg + grp * per, hc.beg, hc.end) : 0;
+        const int64_t hi = hc.ok ? clamp64(lo + per, lo, hc.end) : 0;
         op.begin(hc.key, hc.ok && hi > lo);
         Window<G, 4> gw;
         gw.base = -(int64_t(1) << 40);
