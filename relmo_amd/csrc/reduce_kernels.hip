@@ -313,51 +313,6 @@ __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// W*G consecutive int32 values starting at `base`; lane l of the group holds
-// elements base + w*G + l.  get() must be called by the whole group with the
-// same index.
-template <int G, int W>
-struct Window {
-    int64_t base;
-    int32_t v[W];
-    __device__ __forceinline__ void fill(const int32_t* __restrict__ src, int64_t b, int64_t n,
-                                         int32_t pad, int gl) {
-        base = b;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const int64_t i = b + w * G + gl;
-            v[w] = i < n ? src[i] : pad;
-        }
-    }
-    __device__ __forceinline__ bool covers(int64_t i, int64_t cnt) const {
-        return i >= base && i + cnt <= base + W * G;
-    }
-    __device__ __forceinline__ int32_t get(int64_t i) const {
-        const int sidx = static_cast<int>(i - base);
-        const int w = sidx / G;
-        int32_t x = v[0];
-#pragma unroll
-        for (int ww = 1; ww < W; ++ww) x = w == ww ? v[ww] : x;
-        return __shfl(x, sidx & (G - 1), G);
-    }
-};
-
-// Feeds positions [beg, end) of `gs` to `op` in batches of U, in order
-// (single-key batches: op.consume).
-template <int G, int U, class Op>
-__device__ __forceinline__ void feed(Op& op, const int32_t* __restrict__ gs, int64_t num_edges,
-                                     int64_t beg, int64_t end, Window<G, 4>& gw, int gl) {
-    for (int64_t p = beg; p < end; p += U) {
-        const int cnt = static_cast<int>(end - p < U ? end - p : U);
-        if (!gw.covers(p, cnt)) gw.fill(gs, p, num_edges, 0, gl);
-        int32_t idx[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) idx[u] = gw.get(p + (u < cnt ? u : cnt - 1));
-        op.load(idx, cnt);
-        op.consume(cnt);
-    }
-}
-
 // ---- kernels -------------------------------------------------------------
 
 template <typename T>
@@ -561,7 +516,13 @@ __device__ __forceinline__ HubChunk hub_chunk(int64_t c, const int32_t* __restri
     return hc;
 }
 
-// One workgroup per hub chunk: row group g folds slice g of the chunk, the
+// LDS slot of staged chunk position p: one pad word per 32 positions, so the
+// row groups of a wave, which read positions a slice length apart, hit
+// different banks.
+__device__ __forceinline__ int hub_slot(int p) { return p + (p >> 5); }
+
+// One workgroup per hub chunk: the chunk's gathered row indices are staged in
+// LDS with coalesced loads, row group g folds slice g of the chunk, the
 // slices are folded in order by group 0; a single-chunk hub is finished here.
 template <typename T, int V, int G, class Op>
 __global__ __launch_bounds__(kThreads) void k_hub_chunks(
@@ -572,7 +533,9 @@ __global__ __launch_bounds__(kThreads) void k_hub_chunks(
     using Partial = typename Op::Partial;
     constexpr int NG = kThreads / G;
     constexpr int U = batch_rows<G>();
-    __shared__ Partial red[kThreads];
+    constexpr int kStage = (kChunkSize + kThreads - 1) / kThreads;  // staged indices per thread
+    __shared__ Partial red[kThreads / kWave * G];
+    __shared__ int32_t s_gs[kChunkSize + kChunkSize / 32];
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int grp = static_cast<int>(threadIdx.x) / G;
     op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
@@ -583,16 +546,35 @@ __global__ __launch_bounds__(kThreads) void k_hub_chunks(
     for (int64_t c = blockIdx.x; c < num_chunks; c += gridDim.x) {
         const HubChunk hc =
             hub_chunk(c, offsets, hub_key, hub_chunk_base, chunk_hub, num_hubs, num_edges);
+        const int len = hc.ok ? static_cast<int>(hc.end - hc.beg) : 0;  // <= kChunkSize
+        {
+            int32_t t[kStage];
+#pragma unroll
+            for (int j = 0; j < kStage; ++j) {
+                const int i = static_cast<int>(threadIdx.x) + j * kThreads;
+                t[j] = i < len ? gs[hc.beg + i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < kStage; ++j) {
+                const int i = static_cast<int>(threadIdx.x) + j * kThreads;
+                if (i < len) s_gs[hub_slot(i)] = t[j];
+            }
+        }
+        __syncthreads();
         // the chunk's messages split evenly over the row groups in whole
         // batches (a hub of one short chunk still uses every group)
-        const int64_t len = hc.ok ? hc.end - hc.beg : 0;
-        const int64_t per = ((len + NG * U - 1) / (NG * U)) * U;
-        const int64_t lo = hc.ok ? clamp64(hc.beg + grp * per, hc.beg, hc.end) : 0;
-        const int64_t hi = hc.ok ? clamp64(lo + per, lo, hc.end) : 0;
+        const int per = ((len + NG * U - 1) / (NG * U)) * U;
+        const int lo = min(grp * per, len);
+        const int hi = min(lo + per, len);
         op.begin(hc.key, hc.ok && hi > lo);
-        Window<G, 4> gw;
-        gw.base = -(int64_t(1) << 40);
-        feed<G, U>(op, gs, num_edges, lo, hi, gw, gl);
+        for (int q = lo; q < hi; q += U) {
+            const int cnt = hi - q < U ? hi - q : U;
+            int32_t idx[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) idx[u] = s_gs[hub_slot(q + (u < cnt ? u : cnt - 1))];
+            op.load(idx, cnt);
+            op.consume(cnt);
+        }
         // Fold the slices: a shuffle tree over the groups of each wave, then
         // the waves in order.
         Partial pg = hi > lo ? op.partial() : Partial::identity();
