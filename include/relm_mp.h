@@ -136,16 +136,18 @@ int relm_mp_fanin_reduce_logsumexp_backward(int dtype, const void* grad_out, int
 
 enum relm_mp_plan_kind { RELM_MP_PLAN_INVERSE = 1, RELM_MP_PLAN_CSR = 2 };
 
-/* Statistics of a CSR plan as the build's kernels write them into plan
- * memory.  They are valid in stream order after the build, so compute entry
- * points read them there and a plan is usable before the host has them. */
+/* Statistics of a plan as the build's kernels write them into plan memory.
+ * They are valid in stream order after the build, so compute entry points
+ * read them there and a plan is usable before the host has them. */
 typedef struct relm_mp_plan_counts {
-    int64_t max_degree;
+    int64_t max_degree;      /* CSR plans */
     int64_t num_hubs;
     int64_t num_chunks;
     int64_t num_multi_hubs;
     int64_t num_items;
     int64_t num_short;
+    int64_t collisions;      /* inverse plans */
+    int64_t identity;        /* inverse plans: 1 if keys[e] == e for every edge */
 } relm_mp_plan_counts;
 
 /* Descriptor of a plan.  All pointers point into the caller's plan memory.
@@ -179,7 +181,7 @@ typedef struct relm_mp_plan {
     int32_t* item_short;     /* CSR: [num_items + 1] short_off[item_first[j]]  */
     int32_t* short_off;      /* CSR: [num_keys + 1] edges of non-hub segments before each key */
     int32_t* short_gather;   /* CSR: [num_short] gather_sorted without the hub segments */
-    const relm_mp_plan_counts* counts; /* CSR: the statistics, in device memory */
+    const relm_mp_plan_counts* counts; /* the statistics, in device memory */
 } relm_mp_plan;
 
 /* Inverse plan: inv[k] = largest e with keys[e] == k, or -1 (plan->inv is
@@ -193,6 +195,26 @@ int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* k
                            const int64_t* gathers, int64_t gather_bound, const char* gather_name,
                            int gather_checked_first, int64_t num_edges, void* plan_mem,
                            size_t plan_bytes, relm_mp_plan* plan, relm_mp_stream_t stream);
+/* The same build without waiting: the validation result is pending until
+ * relm_mp_plan_validate(plan).  Meanwhile relm_mp_plan_gather_last may be
+ * enqueued on the plan (its kernels read the identity flag from
+ * plan->counts; bad indices never make them access memory out of bounds),
+ * but its result is only valid once relm_mp_plan_validate returns OK.
+ * collisions is -1 until then, and `keys` / `gathers` must stay valid until
+ * then (a bad index's value is read back for the message).  One validation
+ * may be pending per host thread and device; a plan build on that thread
+ * fails until it is done.
+ * No counterpart in the reference: it lets fanout_scatter enqueue its gather
+ * before the host waits for the index check. */
+int relm_mp_inv_plan_build_async(const int64_t* keys, int64_t key_bound, const char* key_name,
+                                 const int64_t* gathers, int64_t gather_bound,
+                                 const char* gather_name, int gather_checked_first,
+                                 int64_t num_edges, void* plan_mem, size_t plan_bytes,
+                                 relm_mp_plan* plan, relm_mp_stream_t stream);
+/* Waits for the pending validation of `plan` (relm_mp_inv_plan_build_async)
+ * and reports it like relm_mp_inv_plan_build; fills collisions and sets
+ * inv to NULL for the identity.  Returns OK at once if nothing is pending. */
+int relm_mp_plan_validate(relm_mp_plan* plan);
 
 /* CSR plan: stable counting order of the edges by key (edge order kept inside
  * each segment), offsets, the gathered row of every edge in that order, and the

@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "relm_mp_fanin_reduce_logsumexp_backward",
     "relm_mp_inv_plan_bytes",
     "relm_mp_inv_plan_build",
+    "relm_mp_inv_plan_build_async",
+    "relm_mp_plan_validate",
     "relm_mp_csr_plan_bytes",
     "relm_mp_csr_plan_scratch_bytes",
     "relm_mp_csr_plan_build",
@@ -115,6 +117,8 @@ _SIGNATURES = {
     ),
     "relm_mp_inv_plan_bytes": (_sz, [_i64]),
     "relm_mp_inv_plan_build": (_int, [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _PP, _vp]),
+    "relm_mp_inv_plan_build_async": (_int, [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _PP, _vp]),
+    "relm_mp_plan_validate": (_int, [_PP]),
     "relm_mp_csr_plan_bytes": (_sz, [_i64, _i64]),
     "relm_mp_csr_plan_scratch_bytes": (_sz, [_i64, _i64]),
     "relm_mp_csr_plan_build": (
@@ -346,18 +350,30 @@ class BuiltPlan:
 
 
 def inv_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, gather_bound: int,
-             key_name: str = "key", gather_name: str = "gather", gather_first: bool = False) -> BuiltPlan:
+             key_name: str = "key", gather_name: str = "gather", gather_first: bool = False,
+             wait: bool = True) -> BuiltPlan:
+    """Inverse plan; with wait=False the validation stays pending until validate()."""
+
     _check_index(keys)
     mem = _bytes(lib().relm_mp_inv_plan_bytes(key_bound), keys)
     plan = Plan()
+    build = lib().relm_mp_inv_plan_build if wait else lib().relm_mp_inv_plan_build_async
+    # the names must outlive a pending validation: keep them on the plan
+    names = (key_name.encode(), gather_name.encode())
     check(
-        lib().relm_mp_inv_plan_build(
-            _ptr(keys), key_bound, key_name.encode(), _ptr(gathers), gather_bound,
-            gather_name.encode(), int(gather_first), keys.numel(), _ptr(mem), mem.numel(),
+        build(
+            _ptr(keys), key_bound, names[0], _ptr(gathers), gather_bound,
+            names[1], int(gather_first), keys.numel(), _ptr(mem), mem.numel(),
             ctypes.byref(plan), _stream(keys),
         )
     )
-    return BuiltPlan(plan, mem)
+    bp = BuiltPlan(plan, mem)
+    bp.names = names
+    return bp
+
+
+def validate(bp: BuiltPlan) -> None:
+    check(lib().relm_mp_plan_validate(ctypes.byref(bp.plan)))
 
 
 def csr_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, gather_bound: int,

@@ -101,13 +101,36 @@ int finish_validation(const DevStatus* dst, DevStatus& host, const int64_t* keys
 // Per host thread and device: pinned host copies of a plan status and plan
 // counts, and an event marking when the status copy has landed.  A build
 // waits for its own event before returning, so one slot per thread suffices.
+// An index validation whose result has not been read yet (inverse plans
+// built without waiting): what the error message needs.
+struct PendingCheck {
+    bool active = false;
+    const void* plan_counts = nullptr;  // identifies the plan
+    const int64_t* keys = nullptr;
+    int64_t key_bound = 0;
+    std::string key_name;
+    const int64_t* gathers = nullptr;
+    int64_t gather_bound = 0;
+    std::string gather_name;
+    int gather_checked_first = 0;
+};
+
 struct HostSlot {
     int device = -1;
     hipEvent_t ready = nullptr;
     DevStatus* status = nullptr;         // host address
     DevStatus* status_mapped = nullptr;  // the same memory as the device addresses it
     relm_mp_plan_counts* counts = nullptr;
+    PendingCheck pending;
 };
+
+int no_pending(const HostSlot* hs) {
+    if (hs->pending.active)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: a plan built without waiting has not been validated yet "
+                         "(relm_mp_plan_validate)");
+    return RELM_MP_OK;
+}
 
 int host_slot(HostSlot** out) {
     thread_local HostSlot slots[16];
@@ -161,6 +184,7 @@ int read_counts(relm_mp_plan* plan, hipStream_t s) {
 
 struct InvLayout {
     DevStatus* status;
+    relm_mp_plan_counts* counts;
     int32_t* inv;
     size_t bytes;
 };
@@ -169,6 +193,7 @@ InvLayout inv_layout(void* mem, int64_t num_keys) {
     Carver c(mem);
     InvLayout l;
     l.status = c.take<DevStatus>(1);
+    l.counts = c.take<relm_mp_plan_counts>(1);
     l.inv = c.take<int32_t>(static_cast<size_t>(num_keys));
     l.bytes = c.used();
     return l;
@@ -243,9 +268,17 @@ size_t hub_partial_upper_bound(int64_t num_edges, int64_t emb, int dtype, int64_
                     256);
 }
 
+// Fills the host-side statistics of a validated inverse plan.
+void finish_inverse(relm_mp_plan* plan, const DevStatus& host) {
+    plan->collisions = static_cast<int64_t>(host.collisions);
+    // keys[e] == e for every edge: the map is the identity, which the compute
+    // kernels apply without reading inv (one dependent load less per row)
+    if (host.key_mismatch == 0) plan->inv = nullptr;
+}
+
 int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, const int64_t* gathers,
               int64_t gather_bound, const char* gather_name, int gather_checked_first,
-              int64_t num_edges, void* plan_mem, size_t plan_bytes, relm_mp_plan* plan,
+              int64_t num_edges, void* plan_mem, size_t plan_bytes, relm_mp_plan* plan, bool wait,
               hipStream_t s) {
     RELM_TRY(check_rows(key_bound, "num_keys"));
     RELM_TRY(check_rows(num_edges, "num_edges"));
@@ -253,23 +286,56 @@ int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     const InvLayout l = inv_layout(plan_mem, key_bound);
     if (plan_mem == nullptr || plan_bytes < l.bytes)
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: inverse plan memory too small");
+    HostSlot* hs = nullptr;
+    RELM_TRY(host_slot(&hs));
+    RELM_TRY(no_pending(hs));
     std::memset(plan, 0, sizeof(*plan));
     plan->kind = RELM_MP_PLAN_INVERSE;
     plan->num_keys = key_bound;
     plan->num_edges = num_edges;
     plan->num_gather = gather_bound;
     plan->inv = l.inv;
+    plan->counts = l.counts;
+    plan->collisions = -1;
     RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
     RELM_HIP(launch_fill_i32(l.inv, key_bound, -1, s), "relm_mp fill");
     RELM_HIP(launch_inv_build(keys, key_bound, gathers, gather_bound, num_edges, l.inv, l.status, s),
              "relm_mp inverse plan kernel");
-    DevStatus host{};
-    RELM_TRY(finish_validation(l.status, host, keys, key_bound, key_name, gathers, gather_bound,
-                               gather_name, gather_checked_first, s));
-    plan->collisions = static_cast<int64_t>(host.collisions);
-    // keys[e] == e for every edge: the map is the identity, which the compute
-    // kernels apply without reading inv (one dependent load less per row)
-    if (host.key_mismatch == 0) plan->inv = nullptr;
+    RELM_HIP(launch_status_publish(l.status, hs->status_mapped, l.counts, s), "relm_mp status publish");
+    RELM_HIP(hipEventRecord(hs->ready, s), "relm_mp status event");
+    if (!wait) {
+        PendingCheck& p = hs->pending;
+        p.active = true;
+        p.plan_counts = l.counts;
+        p.keys = keys;
+        p.key_bound = key_bound;
+        p.key_name = key_name != nullptr ? key_name : "index";
+        p.gathers = gathers;
+        p.gather_bound = gather_bound;
+        p.gather_name = gather_name != nullptr ? gather_name : "index";
+        p.gather_checked_first = gather_checked_first;
+        return RELM_MP_OK;
+    }
+    RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
+    const DevStatus host = *hs->status;
+    RELM_TRY(check_validation(host, keys, key_bound, key_name, gathers, gather_bound, gather_name,
+                              gather_checked_first));
+    finish_inverse(plan, host);
+    return RELM_MP_OK;
+}
+
+// Waits for and reports the pending validation of `plan`, if there is one.
+int validate_pending(relm_mp_plan* plan) {
+    HostSlot* hs = nullptr;
+    RELM_TRY(host_slot(&hs));
+    PendingCheck& p = hs->pending;
+    if (!p.active || p.plan_counts != plan->counts) return RELM_MP_OK;
+    p.active = false;
+    RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
+    const DevStatus host = *hs->status;
+    RELM_TRY(check_validation(host, p.keys, p.key_bound, p.key_name.c_str(), p.gathers,
+                              p.gather_bound, p.gather_name.c_str(), p.gather_checked_first));
+    finish_inverse(plan, host);
     return RELM_MP_OK;
 }
 
@@ -288,6 +354,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR scratch memory too small");
     HostSlot* hs = nullptr;
     RELM_TRY(host_slot(&hs));
+    RELM_TRY(no_pending(hs));
     std::memset(plan, 0, sizeof(*plan));
     plan->kind = RELM_MP_PLAN_CSR;
     plan->hub_threshold = kHubThreshold;
@@ -313,7 +380,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     // The validation result is final after the first sort pass: copy it to
     // the host and mark the point, then enqueue the rest of the build.
     auto mark_validation = [&]() -> hipError_t {
-        hipError_t e = launch_status_publish(l.status, hs->status_mapped, s);
+        hipError_t e = launch_status_publish(l.status, hs->status_mapped, nullptr, s);
         return e != hipSuccess ? e : hipEventRecord(hs->ready, s);
     };
     if (num_edges > 0) {
@@ -387,8 +454,23 @@ int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* k
                            int gather_checked_first, int64_t num_edges, void* plan_mem,
                            size_t plan_bytes, relm_mp_plan* plan, relm_mp_stream_t stream) {
     return inv_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
-                     gather_checked_first, num_edges, plan_mem, plan_bytes, plan,
+                     gather_checked_first, num_edges, plan_mem, plan_bytes, plan, true,
                      static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_inv_plan_build_async(const int64_t* keys, int64_t key_bound, const char* key_name,
+                                 const int64_t* gathers, int64_t gather_bound,
+                                 const char* gather_name, int gather_checked_first,
+                                 int64_t num_edges, void* plan_mem, size_t plan_bytes,
+                                 relm_mp_plan* plan, relm_mp_stream_t stream) {
+    return inv_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
+                     gather_checked_first, num_edges, plan_mem, plan_bytes, plan, false,
+                     static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_plan_validate(relm_mp_plan* plan) {
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    return validate_pending(plan);
 }
 
 size_t relm_mp_csr_plan_bytes(int64_t num_keys, int64_t num_edges) {
@@ -493,9 +575,12 @@ int relm_mp_fanout_scatter(int dtype, const void* x_cat, int64_t x_rows, int64_t
     if (num_edges == 0 || out_rows == 0)
         return compute_fill(dtype, out, out_rows * emb, 0.0, s);
     relm_mp_plan plan;
+    // the gather is enqueued before the host waits for the index check
     RELM_TRY(inv_build(flat_dst, out_rows, "flat_dst", src_global_idx, x_rows, "src_global_idx", 1,
-                       num_edges, workspace, workspace_bytes, &plan, s));
-    return compute_gather_last(dtype, plan, src_global_idx, x_cat, emb, out, s);
+                       num_edges, workspace, workspace_bytes, &plan, false, s));
+    const int rc = compute_gather_last(dtype, plan, src_global_idx, x_cat, emb, out, s);
+    const int vrc = validate_pending(&plan);
+    return vrc != RELM_MP_OK ? vrc : rc;
 }
 
 size_t relm_mp_fanout_scatter_backward_workspace_size(int64_t num_edges, int64_t x_rows,
@@ -598,7 +683,7 @@ int relm_mp_fanin_reduce_sum_backward(int dtype, const void* grad_out, int64_t g
     const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows);
     relm_mp_plan plan;
     RELM_TRY(inv_build(flat_src, rel_rows, "flat_src", dst_idx, grad_out_rows, "dst_idx", 0,
-                       num_edges, workspace, inv_bytes, &plan, s));
+                       num_edges, workspace, inv_bytes, &plan, true, s));
     if (plan.collisions == 0)
         return compute_gather_last(dtype, plan, dst_idx, grad_out, emb, grad_rel, s);
     char* csr_mem = static_cast<char*>(workspace) + inv_bytes;
@@ -648,7 +733,7 @@ int relm_mp_fanin_reduce_logsumexp_backward(int dtype, const void* grad_out, int
     const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows);
     relm_mp_plan plan;
     RELM_TRY(inv_build(flat_src, key_bound, "flat_src", dst_idx, dim_size, "dst_idx", 1, num_edges,
-                       workspace, inv_bytes, &plan, s));
+                       workspace, inv_bytes, &plan, true, s));
     if (plan.collisions == 0)
         return compute_logsumexp_backward(dtype, plan, dst_idx, grad_out, out, rel_flat, emb,
                                           grad_rel, nullptr, 0, s);

@@ -58,8 +58,10 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // ---- plan kernels (plan_kernels.hip) -------------------------------------
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
 hipError_t launch_status_init(DevStatus* st, hipStream_t s);
-// Copies *st to pinned host memory through its device mapping.
-hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped, hipStream_t s);
+// Copies *st to pinned host memory through its device mapping; with `pc`,
+// also stores the inverse-plan statistics (collisions, identity) there.
+hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped,
+                                 relm_mp_plan_counts* pc, hipStream_t s);
 hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                             int64_t gather_bound, int64_t n, int32_t* inv, DevStatus* st,
                             hipStream_t s);

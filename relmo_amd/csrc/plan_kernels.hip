@@ -49,11 +49,16 @@ __global__ void k_status_init(DevStatus* st) {
 // Copies the status to host memory mapped for the device (vector stores).
 // The host reads it after an event recorded behind this kernel has
 // completed; the event's system-scope release makes the stores visible.
-__global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __restrict__ host) {
+__global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __restrict__ host,
+                                 relm_mp_plan_counts* __restrict__ pc) {
     constexpr int kWords = static_cast<int>(sizeof(DevStatus) / sizeof(unsigned long long));
     const int i = static_cast<int>(threadIdx.x);
     if (i < kWords)
         reinterpret_cast<unsigned long long*>(host)[i] = reinterpret_cast<const unsigned long long*>(st)[i];
+    if (pc != nullptr && i == 0) {
+        pc->collisions = static_cast<int64_t>(st->collisions);
+        pc->identity = st->key_mismatch == 0 ? 1 : 0;
+    }
 }
 
 // inv[k] = max e with keys[e] == k.  Every key and gathered index is checked;
@@ -646,8 +651,9 @@ hipError_t launch_status_init(DevStatus* st, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped, hipStream_t s) {
-    hipLaunchKernelGGL(k_status_publish, dim3(1), dim3(64), 0, s, st, host_mapped);
+hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped,
+                                 relm_mp_plan_counts* pc, hipStream_t s) {
+    hipLaunchKernelGGL(k_status_publish, dim3(1), dim3(64), 0, s, st, host_mapped, pc);
     return hipGetLastError();
 }
 

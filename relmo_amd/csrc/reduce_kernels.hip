@@ -678,8 +678,16 @@ __device__ __forceinline__ int32_t inverse_edge(const int32_t* __restrict__ inv,
 // out[r] = table[gathers[inv[r]]] or 0 (inverse plans: fanout forward and
 // injective sum backward).  Each row group keeps kRowsInFlight rows in flight:
 // rows key0 + j * ngroups, so neighbouring groups touch neighbouring rows.
+// The identity (keys[e] == e for every edge): plans read back by the host
+// have inv == NULL; plans still being validated carry the flag in counts.
+__device__ __forceinline__ const int32_t* inverse_map(const int32_t* inv,
+                                                      const relm_mp_plan_counts* pc) {
+    return pc != nullptr && pc->identity != 0 ? nullptr : inv;
+}
+
 template <typename T, int V, int G>
-__global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restrict__ inv,
+__global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restrict__ inv_in,
+                                                         const relm_mp_plan_counts* __restrict__ pc,
                                                          int64_t num_edges,
                                                          const int64_t* __restrict__ gathers,
                                                          int64_t num_gather,
@@ -691,6 +699,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
+    const int32_t* inv = inverse_map(inv_in, pc);
     const int64_t ngroups = static_cast<int64_t>(gridDim.x) * R;
     for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key0 < num_keys;
          key0 += ngroups * RU) {
@@ -741,7 +750,8 @@ __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __r
 // grad_rel[r] = grad_out[d] * exp(rel[r] - out[d]), d = gathers[inv[r]], or 0.
 template <typename T, int V, int G>
 __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
-    const int32_t* __restrict__ inv, int64_t num_edges, const int64_t* __restrict__ gathers,
+    const int32_t* __restrict__ inv_in, const relm_mp_plan_counts* __restrict__ pc,
+    int64_t num_edges, const int64_t* __restrict__ gathers,
     int64_t num_gather,
     const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
     int64_t num_keys, int64_t D, T* __restrict__ grad_rel) {
@@ -750,6 +760,7 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
+    const int32_t* inv = inverse_map(inv_in, pc);
     const int64_t ngroups = static_cast<int64_t>(gridDim.x) * R;
     for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key0 < num_keys;
          key0 += ngroups * RU) {
@@ -931,8 +942,8 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
             hipLaunchKernelGGL((k_gather_inv<T, V, G>),
                                row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
-                               dim3(kThreads), 0, s, plan.inv, plan.num_edges, gathers,
-                               plan.num_gather, table, plan.num_keys, emb, out);
+                               dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
+                               gathers, plan.num_gather, table, plan.num_keys, emb, out);
         } else {
             hipLaunchKernelGGL((k_gather_last_csr<T, V, G>), row_grid(plan.num_keys, G, geo.slices),
                                dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted,
@@ -984,8 +995,9 @@ int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void*
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
             hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G>),
                                row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
-                               dim3(kThreads), 0, s, plan.inv, plan.num_edges, gathers,
-                               plan.num_gather, grad_out, out, rel, plan.num_keys, emb, grad_rel);
+                               dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
+                               gathers, plan.num_gather, grad_out, out, rel, plan.num_keys, emb,
+                               grad_rel);
             return hip_error(hipGetLastError(), "relm_mp logsumexp backward kernel");
         }
         LseBwdOp<T, V, U> op{};

@@ -318,11 +318,26 @@ Tensor fanout_scatter_gpu(const Tensor& x_cat, const Tensor& src, const Tensor& 
     const Tensor s_idx = contiguous(src);
     const Tensor d_idx = contiguous(dst);
     hipStream_t stream = current_stream(x);
-    GpuPlan gp = inverse_plan(d_idx, out_rows, "flat_dst", s_idx, x.size(0), "src_global_idx",
-                              true, stream);
     Tensor out = at::empty({out_rows, emb}, x_cat.options());
-    raise_if(relm_mp_plan_gather_last(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
-                                      x.data_ptr(), emb, out.data_ptr(), stream));
+    PlanCache& cache = PlanCache::get();
+    GpuPlan gp;
+    if (cache.lookup(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), &gp.plan)) {
+        raise_if(relm_mp_plan_gather_last(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
+                                          x.data_ptr(), emb, out.data_ptr(), stream));
+        return out;
+    }
+    // The gather is enqueued before the host waits for the index check (the
+    // kernels stay in bounds on bad indices; the result is then discarded).
+    gp.mem = byte_buffer(relm_mp_inv_plan_bytes(out_rows), d_idx);
+    raise_if(relm_mp_inv_plan_build_async(d_idx.data_ptr<int64_t>(), out_rows, "flat_dst",
+                                          s_idx.data_ptr<int64_t>(), x.size(0), "src_global_idx", 1,
+                                          d_idx.numel(), gp.mem.data_ptr(),
+                                          static_cast<size_t>(gp.mem.numel()), &gp.plan, stream));
+    const int rc = relm_mp_plan_gather_last(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
+                                            x.data_ptr(), emb, out.data_ptr(), stream);
+    raise_if(relm_mp_plan_validate(&gp.plan));
+    raise_if(rc);
+    cache.insert(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), gp.mem, gp.plan);
     return out;
 }
 

@@ -262,6 +262,42 @@ def test_inverse_plan_matches_oracle() -> None:
         assert np.array_equal(_np(bp.inv), oracle.inverse_build(np.arange(n), k)[0])
 
 
+@pytest.mark.parametrize("identity", [True, False])
+def test_async_inverse_plan_gathers_before_validation(identity: bool) -> None:
+    """An inverse plan whose validation is still pending already serves the
+    gather (identity flag read on the device); validating gives the same
+    statistics as a waiting build, and a bad index is reported by validate."""
+
+    from relmo_amd import capi
+
+    rng = np.random.default_rng(5)
+    n, k, rows = 50_000, 60_000, 7000
+    keys = np.arange(n) if identity else rng.integers(0, k, n)
+    gathers = rng.integers(0, rows, n)
+    table = _t(rng.standard_normal((rows, 32)).astype(np.float32))
+    kt, gt = _t(keys), _t(gathers)
+    want_plan = capi.inv_plan(kt, k, gt, rows)
+    want = capi.plan_gather_last(want_plan, table, gt)
+    bp = capi.inv_plan(kt, k, gt, rows, wait=False)
+    assert bp.plan.collisions == -1 and bp.plan.inv
+    got = capi.plan_gather_last(bp, table, gt)
+    # a second build while a validation is pending is refused
+    with pytest.raises(RuntimeError, match="not been validated"):
+        capi.inv_plan(kt, k, gt, rows)
+    capi.validate(bp)
+    assert np.array_equal(_np(got), _np(want))
+    assert bp.plan.collisions == want_plan.plan.collisions
+    assert bool(bp.plan.inv) == bool(want_plan.plan.inv) == (not identity)
+    bad = gathers.copy()
+    bad[n // 3] = rows + 2
+    bt = _t(bad)  # the index arrays must live until validate() reads the bad value back
+    bp = capi.inv_plan(kt, k, bt, rows, gather_name="src_global_idx", wait=False)
+    capi.plan_gather_last(bp, table, bt)
+    with pytest.raises(RuntimeError, match=rf"src_global_idx index out of bounds: {rows + 2} not in \[0, {rows}\)\."):
+        capi.validate(bp)
+    capi.validate(bp)  # nothing pending any more
+
+
 def _segments_bounded(keys: np.ndarray, bound: int = 64) -> bool:
     return keys.size == 0 or np.bincount(keys).max() <= bound
 
