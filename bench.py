@@ -16,10 +16,11 @@ The JSON line also carries
   cpu_baseline  - the reference's own CPU op library (oracle/_ref) on a
                   bounded 1/8-scale sample of C2, on the host's cores;
   extra         - kernel-only rates with cached plans, C2 with sum, C3 fanout
-                  forward + backward, C1 latencies, C4 / C5 model training
-                  steps (graphs/sec).
+                  forward + backward, C1 latencies, the pack ops (index
+                  preparation) against their ATen formulation, C4 / C5 model
+                  training steps (graphs/sec).
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1|c4|c5|copy]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1|c4|c5|pack|copy]
 """
 
 from __future__ import annotations
@@ -261,6 +262,61 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
     return res
 
 
+def bench_pack(torch, steps: int) -> dict:
+    """Index preparation before one fanout / fanin call: fanout_pack_from_edges
+    and fanin_pack_from_edges (mode 0) over 2 value parts of 2^20 x 64 f32 and
+    16 edge parts (8 relations x arity 2) of 2^18 edges each (2^22 edges), as
+    in a C3-sized batch.  Timed: the op through torch.ops.relm_mp (one HIP
+    launch for all index parts + at::cat of the values), the same op in the
+    reference's formulation (per-part tensor arithmetic + torch.cat, the ATen
+    fallback, on the same GPU), and the index kernel alone (HIP events).
+    Algorithmic bytes of the index kernel: 32 per edge (two int64 read, two
+    written)."""
+
+    from relmo_amd import capi, mp_pack
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    rows, emb, n_rel, arity, per = 1 << 20, 64, 8, 2, 1 << 18
+    xs = [torch.randn(rows, emb, device=dev, generator=gen) for _ in range(2)]
+    src = [torch.randint(0, rows, (per,), device=dev, generator=gen) for _ in range(n_rel * arity)]
+    dst = [torch.randint(0, per, (per,), device=dev, generator=gen) for _ in range(n_rel * arity)]
+    ids = [(r + p) % 2 for r in range(n_rel) for p in range(arity)]
+    ar = [arity] * (n_rel * arity)
+    pos = [p for _ in range(n_rel) for p in range(arity)]
+    slot = [r * per * arity for r in range(n_rel) for _ in range(arity)]
+    ns = torch.ops.relm_mp
+    E = per * n_rel * arity
+    idx_bytes = 32 * E
+    val_bytes = 2 * sum(x.numel() * x.element_size() for x in xs)
+    sync = torch.cuda.synchronize
+    res = {"edges": E, "edge_parts": n_rel * arity, "value_parts": 2, "rows_per_part": rows, "emb": emb,
+           "index_bytes": idx_bytes, "value_cat_bytes": val_bytes}
+    for name, ours, aten in (
+        ("fanout_pack_from_edges",
+         lambda: ns.fanout_pack_from_edges(xs, src, dst, ids, ar, pos, slot),
+         lambda: mp_pack.fanout_pack_from_edges_python(xs, src, dst, ids, ar, pos, slot)),
+        ("fanin_pack_from_edges",
+         lambda: ns.fanin_pack_from_edges(xs, src, dst, ids, ar, pos, 0),
+         lambda: mp_pack.fanin_pack_from_edges_python(xs, src, dst, ids, ar, pos, 0)),
+    ):
+        t_ours = timed(ours, steps, 3, sync)
+        t_aten = timed(aten, steps, 3, sync)
+        res[name] = {"ms_op": t_ours * 1e3, "ms_aten_formulation": t_aten * 1e3,
+                     "gbs_op": gbs(idx_bytes + val_bytes, t_ours),
+                     "gbs_aten_formulation": gbs(idx_bytes + val_bytes, t_aten)}
+    offsets = [0, rows]
+    parts = [(s, d, 1, offsets[i], a, sl + p) for s, d, i, a, p, sl in zip(src, dst, ids, ar, pos, slot)]
+    t_kernel = event_time(lambda: capi.pack_index(parts), max(steps, 20), torch)
+    res["ms_index_kernel"] = t_kernel * 1e3
+    res["gbs_index_kernel"] = gbs(idx_bytes, t_kernel)
+    res["frac_index_kernel"] = res["gbs_index_kernel"] / PEAK_HBM_GBS
+    del xs, src, dst
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_copy(torch, steps: int) -> dict:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the HBM
     byte counters (FETCH_SIZE / WRITE_SIZE per dispatch against 1 GiB)."""
@@ -364,7 +420,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "pack", "copy"], default=None,
                     help="run one workload only and print its figures (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -392,6 +448,7 @@ def main() -> int:
               "c1": lambda: bench_c1(torch, mp, syn),
               "c4": lambda: bench_models(torch, "c4", args.steps, args.warmup),
               "c5": lambda: bench_models(torch, "c5", args.steps, args.warmup),
+              "pack": lambda: bench_pack(torch, args.steps),
               "copy": lambda: bench_copy(torch, args.steps)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
@@ -406,6 +463,8 @@ def main() -> int:
     extra["c3_fanout"] = bench_c3(torch, mp, capi, syn, max(5, args.steps // 2), 2)
     log("C1 latencies ...")
     extra["c1_latency_us"] = bench_c1(torch, mp, syn)
+    log("pack ops (index preparation) ...")
+    extra["pack"] = bench_pack(torch, max(5, args.steps // 2))
     log("C4 RelationalGNN training step ...")
     extra["c4_relational_gnn"] = bench_models(torch, "c4", 5, 2)
     log("C5 CentralizedRelationalGNN training step ...")

@@ -279,6 +279,32 @@ int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
                                        const void* rel_flat, int64_t emb, void* grad_rel,
                                        int64_t rel_rows, relm_mp_stream_t stream);
 
+/* ---- index packing (the pack ops) -------------------------------------- */
+
+/* One part of a packing call: n index pairs (a[i], b[i]) written as
+ * a[i] * a_mul + a_add and b[i] * b_mul + b_add. */
+typedef struct relm_mp_index_part {
+    const int64_t* a;
+    const int64_t* b;
+    int64_t n;
+    int64_t a_mul;
+    int64_t a_add;
+    int64_t b_mul;
+    int64_t b_add;
+} relm_mp_index_part;
+
+/* out_a / out_b [sum of n] = the parts' transformed pairs, back to back in part
+ * order; device pointers, one kernel launch per 16 parts.  out_b may be NULL:
+ * then only out_a is written and the parts' b arrays are not read.  The index arithmetic
+ * of relm::mp::fanout_pack_multi (mp_ops.cpp:412-484: src + row offset, flat_dst
+ * unchanged), fanin_pack_multi (:486-570: flat_src + row offset, dst unchanged),
+ * fanout_pack_from_edges (:2511-2634: src + part offset, slot_offset +
+ * dst * arity + pos) and fanin_pack_from_edges (:2636-2772: src * arity + pos +
+ * part offset, or src + part offset, dst unchanged) - the torch binding maps
+ * each op's parts onto this. */
+int relm_mp_pack_index(const relm_mp_index_part* parts, int32_t num_parts, int64_t* out_a,
+                       int64_t* out_b, relm_mp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,11 @@ OPS = {
     "fanin_reduce": 3,
     "fanin_reduce_sum_backward": 3,
     "fanin_reduce_logsumexp_backward": 5,
+    # list-argument ops: called with "args" (see run_reference)
+    "fanout_pack_multi": 0,
+    "fanin_pack_multi": 0,
+    "fanout_pack_from_edges": 0,
+    "fanin_pack_from_edges": 0,
 }
 
 
@@ -40,8 +45,11 @@ def available() -> bool:
 
 def run_reference(calls: list[dict], arrays: dict[str, np.ndarray], timeout: float = 600.0) -> list[dict]:
     """Each call: {"op", "tensors": [names], "ints": [...], optional "repeat",
-    "warmup", "threads"}.  Returns per call {"out": ndarray} or {"error": str},
-    plus "times" (seconds per repetition) when "repeat" is given."""
+    "warmup", "threads"}, or {"op", "args": [spec, ...]} with each spec one of
+    {"tensor": name}, {"tensors": [names]}, {"int": v}, {"ints": [v, ...]}.
+    Returns per call {"out": ndarray} ({"outs": [ndarray, ...]} for an op
+    returning a tuple) or {"error": str}, plus "times" (seconds per repetition)
+    when "repeat" is given."""
 
     if not available():
         raise FileNotFoundError(f"{REF_LIB} is missing; run `make -C oracle ref` where the reference is present")
@@ -62,6 +70,8 @@ def run_reference(calls: list[dict], arrays: dict[str, np.ndarray], timeout: flo
             r = dict(m)
             if f"out_{i}" in outs.files:
                 r["out"] = outs[f"out_{i}"]
+            if "num_outs" in r:
+                r["outs"] = [outs[f"out_{i}_{k}"] for k in range(r["num_outs"])]
             results.append(r)
         return results
 
@@ -79,8 +89,23 @@ def _child(req_dir: Path) -> None:
         op = call["op"]
         if op not in OPS:
             raise ValueError(f"unknown op {op}")
-        tensors = [torch.from_numpy(np.array(arrays[name])) for name in call["tensors"]]
-        ints = [int(v) for v in call.get("ints", [])]
+        def tensor(name):
+            return torch.from_numpy(np.array(arrays[name]))
+
+        if "args" in call:
+            tensors, ints = [], []
+            for spec in call["args"]:
+                if "tensor" in spec:
+                    tensors.append(tensor(spec["tensor"]))
+                elif "tensors" in spec:
+                    tensors.append([tensor(n) for n in spec["tensors"]])
+                elif "int" in spec:
+                    tensors.append(int(spec["int"]))
+                else:
+                    tensors.append([int(v) for v in spec["ints"]])
+        else:
+            tensors = [tensor(name) for name in call["tensors"]]
+            ints = [int(v) for v in call.get("ints", [])]
         threads = call.get("threads")
         if threads:
             torch.set_num_threads(int(threads))
@@ -95,7 +120,12 @@ def _child(req_dir: Path) -> None:
             entry["error_type"] = type(exc).__name__
             meta.append(entry)
             continue
-        outputs[f"out_{i}"] = out.numpy()
+        if isinstance(out, (tuple, list)):
+            entry["num_outs"] = len(out)
+            for k, o in enumerate(out):
+                outputs[f"out_{i}_{k}"] = o.detach().numpy()
+        else:
+            outputs[f"out_{i}"] = out.numpy()
         repeat = int(call.get("repeat", 0))
         if repeat:
             warmup = int(call.get("warmup", 1))

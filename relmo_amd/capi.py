@@ -55,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "relm_mp_plan_segment_reduce",
     "relm_mp_plan_logsumexp_backward",
     "relm_mp_plan_fanin_backward_by_dst",
+    "relm_mp_pack_index",
 )
 
 
@@ -89,6 +90,20 @@ class Plan(ctypes.Structure):
         ("short_off", ctypes.c_void_p),
         ("short_gather", ctypes.c_void_p),
         ("counts", ctypes.c_void_p),
+    ]
+
+
+class IndexPart(ctypes.Structure):
+    """Mirror of ``struct relm_mp_index_part``."""
+
+    _fields_ = [
+        ("a", ctypes.c_void_p),
+        ("b", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+        ("a_mul", ctypes.c_int64),
+        ("a_add", ctypes.c_int64),
+        ("b_mul", ctypes.c_int64),
+        ("b_add", ctypes.c_int64),
     ]
 
 
@@ -135,6 +150,7 @@ _SIGNATURES = {
     "relm_mp_plan_segment_reduce": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_logsumexp_backward": (_int, [_int, _PP, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_fanin_backward_by_dst": (_int, [_int, _PP, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "relm_mp_pack_index": (_int, [ctypes.POINTER(IndexPart), ctypes.c_int32, _vp, _vp, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -473,3 +489,26 @@ def plan_gather_last(bp: BuiltPlan, table: torch.Tensor, gathers: torch.Tensor |
 
 
 __all__ = [name for name in dir() if not name.startswith("_")]
+
+
+def pack_index(parts: list[tuple], write_b: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """``relm_mp_pack_index`` over parts ``(a, b, a_mul, a_add, b_mul, b_add)``
+    (contiguous int64 device tensors of equal length); returns (out_a, out_b)."""
+
+    if not parts:
+        raise ValueError("pack_index needs at least one part")
+    like = parts[0][0]
+    descs = (IndexPart * len(parts))()
+    total = 0
+    for d, (a, b, a_mul, a_add, b_mul, b_add) in zip(descs, parts):
+        _check_index(a)
+        _check_index(b)
+        if a.numel() != b.numel():
+            raise ValueError("index parts of unequal length")
+        d.a, d.b, d.n = _ptr(a), _ptr(b), a.numel()
+        d.a_mul, d.a_add, d.b_mul, d.b_add = int(a_mul), int(a_add), int(b_mul), int(b_add)
+        total += a.numel()
+    out_a = torch.empty(total, dtype=torch.int64, device=like.device)
+    out_b = torch.empty(total, dtype=torch.int64, device=like.device) if write_b else None
+    check(lib().relm_mp_pack_index(descs, len(parts), _ptr(out_a), _ptr(out_b), _stream(like)))
+    return out_a, out_b

@@ -468,6 +468,24 @@ int relm_mp_inv_plan_build_async(const int64_t* keys, int64_t key_bound, const c
                      static_cast<hipStream_t>(stream));
 }
 
+int relm_mp_pack_index(const relm_mp_index_part* parts, int32_t num_parts, int64_t* out_a,
+                       int64_t* out_b, relm_mp_stream_t stream) {
+    if (num_parts < 0 || (num_parts > 0 && parts == nullptr))
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: bad index parts");
+    int64_t total = 0;
+    for (int32_t i = 0; i < num_parts; ++i) {
+        if (parts[i].n < 0 || (parts[i].n > 0 && (parts[i].a == nullptr ||
+                                                   (out_b != nullptr && parts[i].b == nullptr))))
+            return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: bad index part");
+        total += parts[i].n;
+    }
+    if (total > 0 && out_a == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: output array is NULL");
+    RELM_HIP(launch_pack_index(parts, num_parts, out_a, out_b, static_cast<hipStream_t>(stream)),
+             "relm_mp pack kernel");
+    return RELM_MP_OK;
+}
+
 int relm_mp_plan_validate(relm_mp_plan* plan) {
     if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
     return validate_pending(plan);

@@ -112,6 +112,10 @@ inline int64_t max_chunks(int64_t num_edges) {
     return num_edges / kChunkSize + max_hubs(num_edges) + 1;
 }
 
+// ---- index packing (pack_kernels.hip) -------------------------------------
+hipError_t launch_pack_index(const relm_mp_index_part* parts, int num_parts, int64_t* out_a,
+                             int64_t* out_b, hipStream_t s);
+
 // ---- compute kernels (reduce_kernels.hip) --------------------------------
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
                         const void* table, int64_t emb, void* out, hipStream_t s);

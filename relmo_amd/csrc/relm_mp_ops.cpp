@@ -25,6 +25,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "relm_mp.h"
@@ -690,6 +691,270 @@ Tensor fanin_reduce_logsumexp_backward(const Tensor& grad_out, const Tensor& rel
     return fanin_logsumexp_backward_aten(grad_out, rel_flat, flat_src, dst_idx, out, rel_rows);
 }
 
+// ---- pack ops (mp_ops.cpp:412-570, 2511-2772) --------------------------------
+//
+// Values are concatenated with at::cat (differentiable; a single part is
+// returned as is), the index outputs by one pass over all parts: pair e of part
+// i becomes (a[e] * a_mul + a_add, b[e] * b_mul + b_add).  The reference
+// always returns a new tensor for the first index output and returns the
+// second index tensor of a single part unchanged where it applies no
+// arithmetic to it; `alias_single_b` keeps that.
+
+struct IndexPart {
+    Tensor a;
+    Tensor b;
+    int64_t a_mul, a_add, b_mul, b_add;
+};
+
+void pack_parts_cpu(const std::vector<IndexPart>& parts, int64_t* out_a, int64_t* out_b) {
+    int64_t pos = 0;
+    for (const IndexPart& p : parts) {
+        const Tensor a = contiguous(p.a);
+        const int64_t* pa = a.data_ptr<int64_t>();
+        const int64_t n = a.numel();
+        const uint64_t am = static_cast<uint64_t>(p.a_mul), aa = static_cast<uint64_t>(p.a_add);
+        for (int64_t e = 0; e < n; ++e)
+            out_a[pos + e] = static_cast<int64_t>(static_cast<uint64_t>(pa[e]) * am + aa);
+        if (out_b != nullptr) {
+            const Tensor b = contiguous(p.b);
+            const int64_t* pb = b.data_ptr<int64_t>();
+            const uint64_t bm = static_cast<uint64_t>(p.b_mul), ba = static_cast<uint64_t>(p.b_add);
+            for (int64_t e = 0; e < n; ++e)
+                out_b[pos + e] = static_cast<int64_t>(static_cast<uint64_t>(pb[e]) * bm + ba);
+        }
+        pos += n;
+    }
+}
+
+void pack_parts_gpu(const std::vector<IndexPart>& parts, int64_t* out_a, int64_t* out_b,
+                    const Tensor& like) {
+    std::vector<Tensor> keep;
+    std::vector<relm_mp_index_part> desc;
+    keep.reserve(2 * parts.size());
+    desc.reserve(parts.size());
+    for (const IndexPart& p : parts) {
+        keep.push_back(contiguous(p.a));
+        const int64_t* pa = keep.back().data_ptr<int64_t>();
+        const int64_t* pb = nullptr;
+        if (out_b != nullptr) {
+            keep.push_back(contiguous(p.b));
+            pb = keep.back().data_ptr<int64_t>();
+        }
+        desc.push_back({pa, pb, p.a.numel(), p.a_mul, p.a_add, p.b_mul, p.b_add});
+    }
+    // Contiguous copies made here are released to the caching allocator after
+    // the launch is enqueued on the same stream, so their memory is reused in
+    // stream order only.
+    raise_if(relm_mp_pack_index(desc.data(), static_cast<int32_t>(desc.size()), out_a, out_b,
+                                current_stream(like)));
+}
+
+std::tuple<Tensor, Tensor> pack_index_parts(const std::vector<IndexPart>& parts,
+                                            bool alias_single_b, const Tensor& like) {
+    int64_t total = 0;
+    for (const IndexPart& p : parts) total += p.a.numel();
+    const auto opts = like.options().dtype(at::kLong);
+    const bool b_alias = alias_single_b && parts.size() == 1;
+    Tensor out_a = at::empty({total}, opts);
+    Tensor out_b = b_alias ? parts.front().b : at::empty({total}, opts);
+    if (total == 0) return std::make_tuple(out_a, out_b);
+    int64_t* pb = b_alias ? nullptr : out_b.data_ptr<int64_t>();
+    if (like.is_cuda()) {
+        c10::DeviceGuard guard(like.device());
+        pack_parts_gpu(parts, out_a.data_ptr<int64_t>(), pb, like);
+    } else {
+        pack_parts_cpu(parts, out_a.data_ptr<int64_t>(), pb);
+    }
+    return std::make_tuple(out_a, out_b);
+}
+
+// Checks of one value part shared by the four ops (mp_ops.cpp:443-466, 2543-2569).
+void check_value_part(const Tensor& t, size_t i, const c10::Device& device, at::ScalarType dtype,
+                      int64_t emb, const char* op, const char* part_name, const char* what) {
+    check_rank(t, 2, what);
+    TORCH_CHECK(t.device() == device, op, " expects all ", part_name,
+                " on the same device. Mismatch at part ", i, ".");
+    TORCH_CHECK(t.scalar_type() == dtype, op, " expects all ", part_name,
+                " with the same dtype. Mismatch at part ", i, ".");
+    TORCH_CHECK(t.size(1) == emb, op, " expects matching embedding dim across ", part_name,
+                ". Part ", i, " has emb=", t.size(1), ", expected ", emb, ".");
+}
+
+Tensor cat_values(const std::vector<Tensor>& parts) {
+    return parts.size() == 1 ? parts.front() : at::cat(parts, 0);
+}
+
+std::tuple<Tensor, Tensor, Tensor> pack_multi(const char* op, const char* value_name,
+                                              const char* first_name, const char* second_name,
+                                              const std::vector<Tensor>& values,
+                                              const std::vector<Tensor>& first,
+                                              const std::vector<Tensor>& second) {
+    const Tensor& ref = values.front();
+    check_rank(ref, 2, (std::string(value_name) + "[0]").c_str());
+    const int64_t emb = ref.size(1);
+    std::vector<IndexPart> parts;
+    parts.reserve(values.size());
+    int64_t row_offset = 0;
+    const std::string vname = std::string(value_name) + "[i]";
+    const std::string fname = std::string(first_name) + "_parts[i]";
+    const std::string sname = std::string(second_name) + "_parts[i]";
+    for (size_t i = 0; i < values.size(); ++i) {
+        check_rank(values[i], 2, vname.c_str());
+        check_int64_index(first[i], fname.c_str());
+        check_int64_index(second[i], sname.c_str());
+        check_value_part(values[i], i, ref.device(), ref.scalar_type(), emb, op, value_name,
+                         vname.c_str());
+        TORCH_CHECK(first[i].device() == ref.device() && second[i].device() == ref.device(), op,
+                    " expects all index tensors on the same device as ", value_name, ".");
+        TORCH_CHECK(first[i].size(0) == second[i].size(0), op, " expects ", first_name, " and ",
+                    second_name, " lengths to match for part ", i, ".");
+        parts.push_back({first[i], second[i], 1, row_offset, 1, 0});
+        row_offset += values[i].size(0);
+    }
+    auto [a, b] = pack_index_parts(parts, /*alias_single_b=*/true, ref);
+    return std::make_tuple(cat_values(values), a, b);
+}
+
+std::tuple<Tensor, Tensor, Tensor> fanout_pack_multi(const std::vector<Tensor>& x_parts,
+                                                     const std::vector<Tensor>& src_idx_parts,
+                                                     const std::vector<Tensor>& flat_dst_parts) {
+    TORCH_CHECK(!x_parts.empty(), "fanout_pack_multi requires at least one source tensor.");
+    TORCH_CHECK(x_parts.size() == src_idx_parts.size() && x_parts.size() == flat_dst_parts.size(),
+                "fanout_pack_multi expects x_parts, src_idx_parts, and flat_dst_parts with equal "
+                "lengths.");
+    return pack_multi("fanout_pack_multi", "x_parts", "src_idx", "flat_dst", x_parts,
+                      src_idx_parts, flat_dst_parts);
+}
+
+std::tuple<Tensor, Tensor, Tensor> fanin_pack_multi(const std::vector<Tensor>& rel_parts,
+                                                    const std::vector<Tensor>& flat_src_parts,
+                                                    const std::vector<Tensor>& dst_idx_parts) {
+    TORCH_CHECK(!rel_parts.empty(), "fanin_pack_multi requires at least one relation tensor.");
+    TORCH_CHECK(rel_parts.size() == flat_src_parts.size() && rel_parts.size() == dst_idx_parts.size(),
+                "fanin_pack_multi expects rel_parts, flat_src_parts, and dst_idx_parts with equal "
+                "lengths.");
+    return pack_multi("fanin_pack_multi", "rel_parts", "flat_src", "dst_idx", rel_parts,
+                      flat_src_parts, dst_idx_parts);
+}
+
+// Row offset of each value part (mp_ops.cpp:2540-2572, 2672-2704).
+std::vector<int64_t> value_offsets(const char* op, const char* value_name,
+                                   const std::vector<Tensor>& values) {
+    const Tensor& ref = values.front();
+    check_rank(ref, 2, (std::string(value_name) + "[0]").c_str());
+    const std::string vname = std::string(value_name) + "[i]";
+    std::vector<int64_t> offsets(values.size(), 0);
+    int64_t row_offset = 0;
+    for (size_t i = 0; i < values.size(); ++i) {
+        check_value_part(values[i], i, ref.device(), ref.scalar_type(), ref.size(1), op,
+                         value_name, vname.c_str());
+        offsets[i] = row_offset;
+        row_offset += values[i].size(0);
+    }
+    return offsets;
+}
+
+void check_edge_part(const char* op, const char* value_name, const Tensor& src, const Tensor& dst,
+                     const c10::Device& device, int64_t i) {
+    check_int64_index(src, "edge_src_parts[i]");
+    check_int64_index(dst, "edge_dst_parts[i]");
+    TORCH_CHECK(src.device() == device && dst.device() == device, op,
+                " expects all edge index tensors on the same device as ", value_name, ".");
+    TORCH_CHECK(src.size(0) == dst.size(0), op, " expects edge src/dst lengths to match for part ",
+                i, ".");
+}
+
+std::tuple<Tensor, Tensor, Tensor> empty_edge_pack(const Tensor& values_cat, const Tensor& ref) {
+    Tensor empty_idx = at::empty({0}, ref.options().dtype(at::kLong));
+    return std::make_tuple(values_cat, empty_idx, empty_idx.clone());
+}
+
+std::tuple<Tensor, Tensor, Tensor> fanout_pack_from_edges(
+    const std::vector<Tensor>& x_parts, const std::vector<Tensor>& edge_src_parts,
+    const std::vector<Tensor>& edge_dst_parts, const std::vector<int64_t>& src_part_ids,
+    const std::vector<int64_t>& arity_parts, const std::vector<int64_t>& pos_parts,
+    const std::vector<int64_t>& slot_offset_parts) {
+    const char* op = "fanout_pack_from_edges";
+    TORCH_CHECK(!x_parts.empty(), "fanout_pack_from_edges requires at least one source tensor.");
+    const size_t n_edge = edge_src_parts.size();
+    TORCH_CHECK(edge_dst_parts.size() == n_edge,
+                "fanout_pack_from_edges expects edge_src_parts and edge_dst_parts with equal "
+                "lengths.");
+    TORCH_CHECK(src_part_ids.size() == n_edge && arity_parts.size() == n_edge &&
+                    pos_parts.size() == n_edge && slot_offset_parts.size() == n_edge,
+                "fanout_pack_from_edges expects metadata arrays to match number of edge parts.");
+    const std::vector<int64_t> offsets = value_offsets(op, "x_parts", x_parts);
+    const Tensor& ref = x_parts.front();
+    const Tensor x_cat = cat_values(x_parts);
+    if (n_edge == 0) return empty_edge_pack(x_cat, ref);
+    std::vector<IndexPart> parts;
+    parts.reserve(n_edge);
+    for (size_t i = 0; i < n_edge; ++i) {
+        check_edge_part(op, "x_parts", edge_src_parts[i], edge_dst_parts[i], ref.device(),
+                        static_cast<int64_t>(i));
+        const int64_t src_part = src_part_ids[i];
+        TORCH_CHECK(src_part >= 0 && src_part < static_cast<int64_t>(x_parts.size()),
+                    "fanout_pack_from_edges src_part_ids[", i, "] out of range: ", src_part, ".");
+        const int64_t arity = arity_parts[i], pos = pos_parts[i];
+        TORCH_CHECK(arity > 0, "fanout_pack_from_edges requires arity > 0 for edge part ", i, ".");
+        TORCH_CHECK(pos >= 0 && pos < arity, "fanout_pack_from_edges pos out of range for edge part ",
+                    i, ": pos=", pos, " arity=", arity, ".");
+        // flat_dst = slot_offset + dst * arity + pos, sums wrapping as int64 does.
+        const int64_t b_add = static_cast<int64_t>(static_cast<uint64_t>(slot_offset_parts[i]) +
+                                                   static_cast<uint64_t>(pos));
+        parts.push_back({edge_src_parts[i], edge_dst_parts[i], 1, offsets[src_part], arity, b_add});
+    }
+    auto [src_global, flat_dst] = pack_index_parts(parts, /*alias_single_b=*/false, ref);
+    return std::make_tuple(x_cat, src_global, flat_dst);
+}
+
+std::tuple<Tensor, Tensor, Tensor> fanin_pack_from_edges(
+    const std::vector<Tensor>& rel_parts, const std::vector<Tensor>& edge_src_parts,
+    const std::vector<Tensor>& edge_dst_parts, const std::vector<int64_t>& rel_part_ids,
+    const std::vector<int64_t>& arity_parts, const std::vector<int64_t>& pos_parts, int64_t mode) {
+    const char* op = "fanin_pack_from_edges";
+    TORCH_CHECK(!rel_parts.empty(), "fanin_pack_from_edges requires at least one relation tensor.");
+    TORCH_CHECK(mode == 0 || mode == 1,
+                "fanin_pack_from_edges mode must be 0 (relation) or 1 (label), got ", mode, ".");
+    const size_t n_edge = edge_src_parts.size();
+    TORCH_CHECK(edge_dst_parts.size() == n_edge,
+                "fanin_pack_from_edges expects edge_src_parts and edge_dst_parts with equal "
+                "lengths.");
+    TORCH_CHECK(rel_part_ids.size() == n_edge && arity_parts.size() == n_edge &&
+                    pos_parts.size() == n_edge,
+                "fanin_pack_from_edges expects metadata arrays to match number of edge parts.");
+    const std::vector<int64_t> offsets = value_offsets(op, "rel_parts", rel_parts);
+    const Tensor& ref = rel_parts.front();
+    const Tensor rel_cat = cat_values(rel_parts);
+    if (n_edge == 0) return empty_edge_pack(rel_cat, ref);
+    std::vector<IndexPart> parts;
+    parts.reserve(n_edge);
+    for (size_t i = 0; i < n_edge; ++i) {
+        check_edge_part(op, "rel_parts", edge_src_parts[i], edge_dst_parts[i], ref.device(),
+                        static_cast<int64_t>(i));
+        const int64_t rel_part = rel_part_ids[i];
+        TORCH_CHECK(rel_part >= 0 && rel_part < static_cast<int64_t>(rel_parts.size()),
+                    "fanin_pack_from_edges rel_part_ids[", i, "] out of range: ", rel_part, ".");
+        int64_t a_mul = 1, a_add = offsets[rel_part];
+        if (mode == 0) {
+            const int64_t arity = arity_parts[i], pos = pos_parts[i];
+            TORCH_CHECK(arity > 0,
+                        "fanin_pack_from_edges requires arity > 0 in relation mode for edge part ",
+                        i, ".");
+            TORCH_CHECK(pos >= 0 && pos < arity,
+                        "fanin_pack_from_edges pos out of range for edge part ", i, ": pos=", pos,
+                        " arity=", arity, ".");
+            // flat_src = (src * arity + pos) + rel_offset.
+            a_mul = arity;
+            a_add = static_cast<int64_t>(static_cast<uint64_t>(pos) +
+                                         static_cast<uint64_t>(offsets[rel_part]));
+        }
+        parts.push_back({edge_src_parts[i], edge_dst_parts[i], a_mul, a_add, 1, 0});
+    }
+    auto [flat_src, dst_idx] = pack_index_parts(parts, /*alias_single_b=*/true, ref);
+    return std::make_tuple(rel_cat, flat_src, dst_idx);
+}
+
 std::string build_info() {
     return std::string("build_torch=") + RELM_MP_BUILD_TORCH_VERSION +
            ";build_cuda_tag=cpu;abi_target=rocm-gfx950;abi_lane=nonstable;" + relm_mp_build_info();
@@ -707,6 +972,10 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("fanin_reduce(Tensor rel_flat, Tensor flat_src, Tensor dst_idx, int dim_size, int mode) -> Tensor");
     m.def("fanin_reduce_sum_backward(Tensor grad_out, Tensor flat_src, Tensor dst_idx, int rel_rows) -> Tensor");
     m.def("fanin_reduce_logsumexp_backward(Tensor grad_out, Tensor rel_flat, Tensor flat_src, Tensor dst_idx, Tensor out, int rel_rows) -> Tensor");
+    m.def("fanout_pack_multi(Tensor[] x_parts, Tensor[] src_idx_parts, Tensor[] flat_dst_parts) -> (Tensor, Tensor, Tensor)");
+    m.def("fanin_pack_multi(Tensor[] rel_parts, Tensor[] flat_src_parts, Tensor[] dst_idx_parts) -> (Tensor, Tensor, Tensor)");
+    m.def("fanout_pack_from_edges(Tensor[] x_parts, Tensor[] edge_src_parts, Tensor[] edge_dst_parts, int[] src_part_ids, int[] arity_parts, int[] pos_parts, int[] slot_offset_parts) -> (Tensor, Tensor, Tensor)");
+    m.def("fanin_pack_from_edges(Tensor[] rel_parts, Tensor[] edge_src_parts, Tensor[] edge_dst_parts, int[] rel_part_ids, int[] arity_parts, int[] pos_parts, int mode) -> (Tensor, Tensor, Tensor)");
     m.def("build_info() -> str");
     // No reference counterpart: control of the index-plan cache.
     m.def("plan_cache_clear() -> ()");
@@ -719,6 +988,10 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("fanin_reduce", relm_amd::fanin_reduce);
     m.impl("fanin_reduce_sum_backward", relm_amd::fanin_reduce_sum_backward);
     m.impl("fanin_reduce_logsumexp_backward", relm_amd::fanin_reduce_logsumexp_backward);
+    m.impl("fanout_pack_multi", relm_amd::fanout_pack_multi);
+    m.impl("fanin_pack_multi", relm_amd::fanin_pack_multi);
+    m.impl("fanout_pack_from_edges", relm_amd::fanout_pack_from_edges);
+    m.impl("fanin_pack_from_edges", relm_amd::fanin_pack_from_edges);
     m.impl("build_info", relm_amd::build_info);
     m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
     m.impl("plan_cache_size", relm_amd::plan_cache_size);

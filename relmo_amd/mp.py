@@ -4,7 +4,8 @@
 dispatch (``src/relmo/ops/mp.py:43-70``): modes other than sum (0) and
 logsumexp (1) go to the ATen fallback, which raises ``ValueError``; otherwise
 the custom ops run through autograd Functions unless the policy selects the
-fallback.
+fallback.  The four pack ops (``mp.py:73-146``) call ``torch.ops.relm_mp``
+directly, or their ATen fallbacks, through ``dispatch_namespace_op``.
 """
 
 from __future__ import annotations
@@ -15,8 +16,15 @@ from .mp_autograd import (
     _FanoutScatterFunction,
 )
 from .mp_constants import MODE_LOGSUMEXP, MODE_MEAN, MODE_SUM, activation_code
-from .mp_dispatch import should_use_custom
-from .mp_pack import fanin_reduce_python, fanout_scatter_python
+from .mp_dispatch import dispatch_namespace_op, should_use_custom
+from .mp_pack import (
+    fanin_pack_from_edges_python,
+    fanin_pack_multi_python,
+    fanin_reduce_python,
+    fanout_pack_from_edges_python,
+    fanout_pack_multi_python,
+    fanout_scatter_python,
+)
 from .mp_runtime import TORCH_IMPORT_ERROR, assert_runtime_compat, available, require_torch, torch
 
 
@@ -53,6 +61,73 @@ def fanin_reduce(
     return fanin_reduce_python(rel_flat, flat_src, dst_idx, int(dim_size), mode)
 
 
+def fanout_pack_multi(
+    x_parts: list[torch.Tensor],
+    src_idx_parts: list[torch.Tensor],
+    flat_dst_parts: list[torch.Tensor],
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Concatenate source parts for one ``fanout_scatter``: ``(x_cat, src_global_idx, flat_dst)``."""
+
+    require_torch("fanout_pack_multi")
+    return dispatch_namespace_op(
+        "fanout_pack_multi", x_parts, src_idx_parts, flat_dst_parts,
+        fallback=fanout_pack_multi_python,
+    )
+
+
+def fanin_pack_multi(
+    rel_parts: list[torch.Tensor],
+    flat_src_parts: list[torch.Tensor],
+    dst_idx_parts: list[torch.Tensor],
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Concatenate relation parts for one ``fanin_reduce``: ``(rel_flat, flat_src, dst_idx)``."""
+
+    require_torch("fanin_pack_multi")
+    return dispatch_namespace_op(
+        "fanin_pack_multi", rel_parts, flat_src_parts, dst_idx_parts,
+        fallback=fanin_pack_multi_python,
+    )
+
+
+def fanout_pack_from_edges(
+    x_parts: list[torch.Tensor],
+    edge_src_parts: list[torch.Tensor],
+    edge_dst_parts: list[torch.Tensor],
+    src_part_ids: list[int],
+    arity_parts: list[int],
+    pos_parts: list[int],
+    slot_offset_parts: list[int],
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fanout operands from per-relation edge lists: ``flat_dst = slot_offset + dst * arity + pos``."""
+
+    require_torch("fanout_pack_from_edges")
+    return dispatch_namespace_op(
+        "fanout_pack_from_edges", x_parts, edge_src_parts, edge_dst_parts, src_part_ids,
+        arity_parts, pos_parts, slot_offset_parts,
+        fallback=fanout_pack_from_edges_python,
+    )
+
+
+def fanin_pack_from_edges(
+    rel_parts: list[torch.Tensor],
+    edge_src_parts: list[torch.Tensor],
+    edge_dst_parts: list[torch.Tensor],
+    rel_part_ids: list[int],
+    arity_parts: list[int],
+    pos_parts: list[int],
+    mode: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fanin operands from per-relation edge lists: ``flat_src = src * arity + pos`` (mode 0)
+    or ``src`` (mode 1), plus the part's row offset."""
+
+    require_torch("fanin_pack_from_edges")
+    return dispatch_namespace_op(
+        "fanin_pack_from_edges", rel_parts, edge_src_parts, edge_dst_parts, rel_part_ids,
+        arity_parts, pos_parts, int(mode),
+        fallback=fanin_pack_from_edges_python,
+    )
+
+
 __all__ = [
     "MODE_LOGSUMEXP",
     "MODE_MEAN",
@@ -61,6 +136,10 @@ __all__ = [
     "activation_code",
     "assert_runtime_compat",
     "available",
+    "fanin_pack_from_edges",
+    "fanin_pack_multi",
     "fanin_reduce",
+    "fanout_pack_from_edges",
+    "fanout_pack_multi",
     "fanout_scatter",
 ]

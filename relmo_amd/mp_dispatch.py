@@ -42,4 +42,53 @@ def namespace_has_op(op_name: str) -> bool:
     return hasattr(ops_namespace(), op_name)
 
 
-__all__ = ["namespace_has_op", "ops_namespace", "should_use_custom"]
+def require_available_custom_op(op_name: str) -> None:
+    """Raise under the ``error`` fallback policy: the loaded library lacks ``op_name``."""
+
+    if fallback_mode() == "error":
+        raise RuntimeError(f"Custom mp op {op_name} is unavailable in the loaded relm_mp library.")
+
+
+def use_custom_namespace_op(
+    op_name: str,
+    *,
+    tensor: object | None = None,
+    require_cuda: bool = False,
+) -> bool:
+    """Whether ``op_name`` is called directly on ``torch.ops.relm_mp``."""
+
+    if require_cuda and (tensor is None or not bool(getattr(tensor, "is_cuda", False))):
+        return False
+    return should_use_custom(op_name) and namespace_has_op(op_name)
+
+
+def dispatch_namespace_op(
+    op_name: str,
+    *args,
+    fallback,
+    tensor: object | None = None,
+    require_cuda: bool = False,
+    enforce_fallback_policy: bool = True,
+):
+    """Call ``torch.ops.relm_mp.<op_name>`` or ``fallback`` with ``args``.
+
+    Follows ``src/relmo/ops/mp_dispatch.py:47-81``: the library op when the
+    policy allows it and the library has it; otherwise the fallback, except that
+    under the ``error`` policy a library without the op raises.
+    """
+
+    if use_custom_namespace_op(op_name, tensor=tensor, require_cuda=require_cuda):
+        return getattr(ops_namespace(), op_name)(*args)
+    if enforce_fallback_policy and should_use_custom(op_name):
+        require_available_custom_op(op_name)
+    return fallback(*args)
+
+
+__all__ = [
+    "dispatch_namespace_op",
+    "namespace_has_op",
+    "ops_namespace",
+    "require_available_custom_op",
+    "should_use_custom",
+    "use_custom_namespace_op",
+]

@@ -26,6 +26,37 @@ def golden() -> tuple[list[dict], dict[str, np.ndarray]]:
     return cases, arrays
 
 
+@pytest.fixture(scope="session")
+def pack_golden() -> tuple[list[dict], dict[str, np.ndarray]]:
+    """Pack-op cases written by tests/golden/make_pack_golden.py."""
+
+    cases = json.loads((GOLDEN / "pack_cases.json").read_text())
+    with np.load(GOLDEN / "pack_cases.npz", allow_pickle=False) as data:
+        arrays = {k: data[k] for k in data.files}
+    return cases, arrays
+
+
+def pack_args(case: dict, arrays: dict[str, np.ndarray], device: str = "cpu") -> list:
+    """Arguments of a pack case as torch objects (tensor lists, int lists, ints)."""
+
+    import torch
+
+    def tensor(name: str):
+        return torch.from_numpy(np.array(arrays[name])).to(device)
+
+    args: list = []
+    for spec in case["args"]:
+        if "tensors" in spec:
+            args.append([tensor(n) for n in spec["tensors"]])
+        elif "tensor" in spec:
+            args.append(tensor(spec["tensor"]))
+        elif "ints" in spec:
+            args.append([int(v) for v in spec["ints"]])
+        else:
+            args.append(int(spec["int"]))
+    return args
+
+
 @pytest.fixture
 def mp_env(monkeypatch: pytest.MonkeyPatch):
     """Custom ops on, and a missing library raises instead of falling back."""

@@ -58,23 +58,25 @@ def test_library_exports_exactly_the_header_symbols() -> None:
         assert getattr(lib, name) is not None
 
 
-def test_plan_struct_layout_matches_header(tmp_path) -> None:
+@pytest.mark.parametrize("struct", ["relm_mp_plan", "relm_mp_index_part"])
+def test_struct_layouts_match_header(tmp_path, struct) -> None:
     from relmo_amd import capi
 
-    fields = [name for name, _ in capi.Plan._fields_]
+    mirror = {"relm_mp_plan": capi.Plan, "relm_mp_index_part": capi.IndexPart}[struct]
+    fields = [name for name, _ in mirror._fields_]
     prog = tmp_path / "layout.c"
-    body = "\n".join(f'    printf("{f} %zu\\n", offsetof(relm_mp_plan, {f}));' for f in fields)
+    body = "\n".join(f'    printf("{f} %zu\\n", offsetof({struct}, {f}));' for f in fields)
     prog.write_text(
         "#include <stddef.h>\n#include <stdio.h>\n#include \"relm_mp.h\"\n"
-        f"int main(void) {{\n    printf(\"sizeof %zu\\n\", sizeof(relm_mp_plan));\n{body}\n    return 0;\n}}\n"
+        f"int main(void) {{\n    printf(\"sizeof %zu\\n\", sizeof({struct}));\n{body}\n    return 0;\n}}\n"
     )
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c11", f"-I{HEADER.parent}", str(prog), "-o", str(exe)], check=True)
     out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
                                                         check=True).stdout.splitlines())
-    assert int(out["sizeof"]) == ctypes.sizeof(capi.Plan)
+    assert int(out["sizeof"]) == ctypes.sizeof(mirror)
     for f in fields:
-        assert int(out[f]) == getattr(capi.Plan, f).offset, f
+        assert int(out[f]) == getattr(mirror, f).offset, f
 
 
 # ---- torch binding, CPU lane -------------------------------------------------------------
@@ -331,3 +333,129 @@ def test_model_consumers_cpu_lane_matches_aten(monkeypatch) -> None:
             monkeypatch.setenv("RELM_MP_ENABLE", "0")
             b = C.train_step(model, batch, routing)
             assert torch.allclose(a, b, rtol=1e-5, atol=1e-7), (mode, float(a), float(b))
+
+
+# ---- pack ops on the CPU lane ----------------------------------------------------------------
+
+from tests.conftest import pack_args  # noqa: E402
+
+
+def _check_pack_case(fn, case: dict, arrays: dict, device: str = "cpu", errors: bool = True) -> bool:
+    args = pack_args(case, arrays, device)
+    if "error" in case:
+        if not errors:
+            return False
+        with pytest.raises((RuntimeError, ValueError)) as info:
+            fn(*args)
+        assert str(info.value).splitlines()[0] == case["error"], case["name"]
+        return True
+    got = fn(*args)
+    assert len(got) == len(case["expected"]) == 3, case["name"]
+    for g, name in zip(got, case["expected"]):
+        want = arrays[name]
+        assert str(g.device).startswith(device), case["name"]
+        g = g.detach().cpu().numpy()
+        assert g.dtype == want.dtype and g.shape == want.shape, case["name"]
+        assert np.array_equal(g, want), case["name"]
+    return True
+
+
+def test_pack_cpu_lane_reproduces_golden(ops, pack_golden) -> None:
+    """Outputs bit-exact, and each invalid call raises the reference's message."""
+
+    cases, arrays = pack_golden
+    for case in cases:
+        _check_pack_case(getattr(ops, case["op"]), case, arrays)
+
+
+def test_pack_python_fallbacks_reproduce_golden(pack_golden) -> None:
+    from relmo_amd import mp_pack
+
+    cases, arrays = pack_golden
+    checked = sum(
+        _check_pack_case(getattr(mp_pack, case["op"] + "_python"), case, arrays, errors=False)
+        for case in cases
+    )
+    assert checked >= 30
+
+
+def test_pack_python_fallback_messages() -> None:
+    from relmo_amd import mp_pack
+
+    x = [torch.zeros(3, 2)]
+    s = [torch.tensor([0, 1])]
+    with pytest.raises(ValueError, match="fanout_pack_multi requires at least one source tensor."):
+        mp_pack.fanout_pack_multi_python([], [], [])
+    with pytest.raises(ValueError, match="expects matching sequence lengths, got x_parts=1, "
+                                         "src_idx_parts=1, flat_dst_parts=0"):
+        mp_pack.fanout_pack_multi_python(x, s, [])
+    with pytest.raises(ValueError, match="expects src_idx to have dtype int64"):
+        mp_pack.fanout_pack_multi_python(x, [s[0].int()], s)
+    with pytest.raises(ValueError, match=r"expects pos in \[0, arity\), got pos=2 arity=2"):
+        mp_pack.fanout_pack_from_edges_python(x, s, s, [0], [2], [2], [0])
+    with pytest.raises(ValueError, match="rel_part_ids out of range: 1"):
+        mp_pack.fanin_pack_from_edges_python(x, s, s, [1], [1], [0], 1)
+    with pytest.raises(ValueError, match=r"expects mode in \{0,1\}, got 3"):
+        mp_pack.fanin_pack_from_edges_python(x, s, s, [0], [1], [0], 3)
+
+
+def test_pack_single_part_aliasing(ops) -> None:
+    """One part: the values tensor comes back as is, so does the second index
+    tensor where the op applies no arithmetic to it; the first index output is
+    always a new tensor (mp_ops.cpp:480-483, 565-568, 2630-2633, 2767-2770)."""
+
+    x = torch.randn(4, 3)
+    src, dst = torch.tensor([0, 2, 3]), torch.tensor([5, 1, 0])
+    for op in (ops.fanout_pack_multi, ops.fanin_pack_multi):
+        v, a, b = op([x], [src], [dst])
+        assert v is x or v.data_ptr() == x.data_ptr()
+        assert b.data_ptr() == dst.data_ptr() and a.data_ptr() != src.data_ptr()
+        assert torch.equal(a, src)
+    v, a, b = ops.fanout_pack_from_edges([x], [src], [dst], [0], [1], [0], [0])
+    assert a.data_ptr() != src.data_ptr() and b.data_ptr() != dst.data_ptr()
+    for mode in (0, 1):
+        v, a, b = ops.fanin_pack_from_edges([x], [src], [dst], [0], [1], [0], mode)
+        assert b.data_ptr() == dst.data_ptr() and a.data_ptr() != src.data_ptr()
+    # two parts: everything concatenated into new tensors
+    v, a, b = ops.fanout_pack_multi([x, x], [src, src], [dst, dst])
+    assert v.data_ptr() != x.data_ptr() and torch.equal(b, torch.cat([dst, dst]))
+
+
+def test_pack_accepts_strided_index_views(ops) -> None:
+    base = torch.arange(20).view(10, 2)
+    src, dst = base[:, 0], base[:, 1]
+    assert not src.is_contiguous()
+    x = [torch.randn(30, 2), torch.randn(5, 2)]
+    _, a, b = ops.fanout_pack_from_edges(x, [src, dst], [dst, src], [1, 0], [3, 2], [1, 0], [7, 9])
+    assert torch.equal(a, torch.cat([src + 30, dst]))
+    assert torch.equal(b, torch.cat([7 + dst * 3 + 1, 9 + src * 2]))
+
+
+def test_pack_facade_dispatch_and_grad(mp_env) -> None:
+    """The reference's pack -> fanout / fanin -> backward test on the CPU lane
+    (tests/python/test_mp_ops.py:353-600): gradients reach every value part."""
+
+    from relmo_amd import mp
+
+    torch.manual_seed(3)
+    xs = [torch.randn(5, 3, dtype=torch.float64, requires_grad=True),
+          torch.randn(4, 3, dtype=torch.float64, requires_grad=True)]
+    src = [torch.tensor([0, 2, 4, 4]), torch.tensor([1, 3])]
+    dst = [torch.tensor([1, 0, 2, 3]), torch.tensor([3, 1])]
+    x_cat, s, d = mp.fanout_pack_from_edges(xs, src, dst, [0, 1], [2, 3], [0, 1], [0, 8])
+    out = mp.fanout_scatter(x_cat, s, d, 20)
+    w = torch.randn_like(out)
+    (out * w).sum().backward()
+    for x, si, di, arity, pos, slot in zip(xs, src, dst, [2, 3], [0, 1], [0, 8]):
+        want = torch.zeros_like(x).index_add_(0, si, w[slot + di * arity + pos])
+        assert torch.equal(x.grad, want)
+    rels = [torch.randn(6, 4, dtype=torch.float64, requires_grad=True),
+            torch.randn(3, 4, dtype=torch.float64, requires_grad=True)]
+    fsrc = [torch.tensor([0, 2, 5]), torch.tensor([1, 2])]
+    fdst = [torch.tensor([1, 0, 2]), torch.tensor([2, 1])]
+
+    def packed_lse(a, b):
+        r_cat, fs, fd = mp.fanin_pack_multi([a, b], fsrc, fdst)
+        return mp.fanin_reduce(r_cat, fs, fd, 3, 1)
+
+    assert torch.autograd.gradcheck(packed_lse, tuple(rels))

@@ -216,3 +216,169 @@ def test_oracle_matches_reference_library_on_random_inputs() -> None:
         oracle.fanin_reduce_logsumexp_backward(a["gk"], a["rel"], a["fsrc"], a["fdst"], lse, 3000),
         rtol=2e-6, atol=1e-7,
     )
+
+
+# ---- pack ops (oracle/pack.py) ------------------------------------------------------------
+#
+# Known answers: the inputs of the reference's own tests
+# (tests/python/test_mp_ops.py:353-600) with the outputs worked out by hand
+# from the op definitions (row offsets 0, 5 for x parts of 5 and 4 rows; 0, 6
+# for rel parts of 6 and 3 rows).
+
+from oracle import pack as pack_oracle  # noqa: E402
+
+
+def _xs():
+    return [np.zeros((5, 3), np.float32), np.ones((4, 3), np.float32)]
+
+
+def _rels():
+    return [np.zeros((6, 4), np.float32), np.ones((3, 4), np.float32)]
+
+
+def test_pack_oracle_known_answers() -> None:
+    x_cat, src, dst = pack_oracle.fanout_pack_multi(_xs(), [[0, 2, 4], [1, 3]], [[3, 1, 5], [0, 4]])
+    assert x_cat.shape == (9, 3) and x_cat[5:].all() and not x_cat[:5].any()
+    assert src.tolist() == [0, 2, 4, 6, 8] and dst.tolist() == [3, 1, 5, 0, 4]
+
+    rel_cat, src, dst = pack_oracle.fanin_pack_multi(_rels(), [[0, 2, 5], [1, 2]], [[1, 0, 2], [2, 1]])
+    assert rel_cat.shape == (9, 4)
+    assert src.tolist() == [0, 2, 5, 7, 8] and dst.tolist() == [1, 0, 2, 2, 1]
+
+    _, src, dst = pack_oracle.fanout_pack_from_edges(
+        _xs(), [[0, 2, 4], [1, 3], [2, 0]], [[1, 0, 2], [3, 1], [0, 2]],
+        [0, 1, 0], [2, 3, 2], [0, 1, 1], [0, 8, 0],
+    )
+    # part 0: dst*2+0; part 1: 8 + dst*3 + 1, src + 5; part 2: dst*2+1
+    assert src.tolist() == [0, 2, 4, 6, 8, 2, 0]
+    assert dst.tolist() == [2, 0, 4, 18, 12, 1, 5]
+
+    _, src, dst = pack_oracle.fanin_pack_from_edges(
+        _rels(), [[0, 2, 1], [1, 2]], [[1, 0, 2], [2, 1]], [0, 1], [1, 1], [0, 0], 1)
+    assert src.tolist() == [0, 2, 1, 7, 8] and dst.tolist() == [1, 0, 2, 2, 1]
+    _, src, dst = pack_oracle.fanin_pack_from_edges(
+        _rels(), [[0, 2, 1], [0, 0]], [[1, 0, 2], [2, 1]], [0, 1], [2, 3], [1, 2], 0)
+    # part 0: src*2+1; part 1: src*3+2+6
+    assert src.tolist() == [1, 5, 3, 8, 8] and dst.tolist() == [1, 0, 2, 2, 1]
+
+
+def _random_edge_parts(rng, n_values, n_parts, max_len=300):
+    rows = [int(r) for r in rng.integers(1, 50, n_values)]
+    values = [rng.standard_normal((r, 3)).astype(np.float32) for r in rows]
+    lens = [int(v) for v in rng.integers(0, max_len, n_parts)]
+    lens[0] = 0  # an empty part
+    part_ids = [int(v) for v in rng.integers(0, n_values, n_parts)]
+    arity = [int(v) for v in rng.integers(1, 5, n_parts)]
+    pos = [int(rng.integers(0, a)) for a in arity]
+    slot = [int(v) for v in rng.integers(0, 10_000, n_parts)]
+    src = [rng.integers(0, rows[p], n) for p, n in zip(part_ids, lens)]
+    dst = [rng.integers(0, 1000, n) for n in lens]
+    return values, src, dst, part_ids, arity, pos, slot
+
+
+def test_pack_oracle_invariants() -> None:
+    rng = np.random.default_rng(11)
+    values, src, dst, ids, arity, pos, slot = _random_edge_parts(rng, 4, 9)
+    offsets = np.cumsum([0] + [v.shape[0] for v in values])
+    x_cat, s_out, d_out = pack_oracle.fanout_pack_from_edges(values, src, dst, ids, arity, pos, slot)
+    assert np.array_equal(x_cat, np.concatenate(values))
+    bounds = np.cumsum([0] + [len(s) for s in src])
+    for i in range(len(src)):
+        seg = slice(bounds[i], bounds[i + 1])
+        assert np.array_equal(s_out[seg] - offsets[ids[i]], src[i])
+        q, r = np.divmod(d_out[seg] - slot[i], arity[i])
+        assert np.array_equal(q, dst[i]) and (r == pos[i]).all()
+        # the gathered rows are the rows of the named part
+        assert np.array_equal(x_cat[s_out[seg]], values[ids[i]][src[i]])
+    # arity 1, pos 0, slot 0 and parts in order: fanout_pack_multi
+    k = len(values)
+    multi = pack_oracle.fanout_pack_multi(values, src[:k], dst[:k])
+    edges = pack_oracle.fanout_pack_from_edges(values, src[:k], dst[:k], list(range(k)), [1] * k,
+                                               [0] * k, [0] * k)
+    for m, e in zip(multi, edges):
+        assert np.array_equal(m, e)
+
+    _, f_src, f_dst = pack_oracle.fanin_pack_from_edges(values, src, dst, ids, arity, pos, 0)
+    for i in range(len(src)):
+        seg = slice(bounds[i], bounds[i + 1])
+        q, r = np.divmod(f_src[seg] - offsets[ids[i]], arity[i])
+        assert np.array_equal(q, src[i]) and (r == pos[i]).all()
+        assert np.array_equal(f_dst[seg], dst[i])
+    label = pack_oracle.fanin_pack_from_edges(values, src[:k], dst[:k], list(range(k)), arity[:k],
+                                              pos[:k], 1)
+    for m, e in zip(pack_oracle.fanin_pack_multi(values, src[:k], dst[:k]), label):
+        assert np.array_equal(m, e)
+    # int64 arithmetic wraps as torch's does
+    _, s_big, d_big = pack_oracle.fanout_pack_from_edges(
+        values[:1], [np.array([0])], [np.array([2**62])], [0], [4], [1], [5])
+    assert d_big.tolist() == [(5 + 2**64 + 1) % 2**64]
+
+
+def _pack_calls(values, src, dst, ids, arity, pos, slot):
+    arrays = {f"v{i}": v for i, v in enumerate(values)}
+    arrays.update({f"s{i}": np.asarray(s, np.int64) for i, s in enumerate(src)})
+    arrays.update({f"d{i}": np.asarray(d, np.int64) for i, d in enumerate(dst)})
+    vn = [f"v{i}" for i in range(len(values))]
+    sn = [f"s{i}" for i in range(len(src))]
+    dn = [f"d{i}" for i in range(len(dst))]
+    k = len(values)
+    calls = [
+        {"op": "fanout_pack_multi", "args": [{"tensors": vn}, {"tensors": sn[:k]}, {"tensors": dn[:k]}]},
+        {"op": "fanin_pack_multi", "args": [{"tensors": vn}, {"tensors": sn[:k]}, {"tensors": dn[:k]}]},
+        {"op": "fanout_pack_from_edges", "args": [{"tensors": vn}, {"tensors": sn}, {"tensors": dn},
+                                                  {"ints": ids}, {"ints": arity}, {"ints": pos},
+                                                  {"ints": slot}]},
+        {"op": "fanin_pack_from_edges", "args": [{"tensors": vn}, {"tensors": sn}, {"tensors": dn},
+                                                 {"ints": ids}, {"ints": arity}, {"ints": pos},
+                                                 {"int": 0}]},
+        {"op": "fanin_pack_from_edges", "args": [{"tensors": vn}, {"tensors": sn}, {"tensors": dn},
+                                                 {"ints": ids}, {"ints": arity}, {"ints": pos},
+                                                 {"int": 1}]},
+    ]
+    expected = [
+        pack_oracle.fanout_pack_multi(values, src[:k], dst[:k]),
+        pack_oracle.fanin_pack_multi(values, src[:k], dst[:k]),
+        pack_oracle.fanout_pack_from_edges(values, src, dst, ids, arity, pos, slot),
+        pack_oracle.fanin_pack_from_edges(values, src, dst, ids, arity, pos, 0),
+        pack_oracle.fanin_pack_from_edges(values, src, dst, ids, arity, pos, 1),
+    ]
+    return arrays, calls, expected
+
+
+@pytest.mark.skipif(not ref_runner.available(), reason="oracle/_ref not built")
+def test_pack_oracle_matches_reference_library() -> None:
+    rng = np.random.default_rng(12)
+    for n_values, n_parts in [(1, 1), (3, 5), (4, 20)]:
+        case = _random_edge_parts(rng, n_values, n_parts)
+        arrays, calls, expected = _pack_calls(*case)
+        for res, want in zip(ref_runner.run_reference(calls, arrays), expected):
+            assert "error" not in res, res
+            for got, w in zip(res["outs"], want):
+                assert got.dtype == w.dtype and np.array_equal(got, w), res["op"]
+
+
+def test_pack_oracle_matches_every_golden_case(pack_golden) -> None:
+    cases, arrays = pack_golden
+    fns = {
+        "fanout_pack_multi": pack_oracle.fanout_pack_multi,
+        "fanin_pack_multi": pack_oracle.fanin_pack_multi,
+        "fanout_pack_from_edges": pack_oracle.fanout_pack_from_edges,
+        "fanin_pack_from_edges": pack_oracle.fanin_pack_from_edges,
+    }
+    checked = 0
+    for case in cases:
+        if "error" in case:
+            continue
+        args = []
+        for spec in case["args"]:
+            if "tensors" in spec:
+                args.append([arrays[n] for n in spec["tensors"]])
+            else:
+                args.append(spec.get("ints", spec.get("int")))
+        got = fns[case["op"]](*args)
+        for g, name in zip(got, case["expected"]):
+            want = arrays[name]
+            assert g.dtype == want.dtype and g.shape == want.shape, case["name"]
+            assert np.array_equal(g, want), case["name"]
+        checked += 1
+    assert checked >= 30
