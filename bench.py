@@ -120,10 +120,24 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         out = mp.fanin_reduce(rel, flat_src, dst, K, mode)
         torch.autograd.grad(out, rel, grad_out)
 
+    # The same topology handed over in new index tensors every step (a caller
+    # that rebuilds its routing per forward): the plan cache matches the
+    # contents against the cached entry's tensors instead of rebuilding.
+    fresh = iter([(flat_src.clone(), dst.clone()) for _ in range(steps + warmup)])
+
+    def step_same_topology():
+        s_idx, d_idx = next(fresh)
+        out = mp.fanin_reduce(rel, s_idx, d_idx, K, mode)
+        torch.autograd.grad(out, rel, grad_out)
+
     sync = torch.cuda.synchronize
     t_step = timed(step_uncached, steps, warmup, sync)
     t_bwd_step = statistics.fmean(a.elapsed_time(b) for a, b in bwd_events[-steps:]) / 1e3
     t_cached = timed(step_cached, steps, warmup, sync)
+    stats0 = ns.plan_cache_stats()
+    t_same = timed(step_same_topology, steps, warmup, sync)
+    content_hits = ns.plan_cache_stats()[2] - stats0[2]
+    del fresh
     ns.plan_cache_clear()
 
     # Kernel-only timings with prebuilt plans, HIP events on the launch stream.
@@ -152,6 +166,9 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         "bytes_fwd": b_fwd, "bytes_bwd": b_bwd,
         "ms_step": t_step * 1e3, "gbs_step": gbs(b_fwd + b_bwd, t_step),
         "ms_step_cached_plans": t_cached * 1e3, "gbs_step_cached_plans": gbs(b_fwd + b_bwd, t_cached),
+        "ms_step_same_topology_new_tensors": t_same * 1e3,
+        "gbs_step_same_topology_new_tensors": gbs(b_fwd + b_bwd, t_same),
+        "content_hits_same_topology": content_hits,
         "ms_fwd_kernels": t_fwd * 1e3, "gbs_fwd_kernels": gbs(b_fwd, t_fwd),
         "ms_bwd_in_step": t_bwd_step * 1e3, "gbs_bwd_in_step": gbs(b_bwd, t_bwd_step),
         "ms_bwd_kernel": t_bwd * 1e3, "gbs_bwd_kernel": gbs(b_bwd, t_bwd),

@@ -279,6 +279,25 @@ int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
                                        const void* rel_flat, int64_t emb, void* grad_rel,
                                        int64_t rel_rows, relm_mp_stream_t stream);
 
+/* ---- content match (plan reuse across equal indices) ----------------------- */
+
+/* No counterpart in the reference (its ops build their index structures in
+ * every call).  A caller that keeps plans (the torch binding's plan cache)
+ * uses this to reuse a plan for new index arrays whose contents equal those a
+ * plan was built from, e.g. the same topology rebuilt in every forward. */
+#define RELM_MP_MAX_MATCH 8
+
+size_t relm_mp_index_match_workspace_size(void);
+
+/* match[c] = 1 if keys[0..n) == cand_keys[c][0..n) and (when gathers is not
+ * NULL) gathers[0..n) == cand_gathers[c][0..n), else 0; 0 <= num_cand <=
+ * RELM_MP_MAX_MATCH.  All arrays are device memory; `match` is host memory.
+ * Enqueues one pass on `stream` and returns once the result is known. */
+int relm_mp_index_match(const int64_t* keys, const int64_t* gathers, int64_t n,
+                        const int64_t* const* cand_keys, const int64_t* const* cand_gathers,
+                        int32_t num_cand, int32_t* match, void* workspace, size_t workspace_bytes,
+                        relm_mp_stream_t stream);
+
 /* ---- index packing (the pack ops) -------------------------------------- */
 
 /* One part of a packing call: n index pairs (a[i], b[i]) written as

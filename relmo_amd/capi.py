@@ -56,6 +56,8 @@ EXPORTED_SYMBOLS = (
     "relm_mp_plan_logsumexp_backward",
     "relm_mp_plan_fanin_backward_by_dst",
     "relm_mp_pack_index",
+    "relm_mp_index_match_workspace_size",
+    "relm_mp_index_match",
 )
 
 
@@ -151,6 +153,12 @@ _SIGNATURES = {
     "relm_mp_plan_logsumexp_backward": (_int, [_int, _PP, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_fanin_backward_by_dst": (_int, [_int, _PP, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "relm_mp_pack_index": (_int, [ctypes.POINTER(IndexPart), ctypes.c_int32, _vp, _vp, _vp]),
+    "relm_mp_index_match_workspace_size": (_sz, []),
+    "relm_mp_index_match": (
+        _int,
+        [_vp, _vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.c_int32,
+         ctypes.POINTER(ctypes.c_int32), _vp, _sz, _vp],
+    ),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -512,3 +520,20 @@ def pack_index(parts: list[tuple], write_b: bool = True) -> tuple[torch.Tensor, 
     out_b = torch.empty(total, dtype=torch.int64, device=like.device) if write_b else None
     check(lib().relm_mp_pack_index(descs, len(parts), _ptr(out_a), _ptr(out_b), _stream(like)))
     return out_a, out_b
+
+
+def index_match(keys: torch.Tensor, gathers: torch.Tensor | None,
+                candidates: list[tuple[torch.Tensor, torch.Tensor | None]]) -> list[bool]:
+    """``relm_mp_index_match``: which candidate (keys, gathers) pairs equal the given pair."""
+
+    _check_index(keys)
+    if gathers is not None:
+        _check_index(gathers)
+    k = len(candidates)
+    ck = (_vp * max(k, 1))(*[_ptr(c[0]) for c in candidates])
+    cg = (_vp * max(k, 1))(*[_ptr(c[1]) if c[1] is not None else None for c in candidates])
+    match = (ctypes.c_int32 * max(k, 1))()
+    ws = _bytes(lib().relm_mp_index_match_workspace_size(), keys)
+    check(lib().relm_mp_index_match(_ptr(keys), _ptr(gathers), keys.numel(), ck, cg, k, match,
+                                    _ptr(ws), ws.numel(), _stream(keys)))
+    return [bool(match[i]) for i in range(k)]

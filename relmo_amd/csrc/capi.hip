@@ -121,6 +121,7 @@ struct HostSlot {
     DevStatus* status = nullptr;         // host address
     DevStatus* status_mapped = nullptr;  // the same memory as the device addresses it
     relm_mp_plan_counts* counts = nullptr;
+    int32_t* match = nullptr;  // host address, kMaxMatch flags
     PendingCheck pending;
 };
 
@@ -148,11 +149,14 @@ int host_slot(HostSlot** out) {
             // the kernel before it are visible once the event has completed
             RELM_HIP(hipEventCreateWithFlags(&h.ready, hipEventDisableTiming), "relm_mp event");
             void* mem = nullptr;
-            RELM_HIP(hipHostMalloc(&mem, sizeof(DevStatus) + sizeof(relm_mp_plan_counts),
+            RELM_HIP(hipHostMalloc(&mem,
+                                   sizeof(DevStatus) + sizeof(relm_mp_plan_counts) +
+                                       kMaxMatch * sizeof(int32_t),
                                    hipHostMallocDefault),
                      "relm_mp pinned status");
             h.status = static_cast<DevStatus*>(mem);
             h.counts = reinterpret_cast<relm_mp_plan_counts*>(static_cast<char*>(mem) + sizeof(DevStatus));
+            h.match = reinterpret_cast<int32_t*>(h.counts + 1);
             void* mapped = nullptr;
             RELM_HIP(hipHostGetDevicePointer(&mapped, mem, 0), "relm_mp pinned status mapping");
             h.status_mapped = static_cast<DevStatus*>(mapped);
@@ -466,6 +470,37 @@ int relm_mp_inv_plan_build_async(const int64_t* keys, int64_t key_bound, const c
     return inv_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
                      gather_checked_first, num_edges, plan_mem, plan_bytes, plan, false,
                      static_cast<hipStream_t>(stream));
+}
+
+size_t relm_mp_index_match_workspace_size(void) { return kMaxMatch * sizeof(int32_t); }
+
+int relm_mp_index_match(const int64_t* keys, const int64_t* gathers, int64_t n,
+                        const int64_t* const* cand_keys, const int64_t* const* cand_gathers,
+                        int32_t num_cand, int32_t* match, void* workspace, size_t workspace_bytes,
+                        relm_mp_stream_t stream) {
+    if (n < 0 || num_cand < 0 || num_cand > kMaxMatch || (num_cand > 0 && match == nullptr))
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: bad index match arguments");
+    if (num_cand == 0) return RELM_MP_OK;
+    if (n > 0 && keys == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: keys are NULL");
+    for (int32_t c = 0; c < num_cand; ++c)
+        if (n > 0 && (cand_keys == nullptr || cand_keys[c] == nullptr ||
+                      (gathers != nullptr && (cand_gathers == nullptr || cand_gathers[c] == nullptr))))
+            return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: candidate arrays are NULL");
+    if (workspace == nullptr || workspace_bytes < relm_mp_index_match_workspace_size() ||
+        (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: index match workspace missing or too small");
+    HostSlot* hs = nullptr;
+    RELM_TRY(host_slot(&hs));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int32_t* flags = static_cast<int32_t*>(workspace);
+    RELM_HIP(launch_index_match(keys, gathers, n, cand_keys, cand_gathers, num_cand, flags, s),
+             "relm_mp index match kernel");
+    RELM_HIP(hipMemcpyAsync(hs->match, flags, kMaxMatch * sizeof(int32_t), hipMemcpyDeviceToHost, s),
+             "relm_mp index match copy");
+    RELM_HIP(hipStreamSynchronize(s), "relm_mp index match sync");
+    for (int32_t c = 0; c < num_cand; ++c) match[c] = hs->match[c] == 0 ? 1 : 0;
+    return RELM_MP_OK;
 }
 
 int relm_mp_pack_index(const relm_mp_index_part* parts, int32_t num_parts, int64_t* out_a,

@@ -116,6 +116,14 @@ inline int64_t max_chunks(int64_t num_edges) {
 hipError_t launch_pack_index(const relm_mp_index_part* parts, int num_parts, int64_t* out_a,
                              int64_t* out_b, hipStream_t s);
 
+// ---- content comparison (match_kernels.hip) -------------------------------
+constexpr int kMaxMatch = RELM_MP_MAX_MATCH;
+// mismatch[0..kMaxMatch) is cleared, then mismatch[c] != 0 iff candidate c
+// differs from (keys, gathers); gathers may be null (keys only).
+hipError_t launch_index_match(const int64_t* keys, const int64_t* gathers, int64_t n,
+                              const int64_t* const* cand_keys, const int64_t* const* cand_gathers,
+                              int num_cand, int32_t* mismatch, hipStream_t s);
+
 // ---- compute kernels (reduce_kernels.hip) --------------------------------
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
                         const void* table, int64_t emb, void* out, hipStream_t s);

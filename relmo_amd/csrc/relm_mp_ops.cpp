@@ -18,6 +18,7 @@
 #include <c10/util/intrusive_ptr.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -100,11 +101,19 @@ Tensor byte_buffer(size_t bytes, const Tensor& like) {
 
 // ---- plan cache -------------------------------------------------------------
 //
-// Plans depend only on the index tensors and bounds.  An entry is reused when
-// the same TensorImpl objects (held weakly, so a dead tensor's address cannot
-// be recycled while the entry exists) are passed again with unchanged version
-// counters.  RELM_MP_PLAN_CACHE=0 disables reuse; RELM_MP_PLAN_CACHE_MB bounds
-// the cached plan memory (default 4096).
+// Plans depend only on the index tensors' contents and the bounds.  An entry
+// is reused when
+//   * the same TensorImpl objects are passed again with unchanged version
+//     counters (identity), or
+//   * other tensors of the same length and bounds hold the same indices
+//     (content: one device pass compares them with the entry's tensors, which
+//     the entry keeps alive for that purpose, and the entry then moves to the
+//     new tensors) - the same topology rebuilt in every forward.
+// RELM_MP_PLAN_CACHE=0 disables reuse; RELM_MP_PLAN_CACHE=identity keeps only
+// identity reuse (entries hold the tensors weakly and die with them, so a dead
+// tensor's address cannot be recycled while the entry exists);
+// RELM_MP_PLAN_CACHE_MB bounds the memory of the entries, plans and kept index
+// tensors (default 4096).
 
 enum PlanRole : int {
     kRoleInverse = 1,
@@ -117,6 +126,8 @@ struct PlanEntry {
     int role = 0;
     c10::weak_intrusive_ptr<c10::TensorImpl> key_w;
     c10::weak_intrusive_ptr<c10::TensorImpl> gather_w;
+    Tensor key_t;  // content mode: the indices the plan was built from
+    Tensor gather_t;
     const c10::TensorImpl* key_impl = nullptr;
     const c10::TensorImpl* gather_impl = nullptr;
     uint32_t key_ver = 0;
@@ -141,7 +152,7 @@ class PlanCache {
     bool enabled() const { return enabled_; }
 
     bool lookup(int role, const Tensor& key, const Tensor& gather, int64_t key_bound,
-                int64_t gather_bound, relm_mp_plan* out) {
+                int64_t gather_bound, relm_mp_plan* out, hipStream_t s) {
         if (!enabled_ || !cacheable(key) || !cacheable(gather)) return false;
         std::lock_guard<std::mutex> lock(mu_);
         purge_dead_locked();
@@ -152,10 +163,14 @@ class PlanCache {
                 e.gather_bound == gather_bound && e.num_edges == key.numel() &&
                 e.device == key.get_device()) {
                 e.stamp = ++clock_;
+                ++identity_hits_;
                 *out = e.plan;
                 return true;
             }
         }
+        if (content_ && lookup_content_locked(role, key, gather, key_bound, gather_bound, out, s))
+            return true;
+        ++misses_;
         return false;
     }
 
@@ -185,6 +200,10 @@ class PlanCache {
         if (!enabled_ || !cacheable(key) || !cacheable(gather)) return;
         std::lock_guard<std::mutex> lock(mu_);
         PlanEntry e(key, gather);
+        if (content_) {
+            e.key_t = key;
+            e.gather_t = gather;
+        }
         e.role = role;
         e.key_impl = key.unsafeGetTensorImpl();
         e.gather_impl = gather.unsafeGetTensorImpl();
@@ -196,7 +215,8 @@ class PlanCache {
         e.device = key.get_device();
         e.mem = mem;
         e.plan = plan;
-        e.bytes = static_cast<size_t>(mem.numel());
+        e.bytes = static_cast<size_t>(mem.numel()) +
+                  (content_ ? static_cast<size_t>(key.nbytes() + gather.nbytes()) : 0);
         e.stamp = ++clock_;
         total_ += e.bytes;
         entries_.push_back(std::move(e));
@@ -215,6 +235,13 @@ class PlanCache {
         total_ = 0;
     }
 
+    // entries, identity hits, content hits, misses (lookups that built a plan)
+    std::vector<int64_t> stats() {
+        std::lock_guard<std::mutex> lock(mu_);
+        purge_dead_locked();
+        return {static_cast<int64_t>(entries_.size()), identity_hits_, content_hits_, misses_};
+    }
+
     int64_t size() {
         std::lock_guard<std::mutex> lock(mu_);
         purge_dead_locked();
@@ -230,6 +257,7 @@ class PlanCache {
             std::string v(flag);
             for (char& c : v) c = static_cast<char>(std::tolower(static_cast<unsigned char>(c)));
             enabled_ = !(v == "0" || v == "false" || v == "no" || v == "off");
+            content_ = v != "identity";
         }
         const char* mb = std::getenv("RELM_MP_PLAN_CACHE_MB");
         if (mb != nullptr) limit_ = static_cast<size_t>(std::strtoull(mb, nullptr, 10)) << 20;
@@ -239,6 +267,64 @@ class PlanCache {
 
     static uint32_t version(const Tensor& t) {
         return t.unsafeGetTensorImpl()->version_counter().current_version();
+    }
+
+    // Entries of the same role, device, length and bounds whose kept tensors
+    // are unchanged are compared with (key, gather) on the device (at most
+    // kMaxMatch, most recent first); an equal one serves and moves to the new
+    // tensors.  Entries whose kept tensors were modified in place are dropped.
+    bool lookup_content_locked(int role, const Tensor& key, const Tensor& gather,
+                               int64_t key_bound, int64_t gather_bound, relm_mp_plan* out,
+                               hipStream_t s) {
+        std::vector<size_t> cand;
+        for (size_t i = 0; i < entries_.size();) {
+            PlanEntry& e = entries_[i];
+            if (e.key_t.defined() && (version(e.key_t) != e.key_ver || version(e.gather_t) != e.gather_ver)) {
+                total_ -= e.bytes;
+                entries_.erase(entries_.begin() + static_cast<std::ptrdiff_t>(i));
+                continue;
+            }
+            if (e.key_t.defined() && e.role == role && e.key_bound == key_bound &&
+                e.gather_bound == gather_bound && e.num_edges == key.numel() &&
+                e.device == key.get_device())
+                cand.push_back(i);
+            ++i;
+        }
+        if (cand.empty()) return false;
+        std::sort(cand.begin(), cand.end(),
+                  [&](size_t a, size_t b) { return entries_[a].stamp > entries_[b].stamp; });
+        if (cand.size() > RELM_MP_MAX_MATCH) cand.resize(RELM_MP_MAX_MATCH);
+        std::vector<const int64_t*> ck, cg;
+        for (size_t i : cand) {
+            ck.push_back(entries_[i].key_t.data_ptr<int64_t>());
+            cg.push_back(entries_[i].gather_t.data_ptr<int64_t>());
+        }
+        std::vector<int32_t> match(cand.size(), 0);
+        Tensor ws = byte_buffer(relm_mp_index_match_workspace_size(), key);
+        raise_if(relm_mp_index_match(key.data_ptr<int64_t>(), gather.data_ptr<int64_t>(),
+                                     key.numel(), ck.data(), cg.data(),
+                                     static_cast<int32_t>(cand.size()), match.data(), ws.data_ptr(),
+                                     static_cast<size_t>(ws.numel()), s));
+        for (size_t j = 0; j < cand.size(); ++j) {
+            if (!match[j]) continue;
+            PlanEntry& e = entries_[cand[j]];
+            total_ -= e.bytes;
+            e.key_w = key.getIntrusivePtr();
+            e.gather_w = gather.getIntrusivePtr();
+            e.key_t = key;
+            e.gather_t = gather;
+            e.key_impl = key.unsafeGetTensorImpl();
+            e.gather_impl = gather.unsafeGetTensorImpl();
+            e.key_ver = version(key);
+            e.gather_ver = version(gather);
+            e.bytes = static_cast<size_t>(e.mem.numel() + key.nbytes() + gather.nbytes());
+            total_ += e.bytes;
+            e.stamp = ++clock_;
+            ++content_hits_;
+            *out = e.plan;
+            return true;
+        }
+        return false;
     }
 
     void purge_dead_locked() {
@@ -257,7 +343,11 @@ class PlanCache {
     size_t total_ = 0;
     size_t limit_ = size_t(4096) << 20;
     uint64_t clock_ = 0;
+    int64_t identity_hits_ = 0;
+    int64_t content_hits_ = 0;
+    int64_t misses_ = 0;
     bool enabled_ = true;
+    bool content_ = true;
 };
 
 struct GpuPlan {
@@ -270,7 +360,7 @@ GpuPlan inverse_plan(const Tensor& key, int64_t key_bound, const char* key_name,
                      bool gather_first, hipStream_t s) {
     GpuPlan gp;
     PlanCache& cache = PlanCache::get();
-    if (cache.lookup(kRoleInverse, key, gather, key_bound, gather_bound, &gp.plan)) return gp;
+    if (cache.lookup(kRoleInverse, key, gather, key_bound, gather_bound, &gp.plan, s)) return gp;
     gp.mem = byte_buffer(relm_mp_inv_plan_bytes(key_bound), key);
     raise_if(relm_mp_inv_plan_build(key.data_ptr<int64_t>(), key_bound, key_name,
                                     gather.data_ptr<int64_t>(), gather_bound, gather_name,
@@ -284,7 +374,7 @@ GpuPlan csr_plan(const Tensor& key, int64_t key_bound, const char* key_name, con
                  int64_t gather_bound, const char* gather_name, bool gather_first, hipStream_t s) {
     GpuPlan gp;
     PlanCache& cache = PlanCache::get();
-    if (cache.lookup(kRoleCsr, key, gather, key_bound, gather_bound, &gp.plan)) return gp;
+    if (cache.lookup(kRoleCsr, key, gather, key_bound, gather_bound, &gp.plan, s)) return gp;
     const int64_t n = key.numel();
     gp.mem = byte_buffer(relm_mp_csr_plan_bytes(key_bound, n), key);
     Tensor scratch = byte_buffer(relm_mp_csr_plan_scratch_bytes(key_bound, n), key);
@@ -322,7 +412,7 @@ Tensor fanout_scatter_gpu(const Tensor& x_cat, const Tensor& src, const Tensor& 
     Tensor out = at::empty({out_rows, emb}, x_cat.options());
     PlanCache& cache = PlanCache::get();
     GpuPlan gp;
-    if (cache.lookup(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), &gp.plan)) {
+    if (cache.lookup(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), &gp.plan, stream)) {
         raise_if(relm_mp_plan_gather_last(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
                                           x.data_ptr(), emb, out.data_ptr(), stream));
         return out;
@@ -964,6 +1054,8 @@ void plan_cache_clear() { PlanCache::get().clear(); }
 
 int64_t plan_cache_size() { return PlanCache::get().size(); }
 
+std::vector<int64_t> plan_cache_stats() { return PlanCache::get().stats(); }
+
 }  // namespace relm_amd
 
 TORCH_LIBRARY(relm_mp, m) {
@@ -980,6 +1072,7 @@ TORCH_LIBRARY(relm_mp, m) {
     // No reference counterpart: control of the index-plan cache.
     m.def("plan_cache_clear() -> ()");
     m.def("plan_cache_size() -> int");
+    m.def("plan_cache_stats() -> int[]");
 }
 
 TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
@@ -995,4 +1088,5 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("build_info", relm_amd::build_info);
     m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
     m.impl("plan_cache_size", relm_amd::plan_cache_size);
+    m.impl("plan_cache_stats", relm_amd::plan_cache_stats);
 }
