@@ -279,6 +279,24 @@ int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
                                        const void* rel_flat, int64_t emb, void* grad_rel,
                                        int64_t rel_rows, relm_mp_stream_t stream);
 
+/* ---- row epilogues (the LGAN indexed reductions) ------------------------- */
+
+#define RELM_MP_DIV_NONE 0    /* d_j = 1                                          */
+#define RELM_MP_DIV_SEGMENT 1 /* d_j = max(1, div_offsets[j+1] - div_offsets[j])  */
+#define RELM_MP_DIV_VALUES 2  /* d_j = max(1, (T)div_values[j])                   */
+
+/* For r < rows: j = gather ? gather[r] : r (gather: valid rows of `in` and of
+ * the divisor array), out[r] = base[r] + in[j] / d_j; `in` NULL reads zeros,
+ * `base` NULL adds nothing (out = in[j] / d_j).  out may equal base, or in
+ * when gather is NULL.  The epilogues of the reference's LGAN aggregations
+ * (relm::mp::lgan_pool_reduce / _relation_graph_step and their backward,
+ * mp_ops.cpp:3350-3743): division by the arity or the message count, the
+ * residual addition, the per-slot gradient; with div_offsets the offsets of a
+ * CSR plan keyed by the aggregation's destinations.  Row-major [*, emb]. */
+int relm_mp_rows_scale(int dtype, const void* in, const int64_t* gather, int div_kind,
+                       const int32_t* div_offsets, const int64_t* div_values, const void* base,
+                       int64_t rows, int64_t emb, void* out, relm_mp_stream_t stream);
+
 /* ---- content match (plan reuse across equal indices) ----------------------- */
 
 /* No counterpart in the reference (its ops build their index structures in

@@ -36,6 +36,10 @@ OPS = {
     "fanin_pack_multi": 0,
     "fanout_pack_from_edges": 0,
     "fanin_pack_from_edges": 0,
+    "lgan_pool_reduce": 0,
+    "lgan_pool_reduce_backward": 0,
+    "lgan_relation_graph_step": 0,
+    "lgan_relation_graph_step_backward": 0,
 }
 
 

@@ -58,6 +58,7 @@ EXPORTED_SYMBOLS = (
     "relm_mp_pack_index",
     "relm_mp_index_match_workspace_size",
     "relm_mp_index_match",
+    "relm_mp_rows_scale",
 )
 
 
@@ -154,6 +155,7 @@ _SIGNATURES = {
     "relm_mp_plan_fanin_backward_by_dst": (_int, [_int, _PP, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "relm_mp_pack_index": (_int, [ctypes.POINTER(IndexPart), ctypes.c_int32, _vp, _vp, _vp]),
     "relm_mp_index_match_workspace_size": (_sz, []),
+    "relm_mp_rows_scale": (_int, [_int, _vp, _vp, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "relm_mp_index_match": (
         _int,
         [_vp, _vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.c_int32,
@@ -537,3 +539,18 @@ def index_match(keys: torch.Tensor, gathers: torch.Tensor | None,
     check(lib().relm_mp_index_match(_ptr(keys), _ptr(gathers), keys.numel(), ck, cg, k, match,
                                     _ptr(ws), ws.numel(), _stream(keys)))
     return [bool(match[i]) for i in range(k)]
+
+
+DIV_NONE, DIV_SEGMENT, DIV_VALUES = 0, 1, 2
+
+
+def rows_scale(inp: torch.Tensor | None, rows: int, emb: int, like: torch.Tensor, *,
+               gather: torch.Tensor | None = None, div_kind: int = DIV_NONE,
+               div_offsets: torch.Tensor | None = None, div_values: torch.Tensor | None = None,
+               base: torch.Tensor | None = None) -> torch.Tensor:
+    """``relm_mp_rows_scale`` into a new [rows, emb] tensor of like's dtype."""
+
+    out = torch.empty(rows, emb, dtype=like.dtype, device=like.device)
+    check(lib().relm_mp_rows_scale(_dtype(like), _ptr(inp), _ptr(gather), div_kind, _ptr(div_offsets),
+                                   _ptr(div_values), _ptr(base), rows, emb, _ptr(out), _stream(like)))
+    return out

@@ -472,6 +472,21 @@ int relm_mp_inv_plan_build_async(const int64_t* keys, int64_t key_bound, const c
                      static_cast<hipStream_t>(stream));
 }
 
+int relm_mp_rows_scale(int dtype, const void* in, const int64_t* gather, int div_kind,
+                       const int32_t* div_offsets, const int64_t* div_values, const void* base,
+                       int64_t rows, int64_t emb, void* out, relm_mp_stream_t stream) {
+    if (dtype != RELM_MP_F32 && dtype != RELM_MP_F64)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: dtype must be F32 or F64");
+    if (rows < 0 || emb < 0 || div_kind < RELM_MP_DIV_NONE || div_kind > RELM_MP_DIV_VALUES)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: bad row scale arguments");
+    if (rows > 0 && emb > 0 &&
+        (out == nullptr || (div_kind == RELM_MP_DIV_SEGMENT && div_offsets == nullptr) ||
+         (div_kind == RELM_MP_DIV_VALUES && div_values == nullptr)))
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: row scale arrays are NULL");
+    return compute_rows_scale(dtype, in, gather, div_kind, div_offsets, div_values, base, rows, emb,
+                              out, static_cast<hipStream_t>(stream));
+}
+
 size_t relm_mp_index_match_workspace_size(void) { return kMaxMatch * sizeof(int32_t); }
 
 int relm_mp_index_match(const int64_t* keys, const int64_t* gathers, int64_t n,

@@ -135,6 +135,9 @@ int compute_logsumexp_backward(int dtype, const relm_mp_plan& plan, const int64_
                                int64_t emb, void* grad_rel, void* scratch, size_t scratch_bytes,
                                hipStream_t s);
 int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t s);
+int compute_rows_scale(int dtype, const void* in, const int64_t* gather, int div_kind,
+                       const int32_t* div_offsets, const int64_t* div_values, const void* base,
+                       int64_t rows, int64_t emb, void* out, hipStream_t s);
 // Backward of fanin_reduce (mode 0 / 1) over a CSR plan keyed by destination
 // whose gathered rows are the identity (plan.gather_identity); rows
 // [num_edges, rel_rows) of grad_rel become zero.

@@ -724,6 +724,46 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
     }
 }
 
+// Row epilogues of the LGAN aggregations: out[r] = base[r] + in[j] / d_j with
+// j = gather[r] (or r), d_j = 1, max(1, segment size j of a CSR plan) or
+// max(1, (T)div_values[j]); `in` null reads zeros, `base` null adds nothing.
+// The division and the addition round separately, as the reference's
+// tensor expressions do.
+template <typename T, int V, int G>
+__global__ __launch_bounds__(kThreads) void k_rows_scale(
+    const T* in, const int64_t* __restrict__ gather, int div_kind,
+    const int32_t* __restrict__ div_offsets, const int64_t* __restrict__ div_values,
+    const T* base, int64_t rows, int64_t D, T* out) {
+    constexpr int R = kThreads / G;
+    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
+    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
+    if (col >= D) return;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; r < rows;
+         r += static_cast<int64_t>(gridDim.x) * R) {
+        const int64_t j = gather != nullptr ? gather[r] : r;
+        T d = T(1);
+        if (div_kind == RELM_MP_DIV_SEGMENT) {
+            const int32_t n = div_offsets[j + 1] - div_offsets[j];
+            d = n > 1 ? static_cast<T>(n) : T(1);
+        } else if (div_kind == RELM_MP_DIV_VALUES) {
+            const T v = static_cast<T>(div_values[j]);
+            d = v > T(1) ? v : T(1);
+        }
+        Pack<T, V> x = in != nullptr ? pack_load<T, V>(in + row_offset(j, D) + col)
+                                     : pack_fill<T, V>(T(0));
+        if (div_kind != RELM_MP_DIV_NONE) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) x.v[i] = x.v[i] / d;
+        }
+        if (base != nullptr) {
+            const Pack<T, V> b = pack_load<T, V>(base + r * D + col);
+#pragma unroll
+            for (int i = 0; i < V; ++i) x.v[i] = b.v[i] + x.v[i];
+        }
+        pack_store<T, V>(out + r * D + col, x);
+    }
+}
+
 // out[k] = table[gather of the last edge of segment k] or 0 (CSR plans).
 template <typename T, int V, int G>
 __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __restrict__ offsets,
@@ -1033,6 +1073,35 @@ int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t 
                            static_cast<float*>(out), count, static_cast<float>(value));
     }
     return hip_error(hipGetLastError(), "relm_mp fill kernel");
+}
+
+template <typename T>
+int rows_scale_t(const void* in_v, const int64_t* gather, int div_kind, const int32_t* div_offsets,
+                 const int64_t* div_values, const void* base_v, int64_t rows, int64_t emb,
+                 void* out_v, hipStream_t s) {
+    const T* in = static_cast<const T*>(in_v);
+    const T* base = static_cast<const T*>(base_v);
+    T* out = static_cast<T*>(out_v);
+    const Geometry geo = choose_geometry<T>(emb, {in, base, out});
+    return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
+        constexpr int V = decltype(vt)::value;
+        constexpr int G = decltype(gt)::value;
+        hipLaunchKernelGGL((k_rows_scale<T, V, G>), row_grid(rows, G, geo.slices), dim3(kThreads),
+                           0, s, in, gather, div_kind, div_offsets, div_values, base, rows, emb,
+                           out);
+        return hip_error(hipGetLastError(), "relm_mp row scale kernel");
+    });
+}
+
+int compute_rows_scale(int dtype, const void* in, const int64_t* gather, int div_kind,
+                       const int32_t* div_offsets, const int64_t* div_values, const void* base,
+                       int64_t rows, int64_t emb, void* out, hipStream_t s) {
+    if (rows <= 0 || emb <= 0) return RELM_MP_OK;
+    return dtype == RELM_MP_F64
+               ? rows_scale_t<double>(in, gather, div_kind, div_offsets, div_values, base, rows,
+                                      emb, out, s)
+               : rows_scale_t<float>(in, gather, div_kind, div_offsets, div_values, base, rows, emb,
+                                     out, s);
 }
 
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,

@@ -118,6 +118,7 @@ Tensor byte_buffer(size_t bytes, const Tensor& like) {
 enum PlanRole : int {
     kRoleInverse = 1,
     kRoleCsr = 2,
+    kRoleCsrRows = 3,  // CSR plan whose gathered rows are the edges themselves
 };
 
 struct PlanEntry {
@@ -386,6 +387,23 @@ GpuPlan csr_plan(const Tensor& key, int64_t key_bound, const char* key_name, con
                                           static_cast<size_t>(gp.mem.numel()), scratch.data_ptr(),
                                           static_cast<size_t>(scratch.numel()), &gp.plan, s));
     cache.insert(kRoleCsr, key, gather, key_bound, gather_bound, gp.mem, gp.plan);
+    return gp;
+}
+
+// CSR plan keyed by `key` whose message e reads row e (no gather array); the
+// cache entry uses `key` in the gather position.
+GpuPlan csr_plan_rows(const Tensor& key, int64_t key_bound, const char* key_name, hipStream_t s) {
+    GpuPlan gp;
+    PlanCache& cache = PlanCache::get();
+    const int64_t n = key.numel();
+    if (cache.lookup(kRoleCsrRows, key, key, key_bound, n, &gp.plan, s)) return gp;
+    gp.mem = byte_buffer(relm_mp_csr_plan_bytes(key_bound, n), key);
+    Tensor scratch = byte_buffer(relm_mp_csr_plan_scratch_bytes(key_bound, n), key);
+    raise_if(relm_mp_csr_plan_build_async(key.data_ptr<int64_t>(), key_bound, key_name, nullptr, n,
+                                          "", 0, n, gp.mem.data_ptr(),
+                                          static_cast<size_t>(gp.mem.numel()), scratch.data_ptr(),
+                                          static_cast<size_t>(scratch.numel()), &gp.plan, s));
+    cache.insert(kRoleCsrRows, key, key, key_bound, n, gp.mem, gp.plan);
     return gp;
 }
 
@@ -1045,6 +1063,340 @@ std::tuple<Tensor, Tensor, Tensor> fanin_pack_from_edges(
     return std::make_tuple(rel_cat, flat_src, dst_idx);
 }
 
+// ---- LGAN indexed reductions (mp_ops.cpp:3350-3743) ---------------------------
+//
+// Relation instances pool their slots (sum / arity), take one residual
+// aggregation step over relation-relation edges and aggregate onto entities
+// over two edge sets (tn, nn); sum (0) or mean (2) per destination.  GPU lane
+// (float32 / float64 CUDA tensors of one dtype): every aggregation is a CSR
+// segment sum (edge order inside each destination) followed by one row
+// epilogue (relm_mp_rows_scale: division by the count or arity, residual
+// addition), the backward the transposed sums over plans keyed by the
+// sources.  Other tensors: the reference's tensor sequence.
+
+constexpr int64_t kModeMean = 2;
+
+void check_int32_or_int64_index(const Tensor& t, const char* name) {
+    check_rank(t, 1, name);
+    TORCH_CHECK(t.scalar_type() == at::kLong || t.scalar_type() == at::kInt, name,
+                " must have dtype torch.int64 or torch.int32.");
+}
+
+bool same_device(const Tensor& ref, std::initializer_list<const Tensor*> ts) {
+    for (const Tensor* t : ts)
+        if (t->device() != ref.device()) return false;
+    return true;
+}
+
+// Sum (mean) of src_rows[s[e]] onto rows t[e] of a [dim, emb] result.
+Tensor lgan_aggregate_aten(const Tensor& src_rows, const Tensor& s, const Tensor& t, int64_t dim,
+                           int64_t mode) {
+    Tensor out = at::zeros({dim, src_rows.size(1)}, src_rows.options());
+    if (s.numel() == 0 || t.numel() == 0 || dim == 0) return out;
+    out.index_add_(0, t, src_rows.index_select(0, s));
+    if (mode == kModeMean) {
+        Tensor count = at::zeros({dim, 1}, src_rows.options());
+        count.index_add_(0, t, at::ones({t.size(0), 1}, src_rows.options()));
+        out = out / count.clamp_min_(1.0);
+    }
+    return out;
+}
+
+// Transpose of lgan_aggregate_aten: rows s[e] of a [src_rows, emb] result
+// receive grad[t[e]] (divided by the messages into t[e] in mean mode).
+Tensor lgan_reverse_aten(const Tensor& grad, const Tensor& s, const Tensor& t, int64_t src_rows,
+                         int64_t mode) {
+    Tensor out = at::zeros({src_rows, grad.size(1)}, grad.options());
+    if (s.numel() == 0 || t.numel() == 0 || src_rows == 0) return out;
+    Tensor msgs = grad.index_select(0, t);
+    if (mode == kModeMean) {
+        Tensor count = at::zeros({grad.size(0), 1}, grad.options());
+        count.index_add_(0, t, at::ones({t.size(0), 1}, grad.options()));
+        msgs = msgs / count.index_select(0, t).clamp_min_(1.0);
+    }
+    out.index_add_(0, s, msgs);
+    return out;
+}
+
+Tensor index64(const Tensor& t) {
+    return contiguous(t.scalar_type() == at::kLong ? t : t.to(at::kLong));
+}
+
+bool lgan_gpu_lane(std::initializer_list<const Tensor*> values) {
+    const Tensor& ref = **values.begin();
+    if (!ref.is_cuda() || !is_fastpath_dtype(ref.scalar_type())) return false;
+    for (const Tensor* v : values)
+        if (v->scalar_type() != ref.scalar_type() || v->size(1) != ref.size(1)) return false;
+    return true;
+}
+
+const void* ptr_or_null(const Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
+
+// base + (sum or mean of src_rows[s[e]] onto rows t[e]); base may be undefined.
+Tensor lgan_aggregate_gpu(const Tensor& src_rows, const Tensor& s, const Tensor& t, int64_t dim,
+                          int64_t mode, const Tensor& base, const char* s_name, const char* t_name,
+                          hipStream_t st) {
+    const int64_t D = src_rows.size(1);
+    const int dt = dtype_code(src_rows);
+    Tensor out = at::empty({dim, D}, src_rows.options());
+    if (dim == 0 || D == 0) return out;
+    if (s.numel() == 0 || t.numel() == 0) {
+        raise_if(relm_mp_rows_scale(dt, nullptr, nullptr, RELM_MP_DIV_NONE, nullptr, nullptr,
+                                    ptr_or_null(base), dim, D, out.data_ptr(), st));
+        return out;
+    }
+    GpuPlan gp = csr_plan(t, dim, t_name, s, src_rows.size(0), s_name, true, st);
+    Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, src_rows);
+    raise_if(relm_mp_plan_segment_reduce(dt, &gp.plan, nullptr, src_rows.data_ptr(), D, kModeSum,
+                                         out.data_ptr(), scratch.data_ptr(),
+                                         static_cast<size_t>(scratch.numel()), st));
+    if (mode == kModeMean || base.defined())
+        raise_if(relm_mp_rows_scale(dt, out.data_ptr(), nullptr,
+                                    mode == kModeMean ? RELM_MP_DIV_SEGMENT : RELM_MP_DIV_NONE,
+                                    gp.plan.offsets, nullptr, ptr_or_null(base), dim, D,
+                                    out.data_ptr(), st));
+    return out;
+}
+
+// base + transpose of the aggregation (s, t): rows s[e] of [src_rows, emb]
+// receive grad[t[e]] (divided by the messages into t[e] in mean mode).
+Tensor lgan_reverse_gpu(const Tensor& grad, const Tensor& s, const Tensor& t, int64_t src_rows,
+                        int64_t mode, const Tensor& base, const char* s_name, const char* t_name,
+                        hipStream_t st) {
+    const int64_t D = grad.size(1);
+    const int dt = dtype_code(grad);
+    Tensor out = at::empty({src_rows, D}, grad.options());
+    if (src_rows == 0 || D == 0) return out;
+    if (s.numel() == 0 || t.numel() == 0) {
+        raise_if(relm_mp_rows_scale(dt, nullptr, nullptr, RELM_MP_DIV_NONE, nullptr, nullptr,
+                                    ptr_or_null(base), src_rows, D, out.data_ptr(), st));
+        return out;
+    }
+    Tensor table = grad;
+    if (mode == kModeMean) {
+        // message counts per grad row: the segment sizes of the forward's plan
+        GpuPlan fwd = csr_plan(t, grad.size(0), t_name, s, src_rows, s_name, true, st);
+        table = at::empty_like(grad);
+        raise_if(relm_mp_rows_scale(dt, grad.data_ptr(), nullptr, RELM_MP_DIV_SEGMENT,
+                                    fwd.plan.offsets, nullptr, nullptr, grad.size(0), D,
+                                    table.data_ptr(), st));
+    }
+    GpuPlan gp = csr_plan(s, src_rows, s_name, t, grad.size(0), t_name, false, st);
+    Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, grad);
+    raise_if(relm_mp_plan_segment_reduce(dt, &gp.plan, nullptr, table.data_ptr(), D, kModeSum,
+                                         out.data_ptr(), scratch.data_ptr(),
+                                         static_cast<size_t>(scratch.numel()), st));
+    if (base.defined())
+        raise_if(relm_mp_rows_scale(dt, out.data_ptr(), nullptr, RELM_MP_DIV_NONE, nullptr, nullptr,
+                                    base.data_ptr(), src_rows, D, out.data_ptr(), st));
+    return out;
+}
+
+struct LganEdges {
+    Tensor rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent;
+};
+
+LganEdges lgan_edges64(const Tensor& rr_src, const Tensor& rr_dst, const Tensor& tn_rel,
+                       const Tensor& tn_ent, const Tensor& nn_rel, const Tensor& nn_ent) {
+    return {index64(rr_src), index64(rr_dst), index64(tn_rel),
+            index64(tn_ent), index64(nn_rel), index64(nn_ent)};
+}
+
+std::tuple<Tensor, Tensor, Tensor> lgan_step_gpu(const Tensor& x, const LganEdges& g,
+                                                 int64_t entity_dim_size, int64_t mode,
+                                                 hipStream_t st) {
+    const int64_t K = x.size(0);
+    Tensor upd = lgan_aggregate_gpu(x, g.rr_src, g.rr_dst, K, mode, x, "rr_src", "rr_dst", st);
+    Tensor tn = lgan_aggregate_gpu(upd, g.tn_rel, g.tn_ent, entity_dim_size, mode, Tensor(),
+                                   "tn_rel", "tn_ent", st);
+    Tensor nn = lgan_aggregate_gpu(upd, g.nn_rel, g.nn_ent, entity_dim_size, mode, Tensor(),
+                                   "nn_rel", "nn_ent", st);
+    return std::make_tuple(upd, tn, nn);
+}
+
+Tensor lgan_step_backward_gpu(const Tensor& g, const Tensor& g_tn, const Tensor& g_nn,
+                              const LganEdges& e, int64_t K, int64_t mode, hipStream_t st) {
+    Tensor g1 = lgan_reverse_gpu(g_tn, e.tn_rel, e.tn_ent, K, mode, g, "tn_rel", "tn_ent", st);
+    g1 = lgan_reverse_gpu(g_nn, e.nn_rel, e.nn_ent, K, mode, g1, "nn_rel", "nn_ent", st);
+    return lgan_reverse_gpu(g1, e.rr_src, e.rr_dst, K, mode, g1, "rr_src", "rr_dst", st);
+}
+
+void check_lgan_edges(const Tensor& rr_src, const Tensor& rr_dst, const Tensor& tn_rel,
+                      const Tensor& tn_ent, const Tensor& nn_rel, const Tensor& nn_ent) {
+    check_int32_or_int64_index(rr_src, "rr_src");
+    check_int32_or_int64_index(rr_dst, "rr_dst");
+    check_int32_or_int64_index(tn_rel, "tn_rel");
+    check_int32_or_int64_index(tn_ent, "tn_ent");
+    check_int32_or_int64_index(nn_rel, "nn_rel");
+    check_int32_or_int64_index(nn_ent, "nn_ent");
+}
+
+std::tuple<Tensor, Tensor, Tensor> lgan_pool_reduce(
+    const Tensor& slot_messages, const Tensor& slot_to_relation_instance,
+    const Tensor& relation_instance_arities, const Tensor& rr_src, const Tensor& rr_dst,
+    const Tensor& tn_rel, const Tensor& tn_ent, const Tensor& nn_rel, const Tensor& nn_ent,
+    int64_t entity_dim_size, int64_t mode) {
+    check_rank(slot_messages, 2, "slot_messages");
+    check_int32_or_int64_index(slot_to_relation_instance, "slot_to_relation_instance");
+    check_int64_index(relation_instance_arities, "relation_instance_arities");
+    check_lgan_edges(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent);
+    TORCH_CHECK(same_device(slot_messages, {&slot_to_relation_instance, &relation_instance_arities,
+                                            &rr_src, &rr_dst, &tn_rel, &tn_ent, &nn_rel, &nn_ent}),
+                "lgan_pool_reduce expects all tensors on the same device.");
+    TORCH_CHECK(entity_dim_size >= 0, "entity_dim_size must be >= 0.");
+    TORCH_CHECK(slot_to_relation_instance.size(0) == slot_messages.size(0),
+                "slot_to_relation_instance length must match slot_messages rows.");
+    TORCH_CHECK(tn_rel.size(0) == tn_ent.size(0), "tn_rel and tn_ent must have equal length.");
+    TORCH_CHECK(nn_rel.size(0) == nn_ent.size(0), "nn_rel and nn_ent must have equal length.");
+    TORCH_CHECK(rr_src.size(0) == rr_dst.size(0), "rr_src and rr_dst must have equal length.");
+    TORCH_CHECK(mode == kModeSum || mode == kModeMean,
+                "lgan_pool_reduce supports only mode 0=sum or 2=mean.");
+    const int64_t K = relation_instance_arities.size(0);
+    const int64_t D = slot_messages.size(1);
+    if (lgan_gpu_lane({&slot_messages})) {
+        c10::OptionalDeviceGuard guard(slot_messages.device());
+        hipStream_t st = current_stream(slot_messages);
+        const Tensor slot = contiguous(slot_messages);
+        const bool pooled = slot.numel() > 0 && K > 0;
+        Tensor rpx = pooled ? at::empty({K, D}, slot.options()) : at::zeros({K, D}, slot.options());
+        if (pooled) {
+            const Tensor s2r = index64(slot_to_relation_instance);
+            GpuPlan gp = csr_plan_rows(s2r, K, "slot_to_relation_instance", st);
+            const int dt = dtype_code(slot);
+            Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, slot);
+            raise_if(relm_mp_plan_segment_reduce(dt, &gp.plan, nullptr, slot.data_ptr(), D, kModeSum,
+                                                 rpx.data_ptr(), scratch.data_ptr(),
+                                                 static_cast<size_t>(scratch.numel()), st));
+            const Tensor arity = contiguous(relation_instance_arities);
+            raise_if(relm_mp_rows_scale(dt, rpx.data_ptr(), nullptr, RELM_MP_DIV_VALUES, nullptr,
+                                        arity.data_ptr<int64_t>(), nullptr, K, D, rpx.data_ptr(),
+                                        st));
+        }
+        return lgan_step_gpu(rpx, lgan_edges64(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent),
+                             entity_dim_size, mode, st);
+    }
+    Tensor rpx = slot_messages.new_zeros({K, D});
+    if (slot_messages.numel() > 0) {
+        rpx.index_add_(0, slot_to_relation_instance, slot_messages);
+        rpx = rpx / relation_instance_arities.to(slot_messages.scalar_type()).view({K, 1}).clamp_min_(1.0);
+    }
+    rpx = rpx + lgan_aggregate_aten(rpx, rr_src, rr_dst, K, mode);
+    return std::make_tuple(rpx, lgan_aggregate_aten(rpx, tn_rel, tn_ent, entity_dim_size, mode),
+                           lgan_aggregate_aten(rpx, nn_rel, nn_ent, entity_dim_size, mode));
+}
+
+std::tuple<Tensor, Tensor, Tensor> lgan_relation_graph_step(
+    const Tensor& relation_pair_x, const Tensor& rr_src, const Tensor& rr_dst,
+    const Tensor& tn_rel, const Tensor& tn_ent, const Tensor& nn_rel, const Tensor& nn_ent,
+    int64_t entity_dim_size, int64_t mode) {
+    check_rank(relation_pair_x, 2, "relation_pair_x");
+    check_lgan_edges(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent);
+    TORCH_CHECK(same_device(relation_pair_x, {&rr_src, &rr_dst, &tn_rel, &tn_ent, &nn_rel, &nn_ent}),
+                "lgan_relation_graph_step expects all tensors on the same device.");
+    TORCH_CHECK(entity_dim_size >= 0, "entity_dim_size must be >= 0.");
+    TORCH_CHECK(rr_src.size(0) == rr_dst.size(0), "rr_src and rr_dst must have equal length.");
+    TORCH_CHECK(tn_rel.size(0) == tn_ent.size(0), "tn_rel and tn_ent must have equal length.");
+    TORCH_CHECK(nn_rel.size(0) == nn_ent.size(0), "nn_rel and nn_ent must have equal length.");
+    TORCH_CHECK(mode == kModeSum || mode == kModeMean,
+                "lgan_relation_graph_step supports only mode 0=sum or 2=mean.");
+    if (lgan_gpu_lane({&relation_pair_x})) {
+        c10::OptionalDeviceGuard guard(relation_pair_x.device());
+        return lgan_step_gpu(contiguous(relation_pair_x),
+                             lgan_edges64(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent),
+                             entity_dim_size, mode, current_stream(relation_pair_x));
+    }
+    const int64_t K = relation_pair_x.size(0);
+    Tensor upd = relation_pair_x + lgan_aggregate_aten(relation_pair_x, rr_src, rr_dst, K, mode);
+    return std::make_tuple(upd, lgan_aggregate_aten(upd, tn_rel, tn_ent, entity_dim_size, mode),
+                           lgan_aggregate_aten(upd, nn_rel, nn_ent, entity_dim_size, mode));
+}
+
+Tensor lgan_relation_graph_step_backward(const Tensor& grad_relation_pair_x,
+                                         const Tensor& grad_tn_msgs, const Tensor& grad_nn_msgs,
+                                         const Tensor& rr_src, const Tensor& rr_dst,
+                                         const Tensor& tn_rel, const Tensor& tn_ent,
+                                         const Tensor& nn_rel, const Tensor& nn_ent,
+                                         int64_t relation_count, int64_t mode) {
+    check_rank(grad_relation_pair_x, 2, "grad_relation_pair_x");
+    check_rank(grad_tn_msgs, 2, "grad_tn_msgs");
+    check_rank(grad_nn_msgs, 2, "grad_nn_msgs");
+    check_lgan_edges(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent);
+    TORCH_CHECK(same_device(grad_relation_pair_x, {&grad_tn_msgs, &grad_nn_msgs, &rr_src, &rr_dst,
+                                                   &tn_rel, &tn_ent, &nn_rel, &nn_ent}),
+                "lgan_relation_graph_step_backward expects all tensors on the same device.");
+    TORCH_CHECK(relation_count >= 0, "relation_count must be >= 0.");
+    TORCH_CHECK(mode == kModeSum || mode == kModeMean,
+                "lgan_relation_graph_step_backward supports only mode 0=sum or 2=mean.");
+    if (lgan_gpu_lane({&grad_relation_pair_x, &grad_tn_msgs, &grad_nn_msgs}) &&
+        grad_relation_pair_x.size(0) == relation_count) {
+        c10::OptionalDeviceGuard guard(grad_relation_pair_x.device());
+        return lgan_step_backward_gpu(contiguous(grad_relation_pair_x), contiguous(grad_tn_msgs),
+                                      contiguous(grad_nn_msgs),
+                                      lgan_edges64(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent),
+                                      relation_count, mode, current_stream(grad_relation_pair_x));
+    }
+    Tensor g = grad_relation_pair_x + lgan_reverse_aten(grad_tn_msgs, tn_rel, tn_ent, relation_count, mode) +
+               lgan_reverse_aten(grad_nn_msgs, nn_rel, nn_ent, relation_count, mode);
+    return g + lgan_reverse_aten(g, rr_src, rr_dst, relation_count, mode);
+}
+
+Tensor lgan_pool_reduce_backward(const Tensor& grad_relation_pair_x, const Tensor& grad_tn_msgs,
+                                 const Tensor& grad_nn_msgs,
+                                 const Tensor& slot_to_relation_instance,
+                                 const Tensor& relation_instance_arities, const Tensor& rr_src,
+                                 const Tensor& rr_dst, const Tensor& tn_rel, const Tensor& tn_ent,
+                                 const Tensor& nn_rel, const Tensor& nn_ent,
+                                 int64_t relation_count, int64_t mode) {
+    check_rank(grad_relation_pair_x, 2, "grad_relation_pair_x");
+    check_rank(grad_tn_msgs, 2, "grad_tn_msgs");
+    check_rank(grad_nn_msgs, 2, "grad_nn_msgs");
+    check_int32_or_int64_index(slot_to_relation_instance, "slot_to_relation_instance");
+    check_int64_index(relation_instance_arities, "relation_instance_arities");
+    check_lgan_edges(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent);
+    TORCH_CHECK(same_device(grad_relation_pair_x,
+                            {&grad_tn_msgs, &grad_nn_msgs, &slot_to_relation_instance,
+                             &relation_instance_arities, &rr_src, &rr_dst, &tn_rel, &tn_ent,
+                             &nn_rel, &nn_ent}),
+                "lgan_pool_reduce_backward expects all tensors on the same device.");
+    TORCH_CHECK(mode == kModeSum || mode == kModeMean,
+                "lgan_pool_reduce_backward supports only mode 0=sum or 2=mean.");
+    TORCH_CHECK(relation_count >= 0, "relation_count must be >= 0.");
+    if (lgan_gpu_lane({&grad_relation_pair_x, &grad_tn_msgs, &grad_nn_msgs}) &&
+        grad_relation_pair_x.size(0) == relation_count) {
+        c10::OptionalDeviceGuard guard(grad_relation_pair_x.device());
+        hipStream_t st = current_stream(grad_relation_pair_x);
+        Tensor g = lgan_step_backward_gpu(contiguous(grad_relation_pair_x), contiguous(grad_tn_msgs),
+                                          contiguous(grad_nn_msgs),
+                                          lgan_edges64(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent),
+                                          relation_count, mode, st);
+        const Tensor s2r = index64(slot_to_relation_instance);
+        const int64_t E = s2r.numel(), D = g.size(1);
+        Tensor grad_slot = at::empty({E, D}, g.options());
+        if (E > 0 && D > 0) {
+            // each slot reads its relation instance's row and arity
+            const int64_t bound = std::min<int64_t>(relation_count, relation_instance_arities.numel());
+            const auto mm = at::aminmax(s2r);
+            const int64_t lo = std::get<0>(mm).item<int64_t>(), hi = std::get<1>(mm).item<int64_t>();
+            if (lo < 0) check_in_bounds(lo, bound, "slot_to_relation_instance");
+            check_in_bounds(hi, bound, "slot_to_relation_instance");
+            const Tensor arity = contiguous(relation_instance_arities);
+            raise_if(relm_mp_rows_scale(dtype_code(g), g.data_ptr(), s2r.data_ptr<int64_t>(),
+                                        RELM_MP_DIV_VALUES, nullptr, arity.data_ptr<int64_t>(),
+                                        nullptr, E, D, grad_slot.data_ptr(), st));
+        }
+        return grad_slot;
+    }
+    Tensor g = grad_relation_pair_x + lgan_reverse_aten(grad_tn_msgs, tn_rel, tn_ent, relation_count, mode) +
+               lgan_reverse_aten(grad_nn_msgs, nn_rel, nn_ent, relation_count, mode);
+    g = g + lgan_reverse_aten(g, rr_src, rr_dst, relation_count, mode);
+    Tensor grad_slot = g.index_select(0, slot_to_relation_instance);
+    Tensor counts = relation_instance_arities.to(grad_slot.scalar_type())
+                        .index_select(0, slot_to_relation_instance.to(at::kLong))
+                        .view({slot_to_relation_instance.size(0), 1})
+                        .clamp_min_(1.0);
+    return grad_slot / counts;
+}
+
 std::string build_info() {
     return std::string("build_torch=") + RELM_MP_BUILD_TORCH_VERSION +
            ";build_cuda_tag=cpu;abi_target=rocm-gfx950;abi_lane=nonstable;" + relm_mp_build_info();
@@ -1068,6 +1420,10 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("fanin_pack_multi(Tensor[] rel_parts, Tensor[] flat_src_parts, Tensor[] dst_idx_parts) -> (Tensor, Tensor, Tensor)");
     m.def("fanout_pack_from_edges(Tensor[] x_parts, Tensor[] edge_src_parts, Tensor[] edge_dst_parts, int[] src_part_ids, int[] arity_parts, int[] pos_parts, int[] slot_offset_parts) -> (Tensor, Tensor, Tensor)");
     m.def("fanin_pack_from_edges(Tensor[] rel_parts, Tensor[] edge_src_parts, Tensor[] edge_dst_parts, int[] rel_part_ids, int[] arity_parts, int[] pos_parts, int mode) -> (Tensor, Tensor, Tensor)");
+    m.def("lgan_pool_reduce(Tensor slot_messages, Tensor slot_to_relation_instance, Tensor relation_instance_arities, Tensor rr_src, Tensor rr_dst, Tensor tn_rel, Tensor tn_ent, Tensor nn_rel, Tensor nn_ent, int entity_dim_size, int mode) -> (Tensor, Tensor, Tensor)");
+    m.def("lgan_pool_reduce_backward(Tensor grad_relation_pair_x, Tensor grad_tn_msgs, Tensor grad_nn_msgs, Tensor slot_to_relation_instance, Tensor relation_instance_arities, Tensor rr_src, Tensor rr_dst, Tensor tn_rel, Tensor tn_ent, Tensor nn_rel, Tensor nn_ent, int relation_count, int mode) -> Tensor");
+    m.def("lgan_relation_graph_step(Tensor relation_pair_x, Tensor rr_src, Tensor rr_dst, Tensor tn_rel, Tensor tn_ent, Tensor nn_rel, Tensor nn_ent, int entity_dim_size, int mode) -> (Tensor, Tensor, Tensor)");
+    m.def("lgan_relation_graph_step_backward(Tensor grad_relation_pair_x, Tensor grad_tn_msgs, Tensor grad_nn_msgs, Tensor rr_src, Tensor rr_dst, Tensor tn_rel, Tensor tn_ent, Tensor nn_rel, Tensor nn_ent, int relation_count, int mode) -> Tensor");
     m.def("build_info() -> str");
     // No reference counterpart: control of the index-plan cache.
     m.def("plan_cache_clear() -> ()");
@@ -1085,6 +1441,10 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("fanin_pack_multi", relm_amd::fanin_pack_multi);
     m.impl("fanout_pack_from_edges", relm_amd::fanout_pack_from_edges);
     m.impl("fanin_pack_from_edges", relm_amd::fanin_pack_from_edges);
+    m.impl("lgan_pool_reduce", relm_amd::lgan_pool_reduce);
+    m.impl("lgan_pool_reduce_backward", relm_amd::lgan_pool_reduce_backward);
+    m.impl("lgan_relation_graph_step", relm_amd::lgan_relation_graph_step);
+    m.impl("lgan_relation_graph_step_backward", relm_amd::lgan_relation_graph_step_backward);
     m.impl("build_info", relm_amd::build_info);
     m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
     m.impl("plan_cache_size", relm_amd::plan_cache_size);

@@ -5,7 +5,10 @@ dispatch (``src/relmo/ops/mp.py:43-70``): modes other than sum (0) and
 logsumexp (1) go to the ATen fallback, which raises ``ValueError``; otherwise
 the custom ops run through autograd Functions unless the policy selects the
 fallback.  The four pack ops (``mp.py:73-146``) call ``torch.ops.relm_mp``
-directly, or their ATen fallbacks, through ``dispatch_namespace_op``.
+directly, or their ATen fallbacks, through ``dispatch_namespace_op``.  The
+LGAN reductions (``_lgan_pool_reduce``, ``_lgan_relation_graph_step``,
+``mp.py:394-525``) run the custom ops for CUDA tensors and their ATen fallbacks
+otherwise.
 """
 
 from __future__ import annotations
@@ -14,6 +17,8 @@ from .mp_autograd import (
     _FaninReduceLogSumExpFunction,
     _FaninReduceSumFunction,
     _FanoutScatterFunction,
+    _LGANPoolReduceFunction,
+    _LGANRelationGraphStepFunction,
 )
 from .mp_constants import MODE_LOGSUMEXP, MODE_MEAN, MODE_SUM, activation_code
 from .mp_dispatch import dispatch_namespace_op, should_use_custom
@@ -125,6 +130,39 @@ def fanin_pack_from_edges(
         "fanin_pack_from_edges", rel_parts, edge_src_parts, edge_dst_parts, rel_part_ids,
         arity_parts, pos_parts, int(mode),
         fallback=fanin_pack_from_edges_python,
+    )
+
+
+def _resolve_lgan_mode(op_name: str, mode: str) -> int:
+    key = str(mode).strip().lower()
+    if key == "sum":
+        return MODE_SUM
+    if key == "mean":
+        return MODE_MEAN
+    raise ValueError(f"{op_name} supports only mode='sum' or mode='mean'.")
+
+
+def _lgan_pool_reduce(slot_messages, slot_to_relation_instance, relation_instance_arities, rr_src,
+                      rr_dst, tn_rel, tn_ent, nn_rel, nn_ent, *, entity_dim_size: int, mode: str):
+    """Pool slot messages to relation instances and run the RR / TN / NN
+    reductions (``mp.py:468-497``): ``(relation_pair_x, tn_msgs, nn_msgs)``."""
+
+    require_torch("_lgan_pool_reduce")
+    return _LGANPoolReduceFunction.apply(
+        slot_messages, slot_to_relation_instance, relation_instance_arities, rr_src, rr_dst,
+        tn_rel, tn_ent, nn_rel, nn_ent, int(entity_dim_size),
+        int(_resolve_lgan_mode("_lgan_pool_reduce", mode)),
+    )
+
+
+def _lgan_relation_graph_step(relation_pair_x, rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent, *,
+                              entity_dim_size: int, mode: str):
+    """RR / TN / NN propagation on pooled relation-instance embeddings (``mp.py:500-525``)."""
+
+    require_torch("_lgan_relation_graph_step")
+    return _LGANRelationGraphStepFunction.apply(
+        relation_pair_x, rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent, int(entity_dim_size),
+        int(_resolve_lgan_mode("_lgan_relation_graph_step", mode)),
     )
 
 

@@ -67,3 +67,90 @@ else:  # pragma: no cover - torch missing
     _FanoutScatterFunction = None
     _FaninReduceSumFunction = None
     _FaninReduceLogSumExpFunction = None
+
+
+# ---- LGAN indexed reductions ---------------------------------------------------
+#
+# As relmo's mp_autograd.py:194-537: CUDA tensors run the custom forward op and,
+# in the backward, the custom backward op (missing output gradients become
+# zeros); other tensors run the ATen fallback, differentiated by autograd.
+
+def _zeros_or(grad, rows: int, like):
+    if grad is not None:
+        return grad
+    return torch.zeros((int(rows), int(like.size(-1))), device=like.device, dtype=like.dtype)
+
+
+if torch is not None:
+    from .mp_dispatch import use_custom_namespace_op
+    from .mp_fallbacks import lgan_pool_reduce_python, lgan_relation_graph_step_python
+
+    def _custom(tensor, op_name: str) -> bool:
+        return use_custom_namespace_op(op_name, tensor=tensor, require_cuda=True)
+
+    def _fallback_grad(fn, x, args, grads):
+        with torch.enable_grad():
+            x_req = x.detach().requires_grad_(True)
+            outputs = fn(x_req, *args)
+            grads = tuple(g if g is not None else torch.zeros_like(o) for g, o in zip(grads, outputs))
+            (grad_x,) = torch.autograd.grad(outputs, (x_req,), grad_outputs=grads, allow_unused=True)
+        return grad_x
+
+    class _LGANPoolReduceFunction(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, slot_messages, slot_to_relation_instance, relation_instance_arities,
+                    rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent, entity_dim_size, mode):
+            ctx.entity_dim_size, ctx.mode = int(entity_dim_size), int(mode)
+            ctx.save_for_backward(slot_messages, slot_to_relation_instance,
+                                  relation_instance_arities, rr_src, rr_dst, tn_rel, tn_ent,
+                                  nn_rel, nn_ent)
+            ctx.used_custom = _custom(slot_messages, "lgan_pool_reduce")
+            fn = ops_namespace().lgan_pool_reduce if ctx.used_custom else lgan_pool_reduce_python
+            return fn(slot_messages, slot_to_relation_instance, relation_instance_arities, rr_src,
+                      rr_dst, tn_rel, tn_ent, nn_rel, nn_ent, ctx.entity_dim_size, ctx.mode)
+
+        @staticmethod
+        def backward(ctx, grad_rpx, grad_tn, grad_nn):
+            slot, s2r, arity, *edges = ctx.saved_tensors
+            none = (None,) * 10
+            if (grad_rpx is None and grad_tn is None and grad_nn is None) or not ctx.needs_input_grad[0]:
+                return (None, *none)
+            K = int(arity.numel())
+            if ctx.used_custom and _custom(slot, "lgan_pool_reduce_backward"):
+                grad = ops_namespace().lgan_pool_reduce_backward(
+                    _zeros_or(grad_rpx, K, slot), _zeros_or(grad_tn, ctx.entity_dim_size, slot),
+                    _zeros_or(grad_nn, ctx.entity_dim_size, slot), s2r, arity, *edges, K, ctx.mode)
+                return (grad, *none)
+            grad = _fallback_grad(
+                lambda x, *a: lgan_pool_reduce_python(x, *a),
+                slot, (s2r, arity, *edges, ctx.entity_dim_size, ctx.mode), (grad_rpx, grad_tn, grad_nn))
+            return (grad, *none)
+
+    class _LGANRelationGraphStepFunction(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, relation_pair_x, rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent,
+                    entity_dim_size, mode):
+            ctx.entity_dim_size, ctx.mode = int(entity_dim_size), int(mode)
+            ctx.save_for_backward(relation_pair_x, rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent)
+            ctx.used_custom = _custom(relation_pair_x, "lgan_relation_graph_step")
+            fn = (ops_namespace().lgan_relation_graph_step if ctx.used_custom
+                  else lgan_relation_graph_step_python)
+            return fn(relation_pair_x, rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent,
+                      ctx.entity_dim_size, ctx.mode)
+
+        @staticmethod
+        def backward(ctx, grad_rpx, grad_tn, grad_nn):
+            x, *edges = ctx.saved_tensors
+            none = (None,) * 8
+            if (grad_rpx is None and grad_tn is None and grad_nn is None) or not ctx.needs_input_grad[0]:
+                return (None, *none)
+            K = int(x.size(0))
+            if ctx.used_custom and _custom(x, "lgan_relation_graph_step_backward"):
+                grad = ops_namespace().lgan_relation_graph_step_backward(
+                    _zeros_or(grad_rpx, K, x), _zeros_or(grad_tn, ctx.entity_dim_size, x),
+                    _zeros_or(grad_nn, ctx.entity_dim_size, x), *edges, K, ctx.mode)
+                return (grad, *none)
+            grad = _fallback_grad(
+                lambda v, *a: lgan_relation_graph_step_python(v, *a),
+                x, (*edges, ctx.entity_dim_size, ctx.mode), (grad_rpx, grad_tn, grad_nn))
+            return (grad, *none)

@@ -60,10 +60,35 @@ def empty_index(device) -> torch.Tensor:
     return torch.empty(0, device=device, dtype=torch.int64)
 
 
+def indexed_sum_or_mean(source_embeddings, source_index, target_index, dim_size: int, mode: int,
+                        *, op_name: str):
+    """Rows ``target_index[e]`` of a [dim_size, emb] result receive
+    ``source_embeddings[source_index[e]]``: summed, or averaged over the messages
+    of each row in mean mode (``mp_common.py:88-118``)."""
+
+    from .mp_constants import MODE_MEAN, MODE_SUM
+
+    if mode not in (MODE_SUM, MODE_MEAN):
+        raise ValueError(f"{op_name} supports only sum and mean modes.")
+    out = source_embeddings.new_zeros((int(dim_size), int(source_embeddings.size(-1))))
+    if int(source_index.numel()) == 0 or int(dim_size) == 0:
+        return out
+    out.index_add_(0, target_index, source_embeddings.index_select(0, source_index))
+    if mode == MODE_MEAN:
+        counts = out.new_zeros((int(dim_size), 1))
+        counts.index_add_(
+            0, target_index,
+            torch.ones((int(target_index.numel()), 1), device=out.device, dtype=out.dtype),
+        )
+        out = out / counts.clamp_min_(1.0)
+    return out
+
+
 __all__ = [
     "cat_or_empty",
     "cat_or_single",
     "empty_index",
+    "indexed_sum_or_mean",
     "require_int64",
     "require_matching_lengths",
     "require_non_empty",

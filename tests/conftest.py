@@ -36,6 +36,16 @@ def pack_golden() -> tuple[list[dict], dict[str, np.ndarray]]:
     return cases, arrays
 
 
+@pytest.fixture(scope="session")
+def lgan_golden() -> tuple[list[dict], dict[str, np.ndarray]]:
+    """LGAN-op cases written by tests/golden/make_lgan_golden.py."""
+
+    cases = json.loads((GOLDEN / "lgan_cases.json").read_text())
+    with np.load(GOLDEN / "lgan_cases.npz", allow_pickle=False) as data:
+        arrays = {k: data[k] for k in data.files}
+    return cases, arrays
+
+
 def pack_args(case: dict, arrays: dict[str, np.ndarray], device: str = "cpu") -> list:
     """Arguments of a pack case as torch objects (tensor lists, int lists, ints)."""
 

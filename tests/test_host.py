@@ -459,3 +459,74 @@ def test_pack_facade_dispatch_and_grad(mp_env) -> None:
         return mp.fanin_reduce(r_cat, fs, fd, 3, 1)
 
     assert torch.autograd.gradcheck(packed_lse, tuple(rels))
+
+
+# ---- LGAN indexed reductions on the CPU lane --------------------------------------------------
+
+LGAN_OUTPUTS = {"lgan_pool_reduce": 3, "lgan_relation_graph_step": 3,
+                "lgan_pool_reduce_backward": 1, "lgan_relation_graph_step_backward": 1}
+
+
+def _check_lgan_case(fn, case: dict, arrays: dict, device: str = "cpu", errors: bool = True) -> bool:
+    args = pack_args(case, arrays, device)
+    if "error" in case:
+        if not errors:
+            return False
+        with pytest.raises((RuntimeError, ValueError, IndexError)) as info:
+            fn(*args)
+        assert str(info.value).splitlines()[0] == case["error"], case["name"]
+        return True
+    got = fn(*args)
+    got = got if isinstance(got, (tuple, list)) else (got,)
+    assert len(got) == LGAN_OUTPUTS[case["op"]] == len(case["expected"]), case["name"]
+    for g, name in zip(got, case["expected"]):
+        assert str(g.device).startswith(device), case["name"]
+        g = g.detach().cpu().numpy()
+        want = arrays[name]
+        assert g.dtype == want.dtype and g.shape == want.shape, case["name"]
+        assert np.array_equal(g, want), case["name"]
+    return True
+
+
+def test_lgan_cpu_lane_reproduces_golden(ops, lgan_golden) -> None:
+    cases, arrays = lgan_golden
+    for case in cases:
+        _check_lgan_case(getattr(ops, case["op"]), case, arrays)
+
+
+def test_lgan_python_fallbacks_reproduce_golden(lgan_golden) -> None:
+    from relmo_amd import mp_fallbacks
+
+    cases, arrays = lgan_golden
+    fns = {"lgan_pool_reduce": mp_fallbacks.lgan_pool_reduce_python,
+           "lgan_relation_graph_step": mp_fallbacks.lgan_relation_graph_step_python}
+    checked = sum(_check_lgan_case(fns[c["op"]], c, arrays, errors=False)
+                  for c in cases if c["op"] in fns)
+    assert checked >= 20
+
+
+@pytest.mark.parametrize("mode", ["sum", "mean"])
+def test_lgan_facade_autograd_on_cpu(mode) -> None:
+    """CPU tensors take the ATen fallback; gradients equal the backward ops'
+    (reference library semantics, pinned by the golden cases) and pass gradcheck."""
+
+    from relmo_amd import mp
+
+    rng = np.random.default_rng(41)
+    K, ent, E, D = 25, 11, 60, 3
+    s2r = torch.from_numpy(rng.integers(0, K, E))
+    arity = torch.from_numpy(rng.integers(0, 4, K))
+    edges = [torch.from_numpy(rng.integers(0, b, n)) for b, n in
+             [(K, 70), (K, 70), (K, 40), (ent, 40), (K, 30), (ent, 30)]]
+    slot = torch.randn(E, D, dtype=torch.float64, requires_grad=True)
+    outs = mp._lgan_pool_reduce(slot, s2r, arity, *edges, entity_dim_size=ent, mode=mode)
+    gs = [torch.randn_like(o) for o in outs]
+    (grad,) = torch.autograd.grad(outs, slot, gs)
+    m = 0 if mode == "sum" else 2
+    want = torch.ops.relm_mp.lgan_pool_reduce_backward(*gs, s2r, arity, *edges, K, m)
+    torch.testing.assert_close(grad, want, rtol=1e-12, atol=1e-12)
+    assert torch.autograd.gradcheck(
+        lambda x: mp._lgan_relation_graph_step(x, *edges, entity_dim_size=ent, mode=mode),
+        (torch.randn(K, D, dtype=torch.float64, requires_grad=True),))
+    with pytest.raises(ValueError, match="supports only mode='sum' or mode='mean'"):
+        mp._lgan_relation_graph_step(slot, *edges, entity_dim_size=ent, mode="max")

@@ -382,3 +382,97 @@ def test_pack_oracle_matches_every_golden_case(pack_golden) -> None:
             assert np.array_equal(g, want), case["name"]
         checked += 1
     assert checked >= 30
+
+
+# ---- LGAN indexed reductions (oracle/lgan.py) ---------------------------------------------
+
+from oracle import lgan as lgan_oracle  # noqa: E402
+
+LGAN_FNS = {
+    "lgan_pool_reduce": lgan_oracle.lgan_pool_reduce,
+    "lgan_pool_reduce_backward": lgan_oracle.lgan_pool_reduce_backward,
+    "lgan_relation_graph_step": lgan_oracle.lgan_relation_graph_step,
+    "lgan_relation_graph_step_backward": lgan_oracle.lgan_relation_graph_step_backward,
+}
+
+
+def _np_args(case: dict, arrays: dict) -> list:
+    return [arrays[s["tensor"]] if "tensor" in s else s["int"] for s in case["args"]]
+
+
+def test_lgan_oracle_matches_every_golden_case(lgan_golden) -> None:
+    cases, arrays = lgan_golden
+    checked = 0
+    for case in cases:
+        if "error" in case:
+            continue
+        got = LGAN_FNS[case["op"]](*_np_args(case, arrays))
+        got = got if isinstance(got, tuple) else (got,)
+        for g, name in zip(got, case["expected"]):
+            want = arrays[name]
+            assert g.dtype == want.dtype and g.shape == want.shape, case["name"]
+            assert np.array_equal(g, want), case["name"]
+        checked += 1
+    assert checked >= 40
+
+
+def _dense(src, dst, rows, cols, mode):
+    """Matrix M with (M x)[d] = aggregate of x[src[e]] over dst[e] == d."""
+
+    m = np.zeros((rows, cols))
+    for s, d in zip(src, dst):
+        m[d, s] += 1.0
+    if mode == 2:
+        m /= np.maximum(m.sum(axis=1, keepdims=True), 1.0)
+    return m
+
+
+def _random_lgan(rng, K=30, ent=17, E=70, D=4):
+    return dict(
+        slot=rng.standard_normal((E, D)), s2r=rng.integers(0, K, E), arity=rng.integers(-1, 4, K),
+        rr=(rng.integers(0, K, 90), rng.integers(0, K, 90)),
+        tn=(rng.integers(0, K, 60), rng.integers(0, ent, 60)),
+        nn=(rng.integers(0, K, 40), rng.integers(0, ent, 40)), K=K, ent=ent, E=E, D=D)
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_lgan_oracle_against_dense_matrices(mode) -> None:
+    """float64 truth: the ops are linear maps; build their matrices densely."""
+
+    rng = np.random.default_rng(31 + mode)
+    r = _random_lgan(rng)
+    K, ent, E = r["K"], r["ent"], r["E"]
+    P = np.zeros((K, E))
+    P[r["s2r"], np.arange(E)] = 1.0
+    P /= np.maximum(r["arity"], 1)[:, None]
+    R = np.eye(K) + _dense(*r["rr"], K, K, mode)
+    T, N = _dense(*r["tn"], ent, K, mode), _dense(*r["nn"], ent, K, mode)
+    rpx, tn, nn = lgan_oracle.lgan_pool_reduce(r["slot"], r["s2r"], r["arity"], *r["rr"], *r["tn"],
+                                              *r["nn"], ent, mode)
+    x = R @ (P @ r["slot"])
+    np.testing.assert_allclose(rpx, x, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(tn, T @ x, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(nn, N @ x, rtol=1e-12, atol=1e-12)
+    # the backward ops are the transposed maps
+    g = rng.standard_normal((K, r["D"]))
+    gt, gn = rng.standard_normal((ent, r["D"])), rng.standard_normal((ent, r["D"]))
+    grad = lgan_oracle.lgan_pool_reduce_backward(g, gt, gn, r["s2r"], r["arity"], *r["rr"], *r["tn"],
+                                                 *r["nn"], K, mode)
+    want = P.T @ (R.T @ (g + T.T @ gt + N.T @ gn))
+    np.testing.assert_allclose(grad, want, rtol=1e-12, atol=1e-12)
+    step_grad = lgan_oracle.lgan_relation_graph_step_backward(g, gt, gn, *r["rr"], *r["tn"], *r["nn"],
+                                                              K, mode)
+    np.testing.assert_allclose(step_grad, R.T @ (g + T.T @ gt + N.T @ gn), rtol=1e-12, atol=1e-12)
+
+
+def test_lgan_oracle_mean_of_equal_rows() -> None:
+    """mean mode: every entity that receives messages from identical rows gets that row."""
+
+    rng = np.random.default_rng(33)
+    row = rng.standard_normal(6)
+    x = np.tile(row, (20, 1))
+    src, dst = rng.integers(0, 20, 50), rng.integers(0, 9, 50)
+    out = lgan_oracle.indexed_sum_or_mean(x, src, dst, 9, 2)
+    hit = np.bincount(dst, minlength=9) > 0
+    np.testing.assert_allclose(out[hit], np.tile(row, (hit.sum(), 1)), rtol=1e-15)
+    assert not out[~hit].any()
