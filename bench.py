@@ -17,10 +17,11 @@ The JSON line also carries
                   bounded 1/8-scale sample of C2, on the host's cores;
   extra         - kernel-only rates with cached plans, C2 with sum, C3 fanout
                   forward + backward, C1 latencies, the pack ops (index
-                  preparation) against their ATen formulation, C4 / C5 model
-                  training steps (graphs/sec).
+                  preparation) and the LGAN pooling step against their ATen
+                  formulation, C4 / C5 model training steps (graphs/sec).
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c2sum|c3|c1|c4|c5|pack|copy]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--only c2|c2sum|c3|c1|c4|c5|pack|lgan|copy]
 """
 
 from __future__ import annotations
@@ -334,6 +335,67 @@ def bench_pack(torch, steps: int) -> dict:
     return res
 
 
+def bench_lgan(torch, steps: int) -> dict:
+    """LGAN pooling step forward + backward through relmo_amd.mp._lgan_pool_reduce
+    (custom HIP ops) against the ATen formulation of the same op on the same
+    GPU (the fallback, differentiated by autograd): 2^20 relation instances of
+    arity 2 (2^21 slots), D = 64, 2^22 relation-relation edges, 2^21 tn and
+    2^21 nn edges onto 2^19 entities, uniform random indices.  Loss = sum of
+    the three outputs weighted by fixed random tensors.  Algorithmic bytes per
+    forward: 4*D per slot read, per edge of each edge set (rows gathered), per
+    output row written and per base row read; the backward the same over the
+    transposed sets plus the slot gradients.  Timed with plans rebuilt in
+    every step (cache cleared) and with plans kept."""
+
+    from relmo_amd import mp
+    from relmo_amd import mp_fallbacks
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    K, ent, D = 1 << 20, 1 << 19, 64
+    E_slots, n_rr, n_tn, n_nn = 1 << 21, 1 << 22, 1 << 21, 1 << 21
+    ri = lambda hi, n: torch.randint(0, hi, (n,), device=dev, generator=gen)  # noqa: E731
+    slot = torch.randn(E_slots, D, device=dev, generator=gen).requires_grad_(True)
+    s2r = torch.arange(E_slots, device=dev) // 2
+    arity = torch.full((K,), 2, dtype=torch.long, device=dev)
+    edges = [ri(K, n_rr), ri(K, n_rr), ri(K, n_tn), ri(ent, n_tn), ri(K, n_nn), ri(ent, n_nn)]
+    w = [torch.randn(K, D, device=dev, generator=gen), torch.randn(ent, D, device=dev, generator=gen),
+         torch.randn(ent, D, device=dev, generator=gen)]
+    ns = torch.ops.relm_mp
+    row = 4 * D
+    fwd_bytes = row * (E_slots + K + n_rr + 2 * K + n_tn + ent + n_nn + ent)
+    bwd_bytes = row * (n_tn + ent + 2 * K + n_nn + 2 * K + n_rr + 2 * K + E_slots + E_slots)
+    res = {"relation_instances": K, "entities": ent, "emb": D, "slots": E_slots, "rr_edges": n_rr,
+           "tn_edges": n_tn, "nn_edges": n_nn, "bytes_fwd": fwd_bytes, "bytes_bwd": bwd_bytes}
+
+    def make_step(fn, clear):
+        def step():
+            if clear:
+                ns.plan_cache_clear()
+            outs = fn()
+            torch.autograd.grad(outs, slot, w)
+        return step
+
+    sync = torch.cuda.synchronize
+    for mode in ("sum", "mean"):
+        custom = lambda: mp._lgan_pool_reduce(slot, s2r, arity, *edges, entity_dim_size=ent,  # noqa: E731
+                                              mode=mode)
+        m = 0 if mode == "sum" else 2
+        aten = lambda: mp_fallbacks.lgan_pool_reduce_python(slot, s2r, arity, *edges, ent, m)  # noqa: E731
+        t_unc = timed(make_step(custom, True), steps, 2, sync)
+        t_cached = timed(make_step(custom, False), steps, 2, sync)
+        t_aten = timed(make_step(aten, False), max(3, steps // 2), 1, sync)
+        res[mode] = {"ms_step": t_unc * 1e3, "gbs_step": gbs(fwd_bytes + bwd_bytes, t_unc),
+                     "ms_step_cached_plans": t_cached * 1e3,
+                     "gbs_step_cached_plans": gbs(fwd_bytes + bwd_bytes, t_cached),
+                     "ms_step_aten_formulation": t_aten * 1e3}
+    ns.plan_cache_clear()
+    del slot, edges, w
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_copy(torch, steps: int) -> dict:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the HBM
     byte counters (FETCH_SIZE / WRITE_SIZE per dispatch against 1 GiB)."""
@@ -437,7 +499,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "pack", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "pack", "lgan", "copy"],
+                    default=None,
                     help="run one workload only and print its figures (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -466,6 +529,7 @@ def main() -> int:
               "c4": lambda: bench_models(torch, "c4", args.steps, args.warmup),
               "c5": lambda: bench_models(torch, "c5", args.steps, args.warmup),
               "pack": lambda: bench_pack(torch, args.steps),
+              "lgan": lambda: bench_lgan(torch, args.steps),
               "copy": lambda: bench_copy(torch, args.steps)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
@@ -482,6 +546,8 @@ def main() -> int:
     extra["c1_latency_us"] = bench_c1(torch, mp, syn)
     log("pack ops (index preparation) ...")
     extra["pack"] = bench_pack(torch, max(5, args.steps // 2))
+    log("LGAN pooling step ...")
+    extra["lgan"] = bench_lgan(torch, max(5, args.steps // 2))
     log("C4 RelationalGNN training step ...")
     extra["c4_relational_gnn"] = bench_models(torch, "c4", 5, 2)
     log("C5 CentralizedRelationalGNN training step ...")

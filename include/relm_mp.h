@@ -297,6 +297,18 @@ int relm_mp_rows_scale(int dtype, const void* in, const int64_t* gather, int div
                        const int32_t* div_offsets, const int64_t* div_values, const void* base,
                        int64_t rows, int64_t emb, void* out, relm_mp_stream_t stream);
 
+/* out[num_keys, emb] = per key k of a CSR plan: base[k] + S_k / d_k, S_k the
+ * sum over the segment of table[gathered row] (as relm_mp_plan_segment_reduce
+ * mode 0), d_k = 1 (RELM_MP_DIV_NONE), max(1, segment size) (RELM_MP_DIV_SEGMENT:
+ * the mean) or max(1, (T)div_values[k]) (RELM_MP_DIV_VALUES); base may be NULL
+ * and must not alias out.  One pass: the LGAN aggregations with their epilogue
+ * (mp_ops.cpp:3439-3467, 3650-3655: sum or mean, the residual addition, the
+ * division by the arity). */
+int relm_mp_plan_segment_sum_scaled(int dtype, const relm_mp_plan* plan, const void* table,
+                                    int64_t emb, int div_kind, const int64_t* div_values,
+                                    const void* base, void* out, void* scratch,
+                                    size_t scratch_bytes, relm_mp_stream_t stream);
+
 /* ---- content match (plan reuse across equal indices) ----------------------- */
 
 /* No counterpart in the reference (its ops build their index structures in

@@ -59,6 +59,7 @@ EXPORTED_SYMBOLS = (
     "relm_mp_index_match_workspace_size",
     "relm_mp_index_match",
     "relm_mp_rows_scale",
+    "relm_mp_plan_segment_sum_scaled",
 )
 
 
@@ -156,6 +157,7 @@ _SIGNATURES = {
     "relm_mp_pack_index": (_int, [ctypes.POINTER(IndexPart), ctypes.c_int32, _vp, _vp, _vp]),
     "relm_mp_index_match_workspace_size": (_sz, []),
     "relm_mp_rows_scale": (_int, [_int, _vp, _vp, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "relm_mp_plan_segment_sum_scaled": (_int, [_int, _PP, _vp, _i64, _int, _vp, _vp, _vp, _vp, _sz, _vp]),
     "relm_mp_index_match": (
         _int,
         [_vp, _vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.c_int32,
@@ -439,6 +441,22 @@ def plan_segment_reduce(bp: BuiltPlan, table: torch.Tensor, mode: int, gathers: 
         lib().relm_mp_plan_segment_reduce(
             _dtype(table), ctypes.byref(bp.plan), _ptr(gathers), _ptr(table), emb, mode, _ptr(out),
             _ptr(scratch), scratch.numel(), _stream(table),
+        )
+    )
+    return out
+
+
+def plan_segment_sum_scaled(bp: BuiltPlan, table: torch.Tensor, div_kind: int = 0,
+                            div_values: torch.Tensor | None = None,
+                            base: torch.Tensor | None = None) -> torch.Tensor:
+    emb = table.size(1)
+    out = torch.empty(bp.plan.num_keys, emb, dtype=table.dtype, device=table.device)
+    n = lib().relm_mp_plan_compute_scratch_bytes(ctypes.byref(bp.plan), emb, _dtype(table), 0)
+    scratch = _bytes(n, table)
+    check(
+        lib().relm_mp_plan_segment_sum_scaled(
+            _dtype(table), ctypes.byref(bp.plan), _ptr(table), emb, div_kind, _ptr(div_values),
+            _ptr(base), _ptr(out), _ptr(scratch), scratch.numel(), _stream(table),
         )
     )
     return out

@@ -135,6 +135,10 @@ int compute_logsumexp_backward(int dtype, const relm_mp_plan& plan, const int64_
                                int64_t emb, void* grad_rel, void* scratch, size_t scratch_bytes,
                                hipStream_t s);
 int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t s);
+int compute_segment_sum_scaled(int dtype, const relm_mp_plan& plan, const void* table,
+                               int64_t emb, int div_kind, const int64_t* div_values,
+                               const void* base, void* out, void* scratch, size_t scratch_bytes,
+                               hipStream_t s);
 int compute_rows_scale(int dtype, const void* in, const int64_t* gather, int div_kind,
                        const int32_t* div_offsets, const int64_t* div_values, const void* base,
                        int64_t rows, int64_t emb, void* out, hipStream_t s);

@@ -307,6 +307,53 @@ struct LseBwdOp {
     __device__ __forceinline__ Partial partial() const { return {acc}; }
 };
 
+// ---- epilogues: applied to each key's result as it is stored ----------------
+
+// Stores the result as is.
+struct NoEpilogue {
+    template <typename T, int V>
+    __device__ __forceinline__ Pack<T, V> operator()(int64_t, const Pack<T, V>& v, int64_t,
+                                                     int64_t) const {
+        return v;
+    }
+};
+
+// base[key] + result / d_key, d_key = max(1, segment size) or max(1,
+// (T)values[key]) (relm_mp_plan_segment_sum_scaled).  The division and the
+// addition round separately; `base` must not alias the output (hub keys are
+// written twice).
+template <typename T>
+struct ScaleEpilogue {
+    const T* __restrict__ base;
+    int div_kind;
+    const int32_t* __restrict__ offsets;
+    const int64_t* __restrict__ values;
+
+    template <int V>
+    __device__ __forceinline__ Pack<T, V> operator()(int64_t key, const Pack<T, V>& v, int64_t D,
+                                                     int64_t col) const {
+        Pack<T, V> r = v;
+        if (div_kind != RELM_MP_DIV_NONE) {
+            T d = T(1);
+            if (div_kind == RELM_MP_DIV_SEGMENT) {
+                const int32_t n = offsets[key + 1] - offsets[key];
+                d = n > 1 ? static_cast<T>(n) : T(1);
+            } else {
+                const T x = static_cast<T>(values[key]);
+                d = x > T(1) ? x : T(1);
+            }
+#pragma unroll
+            for (int i = 0; i < V; ++i) r.v[i] = r.v[i] / d;
+        }
+        if (base != nullptr) {
+            const Pack<T, V> b = pack_load<T, V>(base + key * D + col);
+#pragma unroll
+            for (int i = 0; i < V; ++i) r.v[i] = b.v[i] + r.v[i];
+        }
+        return r;
+    }
+};
+
 // ---- shared walking helpers -------------------------------------------------
 
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
@@ -336,11 +383,12 @@ __global__ __launch_bounds__(kThreads) void k_fill(T* __restrict__ p, int64_t n,
 // whose label differs from the previous one restarts the accumulator and one
 // whose label differs from the next one stores its key's result - no
 // per-key loop, so the row groups of a wave stay in step.
-template <typename T, int V, int G, class Op>
+template <typename T, int V, int G, class Op, class Epi>
 __global__ __launch_bounds__(kThreads) void k_walk_items(
     const int32_t* __restrict__ short_off, const int32_t* __restrict__ short_gather,
     const int32_t* __restrict__ item_first, const int32_t* __restrict__ item_short,
-    const relm_mp_plan_counts* __restrict__ pc, int64_t num_keys, T* __restrict__ out, Op op) {
+    const relm_mp_plan_counts* __restrict__ pc, int64_t num_keys, T* __restrict__ out, Op op,
+    Epi epi) {
     constexpr int R = kThreads / G;
     constexpr int U = batch_rows<G>();
     // R items hold at most R * kItemSize keys and R * kItemSize + kHubThreshold
@@ -455,7 +503,8 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
         // keys without short messages: the empty-segment result
         for (int64_t k = bk0 + grp; k < bk1; k += R) {
             const int i = static_cast<int>(k - bk0 < kKeyCap - 1 ? k - bk0 : kKeyCap - 2);
-            if (s_off[i + 1] == s_off[i] && op.colok) pack_store_stream<T, V>(out + k * D + op.col, op.empty());
+            if (s_off[i + 1] == s_off[i] && op.colok)
+                pack_store_stream<T, V>(out + k * D + op.col, epi(k, op.empty(), D, op.col));
         }
         // the item's messages [sb, se), as staged positions [lb, le)
         const int lb = static_cast<int>(sb - bs0 < np ? sb - bs0 : np);
@@ -481,7 +530,8 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
                     op.restart(lab[u] != prev, key);
                     op.add(u);
                     if (next != lab[u] && op.colok)
-                        pack_store_stream<T, V>(out + key * D + op.col, op.result(true));
+                        pack_store_stream<T, V>(out + key * D + op.col,
+                                                epi(key, op.result(true), D, op.col));
                     prev = lab[u];
                 }
             }
@@ -524,12 +574,12 @@ __device__ __forceinline__ int hub_slot(int p) { return p + (p >> 5); }
 // One workgroup per hub chunk: the chunk's gathered row indices are staged in
 // LDS with coalesced loads, row group g folds slice g of the chunk, the
 // slices are folded in order by group 0; a single-chunk hub is finished here.
-template <typename T, int V, int G, class Op>
+template <typename T, int V, int G, class Op, class Epi>
 __global__ __launch_bounds__(kThreads) void k_hub_chunks(
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_edges,
     const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
     const int32_t* __restrict__ chunk_hub, const relm_mp_plan_counts* __restrict__ pc,
-    T* __restrict__ partial, T* __restrict__ out, Op op) {
+    T* __restrict__ partial, T* __restrict__ out, Op op, Epi epi) {
     using Partial = typename Op::Partial;
     constexpr int NG = kThreads / G;
     constexpr int U = batch_rows<G>();
@@ -590,7 +640,7 @@ __global__ __launch_bounds__(kThreads) void k_hub_chunks(
             Partial acc = red[gl];
             for (int wv = 1; wv < kThreads / kWave; ++wv) acc.merge(red[wv * G + gl]);
             if (hc.nch == 1)
-                pack_store<T, V>(out + hc.key * D + op.col, acc.value());
+                pack_store<T, V>(out + hc.key * D + op.col, epi(hc.key, acc.value(), D, op.col));
             else
                 acc.store(partial + c * Partial::kWords * D, D, op.col);
         }
@@ -619,12 +669,12 @@ __device__ __forceinline__ Partial fold_partials(const T* __restrict__ partial, 
 // contiguous range of the hub's chunk partials in chunk order; the group
 // results are folded as a fixed tree (shuffles inside a wave, then the waves in
 // order), so the result is deterministic.
-template <typename T, int V, int G, class Partial>
+template <typename T, int V, int G, class Partial, class Epi>
 __global__ __launch_bounds__(kThreads) void k_hub_combine(
     const int32_t* __restrict__ offsets, int64_t num_edges, int64_t D,
     const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
     const int32_t* __restrict__ multi_hubs, const relm_mp_plan_counts* __restrict__ pc,
-    const T* __restrict__ partial, T* __restrict__ out) {
+    const T* __restrict__ partial, T* __restrict__ out, Epi epi) {
     constexpr int NG = kThreads / G;
     constexpr int U = batch_rows<G>();
     __shared__ Partial red[kThreads / kWave * G];
@@ -660,7 +710,7 @@ __global__ __launch_bounds__(kThreads) void k_hub_combine(
         if (grp == 0 && colok && hok && nch > 0) {
             Partial acc = red[gl];
             for (int wv = 1; wv < kThreads / kWave; ++wv) acc.merge(red[wv * G + gl]);
-            pack_store<T, V>(out + key * D + col, acc.value());
+            pack_store<T, V>(out + key * D + col, epi(key, acc.value(), D, col));
         }
         __syncthreads();
     }
@@ -937,36 +987,37 @@ dim3 persistent_grid(const void* kernel, int64_t work, int64_t per_block, int64_
 // The item, hub and chunk counts are read from plan.counts on the device:
 // grids are sized by the host-side counts where the plan has them (>= 0),
 // else by the plan's capacities, and capped (persistent_grid).
-template <typename T, int V, int G, class Op>
+template <typename T, int V, int G, class Op, class Epi = NoEpilogue>
 int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, T* out,
-            hipStream_t s) {
+            hipStream_t s, const Epi& epi = Epi{}) {
     using Partial = typename Op::Partial;
     if (plan.counts == nullptr)
         return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: CSR plan without counts");
     const int64_t E = plan.num_edges;
     const int64_t items = plan.num_items >= 0 ? plan.num_items : item_capacity_for(plan.num_keys);
-    const void* walk = reinterpret_cast<const void*>(&k_walk_items<T, V, G, Op>);
-    hipLaunchKernelGGL((k_walk_items<T, V, G, Op>), persistent_grid(walk, items, kThreads / G, slices, 4),
-                       dim3(kThreads), 0, s, plan.short_off, plan.short_gather, plan.item_first,
-                       plan.item_short, plan.counts, plan.num_keys, out, op);
+    const void* walk = reinterpret_cast<const void*>(&k_walk_items<T, V, G, Op, Epi>);
+    hipLaunchKernelGGL((k_walk_items<T, V, G, Op, Epi>),
+                       persistent_grid(walk, items, kThreads / G, slices, 4), dim3(kThreads), 0, s,
+                       plan.short_off, plan.short_gather, plan.item_first, plan.item_short,
+                       plan.counts, plan.num_keys, out, op, epi);
     int rc = hip_error(hipGetLastError(), "relm_mp item kernel");
     // no hub when the counts say so, or when no segment can be longer than the threshold
     if (rc != RELM_MP_OK || plan.num_hubs == 0 || E <= kHubThreshold) return rc;
     const int64_t chunks = plan.num_chunks >= 0 ? plan.num_chunks : max_chunks(E);
-    const void* hub = reinterpret_cast<const void*>(&k_hub_chunks<T, V, G, Op>);
-    hipLaunchKernelGGL((k_hub_chunks<T, V, G, Op>), persistent_grid(hub, chunks, 1, slices, 8),
+    const void* hub = reinterpret_cast<const void*>(&k_hub_chunks<T, V, G, Op, Epi>);
+    hipLaunchKernelGGL((k_hub_chunks<T, V, G, Op, Epi>), persistent_grid(hub, chunks, 1, slices, 8),
                        dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted, plan.num_edges,
                        plan.hub_key, plan.hub_chunk_base, plan.chunk_hub, plan.counts, partial, out,
-                       op);
+                       op, epi);
     rc = hip_error(hipGetLastError(), "relm_mp hub chunk kernel");
     // no hub of more than one chunk when the counts say so, or when none fits
     if (rc != RELM_MP_OK || plan.num_multi_hubs == 0 || E <= kChunkSize) return rc;
     const int64_t multi = plan.num_multi_hubs >= 0 ? plan.num_multi_hubs : E / (kChunkSize + 1) + 1;
-    const void* comb = reinterpret_cast<const void*>(&k_hub_combine<T, V, G, Partial>);
-    hipLaunchKernelGGL((k_hub_combine<T, V, G, Partial>), persistent_grid(comb, multi, 1, slices, 8),
-                       dim3(kThreads), 0, s, plan.offsets, plan.num_edges, op.D, plan.hub_key,
-                       plan.hub_chunk_base, plan.multi_hubs, plan.counts,
-                       static_cast<const T*>(partial), out);
+    const void* comb = reinterpret_cast<const void*>(&k_hub_combine<T, V, G, Partial, Epi>);
+    hipLaunchKernelGGL((k_hub_combine<T, V, G, Partial, Epi>),
+                       persistent_grid(comb, multi, 1, slices, 8), dim3(kThreads), 0, s,
+                       plan.offsets, plan.num_edges, op.D, plan.hub_key, plan.hub_chunk_base,
+                       plan.multi_hubs, plan.counts, static_cast<const T*>(partial), out, epi);
     return hip_error(hipGetLastError(), "relm_mp hub combine kernel");
 }
 
@@ -1019,6 +1070,27 @@ int segment_reduce_t(const relm_mp_plan& plan, const void* table_v, int64_t emb,
 }
 
 template <typename T>
+int segment_sum_scaled_t(const relm_mp_plan& plan, const void* table_v, int64_t emb, int div_kind,
+                         const int64_t* div_values, const void* base_v, void* out_v, void* scratch,
+                         hipStream_t s) {
+    const T* table = static_cast<const T*>(table_v);
+    const T* base = static_cast<const T*>(base_v);
+    T* out = static_cast<T*>(out_v);
+    T* partial = static_cast<T*>(scratch);
+    const Geometry geo = choose_geometry<T>(emb, {table, base, out, partial});
+    return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
+        constexpr int V = decltype(vt)::value;
+        constexpr int G = decltype(gt)::value;
+        constexpr int U = batch_rows<G>();
+        SumOp<T, V, U> op{};
+        op.table = table;
+        op.D = emb;
+        const ScaleEpilogue<T> epi{base, div_kind, plan.offsets, div_values};
+        return run_csr<T, V, G>(plan, op, geo.slices, partial, out, s, epi);
+    });
+}
+
+template <typename T>
 int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void* grad_out_v,
                    const void* out_v, const void* rel_v, int64_t emb, void* grad_rel_v,
                    void* scratch, hipStream_t s) {
@@ -1059,6 +1131,22 @@ size_t hub_partial_bytes(const relm_mp_plan& plan, int64_t emb, int dtype, int64
     // counts not read back yet: the capacity of the chunk list
     const int64_t chunks = plan.num_chunks >= 0 ? plan.num_chunks : max_chunks(plan.num_edges);
     return static_cast<size_t>(chunks) * per;
+}
+
+int compute_segment_sum_scaled(int dtype, const relm_mp_plan& plan, const void* table,
+                               int64_t emb, int div_kind, const int64_t* div_values,
+                               const void* base, void* out, void* scratch, size_t scratch_bytes,
+                               hipStream_t s) {
+    if (plan.num_keys == 0 || emb == 0) return RELM_MP_OK;
+    if (plan.kind != RELM_MP_PLAN_CSR)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: scaled sums need a CSR plan");
+    if (scratch_bytes < hub_partial_bytes(plan, emb, dtype, RELM_MP_MODE_SUM))
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: hub scratch too small");
+    return dtype == RELM_MP_F64
+               ? segment_sum_scaled_t<double>(plan, table, emb, div_kind, div_values, base, out,
+                                              scratch, s)
+               : segment_sum_scaled_t<float>(plan, table, emb, div_kind, div_values, base, out,
+                                             scratch, s);
 }
 
 int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t s) {

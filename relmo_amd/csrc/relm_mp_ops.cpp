@@ -1068,11 +1068,13 @@ std::tuple<Tensor, Tensor, Tensor> fanin_pack_from_edges(
 // Relation instances pool their slots (sum / arity), take one residual
 // aggregation step over relation-relation edges and aggregate onto entities
 // over two edge sets (tn, nn); sum (0) or mean (2) per destination.  GPU lane
-// (float32 / float64 CUDA tensors of one dtype): every aggregation is a CSR
-// segment sum (edge order inside each destination) followed by one row
-// epilogue (relm_mp_rows_scale: division by the count or arity, residual
-// addition), the backward the transposed sums over plans keyed by the
-// sources.  Other tensors: the reference's tensor sequence.
+// (float32 / float64 CUDA tensors of one dtype): every aggregation is one CSR
+// segment sum (edge order inside each destination) whose result rows are
+// finished as they are stored (relm_mp_plan_segment_sum_scaled: division by
+// the count or arity, residual addition); the backward runs the transposed
+// sums over plans keyed by the sources, with the mean's per-message division
+// applied once per gradient row beforehand (relm_mp_rows_scale).  Other
+// tensors: the reference's tensor sequence.
 
 constexpr int64_t kModeMean = 2;
 
@@ -1147,14 +1149,10 @@ Tensor lgan_aggregate_gpu(const Tensor& src_rows, const Tensor& s, const Tensor&
     }
     GpuPlan gp = csr_plan(t, dim, t_name, s, src_rows.size(0), s_name, true, st);
     Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, src_rows);
-    raise_if(relm_mp_plan_segment_reduce(dt, &gp.plan, nullptr, src_rows.data_ptr(), D, kModeSum,
-                                         out.data_ptr(), scratch.data_ptr(),
-                                         static_cast<size_t>(scratch.numel()), st));
-    if (mode == kModeMean || base.defined())
-        raise_if(relm_mp_rows_scale(dt, out.data_ptr(), nullptr,
-                                    mode == kModeMean ? RELM_MP_DIV_SEGMENT : RELM_MP_DIV_NONE,
-                                    gp.plan.offsets, nullptr, ptr_or_null(base), dim, D,
-                                    out.data_ptr(), st));
+    raise_if(relm_mp_plan_segment_sum_scaled(
+        dt, &gp.plan, src_rows.data_ptr(), D,
+        mode == kModeMean ? RELM_MP_DIV_SEGMENT : RELM_MP_DIV_NONE, nullptr, ptr_or_null(base),
+        out.data_ptr(), scratch.data_ptr(), static_cast<size_t>(scratch.numel()), st));
     return out;
 }
 
@@ -1183,12 +1181,10 @@ Tensor lgan_reverse_gpu(const Tensor& grad, const Tensor& s, const Tensor& t, in
     }
     GpuPlan gp = csr_plan(s, src_rows, s_name, t, grad.size(0), t_name, false, st);
     Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, grad);
-    raise_if(relm_mp_plan_segment_reduce(dt, &gp.plan, nullptr, table.data_ptr(), D, kModeSum,
-                                         out.data_ptr(), scratch.data_ptr(),
-                                         static_cast<size_t>(scratch.numel()), st));
-    if (base.defined())
-        raise_if(relm_mp_rows_scale(dt, out.data_ptr(), nullptr, RELM_MP_DIV_NONE, nullptr, nullptr,
-                                    base.data_ptr(), src_rows, D, out.data_ptr(), st));
+    raise_if(relm_mp_plan_segment_sum_scaled(dt, &gp.plan, table.data_ptr(), D, RELM_MP_DIV_NONE,
+                                             nullptr, ptr_or_null(base), out.data_ptr(),
+                                             scratch.data_ptr(),
+                                             static_cast<size_t>(scratch.numel()), st));
     return out;
 }
 
@@ -1264,13 +1260,11 @@ std::tuple<Tensor, Tensor, Tensor> lgan_pool_reduce(
             GpuPlan gp = csr_plan_rows(s2r, K, "slot_to_relation_instance", st);
             const int dt = dtype_code(slot);
             Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, slot);
-            raise_if(relm_mp_plan_segment_reduce(dt, &gp.plan, nullptr, slot.data_ptr(), D, kModeSum,
-                                                 rpx.data_ptr(), scratch.data_ptr(),
-                                                 static_cast<size_t>(scratch.numel()), st));
             const Tensor arity = contiguous(relation_instance_arities);
-            raise_if(relm_mp_rows_scale(dt, rpx.data_ptr(), nullptr, RELM_MP_DIV_VALUES, nullptr,
-                                        arity.data_ptr<int64_t>(), nullptr, K, D, rpx.data_ptr(),
-                                        st));
+            raise_if(relm_mp_plan_segment_sum_scaled(
+                dt, &gp.plan, slot.data_ptr(), D, RELM_MP_DIV_VALUES, arity.data_ptr<int64_t>(),
+                nullptr, rpx.data_ptr(), scratch.data_ptr(), static_cast<size_t>(scratch.numel()),
+                st));
         }
         return lgan_step_gpu(rpx, lgan_edges64(rr_src, rr_dst, tn_rel, tn_ent, nn_rel, nn_ent),
                              entity_dim_size, mode, st);
