@@ -37,6 +37,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRowsInFlight = 4;          // rows per row group per iteration (inverse plans)
 constexpr int64_t kMaxBlocksX = 1 << 22;  // keeps blocks * 1024 threads below 2^32
+// Largest pair of arrays read into the memory-side cache (256 MB on MI355X)
+// ahead of a write-dominated kernel.
+constexpr size_t kPrefetchMaxBytes = size_t(256) << 20;
 
 template <int G>
 constexpr int batch_rows() {
@@ -774,6 +777,21 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
     }
 }
 
+// Reads [a, a + na) and [b, b + nb) (16-byte units) and discards the data: a
+// read-only pass that leaves the arrays in the memory-side cache for the
+// kernel after it.
+__global__ __launch_bounds__(kThreads) void k_touch(const uint4* __restrict__ a, int64_t na,
+                                                    const uint4* __restrict__ b, int64_t nb) {
+    uint32_t acc = 0;
+    const int64_t n = na + nb;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const uint4 v = i < na ? a[i] : b[i - na];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    asm volatile("" ::"v"(acc));
+}
+
 // Row epilogues of the LGAN aggregations: out[r] = base[r] + in[j] / d_j with
 // j = gather[r] (or r), d_j = 1, max(1, segment size j of a CSR plan) or
 // max(1, (T)div_values[j]); `in` null reads zeros, `base` null adds nothing.
@@ -1270,8 +1288,28 @@ int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* 
     ident.num_keys = rel_rows;
     ident.num_edges = plan.num_edges;
     ident.num_gather = plan.num_keys;
-    if (mode == RELM_MP_MODE_SUM)
+    if (mode == RELM_MP_MODE_SUM) {
+        // The sum backward writes every message row and reads only the
+        // destination rows and dst_idx.  HBM sustains a pure write stream far
+        // better than one with reads interleaved (C2: 0.40 ms against 0.62 ms
+        // per launch when grad_out and dst_idx were not cached), so when both
+        // fit the memory-side cache they are read into it first.
+        const size_t elem = dtype == RELM_MP_F64 ? 8 : 4;
+        const size_t tb = static_cast<size_t>(plan.num_keys) * static_cast<size_t>(emb) * elem;
+        const size_t ib = static_cast<size_t>(plan.num_edges) * sizeof(int64_t);
+        if (tb + ib <= kPrefetchMaxBytes && tb % 16 == 0 && ib % 16 == 0 &&
+            (reinterpret_cast<uintptr_t>(grad_out) | reinterpret_cast<uintptr_t>(dst_idx)) % 16 == 0) {
+            const int64_t units = static_cast<int64_t>((tb + ib) / 16);
+            const int64_t blocks = std::min<int64_t>((units + kThreads * 8 - 1) / (kThreads * 8), 4096);
+            hipLaunchKernelGGL(k_touch, dim3(static_cast<unsigned>(std::max<int64_t>(blocks, 1))),
+                               dim3(kThreads), 0, s, static_cast<const uint4*>(grad_out),
+                               static_cast<int64_t>(tb / 16),
+                               reinterpret_cast<const uint4*>(dst_idx), static_cast<int64_t>(ib / 16));
+            const int rc = hip_error(hipGetLastError(), "relm_mp prefetch kernel");
+            if (rc != RELM_MP_OK) return rc;
+        }
         return compute_gather_last(dtype, ident, dst_idx, grad_out, emb, grad_rel, s);
+    }
     return compute_logsumexp_backward(dtype, ident, dst_idx, grad_out, out, rel_flat, emb, grad_rel,
                                       nullptr, 0, s);
 }
