@@ -145,6 +145,78 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict
     if (threadIdx.x == 0) tot[blockIdx.x] = carry;
 }
 
+// Exclusive scan over tiles of tile-major digit counts: hist[t * kSortBins + d]
+// becomes the number of keys with digit d in the tiles before t; tot[d] the
+// count over all tiles.  Workgroup (g, c) covers digits [32g, 32g + 32) of the
+// tile chunk [c * kColChunk, (c + 1) * kColChunk): for each tile those counts
+// are one 128-byte line, so every load is a full line (digit-major counts
+// written by concurrent tiles on different XCDs would be partial lines).
+// Thread t handles digit 32g + t % 32 over kColItems consecutive tiles.  Two
+// launches: the chunk sums (k_hist_chunk_sums), then each chunk adds the sums
+// of the chunks before it (k_scan_cols).
+constexpr int kColDigits = 32;
+constexpr int kColItems = 16;
+constexpr int kColLanes = kScanThreads / kColDigits;  // tile lanes per digit
+constexpr int kColChunk = kColLanes * kColItems;      // tiles per workgroup
+
+__global__ __launch_bounds__(kScanThreads) void k_hist_chunk_sums(const uint32_t* __restrict__ hist,
+                                                                  int64_t ntiles,
+                                                                  uint32_t* __restrict__ chunk_sum) {
+    __shared__ uint32_t part[kColLanes][kColDigits];
+    const int dl = static_cast<int>(threadIdx.x) % kColDigits;
+    const int tl = static_cast<int>(threadIdx.x) / kColDigits;
+    const int64_t d = static_cast<int64_t>(blockIdx.x) * kColDigits + dl;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kColChunk + static_cast<int64_t>(tl) * kColItems;
+    uint32_t sum = 0;
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) sum += t0 + i < ntiles ? hist[(t0 + i) * kSortBins + d] : 0u;
+    part[tl][dl] = sum;
+    __syncthreads();
+    if (tl == 0) {
+        uint32_t total = 0;
+#pragma unroll
+        for (int l = 0; l < kColLanes; ++l) total += part[l][dl];
+        chunk_sum[static_cast<int64_t>(blockIdx.y) * kSortBins + d] = total;
+    }
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_scan_cols(uint32_t* __restrict__ hist,
+                                                            int64_t ntiles,
+                                                            const uint32_t* __restrict__ chunk_sum,
+                                                            uint32_t* __restrict__ tot) {
+    __shared__ uint32_t part[kColLanes][kColDigits];
+    __shared__ uint32_t prior[kColLanes][kColDigits];
+    const int dl = static_cast<int>(threadIdx.x) % kColDigits;
+    const int tl = static_cast<int>(threadIdx.x) / kColDigits;
+    const int64_t d = static_cast<int64_t>(blockIdx.x) * kColDigits + dl;
+    const int64_t c = blockIdx.y;
+    const int64_t t0 = c * kColChunk + static_cast<int64_t>(tl) * kColItems;
+    uint32_t v[kColItems];
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) v[i] = t0 + i < ntiles ? hist[(t0 + i) * kSortBins + d] : 0u;
+    // the chunks before this one, split over the tile lanes
+    uint32_t pri = 0;
+    for (int64_t cc = tl; cc < c; cc += kColLanes) pri += chunk_sum[cc * kSortBins + d];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) sum += v[i];
+    part[tl][dl] = sum;
+    prior[tl][dl] = pri;
+    __syncthreads();
+    uint32_t before = 0;
+#pragma unroll
+    for (int l = 0; l < kColLanes; ++l) {
+        if (l < tl) before += part[l][dl];
+        before += prior[l][dl];
+    }
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) {
+        if (t0 + i < ntiles) hist[(t0 + i) * kSortBins + d] = before;
+        before += v[i];
+    }
+    if (tl == kColLanes - 1 && c == static_cast<int64_t>(gridDim.y) - 1) tot[d] = before;
+}
+
 // ---- radix sort ----------------------------------------------------------
 
 // Tile digit histogram in LDS: kSubHists copies per wave (lane & 3), so that
@@ -173,7 +245,7 @@ __device__ __forceinline__ uint32_t hist_total(const uint32_t* h) {
 
 // First pass over the caller's int64 arrays: validates every key (and
 // gathered index), narrows both to int32 for the sort passes and counts the
-// tile's digits of the first pass (hist[d * nblocks + tile]).  Gathered
+// tile's digits of the first pass (hist[tile * kSortBins + d]).  Gathered
 // indices equal to their edge ids (or no gathers) are common; a tile made of
 // those only is flagged in tile_plain instead of written, and the first
 // scatter generates its values.
@@ -274,11 +346,11 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
         if (any) atomicOr(&st->gather_mismatch, 1ull);
     }
     __syncthreads();
-    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = hist_total(h);
+    hist[static_cast<int64_t>(blockIdx.x) * kSortBins + threadIdx.x] = hist_total(h);
 }
 
-// Per-tile digit histogram of the narrowed keys, written digit-major:
-// hist[d * nblocks + tile].  Lanes holding the same digit are matched and the
+// Per-tile digit histogram of the narrowed keys, written tile-major:
+// hist[tile * kSortBins + d] (one contiguous row per tile).  Lanes holding the same digit are matched and the
 // lowest of them adds their number to the wave's own histogram, so runs of
 // one key (hub messages, already grouped by the earlier passes) cost one LDS
 // update per wave instead of a chain of conflicting atomics.
@@ -311,7 +383,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
     uint32_t t = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) t += h[w * kSortBins + threadIdx.x];
-    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = t;
+    hist[static_cast<int64_t>(blockIdx.x) * kSortBins + threadIdx.x] = t;
 }
 
 // Stable scatter of one tile.  Wave w owns tile positions [w*1024, (w+1)*1024)
@@ -340,7 +412,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     constexpr uint32_t dmask = (1u << BITS) - 1u;
     // this tile's start within each digit does not depend on the keys: fetch
     // it together with them
-    const uint32_t tile_prefix = hist_scanned[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x];
+    const uint32_t tile_prefix = hist_scanned[static_cast<int64_t>(blockIdx.x) * kSortBins + threadIdx.x];
     const uint32_t dt = digit_tot[threadIdx.x];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][threadIdx.x] = 0;
@@ -387,7 +459,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     const uint32_t incl = block_inclusive_scan<kSortThreads>(run, scan_lds, total);
     dstart[dd] = incl - run;
     // global start of digit dd: all smaller digits of every tile, then this
-    // digit in the tiles before this one (rows of hist_scanned)
+    // digit in the tiles before this one (this tile's row of hist_scanned)
     uint32_t all;
     const uint32_t dincl = block_inclusive_scan<kSortThreads>(dt, scan_lds, all);
     gbase[dd] = (dincl - dt) + tile_prefix;
@@ -670,8 +742,9 @@ int64_t sort_tiles(int64_t n) { return std::max<int64_t>(1, (n + kSortTile - 1) 
 
 size_t sort_hist_words(int64_t n) {
     const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
-    // per-tile digit counts, then the digit totals
-    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks + 1);
+    const int64_t chunks = (nblocks + kColChunk - 1) / kColChunk;
+    // per-tile digit counts, the digit totals, the per-chunk digit sums
+    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks + 1 + chunks);
 }
 
 namespace {
@@ -705,6 +778,8 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
     const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
     const int64_t hist_n = static_cast<int64_t>(kSortBins) * nblocks;
     uint32_t* digit_tot = buf.hist + hist_n;
+    const int64_t col_chunks = (nblocks + kColChunk - 1) / kColChunk;
+    uint32_t* chunk_sum = digit_tot + kSortBins;
     // the narrowed input goes to the b buffers; pass p writes a, b, a, ... and
     // the last pass the plan arrays
     const uint32_t* in_k = buf.keys_b;
@@ -732,8 +807,13 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
             err = after_validation();
             if (err != hipSuccess) return err;
         }
-        hipLaunchKernelGGL(k_scan_rows, dim3(kSortBins), dim3(kScanThreads), 0, s, buf.hist, nblocks,
-                           digit_tot);
+        const dim3 cgrid(kSortBins / kColDigits, static_cast<unsigned>(col_chunks));
+        hipLaunchKernelGGL(k_hist_chunk_sums, cgrid, dim3(kScanThreads), 0, s,
+                           static_cast<const uint32_t*>(buf.hist), nblocks, chunk_sum);
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        hipLaunchKernelGGL(k_scan_cols, cgrid, dim3(kScanThreads), 0, s, buf.hist, nblocks,
+                           static_cast<const uint32_t*>(chunk_sum), digit_tot);
         err = hipGetLastError();
         if (err != hipSuccess) return err;
         const uint32_t* plain = p == 0 ? static_cast<const uint32_t*>(buf.tile_plain) : nullptr;
