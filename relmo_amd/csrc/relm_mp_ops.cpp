@@ -1253,6 +1253,9 @@ std::tuple<Tensor, Tensor, Tensor> lgan_pool_reduce(
         c10::OptionalDeviceGuard guard(slot_messages.device());
         hipStream_t st = current_stream(slot_messages);
         const Tensor slot = contiguous(slot_messages);
+        if (slot.numel() > 0 && K == 0)  // every slot's relation instance is out of range
+            check_in_bounds(index64(slot_to_relation_instance)[0].item<int64_t>(), 0,
+                            "slot_to_relation_instance");
         const bool pooled = slot.numel() > 0 && K > 0;
         Tensor rpx = pooled ? at::empty({K, D}, slot.options()) : at::zeros({K, D}, slot.options());
         if (pooled) {
@@ -1366,13 +1369,15 @@ Tensor lgan_pool_reduce_backward(const Tensor& grad_relation_pair_x, const Tenso
         const Tensor s2r = index64(slot_to_relation_instance);
         const int64_t E = s2r.numel(), D = g.size(1);
         Tensor grad_slot = at::empty({E, D}, g.options());
-        if (E > 0 && D > 0) {
+        if (E > 0) {
             // each slot reads its relation instance's row and arity
             const int64_t bound = std::min<int64_t>(relation_count, relation_instance_arities.numel());
             const auto mm = at::aminmax(s2r);
             const int64_t lo = std::get<0>(mm).item<int64_t>(), hi = std::get<1>(mm).item<int64_t>();
             if (lo < 0) check_in_bounds(lo, bound, "slot_to_relation_instance");
             check_in_bounds(hi, bound, "slot_to_relation_instance");
+        }
+        if (E > 0 && D > 0) {
             const Tensor arity = contiguous(relation_instance_arities);
             raise_if(relm_mp_rows_scale(dtype_code(g), g.data_ptr(), s2r.data_ptr<int64_t>(),
                                         RELM_MP_DIV_VALUES, nullptr, arity.data_ptr<int64_t>(),

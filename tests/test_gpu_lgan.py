@@ -181,6 +181,10 @@ def test_lgan_empty_and_degenerate_on_gpu(ops) -> None:
         ops.lgan_relation_graph_step(x, torch.tensor([0, 6], device=DEV), torch.tensor([1, 2], device=DEV),
                                      empty, empty, empty, empty, 3, 0)
     with pytest.raises(RuntimeError, match="slot_to_relation_instance index out of bounds"):
+        ops.lgan_pool_reduce(torch.ones(2, 4, device=DEV), torch.tensor([0, 0], device=DEV),
+                             torch.zeros(0, dtype=torch.long, device=DEV),
+                             empty, empty, empty, empty, empty, empty, 3, 0)
+    with pytest.raises(RuntimeError, match="slot_to_relation_instance index out of bounds"):
         ops.lgan_pool_reduce_backward(x, torch.zeros(3, 4, device=DEV), torch.zeros(3, 4, device=DEV),
                                       torch.tensor([0, 6], device=DEV),
                                       torch.ones(6, dtype=torch.long, device=DEV),
