@@ -808,10 +808,12 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
             if (err != hipSuccess) return err;
         }
         const dim3 cgrid(kSortBins / kColDigits, static_cast<unsigned>(col_chunks));
-        hipLaunchKernelGGL(k_hist_chunk_sums, cgrid, dim3(kScanThreads), 0, s,
-                           static_cast<const uint32_t*>(buf.hist), nblocks, chunk_sum);
-        err = hipGetLastError();
-        if (err != hipSuccess) return err;
+        if (col_chunks > 1) {  // a single chunk has no chunks before it
+            hipLaunchKernelGGL(k_hist_chunk_sums, cgrid, dim3(kScanThreads), 0, s,
+                               static_cast<const uint32_t*>(buf.hist), nblocks, chunk_sum);
+            err = hipGetLastError();
+            if (err != hipSuccess) return err;
+        }
         hipLaunchKernelGGL(k_scan_cols, cgrid, dim3(kScanThreads), 0, s, buf.hist, nblocks,
                            static_cast<const uint32_t*>(chunk_sum), digit_tot);
         err = hipGetLastError();
