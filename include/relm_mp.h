@@ -180,7 +180,9 @@ typedef struct relm_mp_plan {
     int32_t* item_first;     /* CSR: [num_items + 1] first key of each item    */
     int32_t* item_short;     /* CSR: [num_items + 1] short_off[item_first[j]]  */
     int32_t* short_off;      /* CSR: [num_keys + 1] edges of non-hub segments before each key */
-    int32_t* short_gather;   /* CSR: [num_short] gather_sorted without the hub segments */
+    int32_t* short_gather;   /* CSR: [num_short] gather_sorted without the hub segments;
+                                equal to gather_sorted when there is no hub (set so once the
+                                statistics are read: a waiting build, relm_mp_plan_read_counts) */
     const relm_mp_plan_counts* counts; /* the statistics, in device memory */
 } relm_mp_plan;
 

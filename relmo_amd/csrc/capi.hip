@@ -183,6 +183,9 @@ int read_counts(relm_mp_plan* plan, hipStream_t s) {
     plan->num_multi_hubs = c.num_multi_hubs;
     plan->num_items = c.num_items;
     plan->num_short = c.num_short;
+    // without hubs the short segments are the whole sorted gather array, which
+    // the key index then does not copy
+    if (c.num_hubs == 0) plan->short_gather = plan->gather_sorted;
     return RELM_MP_OK;
 }
 

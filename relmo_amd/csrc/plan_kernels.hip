@@ -694,8 +694,9 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
         pc->num_short = W - num_keys;
         return;
     }
-    // the short segment's gathered rows, back to back in key order
-    if (f.deg > 0 && f.deg <= kHubThreshold) {
+    // the short segment's gathered rows, back to back in key order (without
+    // hubs that is gather_sorted itself: nothing to copy, the walker reads it)
+    if (totals[0] != 0 && f.deg > 0 && f.deg <= kHubThreshold) {
         const int64_t b = offsets[k];
         int64_t j = 0;
         for (; j + 4 <= f.deg; j += 4) {

@@ -388,10 +388,10 @@ __global__ __launch_bounds__(kThreads) void k_fill(T* __restrict__ p, int64_t n,
 // per-key loop, so the row groups of a wave stay in step.
 template <typename T, int V, int G, class Op, class Epi>
 __global__ __launch_bounds__(kThreads) void k_walk_items(
-    const int32_t* __restrict__ short_off, const int32_t* __restrict__ short_gather,
-    const int32_t* __restrict__ item_first, const int32_t* __restrict__ item_short,
-    const relm_mp_plan_counts* __restrict__ pc, int64_t num_keys, T* __restrict__ out, Op op,
-    Epi epi) {
+    const int32_t* __restrict__ short_off, const int32_t* __restrict__ short_gather_in,
+    const int32_t* __restrict__ gather_sorted, const int32_t* __restrict__ item_first,
+    const int32_t* __restrict__ item_short, const relm_mp_plan_counts* __restrict__ pc,
+    int64_t num_keys, T* __restrict__ out, Op op, Epi epi) {
     constexpr int R = kThreads / G;
     constexpr int U = batch_rows<G>();
     // R items hold at most R * kItemSize keys and R * kItemSize + kHubThreshold
@@ -411,6 +411,8 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
     const int64_t D = op.D;
     const int64_t num_items = pc->num_items;
     const int64_t num_short = pc->num_short;
+    // a plan without hubs has no separate short-segment copy
+    const int32_t* __restrict__ short_gather = pc->num_hubs == 0 ? gather_sorted : short_gather_in;
     // block-uniform loop: every thread reaches the barriers below
     for (int64_t ib = static_cast<int64_t>(blockIdx.x) * R; ib < num_items;
          ib += static_cast<int64_t>(gridDim.x) * R) {
@@ -1016,8 +1018,8 @@ int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, 
     const void* walk = reinterpret_cast<const void*>(&k_walk_items<T, V, G, Op, Epi>);
     hipLaunchKernelGGL((k_walk_items<T, V, G, Op, Epi>),
                        persistent_grid(walk, items, kThreads / G, slices, 4), dim3(kThreads), 0, s,
-                       plan.short_off, plan.short_gather, plan.item_first, plan.item_short,
-                       plan.counts, plan.num_keys, out, op, epi);
+                       plan.short_off, plan.short_gather, plan.gather_sorted, plan.item_first,
+                       plan.item_short, plan.counts, plan.num_keys, out, op, epi);
     int rc = hip_error(hipGetLastError(), "relm_mp item kernel");
     // no hub when the counts say so, or when no segment can be longer than the threshold
     if (rc != RELM_MP_OK || plan.num_hubs == 0 || E <= kHubThreshold) return rc;
