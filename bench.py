@@ -506,7 +506,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the op library has no multi-GPU path: see DESIGN.md for how it would shard).", file=sys.stderr)
+              "(the op library has no multi-GPU path; one GPU holds a whole C2 / C3 batch).", file=sys.stderr)
         return 2
 
     os.environ["RELM_MP_FALLBACK"] = "error"
