@@ -108,10 +108,13 @@ __device__ __forceinline__ T max_num(T a, T b) { return fmax(a, b); }
 template <typename T>
 __device__ __forceinline__ T dev_log(T x);
 // Callers take the log of a sum of exp terms one of which is exp(0) = 1, so
-// x >= 1 (or NaN): the hardware log2 (v_log_f32, ~1 ulp on normal inputs)
-// without the denormal range reduction of logf.
+// x >= 1 (or NaN, or +inf): the hardware log2 (v_log_f32, ~1 ulp on normal
+// inputs) times ln 2, without the denormal range reduction and the
+// extra-precision ln 2 product of logf (which __logf also expands to).
 template <>
-__device__ __forceinline__ float dev_log<float>(float x) { return __logf(x); }
+__device__ __forceinline__ float dev_log<float>(float x) {
+    return __builtin_amdgcn_logf(x) * 0.693147180559945309f;
+}
 template <>
 __device__ __forceinline__ double dev_log<double>(double x) { return log(x); }
 
