@@ -189,3 +189,38 @@ def test_lgan_empty_and_degenerate_on_gpu(ops) -> None:
                                       torch.tensor([0, 6], device=DEV),
                                       torch.ones(6, dtype=torch.long, device=DEV),
                                       empty, empty, empty, empty, empty, empty, 6, 0)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_lgan_random_shapes_match_oracle(ops, seed) -> None:
+    """Random small shapes: D from 1 to 70 (odd widths take the scalar path),
+    float32 / float64, int32 / int64 indices, empty edge sets, both modes."""
+
+    rng = np.random.default_rng(100 + seed)
+    K, ent, E = int(rng.integers(1, 300)), int(rng.integers(0, 120)), int(rng.integers(0, 700))
+    D = int(rng.choice([1, 3, 4, 7, 16, 33, 64, 70]))
+    dtype = np.float64 if seed % 3 == 0 else np.float32
+    itype = np.int32 if seed % 2 else np.int64
+    n = [int(rng.integers(0, 900)) if rng.random() > 0.15 else 0 for _ in range(3)]
+    if ent == 0:
+        n[1] = n[2] = 0
+    edges = [rng.integers(0, K, n[0]), rng.integers(0, K, n[0]),
+             rng.integers(0, K, n[1]), rng.integers(0, max(ent, 1), n[1]),
+             rng.integers(0, K, n[2]), rng.integers(0, max(ent, 1), n[2])]
+    edges = [e.astype(itype) for e in edges]
+    slot = rng.standard_normal((E, D)).astype(dtype)
+    s2r = rng.integers(0, K, E).astype(itype)
+    arity = rng.integers(-1, 4, K)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)  # noqa: E731
+    for mode in (0, 2):
+        _log(f"lgan random seed {seed} mode {mode}: K={K} ent={ent} E={E} D={D} {dtype.__name__} {itype.__name__}")
+        got = ops.lgan_pool_reduce(t(slot), t(s2r), t(arity), *map(t, edges), ent, mode)
+        want = lgan_oracle.lgan_pool_reduce(slot, s2r, arity, *edges, ent, mode)
+        for g, w in zip(got, want):
+            np.testing.assert_allclose(g.cpu().numpy(), w, rtol=1e-5 if dtype == np.float32 else 1e-12,
+                                       atol=1e-5 if dtype == np.float32 else 1e-12)
+        gr = [rng.standard_normal(w.shape).astype(dtype) for w in want]
+        grad = ops.lgan_pool_reduce_backward(*map(t, gr), t(s2r), t(arity), *map(t, edges), K, mode)
+        want_g = lgan_oracle.lgan_pool_reduce_backward(*gr, s2r, arity, *edges, K, mode)
+        np.testing.assert_allclose(grad.cpu().numpy(), want_g, rtol=1e-5 if dtype == np.float32 else 1e-12,
+                                   atol=1e-5 if dtype == np.float32 else 1e-12)

@@ -182,3 +182,37 @@ def test_pack_then_reduce_gradients_on_gpu(mode) -> None:
         grads.append([x.grad.cpu() for x in xs])
     for g_cpu, g_gpu in zip(*grads):
         assert torch.equal(g_cpu, g_gpu)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_pack_random_layouts_match_oracle(ops, seed) -> None:
+    rng = np.random.default_rng(200 + seed)
+    n_values, n_parts = int(rng.integers(1, 6)), int(rng.integers(1, 40))
+    rows = [int(r) for r in rng.integers(1, 5000, n_values)]
+    xs = [torch.zeros((r, 2), device=DEV) for r in rows]
+    xs_np = [np.zeros((r, 0), np.float32) for r in rows]
+    lens = [int(v) if rng.random() > 0.2 else 0 for v in rng.integers(0, 20000, n_parts)]
+    ids = [int(v) for v in rng.integers(0, n_values, n_parts)]
+    arity = [int(v) for v in rng.integers(1, 6, n_parts)]
+    pos = [int(rng.integers(0, a)) for a in arity]
+    slot = [int(v) for v in rng.integers(-(2**40), 2**40, n_parts)]
+    src = [rng.integers(-(2**50), 2**50, n) for n in lens]
+    dst = [rng.integers(-(2**50), 2**50, n) for n in lens]
+    st, dt = [torch.from_numpy(a).to(DEV) for a in src], [torch.from_numpy(a).to(DEV) for a in dst]
+    _log(f"pack random seed {seed}: {n_parts} parts, {sum(lens)} pairs")
+    got = ops.fanout_pack_from_edges(xs, st, dt, ids, arity, pos, slot)
+    want = pack_oracle.fanout_pack_from_edges(xs_np, src, dst, ids, arity, pos, slot)
+    for g, w in zip(got[1:], want[1:]):
+        assert np.array_equal(g.cpu().numpy(), w)
+    for mode in (0, 1):
+        got = ops.fanin_pack_from_edges(xs, st, dt, ids, arity, pos, mode)
+        want = pack_oracle.fanin_pack_from_edges(xs_np, src, dst, ids, arity, pos, mode)
+        for g, w in zip(got[1:], want[1:]):
+            assert np.array_equal(g.cpu().numpy(), w)
+    k = min(n_values, n_parts)
+    for op, fn in ((ops.fanout_pack_multi, pack_oracle.fanout_pack_multi),
+                   (ops.fanin_pack_multi, pack_oracle.fanin_pack_multi)):
+        got = op(xs[:k], st[:k], dt[:k])
+        want = fn(xs_np[:k], src[:k], dst[:k])
+        for g, w in zip(got[1:], want[1:]):
+            assert np.array_equal(g.cpu().numpy(), w)
