@@ -154,3 +154,8 @@ if torch is not None:
                 lambda v, *a: lgan_relation_graph_step_python(v, *a),
                 x, (*edges, ctx.entity_dim_size, ctx.mode), (grad_rpx, grad_tn, grad_nn))
             return (grad, *none)
+
+
+if torch is None:  # the facade still imports; its functions raise in require_torch first
+    _FanoutScatterFunction = _FaninReduceSumFunction = _FaninReduceLogSumExpFunction = None
+    _LGANPoolReduceFunction = _LGANRelationGraphStepFunction = None

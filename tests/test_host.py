@@ -530,3 +530,37 @@ def test_lgan_facade_autograd_on_cpu(mode) -> None:
         (torch.randn(K, D, dtype=torch.float64, requires_grad=True),))
     with pytest.raises(ValueError, match="supports only mode='sum' or mode='mean'"):
         mp._lgan_relation_graph_step(slot, *edges, entity_dim_size=ent, mode="max")
+
+
+def test_facade_imports_without_torch() -> None:
+    """As relmo's facade (tests/python/test_mp_module_layout.py:21-60): without
+    torch the module imports, available() is False and the ops fail lazily."""
+
+    code = """
+import builtins, importlib, sys
+real_import = builtins.__import__
+def fake_import(name, globals=None, locals=None, fromlist=(), level=0):
+    if name == "torch" or name.startswith("torch."):
+        raise ModuleNotFoundError("simulated missing torch")
+    return real_import(name, globals, locals, fromlist, level)
+builtins.__import__ = fake_import
+for key in list(sys.modules):
+    if key == "torch" or key.startswith("torch.") or key.startswith("relmo_amd"):
+        sys.modules.pop(key, None)
+mp = importlib.import_module("relmo_amd.mp")
+assert mp.torch is None and mp.available() is False
+assert mp.activation_code(("relu",)) == 1
+calls = [lambda: mp.fanout_scatter(None, None, None, 0), lambda: mp.fanin_reduce(None, None, None, 0, 0),
+         lambda: mp.fanout_pack_multi([], [], []),
+         lambda: mp._lgan_relation_graph_step(None, None, None, None, None, None, None,
+                                              entity_dim_size=0, mode="sum")]
+for call in calls:
+    try:
+        call()
+    except ModuleNotFoundError as exc:
+        assert "requires torch" in str(exc)
+    else:
+        raise AssertionError("no lazy failure")
+"""
+    proc = subprocess.run([sys.executable, "-c", code], cwd=str(REPO), capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr or proc.stdout
