@@ -15,6 +15,18 @@ __device__ __forceinline__ unsigned long long lanemask_lt() {
     return (1ull << lane_id()) - 1ull;
 }
 
+// The dispatcher hands workgroups to the 8 XCDs round robin (workgroup b to
+// XCD b % 8).  xcd_tile maps workgroup b to a tile so that each XCD works
+// through one contiguous range of tiles: neighbouring tiles then share an L2,
+// where the partial lines they write at the seams of their output ranges
+// merge.  A bijection of [0, ntiles).
+__device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t ntiles) {
+    constexpr int64_t kXcds = 8;
+    const int64_t q = ntiles / kXcds, r = ntiles % kXcds;
+    const int64_t x = b % kXcds;
+    return x * q + (x < r ? x : r) + b / kXcds;
+}
+
 // Lanes of the wave whose `digit` (of BITS bits) equals this lane's, among
 // the lanes in `active`.  One ballot per bit; each bit keeps the lanes whose
 // ballot bit agrees with this lane's digit bit, peers &= ~(ballot ^ bitmask):

@@ -408,18 +408,19 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
 
     const int lane = lane_id();
     const int wave = static_cast<int>(threadIdx.x) / kWave;
-    const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+    const int64_t tile = xcd_tile(blockIdx.x, nblocks);
+    const int64_t tile_base = tile * kSortTile;
     constexpr uint32_t dmask = (1u << BITS) - 1u;
     // this tile's start within each digit does not depend on the keys: fetch
     // it together with them
-    const uint32_t tile_prefix = hist_scanned[static_cast<int64_t>(blockIdx.x) * kSortBins + threadIdx.x];
+    const uint32_t tile_prefix = hist_scanned[tile * kSortBins + threadIdx.x];
     const uint32_t dt = digit_tot[threadIdx.x];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][threadIdx.x] = 0;
     __syncthreads();
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
-    const bool plain = tile_plain != nullptr && tile_plain[blockIdx.x] != 0u;
+    const bool plain = tile_plain != nullptr && tile_plain[tile] != 0u;
     const int64_t wave_base = tile_base + wave * kPerWave + lane;
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {

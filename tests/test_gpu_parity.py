@@ -164,7 +164,9 @@ def test_c1_outputs_match_reference_digests() -> None:
     [(1, 1000, False), (2, 5000, False), (300, 1, False), (4096, 98304, False),
      (50_000, 400_000, True), ((1 << 20) + 3, 300_000, False), (70_000, 4096 * 3 + 17, True),
      # three sort passes; several tiles per sort chunk (more tiles than resident workgroups)
-     ((1 << 23) + 1, 200_000, False), (1 << 20, 5_000_003, True), ((1 << 21) - 7, 4_000_000, False)],
+     ((1 << 23) + 1, 200_000, False), (1 << 20, 5_000_003, True), ((1 << 21) - 7, 4_000_000, False),
+     # 15 to 20-bit keys over 2^20 edges and more, a partial last tile of 5 keys
+     (1 << 15, 2_000_000, False), ((1 << 18) + 5, 1 << 20, True), (1 << 20, 16_384 * 70 + 5, False)],
 )
 def test_csr_plan_is_the_stable_counting_order(num_keys: int, num_edges: int, skew: bool) -> None:
     from relmo_amd import capi
@@ -242,6 +244,31 @@ def test_async_csr_plan_computes_before_its_counts_are_read(num_keys: int, num_e
     bad[num_edges // 2] = num_keys
     with pytest.raises((RuntimeError, ValueError), match=rf"key index out of bounds: {num_keys} not in"):
         capi.csr_plan(_t(bad), num_keys, None, num_edges, wait_counts=False)
+
+
+@pytest.mark.parametrize("large", [True, False])
+def test_csr_plan_gathers_in_mixed_tiles(large: bool) -> None:
+    """Gathered indices equal to their edge ids in some first-pass tiles and
+    not in others: the first scatter generates the values of the former and
+    reads the latter."""
+
+    from relmo_amd import capi
+
+    num_keys = (1 << 20) if large else 3000
+    n = 3_000_001 if large else 300_001
+    _log(f"csr plan mixed gather tiles keys={num_keys} edges={n}")
+    rng = np.random.default_rng(5 + large)
+    keys = rng.integers(0, num_keys, n)
+    gathers = np.arange(n)
+    tiles = rng.random((n + 4095) // 4096) < 0.5
+    for t in np.flatnonzero(tiles):
+        lo, hi = 4096 * t, min(4096 * (t + 1), n)
+        gathers[lo:hi] = rng.permutation(gathers[lo:hi])
+    bp = capi.csr_plan(_t(keys), num_keys, _t(gathers), n)
+    offsets, perm = oracle.csr_build(keys, num_keys)
+    assert np.array_equal(_np(bp.offsets), offsets)
+    assert np.array_equal(_np(bp.gather_sorted), gathers[perm])
+    assert bp.plan.gather_identity == 0
 
 
 def test_inverse_plan_matches_oracle() -> None:
