@@ -280,6 +280,58 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
     return res
 
 
+def bench_slots(torch, steps: int) -> dict:
+    """The central layer's input assembly at a C5-like shape: 2^20 relation
+    nodes x 3 argument slots of D = 128 after 14 context columns, 2^19
+    objects, 2 arguments per node on average (2^21 fanout edges, slots of
+    nodes with fewer arguments stay zero).  Timed, forward and forward +
+    backward (random upstream gradient, gradients for the objects and the
+    context): mp.fanout_concat (fanout_scatter_into / fanout_scatter_backward_from)
+    against the reference's formulation (fanout_scatter into [nodes * 3, D],
+    then torch.cat with the context).  Algorithmic bytes of the forward:
+    the [nodes, 14 + 3 * 128] result written, the context and one object row
+    per edge read, the indices read."""
+
+    from relmo_amd import mp
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    nodes, slots, emb, ctx_cols, objects = 1 << 20, 3, 128, 14, 1 << 19
+    edges = 2 * nodes
+    x = torch.randn(objects, emb, device=dev, generator=gen, requires_grad=True)
+    context = torch.randn(nodes, ctx_cols, device=dev, generator=gen, requires_grad=True)
+    src = torch.randint(0, objects, (edges,), device=dev, generator=gen)
+    dst = torch.randperm(nodes * slots, device=dev, generator=gen)[:edges]
+    grad = torch.randn(nodes, ctx_cols + slots * emb, device=dev, generator=gen)
+
+    def into():
+        return mp.fanout_concat(context, x, src, dst, slots)
+
+    def composed():
+        args = mp.fanout_scatter(x, src, dst, nodes * slots)
+        return torch.cat([context, args.view(nodes, slots * emb)], dim=1)
+
+    res = {"config": {"nodes": nodes, "slots": slots, "emb": emb, "context_cols": ctx_cols,
+                      "objects": objects, "edges": edges}}
+    sync = torch.cuda.synchronize
+    for name, fn in (("fanout_concat", into), ("fanout_then_cat", composed)):
+        with torch.no_grad():
+            t_f = timed(fn, steps, 2, sync)
+
+        def step(fn=fn):
+            x.grad = None
+            context.grad = None
+            fn().backward(grad)
+
+        t_fb = timed(step, steps, 2, sync)
+        res[name] = {"ms_fwd": t_f * 1e3, "ms_fwd_bwd": t_fb * 1e3}
+    fwd_bytes = 4 * (nodes * (ctx_cols + slots * emb) + nodes * ctx_cols + edges * emb) + 16 * edges
+    res["bytes_fwd"] = fwd_bytes
+    res["gbs_fwd_fanout_concat"] = gbs(fwd_bytes, res["fanout_concat"]["ms_fwd"] / 1e3)
+    return res
+
+
 def bench_pack(torch, steps: int) -> dict:
     """Index preparation before one fanout / fanin call: fanout_pack_from_edges
     and fanin_pack_from_edges (mode 0) over 2 value parts of 2^20 x 64 f32 and
@@ -499,7 +551,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "pack", "lgan", "copy"],
+    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "pack", "lgan", "slots",
+                                       "copy"],
                     default=None,
                     help="run one workload only and print its figures (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -530,6 +583,7 @@ def main() -> int:
               "c5": lambda: bench_models(torch, "c5", args.steps, args.warmup),
               "pack": lambda: bench_pack(torch, args.steps),
               "lgan": lambda: bench_lgan(torch, args.steps),
+              "slots": lambda: bench_slots(torch, args.steps),
               "copy": lambda: bench_copy(torch, args.steps)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
@@ -548,6 +602,8 @@ def main() -> int:
     extra["pack"] = bench_pack(torch, max(5, args.steps // 2))
     log("LGAN pooling step ...")
     extra["lgan"] = bench_lgan(torch, max(5, args.steps // 2))
+    log("fanout into argument slots ...")
+    extra["slots"] = bench_slots(torch, max(5, args.steps // 2))
     log("C4 RelationalGNN training step ...")
     extra["c4_relational_gnn"] = bench_models(torch, "c4", 5, 2)
     log("C5 CentralizedRelationalGNN training step ...")

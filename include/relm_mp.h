@@ -311,6 +311,35 @@ int relm_mp_plan_segment_sum_scaled(int dtype, const relm_mp_plan* plan, const v
                                     const void* base, void* out, void* scratch,
                                     size_t scratch_bytes, relm_mp_stream_t stream);
 
+/* ---- rows in groups (fanout straight into a wider input matrix) ----------- */
+
+/* Grouped row layout: row r of a [rows, emb] operand lies at element offset
+ * (r / group) * group_stride + (r % group) * emb from its base pointer, i.e.
+ * `group` consecutive rows per line of a wider row-major matrix whose lines
+ * are group_stride elements apart (group >= 1, group_stride >= group * emb).
+ * The relational models assemble their central MLP input as [nodes, width]
+ * lines of context columns followed by max_arity argument slots of emb
+ * columns (relmo/models/hetero_mp/fused.py:299-375: fanout_scatter into
+ * args_flat [nodes * max_arity, emb], reshape, copy into all_inputs).  With
+ * group = max_arity, group_stride = width and the base pointer at the first
+ * argument column, the fanout writes there directly and its backward reads
+ * the gradient from there, without the [nodes * max_arity, emb] copy.  No
+ * counterpart in the reference, which has no out-variant of the op. */
+
+/* relm_mp_plan_gather_last with grouped output rows: row k (k < num_keys,
+ * num_keys a multiple of group) is written at the grouped offset; the
+ * elements between the rows (other columns of the lines) are not touched. */
+int relm_mp_plan_gather_last_grouped(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                                     const void* table, int64_t emb, int64_t group,
+                                     int64_t group_stride, void* out, relm_mp_stream_t stream);
+/* relm_mp_plan_segment_reduce mode 0 over a CSR plan whose gathered rows are
+ * read from `table` in the grouped layout (gathered index r < table_rows, a
+ * multiple of group); out[num_keys, emb] is row-major. */
+int relm_mp_plan_segment_sum_grouped(int dtype, const relm_mp_plan* plan, const void* table,
+                                     int64_t table_rows, int64_t emb, int64_t group,
+                                     int64_t group_stride, void* out, void* scratch,
+                                     size_t scratch_bytes, relm_mp_stream_t stream);
+
 /* ---- content match (plan reuse across equal indices) ----------------------- */
 
 /* No counterpart in the reference (its ops build their index structures in

@@ -22,6 +22,9 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   fanin_reduce_logsumexp_backward pinned: reference library (rtol 1e-6), softmax
                                   weights sum to one, float64 finite differences
   csr_build / inverse_build       pinned: numpy stable argsort / bincount, brute force
+  fanout_into_slots /             compositions of the two fanout functions above
+  fanout_backward_from_slots      with numpy's row-major reshape (the models' input
+                                  assembly); pinned through them and a per-element loop
 """
 
 from __future__ import annotations
@@ -129,6 +132,30 @@ def fanout_scatter_backward(grad_out, src_global_idx, flat_dst, x_rows: int) -> 
             ctypes.c_int64(src.size), ctypes.c_int64(out.shape[0]), _p(out), ctypes.byref(bad))
     _raise(rc, bad, ("src_global_idx", "flat_dst"))
     return out
+
+
+def fanout_into_slots(x_cat, src_global_idx, flat_dst, out, col_offset: int, slots: int) -> np.ndarray:
+    """The central input assembly of relmo/models/hetero_mp/fused.py:299-375:
+    fanout_scatter into [lines * slots, D] rows, reshaped to [lines, slots * D]
+    and copied into columns [col_offset, col_offset + slots * D) of a copy of
+    ``out``; the other columns keep their values."""
+
+    x = _vals(x_cat)
+    res = np.array(out, copy=True)
+    lines, d = res.shape[0], x.shape[1]
+    rows = fanout_scatter(x, src_global_idx, flat_dst, lines * slots)
+    res[:, col_offset:col_offset + slots * d] = rows.reshape(lines, slots * d)
+    return res
+
+
+def fanout_backward_from_slots(grad, src_global_idx, flat_dst, x_rows: int, col_offset: int,
+                               slots: int, emb: int) -> np.ndarray:
+    """Backward of ``fanout_into_slots``: fanout_scatter_backward of the
+    argument columns of ``grad`` read as [lines * slots, emb] rows."""
+
+    g = _vals(grad)
+    rows = np.ascontiguousarray(g[:, col_offset:col_offset + slots * emb]).reshape(-1, emb)
+    return fanout_scatter_backward(rows, src_global_idx, flat_dst, x_rows)
 
 
 def fanin_reduce_sum(rel_flat, flat_src, dst_idx, dim_size: int) -> np.ndarray:

@@ -60,6 +60,8 @@ EXPORTED_SYMBOLS = (
     "relm_mp_index_match",
     "relm_mp_rows_scale",
     "relm_mp_plan_segment_sum_scaled",
+    "relm_mp_plan_gather_last_grouped",
+    "relm_mp_plan_segment_sum_grouped",
 )
 
 
@@ -158,6 +160,9 @@ _SIGNATURES = {
     "relm_mp_index_match_workspace_size": (_sz, []),
     "relm_mp_rows_scale": (_int, [_int, _vp, _vp, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "relm_mp_plan_segment_sum_scaled": (_int, [_int, _PP, _vp, _i64, _int, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "relm_mp_plan_gather_last_grouped": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "relm_mp_plan_segment_sum_grouped": (
+        _int, [_int, _PP, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_index_match": (
         _int,
         [_vp, _vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.c_int32,
@@ -511,6 +516,45 @@ def plan_gather_last(bp: BuiltPlan, table: torch.Tensor, gathers: torch.Tensor |
         lib().relm_mp_plan_gather_last(
             _dtype(table), ctypes.byref(bp.plan), _ptr(gathers), _ptr(table), emb, _ptr(out),
             _stream(table),
+        )
+    )
+    return out
+
+
+def _slot_base(mat: torch.Tensor, col_offset: int) -> int:
+    assert mat.dim() == 2 and mat.stride(1) == 1
+    return mat.data_ptr() + col_offset * mat.element_size()
+
+
+def plan_gather_last_grouped(bp: BuiltPlan, table: torch.Tensor, out: torch.Tensor, col_offset: int,
+                             group: int, gathers: torch.Tensor | None = None) -> torch.Tensor:
+    """Gather of the plan's rows into ``out`` [lines, width]: row k goes to line
+    k // group, columns col_offset + (k % group) * D ... + D."""
+
+    emb = table.size(1)
+    check(
+        lib().relm_mp_plan_gather_last_grouped(
+            _dtype(table), ctypes.byref(bp.plan), _ptr(gathers), _ptr(table), emb, group,
+            out.stride(0), _slot_base(out, col_offset), _stream(table),
+        )
+    )
+    return out
+
+
+def plan_segment_sum_grouped(bp: BuiltPlan, table: torch.Tensor, col_offset: int, group: int,
+                             emb: int) -> torch.Tensor:
+    """Segment sums over a CSR plan whose gathered rows are read from the
+    argument columns of ``table`` [lines, width] (row r = line r // group,
+    columns col_offset + (r % group) * emb ... + emb)."""
+
+    out = torch.empty(bp.plan.num_keys, emb, dtype=table.dtype, device=table.device)
+    n = lib().relm_mp_plan_compute_scratch_bytes(ctypes.byref(bp.plan), emb, _dtype(table), 0)
+    scratch = _bytes(n, table)
+    check(
+        lib().relm_mp_plan_segment_sum_grouped(
+            _dtype(table), ctypes.byref(bp.plan), _slot_base(table, col_offset),
+            table.size(0) * group, emb, group, table.stride(0), _ptr(out), _ptr(scratch),
+            scratch.numel(), _stream(table),
         )
     )
     return out

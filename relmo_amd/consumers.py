@@ -275,8 +275,8 @@ class CentralizedRelationalGNN(nn.Module):
             ctx.append(self.slot_mask[cond_rows])
         context = torch.cat(ctx, dim=1)
         for _ in range(self.num_layers):
-            args = mp.fanout_scatter(x, r["obj"], r["flat"], nodes * ma)
-            outputs = self.central(torch.cat([context, args.view(nodes, ma * d)], dim=1))
+            # [context | argument slots]: the fanout writes into the slots directly
+            outputs = self.central(mp.fanout_concat(context, x, r["obj"], r["flat"], ma))
             out_flat = outputs.reshape(nodes * ma, d)
             msgs = mp.fanin_reduce(out_flat, r["flat"], r["obj"], batch.num_objects, self.mode)
             if self.mode == mp.MODE_LOGSUMEXP:

@@ -592,6 +592,44 @@ int relm_mp_plan_gather_last(int dtype, const relm_mp_plan* plan, const int64_t*
                                static_cast<hipStream_t>(stream));
 }
 
+// Checks of a grouped row layout over `rows` rows of emb columns.
+static int check_grouped(int64_t rows, int64_t emb, int64_t group, int64_t group_stride) {
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    if (group < 1 || group > RELM_MP_MAX_ROWS)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: group must be >= 1");
+    if (group_stride < group * emb)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: group_stride must be at least group * emb");
+    if (rows % group != 0)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: grouped rows must be a multiple of group");
+    return RELM_MP_OK;
+}
+
+int relm_mp_plan_gather_last_grouped(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
+                                     const void* table, int64_t emb, int64_t group,
+                                     int64_t group_stride, void* out, relm_mp_stream_t stream) {
+    RELM_TRY(check_dtype(dtype));
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    RELM_TRY(check_grouped(plan->num_keys, emb, group, group_stride));
+    return compute_gather_last_grouped(dtype, *plan, gathers, table, emb, group, group_stride, out,
+                                       static_cast<hipStream_t>(stream));
+}
+
+int relm_mp_plan_segment_sum_grouped(int dtype, const relm_mp_plan* plan, const void* table,
+                                     int64_t table_rows, int64_t emb, int64_t group,
+                                     int64_t group_stride, void* out, void* scratch,
+                                     size_t scratch_bytes, relm_mp_stream_t stream) {
+    RELM_TRY(check_dtype(dtype));
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    RELM_TRY(check_grouped(table_rows, emb, group, group_stride));
+    if (plan->num_gather > table_rows)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: the plan gathers beyond table_rows");
+    return compute_segment_sum_grouped(dtype, *plan, table, emb, group, group_stride, out, scratch,
+                                       scratch_bytes, static_cast<hipStream_t>(stream));
+}
+
 int relm_mp_plan_segment_reduce(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
                                 const void* table, int64_t emb, int64_t mode, void* out,
                                 void* scratch, size_t scratch_bytes, relm_mp_stream_t stream) {

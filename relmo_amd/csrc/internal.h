@@ -127,6 +127,13 @@ hipError_t launch_index_match(const int64_t* keys, const int64_t* gathers, int64
 // ---- compute kernels (reduce_kernels.hip) --------------------------------
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
                         const void* table, int64_t emb, void* out, hipStream_t s);
+// Rows in groups (relm_mp.h): the output of the gather, the table of the sum.
+int compute_gather_last_grouped(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
+                                const void* table, int64_t emb, int64_t group,
+                                int64_t group_stride, void* out, hipStream_t s);
+int compute_segment_sum_grouped(int dtype, const relm_mp_plan& plan, const void* table,
+                                int64_t emb, int64_t group, int64_t group_stride, void* out,
+                                void* scratch, size_t scratch_bytes, hipStream_t s);
 int compute_segment_reduce(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
                            const void* table, int64_t emb, int64_t mode, void* out,
                            void* scratch, size_t scratch_bytes, hipStream_t s);

@@ -53,6 +53,28 @@ __device__ __forceinline__ uint64_t row_offset(int64_t row, int64_t D) {
            static_cast<uint64_t>(static_cast<uint32_t>(D));
 }
 
+// Row layouts of a table or an output.  DenseRows: row r at r * D.
+// GroupedRows: rows in groups of `group` consecutive rows per line of a wider
+// matrix, row r at (r / group) * stride + (r % group) * D - the argument
+// columns of a [nodes, width] input matrix with `group` slots per node
+// (stride = width, the base pointer at the first argument column).
+struct DenseRows {
+    __device__ __forceinline__ uint64_t operator()(int64_t row, int64_t D) const {
+        return row_offset(row, D);
+    }
+};
+
+struct GroupedRows {
+    uint32_t group;
+    uint64_t stride;
+    __device__ __forceinline__ uint64_t operator()(int64_t row, int64_t D) const {
+        const uint32_t r = static_cast<uint32_t>(row);
+        const uint32_t q = r / group;
+        return static_cast<uint64_t>(q) * stride +
+               static_cast<uint64_t>(r - q * group) * static_cast<uint32_t>(D);
+    }
+};
+
 template <typename T, int V>
 __device__ __forceinline__ void pack_add(Pack<T, V>& a, const Pack<T, V>& b) {
 #pragma unroll
@@ -131,7 +153,7 @@ struct LsePartial {
 // ---- ops: what is accumulated per message ----------------------------------
 
 // Sum of table rows.
-template <typename T, int V, int U>
+template <typename T, int V, int U, class Rows = DenseRows>
 struct SumOp {
     using Partial = SumPartial<T, V>;
     const T* __restrict__ table;
@@ -140,6 +162,7 @@ struct SumOp {
     bool colok;
     Pack<T, V> x[U];
     Pack<T, V> acc;
+    Rows rows;  // layout of the table rows
 
     __device__ __forceinline__ void begin(int64_t, bool) { acc = pack_fill<T, V>(T(0)); }
     // Starts a new segment when `head` (branch-free).
@@ -150,7 +173,7 @@ struct SumOp {
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + row_offset(idx[u], D) + col)
+            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + rows(idx[u], D) + col)
                                       : pack_fill<T, V>(T(0));
     }
     __device__ __forceinline__ void consume(int cnt) {
@@ -740,7 +763,7 @@ __device__ __forceinline__ const int32_t* inverse_map(const int32_t* inv,
     return pc != nullptr && pc->identity != 0 ? nullptr : inv;
 }
 
-template <typename T, int V, int G>
+template <typename T, int V, int G, class Rows>
 __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restrict__ inv_in,
                                                          const relm_mp_plan_counts* __restrict__ pc,
                                                          int64_t num_edges,
@@ -748,7 +771,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
                                                          int64_t num_gather,
                                                          const T* __restrict__ table,
                                                          int64_t num_keys, int64_t D,
-                                                         T* __restrict__ out) {
+                                                         T* __restrict__ out, Rows out_rows) {
     constexpr int R = kThreads / G;
     constexpr int RU = kRowsInFlight;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
@@ -774,7 +797,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
             const int64_t key = key0 + j * ngroups;
-            if (key < num_keys) pack_store_stream<T, V>(out + key * D + col, v[j]);
+            if (key < num_keys) pack_store_stream<T, V>(out + out_rows(key, D) + col, v[j]);
         }
     }
 }
@@ -835,13 +858,13 @@ __global__ __launch_bounds__(kThreads) void k_rows_scale(
 }
 
 // out[k] = table[gather of the last edge of segment k] or 0 (CSR plans).
-template <typename T, int V, int G>
+template <typename T, int V, int G, class Rows>
 __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __restrict__ offsets,
                                                               const int32_t* __restrict__ gs,
                                                               int64_t num_edges,
                                                               const T* __restrict__ table,
                                                               int64_t num_keys, int64_t D,
-                                                              T* __restrict__ out) {
+                                                              T* __restrict__ out, Rows out_rows) {
     constexpr int R = kThreads / G;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
@@ -852,7 +875,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __r
         const int64_t e = clamp64(offsets[key + 1], b, num_edges);
         Pack<T, V> v = pack_fill<T, V>(T(0));
         if (e > b) v = pack_load<T, V>(table + row_offset(gs[e - 1], D) + col);
-        pack_store_stream<T, V>(out + key * D + col, v);
+        pack_store_stream<T, V>(out + out_rows(key, D) + col, v);
     }
 }
 
@@ -916,11 +939,13 @@ struct Geometry {
     int64_t slices;
 };
 
+// `stride` (elements; 0 if none) is the line stride of a grouped row layout,
+// which must keep every row start as aligned as the base pointers.
 template <typename T>
-Geometry choose_geometry(int64_t D, std::initializer_list<const void*> ptrs) {
+Geometry choose_geometry(int64_t D, std::initializer_list<const void*> ptrs, int64_t stride = 0) {
     constexpr int kVecMax = 16 / static_cast<int>(sizeof(T));
     int V = kVecMax;
-    if (D % V != 0) V = 1;
+    if (D % V != 0 || stride % V != 0) V = 1;
     for (const void* p : ptrs) {
         if (p != nullptr && reinterpret_cast<uintptr_t>(p) % (sizeof(T) * V) != 0) V = 1;
     }
@@ -1041,26 +1066,56 @@ int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, 
     return hip_error(hipGetLastError(), "relm_mp hub combine kernel");
 }
 
+// group > 0: the output rows are grouped (GroupedRows{group, group_stride}).
 template <typename T>
 int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* table_v,
-                  int64_t emb, void* out_v, hipStream_t s) {
+                  int64_t emb, void* out_v, int64_t group, int64_t group_stride, hipStream_t s) {
     const T* table = static_cast<const T*>(table_v);
     T* out = static_cast<T*>(out_v);
-    const Geometry geo = choose_geometry<T>(emb, {table, out});
+    const Geometry geo = choose_geometry<T>(emb, {table, out}, group > 0 ? group_stride : 0);
     return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
         constexpr int V = decltype(vt)::value;
         constexpr int G = decltype(gt)::value;
-        if (plan.kind == RELM_MP_PLAN_INVERSE) {
-            hipLaunchKernelGGL((k_gather_inv<T, V, G>),
-                               row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
-                               dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
-                               gathers, plan.num_gather, table, plan.num_keys, emb, out);
-        } else {
-            hipLaunchKernelGGL((k_gather_last_csr<T, V, G>), row_grid(plan.num_keys, G, geo.slices),
-                               dim3(kThreads), 0, s, plan.offsets, plan.gather_sorted,
-                               plan.num_edges, table, plan.num_keys, emb, out);
-        }
+        auto launch = [&](auto rows) {
+            using Rows = decltype(rows);
+            if (plan.kind == RELM_MP_PLAN_INVERSE) {
+                hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows>),
+                                   row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
+                                   dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
+                                   gathers, plan.num_gather, table, plan.num_keys, emb, out, rows);
+            } else {
+                hipLaunchKernelGGL((k_gather_last_csr<T, V, G, Rows>),
+                                   row_grid(plan.num_keys, G, geo.slices), dim3(kThreads), 0, s,
+                                   plan.offsets, plan.gather_sorted, plan.num_edges, table,
+                                   plan.num_keys, emb, out, rows);
+            }
+        };
+        if (group > 0)
+            launch(GroupedRows{static_cast<uint32_t>(group), static_cast<uint64_t>(group_stride)});
+        else
+            launch(DenseRows{});
         return hip_error(hipGetLastError(), "relm_mp gather kernel");
+    });
+}
+
+// Sum over each key's segment of table rows in a grouped layout.
+template <typename T>
+int segment_sum_grouped_t(const relm_mp_plan& plan, const void* table_v, int64_t emb,
+                          int64_t group, int64_t group_stride, void* out_v, void* scratch,
+                          hipStream_t s) {
+    const T* table = static_cast<const T*>(table_v);
+    T* out = static_cast<T*>(out_v);
+    T* partial = static_cast<T*>(scratch);
+    const Geometry geo = choose_geometry<T>(emb, {table, out, partial}, group_stride);
+    return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
+        constexpr int V = decltype(vt)::value;
+        constexpr int G = decltype(gt)::value;
+        constexpr int U = batch_rows<G>();
+        SumOp<T, V, U, GroupedRows> op{};
+        op.table = table;
+        op.D = emb;
+        op.rows = GroupedRows{static_cast<uint32_t>(group), static_cast<uint64_t>(group_stride)};
+        return run_csr<T, V, G>(plan, op, geo.slices, partial, out, s);
     });
 }
 
@@ -1214,11 +1269,31 @@ int compute_rows_scale(int dtype, const void* in, const int64_t* gather, int div
 
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
                         const void* table, int64_t emb, void* out, hipStream_t s) {
+    return compute_gather_last_grouped(dtype, plan, gathers, table, emb, 0, 0, out, s);
+}
+
+int compute_gather_last_grouped(int dtype, const relm_mp_plan& plan, const int64_t* gathers,
+                                const void* table, int64_t emb, int64_t group,
+                                int64_t group_stride, void* out, hipStream_t s) {
     if (plan.num_keys == 0 || emb == 0) return RELM_MP_OK;
     if (plan.kind == RELM_MP_PLAN_INVERSE && gathers == nullptr)
         return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: inverse plans need the gather array");
-    return dtype == RELM_MP_F64 ? gather_last_t<double>(plan, gathers, table, emb, out, s)
-                                : gather_last_t<float>(plan, gathers, table, emb, out, s);
+    return dtype == RELM_MP_F64
+               ? gather_last_t<double>(plan, gathers, table, emb, out, group, group_stride, s)
+               : gather_last_t<float>(plan, gathers, table, emb, out, group, group_stride, s);
+}
+
+int compute_segment_sum_grouped(int dtype, const relm_mp_plan& plan, const void* table,
+                                int64_t emb, int64_t group, int64_t group_stride, void* out,
+                                void* scratch, size_t scratch_bytes, hipStream_t s) {
+    if (plan.num_keys == 0 || emb == 0) return RELM_MP_OK;
+    if (plan.kind != RELM_MP_PLAN_CSR)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: grouped sums need a CSR plan");
+    if (scratch_bytes < hub_partial_bytes(plan, emb, dtype, RELM_MP_MODE_SUM))
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: hub scratch too small");
+    return dtype == RELM_MP_F64
+               ? segment_sum_grouped_t<double>(plan, table, emb, group, group_stride, out, scratch, s)
+               : segment_sum_grouped_t<float>(plan, table, emb, group, group_stride, out, scratch, s);
 }
 
 int compute_segment_reduce(int dtype, const relm_mp_plan& plan, const int64_t* gathers,

@@ -472,6 +472,71 @@ Tensor fanout_scatter_backward_gpu(const Tensor& grad_out, const Tensor& src, co
     return grad_x;
 }
 
+// Fanout rows written into / read from `slots` argument slots of emb columns
+// per line of a wider matrix (relm_mp.h, grouped row layout): line n, slot s
+// holds fanout row n * slots + s at columns [col_offset + s * emb, + emb).
+// `mat` has unit column stride and non-overlapping lines.
+bool grouped_gpu_ok(const Tensor& mat) {
+    return mat.stride(1) == 1 && (mat.size(0) <= 1 || mat.stride(0) >= mat.size(1));
+}
+
+int64_t line_stride(const Tensor& mat) { return mat.size(0) <= 1 ? mat.size(1) : mat.stride(0); }
+
+void fanout_scatter_into_gpu(const Tensor& x_cat, const Tensor& src, const Tensor& dst,
+                             const Tensor& out, int64_t col_offset, int64_t slots) {
+    c10::OptionalDeviceGuard guard(x_cat.device());
+    check_same_gpu(x_cat, src, "x_cat", "src_global_idx");
+    check_same_gpu(x_cat, dst, "x_cat", "flat_dst");
+    check_same_gpu(x_cat, out, "x_cat", "out");
+    const int64_t emb = x_cat.size(1);
+    const int64_t out_rows = out.size(0) * slots;
+    const Tensor x = contiguous(x_cat);
+    const Tensor s_idx = contiguous(src);
+    const Tensor d_idx = contiguous(dst);
+    hipStream_t stream = current_stream(x);
+    char* base = static_cast<char*>(out.data_ptr()) + col_offset * out.element_size();
+    const int64_t stride = line_stride(out);
+    PlanCache& cache = PlanCache::get();
+    GpuPlan gp;
+    if (cache.lookup(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), &gp.plan, stream)) {
+        raise_if(relm_mp_plan_gather_last_grouped(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
+                                                  x.data_ptr(), emb, slots, stride, base, stream));
+        return;
+    }
+    gp.mem = byte_buffer(relm_mp_inv_plan_bytes(out_rows), d_idx);
+    raise_if(relm_mp_inv_plan_build_async(d_idx.data_ptr<int64_t>(), out_rows, "flat_dst",
+                                          s_idx.data_ptr<int64_t>(), x.size(0), "src_global_idx", 1,
+                                          d_idx.numel(), gp.mem.data_ptr(),
+                                          static_cast<size_t>(gp.mem.numel()), &gp.plan, stream));
+    const int rc = relm_mp_plan_gather_last_grouped(dtype_code(x), &gp.plan,
+                                                    s_idx.data_ptr<int64_t>(), x.data_ptr(), emb,
+                                                    slots, stride, base, stream);
+    raise_if(relm_mp_plan_validate(&gp.plan));
+    raise_if(rc);
+    cache.insert(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), gp.mem, gp.plan);
+}
+
+Tensor fanout_scatter_backward_from_gpu(const Tensor& grad, const Tensor& src, const Tensor& dst,
+                                        int64_t x_rows, int64_t col_offset, int64_t slots,
+                                        int64_t emb) {
+    c10::OptionalDeviceGuard guard(grad.device());
+    check_same_gpu(grad, src, "grad", "src_global_idx");
+    check_same_gpu(grad, dst, "grad", "flat_dst");
+    const Tensor g = grouped_gpu_ok(grad) ? grad : grad.contiguous();
+    const Tensor s_idx = contiguous(src);
+    const Tensor d_idx = contiguous(dst);
+    const int64_t rows = g.size(0) * slots;
+    hipStream_t stream = current_stream(g);
+    GpuPlan gp = csr_plan(s_idx, x_rows, "src_global_idx", d_idx, rows, "flat_dst", false, stream);
+    Tensor grad_x = at::empty({x_rows, emb}, grad.options());
+    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(g), kModeSum, g);
+    const char* base = static_cast<const char*>(g.data_ptr()) + col_offset * g.element_size();
+    raise_if(relm_mp_plan_segment_sum_grouped(dtype_code(g), &gp.plan, base, rows, emb, slots,
+                                              line_stride(g), grad_x.data_ptr(), scratch.data_ptr(),
+                                              static_cast<size_t>(scratch.numel()), stream));
+    return grad_x;
+}
+
 Tensor fanin_reduce_gpu(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
                         int64_t dim_size, int64_t mode) {
     c10::OptionalDeviceGuard guard(rel_flat.device());
@@ -716,6 +781,64 @@ Tensor fanout_scatter_backward(const Tensor& grad_out, const Tensor& src_global_
     }
     grad_x.index_add_(0, src_global_idx, grad_out.index_select(0, flat_dst));
     return grad_x;
+}
+
+// No counterpart in the reference: fanout_scatter written straight into the
+// argument columns of the central input matrix, and its backward reading the
+// gradient from there (fused.py:299-375 fans out into args_flat
+// [nodes * max_arity, emb], reshapes it and copies it into all_inputs).
+// out[n, col_offset + s * emb + c] = fanout_scatter(x_cat, src_global_idx,
+// flat_dst, out.size(0) * slots)[n * slots + s, c]; the other columns of out
+// keep their values.
+void check_slot_columns(int64_t width, int64_t col_offset, int64_t slots, int64_t emb) {
+    TORCH_CHECK(slots >= 1, "slots must be >= 1.");
+    TORCH_CHECK(col_offset >= 0, "col_offset must be >= 0.");
+    TORCH_CHECK(emb >= 0, "emb must be >= 0.");
+    TORCH_CHECK(col_offset + slots * emb <= width,
+                "the argument slots [col_offset, col_offset + slots * emb) exceed the ", width,
+                " columns.");
+}
+
+void fanout_scatter_into(const Tensor& x_cat, const Tensor& src_global_idx, const Tensor& flat_dst,
+                         const Tensor& out, int64_t col_offset, int64_t slots) {
+    check_rank(x_cat, 2, "x_cat");
+    check_rank(out, 2, "out");
+    check_int64_index(src_global_idx, "src_global_idx");
+    check_int64_index(flat_dst, "flat_dst");
+    TORCH_CHECK(src_global_idx.size(0) == flat_dst.size(0),
+                "src_global_idx and flat_dst must have equal length.");
+    const int64_t emb = x_cat.size(1);
+    check_slot_columns(out.size(1), col_offset, slots, emb);
+    TORCH_CHECK(out.scalar_type() == x_cat.scalar_type(), "out must have the dtype of x_cat.");
+    TORCH_CHECK(out.device() == x_cat.device(), "out must be on the device of x_cat.");
+    const int64_t rows = out.size(0) * slots;
+    if (rows == 0 || emb == 0) return;
+    if (src_global_idx.numel() > 0 && all_gpu({&x_cat, &src_global_idx, &flat_dst}) &&
+        is_fastpath_dtype(x_cat.scalar_type()) && grouped_gpu_ok(out)) {
+        fanout_scatter_into_gpu(x_cat, src_global_idx, flat_dst, out, col_offset, slots);
+        return;
+    }
+    const Tensor res = fanout_scatter(x_cat, src_global_idx, flat_dst, rows);
+    out.narrow(1, col_offset, slots * emb).copy_(res.view({out.size(0), slots * emb}));
+}
+
+Tensor fanout_scatter_backward_from(const Tensor& grad, const Tensor& src_global_idx,
+                                    const Tensor& flat_dst, int64_t x_rows, int64_t col_offset,
+                                    int64_t slots, int64_t emb) {
+    check_rank(grad, 2, "grad");
+    check_int64_index(src_global_idx, "src_global_idx");
+    check_int64_index(flat_dst, "flat_dst");
+    TORCH_CHECK(src_global_idx.size(0) == flat_dst.size(0),
+                "src_global_idx and flat_dst must have equal length.");
+    TORCH_CHECK(x_rows >= 0, "x_rows must be >= 0.");
+    check_slot_columns(grad.size(1), col_offset, slots, emb);
+    if (src_global_idx.numel() == 0 || x_rows == 0 || emb == 0)
+        return at::zeros({x_rows, emb}, grad.options());
+    if (all_gpu({&grad, &src_global_idx, &flat_dst}) && is_fastpath_dtype(grad.scalar_type()))
+        return fanout_scatter_backward_from_gpu(grad, src_global_idx, flat_dst, x_rows, col_offset,
+                                                slots, emb);
+    const Tensor slice = grad.narrow(1, col_offset, slots * emb).reshape({grad.size(0) * slots, emb});
+    return fanout_scatter_backward(slice, src_global_idx, flat_dst, x_rows);
 }
 
 Tensor fanin_reduce_sum(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
@@ -1423,6 +1546,8 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("lgan_pool_reduce_backward(Tensor grad_relation_pair_x, Tensor grad_tn_msgs, Tensor grad_nn_msgs, Tensor slot_to_relation_instance, Tensor relation_instance_arities, Tensor rr_src, Tensor rr_dst, Tensor tn_rel, Tensor tn_ent, Tensor nn_rel, Tensor nn_ent, int relation_count, int mode) -> Tensor");
     m.def("lgan_relation_graph_step(Tensor relation_pair_x, Tensor rr_src, Tensor rr_dst, Tensor tn_rel, Tensor tn_ent, Tensor nn_rel, Tensor nn_ent, int entity_dim_size, int mode) -> (Tensor, Tensor, Tensor)");
     m.def("lgan_relation_graph_step_backward(Tensor grad_relation_pair_x, Tensor grad_tn_msgs, Tensor grad_nn_msgs, Tensor rr_src, Tensor rr_dst, Tensor tn_rel, Tensor tn_ent, Tensor nn_rel, Tensor nn_ent, int relation_count, int mode) -> Tensor");
+    m.def("fanout_scatter_into(Tensor x_cat, Tensor src_global_idx, Tensor flat_dst, Tensor(a!) out, int col_offset, int slots) -> ()");
+    m.def("fanout_scatter_backward_from(Tensor grad, Tensor src_global_idx, Tensor flat_dst, int x_rows, int col_offset, int slots, int emb) -> Tensor");
     m.def("build_info() -> str");
     // No reference counterpart: control of the index-plan cache.
     m.def("plan_cache_clear() -> ()");
@@ -1444,6 +1569,8 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("lgan_pool_reduce_backward", relm_amd::lgan_pool_reduce_backward);
     m.impl("lgan_relation_graph_step", relm_amd::lgan_relation_graph_step);
     m.impl("lgan_relation_graph_step_backward", relm_amd::lgan_relation_graph_step_backward);
+    m.impl("fanout_scatter_into", relm_amd::fanout_scatter_into);
+    m.impl("fanout_scatter_backward_from", relm_amd::fanout_scatter_backward_from);
     m.impl("build_info", relm_amd::build_info);
     m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
     m.impl("plan_cache_size", relm_amd::plan_cache_size);

@@ -16,12 +16,13 @@ from __future__ import annotations
 from .mp_autograd import (
     _FaninReduceLogSumExpFunction,
     _FaninReduceSumFunction,
+    _FanoutConcatFunction,
     _FanoutScatterFunction,
     _LGANPoolReduceFunction,
     _LGANRelationGraphStepFunction,
 )
 from .mp_constants import MODE_LOGSUMEXP, MODE_MEAN, MODE_SUM, activation_code
-from .mp_dispatch import dispatch_namespace_op, should_use_custom
+from .mp_dispatch import dispatch_namespace_op, should_use_custom, use_custom_namespace_op
 from .mp_pack import (
     fanin_pack_from_edges_python,
     fanin_pack_multi_python,
@@ -45,6 +46,32 @@ def fanout_scatter(
     if should_use_custom("fanout_scatter"):
         return _FanoutScatterFunction.apply(x_cat, src_global_idx, flat_dst, int(out_rows))
     return fanout_scatter_python(x_cat, src_global_idx, flat_dst, int(out_rows))
+
+
+def fanout_concat(
+    prefix: torch.Tensor,
+    x_cat: torch.Tensor,
+    src_global_idx: torch.Tensor,
+    flat_dst: torch.Tensor,
+    slots: int,
+) -> torch.Tensor:
+    """``cat([prefix, fanout_scatter(x_cat, src_global_idx, flat_dst, n * slots).view(n, slots * D)], 1)``
+    with ``n = prefix.size(0)``, in one pass.
+
+    The central layer's input assembly (relmo ``models/hetero_mp/fused.py:299-375``:
+    fanout into ``args_flat``, reshape, copy into ``all_inputs`` after the context
+    columns), with the fanout rows written straight into the argument slots and
+    the backward reading them from the gradient in place.  No counterpart in
+    relmo's facade; without the ``fanout_scatter_into`` op it runs that composition.
+    """
+
+    require_torch("fanout_concat")
+    slots = int(slots)
+    if use_custom_namespace_op("fanout_scatter_into"):
+        return _FanoutConcatFunction.apply(prefix, x_cat, src_global_idx, flat_dst, slots)
+    nodes = int(prefix.size(0))
+    args = fanout_scatter(x_cat, src_global_idx, flat_dst, nodes * slots)
+    return torch.cat([prefix, args.view(nodes, slots * int(x_cat.size(1)))], dim=1)
 
 
 def fanin_reduce(
@@ -177,6 +204,7 @@ __all__ = [
     "fanin_pack_from_edges",
     "fanin_pack_multi",
     "fanin_reduce",
+    "fanout_concat",
     "fanout_pack_from_edges",
     "fanout_pack_multi",
     "fanout_scatter",

@@ -63,10 +63,39 @@ if torch is not None:
             )
             return grad_rel, None, None, None
 
+    class _FanoutConcatFunction(torch.autograd.Function):
+        """``[prefix | fanout rows in `slots` argument slots per line]`` in one
+        pass (``fanout_scatter_into``); the backward reads the argument
+        columns of the incoming gradient in place (``fanout_scatter_backward_from``)."""
+
+        @staticmethod
+        def forward(ctx, prefix, x_cat, src_global_idx, flat_dst, slots):
+            nodes, cols = int(prefix.size(0)), int(prefix.size(1))
+            emb = int(x_cat.size(1))
+            out = prefix.new_empty((nodes, cols + slots * emb))
+            out[:, :cols] = prefix
+            ops_namespace().fanout_scatter_into(x_cat, src_global_idx, flat_dst, out, cols, slots)
+            ctx.save_for_backward(src_global_idx, flat_dst)
+            ctx.shape = (int(x_cat.size(0)), cols, slots, emb)
+            return out
+
+        @staticmethod
+        def backward(ctx, grad):
+            src_global_idx, flat_dst = ctx.saved_tensors
+            x_rows, cols, slots, emb = ctx.shape
+            grad_prefix = grad[:, :cols] if ctx.needs_input_grad[0] else None
+            grad_x = None
+            if ctx.needs_input_grad[1]:
+                grad_x = ops_namespace().fanout_scatter_backward_from(
+                    grad, src_global_idx, flat_dst, x_rows, cols, slots, emb
+                )
+            return grad_prefix, grad_x, None, None, None
+
 else:  # pragma: no cover - torch missing
     _FanoutScatterFunction = None
     _FaninReduceSumFunction = None
     _FaninReduceLogSumExpFunction = None
+    _FanoutConcatFunction = None
 
 
 # ---- LGAN indexed reductions ---------------------------------------------------
@@ -158,4 +187,5 @@ if torch is not None:
 
 if torch is None:  # the facade still imports; its functions raise in require_torch first
     _FanoutScatterFunction = _FaninReduceSumFunction = _FaninReduceLogSumExpFunction = None
+    _FanoutConcatFunction = None
     _LGANPoolReduceFunction = _LGANRelationGraphStepFunction = None

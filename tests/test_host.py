@@ -307,10 +307,6 @@ def test_autograd_matches_aten_on_cpu(mp_env) -> None:
     torch.testing.assert_close(out, ref)
 
 
-if __name__ == "__main__":  # pragma: no cover
-    sys.exit(pytest.main([__file__, "-q"]))
-
-
 def test_model_consumers_cpu_lane_matches_aten(monkeypatch) -> None:
     """The C4 / C5 model structure on CPU tensors: the torch binding's CPU
     lane and the ATen (python_only) lane give the same loss."""
@@ -564,3 +560,45 @@ for call in calls:
 """
     proc = subprocess.run([sys.executable, "-c", code], cwd=str(REPO), capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr or proc.stdout
+
+
+# ---- fanout into argument slots (CPU lane) ----------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_fanout_slots_cpu_lane_matches_oracle(ops, dtype) -> None:
+    gen = torch.Generator().manual_seed(12)
+    lines, slots, d, col = 40, 3, 6, 5
+    x = torch.randn(25, d, dtype=dtype, generator=gen)
+    src = torch.randint(0, 25, (100,), generator=gen)
+    dst = torch.randint(0, lines * slots, (100,), generator=gen)
+    out = torch.randn(lines, col + slots * d + 3, dtype=dtype, generator=gen)
+    want = oracle.fanout_into_slots(x.numpy(), src.numpy(), dst.numpy(), out.numpy(), col, slots)
+    ops.fanout_scatter_into(x, src, dst, out, col, slots)
+    assert np.array_equal(out.numpy(), want)
+    grad = torch.randn(lines, col + slots * d + 3, dtype=dtype, generator=gen)
+    got = ops.fanout_scatter_backward_from(grad, src, dst, 25, col, slots, d)
+    want = oracle.fanout_backward_from_slots(grad.numpy(), src.numpy(), dst.numpy(), 25, col, slots, d)
+    assert np.array_equal(got.numpy(), want)
+    with pytest.raises(RuntimeError, match="exceed the"):
+        ops.fanout_scatter_into(x, src, dst, out, col + 4, slots)
+    with pytest.raises(RuntimeError, match="flat_dst index out of bounds"):
+        ops.fanout_scatter_into(x, src, dst, out[:10], col, slots)
+
+
+def test_fanout_concat_autograd_on_cpu(mp_env) -> None:
+    from relmo_amd import mp
+
+    gen = torch.Generator().manual_seed(13)
+    prefix = torch.randn(9, 4, dtype=torch.float64, generator=gen, requires_grad=True)
+    x = torch.randn(7, 3, dtype=torch.float64, generator=gen, requires_grad=True)
+    src = torch.randint(0, 7, (14,), generator=gen)
+    dst = torch.randperm(9 * 2, generator=gen)[:14]
+    got = mp.fanout_concat(prefix, x, src, dst, 2)
+    want = torch.cat([prefix, mp.fanout_scatter(x, src, dst, 18).view(9, 6)], dim=1)
+    assert torch.equal(got, want)
+    assert torch.autograd.gradcheck(lambda p, t: mp.fanout_concat(p, t, src, dst, 2), (prefix, x))
+
+
+if __name__ == "__main__":  # pragma: no cover
+    sys.exit(pytest.main([__file__, "-q"]))

@@ -103,6 +103,36 @@ def test_sums_match_float64_truth_and_conserve_mass() -> None:
     assert abs(lhs - rhs) < 1e-9 * max(1.0, abs(lhs))
 
 
+def test_slot_oracle_matches_elementwise_loop_and_is_adjoint() -> None:
+    """fanout_into_slots against a loop over edges and elements (line
+    flat_dst // slots, column col + (flat_dst % slots) * D + c, last edge
+    wins), and fanout_backward_from_slots as its adjoint over the slot
+    columns."""
+
+    rng = np.random.default_rng(11)
+    lines, slots, d, col, width = 23, 3, 5, 4, 4 + 3 * 5 + 2
+    x = rng.standard_normal((17, d))
+    src = rng.integers(0, 17, 90)
+    dst = rng.integers(0, lines * slots, 90)  # duplicates and empty slots
+    out = rng.standard_normal((lines, width))
+    want = out.copy()
+    want[:, col:col + slots * d] = 0.0
+    for e in range(src.size):
+        line, slot = divmod(int(dst[e]), slots)
+        for c in range(d):
+            want[line, col + slot * d + c] = x[src[e], c]
+    got = oracle.fanout_into_slots(x, src, dst, out, col, slots)
+    assert np.array_equal(got, want)
+    # adjoint over the slot columns (edges with distinct destinations)
+    dst1 = rng.permutation(lines * slots)[:40]
+    src1 = rng.integers(0, 17, 40)
+    g = rng.standard_normal((lines, width))
+    fwd = oracle.fanout_into_slots(x, src1, dst1, np.zeros((lines, width)), col, slots)
+    lhs = np.sum(fwd * g)
+    rhs = np.sum(x * oracle.fanout_backward_from_slots(g, src1, dst1, 17, col, slots, d))
+    assert abs(lhs - rhs) < 1e-10 * max(1.0, abs(lhs))
+
+
 def test_sum_backward_is_adjoint_of_sum() -> None:
     rng = np.random.default_rng(3)
     rel = rng.standard_normal((60, 4))
