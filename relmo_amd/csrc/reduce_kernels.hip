@@ -939,13 +939,11 @@ struct Geometry {
     int64_t slices;
 };
 
-// `stride` (elements; 0 if none) is the line stride of a grouped row layout,
-// which must keep every row start as aligned as the base pointers.
 template <typename T>
-Geometry choose_geometry(int64_t D, std::initializer_list<const void*> ptrs, int64_t stride = 0) {
+Geometry choose_geometry(int64_t D, std::initializer_list<const void*> ptrs) {
     constexpr int kVecMax = 16 / static_cast<int>(sizeof(T));
     int V = kVecMax;
-    if (D % V != 0 || stride % V != 0) V = 1;
+    if (D % V != 0) V = 1;
     for (const void* p : ptrs) {
         if (p != nullptr && reinterpret_cast<uintptr_t>(p) % (sizeof(T) * V) != 0) V = 1;
     }
@@ -971,6 +969,46 @@ int with_geometry(const Geometry& geo, F&& f) {
     };
     constexpr int kVecMax = 16 / static_cast<int>(sizeof(T));
     if (geo.V == kVecMax) return by_g(std::integral_constant<int, kVecMax>{});
+    return by_g(std::integral_constant<int, 1>{});
+}
+
+// Grouped row layouts (argument slots of a wider matrix): the widest of
+// kVecMax, kVecMax / 2 and 1 elements per lane that keeps every row start
+// aligned - lines of an odd number of 8-byte pairs still move 8 bytes per lane.
+template <typename T>
+Geometry choose_grouped_geometry(int64_t D, int64_t stride, std::initializer_list<const void*> ptrs) {
+    constexpr int kVecMax = 16 / static_cast<int>(sizeof(T));
+    int V = kVecMax;
+    for (; V > 1; V /= 2) {
+        bool ok = D % V == 0 && stride % V == 0;
+        for (const void* p : ptrs)
+            ok = ok && (p == nullptr || reinterpret_cast<uintptr_t>(p) % (sizeof(T) * V) == 0);
+        if (ok) break;
+    }
+    const int64_t vcols = (D + V - 1) / V;
+    int G = 4;
+    while (G < vcols && G < 64) G *= 2;
+    return {V, G, (vcols + G - 1) / G};
+}
+
+template <typename T, typename F>
+int with_grouped_geometry(const Geometry& geo, F&& f) {
+    constexpr int kVecMax = 16 / static_cast<int>(sizeof(T));
+    auto by_g = [&](auto vt) -> int {
+        switch (geo.G) {
+            case 4: return f(vt, std::integral_constant<int, 4>{});
+            case 8: return f(vt, std::integral_constant<int, 8>{});
+            case 16: return f(vt, std::integral_constant<int, 16>{});
+            case 32: return f(vt, std::integral_constant<int, 32>{});
+            case 64: return f(vt, std::integral_constant<int, 64>{});
+            default: break;
+        }
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: unsupported row geometry");
+    };
+    if (geo.V == kVecMax) return by_g(std::integral_constant<int, kVecMax>{});
+    if constexpr (kVecMax > 2) {
+        if (geo.V == kVecMax / 2) return by_g(std::integral_constant<int, kVecMax / 2>{});
+    }
     return by_g(std::integral_constant<int, 1>{});
 }
 
@@ -1072,30 +1110,32 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
                   int64_t emb, void* out_v, int64_t group, int64_t group_stride, hipStream_t s) {
     const T* table = static_cast<const T*>(table_v);
     T* out = static_cast<T*>(out_v);
-    const Geometry geo = choose_geometry<T>(emb, {table, out}, group > 0 ? group_stride : 0);
-    return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
+    auto launch = [&](auto vt, auto gt, const Geometry& geo, auto rows) -> int {
         constexpr int V = decltype(vt)::value;
         constexpr int G = decltype(gt)::value;
-        auto launch = [&](auto rows) {
-            using Rows = decltype(rows);
-            if (plan.kind == RELM_MP_PLAN_INVERSE) {
-                hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows>),
-                                   row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
-                                   dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
-                                   gathers, plan.num_gather, table, plan.num_keys, emb, out, rows);
-            } else {
-                hipLaunchKernelGGL((k_gather_last_csr<T, V, G, Rows>),
-                                   row_grid(plan.num_keys, G, geo.slices), dim3(kThreads), 0, s,
-                                   plan.offsets, plan.gather_sorted, plan.num_edges, table,
-                                   plan.num_keys, emb, out, rows);
-            }
-        };
-        if (group > 0)
-            launch(GroupedRows{static_cast<uint32_t>(group), static_cast<uint64_t>(group_stride)});
-        else
-            launch(DenseRows{});
+        using Rows = decltype(rows);
+        if (plan.kind == RELM_MP_PLAN_INVERSE) {
+            hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows>),
+                               row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
+                               dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
+                               gathers, plan.num_gather, table, plan.num_keys, emb, out, rows);
+        } else {
+            hipLaunchKernelGGL((k_gather_last_csr<T, V, G, Rows>),
+                               row_grid(plan.num_keys, G, geo.slices), dim3(kThreads), 0, s,
+                               plan.offsets, plan.gather_sorted, plan.num_edges, table,
+                               plan.num_keys, emb, out, rows);
+        }
         return hip_error(hipGetLastError(), "relm_mp gather kernel");
-    });
+    };
+    if (group > 0) {
+        const Geometry geo = choose_grouped_geometry<T>(emb, group_stride, {table, out});
+        const GroupedRows rows{static_cast<uint32_t>(group), static_cast<uint64_t>(group_stride)};
+        return with_grouped_geometry<T>(
+            geo, [&](auto vt, auto gt) -> int { return launch(vt, gt, geo, rows); });
+    }
+    const Geometry geo = choose_geometry<T>(emb, {table, out});
+    return with_geometry<T>(geo,
+                            [&](auto vt, auto gt) -> int { return launch(vt, gt, geo, DenseRows{}); });
 }
 
 // Sum over each key's segment of table rows in a grouped layout.
@@ -1106,8 +1146,8 @@ int segment_sum_grouped_t(const relm_mp_plan& plan, const void* table_v, int64_t
     const T* table = static_cast<const T*>(table_v);
     T* out = static_cast<T*>(out_v);
     T* partial = static_cast<T*>(scratch);
-    const Geometry geo = choose_geometry<T>(emb, {table, out, partial}, group_stride);
-    return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
+    const Geometry geo = choose_grouped_geometry<T>(emb, group_stride, {table, out, partial});
+    return with_grouped_geometry<T>(geo, [&](auto vt, auto gt) -> int {
         constexpr int V = decltype(vt)::value;
         constexpr int G = decltype(gt)::value;
         constexpr int U = batch_rows<G>();

@@ -57,10 +57,11 @@ def _case(seed: int, lines: int, slots: int, d: int, x_rows: int, n: int, dtype=
     return x, src, dst
 
 
-# (lines, slots, D, col_offset, extra columns): 16-byte aligned rows (vector
-# path) and unaligned ones (scalar path: odd offsets or strides)
+# (lines, slots, D, col_offset, extra columns): 16-byte aligned rows, 8-byte
+# aligned ones (the C5 layout: 14 context columns, 3 slots of 128) and
+# unaligned ones (odd offsets or strides: 4 bytes per lane)
 LAYOUTS = [(1000, 3, 32, 12, 4), (777, 2, 64, 11, 3), (500, 1, 128, 0, 0), (3000, 3, 20, 7, 1),
-           (64, 4, 5, 3, 2)]
+           (64, 4, 5, 3, 2), (2000, 3, 128, 14, 0), (1500, 2, 32, 6, 2)]
 
 
 @pytest.mark.parametrize("lines,slots,d,col,extra", LAYOUTS)
