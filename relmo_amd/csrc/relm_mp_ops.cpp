@@ -816,6 +816,9 @@ void fanout_scatter_into(const Tensor& x_cat, const Tensor& src_global_idx, cons
     if (src_global_idx.numel() > 0 && all_gpu({&x_cat, &src_global_idx, &flat_dst}) &&
         is_fastpath_dtype(x_cat.scalar_type()) && grouped_gpu_ok(out)) {
         fanout_scatter_into_gpu(x_cat, src_global_idx, flat_dst, out, col_offset, slots);
+        // written through its pointer: count it as an in-place change, as
+        // the ATen path's copy_ does
+        out.unsafeGetTensorImpl()->bump_version();
         return;
     }
     const Tensor res = fanout_scatter(x_cat, src_global_idx, flat_dst, rows);

@@ -127,7 +127,9 @@ def test_torch_ops_match_composition(ops, dtype) -> None:
     xg, sg, dg = x.to(DEV), src.to(DEV), dst.to(DEV)
     big = torch.randn(lines, col + slots * d + 9, dtype=dtype, device=DEV)
     keep = big.clone()
+    version = big._version
     ops.fanout_scatter_into(xg, sg, dg, big, col, slots)
+    assert big._version > version  # an in-place change for autograd's checks
     rows = ops.fanout_scatter(xg, sg, dg, lines * slots)
     assert torch.equal(big[:, col:col + slots * d], rows.view(lines, slots * d))
     assert torch.equal(big[:, :col], keep[:, :col]) and torch.equal(big[:, col + slots * d:],

@@ -574,8 +574,10 @@ def test_fanout_slots_cpu_lane_matches_oracle(ops, dtype) -> None:
     dst = torch.randint(0, lines * slots, (100,), generator=gen)
     out = torch.randn(lines, col + slots * d + 3, dtype=dtype, generator=gen)
     want = oracle.fanout_into_slots(x.numpy(), src.numpy(), dst.numpy(), out.numpy(), col, slots)
+    version = out._version
     ops.fanout_scatter_into(x, src, dst, out, col, slots)
     assert np.array_equal(out.numpy(), want)
+    assert out._version > version
     grad = torch.randn(lines, col + slots * d + 3, dtype=dtype, generator=gen)
     got = ops.fanout_scatter_backward_from(grad, src, dst, 25, col, slots, d)
     want = oracle.fanout_backward_from_slots(grad.numpy(), src.numpy(), dst.numpy(), 25, col, slots, d)
