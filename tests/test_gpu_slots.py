@@ -187,3 +187,39 @@ def test_fanout_concat_autograd_on_gpu(mp_env) -> None:
     assert torch.equal(out.detach().cpu(), ref.detach())
     torch.testing.assert_close(p_g.grad.cpu(), p_c.grad, rtol=0, atol=0)
     torch.testing.assert_close(x_g.grad.cpu(), x_c.grad, rtol=1e-12, atol=1e-12)
+
+
+def test_grouped_entry_points_reject_bad_layouts() -> None:
+    import ctypes
+
+    from relmo_amd import capi
+
+    x = torch.randn(10, 8, device=DEV)
+    dst = torch.arange(12, device=DEV)
+    src = torch.randint(0, 10, (12,), device=DEV)
+    out = torch.zeros(4, 3 * 8, device=DEV)
+    inv = capi.inv_plan(dst, 12, src, 10)
+    lib = capi.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def gather(group, stride):
+        return lib.relm_mp_plan_gather_last_grouped(capi.F32, ctypes.byref(inv.plan), src.data_ptr(),
+                                                     x.data_ptr(), 8, group, stride, out.data_ptr(), stream)
+
+    assert gather(0, 24) == capi.ERR_INVALID_ARGUMENT and "group" in capi.last_error()
+    assert gather(3, 23) == capi.ERR_INVALID_ARGUMENT and "group_stride" in capi.last_error()
+    assert gather(5, 40) == capi.ERR_INVALID_ARGUMENT and "multiple" in capi.last_error()
+    assert gather(3, 24) == capi.OK
+    csr = capi.csr_plan(src, 10, dst, 12)
+    scratch = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    g = torch.zeros(10, 8, device=DEV)
+    rc = lib.relm_mp_plan_segment_sum_grouped(capi.F32, ctypes.byref(csr.plan), out.data_ptr(), 10, 8, 3, 24,
+                                              g.data_ptr(), scratch.data_ptr(), scratch.numel(), stream)
+    assert rc == capi.ERR_INVALID_ARGUMENT and "multiple" in capi.last_error()
+    rc = lib.relm_mp_plan_segment_sum_grouped(capi.F32, ctypes.byref(csr.plan), out.data_ptr(), 9, 8, 3, 24,
+                                              g.data_ptr(), scratch.data_ptr(), scratch.numel(), stream)
+    assert rc == capi.ERR_INVALID_ARGUMENT and "table_rows" in capi.last_error()
+    torch.cuda.synchronize()
+    want = oracle.fanout_into_slots(x.cpu().numpy(), src.cpu().numpy(), dst.cpu().numpy(),
+                                    np.zeros((4, 24), np.float32), 0, 3)
+    assert np.array_equal(out.cpu().numpy(), want)
