@@ -61,7 +61,9 @@ def _case(seed: int, lines: int, slots: int, d: int, x_rows: int, n: int, dtype=
 # aligned ones (the C5 layout: 14 context columns, 3 slots of 128) and
 # unaligned ones (odd offsets or strides: 4 bytes per lane)
 LAYOUTS = [(1000, 3, 32, 12, 4), (777, 2, 64, 11, 3), (500, 1, 128, 0, 0), (3000, 3, 20, 7, 1),
-           (64, 4, 5, 3, 2), (2000, 3, 128, 14, 0), (1500, 2, 32, 6, 2)]
+           (64, 4, 5, 3, 2), (2000, 3, 128, 14, 0), (1500, 2, 32, 6, 2),
+           # rows wider than one row group covers (two column slices)
+           (200, 2, 300, 6, 2), (150, 3, 520, 0, 0)]
 
 
 @pytest.mark.parametrize("lines,slots,d,col,extra", LAYOUTS)
@@ -83,6 +85,29 @@ def test_grouped_gather_c_abi(lines, slots, d, col, extra, kind) -> None:
         capi.plan_gather_last_grouped(bp, xg, og, col, slots)
     torch.cuda.synchronize()
     assert np.array_equal(og.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("lines,slots,d,col,extra", [(400, 3, 32, 6, 2), (300, 2, 7, 1, 0), (100, 2, 200, 4, 0)])
+def test_grouped_layouts_in_float64(lines, slots, d, col, extra) -> None:
+    from relmo_amd import capi
+
+    _log(f"grouped float64 lines={lines} slots={slots} D={d} col={col}")
+    x, src, dst = _case(lines + 3 * d, lines, slots, d, 250, lines * slots, dtype=torch.float64)
+    width = col + slots * d + extra
+    out = torch.randn(lines, width, dtype=torch.float64, generator=torch.Generator().manual_seed(4))
+    want = oracle.fanout_into_slots(x.numpy(), src.numpy(), dst.numpy(), out.numpy(), col, slots)
+    xg, sg, dg, og = x.to(DEV), src.to(DEV), dst.to(DEV), out.to(DEV)
+    bp = capi.inv_plan(dg, lines * slots, sg, 250)
+    capi.plan_gather_last_grouped(bp, xg, og, col, slots, gathers=sg)
+    csr = capi.csr_plan(sg, 250, dg, lines * slots)
+    got = capi.plan_segment_sum_grouped(csr, og, col, slots, d)
+    torch.cuda.synchronize()
+    assert np.array_equal(og.cpu().numpy(), want)
+    ref = oracle.fanout_backward_from_slots(want, src.numpy(), dst.numpy(), 250, col, slots, d)
+    counts = np.bincount(src.numpy(), minlength=250)
+    short = counts <= 64
+    assert np.array_equal(got.cpu().numpy()[short], ref[short])
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-12, atol=1e-12)
 
 
 @pytest.mark.parametrize("lines,slots,d,col,extra", LAYOUTS)
