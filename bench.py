@@ -123,12 +123,21 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
 
     # The same topology handed over in new index tensors every step (a caller
     # that rebuilds its routing per forward): the plan cache matches the
-    # contents against the cached entry's tensors instead of rebuilding.
+    # contents against the cached plan's snapshot instead of rebuilding.
     fresh = iter([(flat_src.clone(), dst.clone()) for _ in range(steps + warmup)])
 
     def step_same_topology():
         s_idx, d_idx = next(fresh)
         out = mp.fanin_reduce(rel, s_idx, d_idx, K, mode)
+        torch.autograd.grad(out, rel, grad_out)
+
+    # A new topology every step with the cache kept: every forward compares
+    # the new indices with the cached plans of the same shape (a mismatch ends
+    # the comparison after the first tiles), then builds and keeps its plan.
+    shifted = iter([(dst + i) % K for i in range(1, steps + warmup + 1)])
+
+    def step_new_topology():
+        out = mp.fanin_reduce(rel, flat_src, next(shifted), K, mode)
         torch.autograd.grad(out, rel, grad_out)
 
     sync = torch.cuda.synchronize
@@ -139,6 +148,11 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
     t_same = timed(step_same_topology, steps, warmup, sync)
     content_hits = ns.plan_cache_stats()[2] - stats0[2]
     del fresh
+    ns.plan_cache_clear()
+    stats0 = ns.plan_cache_stats()
+    t_new = timed(step_new_topology, steps, warmup, sync)
+    stats1 = ns.plan_cache_stats()
+    del shifted
     ns.plan_cache_clear()
 
     # Kernel-only timings with prebuilt plans, HIP events on the launch stream.
@@ -170,6 +184,10 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         "ms_step_same_topology_new_tensors": t_same * 1e3,
         "gbs_step_same_topology_new_tensors": gbs(b_fwd + b_bwd, t_same),
         "content_hits_same_topology": content_hits,
+        "ms_step_new_topology_cache_kept": t_new * 1e3,
+        "gbs_step_new_topology_cache_kept": gbs(b_fwd + b_bwd, t_new),
+        "misses_new_topology": stats1[3] - stats0[3],
+        "plan_cache_peak_mb": stats1[5] / 2**20,
         "ms_fwd_kernels": t_fwd * 1e3, "gbs_fwd_kernels": gbs(b_fwd, t_fwd),
         "ms_bwd_in_step": t_bwd_step * 1e3, "gbs_bwd_in_step": gbs(b_bwd, t_bwd_step),
         "ms_bwd_kernel": t_bwd * 1e3, "gbs_bwd_kernel": gbs(b_bwd, t_bwd),

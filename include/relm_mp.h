@@ -184,18 +184,35 @@ typedef struct relm_mp_plan {
                                 equal to gather_sorted when there is no hub (set so once the
                                 statistics are read: a waiting build, relm_mp_plan_read_counts) */
     const relm_mp_plan_counts* counts; /* the statistics, in device memory */
+    /* The indices the plan was built from, as validated, in edge order: int32
+     * per edge, for recognising them again (relm_mp_plan_match).  A tile of
+     * RELM_MP_SNAP_TILE edges flagged in the *_plain array holds the edge ids
+     * themselves (index[e] == e) and is not stored.  NULL where the plan keeps
+     * no snapshot (snap_keys) or has no gathers (snap_gathers); a NULL *_plain
+     * array means every tile is stored. */
+    const int32_t* snap_keys;
+    const int32_t* snap_gathers;
+    const uint32_t* snap_key_plain;
+    const uint32_t* snap_gather_plain;
 } relm_mp_plan;
+
+/* Edges per tile of a plan's index snapshot. */
+#define RELM_MP_SNAP_TILE 4096
+/* Flag of the inverse-plan builds: keep a snapshot of the indices. */
+#define RELM_MP_PLAN_SNAPSHOT 1
 
 /* Inverse plan: inv[k] = largest e with keys[e] == k, or -1 (plan->inv is
  * set to NULL when keys[e] == e for every edge: the identity).  Validates keys
  * against key_bound and gathers (if non-NULL) against gather_bound; the first
  * edge (in edge order) with a bad index is reported, `gather_checked_first`
- * choosing which array the reference checks first within one edge.
+ * choosing which array the reference checks first within one edge.  With
+ * flags & RELM_MP_PLAN_SNAPSHOT the plan also keeps a snapshot of the indices
+ * (plan memory from relm_mp_inv_plan_bytes with the same flags).
  * Synchronises `stream` once. */
-size_t relm_mp_inv_plan_bytes(int64_t num_keys);
+size_t relm_mp_inv_plan_bytes(int64_t num_keys, int64_t num_edges, int flags);
 int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
                            const int64_t* gathers, int64_t gather_bound, const char* gather_name,
-                           int gather_checked_first, int64_t num_edges, void* plan_mem,
+                           int gather_checked_first, int64_t num_edges, int flags, void* plan_mem,
                            size_t plan_bytes, relm_mp_plan* plan, relm_mp_stream_t stream);
 /* The same build without waiting: the validation result is pending until
  * relm_mp_plan_validate(plan).  Meanwhile relm_mp_plan_gather_last may be
@@ -211,7 +228,7 @@ int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* k
 int relm_mp_inv_plan_build_async(const int64_t* keys, int64_t key_bound, const char* key_name,
                                  const int64_t* gathers, int64_t gather_bound,
                                  const char* gather_name, int gather_checked_first,
-                                 int64_t num_edges, void* plan_mem, size_t plan_bytes,
+                                 int64_t num_edges, int flags, void* plan_mem, size_t plan_bytes,
                                  relm_mp_plan* plan, relm_mp_stream_t stream);
 /* Waits for the pending validation of `plan` (relm_mp_inv_plan_build_async)
  * and reports it like relm_mp_inv_plan_build; fills collisions and sets
@@ -221,7 +238,8 @@ int relm_mp_plan_validate(relm_mp_plan* plan);
 /* CSR plan: stable counting order of the edges by key (edge order kept inside
  * each segment), offsets, the gathered row of every edge in that order, and the
  * list of hub segments.  Validates like relm_mp_inv_plan_build.  Waits for
- * `stream` to finish the build and fills the statistics. */
+ * `stream` to finish the build and fills the statistics.  CSR plans always
+ * keep the snapshot of their indices (the sort's first pass writes it). */
 size_t relm_mp_csr_plan_bytes(int64_t num_keys, int64_t num_edges);
 size_t relm_mp_csr_plan_scratch_bytes(int64_t num_keys, int64_t num_edges);
 int relm_mp_csr_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
@@ -344,20 +362,23 @@ int relm_mp_plan_segment_sum_grouped(int dtype, const relm_mp_plan* plan, const 
 
 /* No counterpart in the reference (its ops build their index structures in
  * every call).  A caller that keeps plans (the torch binding's plan cache)
- * uses this to reuse a plan for new index arrays whose contents equal those a
- * plan was built from, e.g. the same topology rebuilt in every forward. */
+ * uses this to reuse a plan only for index arrays whose contents equal the
+ * snapshot the plan was built from - so a plan is never served for indices
+ * that were changed after the build, however they were changed. */
 #define RELM_MP_MAX_MATCH 8
 
-size_t relm_mp_index_match_workspace_size(void);
+size_t relm_mp_plan_match_workspace_size(void);
 
-/* match[c] = 1 if keys[0..n) == cand_keys[c][0..n) and (when gathers is not
- * NULL) gathers[0..n) == cand_gathers[c][0..n), else 0; 0 <= num_cand <=
- * RELM_MP_MAX_MATCH.  All arrays are device memory; `match` is host memory.
- * Enqueues one pass on `stream` and returns once the result is known. */
-int relm_mp_index_match(const int64_t* keys, const int64_t* gathers, int64_t n,
-                        const int64_t* const* cand_keys, const int64_t* const* cand_gathers,
-                        int32_t num_cand, int32_t* match, void* workspace, size_t workspace_bytes,
-                        relm_mp_stream_t stream);
+/* match[c] = 1 if n == plans[c]->num_edges, keys[0..n) equal the plan's key
+ * snapshot and (when gathers is not NULL) gathers[0..n) equal its gather
+ * snapshot, else 0; 0 <= num_plans <= RELM_MP_MAX_MATCH, every plan with a
+ * snapshot (and a gather snapshot when gathers is not NULL).  keys / gathers
+ * are device memory, `match` host memory.  Enqueues one pass on `stream`
+ * (the plans' builds must precede it in stream order) and returns once the
+ * result is known. */
+int relm_mp_plan_match(const int64_t* keys, const int64_t* gathers, int64_t n,
+                       const relm_mp_plan* const* plans, int32_t num_plans, int32_t* match,
+                       void* workspace, size_t workspace_bytes, relm_mp_stream_t stream);
 
 /* ---- index packing (the pack ops) -------------------------------------- */
 

@@ -27,6 +27,7 @@ F32 = 0
 F64 = 1
 PLAN_INVERSE = 1
 PLAN_CSR = 2
+PLAN_SNAPSHOT = 1  # inverse-plan build flag: keep a snapshot of the indices
 
 EXPORTED_SYMBOLS = (
     "relm_mp_last_error",
@@ -56,8 +57,8 @@ EXPORTED_SYMBOLS = (
     "relm_mp_plan_logsumexp_backward",
     "relm_mp_plan_fanin_backward_by_dst",
     "relm_mp_pack_index",
-    "relm_mp_index_match_workspace_size",
-    "relm_mp_index_match",
+    "relm_mp_plan_match_workspace_size",
+    "relm_mp_plan_match",
     "relm_mp_rows_scale",
     "relm_mp_plan_segment_sum_scaled",
     "relm_mp_plan_gather_last_grouped",
@@ -96,6 +97,10 @@ class Plan(ctypes.Structure):
         ("short_off", ctypes.c_void_p),
         ("short_gather", ctypes.c_void_p),
         ("counts", ctypes.c_void_p),
+        ("snap_keys", ctypes.c_void_p),
+        ("snap_gathers", ctypes.c_void_p),
+        ("snap_key_plain", ctypes.c_void_p),
+        ("snap_gather_plain", ctypes.c_void_p),
     ]
 
 
@@ -136,9 +141,10 @@ _SIGNATURES = {
         _int,
         [_int, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _sz, _vp],
     ),
-    "relm_mp_inv_plan_bytes": (_sz, [_i64]),
-    "relm_mp_inv_plan_build": (_int, [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _PP, _vp]),
-    "relm_mp_inv_plan_build_async": (_int, [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _vp, _sz, _PP, _vp]),
+    "relm_mp_inv_plan_bytes": (_sz, [_i64, _i64, _int]),
+    "relm_mp_inv_plan_build": (_int, [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _int, _vp, _sz, _PP, _vp]),
+    "relm_mp_inv_plan_build_async": (
+        _int, [_vp, _i64, _cp, _vp, _i64, _cp, _int, _i64, _int, _vp, _sz, _PP, _vp]),
     "relm_mp_plan_validate": (_int, [_PP]),
     "relm_mp_csr_plan_bytes": (_sz, [_i64, _i64]),
     "relm_mp_csr_plan_scratch_bytes": (_sz, [_i64, _i64]),
@@ -157,16 +163,16 @@ _SIGNATURES = {
     "relm_mp_plan_logsumexp_backward": (_int, [_int, _PP, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_fanin_backward_by_dst": (_int, [_int, _PP, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "relm_mp_pack_index": (_int, [ctypes.POINTER(IndexPart), ctypes.c_int32, _vp, _vp, _vp]),
-    "relm_mp_index_match_workspace_size": (_sz, []),
+    "relm_mp_plan_match_workspace_size": (_sz, []),
     "relm_mp_rows_scale": (_int, [_int, _vp, _vp, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "relm_mp_plan_segment_sum_scaled": (_int, [_int, _PP, _vp, _i64, _int, _vp, _vp, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_gather_last_grouped": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "relm_mp_plan_segment_sum_grouped": (
         _int, [_int, _PP, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
-    "relm_mp_index_match": (
+    "relm_mp_plan_match": (
         _int,
-        [_vp, _vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.c_int32,
-         ctypes.POINTER(ctypes.c_int32), _vp, _sz, _vp],
+        [_vp, _vp, _i64, ctypes.POINTER(_PP), ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), _vp,
+         _sz, _vp],
     ),
 }
 
@@ -384,11 +390,13 @@ class BuiltPlan:
 
 def inv_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, gather_bound: int,
              key_name: str = "key", gather_name: str = "gather", gather_first: bool = False,
-             wait: bool = True) -> BuiltPlan:
-    """Inverse plan; with wait=False the validation stays pending until validate()."""
+             wait: bool = True, snapshot: bool = False) -> BuiltPlan:
+    """Inverse plan; with wait=False the validation stays pending until validate();
+    with snapshot=True the plan keeps a snapshot of its indices (plan_match)."""
 
     _check_index(keys)
-    mem = _bytes(lib().relm_mp_inv_plan_bytes(key_bound), keys)
+    flags = PLAN_SNAPSHOT if snapshot else 0
+    mem = _bytes(lib().relm_mp_inv_plan_bytes(key_bound, keys.numel(), flags), keys)
     plan = Plan()
     build = lib().relm_mp_inv_plan_build if wait else lib().relm_mp_inv_plan_build_async
     # the names must outlive a pending validation: keep them on the plan
@@ -396,7 +404,7 @@ def inv_plan(keys: torch.Tensor, key_bound: int, gathers: torch.Tensor | None, g
     check(
         build(
             _ptr(keys), key_bound, names[0], _ptr(gathers), gather_bound,
-            names[1], int(gather_first), keys.numel(), _ptr(mem), mem.numel(),
+            names[1], int(gather_first), keys.numel(), flags, _ptr(mem), mem.numel(),
             ctypes.byref(plan), _stream(keys),
         )
     )
@@ -586,20 +594,18 @@ def pack_index(parts: list[tuple], write_b: bool = True) -> tuple[torch.Tensor, 
     return out_a, out_b
 
 
-def index_match(keys: torch.Tensor, gathers: torch.Tensor | None,
-                candidates: list[tuple[torch.Tensor, torch.Tensor | None]]) -> list[bool]:
-    """``relm_mp_index_match``: which candidate (keys, gathers) pairs equal the given pair."""
+def plan_match(keys: torch.Tensor, gathers: torch.Tensor | None, plans: list[BuiltPlan]) -> list[bool]:
+    """``relm_mp_plan_match``: which plans were built from indices equal to (keys, gathers)."""
 
     _check_index(keys)
     if gathers is not None:
         _check_index(gathers)
-    k = len(candidates)
-    ck = (_vp * max(k, 1))(*[_ptr(c[0]) for c in candidates])
-    cg = (_vp * max(k, 1))(*[_ptr(c[1]) if c[1] is not None else None for c in candidates])
+    k = len(plans)
+    arr = (_PP * max(k, 1))(*[ctypes.pointer(bp.plan) for bp in plans])
     match = (ctypes.c_int32 * max(k, 1))()
-    ws = _bytes(lib().relm_mp_index_match_workspace_size(), keys)
-    check(lib().relm_mp_index_match(_ptr(keys), _ptr(gathers), keys.numel(), ck, cg, k, match,
-                                    _ptr(ws), ws.numel(), _stream(keys)))
+    ws = _bytes(lib().relm_mp_plan_match_workspace_size(), keys)
+    check(lib().relm_mp_plan_match(_ptr(keys), _ptr(gathers), keys.numel(), arr, k, match,
+                                   _ptr(ws), ws.numel(), _stream(keys)))
     return [bool(match[i]) for i in range(k)]
 
 

@@ -147,6 +147,29 @@ class FiLMConcatMLP(nn.Module):
         return self.out(h)
 
 
+def _object_degrees(obj: Tensor, num_objects: int) -> Tensor:
+    """Messages per object (the fanin segment sizes)."""
+
+    return torch.bincount(obj, minlength=num_objects)
+
+
+def fanin_objects(mode: int, rel_flat: Tensor, r: dict, num_objects: int) -> Tensor:
+    """Aggregation of the slot messages onto the objects as the reference's
+    layers do it (fused.py:381-404, fast_fused.py:280-296): sum and logsumexp
+    through ``fanin_reduce``, mean as PyG's MeanAggregation (the sum divided by
+    max(count, 1)); objects without messages get 0, as from PyG's aggregators
+    (the op's logsumexp leaves -inf there, which is replaced - NaN and +inf
+    results of objects with messages pass through unchanged)."""
+
+    if mode == mp.MODE_MEAN:
+        total = mp.fanin_reduce(rel_flat, r["flat"], r["obj"], num_objects, mp.MODE_SUM)
+        return total / r["deg"].clamp_min(1).to(total.dtype).unsqueeze(1)
+    msgs = mp.fanin_reduce(rel_flat, r["flat"], r["obj"], num_objects, mode)
+    if mode == mp.MODE_LOGSUMEXP:
+        msgs = msgs.masked_fill((r["deg"] == 0).unsqueeze(1), 0.0)
+    return msgs
+
+
 # ---- RelationalGNN, fast fused relation layer ------------------------------------------
 
 
@@ -188,7 +211,8 @@ class RelationalGNN(nn.Module):
         flat_t = torch.cat(flat) if flat else torch.zeros(0, dtype=torch.long)
         obj_t = torch.cat(obj) if obj else torch.zeros(0, dtype=torch.long)
         # the fanin pair (flat_src, dst) is the same edge list as the fanout pair
-        return {"meta": meta, "total": total, "flat": flat_t, "obj": obj_t}
+        return {"meta": meta, "total": total, "flat": flat_t, "obj": obj_t,
+                "deg": _object_degrees(obj_t, batch.num_objects)}
 
     def forward(self, batch: RelationalBatch, routing: dict | None = None) -> Tensor:
         r = routing or self.routing(batch)
@@ -201,11 +225,7 @@ class RelationalGNN(nn.Module):
                 feat = args[off: off + n * arity].view(n, arity * self.d)
                 outs.append(self.rel_mlps[pred](feat).view(n * arity, self.d))
             rel_flat = torch.cat(outs) if len(outs) > 1 else outs[0]
-            msgs = mp.fanin_reduce(rel_flat, r["flat"], r["obj"], batch.num_objects, self.mode)
-            if self.mode == mp.MODE_LOGSUMEXP:
-                # objects without atoms receive -inf; the reference's PyG
-                # aggregators give 0 there
-                msgs = torch.where(torch.isfinite(msgs), msgs, torch.zeros_like(msgs))
+            msgs = fanin_objects(self.mode, rel_flat, r, batch.num_objects)
             x = x + self.updater(torch.cat([x, msgs], dim=1))
         return x
 
@@ -259,7 +279,9 @@ class CentralizedRelationalGNN(nn.Module):
                 flat.append(node * self.max_arity + pos)
                 obj.append(args[:, pos])
             start += n
-        return {"meta": meta, "nodes": start, "flat": torch.cat(flat), "obj": torch.cat(obj)}
+        obj_t = torch.cat(obj)
+        return {"meta": meta, "nodes": start, "flat": torch.cat(flat), "obj": obj_t,
+                "deg": _object_degrees(obj_t, batch.num_objects)}
 
     def forward(self, batch: RelationalBatch, routing: dict | None = None) -> Tensor:
         r = routing or self.routing(batch)
@@ -278,9 +300,7 @@ class CentralizedRelationalGNN(nn.Module):
             # [context | argument slots]: the fanout writes into the slots directly
             outputs = self.central(mp.fanout_concat(context, x, r["obj"], r["flat"], ma))
             out_flat = outputs.reshape(nodes * ma, d)
-            msgs = mp.fanin_reduce(out_flat, r["flat"], r["obj"], batch.num_objects, self.mode)
-            if self.mode == mp.MODE_LOGSUMEXP:
-                msgs = torch.where(torch.isfinite(msgs), msgs, torch.zeros_like(msgs))
+            msgs = fanin_objects(self.mode, out_flat, r, batch.num_objects)
             x = x + self.updater(torch.cat([x, msgs], dim=1))
         return x
 

@@ -193,15 +193,25 @@ struct InvLayout {
     DevStatus* status;
     relm_mp_plan_counts* counts;
     int32_t* inv;
+    SnapOut snap;  // all null without RELM_MP_PLAN_SNAPSHOT
     size_t bytes;
 };
 
-InvLayout inv_layout(void* mem, int64_t num_keys) {
+InvLayout inv_layout(void* mem, int64_t num_keys, int64_t num_edges, int flags) {
     Carver c(mem);
     InvLayout l;
     l.status = c.take<DevStatus>(1);
     l.counts = c.take<relm_mp_plan_counts>(1);
     l.inv = c.take<int32_t>(static_cast<size_t>(num_keys));
+    l.snap = SnapOut{nullptr, nullptr, nullptr, nullptr};
+    if (flags & RELM_MP_PLAN_SNAPSHOT) {
+        const size_t n = static_cast<size_t>(num_edges);
+        const size_t tiles = static_cast<size_t>(sort_tiles(num_edges));
+        l.snap.keys = c.take<uint32_t>(n);
+        l.snap.gathers = c.take<uint32_t>(n);
+        l.snap.key_plain = c.take<uint32_t>(tiles);
+        l.snap.gather_plain = c.take<uint32_t>(tiles);
+    }
     l.bytes = c.used();
     return l;
 }
@@ -221,6 +231,9 @@ struct CsrLayout {
     int32_t* item_short;
     int32_t* short_off;
     int32_t* short_gather;
+    uint32_t* snap_keys;   // the sort's narrowed input (edge order) is the plan's snapshot
+    uint32_t* snap_gathers;
+    uint32_t* snap_plain;  // per sort tile: gathers are the edge ids, snap_gathers not written
     int64_t num_items;
     size_t bytes;
 };
@@ -242,6 +255,9 @@ CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
     l.item_short = c.take<int32_t>(static_cast<size_t>(l.num_items) + 1);
     l.short_off = c.take<int32_t>(static_cast<size_t>(num_keys) + 1);
     l.short_gather = c.take<int32_t>(static_cast<size_t>(num_edges));
+    l.snap_keys = c.take<uint32_t>(static_cast<size_t>(num_edges));
+    l.snap_gathers = c.take<uint32_t>(static_cast<size_t>(num_edges));
+    l.snap_plain = c.take<uint32_t>(static_cast<size_t>(sort_tiles(num_edges)));
     l.bytes = c.used();
     return l;
 }
@@ -262,7 +278,7 @@ CsrScratch csr_scratch(void* mem, int64_t num_keys, int64_t num_edges) {
     l.sort.vals_b = c.take<uint32_t>(n);
     const size_t hist = sort_hist_words(num_edges);
     l.sort.hist = c.take<uint32_t>(hist);
-    l.sort.tile_plain = c.take<uint32_t>(static_cast<size_t>(sort_tiles(num_edges)));
+    l.sort.keys_n = l.sort.vals_n = l.sort.tile_plain = nullptr;  // in the plan (csr_layout)
     l.key_index = c.take<uint32_t>(key_index_words(num_keys));
     l.bytes = c.used();
     return l;
@@ -285,12 +301,14 @@ void finish_inverse(relm_mp_plan* plan, const DevStatus& host) {
 
 int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, const int64_t* gathers,
               int64_t gather_bound, const char* gather_name, int gather_checked_first,
-              int64_t num_edges, void* plan_mem, size_t plan_bytes, relm_mp_plan* plan, bool wait,
-              hipStream_t s) {
+              int64_t num_edges, int flags, void* plan_mem, size_t plan_bytes, relm_mp_plan* plan,
+              bool wait, hipStream_t s) {
     RELM_TRY(check_rows(key_bound, "num_keys"));
     RELM_TRY(check_rows(num_edges, "num_edges"));
     if (gathers != nullptr) RELM_TRY(check_rows(gather_bound, "num_gather"));
-    const InvLayout l = inv_layout(plan_mem, key_bound);
+    if (flags & ~RELM_MP_PLAN_SNAPSHOT)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: unknown inverse plan flags");
+    const InvLayout l = inv_layout(plan_mem, key_bound, num_edges, flags);
     if (plan_mem == nullptr || plan_bytes < l.bytes)
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: inverse plan memory too small");
     HostSlot* hs = nullptr;
@@ -304,9 +322,16 @@ int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->inv = l.inv;
     plan->counts = l.counts;
     plan->collisions = -1;
+    SnapOut snap = l.snap;
+    if (gathers == nullptr) snap.gathers = snap.gather_plain = nullptr;
+    plan->snap_keys = reinterpret_cast<const int32_t*>(snap.keys);
+    plan->snap_key_plain = snap.key_plain;
+    plan->snap_gathers = reinterpret_cast<const int32_t*>(snap.gathers);
+    plan->snap_gather_plain = snap.gather_plain;
     RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
     RELM_HIP(launch_fill_i32(l.inv, key_bound, -1, s), "relm_mp fill");
-    RELM_HIP(launch_inv_build(keys, key_bound, gathers, gather_bound, num_edges, l.inv, l.status, s),
+    RELM_HIP(launch_inv_build(keys, key_bound, gathers, gather_bound, num_edges, l.inv, snap,
+                              l.status, s),
              "relm_mp inverse plan kernel");
     RELM_HIP(launch_status_publish(l.status, hs->status_mapped, l.counts, s), "relm_mp status publish");
     RELM_HIP(hipEventRecord(hs->ready, s), "relm_mp status event");
@@ -354,7 +379,10 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_TRY(check_rows(num_edges, "num_edges"));
     if (gathers != nullptr) RELM_TRY(check_rows(gather_bound, "num_gather"));
     const CsrLayout l = csr_layout(plan_mem, key_bound, num_edges);
-    const CsrScratch sc = csr_scratch(scratch, key_bound, num_edges);
+    CsrScratch sc = csr_scratch(scratch, key_bound, num_edges);
+    sc.sort.keys_n = l.snap_keys;
+    sc.sort.vals_n = l.snap_gathers;
+    sc.sort.tile_plain = l.snap_plain;
     if (plan_mem == nullptr || plan_bytes < l.bytes)
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR plan memory too small");
     if (scratch == nullptr || scratch_bytes < sc.bytes)
@@ -381,6 +409,10 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->short_off = l.short_off;
     plan->short_gather = l.short_gather;
     plan->counts = l.counts;
+    plan->snap_keys = reinterpret_cast<const int32_t*>(l.snap_keys);
+    plan->snap_key_plain = nullptr;
+    plan->snap_gathers = gathers != nullptr ? reinterpret_cast<const int32_t*>(l.snap_gathers) : nullptr;
+    plan->snap_gather_plain = gathers != nullptr ? l.snap_plain : nullptr;
     plan->max_degree = plan->num_hubs = plan->num_chunks = plan->num_multi_hubs = -1;
     plan->num_items = plan->num_short = -1;
     RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
@@ -452,26 +484,28 @@ const char* relm_mp_build_info(void) {
     return info.c_str();
 }
 
-size_t relm_mp_inv_plan_bytes(int64_t num_keys) {
-    return inv_layout(nullptr, std::max<int64_t>(num_keys, 0)).bytes;
+size_t relm_mp_inv_plan_bytes(int64_t num_keys, int64_t num_edges, int flags) {
+    return inv_layout(nullptr, std::max<int64_t>(num_keys, 0), std::max<int64_t>(num_edges, 0),
+                      flags)
+        .bytes;
 }
 
 int relm_mp_inv_plan_build(const int64_t* keys, int64_t key_bound, const char* key_name,
                            const int64_t* gathers, int64_t gather_bound, const char* gather_name,
-                           int gather_checked_first, int64_t num_edges, void* plan_mem,
+                           int gather_checked_first, int64_t num_edges, int flags, void* plan_mem,
                            size_t plan_bytes, relm_mp_plan* plan, relm_mp_stream_t stream) {
     return inv_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
-                     gather_checked_first, num_edges, plan_mem, plan_bytes, plan, true,
+                     gather_checked_first, num_edges, flags, plan_mem, plan_bytes, plan, true,
                      static_cast<hipStream_t>(stream));
 }
 
 int relm_mp_inv_plan_build_async(const int64_t* keys, int64_t key_bound, const char* key_name,
                                  const int64_t* gathers, int64_t gather_bound,
                                  const char* gather_name, int gather_checked_first,
-                                 int64_t num_edges, void* plan_mem, size_t plan_bytes,
+                                 int64_t num_edges, int flags, void* plan_mem, size_t plan_bytes,
                                  relm_mp_plan* plan, relm_mp_stream_t stream) {
     return inv_build(keys, key_bound, key_name, gathers, gather_bound, gather_name,
-                     gather_checked_first, num_edges, plan_mem, plan_bytes, plan, false,
+                     gather_checked_first, num_edges, flags, plan_mem, plan_bytes, plan, false,
                      static_cast<hipStream_t>(stream));
 }
 
@@ -490,34 +524,48 @@ int relm_mp_rows_scale(int dtype, const void* in, const int64_t* gather, int div
                               out, static_cast<hipStream_t>(stream));
 }
 
-size_t relm_mp_index_match_workspace_size(void) { return kMaxMatch * sizeof(int32_t); }
+size_t relm_mp_plan_match_workspace_size(void) { return kMaxMatch * sizeof(int32_t); }
 
-int relm_mp_index_match(const int64_t* keys, const int64_t* gathers, int64_t n,
-                        const int64_t* const* cand_keys, const int64_t* const* cand_gathers,
-                        int32_t num_cand, int32_t* match, void* workspace, size_t workspace_bytes,
-                        relm_mp_stream_t stream) {
-    if (n < 0 || num_cand < 0 || num_cand > kMaxMatch || (num_cand > 0 && match == nullptr))
-        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: bad index match arguments");
-    if (num_cand == 0) return RELM_MP_OK;
+int relm_mp_plan_match(const int64_t* keys, const int64_t* gathers, int64_t n,
+                       const relm_mp_plan* const* plans, int32_t num_plans, int32_t* match,
+                       void* workspace, size_t workspace_bytes, relm_mp_stream_t stream) {
+    if (n < 0 || num_plans < 0 || num_plans > kMaxMatch || (num_plans > 0 && match == nullptr) ||
+        (num_plans > 0 && plans == nullptr))
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: bad plan match arguments");
+    if (num_plans == 0) return RELM_MP_OK;
     if (n > 0 && keys == nullptr)
         return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: keys are NULL");
-    for (int32_t c = 0; c < num_cand; ++c)
-        if (n > 0 && (cand_keys == nullptr || cand_keys[c] == nullptr ||
-                      (gathers != nullptr && (cand_gathers == nullptr || cand_gathers[c] == nullptr))))
-            return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: candidate arrays are NULL");
-    if (workspace == nullptr || workspace_bytes < relm_mp_index_match_workspace_size() ||
+    const relm_mp_plan* cand[kMaxMatch];
+    int32_t slot[kMaxMatch];
+    int32_t num = 0;
+    for (int32_t c = 0; c < num_plans; ++c) {
+        const relm_mp_plan* p = plans[c];
+        if (p == nullptr || (p->num_edges > 0 && p->snap_keys == nullptr) ||
+            (gathers != nullptr && p->num_edges > 0 && p->snap_gathers == nullptr))
+            return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                             "relm_mp: plan without the index snapshot to match");
+        match[c] = 0;
+        if (p->num_edges != n) continue;  // another length: never equal
+        if (n == 0) {
+            match[c] = 1;
+            continue;
+        }
+        cand[num] = p;
+        slot[num++] = c;
+    }
+    if (num == 0) return RELM_MP_OK;
+    if (workspace == nullptr || workspace_bytes < relm_mp_plan_match_workspace_size() ||
         (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
-        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: index match workspace missing or too small");
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: plan match workspace missing or too small");
     HostSlot* hs = nullptr;
     RELM_TRY(host_slot(&hs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     int32_t* flags = static_cast<int32_t*>(workspace);
-    RELM_HIP(launch_index_match(keys, gathers, n, cand_keys, cand_gathers, num_cand, flags, s),
-             "relm_mp index match kernel");
+    RELM_HIP(launch_plan_match(keys, gathers, n, cand, num, flags, s), "relm_mp plan match kernel");
     RELM_HIP(hipMemcpyAsync(hs->match, flags, kMaxMatch * sizeof(int32_t), hipMemcpyDeviceToHost, s),
-             "relm_mp index match copy");
-    RELM_HIP(hipStreamSynchronize(s), "relm_mp index match sync");
-    for (int32_t c = 0; c < num_cand; ++c) match[c] = hs->match[c] == 0 ? 1 : 0;
+             "relm_mp plan match copy");
+    RELM_HIP(hipStreamSynchronize(s), "relm_mp plan match sync");
+    for (int32_t j = 0; j < num; ++j) match[slot[j]] = hs->match[j] == 0 ? 1 : 0;
     return RELM_MP_OK;
 }
 
@@ -680,8 +728,7 @@ int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
 /* ---- op-level entry points -------------------------------------------- */
 
 size_t relm_mp_fanout_scatter_workspace_size(int64_t num_edges, int64_t out_rows) {
-    (void)num_edges;
-    return relm_mp_inv_plan_bytes(out_rows);
+    return relm_mp_inv_plan_bytes(out_rows, num_edges, 0);
 }
 
 // mp_ops.cpp:3038-3101 and the CPU loop 2815-2836: per edge the reference
@@ -701,7 +748,7 @@ int relm_mp_fanout_scatter(int dtype, const void* x_cat, int64_t x_rows, int64_t
     relm_mp_plan plan;
     // the gather is enqueued before the host waits for the index check
     RELM_TRY(inv_build(flat_dst, out_rows, "flat_dst", src_global_idx, x_rows, "src_global_idx", 1,
-                       num_edges, workspace, workspace_bytes, &plan, false, s));
+                       num_edges, 0, workspace, workspace_bytes, &plan, false, s));
     const int rc = compute_gather_last(dtype, plan, src_global_idx, x_cat, emb, out, s);
     const int vrc = validate_pending(&plan);
     return vrc != RELM_MP_OK ? vrc : rc;
@@ -781,7 +828,7 @@ int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int6
 
 size_t relm_mp_fanin_reduce_sum_backward_workspace_size(int64_t num_edges, int64_t rel_rows,
                                                         int64_t emb, int dtype) {
-    const size_t inv = relm_mp_inv_plan_bytes(rel_rows);
+    const size_t inv = relm_mp_inv_plan_bytes(rel_rows, num_edges, 0);
     const size_t plan = relm_mp_csr_plan_bytes(rel_rows, num_edges);
     const size_t scratch = std::max(relm_mp_csr_plan_scratch_bytes(rel_rows, num_edges),
                                     hub_partial_upper_bound(num_edges, emb, dtype, RELM_MP_MODE_SUM));
@@ -804,10 +851,10 @@ int relm_mp_fanin_reduce_sum_backward(int dtype, const void* grad_out, int64_t g
     const size_t need = relm_mp_fanin_reduce_sum_backward_workspace_size(num_edges, rel_rows, emb, dtype);
     if (workspace == nullptr || workspace_bytes < need)
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: workspace too small");
-    const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows);
+    const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows, num_edges, 0);
     relm_mp_plan plan;
     RELM_TRY(inv_build(flat_src, rel_rows, "flat_src", dst_idx, grad_out_rows, "dst_idx", 0,
-                       num_edges, workspace, inv_bytes, &plan, true, s));
+                       num_edges, 0, workspace, inv_bytes, &plan, true, s));
     if (plan.collisions == 0)
         return compute_gather_last(dtype, plan, dst_idx, grad_out, emb, grad_rel, s);
     char* csr_mem = static_cast<char*>(workspace) + inv_bytes;
@@ -854,10 +901,10 @@ int relm_mp_fanin_reduce_logsumexp_backward(int dtype, const void* grad_out, int
         RELM_TRY(compute_fill(dtype, static_cast<char*>(grad_rel) + key_bound * emb * elem,
                               (rel_rows - key_bound) * emb, 0.0, s));
     }
-    const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows);
+    const size_t inv_bytes = relm_mp_inv_plan_bytes(rel_rows, num_edges, 0);
     relm_mp_plan plan;
     RELM_TRY(inv_build(flat_src, key_bound, "flat_src", dst_idx, dim_size, "dst_idx", 1, num_edges,
-                       workspace, inv_bytes, &plan, true, s));
+                       0, workspace, inv_bytes, &plan, true, s));
     if (plan.collisions == 0)
         return compute_logsumexp_backward(dtype, plan, dst_idx, grad_out, out, rel_flat, emb,
                                           grad_rel, nullptr, 0, s);

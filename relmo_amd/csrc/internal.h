@@ -44,6 +44,8 @@ constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys per block
 constexpr int kSortBins = 256;
+constexpr int kSnapTile = RELM_MP_SNAP_TILE;
+static_assert(kSnapTile == kSortTile, "the sort's first pass writes the snapshot tiles");
 
 // Scan geometry.
 constexpr int kScanThreads = 256;
@@ -62,21 +64,34 @@ hipError_t launch_status_init(DevStatus* st, hipStream_t s);
 // also stores the inverse-plan statistics (collisions, identity) there.
 hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped,
                                  relm_mp_plan_counts* pc, hipStream_t s);
+// Index snapshot written by a plan build (relm_mp_plan::snap_*): int32 per
+// edge, tiles of kSnapTile edges whose values are their edge ids flagged in
+// the plain arrays and not stored.  Null members are not written.
+struct SnapOut {
+    uint32_t* keys;
+    uint32_t* gathers;
+    uint32_t* key_plain;
+    uint32_t* gather_plain;
+};
 hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
-                            int64_t gather_bound, int64_t n, int32_t* inv, DevStatus* st,
-                            hipStream_t s);
+                            int64_t gather_bound, int64_t n, int32_t* inv, const SnapOut& snap,
+                            DevStatus* st, hipStream_t s);
 
 
 // Stable LSD radix sort of (key, value) by key.  The first pass reads the
 // caller's int64 keys / gathers, validates them against the bounds (bad
-// entries are recorded in `st` and replaced by 0) and narrows them to 32 bit.
+// entries are recorded in `st` and replaced by 0) and narrows them to 32 bit
+// into keys_n / vals_n in edge order (a plan keeps these as its snapshot);
+// the scatter passes ping-pong between the a and b buffers.
 struct SortBuffers {
+    uint32_t* keys_n;
+    uint32_t* vals_n;
+    uint32_t* tile_plain;  // sort_tiles(n): tiles whose values are the edge ids (vals_n not written)
     uint32_t* keys_a;
     uint32_t* vals_a;
     uint32_t* keys_b;
     uint32_t* vals_b;
     uint32_t* hist;        // sort_hist_words(n): per-tile digit counts, digit totals
-    uint32_t* tile_plain;  // sort_tiles(n): first-pass tiles whose values are the edge ids
 };
 int64_t sort_tiles(int64_t n);
 size_t sort_hist_words(int64_t n);
@@ -118,11 +133,12 @@ hipError_t launch_pack_index(const relm_mp_index_part* parts, int num_parts, int
 
 // ---- content comparison (match_kernels.hip) -------------------------------
 constexpr int kMaxMatch = RELM_MP_MAX_MATCH;
-// mismatch[0..kMaxMatch) is cleared, then mismatch[c] != 0 iff candidate c
-// differs from (keys, gathers); gathers may be null (keys only).
-hipError_t launch_index_match(const int64_t* keys, const int64_t* gathers, int64_t n,
-                              const int64_t* const* cand_keys, const int64_t* const* cand_gathers,
-                              int num_cand, int32_t* mismatch, hipStream_t s);
+// mismatch[0..kMaxMatch) is cleared, then mismatch[c] != 0 iff the snapshot of
+// plans[c] differs from (keys, gathers) (gathers null: keys only; every plan
+// has num_edges == n).
+hipError_t launch_plan_match(const int64_t* keys, const int64_t* gathers, int64_t n,
+                             const relm_mp_plan* const* plans, int num_plans, int32_t* mismatch,
+                             hipStream_t s);
 
 // ---- compute kernels (reduce_kernels.hip) --------------------------------
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,

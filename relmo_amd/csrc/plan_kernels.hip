@@ -62,38 +62,71 @@ __global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __
 }
 
 // inv[k] = max e with keys[e] == k.  Every key and gathered index is checked;
-// the smallest offending edge of each array is recorded.
+// the smallest offending edge of each array is recorded.  Workgroups take
+// tiles of kSnapTile edges (grid-stride); with a snapshot, a tile's narrowed
+// indices are stored unless they are the tile's own edge ids, which the
+// tile's plain flag records instead.
 __global__ __launch_bounds__(kThreads) void k_inv_build(const int64_t* __restrict__ keys,
                                                         int64_t key_bound,
                                                         const int64_t* __restrict__ gathers,
                                                         int64_t gather_bound, int64_t n,
-                                                        int32_t* __restrict__ inv,
+                                                        int32_t* __restrict__ inv, SnapOut snap,
                                                         DevStatus* __restrict__ st) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    unsigned long long collisions = 0;
-    bool mismatch = false;
-    for (int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x; base < n; base += stride) {
-        const int64_t e = base + threadIdx.x;
-        bool coll = false;
-        if (e < n) {
-            const int64_t k = keys[e];
-            mismatch = mismatch || k != e;
-            const bool bad_k = static_cast<uint64_t>(k) >= static_cast<uint64_t>(key_bound);
-            if (bad_k) atomicMin(&st->bad_key_edge, static_cast<unsigned long long>(e));
-            if (gathers != nullptr) {
-                const int64_t g = gathers[e];
-                if (static_cast<uint64_t>(g) >= static_cast<uint64_t>(gather_bound))
-                    atomicMin(&st->bad_gather_edge, static_cast<unsigned long long>(e));
+    constexpr int kItems = kSnapTile / kThreads;
+    const int64_t tiles = (n + kSnapTile - 1) / kSnapTile;
+    const bool snapshot = snap.keys != nullptr || snap.gathers != nullptr;
+    unsigned long long collisions = 0, bad_k = kNoEdge, bad_g = kNoEdge;
+    int key_mismatch = 0;
+    for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const int64_t base = t * kSnapTile + threadIdx.x;
+        uint32_t k32[kItems], g32[kItems];
+        int kmis = 0, gmis = 0;
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kThreads;
+            bool coll = false;
+            k32[i] = g32[i] = 0;
+            if (p < n) {
+                const int64_t k = keys[p];
+                kmis |= k != p ? 1 : 0;
+                if (static_cast<uint64_t>(k) < static_cast<uint64_t>(key_bound)) {
+                    k32[i] = static_cast<uint32_t>(k);
+                    coll = atomicMax(inv + k, static_cast<int32_t>(p)) >= 0;
+                } else {
+                    bad_k = min(bad_k, static_cast<unsigned long long>(p));
+                }
+                if (gathers != nullptr) {
+                    const int64_t g = gathers[p];
+                    gmis |= g != p ? 1 : 0;
+                    if (static_cast<uint64_t>(g) < static_cast<uint64_t>(gather_bound))
+                        g32[i] = static_cast<uint32_t>(g);
+                    else
+                        bad_g = min(bad_g, static_cast<unsigned long long>(p));
+                }
             }
-            if (!bad_k) {
-                const int32_t old = atomicMax(inv + k, static_cast<int32_t>(e));
-                coll = old >= 0;
+            collisions += __popcll(__ballot(coll));
+        }
+        key_mismatch |= kmis;
+        if (snapshot) {
+            const int any_k = __syncthreads_or(kmis);
+            const int any_g = __syncthreads_or(gmis);
+#pragma unroll
+            for (int i = 0; i < kItems; ++i) {
+                const int64_t p = base + static_cast<int64_t>(i) * kThreads;
+                if (p >= n) continue;
+                if (snap.keys != nullptr && any_k) snap.keys[p] = k32[i];
+                if (snap.gathers != nullptr && any_g) snap.gathers[p] = g32[i];
+            }
+            if (threadIdx.x == 0) {
+                if (snap.key_plain != nullptr) snap.key_plain[t] = any_k ? 0u : 1u;
+                if (snap.gather_plain != nullptr) snap.gather_plain[t] = any_g ? 0u : 1u;
             }
         }
-        collisions += __popcll(__ballot(coll));
     }
+    if (bad_k != kNoEdge) atomicMin(&st->bad_key_edge, bad_k);
+    if (bad_g != kNoEdge) atomicMin(&st->bad_gather_edge, bad_g);
     if (lane_id() == 0 && collisions != 0) atomicAdd(&st->collisions, collisions);
-    if (__ballot(mismatch) != 0 && lane_id() == 0) atomicOr(&st->key_mismatch, 1ull);
+    if (__ballot(key_mismatch != 0) != 0 && lane_id() == 0) atomicOr(&st->key_mismatch, 1ull);
 }
 
 // ---- scan ----------------------------------------------------------------
@@ -732,11 +765,11 @@ hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped,
 }
 
 hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
-                            int64_t gather_bound, int64_t n, int32_t* inv, DevStatus* st,
-                            hipStream_t s) {
+                            int64_t gather_bound, int64_t n, int32_t* inv, const SnapOut& snap,
+                            DevStatus* st, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_inv_build, dim3(grid_1d(n, kThreads * 4)), dim3(kThreads), 0, s, keys,
-                       key_bound, gathers, gather_bound, n, inv, st);
+    hipLaunchKernelGGL(k_inv_build, dim3(grid_1d(n, kSnapTile)), dim3(kThreads), 0, s, keys,
+                       key_bound, gathers, gather_bound, n, inv, snap, st);
     return hipGetLastError();
 }
 
@@ -782,10 +815,10 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
     uint32_t* digit_tot = buf.hist + hist_n;
     const int64_t col_chunks = (nblocks + kColChunk - 1) / kColChunk;
     uint32_t* chunk_sum = digit_tot + kSortBins;
-    // the narrowed input goes to the b buffers; pass p writes a, b, a, ... and
-    // the last pass the plan arrays
-    const uint32_t* in_k = buf.keys_b;
-    const uint32_t* in_v = buf.vals_b;
+    // the narrowed input goes to the n buffers (the plan's snapshot); pass p
+    // writes a, b, a, ... and the last pass the plan arrays
+    const uint32_t* in_k = buf.keys_n;
+    const uint32_t* in_v = buf.vals_n;
     int shift = 0;
     for (int p = 0; p < passes; ++p) {
         const int width = bits / passes + (p < bits % passes ? 1 : 0);
@@ -795,7 +828,7 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         const dim3 grid(static_cast<unsigned>(nblocks)), block(kSortThreads);
         if (p == 0) {
             hipLaunchKernelGGL(k_radix_narrow, grid, block, 0, s, keys, gathers, n, shift, width,
-                               key_bound, gather_bound, buf.keys_b, buf.vals_b, buf.tile_plain,
+                               key_bound, gather_bound, buf.keys_n, buf.vals_n, buf.tile_plain,
                                buf.hist, nblocks, st);
         } else {
             with_digit_bits(width, [&](auto bt) {

@@ -16,6 +16,8 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <c10/util/intrusive_ptr.h>
+#include <c10/hip/HIPCachingAllocator.h>
+#include <torch/custom_class.h>
 #include <torch/library.h>
 
 #include <algorithm>
@@ -99,21 +101,24 @@ Tensor byte_buffer(size_t bytes, const Tensor& like) {
                      like.options().dtype(at::kByte));
 }
 
-// ---- plan cache -------------------------------------------------------------
+// ---- index plans and their cache ---------------------------------------------
 //
-// Plans depend only on the index tensors' contents and the bounds.  An entry
-// is reused when
-//   * the same TensorImpl objects are passed again with unchanged version
-//     counters (identity), or
-//   * other tensors of the same length and bounds hold the same indices
-//     (content: one device pass compares them with the entry's tensors, which
-//     the entry keeps alive for that purpose, and the entry then moves to the
-//     new tensors) - the same topology rebuilt in every forward.
-// RELM_MP_PLAN_CACHE=0 disables reuse; RELM_MP_PLAN_CACHE=identity keeps only
-// identity reuse (entries hold the tensors weakly and die with them, so a dead
-// tensor's address cannot be recycled while the entry exists);
-// RELM_MP_PLAN_CACHE_MB bounds the memory of the entries, plans and kept index
-// tensors (default 4096).
+// A plan (relm_mp.h) lives in a byte tensor on the device together with a
+// snapshot of the indices it was built from.  PlanRef holds it with the
+// stream that built it and an event recorded behind the build, so that work
+// on another stream can wait for the plan.
+//
+// The cache keeps recent plans.  A plan is served to a later call only when
+// that call's index arrays equal the plan's snapshot: one device pass compares
+// them with up to RELM_MP_MAX_MATCH candidates of the same role, device,
+// length and bounds, so an index tensor written after the build - in place,
+// through .data, through a raw pointer - leads to a new plan, never to a stale
+// one.  Candidates last used with the same tensor objects are compared first.
+// The autograd functions of the facade hand a forward's plan to its backward
+// directly (fanin_reduce_planned and the *_planned backward ops).
+// RELM_MP_PLAN_CACHE=0 disables the cache; RELM_MP_PLAN_CACHE=identity
+// compares only with plans last used with the same tensor objects;
+// RELM_MP_PLAN_CACHE_MB bounds the plan memory the cache keeps (default 2048).
 
 enum PlanRole : int {
     kRoleInverse = 1,
@@ -121,27 +126,48 @@ enum PlanRole : int {
     kRoleCsrRows = 3,  // CSR plan whose gathered rows are the edges themselves
 };
 
-struct PlanEntry {
-    PlanEntry(const Tensor& key, const Tensor& gather)
-        : key_w(key.getIntrusivePtr()), gather_w(gather.getIntrusivePtr()) {}
+void check_hip(hipError_t e, const char* what) {
+    TORCH_CHECK(e == hipSuccess, "relm_mp: ", what, ": ", hipGetErrorString(e));
+}
+
+struct PlanRef : torch::CustomClassHolder {
+    relm_mp_plan plan{};
+    Tensor mem;
     int role = 0;
-    c10::weak_intrusive_ptr<c10::TensorImpl> key_w;
-    c10::weak_intrusive_ptr<c10::TensorImpl> gather_w;
-    Tensor key_t;  // content mode: the indices the plan was built from
-    Tensor gather_t;
-    const c10::TensorImpl* key_impl = nullptr;
-    const c10::TensorImpl* gather_impl = nullptr;
-    uint32_t key_ver = 0;
-    uint32_t gather_ver = 0;
+    int device = -1;
     int64_t key_bound = 0;
     int64_t gather_bound = 0;
-    int64_t num_edges = 0;
-    int device = -1;
-    Tensor mem;
-    relm_mp_plan plan{};
-    size_t bytes = 0;
-    uint64_t stamp = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t built = nullptr;
+
+    PlanRef() = default;
+    PlanRef(const PlanRef&) = delete;
+    PlanRef& operator=(const PlanRef&) = delete;
+    ~PlanRef() {
+        if (built != nullptr) (void)hipEventDestroy(built);
+    }
+
+    bool defined() const { return plan.kind != 0; }
+
+    // Records the end of the build on its stream (after the build's last
+    // kernel has been enqueued).
+    void mark_built() {
+        if (built == nullptr)
+            check_hip(hipEventCreateWithFlags(&built, hipEventDisableTiming), "plan event");
+        check_hip(hipEventRecord(built, stream), "plan event record");
+    }
+
+    // Work enqueued on `s` from now on waits for the build, and the plan
+    // memory is not handed out again before that work has finished.
+    void use_on(hipStream_t s) const {
+        if (s == stream || !mem.defined()) return;
+        check_hip(hipStreamWaitEvent(s, built, 0), "plan stream wait");
+        c10::hip::HIPCachingAllocator::recordStream(
+            mem.storage().data_ptr(), c10::hip::getStreamFromExternal(s, device));
+    }
 };
+
+using PlanPtr = c10::intrusive_ptr<PlanRef>;
 
 class PlanCache {
    public:
@@ -152,74 +178,82 @@ class PlanCache {
 
     bool enabled() const { return enabled_; }
 
-    bool lookup(int role, const Tensor& key, const Tensor& gather, int64_t key_bound,
-                int64_t gather_bound, relm_mp_plan* out, hipStream_t s) {
-        if (!enabled_ || !cacheable(key) || !cacheable(gather)) return false;
-        std::lock_guard<std::mutex> lock(mu_);
-        purge_dead_locked();
-        for (PlanEntry& e : entries_) {
-            if (e.role == role && e.key_impl == key.unsafeGetTensorImpl() &&
-                e.gather_impl == gather.unsafeGetTensorImpl() && e.key_ver == version(key) &&
-                e.gather_ver == version(gather) && e.key_bound == key_bound &&
-                e.gather_bound == gather_bound && e.num_edges == key.numel() &&
-                e.device == key.get_device()) {
-                e.stamp = ++clock_;
-                ++identity_hits_;
-                *out = e.plan;
-                return true;
+    // A cached plan of `role` built from indices equal to (key, gather) under
+    // the same bounds (gather_bound < 0: any gather bound), ready for use on
+    // `s`; null if there is none.  gather null: only the keys are compared.
+    PlanPtr lookup(int role, const Tensor& key, const Tensor* gather, int64_t key_bound,
+                   int64_t gather_bound, hipStream_t s) {
+        if (!enabled_) return PlanPtr();
+        struct Cand {
+            PlanPtr ref;
+            bool same;
+            uint64_t stamp;
+        };
+        std::vector<Cand> cand;
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            for (const Entry& e : entries_) {
+                const PlanRef& r = *e.ref;
+                if (r.role != role || r.device != key.get_device() ||
+                    r.plan.num_edges != key.numel() || r.key_bound != key_bound ||
+                    (gather_bound >= 0 && r.gather_bound != gather_bound))
+                    continue;
+                const bool same = e.key_impl == key.unsafeGetTensorImpl() &&
+                                  e.key_ver == version(key) &&
+                                  (gather == nullptr ||
+                                   (e.gather_impl == gather->unsafeGetTensorImpl() &&
+                                    e.gather_ver == version(*gather)));
+                if (identity_only_ && !same) continue;
+                cand.push_back({e.ref, same, e.stamp});
+            }
+            if (cand.empty()) {
+                ++misses_;
+                return PlanPtr();
             }
         }
-        if (content_ && lookup_content_locked(role, key, gather, key_bound, gather_bound, out, s))
-            return true;
+        std::sort(cand.begin(), cand.end(), [](const Cand& a, const Cand& b) {
+            return a.same != b.same ? a.same : a.stamp > b.stamp;
+        });
+        if (cand.size() > RELM_MP_MAX_MATCH) cand.resize(RELM_MP_MAX_MATCH);
+        std::vector<const relm_mp_plan*> plans;
+        for (const Cand& c : cand) {
+            c.ref->use_on(s);  // the comparison reads the snapshot the build wrote
+            plans.push_back(&c.ref->plan);
+        }
+        std::vector<int32_t> match(cand.size(), 0);
+        Tensor ws = byte_buffer(relm_mp_plan_match_workspace_size(), key);
+        raise_if(relm_mp_plan_match(key.data_ptr<int64_t>(),
+                                    gather != nullptr ? gather->data_ptr<int64_t>() : nullptr,
+                                    key.numel(), plans.data(), static_cast<int32_t>(plans.size()),
+                                    match.data(), ws.data_ptr(), static_cast<size_t>(ws.numel()), s));
+        std::lock_guard<std::mutex> lock(mu_);
+        for (size_t j = 0; j < cand.size(); ++j) {
+            if (!match[j]) continue;
+            for (Entry& e : entries_) {
+                if (e.ref.get() != cand[j].ref.get()) continue;
+                e.stamp = ++clock_;
+                note_tensors(e, key, gather);
+            }
+            ++(cand[j].same ? same_hits_ : other_hits_);
+            return cand[j].ref;
+        }
         ++misses_;
-        return false;
+        return PlanPtr();
     }
 
-    // A cached CSR plan for (key, gather) with any gather bound: the forward's
-    // plan, looked up by a backward op whose own bound for the gathered rows
-    // may differ.
-    bool lookup_csr_any_gather_bound(const Tensor& key, const Tensor& gather, int64_t key_bound,
-                                     relm_mp_plan* out) {
-        if (!enabled_ || !cacheable(key) || !cacheable(gather)) return false;
+    // Keeps `ref` (a completed build of `key` / `gather`), evicting the least
+    // recently used plans beyond the memory bound.
+    void insert(const PlanPtr& ref, const Tensor& key, const Tensor* gather) {
+        if (!enabled_) return;
+        const size_t bytes = static_cast<size_t>(ref->mem.numel());
+        if (bytes > limit_) return;
         std::lock_guard<std::mutex> lock(mu_);
-        purge_dead_locked();
-        for (PlanEntry& e : entries_) {
-            if (e.role == kRoleCsr && e.key_impl == key.unsafeGetTensorImpl() &&
-                e.gather_impl == gather.unsafeGetTensorImpl() && e.key_ver == version(key) &&
-                e.gather_ver == version(gather) && e.key_bound == key_bound &&
-                e.num_edges == key.numel() && e.device == key.get_device()) {
-                e.stamp = ++clock_;
-                *out = e.plan;
-                return true;
-            }
-        }
-        return false;
-    }
-
-    void insert(int role, const Tensor& key, const Tensor& gather, int64_t key_bound,
-                int64_t gather_bound, const Tensor& mem, const relm_mp_plan& plan) {
-        if (!enabled_ || !cacheable(key) || !cacheable(gather)) return;
-        std::lock_guard<std::mutex> lock(mu_);
-        PlanEntry e(key, gather);
-        if (content_) {
-            e.key_t = key;
-            e.gather_t = gather;
-        }
-        e.role = role;
-        e.key_impl = key.unsafeGetTensorImpl();
-        e.gather_impl = gather.unsafeGetTensorImpl();
-        e.key_ver = version(key);
-        e.gather_ver = version(gather);
-        e.key_bound = key_bound;
-        e.gather_bound = gather_bound;
-        e.num_edges = key.numel();
-        e.device = key.get_device();
-        e.mem = mem;
-        e.plan = plan;
-        e.bytes = static_cast<size_t>(mem.numel()) +
-                  (content_ ? static_cast<size_t>(key.nbytes() + gather.nbytes()) : 0);
+        Entry e;
+        e.ref = ref;
+        e.bytes = bytes;
         e.stamp = ++clock_;
-        total_ += e.bytes;
+        note_tensors(e, key, gather);
+        total_ += bytes;
         entries_.push_back(std::move(e));
         while ((total_ > limit_ || entries_.size() > kMaxEntries) && entries_.size() > 1) {
             size_t victim = 0;
@@ -228,6 +262,7 @@ class PlanCache {
             total_ -= entries_[victim].bytes;
             entries_.erase(entries_.begin() + static_cast<std::ptrdiff_t>(victim));
         }
+        peak_ = std::max(peak_, total_);
     }
 
     void clear() {
@@ -236,21 +271,34 @@ class PlanCache {
         total_ = 0;
     }
 
-    // entries, identity hits, content hits, misses (lookups that built a plan)
+    // entries, hits with the same tensors, hits with other tensors of equal
+    // content, misses (lookups that found no equal plan), bytes kept, peak bytes
     std::vector<int64_t> stats() {
         std::lock_guard<std::mutex> lock(mu_);
-        purge_dead_locked();
-        return {static_cast<int64_t>(entries_.size()), identity_hits_, content_hits_, misses_};
+        return {static_cast<int64_t>(entries_.size()), same_hits_, other_hits_, misses_,
+                static_cast<int64_t>(total_), static_cast<int64_t>(peak_)};
     }
 
     int64_t size() {
         std::lock_guard<std::mutex> lock(mu_);
-        purge_dead_locked();
         return static_cast<int64_t>(entries_.size());
     }
 
    private:
     static constexpr size_t kMaxEntries = 64;
+
+    // The tensors a plan was last used with, kept only as a hint for ordering
+    // the candidates: the address may belong to a later tensor by now, which
+    // costs nothing because every candidate's content is compared.
+    struct Entry {
+        PlanPtr ref;
+        const c10::TensorImpl* key_impl = nullptr;
+        const c10::TensorImpl* gather_impl = nullptr;
+        uint32_t key_ver = 0;
+        uint32_t gather_ver = 0;
+        size_t bytes = 0;
+        uint64_t stamp = 0;
+    };
 
     PlanCache() {
         const char* flag = std::getenv("RELM_MP_PLAN_CACHE");
@@ -258,153 +306,100 @@ class PlanCache {
             std::string v(flag);
             for (char& c : v) c = static_cast<char>(std::tolower(static_cast<unsigned char>(c)));
             enabled_ = !(v == "0" || v == "false" || v == "no" || v == "off");
-            content_ = v != "identity";
+            identity_only_ = v == "identity";
         }
         const char* mb = std::getenv("RELM_MP_PLAN_CACHE_MB");
         if (mb != nullptr) limit_ = static_cast<size_t>(std::strtoull(mb, nullptr, 10)) << 20;
     }
 
-    static bool cacheable(const Tensor& t) { return !t.is_inference(); }
-
     static uint32_t version(const Tensor& t) {
         return t.unsafeGetTensorImpl()->version_counter().current_version();
     }
 
-    // Entries of the same role, device, length and bounds whose kept tensors
-    // are unchanged are compared with (key, gather) on the device (at most
-    // kMaxMatch, most recent first); an equal one serves and moves to the new
-    // tensors.  Entries whose kept tensors were modified in place are dropped.
-    bool lookup_content_locked(int role, const Tensor& key, const Tensor& gather,
-                               int64_t key_bound, int64_t gather_bound, relm_mp_plan* out,
-                               hipStream_t s) {
-        std::vector<size_t> cand;
-        for (size_t i = 0; i < entries_.size();) {
-            PlanEntry& e = entries_[i];
-            if (e.key_t.defined() && (version(e.key_t) != e.key_ver || version(e.gather_t) != e.gather_ver)) {
-                total_ -= e.bytes;
-                entries_.erase(entries_.begin() + static_cast<std::ptrdiff_t>(i));
-                continue;
-            }
-            if (e.key_t.defined() && e.role == role && e.key_bound == key_bound &&
-                e.gather_bound == gather_bound && e.num_edges == key.numel() &&
-                e.device == key.get_device())
-                cand.push_back(i);
-            ++i;
-        }
-        if (cand.empty()) return false;
-        std::sort(cand.begin(), cand.end(),
-                  [&](size_t a, size_t b) { return entries_[a].stamp > entries_[b].stamp; });
-        if (cand.size() > RELM_MP_MAX_MATCH) cand.resize(RELM_MP_MAX_MATCH);
-        std::vector<const int64_t*> ck, cg;
-        for (size_t i : cand) {
-            ck.push_back(entries_[i].key_t.data_ptr<int64_t>());
-            cg.push_back(entries_[i].gather_t.data_ptr<int64_t>());
-        }
-        std::vector<int32_t> match(cand.size(), 0);
-        Tensor ws = byte_buffer(relm_mp_index_match_workspace_size(), key);
-        raise_if(relm_mp_index_match(key.data_ptr<int64_t>(), gather.data_ptr<int64_t>(),
-                                     key.numel(), ck.data(), cg.data(),
-                                     static_cast<int32_t>(cand.size()), match.data(), ws.data_ptr(),
-                                     static_cast<size_t>(ws.numel()), s));
-        for (size_t j = 0; j < cand.size(); ++j) {
-            if (!match[j]) continue;
-            PlanEntry& e = entries_[cand[j]];
-            total_ -= e.bytes;
-            e.key_w = key.getIntrusivePtr();
-            e.gather_w = gather.getIntrusivePtr();
-            e.key_t = key;
-            e.gather_t = gather;
-            e.key_impl = key.unsafeGetTensorImpl();
-            e.gather_impl = gather.unsafeGetTensorImpl();
-            e.key_ver = version(key);
-            e.gather_ver = version(gather);
-            e.bytes = static_cast<size_t>(e.mem.numel() + key.nbytes() + gather.nbytes());
-            total_ += e.bytes;
-            e.stamp = ++clock_;
-            ++content_hits_;
-            *out = e.plan;
-            return true;
-        }
-        return false;
-    }
-
-    void purge_dead_locked() {
-        for (size_t i = 0; i < entries_.size();) {
-            if (entries_[i].key_w.expired() || entries_[i].gather_w.expired()) {
-                total_ -= entries_[i].bytes;
-                entries_.erase(entries_.begin() + static_cast<std::ptrdiff_t>(i));
-            } else {
-                ++i;
-            }
-        }
+    static void note_tensors(Entry& e, const Tensor& key, const Tensor* gather) {
+        e.key_impl = key.unsafeGetTensorImpl();
+        e.key_ver = version(key);
+        e.gather_impl = gather != nullptr ? gather->unsafeGetTensorImpl() : nullptr;
+        e.gather_ver = gather != nullptr ? version(*gather) : 0;
     }
 
     std::mutex mu_;
-    std::vector<PlanEntry> entries_;
+    std::vector<Entry> entries_;
     size_t total_ = 0;
-    size_t limit_ = size_t(4096) << 20;
+    size_t peak_ = 0;
+    size_t limit_ = size_t(2048) << 20;
     uint64_t clock_ = 0;
-    int64_t identity_hits_ = 0;
-    int64_t content_hits_ = 0;
+    int64_t same_hits_ = 0;
+    int64_t other_hits_ = 0;
     int64_t misses_ = 0;
     bool enabled_ = true;
-    bool content_ = true;
+    bool identity_only_ = false;
 };
 
-struct GpuPlan {
-    relm_mp_plan plan{};
-    Tensor mem;  // keeps uncached plan memory alive for the call
-};
-
-GpuPlan inverse_plan(const Tensor& key, int64_t key_bound, const char* key_name,
-                     const Tensor& gather, int64_t gather_bound, const char* gather_name,
-                     bool gather_first, hipStream_t s) {
-    GpuPlan gp;
-    PlanCache& cache = PlanCache::get();
-    if (cache.lookup(kRoleInverse, key, gather, key_bound, gather_bound, &gp.plan, s)) return gp;
-    gp.mem = byte_buffer(relm_mp_inv_plan_bytes(key_bound), key);
-    raise_if(relm_mp_inv_plan_build(key.data_ptr<int64_t>(), key_bound, key_name,
-                                    gather.data_ptr<int64_t>(), gather_bound, gather_name,
-                                    gather_first ? 1 : 0, key.numel(), gp.mem.data_ptr(),
-                                    static_cast<size_t>(gp.mem.numel()), &gp.plan, s));
-    cache.insert(kRoleInverse, key, gather, key_bound, gather_bound, gp.mem, gp.plan);
-    return gp;
+PlanPtr new_plan(int role, const Tensor& like, int64_t key_bound, int64_t gather_bound,
+                 size_t bytes, hipStream_t s) {
+    PlanPtr r = c10::make_intrusive<PlanRef>();
+    r->mem = byte_buffer(bytes, like);
+    r->role = role;
+    r->device = like.get_device();
+    r->key_bound = key_bound;
+    r->gather_bound = gather_bound;
+    r->stream = s;
+    return r;
 }
 
-GpuPlan csr_plan(const Tensor& key, int64_t key_bound, const char* key_name, const Tensor& gather,
-                 int64_t gather_bound, const char* gather_name, bool gather_first, hipStream_t s) {
-    GpuPlan gp;
+int inverse_flags() { return PlanCache::get().enabled() ? RELM_MP_PLAN_SNAPSHOT : 0; }
+
+PlanPtr inverse_plan(const Tensor& key, int64_t key_bound, const char* key_name,
+                     const Tensor& gather, int64_t gather_bound, const char* gather_name,
+                     bool gather_first, hipStream_t s) {
     PlanCache& cache = PlanCache::get();
-    if (cache.lookup(kRoleCsr, key, gather, key_bound, gather_bound, &gp.plan, s)) return gp;
+    if (PlanPtr hit = cache.lookup(kRoleInverse, key, &gather, key_bound, gather_bound, s)) return hit;
+    const int flags = inverse_flags();
+    PlanPtr r = new_plan(kRoleInverse, key, key_bound, gather_bound,
+                         relm_mp_inv_plan_bytes(key_bound, key.numel(), flags), s);
+    raise_if(relm_mp_inv_plan_build(key.data_ptr<int64_t>(), key_bound, key_name,
+                                    gather.data_ptr<int64_t>(), gather_bound, gather_name,
+                                    gather_first ? 1 : 0, key.numel(), flags, r->mem.data_ptr(),
+                                    static_cast<size_t>(r->mem.numel()), &r->plan, s));
+    r->mark_built();
+    cache.insert(r, key, &gather);
+    return r;
+}
+
+// CSR plan keyed by `key` gathering `gather` (null: message e reads row e).
+PlanPtr csr_build(int role, const Tensor& key, int64_t key_bound, const char* key_name,
+                  const Tensor* gather, int64_t gather_bound, const char* gather_name,
+                  bool gather_first, hipStream_t s) {
     const int64_t n = key.numel();
-    gp.mem = byte_buffer(relm_mp_csr_plan_bytes(key_bound, n), key);
+    PlanPtr r = new_plan(role, key, key_bound, gather_bound, relm_mp_csr_plan_bytes(key_bound, n), s);
     Tensor scratch = byte_buffer(relm_mp_csr_plan_scratch_bytes(key_bound, n), key);
     // returns once the indices are validated; the build's remaining kernels
     // and the caller's compute stay queued on the stream
-    raise_if(relm_mp_csr_plan_build_async(key.data_ptr<int64_t>(), key_bound, key_name,
-                                          gather.data_ptr<int64_t>(), gather_bound, gather_name,
-                                          gather_first ? 1 : 0, n, gp.mem.data_ptr(),
-                                          static_cast<size_t>(gp.mem.numel()), scratch.data_ptr(),
-                                          static_cast<size_t>(scratch.numel()), &gp.plan, s));
-    cache.insert(kRoleCsr, key, gather, key_bound, gather_bound, gp.mem, gp.plan);
-    return gp;
+    raise_if(relm_mp_csr_plan_build_async(
+        key.data_ptr<int64_t>(), key_bound, key_name,
+        gather != nullptr ? gather->data_ptr<int64_t>() : nullptr, gather_bound, gather_name,
+        gather_first ? 1 : 0, n, r->mem.data_ptr(), static_cast<size_t>(r->mem.numel()),
+        scratch.data_ptr(), static_cast<size_t>(scratch.numel()), &r->plan, s));
+    r->mark_built();
+    PlanCache::get().insert(r, key, gather);
+    return r;
 }
 
-// CSR plan keyed by `key` whose message e reads row e (no gather array); the
-// cache entry uses `key` in the gather position.
-GpuPlan csr_plan_rows(const Tensor& key, int64_t key_bound, const char* key_name, hipStream_t s) {
-    GpuPlan gp;
-    PlanCache& cache = PlanCache::get();
+PlanPtr csr_plan(const Tensor& key, int64_t key_bound, const char* key_name, const Tensor& gather,
+                 int64_t gather_bound, const char* gather_name, bool gather_first, hipStream_t s) {
+    if (PlanPtr hit = PlanCache::get().lookup(kRoleCsr, key, &gather, key_bound, gather_bound, s))
+        return hit;
+    return csr_build(kRoleCsr, key, key_bound, key_name, &gather, gather_bound, gather_name,
+                     gather_first, s);
+}
+
+// CSR plan keyed by `key` whose message e reads row e (no gather array).
+PlanPtr csr_plan_rows(const Tensor& key, int64_t key_bound, const char* key_name, hipStream_t s) {
     const int64_t n = key.numel();
-    if (cache.lookup(kRoleCsrRows, key, key, key_bound, n, &gp.plan, s)) return gp;
-    gp.mem = byte_buffer(relm_mp_csr_plan_bytes(key_bound, n), key);
-    Tensor scratch = byte_buffer(relm_mp_csr_plan_scratch_bytes(key_bound, n), key);
-    raise_if(relm_mp_csr_plan_build_async(key.data_ptr<int64_t>(), key_bound, key_name, nullptr, n,
-                                          "", 0, n, gp.mem.data_ptr(),
-                                          static_cast<size_t>(gp.mem.numel()), scratch.data_ptr(),
-                                          static_cast<size_t>(scratch.numel()), &gp.plan, s));
-    cache.insert(kRoleCsrRows, key, key, key_bound, n, gp.mem, gp.plan);
-    return gp;
+    if (PlanPtr hit = PlanCache::get().lookup(kRoleCsrRows, key, nullptr, key_bound, n, s))
+        return hit;
+    return csr_build(kRoleCsrRows, key, key_bound, key_name, nullptr, n, "", false, s);
 }
 
 Tensor compute_scratch(const relm_mp_plan& plan, int64_t emb, int dtype, int64_t mode,
@@ -414,6 +409,32 @@ Tensor compute_scratch(const relm_mp_plan& plan, int64_t emb, int dtype, int64_t
 }
 
 // ---- GPU lane ----------------------------------------------------------------
+
+// Inverse plan keyed by flat_dst gathering src_global_idx, with `gather`
+// (the plan's first compute step, which reads the gathered rows through the
+// plan) enqueued before the host waits for the index check: its kernels stay
+// in bounds on bad indices and the result is discarded then.
+template <class Gather>
+void fanout_inverse(const Tensor& d_idx, int64_t out_rows, const Tensor& s_idx, int64_t x_rows,
+                    hipStream_t stream, Gather&& gather) {
+    PlanCache& cache = PlanCache::get();
+    if (PlanPtr hit = cache.lookup(kRoleInverse, d_idx, &s_idx, out_rows, x_rows, stream)) {
+        raise_if(gather(hit->plan));
+        return;
+    }
+    const int flags = inverse_flags();
+    PlanPtr r = new_plan(kRoleInverse, d_idx, out_rows, x_rows,
+                         relm_mp_inv_plan_bytes(out_rows, d_idx.numel(), flags), stream);
+    raise_if(relm_mp_inv_plan_build_async(d_idx.data_ptr<int64_t>(), out_rows, "flat_dst",
+                                          s_idx.data_ptr<int64_t>(), x_rows, "src_global_idx", 1,
+                                          d_idx.numel(), flags, r->mem.data_ptr(),
+                                          static_cast<size_t>(r->mem.numel()), &r->plan, stream));
+    const int rc = gather(r->plan);
+    raise_if(relm_mp_plan_validate(&r->plan));
+    raise_if(rc);
+    r->mark_built();
+    cache.insert(r, d_idx, &s_idx);
+}
 
 Tensor fanout_scatter_gpu(const Tensor& x_cat, const Tensor& src, const Tensor& dst,
                           int64_t out_rows) {
@@ -428,25 +449,10 @@ Tensor fanout_scatter_gpu(const Tensor& x_cat, const Tensor& src, const Tensor& 
     const Tensor d_idx = contiguous(dst);
     hipStream_t stream = current_stream(x);
     Tensor out = at::empty({out_rows, emb}, x_cat.options());
-    PlanCache& cache = PlanCache::get();
-    GpuPlan gp;
-    if (cache.lookup(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), &gp.plan, stream)) {
-        raise_if(relm_mp_plan_gather_last(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
-                                          x.data_ptr(), emb, out.data_ptr(), stream));
-        return out;
-    }
-    // The gather is enqueued before the host waits for the index check (the
-    // kernels stay in bounds on bad indices; the result is then discarded).
-    gp.mem = byte_buffer(relm_mp_inv_plan_bytes(out_rows), d_idx);
-    raise_if(relm_mp_inv_plan_build_async(d_idx.data_ptr<int64_t>(), out_rows, "flat_dst",
-                                          s_idx.data_ptr<int64_t>(), x.size(0), "src_global_idx", 1,
-                                          d_idx.numel(), gp.mem.data_ptr(),
-                                          static_cast<size_t>(gp.mem.numel()), &gp.plan, stream));
-    const int rc = relm_mp_plan_gather_last(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
-                                            x.data_ptr(), emb, out.data_ptr(), stream);
-    raise_if(relm_mp_plan_validate(&gp.plan));
-    raise_if(rc);
-    cache.insert(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), gp.mem, gp.plan);
+    fanout_inverse(d_idx, out_rows, s_idx, x.size(0), stream, [&](const relm_mp_plan& plan) {
+        return relm_mp_plan_gather_last(dtype_code(x), &plan, s_idx.data_ptr<int64_t>(),
+                                        x.data_ptr(), emb, out.data_ptr(), stream);
+    });
     return out;
 }
 
@@ -462,11 +468,11 @@ Tensor fanout_scatter_backward_gpu(const Tensor& grad_out, const Tensor& src, co
     const Tensor s_idx = contiguous(src);
     const Tensor d_idx = contiguous(dst);
     hipStream_t stream = current_stream(g);
-    GpuPlan gp = csr_plan(s_idx, x_rows, "src_global_idx", d_idx, g.size(0), "flat_dst", false,
+    PlanPtr gp = csr_plan(s_idx, x_rows, "src_global_idx", d_idx, g.size(0), "flat_dst", false,
                           stream);
     Tensor grad_x = at::empty({x_rows, emb}, grad_out.options());
-    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(g), kModeSum, g);
-    raise_if(relm_mp_plan_segment_reduce(dtype_code(g), &gp.plan, nullptr, g.data_ptr(), emb,
+    Tensor scratch = compute_scratch(gp->plan, emb, dtype_code(g), kModeSum, g);
+    raise_if(relm_mp_plan_segment_reduce(dtype_code(g), &gp->plan, nullptr, g.data_ptr(), emb,
                                          kModeSum, grad_x.data_ptr(), scratch.data_ptr(),
                                          static_cast<size_t>(scratch.numel()), stream));
     return grad_x;
@@ -496,24 +502,10 @@ void fanout_scatter_into_gpu(const Tensor& x_cat, const Tensor& src, const Tenso
     hipStream_t stream = current_stream(x);
     char* base = static_cast<char*>(out.data_ptr()) + col_offset * out.element_size();
     const int64_t stride = line_stride(out);
-    PlanCache& cache = PlanCache::get();
-    GpuPlan gp;
-    if (cache.lookup(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), &gp.plan, stream)) {
-        raise_if(relm_mp_plan_gather_last_grouped(dtype_code(x), &gp.plan, s_idx.data_ptr<int64_t>(),
-                                                  x.data_ptr(), emb, slots, stride, base, stream));
-        return;
-    }
-    gp.mem = byte_buffer(relm_mp_inv_plan_bytes(out_rows), d_idx);
-    raise_if(relm_mp_inv_plan_build_async(d_idx.data_ptr<int64_t>(), out_rows, "flat_dst",
-                                          s_idx.data_ptr<int64_t>(), x.size(0), "src_global_idx", 1,
-                                          d_idx.numel(), gp.mem.data_ptr(),
-                                          static_cast<size_t>(gp.mem.numel()), &gp.plan, stream));
-    const int rc = relm_mp_plan_gather_last_grouped(dtype_code(x), &gp.plan,
-                                                    s_idx.data_ptr<int64_t>(), x.data_ptr(), emb,
-                                                    slots, stride, base, stream);
-    raise_if(relm_mp_plan_validate(&gp.plan));
-    raise_if(rc);
-    cache.insert(kRoleInverse, d_idx, s_idx, out_rows, x.size(0), gp.mem, gp.plan);
+    fanout_inverse(d_idx, out_rows, s_idx, x.size(0), stream, [&](const relm_mp_plan& plan) {
+        return relm_mp_plan_gather_last_grouped(dtype_code(x), &plan, s_idx.data_ptr<int64_t>(),
+                                                x.data_ptr(), emb, slots, stride, base, stream);
+    });
 }
 
 Tensor fanout_scatter_backward_from_gpu(const Tensor& grad, const Tensor& src, const Tensor& dst,
@@ -527,18 +519,20 @@ Tensor fanout_scatter_backward_from_gpu(const Tensor& grad, const Tensor& src, c
     const Tensor d_idx = contiguous(dst);
     const int64_t rows = g.size(0) * slots;
     hipStream_t stream = current_stream(g);
-    GpuPlan gp = csr_plan(s_idx, x_rows, "src_global_idx", d_idx, rows, "flat_dst", false, stream);
+    PlanPtr gp = csr_plan(s_idx, x_rows, "src_global_idx", d_idx, rows, "flat_dst", false, stream);
     Tensor grad_x = at::empty({x_rows, emb}, grad.options());
-    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(g), kModeSum, g);
+    Tensor scratch = compute_scratch(gp->plan, emb, dtype_code(g), kModeSum, g);
     const char* base = static_cast<const char*>(g.data_ptr()) + col_offset * g.element_size();
-    raise_if(relm_mp_plan_segment_sum_grouped(dtype_code(g), &gp.plan, base, rows, emb, slots,
+    raise_if(relm_mp_plan_segment_sum_grouped(dtype_code(g), &gp->plan, base, rows, emb, slots,
                                               line_stride(g), grad_x.data_ptr(), scratch.data_ptr(),
                                               static_cast<size_t>(scratch.numel()), stream));
     return grad_x;
 }
 
+// fanin_reduce on the GPU; *plan_out (if given) receives the forward's CSR
+// plan (keys dst_idx, gathers flat_src) for the backward.
 Tensor fanin_reduce_gpu(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
-                        int64_t dim_size, int64_t mode) {
+                        int64_t dim_size, int64_t mode, PlanPtr* plan_out = nullptr) {
     c10::OptionalDeviceGuard guard(rel_flat.device());
     check_same_gpu(rel_flat, flat_src, "rel_flat", "flat_src");
     check_same_gpu(rel_flat, dst_idx, "rel_flat", "dst_idx");
@@ -552,17 +546,34 @@ Tensor fanin_reduce_gpu(const Tensor& rel_flat, const Tensor& flat_src, const Te
     const Tensor s_idx = contiguous(flat_src);
     const Tensor d_idx = contiguous(dst_idx);
     hipStream_t stream = current_stream(rel);
-    GpuPlan gp = csr_plan(d_idx, dim_size, "dst_idx", s_idx, rel.size(0), "flat_src", true, stream);
+    PlanPtr gp = csr_plan(d_idx, dim_size, "dst_idx", s_idx, rel.size(0), "flat_src", true, stream);
     Tensor out = at::empty({dim_size, emb}, rel_flat.options());
-    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(rel), mode, rel);
-    raise_if(relm_mp_plan_segment_reduce(dtype_code(rel), &gp.plan, nullptr, rel.data_ptr(), emb,
+    Tensor scratch = compute_scratch(gp->plan, emb, dtype_code(rel), mode, rel);
+    raise_if(relm_mp_plan_segment_reduce(dtype_code(rel), &gp->plan, nullptr, rel.data_ptr(), emb,
                                          mode, out.data_ptr(), scratch.data_ptr(),
                                          static_cast<size_t>(scratch.numel()), stream));
+    if (plan_out != nullptr) *plan_out = gp;
     return out;
 }
 
+// The forward's CSR plan for a fanin backward: the plan handed over by the
+// autograd function when it fits these indices (a handoff within one call's
+// graph: not compared again), else a cached plan of equal indices.  Null if
+// neither exists.
+PlanPtr fanin_forward_plan(const PlanRef* handoff, const Tensor& d_idx, const Tensor& s_idx,
+                           int64_t dim_size, hipStream_t stream) {
+    if (handoff != nullptr && handoff->defined() && handoff->role == kRoleCsr &&
+        handoff->device == d_idx.get_device() && handoff->plan.num_edges == d_idx.numel() &&
+        handoff->key_bound == dim_size) {
+        handoff->use_on(stream);
+        return PlanPtr::reclaim_copy(const_cast<PlanRef*>(handoff));
+    }
+    return PlanCache::get().lookup(kRoleCsr, d_idx, &s_idx, dim_size, -1, stream);
+}
+
 Tensor fanin_reduce_sum_backward_gpu(const Tensor& grad_out, const Tensor& flat_src,
-                                     const Tensor& dst_idx, int64_t rel_rows) {
+                                     const Tensor& dst_idx, int64_t rel_rows,
+                                     const PlanRef* handoff = nullptr) {
     c10::OptionalDeviceGuard guard(grad_out.device());
     check_same_gpu(grad_out, flat_src, "grad_out", "flat_src");
     check_same_gpu(grad_out, dst_idx, "grad_out", "dst_idx");
@@ -576,25 +587,24 @@ Tensor fanin_reduce_sum_backward_gpu(const Tensor& grad_out, const Tensor& flat_
     Tensor grad_rel = at::empty({rel_rows, emb}, grad_out.options());
     // The forward's plan (keys dst_idx, gathers flat_src, validated) serves
     // directly when flat_src is the identity.
-    relm_mp_plan fwd{};
-    if (PlanCache::get().lookup_csr_any_gather_bound(d_idx, s_idx, g.size(0), &fwd) &&
-        fwd.gather_identity != 0 && fwd.num_edges <= rel_rows) {
-        raise_if(relm_mp_plan_fanin_backward_by_dst(dtype_code(g), &fwd, d_idx.data_ptr<int64_t>(),
-                                                    kModeSum, g.data_ptr(),
-                                                    nullptr, nullptr, emb, grad_rel.data_ptr(),
-                                                    rel_rows, stream));
+    const PlanPtr fwd = fanin_forward_plan(handoff, d_idx, s_idx, g.size(0), stream);
+    if (fwd && fwd->plan.gather_identity != 0 && fwd->plan.num_edges <= rel_rows) {
+        raise_if(relm_mp_plan_fanin_backward_by_dst(dtype_code(g), &fwd->plan,
+                                                    d_idx.data_ptr<int64_t>(), kModeSum,
+                                                    g.data_ptr(), nullptr, nullptr, emb,
+                                                    grad_rel.data_ptr(), rel_rows, stream));
         return grad_rel;
     }
-    GpuPlan inv = inverse_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false,
+    PlanPtr inv = inverse_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false,
                                stream);
-    if (inv.plan.collisions == 0) {
-        raise_if(relm_mp_plan_gather_last(dtype_code(g), &inv.plan, d_idx.data_ptr<int64_t>(),
+    if (inv->plan.collisions == 0) {
+        raise_if(relm_mp_plan_gather_last(dtype_code(g), &inv->plan, d_idx.data_ptr<int64_t>(),
                                           g.data_ptr(), emb, grad_rel.data_ptr(), stream));
         return grad_rel;
     }
-    GpuPlan gp = csr_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false, stream);
-    Tensor scratch = compute_scratch(gp.plan, emb, dtype_code(g), kModeSum, g);
-    raise_if(relm_mp_plan_segment_reduce(dtype_code(g), &gp.plan, nullptr, g.data_ptr(), emb,
+    PlanPtr gp = csr_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false, stream);
+    Tensor scratch = compute_scratch(gp->plan, emb, dtype_code(g), kModeSum, g);
+    raise_if(relm_mp_plan_segment_reduce(dtype_code(g), &gp->plan, nullptr, g.data_ptr(), emb,
                                          kModeSum, grad_rel.data_ptr(), scratch.data_ptr(),
                                          static_cast<size_t>(scratch.numel()), stream));
     return grad_rel;
@@ -602,7 +612,8 @@ Tensor fanin_reduce_sum_backward_gpu(const Tensor& grad_out, const Tensor& flat_
 
 Tensor fanin_reduce_logsumexp_backward_gpu(const Tensor& grad_out, const Tensor& rel_flat,
                                            const Tensor& flat_src, const Tensor& dst_idx,
-                                           const Tensor& out, int64_t rel_rows) {
+                                           const Tensor& out, int64_t rel_rows,
+                                           const PlanRef* handoff = nullptr) {
     c10::OptionalDeviceGuard guard(grad_out.device());
     check_same_gpu(grad_out, rel_flat, "grad_out", "rel_flat");
     check_same_gpu(grad_out, flat_src, "grad_out", "flat_src");
@@ -612,7 +623,6 @@ Tensor fanin_reduce_logsumexp_backward_gpu(const Tensor& grad_out, const Tensor&
                     grad_out.scalar_type() == out.scalar_type(),
                 "grad_out, rel_flat, and out must share dtype.");
     const int64_t emb = grad_out.size(1);
-    Tensor grad_rel = at::zeros({0, emb}, rel_flat.options());
     if (flat_src.numel() == 0 || rel_rows == 0 || emb == 0)
         return at::zeros({rel_rows, emb}, rel_flat.options());
     const Tensor g = contiguous(grad_out);
@@ -624,29 +634,28 @@ Tensor fanin_reduce_logsumexp_backward_gpu(const Tensor& grad_out, const Tensor&
     // A message row is read from rel_flat and written to grad_rel, so flat_src
     // must index both; rows beyond rel_flat cannot receive a gradient.
     const int64_t key_bound = std::min<int64_t>(rel_rows, rel.size(0));
-    grad_rel = at::empty({rel_rows, emb}, rel_flat.options());
+    Tensor grad_rel = at::empty({rel_rows, emb}, rel_flat.options());
     const int dt = dtype_code(rel);
-    relm_mp_plan fwd{};
-    if (PlanCache::get().lookup_csr_any_gather_bound(d_idx, s_idx, g.size(0), &fwd) &&
-        fwd.gather_identity != 0 && fwd.num_edges <= key_bound) {
-        raise_if(relm_mp_plan_fanin_backward_by_dst(dt, &fwd, d_idx.data_ptr<int64_t>(),
+    const PlanPtr fwd = fanin_forward_plan(handoff, d_idx, s_idx, g.size(0), stream);
+    if (fwd && fwd->plan.gather_identity != 0 && fwd->plan.num_edges <= key_bound) {
+        raise_if(relm_mp_plan_fanin_backward_by_dst(dt, &fwd->plan, d_idx.data_ptr<int64_t>(),
                                                     kModeLogSumExp, g.data_ptr(), o.data_ptr(),
                                                     rel.data_ptr(), emb, grad_rel.data_ptr(),
                                                     rel_rows, stream));
         return grad_rel;
     }
     if (key_bound < rel_rows) grad_rel.narrow(0, key_bound, rel_rows - key_bound).zero_();
-    GpuPlan inv = inverse_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true,
+    PlanPtr inv = inverse_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true,
                                stream);
-    if (inv.plan.collisions == 0) {
-        raise_if(relm_mp_plan_logsumexp_backward(dt, &inv.plan, d_idx.data_ptr<int64_t>(),
+    if (inv->plan.collisions == 0) {
+        raise_if(relm_mp_plan_logsumexp_backward(dt, &inv->plan, d_idx.data_ptr<int64_t>(),
                                                  g.data_ptr(), o.data_ptr(), rel.data_ptr(), emb,
                                                  grad_rel.data_ptr(), nullptr, 0, stream));
         return grad_rel;
     }
-    GpuPlan gp = csr_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true, stream);
-    Tensor scratch = compute_scratch(gp.plan, emb, dt, kModeSum, g);
-    raise_if(relm_mp_plan_logsumexp_backward(dt, &gp.plan, nullptr, g.data_ptr(), o.data_ptr(),
+    PlanPtr gp = csr_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true, stream);
+    Tensor scratch = compute_scratch(gp->plan, emb, dt, kModeSum, g);
+    raise_if(relm_mp_plan_logsumexp_backward(dt, &gp->plan, nullptr, g.data_ptr(), o.data_ptr(),
                                              rel.data_ptr(), emb, grad_rel.data_ptr(),
                                              scratch.data_ptr(),
                                              static_cast<size_t>(scratch.numel()), stream));
@@ -845,12 +854,12 @@ Tensor fanout_scatter_backward_from(const Tensor& grad, const Tensor& src_global
 }
 
 Tensor fanin_reduce_sum(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
-                        int64_t dim_size) {
+                        int64_t dim_size, PlanPtr* plan_out) {
     const int64_t emb = rel_flat.size(1);
     if (flat_src.numel() == 0 || dim_size == 0)
         return at::zeros({dim_size, emb}, rel_flat.options());
     if (all_gpu({&rel_flat, &flat_src, &dst_idx}) && is_fastpath_dtype(rel_flat.scalar_type()))
-        return fanin_reduce_gpu(rel_flat, flat_src, dst_idx, dim_size, kModeSum);
+        return fanin_reduce_gpu(rel_flat, flat_src, dst_idx, dim_size, kModeSum, plan_out);
     Tensor out = at::zeros({dim_size, emb}, rel_flat.options());
     if (all_cpu({&rel_flat, &flat_src, &dst_idx}) && is_fastpath_dtype(rel_flat.scalar_type())) {
         cpu_lane(rel_flat, flat_src, "flat_src", dst_idx, "dst_idx", true, out, true);
@@ -861,26 +870,33 @@ Tensor fanin_reduce_sum(const Tensor& rel_flat, const Tensor& flat_src, const Te
 }
 
 Tensor fanin_reduce_logsumexp(const Tensor& rel_flat, const Tensor& flat_src,
-                              const Tensor& dst_idx, int64_t dim_size) {
+                              const Tensor& dst_idx, int64_t dim_size, PlanPtr* plan_out) {
     if (all_gpu({&rel_flat, &flat_src, &dst_idx}) && is_fastpath_dtype(rel_flat.scalar_type()))
-        return fanin_reduce_gpu(rel_flat, flat_src, dst_idx, dim_size, kModeLogSumExp);
+        return fanin_reduce_gpu(rel_flat, flat_src, dst_idx, dim_size, kModeLogSumExp, plan_out);
     return fanin_logsumexp_aten(rel_flat, flat_src, dst_idx, dim_size);
 }
 
-Tensor fanin_reduce(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
-                    int64_t dim_size, int64_t mode) {
+Tensor fanin_reduce_impl(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
+                         int64_t dim_size, int64_t mode, PlanPtr* plan_out) {
     check_rank(rel_flat, 2, "rel_flat");
     check_int64_index(flat_src, "flat_src");
     check_int64_index(dst_idx, "dst_idx");
     TORCH_CHECK(flat_src.size(0) == dst_idx.size(0), "flat_src and dst_idx must have equal length.");
     TORCH_CHECK(dim_size >= 0, "dim_size must be >= 0.");
-    if (mode == kModeSum) return fanin_reduce_sum(rel_flat, flat_src, dst_idx, dim_size);
-    if (mode == kModeLogSumExp) return fanin_reduce_logsumexp(rel_flat, flat_src, dst_idx, dim_size);
+    if (mode == kModeSum) return fanin_reduce_sum(rel_flat, flat_src, dst_idx, dim_size, plan_out);
+    if (mode == kModeLogSumExp)
+        return fanin_reduce_logsumexp(rel_flat, flat_src, dst_idx, dim_size, plan_out);
     throw std::invalid_argument("Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
 }
 
-Tensor fanin_reduce_sum_backward(const Tensor& grad_out, const Tensor& flat_src,
-                                 const Tensor& dst_idx, int64_t rel_rows) {
+Tensor fanin_reduce(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
+                    int64_t dim_size, int64_t mode) {
+    return fanin_reduce_impl(rel_flat, flat_src, dst_idx, dim_size, mode, nullptr);
+}
+
+Tensor fanin_reduce_sum_backward_impl(const Tensor& grad_out, const Tensor& flat_src,
+                                      const Tensor& dst_idx, int64_t rel_rows,
+                                      const PlanRef* handoff) {
     check_rank(grad_out, 2, "grad_out");
     check_int64_index(flat_src, "flat_src");
     check_int64_index(dst_idx, "dst_idx");
@@ -890,7 +906,7 @@ Tensor fanin_reduce_sum_backward(const Tensor& grad_out, const Tensor& flat_src,
     if (flat_src.numel() == 0 || rel_rows == 0)
         return at::zeros({rel_rows, emb}, grad_out.options());
     if (all_gpu({&grad_out, &flat_src, &dst_idx}) && is_fastpath_dtype(grad_out.scalar_type()))
-        return fanin_reduce_sum_backward_gpu(grad_out, flat_src, dst_idx, rel_rows);
+        return fanin_reduce_sum_backward_gpu(grad_out, flat_src, dst_idx, rel_rows, handoff);
     Tensor grad_rel = at::zeros({rel_rows, emb}, grad_out.options());
     if (all_cpu({&grad_out, &flat_src, &dst_idx}) && is_fastpath_dtype(grad_out.scalar_type())) {
         // mp_ops.cpp:2888-2911: flat_src (write side) is checked before dst_idx.
@@ -901,9 +917,10 @@ Tensor fanin_reduce_sum_backward(const Tensor& grad_out, const Tensor& flat_src,
     return grad_rel;
 }
 
-Tensor fanin_reduce_logsumexp_backward(const Tensor& grad_out, const Tensor& rel_flat,
-                                       const Tensor& flat_src, const Tensor& dst_idx,
-                                       const Tensor& out, int64_t rel_rows) {
+Tensor fanin_reduce_logsumexp_backward_impl(const Tensor& grad_out, const Tensor& rel_flat,
+                                            const Tensor& flat_src, const Tensor& dst_idx,
+                                            const Tensor& out, int64_t rel_rows,
+                                            const PlanRef* handoff) {
     check_rank(grad_out, 2, "grad_out");
     check_rank(rel_flat, 2, "rel_flat");
     check_int64_index(flat_src, "flat_src");
@@ -921,8 +938,47 @@ Tensor fanin_reduce_logsumexp_backward(const Tensor& grad_out, const Tensor& rel
     if (all_gpu({&grad_out, &rel_flat, &flat_src, &dst_idx, &out}) &&
         is_fastpath_dtype(grad_out.scalar_type()))
         return fanin_reduce_logsumexp_backward_gpu(grad_out, rel_flat, flat_src, dst_idx, out,
-                                                   rel_rows);
+                                                   rel_rows, handoff);
     return fanin_logsumexp_backward_aten(grad_out, rel_flat, flat_src, dst_idx, out, rel_rows);
+}
+
+Tensor fanin_reduce_sum_backward(const Tensor& grad_out, const Tensor& flat_src,
+                                 const Tensor& dst_idx, int64_t rel_rows) {
+    return fanin_reduce_sum_backward_impl(grad_out, flat_src, dst_idx, rel_rows, nullptr);
+}
+
+Tensor fanin_reduce_logsumexp_backward(const Tensor& grad_out, const Tensor& rel_flat,
+                                       const Tensor& flat_src, const Tensor& dst_idx,
+                                       const Tensor& out, int64_t rel_rows) {
+    return fanin_reduce_logsumexp_backward_impl(grad_out, rel_flat, flat_src, dst_idx, out,
+                                                rel_rows, nullptr);
+}
+
+// No reference counterpart: fanin_reduce together with the index plan it ran
+// on (an empty PlanRef on the CPU lanes), and the backward ops taking that
+// plan, so that the autograd function of the facade hands the forward's plan
+// to the backward of the same call without a cache lookup.
+std::tuple<Tensor, PlanPtr> fanin_reduce_planned(const Tensor& rel_flat, const Tensor& flat_src,
+                                                 const Tensor& dst_idx, int64_t dim_size,
+                                                 int64_t mode) {
+    PlanPtr plan;
+    Tensor out = fanin_reduce_impl(rel_flat, flat_src, dst_idx, dim_size, mode, &plan);
+    if (!plan) plan = c10::make_intrusive<PlanRef>();
+    return std::make_tuple(out, plan);
+}
+
+Tensor fanin_reduce_sum_backward_planned(const Tensor& grad_out, const Tensor& flat_src,
+                                         const Tensor& dst_idx, int64_t rel_rows,
+                                         const PlanPtr& plan) {
+    return fanin_reduce_sum_backward_impl(grad_out, flat_src, dst_idx, rel_rows, plan.get());
+}
+
+Tensor fanin_reduce_logsumexp_backward_planned(const Tensor& grad_out, const Tensor& rel_flat,
+                                               const Tensor& flat_src, const Tensor& dst_idx,
+                                               const Tensor& out, int64_t rel_rows,
+                                               const PlanPtr& plan) {
+    return fanin_reduce_logsumexp_backward_impl(grad_out, rel_flat, flat_src, dst_idx, out,
+                                                rel_rows, plan.get());
 }
 
 // ---- pack ops (mp_ops.cpp:412-570, 2511-2772) --------------------------------
@@ -1273,10 +1329,10 @@ Tensor lgan_aggregate_gpu(const Tensor& src_rows, const Tensor& s, const Tensor&
                                     ptr_or_null(base), dim, D, out.data_ptr(), st));
         return out;
     }
-    GpuPlan gp = csr_plan(t, dim, t_name, s, src_rows.size(0), s_name, true, st);
-    Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, src_rows);
+    PlanPtr gp = csr_plan(t, dim, t_name, s, src_rows.size(0), s_name, true, st);
+    Tensor scratch = compute_scratch(gp->plan, D, dt, kModeSum, src_rows);
     raise_if(relm_mp_plan_segment_sum_scaled(
-        dt, &gp.plan, src_rows.data_ptr(), D,
+        dt, &gp->plan, src_rows.data_ptr(), D,
         mode == kModeMean ? RELM_MP_DIV_SEGMENT : RELM_MP_DIV_NONE, nullptr, ptr_or_null(base),
         out.data_ptr(), scratch.data_ptr(), static_cast<size_t>(scratch.numel()), st));
     return out;
@@ -1299,15 +1355,15 @@ Tensor lgan_reverse_gpu(const Tensor& grad, const Tensor& s, const Tensor& t, in
     Tensor table = grad;
     if (mode == kModeMean) {
         // message counts per grad row: the segment sizes of the forward's plan
-        GpuPlan fwd = csr_plan(t, grad.size(0), t_name, s, src_rows, s_name, true, st);
+        PlanPtr fwd = csr_plan(t, grad.size(0), t_name, s, src_rows, s_name, true, st);
         table = at::empty_like(grad);
         raise_if(relm_mp_rows_scale(dt, grad.data_ptr(), nullptr, RELM_MP_DIV_SEGMENT,
-                                    fwd.plan.offsets, nullptr, nullptr, grad.size(0), D,
+                                    fwd->plan.offsets, nullptr, nullptr, grad.size(0), D,
                                     table.data_ptr(), st));
     }
-    GpuPlan gp = csr_plan(s, src_rows, s_name, t, grad.size(0), t_name, false, st);
-    Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, grad);
-    raise_if(relm_mp_plan_segment_sum_scaled(dt, &gp.plan, table.data_ptr(), D, RELM_MP_DIV_NONE,
+    PlanPtr gp = csr_plan(s, src_rows, s_name, t, grad.size(0), t_name, false, st);
+    Tensor scratch = compute_scratch(gp->plan, D, dt, kModeSum, grad);
+    raise_if(relm_mp_plan_segment_sum_scaled(dt, &gp->plan, table.data_ptr(), D, RELM_MP_DIV_NONE,
                                              nullptr, ptr_or_null(base), out.data_ptr(),
                                              scratch.data_ptr(),
                                              static_cast<size_t>(scratch.numel()), st));
@@ -1386,12 +1442,12 @@ std::tuple<Tensor, Tensor, Tensor> lgan_pool_reduce(
         Tensor rpx = pooled ? at::empty({K, D}, slot.options()) : at::zeros({K, D}, slot.options());
         if (pooled) {
             const Tensor s2r = index64(slot_to_relation_instance);
-            GpuPlan gp = csr_plan_rows(s2r, K, "slot_to_relation_instance", st);
+            PlanPtr gp = csr_plan_rows(s2r, K, "slot_to_relation_instance", st);
             const int dt = dtype_code(slot);
-            Tensor scratch = compute_scratch(gp.plan, D, dt, kModeSum, slot);
+            Tensor scratch = compute_scratch(gp->plan, D, dt, kModeSum, slot);
             const Tensor arity = contiguous(relation_instance_arities);
             raise_if(relm_mp_plan_segment_sum_scaled(
-                dt, &gp.plan, slot.data_ptr(), D, RELM_MP_DIV_VALUES, arity.data_ptr<int64_t>(),
+                dt, &gp->plan, slot.data_ptr(), D, RELM_MP_DIV_VALUES, arity.data_ptr<int64_t>(),
                 nullptr, rpx.data_ptr(), scratch.data_ptr(), static_cast<size_t>(scratch.numel()),
                 st));
         }
@@ -1552,6 +1608,11 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("fanout_scatter_into(Tensor x_cat, Tensor src_global_idx, Tensor flat_dst, Tensor(a!) out, int col_offset, int slots) -> ()");
     m.def("fanout_scatter_backward_from(Tensor grad, Tensor src_global_idx, Tensor flat_dst, int x_rows, int col_offset, int slots, int emb) -> Tensor");
     m.def("build_info() -> str");
+    // No reference counterpart: the forward's index plan handed to the backward.
+    m.class_<relm_amd::PlanRef>("PlanRef");
+    m.def("fanin_reduce_planned(Tensor rel_flat, Tensor flat_src, Tensor dst_idx, int dim_size, int mode) -> (Tensor, __torch__.torch.classes.relm_mp.PlanRef)");
+    m.def("fanin_reduce_sum_backward_planned(Tensor grad_out, Tensor flat_src, Tensor dst_idx, int rel_rows, __torch__.torch.classes.relm_mp.PlanRef plan) -> Tensor");
+    m.def("fanin_reduce_logsumexp_backward_planned(Tensor grad_out, Tensor rel_flat, Tensor flat_src, Tensor dst_idx, Tensor out, int rel_rows, __torch__.torch.classes.relm_mp.PlanRef plan) -> Tensor");
     // No reference counterpart: control of the index-plan cache.
     m.def("plan_cache_clear() -> ()");
     m.def("plan_cache_size() -> int");
@@ -1575,6 +1636,10 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("fanout_scatter_into", relm_amd::fanout_scatter_into);
     m.impl("fanout_scatter_backward_from", relm_amd::fanout_scatter_backward_from);
     m.impl("build_info", relm_amd::build_info);
+    m.impl("fanin_reduce_planned", relm_amd::fanin_reduce_planned);
+    m.impl("fanin_reduce_sum_backward_planned", relm_amd::fanin_reduce_sum_backward_planned);
+    m.impl("fanin_reduce_logsumexp_backward_planned",
+           relm_amd::fanin_reduce_logsumexp_backward_planned);
     m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
     m.impl("plan_cache_size", relm_amd::plan_cache_size);
     m.impl("plan_cache_stats", relm_amd::plan_cache_stats);

@@ -5,7 +5,7 @@ dispatch (``src/relmo/ops/mp.py:43-70``): modes other than sum (0) and
 logsumexp (1) go to the ATen fallback, which raises ``ValueError``; otherwise
 the custom ops run through autograd Functions unless the policy selects the
 fallback.  The four pack ops (``mp.py:73-146``) call ``torch.ops.relm_mp``
-directly, or their ATen fallbacks, through ``dispatch_namespace_op``.  The
+directly, or their ATen fallbacks, as ``mp_dispatch.run_op`` routes them.  The
 LGAN reductions (``_lgan_pool_reduce``, ``_lgan_relation_graph_step``,
 ``mp.py:394-525``) run the custom ops for CUDA tensors and their ATen fallbacks
 otherwise.
@@ -22,7 +22,7 @@ from .mp_autograd import (
     _LGANRelationGraphStepFunction,
 )
 from .mp_constants import MODE_LOGSUMEXP, MODE_MEAN, MODE_SUM, activation_code
-from .mp_dispatch import dispatch_namespace_op, should_use_custom, use_custom_namespace_op
+from .mp_dispatch import library_op, library_ready, run_op
 from .mp_pack import (
     fanin_pack_from_edges_python,
     fanin_pack_multi_python,
@@ -34,6 +34,12 @@ from .mp_pack import (
 from .mp_runtime import TORCH_IMPORT_ERROR, assert_runtime_compat, available, require_torch, torch
 
 
+def _first(parts):
+    """The tensor whose device sets the fallback policy of a pack op."""
+
+    return parts[0] if parts else None
+
+
 def fanout_scatter(
     x_cat: torch.Tensor,
     src_global_idx: torch.Tensor,
@@ -43,7 +49,7 @@ def fanout_scatter(
     """``out[flat_dst[e]] = x_cat[src_global_idx[e]]``; other rows are zero."""
 
     require_torch("fanout_scatter")
-    if should_use_custom("fanout_scatter"):
+    if library_ready("fanout_scatter", x_cat):
         return _FanoutScatterFunction.apply(x_cat, src_global_idx, flat_dst, int(out_rows))
     return fanout_scatter_python(x_cat, src_global_idx, flat_dst, int(out_rows))
 
@@ -67,7 +73,7 @@ def fanout_concat(
 
     require_torch("fanout_concat")
     slots = int(slots)
-    if use_custom_namespace_op("fanout_scatter_into"):
+    if library_op("fanout_scatter_into", tensor=x_cat) is not None:
         return _FanoutConcatFunction.apply(prefix, x_cat, src_global_idx, flat_dst, slots)
     nodes = int(prefix.size(0))
     args = fanout_scatter(x_cat, src_global_idx, flat_dst, nodes * slots)
@@ -87,7 +93,7 @@ def fanin_reduce(
     mode = int(mode)
     if mode not in (MODE_SUM, MODE_LOGSUMEXP):
         return fanin_reduce_python(rel_flat, flat_src, dst_idx, int(dim_size), mode)
-    if should_use_custom("fanin_reduce"):
+    if library_ready("fanin_reduce", rel_flat):
         fn = _FaninReduceSumFunction if mode == MODE_SUM else _FaninReduceLogSumExpFunction
         return fn.apply(rel_flat, flat_src, dst_idx, int(dim_size))
     return fanin_reduce_python(rel_flat, flat_src, dst_idx, int(dim_size), mode)
@@ -101,9 +107,9 @@ def fanout_pack_multi(
     """Concatenate source parts for one ``fanout_scatter``: ``(x_cat, src_global_idx, flat_dst)``."""
 
     require_torch("fanout_pack_multi")
-    return dispatch_namespace_op(
+    return run_op(
         "fanout_pack_multi", x_parts, src_idx_parts, flat_dst_parts,
-        fallback=fanout_pack_multi_python,
+        fallback=fanout_pack_multi_python, tensor=_first(x_parts),
     )
 
 
@@ -115,9 +121,9 @@ def fanin_pack_multi(
     """Concatenate relation parts for one ``fanin_reduce``: ``(rel_flat, flat_src, dst_idx)``."""
 
     require_torch("fanin_pack_multi")
-    return dispatch_namespace_op(
+    return run_op(
         "fanin_pack_multi", rel_parts, flat_src_parts, dst_idx_parts,
-        fallback=fanin_pack_multi_python,
+        fallback=fanin_pack_multi_python, tensor=_first(rel_parts),
     )
 
 
@@ -133,10 +139,10 @@ def fanout_pack_from_edges(
     """Fanout operands from per-relation edge lists: ``flat_dst = slot_offset + dst * arity + pos``."""
 
     require_torch("fanout_pack_from_edges")
-    return dispatch_namespace_op(
+    return run_op(
         "fanout_pack_from_edges", x_parts, edge_src_parts, edge_dst_parts, src_part_ids,
         arity_parts, pos_parts, slot_offset_parts,
-        fallback=fanout_pack_from_edges_python,
+        fallback=fanout_pack_from_edges_python, tensor=_first(x_parts),
     )
 
 
@@ -153,10 +159,10 @@ def fanin_pack_from_edges(
     or ``src`` (mode 1), plus the part's row offset."""
 
     require_torch("fanin_pack_from_edges")
-    return dispatch_namespace_op(
+    return run_op(
         "fanin_pack_from_edges", rel_parts, edge_src_parts, edge_dst_parts, rel_part_ids,
         arity_parts, pos_parts, int(mode),
-        fallback=fanin_pack_from_edges_python,
+        fallback=fanin_pack_from_edges_python, tensor=_first(rel_parts),
     )
 
 

@@ -3,15 +3,23 @@
 The forward passes save what relmo's ``src/relmo/ops/mp_autograd.py:110-191``
 saves (index tensors and row counts; the logsumexp also keeps ``rel_flat`` and
 its output) and the backward passes call the explicit ``*_backward`` ops, so
-both directions run on the custom library.  The index tensors reach the
-backward as the same tensor objects, which lets the library reuse the index
-plan it built in the forward.
+both directions run on the custom library.  The fanin functions also keep the
+index plan the forward ran on (``fanin_reduce_planned``, an opaque
+``torch.classes.relm_mp.PlanRef``) and hand it to the backward op of the same
+call, which then needs neither a new plan nor a cache lookup.
 """
 
 from __future__ import annotations
 
 from .mp_constants import MODE_LOGSUMEXP, MODE_SUM
 from .mp_runtime import ops_namespace, torch
+
+
+def _planned_ops(ns) -> bool:
+    """Whether the loaded library hands index plans from forward to backward."""
+
+    return hasattr(ns, "fanin_reduce_planned")
+
 
 if torch is not None:
 
@@ -30,37 +38,53 @@ if torch is not None:
             )
             return grad_x, None, None, None
 
+    def _fanin_forward(ctx, rel_flat, flat_src, dst_idx, dim_size, mode):
+        ns = ops_namespace()
+        ctx.plan = None
+        if _planned_ops(ns):
+            out, ctx.plan = ns.fanin_reduce_planned(rel_flat, flat_src, dst_idx, int(dim_size), mode)
+            return out
+        return ns.fanin_reduce(rel_flat, flat_src, dst_idx, int(dim_size), mode)
+
     class _FaninReduceSumFunction(torch.autograd.Function):
         @staticmethod
         def forward(ctx, rel_flat, flat_src, dst_idx, dim_size):
             ctx.save_for_backward(flat_src, dst_idx)
             ctx.rel_rows = int(rel_flat.size(0))
-            return ops_namespace().fanin_reduce(rel_flat, flat_src, dst_idx, int(dim_size), MODE_SUM)
+            return _fanin_forward(ctx, rel_flat, flat_src, dst_idx, dim_size, MODE_SUM)
 
         @staticmethod
         def backward(ctx, grad_out):
             flat_src, dst_idx = ctx.saved_tensors
-            grad_rel = ops_namespace().fanin_reduce_sum_backward(
-                grad_out, flat_src, dst_idx, ctx.rel_rows
-            )
+            ns = ops_namespace()
+            if ctx.plan is not None:
+                grad_rel = ns.fanin_reduce_sum_backward_planned(
+                    grad_out, flat_src, dst_idx, ctx.rel_rows, ctx.plan
+                )
+            else:
+                grad_rel = ns.fanin_reduce_sum_backward(grad_out, flat_src, dst_idx, ctx.rel_rows)
             return grad_rel, None, None, None
 
     class _FaninReduceLogSumExpFunction(torch.autograd.Function):
         @staticmethod
         def forward(ctx, rel_flat, flat_src, dst_idx, dim_size):
             ctx.rel_rows = int(rel_flat.size(0))
-            out = ops_namespace().fanin_reduce(
-                rel_flat, flat_src, dst_idx, int(dim_size), MODE_LOGSUMEXP
-            )
+            out = _fanin_forward(ctx, rel_flat, flat_src, dst_idx, dim_size, MODE_LOGSUMEXP)
             ctx.save_for_backward(rel_flat, flat_src, dst_idx, out)
             return out
 
         @staticmethod
         def backward(ctx, grad_out):
             rel_flat, flat_src, dst_idx, out = ctx.saved_tensors
-            grad_rel = ops_namespace().fanin_reduce_logsumexp_backward(
-                grad_out, rel_flat, flat_src, dst_idx, out, ctx.rel_rows
-            )
+            ns = ops_namespace()
+            if ctx.plan is not None:
+                grad_rel = ns.fanin_reduce_logsumexp_backward_planned(
+                    grad_out, rel_flat, flat_src, dst_idx, out, ctx.rel_rows, ctx.plan
+                )
+            else:
+                grad_rel = ns.fanin_reduce_logsumexp_backward(
+                    grad_out, rel_flat, flat_src, dst_idx, out, ctx.rel_rows
+                )
             return grad_rel, None, None, None
 
     class _FanoutConcatFunction(torch.autograd.Function):
@@ -111,11 +135,11 @@ def _zeros_or(grad, rows: int, like):
 
 
 if torch is not None:
-    from .mp_dispatch import use_custom_namespace_op
+    from .mp_dispatch import library_op
     from .mp_fallbacks import lgan_pool_reduce_python, lgan_relation_graph_step_python
 
     def _custom(tensor, op_name: str) -> bool:
-        return use_custom_namespace_op(op_name, tensor=tensor, require_cuda=True)
+        return library_op(op_name, tensor=tensor, gpu_only=True) is not None
 
     def _fallback_grad(fn, x, args, grads):
         with torch.enable_grad():

@@ -1,94 +1,72 @@
-"""Choice between the custom ops and the ATen fallbacks.
+"""Routing of the facade's calls: the ``relm_mp`` library or the ATen fallbacks.
 
-Follows relmo's ``src/relmo/ops/mp_dispatch.py:15-36``: ``RELM_MP_ENABLE=0``
-selects the fallback; otherwise the library is loaded and checked once, and a
-failure either raises (``RELM_MP_FALLBACK=error``, the default here) or falls
-back to ATen (``RELM_MP_FALLBACK=python``).
+Every facade function asks one question, :func:`library_op`: which callable of
+the library serves this op for this tensor, or ``None`` when the fallback runs.
+The answer follows relmo's dispatch policy (``src/relmo/ops/mp_dispatch.py:15-78``),
+whose environment variables and error messages are the contract callers match:
+
+* ``RELM_MP_ENABLE=0`` routes every op to its fallback;
+* otherwise the library is loaded and checked against the running torch once;
+  if that fails, the fallback policy (:func:`mp_runtime.fallback_mode`)
+  either raises ``Custom mp op <name> is unavailable.`` or routes to the
+  fallback;
+* an op the loaded library does not register (the optional pack and LGAN
+  ops) runs its fallback, or raises
+  ``Custom mp op <name> is unavailable in the loaded relm_mp library.`` under
+  the ``error`` policy;
+* ``gpu_only`` ops (the LGAN reductions) run on the library for GPU tensors
+  only.
+
+The policy depends on the tensor: with ``RELM_MP_FALLBACK`` unset, CPU tensors
+fall back quietly as in relmo, GPU tensors raise (a GPU run never drops to
+ATen without saying so).
 """
 
 from __future__ import annotations
 
-from .mp_runtime import (
-    ensure_loaded,
-    ensure_runtime_compat_once,
-    env_bool_any,
-    fallback_mode,
-    ops_namespace,
-    torch,
-)
+from .mp_runtime import ensure_runtime_compat_once, env_bool_any, fallback_mode, ops_namespace
 
 
-def should_use_custom(op_name: str) -> bool:
-    """Whether ``op_name`` runs on the custom op library under the current policy."""
+def _on_gpu(tensor: object | None) -> bool:
+    return bool(getattr(tensor, "is_cuda", False))
+
+
+def library_ready(op_name: str, tensor: object | None = None) -> bool:
+    """Whether the policy lets ``op_name`` run on the library at all.
+
+    Raises ``RuntimeError`` where the library is wanted but unusable and the
+    policy for ``tensor`` is ``error``.
+    """
 
     if not env_bool_any(("RELM_MP_ENABLE",), True):
         return False
     try:
         ensure_runtime_compat_once()
     except Exception as exc:
-        if fallback_mode() == "error":
+        if fallback_mode(tensor) == "error":
             raise RuntimeError(f"Custom mp op {op_name} is unavailable.") from exc
         return False
     return True
 
 
-def namespace_has_op(op_name: str) -> bool:
-    if torch is None:
-        return False
-    try:
-        ensure_loaded()
-    except Exception:
-        return False
-    return hasattr(ops_namespace(), op_name)
+def library_op(op_name: str, *, tensor: object | None = None, gpu_only: bool = False):
+    """The library's ``torch.ops.relm_mp.<op_name>``, or ``None`` where the fallback runs."""
 
-
-def require_available_custom_op(op_name: str) -> None:
-    """Raise under the ``error`` fallback policy: the loaded library lacks ``op_name``."""
-
-    if fallback_mode() == "error":
+    if gpu_only and not _on_gpu(tensor):
+        return None
+    if not library_ready(op_name, tensor):
+        return None
+    op = getattr(ops_namespace(), op_name, None)
+    if op is None and fallback_mode(tensor) == "error":
         raise RuntimeError(f"Custom mp op {op_name} is unavailable in the loaded relm_mp library.")
+    return op
 
 
-def use_custom_namespace_op(
-    op_name: str,
-    *,
-    tensor: object | None = None,
-    require_cuda: bool = False,
-) -> bool:
-    """Whether ``op_name`` is called directly on ``torch.ops.relm_mp``."""
+def run_op(op_name: str, *args, fallback, tensor: object | None = None, gpu_only: bool = False):
+    """``op_name(*args)`` on the library, or ``fallback(*args)`` where the policy says so."""
 
-    if require_cuda and (tensor is None or not bool(getattr(tensor, "is_cuda", False))):
-        return False
-    return should_use_custom(op_name) and namespace_has_op(op_name)
+    op = library_op(op_name, tensor=tensor, gpu_only=gpu_only)
+    return fallback(*args) if op is None else op(*args)
 
 
-def dispatch_namespace_op(
-    op_name: str,
-    *args,
-    fallback,
-    tensor: object | None = None,
-    require_cuda: bool = False,
-    enforce_fallback_policy: bool = True,
-):
-    """Call ``torch.ops.relm_mp.<op_name>`` or ``fallback`` with ``args``.
-
-    Follows ``src/relmo/ops/mp_dispatch.py:47-81``: the library op when the
-    policy allows it and the library has it; otherwise the fallback, except that
-    under the ``error`` policy a library without the op raises.
-    """
-
-    if use_custom_namespace_op(op_name, tensor=tensor, require_cuda=require_cuda):
-        return getattr(ops_namespace(), op_name)(*args)
-    if enforce_fallback_policy and should_use_custom(op_name):
-        require_available_custom_op(op_name)
-    return fallback(*args)
-
-
-__all__ = [
-    "dispatch_namespace_op",
-    "namespace_has_op",
-    "ops_namespace",
-    "require_available_custom_op",
-    "should_use_custom",
-    "use_custom_namespace_op",
-]
+__all__ = ["library_op", "library_ready", "run_op"]

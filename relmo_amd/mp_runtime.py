@@ -7,10 +7,11 @@ Behaviour follows relmo's ``src/relmo/ops/mp_runtime.py``:
   (mp_runtime.py:21-42);
 * environment flags ``RELM_MP_ENABLE``, ``RELM_MP_FALLBACK`` (``python`` |
   ``error``) and ``RELM_MP_TORCH_VERSION_POLICY`` (``forward`` | ``strict``)
-  keep their meaning (mp_runtime.py:44-69).  One deliberate difference: the
-  default fallback is ``error``, so a GPU run never falls back to ATen
-  silently when the HIP library is missing; ``RELM_MP_FALLBACK=python``
-  restores the reference default;
+  keep their meaning (mp_runtime.py:44-69).  One deliberate difference: with
+  ``RELM_MP_FALLBACK`` unset (or invalid) the policy is relmo's ``python`` for
+  CPU tensors but ``error`` for GPU tensors, so a GPU run never falls back to
+  ATen silently when the HIP library is missing; setting the variable applies
+  it to every tensor, as in relmo;
 * the library is found by globbing ``relm_mp_ops*.so`` / ``librelm_mp_ops*.so``
   in the package directory (mp_runtime.py:97-125), loaded with
   ``torch.ops.load_library`` and must register every op of
@@ -46,7 +47,7 @@ _RUNTIME_COMPAT_VALIDATED = False
 _FALSE_WORDS = frozenset({"0", "false", "no", "off"})
 _MAJOR_MINOR = re.compile(r"^(\d+)\.(\d+)")
 
-DEFAULT_FALLBACK_MODE = "error"
+_FALLBACK_MODES = frozenset({"python", "error"})
 
 
 def require_torch(feature_name: str) -> None:
@@ -77,8 +78,14 @@ def _choice(name: str, allowed: frozenset[str], default: str) -> str:
     return raw if raw in allowed else default
 
 
-def fallback_mode() -> str:
-    return _choice("RELM_MP_FALLBACK", frozenset({"python", "error"}), DEFAULT_FALLBACK_MODE)
+def fallback_mode(tensor: object | None = None) -> str:
+    """``python`` or ``error`` for ops on ``tensor``: ``RELM_MP_FALLBACK`` where it
+    names one of them, else ``error`` for GPU tensors and ``python`` otherwise."""
+
+    raw = env_first(("RELM_MP_FALLBACK",))
+    if raw is not None and raw.strip().lower() in _FALLBACK_MODES:
+        return raw.strip().lower()
+    return "error" if getattr(tensor, "is_cuda", False) else "python"
 
 
 def torch_version_policy() -> str:

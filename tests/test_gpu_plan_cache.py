@@ -1,7 +1,9 @@
-"""GPU tests of plan reuse by index content: the C ABI's relm_mp_index_match
-and the torch binding's plan cache, which serves a plan for new index tensors
-whose contents equal those a cached plan was built from (the same topology
-rebuilt in every forward), and never for different or modified indices."""
+"""GPU tests of plan reuse: the C ABI's relm_mp_plan_match (index arrays against
+the snapshot a plan keeps of the indices it was built from) and the torch
+binding's plan cache, which serves a plan only for index arrays equal to that
+snapshot - for new tensors of equal content (the same topology rebuilt in every
+forward), never for different indices, whether they were changed in place,
+through ``.data`` (no version-counter bump) or on another stream."""
 
 from __future__ import annotations
 
@@ -36,39 +38,54 @@ def _gpu():
 
 
 def _stats() -> dict[str, int]:
-    entries, identity, content, misses = torch.ops.relm_mp.plan_cache_stats()
-    return {"entries": entries, "identity": identity, "content": content, "misses": misses}
+    """Cache counters; "hits" counts every plan served.  Whether a hit counts as
+    "same" (last used with the same tensor objects) or "other" is only the
+    cache's ordering hint: a new tensor can occupy a freed tensor's address."""
+
+    entries, same, other, misses, kept, peak = torch.ops.relm_mp.plan_cache_stats()
+    return {"entries": entries, "same": same, "other": other, "hits": same + other, "misses": misses}
 
 
 def _delta(before: dict, after: dict) -> dict:
     return {k: after[k] - before[k] for k in before}
 
 
-@pytest.mark.parametrize("n", [0, 1, 2047, 2048, 5_000_011])
-def test_index_match_c_abi(n) -> None:
+@pytest.mark.parametrize("n", [0, 1, 4095, 4096, 4097, 5_000_011])
+def test_plan_match_c_abi(n) -> None:
+    """Snapshots of CSR and inverse plans against equal and altered indices:
+    random tiles (stored) and tiles whose gathers are the edge ids (flagged)."""
+
     from relmo_amd import capi
 
     g = torch.Generator(device=DEV)
     g.manual_seed(n)
-    keys = torch.randint(0, 1 << 40, (n,), device=DEV, generator=g)
-    gathers = torch.randint(0, 1 << 40, (n,), device=DEV, generator=g)
-    cands = [(keys.clone(), gathers.clone())]
-    if n > 0:
-        for pos in sorted({0, n // 2, n - 1}):
-            k2 = keys.clone()
-            k2[pos] += 1
-            g2 = gathers.clone()
-            g2[pos] -= 1
-            cands += [(k2, gathers.clone()), (keys.clone(), g2)]
-    cands = cands[:8]
-    _log(f"index_match n={n} candidates={len(cands)}")
-    got = capi.index_match(keys, gathers, cands)
+    K = max(n // 3, 1)
+    keys = torch.randint(0, K, (n,), device=DEV, generator=g)
+    gathers = torch.arange(n, device=DEV)
+    if n > 8192:  # one stored tile in the middle, the others plain
+        gathers[4096:8192] = torch.randint(0, n, (4096,), device=DEV, generator=g)
+    plans = [capi.csr_plan(keys, K, gathers, n),
+             capi.inv_plan(keys, K, gathers, n, snapshot=True)]
     torch.cuda.synchronize()
-    assert got == [bool(torch.equal(k, keys) and torch.equal(gg, gathers)) for k, gg in cands]
-    assert got[0] and (n == 0 or not any(got[1:]))
-    # keys only: candidates whose keys are equal match whatever their gathers
-    got_k = capi.index_match(keys, None, [(k, None) for k, _ in cands])
-    assert got_k == [bool(torch.equal(k, keys)) for k, _ in cands]
+    _log(f"plan_match n={n}")
+    assert capi.plan_match(keys.clone(), gathers.clone(), plans) == [True, True]
+    assert capi.plan_match(keys.clone(), None, plans) == [True, True]
+    if n == 0:
+        return
+    for pos in sorted({0, n // 2, n - 1, min(n - 1, 5000)}):
+        k2 = keys.clone()
+        k2[pos] = (k2[pos] + 1) % (K + 1)
+        g2 = gathers.clone()
+        g2[pos] += 1
+        assert capi.plan_match(k2, gathers, plans) == [False, False], ("key", pos)
+        assert capi.plan_match(keys, g2, plans) == [False, False], ("gather", pos)
+        assert capi.plan_match(keys, None, plans) == [True, True]
+    # another length never matches; a plan without a snapshot is refused
+    if n > 1:
+        assert capi.plan_match(keys[:-1].clone(), gathers[:-1].clone(), plans) == [False, False]
+    bare = capi.inv_plan(keys, K, gathers, n)
+    with pytest.raises(RuntimeError, match="snapshot"):
+        capi.plan_match(keys, gathers, [bare])
 
 
 def _fanin_case(seed: int, K: int = 20_000, E: int = 200_000, D: int = 32):
@@ -82,7 +99,11 @@ def _fanin_case(seed: int, K: int = 20_000, E: int = 200_000, D: int = 32):
     return rel, src, dst, K
 
 
-def test_content_hit_reuses_the_forward_plan(mp_env) -> None:
+def _want_sum(rel, src, dst, K):
+    return oracle.fanin_reduce_sum(rel.cpu().numpy(), src.cpu().numpy(), dst.cpu().numpy(), K)
+
+
+def test_content_hit_for_new_tensors_and_handoff(mp_env) -> None:
     from relmo_amd import mp
 
     ns = torch.ops.relm_mp
@@ -96,8 +117,11 @@ def test_content_hit_reuses_the_forward_plan(mp_env) -> None:
         (grad,) = torch.autograd.grad(out, r, torch.ones_like(out))
         d = _delta(before, _stats())
         _log(f"content cache step {step}: {d}")
-        if step > 0:  # forward CSR plan and backward inverse plan both served by content
-            assert d["content"] == 2 and d["misses"] == 0 and d["entries"] == 0, d
+        # the forward's CSR plan: built once, then served by content; the
+        # backward gets it from the autograd function and builds an inverse
+        # plan (flat_src is a permutation), served by content after step 0
+        if step > 0:
+            assert d["hits"] == 2 and d["misses"] == 0 and d["entries"] == 0, d
         outs.append((out.detach(), grad))
     for out, grad in outs[1:]:
         assert torch.equal(out, outs[0][0]) and torch.equal(grad, outs[0][1])
@@ -119,26 +143,91 @@ def test_content_miss_on_different_indices(mp_env) -> None:
         before = _stats()
         out = mp.fanin_reduce(rel, s2, d2, K, 0)
         d = _delta(before, _stats())
-        assert d["content"] == 0 and d["misses"] >= 1, (name, d)
-        want = oracle.fanin_reduce_sum(rel.cpu().numpy(), s2.cpu().numpy(), d2.cpu().numpy(), K)
-        assert np.array_equal(out.cpu().numpy(), want), name
+        assert d["hits"] == 0 and d["misses"] >= 1, (name, d)
+        assert np.array_equal(out.cpu().numpy(), _want_sum(rel, s2, d2, K)), name
 
 
-def test_content_cache_drops_entries_modified_in_place(mp_env) -> None:
+@pytest.mark.parametrize("how", ["in_place", "data", "raw_pointer"])
+def test_index_written_after_the_build_gets_a_new_plan(mp_env, how) -> None:
+    """The same tensor objects called again after their indices changed: a write
+    that bumps the version counter, one through ``.data`` that does not, and one
+    into the storage by a kernel that autograd never sees (a view created
+    before, written after) - every one must give the new indices' result."""
+
     from relmo_amd import mp
 
     ns = torch.ops.relm_mp
     ns.plan_cache_clear()
     rel, src, dst, K = _fanin_case(3)
-    original = dst.clone()
-    mp.fanin_reduce(rel, src, dst, K, 0)
-    dst.copy_(torch.flip(original, [0]))  # the cached entry's tensor now holds other indices
+    first = mp.fanin_reduce(rel, src, dst, K, 0)
+    assert np.array_equal(first.cpu().numpy(), _want_sum(rel, src, dst, K))
+    new_dst = torch.flip(dst, [0]).contiguous()
+    version = dst._version
+    if how == "in_place":
+        dst.copy_(new_dst)
+        assert dst._version != version
+    elif how == "data":
+        dst.data[:] = new_dst
+        assert dst._version == version  # the hole a version check alone would miss
+    else:
+        alias = torch.from_dlpack(torch.utils.dlpack.to_dlpack(dst.detach()))
+        alias.copy_(new_dst)
+        assert dst._version == version
+    assert torch.equal(dst, new_dst)
     before = _stats()
-    out = mp.fanin_reduce(rel, src, original.clone(), K, 0)
+    out = mp.fanin_reduce(rel, src, dst, K, 0)
     d = _delta(before, _stats())
-    assert d["content"] == 0 and d["identity"] == 0, d
-    want = oracle.fanin_reduce_sum(rel.cpu().numpy(), src.cpu().numpy(), original.cpu().numpy(), K)
-    assert np.array_equal(out.cpu().numpy(), want)
+    _log(f"{how}: {d}")
+    assert d["hits"] == 0 and d["misses"] == 1, d
+    assert np.array_equal(out.cpu().numpy(), _want_sum(rel, src, new_dst, K))
+
+
+def test_raw_schema_backward_finds_the_forward_plan(mp_env) -> None:
+    """The reference's own autograd functions call the plain schemas; the
+    backward then finds the forward's plan by content (the same tensors)."""
+
+    ns = torch.ops.relm_mp
+    ns.plan_cache_clear()
+    rel, _, dst, K = _fanin_case(5)
+    src = torch.arange(rel.size(0), device=DEV)
+    out = ns.fanin_reduce(rel, src, dst, K, 1)
+    g = torch.randn_like(out)
+    before = _stats()
+    got = ns.fanin_reduce_logsumexp_backward(g, rel, src, dst, out, rel.size(0))
+    d = _delta(before, _stats())
+    assert d["hits"] == 1 and d["misses"] == 0, d
+    want = oracle.fanin_reduce_logsumexp_backward(
+        g.cpu().numpy(), rel.cpu().numpy(), src.cpu().numpy(), dst.cpu().numpy(),
+        out.cpu().numpy(), rel.size(0))
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=1e-4, atol=1e-6)
+
+
+def test_plan_built_on_one_stream_reused_on_another(mp_env) -> None:
+    """A plan built on stream A and served on stream B: B waits for A's build
+    (the cached entry is inserted before A has run it) and the plan memory is
+    recorded for B, so dropping the entry while B still works is safe."""
+
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    ns.plan_cache_clear()
+    rel, src, dst, K = _fanin_case(6, K=200_000, E=2_000_000)
+    want = _want_sum(rel, src, dst, K)
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(a):
+        torch.cuda._sleep(20_000_000)  # keeps A busy, so the build is still queued
+        out_a = mp.fanin_reduce(rel, src, dst, K, 0)
+    with torch.cuda.stream(b):
+        before = _stats()
+        out_b = mp.fanin_reduce(rel, src.clone(), dst.clone(), K, 0)
+        d = _delta(before, _stats())
+        ns.plan_cache_clear()  # drops the entry while B's kernels may still run
+        out_b2 = out_b * 1.0
+    torch.cuda.synchronize()
+    assert d["hits"] == 1, d
+    assert np.array_equal(out_a.cpu().numpy(), want)
+    assert np.array_equal(out_b2.cpu().numpy(), want)
 
 
 def test_content_hit_for_fanout_and_strided_indices(mp_env) -> None:
@@ -158,7 +247,23 @@ def test_content_hit_for_fanout_and_strided_indices(mp_env) -> None:
     before = _stats()
     second = mp.fanout_scatter(x, src, dst, slots)
     d = _delta(before, _stats())
-    assert d["content"] == 1, d
+    assert d["hits"] == 1, d
     assert torch.equal(first, second)
     want = oracle.fanout_scatter(x.cpu().numpy(), src.cpu().numpy(), dst.cpu().numpy(), slots)
     assert np.array_equal(second.cpu().numpy(), want)
+
+
+def test_cache_memory_stays_bounded(mp_env) -> None:
+    """New topologies every call: entries are evicted to the memory bound and
+    the kept / peak byte counts are reported."""
+
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    ns.plan_cache_clear()
+    for seed in range(12):
+        rel, src, dst, K = _fanin_case(100 + seed)
+        mp.fanin_reduce(rel, src, dst, K, 0)
+    entries, _, _, _, kept, peak = ns.plan_cache_stats()
+    limit = int(os.environ.get("RELM_MP_PLAN_CACHE_MB", "2048")) << 20
+    assert 0 < kept <= peak <= limit and entries >= 1

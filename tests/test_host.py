@@ -204,7 +204,10 @@ def test_env_policies(monkeypatch) -> None:
     from relmo_amd import mp_runtime
 
     monkeypatch.delenv("RELM_MP_FALLBACK", raising=False)
-    assert mp_runtime.fallback_mode() == "error"
+    assert mp_runtime.fallback_mode() == "python"
+    assert mp_runtime.fallback_mode(torch.empty(0)) == "python"
+    gpu_like = type("GpuTensor", (), {"is_cuda": True})()
+    assert mp_runtime.fallback_mode(gpu_like) == "error"
     monkeypatch.setenv("RELM_MP_FALLBACK", "PYTHON")
     assert mp_runtime.fallback_mode() == "python"
     monkeypatch.setenv("RELM_MP_TORCH_VERSION_POLICY", "strict")
@@ -213,7 +216,8 @@ def test_env_policies(monkeypatch) -> None:
     monkeypatch.setenv("RELM_MP_TORCH_VERSION_POLICY", "bogus")
     assert mp_runtime.torch_version_policy() == "forward"
     monkeypatch.setenv("RELM_MP_FALLBACK", "bogus")
-    assert mp_runtime.fallback_mode() == "error"
+    assert mp_runtime.fallback_mode() == "python"
+    assert mp_runtime.fallback_mode(gpu_like) == "error"
 
 
 def _fake_build(monkeypatch, info: str) -> None:
@@ -258,8 +262,10 @@ def test_compat_rejects_mismatched_builds(monkeypatch) -> None:
 def test_dispatch_policy(monkeypatch) -> None:
     from relmo_amd import mp_dispatch, mp_runtime
 
+    gpu_like = type("GpuTensor", (), {"is_cuda": True})()
     monkeypatch.setenv("RELM_MP_ENABLE", "0")
-    assert mp_dispatch.should_use_custom("fanin_reduce") is False
+    assert mp_dispatch.library_ready("fanin_reduce") is False
+    assert mp_dispatch.library_op("fanin_pack_multi") is None
 
     def broken() -> None:
         raise RuntimeError("library missing")
@@ -268,10 +274,34 @@ def test_dispatch_policy(monkeypatch) -> None:
     monkeypatch.setattr(mp_dispatch, "ensure_runtime_compat_once", broken)
     monkeypatch.setenv("RELM_MP_FALLBACK", "error")
     with pytest.raises(RuntimeError, match="Custom mp op fanin_reduce is unavailable"):
-        mp_dispatch.should_use_custom("fanin_reduce")
+        mp_dispatch.library_ready("fanin_reduce")
     monkeypatch.setenv("RELM_MP_FALLBACK", "python")
-    assert mp_dispatch.should_use_custom("fanin_reduce") is False
+    assert mp_dispatch.library_ready("fanin_reduce") is False
+    assert mp_dispatch.library_ready("fanin_reduce", gpu_like) is False
+    # unset: relmo's quiet fallback for CPU tensors, an error for GPU tensors
+    monkeypatch.delenv("RELM_MP_FALLBACK")
+    assert mp_dispatch.library_ready("fanin_reduce", torch.empty(0)) is False
+    with pytest.raises(RuntimeError, match="Custom mp op fanin_reduce is unavailable"):
+        mp_dispatch.library_ready("fanin_reduce", gpu_like)
+    calls = []
+    assert mp_dispatch.run_op("fanin_pack_multi", 1, 2, fallback=lambda *a: calls.append(a) or "fb") == "fb"
+    assert calls == [(1, 2)]
     assert mp_runtime.candidate_libraries()[0].name.startswith("relm_mp_ops")
+
+
+def test_dispatch_routes_to_the_library(monkeypatch) -> None:
+    from relmo_amd import mp_dispatch
+
+    monkeypatch.setenv("RELM_MP_ENABLE", "1")
+    monkeypatch.setenv("RELM_MP_FALLBACK", "error")
+    op = mp_dispatch.library_op("fanin_pack_multi")
+    assert op is torch.ops.relm_mp.fanin_pack_multi
+    # gpu-only ops stay on the fallback for CPU tensors, without an error
+    assert mp_dispatch.library_op("lgan_pool_reduce", tensor=torch.empty(0), gpu_only=True) is None
+    with pytest.raises(RuntimeError, match="unavailable in the loaded relm_mp library"):
+        mp_dispatch.library_op("no_such_op")
+    monkeypatch.setenv("RELM_MP_FALLBACK", "python")
+    assert mp_dispatch.library_op("no_such_op") is None
 
 
 def test_facade_public_names() -> None:
@@ -320,7 +350,7 @@ def test_model_consumers_cpu_lane_matches_aten(monkeypatch) -> None:
          lambda b, mode: C.CentralizedRelationalGNN(8, 2, b.relations, mode)),
     ):
         batch = make_batch()
-        for mode in (0, 1):
+        for mode in (0, 1, 2):
             torch.manual_seed(0)
             model = make_model(batch, mode)
             routing = model.routing(batch)
@@ -329,6 +359,25 @@ def test_model_consumers_cpu_lane_matches_aten(monkeypatch) -> None:
             monkeypatch.setenv("RELM_MP_ENABLE", "0")
             b = C.train_step(model, batch, routing)
             assert torch.allclose(a, b, rtol=1e-5, atol=1e-7), (mode, float(a), float(b))
+
+
+def test_model_fanin_masks_only_objects_without_messages(mp_env) -> None:
+    """Objects without messages get 0 (PyG's aggregators); a NaN or +inf in an
+    object's messages still reaches that object's aggregate."""
+
+    from relmo_amd import consumers as C
+
+    rel = torch.tensor([[1.0, 2.0], [float("nan"), 0.0], [float("inf"), 3.0], [4.0, 5.0]])
+    r = {"flat": torch.arange(4), "obj": torch.tensor([0, 0, 1, 3])}
+    r["deg"] = torch.bincount(r["obj"], minlength=5)
+    lse = C.fanin_objects(1, rel, r, 5)
+    # relmo's logsumexp (ATen sequence) turns a +inf message into NaN
+    assert torch.isnan(lse[0, 0]) and torch.isnan(lse[1, 0])
+    assert torch.equal(lse[2], torch.zeros(2)) and torch.equal(lse[4], torch.zeros(2))
+    assert torch.equal(lse[3], rel[3])
+    mean = C.fanin_objects(2, rel, r, 5)
+    assert torch.isnan(mean[0, 0]) and mean[0, 1] == 1.0
+    assert torch.equal(mean[3], rel[3]) and torch.equal(mean[2], torch.zeros(2))
 
 
 # ---- pack ops on the CPU lane ----------------------------------------------------------------
@@ -604,3 +653,28 @@ def test_fanout_concat_autograd_on_cpu(mp_env) -> None:
 
 if __name__ == "__main__":  # pragma: no cover
     sys.exit(pytest.main([__file__, "-q"]))
+
+
+def test_planned_ops_on_the_cpu_lane(ops) -> None:
+    """fanin_reduce_planned returns the plain op's result and an empty plan
+    handle on the CPU lane; the *_planned backward ops then equal the plain
+    backward ops, and the autograd facade uses them."""
+
+    gen = torch.Generator().manual_seed(11)
+    rel = torch.randn(9, 3, dtype=torch.float64, generator=gen)
+    src = torch.tensor([0, 2, 4, 6, 8, 1, 3])
+    dst = torch.tensor([1, 1, 0, 3, 1, 0, 3])
+    g = torch.randn(4, 3, dtype=torch.float64, generator=gen)
+    for mode in (0, 1):
+        out, plan = ops.fanin_reduce_planned(rel, src, dst, 4, mode)
+        assert isinstance(plan, torch.ScriptObject)
+        assert torch.equal(out, ops.fanin_reduce(rel, src, dst, 4, mode))
+        if mode == 0:
+            got = ops.fanin_reduce_sum_backward_planned(g, src, dst, 9, plan)
+            want = ops.fanin_reduce_sum_backward(g, src, dst, 9)
+        else:
+            got = ops.fanin_reduce_logsumexp_backward_planned(g, rel, src, dst, out, 9, plan)
+            want = ops.fanin_reduce_logsumexp_backward(g, rel, src, dst, out, 9)
+        assert torch.equal(got, want)
+    with pytest.raises((RuntimeError, ValueError), match="Unsupported fanin_reduce mode"):
+        ops.fanin_reduce_planned(rel, src, dst, 4, 2)
