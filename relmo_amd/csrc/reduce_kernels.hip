@@ -1020,11 +1020,6 @@ dim3 row_grid(int64_t rows, int G, int64_t slices, int rows_per_group = 1) {
     return dim3(static_cast<unsigned>(bx), static_cast<unsigned>(slices));
 }
 
-dim3 block_grid(int64_t blocks, int64_t slices) {
-    int64_t bx = blocks < 1 ? 1 : (blocks > kMaxBlocksX ? kMaxBlocksX : blocks);
-    return dim3(static_cast<unsigned>(bx), static_cast<unsigned>(slices));
-}
-
 // Workgroups of `kernel` (kThreads each) resident on the current device at
 // once; persistent launches size their grids with it.
 int64_t resident_blocks(const void* kernel) {
