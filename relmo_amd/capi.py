@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "relm_mp_fanout_scatter_backward",
     "relm_mp_fanin_reduce_workspace_size",
     "relm_mp_fanin_reduce",
+    "relm_mp_fanin_reduce_noalloc",
     "relm_mp_fanin_reduce_sum_backward_workspace_size",
     "relm_mp_fanin_reduce_sum_backward",
     "relm_mp_fanin_reduce_logsumexp_backward_workspace_size",
@@ -134,6 +135,7 @@ _SIGNATURES = {
     "relm_mp_fanout_scatter_backward": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_fanin_reduce_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
     "relm_mp_fanin_reduce": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_fanin_reduce_noalloc": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "relm_mp_fanin_reduce_sum_backward_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
     "relm_mp_fanin_reduce_sum_backward": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_fanin_reduce_logsumexp_backward_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
@@ -290,6 +292,27 @@ def fanin_reduce(rel_flat: torch.Tensor, flat_src: torch.Tensor, dst_idx: torch.
         )
     )
     return out
+
+
+def fanin_reduce_noalloc(rel_flat: torch.Tensor, flat_src: torch.Tensor, dst_idx: torch.Tensor, dim_size: int,
+                        mode: int) -> torch.Tensor:
+    """``relm_mp_fanin_reduce_noalloc``: the same op on the library's own device
+    scratch (the caller passes inputs and the output only)."""
+
+    _check_index(flat_src)
+    _check_index(dst_idx)
+    emb = rel_flat.size(1)
+    out = torch.empty(dim_size, emb, dtype=rel_flat.dtype, device=rel_flat.device)
+    check(
+        lib().relm_mp_fanin_reduce_noalloc(
+            _dtype(rel_flat), _ptr(rel_flat), rel_flat.size(0), emb, _ptr(flat_src), _ptr(dst_idx),
+            flat_src.numel(), dim_size, mode, _ptr(out), _stream(rel_flat),
+        )
+    )
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20  # RELM_MP_NOALLOC_SCRATCH_BYTES
 
 
 def fanin_reduce_sum_backward(grad_out: torch.Tensor, flat_src: torch.Tensor, dst_idx: torch.Tensor, rel_rows: int) -> torch.Tensor:

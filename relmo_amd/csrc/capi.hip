@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "internal.h"
@@ -85,17 +86,6 @@ int check_validation(const DevStatus& host, const int64_t* keys, int64_t key_bou
                   name != nullptr ? name : "index", static_cast<long long>(value),
                   static_cast<long long>(bound));
     return set_error(RELM_MP_ERR_INDEX_OUT_OF_BOUNDS, buf);
-}
-
-// Reads the status back (one stream synchronisation) and checks it.
-int finish_validation(const DevStatus* dst, DevStatus& host, const int64_t* keys, int64_t key_bound,
-                      const char* key_name, const int64_t* gathers, int64_t gather_bound,
-                      const char* gather_name, int gather_checked_first, hipStream_t s) {
-    RELM_HIP(hipMemcpyAsync(&host, dst, sizeof(DevStatus), hipMemcpyDeviceToHost, s),
-             "relm_mp status copy");
-    RELM_HIP(hipStreamSynchronize(s), "relm_mp status sync");
-    return check_validation(host, keys, key_bound, key_name, gathers, gather_bound, gather_name,
-                            gather_checked_first);
 }
 
 // Per host thread and device: pinned host copies of a plan status and plan
@@ -371,10 +361,17 @@ int validate_pending(relm_mp_plan* plan) {
     return RELM_MP_OK;
 }
 
+// How a build reads its validation status back: through the calling thread's
+// pinned host slot (the status is published right after the first sort pass,
+// so the host waits only for that), or with a plain copy after the build
+// (no host memory of the library's own: the no-allocation entry point).
+enum class StatusPath { kPinnedSlot, kStreamCopy };
+
 int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, const int64_t* gathers,
               int64_t gather_bound, const char* gather_name, int gather_checked_first,
               int64_t num_edges, void* plan_mem, size_t plan_bytes, void* scratch,
-              size_t scratch_bytes, relm_mp_plan* plan, bool wait_counts, hipStream_t s) {
+              size_t scratch_bytes, relm_mp_plan* plan, bool wait_counts, hipStream_t s,
+              StatusPath path = StatusPath::kPinnedSlot) {
     RELM_TRY(check_rows(key_bound, "num_keys"));
     RELM_TRY(check_rows(num_edges, "num_edges"));
     if (gathers != nullptr) RELM_TRY(check_rows(gather_bound, "num_gather"));
@@ -388,8 +385,10 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     if (scratch == nullptr || scratch_bytes < sc.bytes)
         return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: CSR scratch memory too small");
     HostSlot* hs = nullptr;
-    RELM_TRY(host_slot(&hs));
-    RELM_TRY(no_pending(hs));
+    if (path == StatusPath::kPinnedSlot) {
+        RELM_TRY(host_slot(&hs));
+        RELM_TRY(no_pending(hs));
+    }
     std::memset(plan, 0, sizeof(*plan));
     plan->kind = RELM_MP_PLAN_CSR;
     plan->hub_threshold = kHubThreshold;
@@ -419,6 +418,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     // The validation result is final after the first sort pass: copy it to
     // the host and mark the point, then enqueue the rest of the build.
     auto mark_validation = [&]() -> hipError_t {
+        if (hs == nullptr) return hipSuccess;
         hipError_t e = launch_status_publish(l.status, hs->status_mapped, nullptr, s);
         return e != hipSuccess ? e : hipEventRecord(hs->ready, s);
     };
@@ -439,8 +439,15 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
                               max_chunks(num_edges), l.item_first, l.item_short, l.num_items,
                               l.short_off, l.short_gather, l.counts, l.status, s),
              "relm_mp key index kernels");
-    RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
-    const DevStatus host = *hs->status;
+    DevStatus host{};
+    if (hs != nullptr) {
+        RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
+        host = *hs->status;
+    } else {
+        RELM_HIP(hipMemcpyAsync(&host, l.status, sizeof(DevStatus), hipMemcpyDeviceToHost, s),
+                 "relm_mp status copy");
+        RELM_HIP(hipStreamSynchronize(s), "relm_mp status sync");
+    }
     RELM_TRY(check_validation(host, keys, key_bound, key_name, gathers, gather_bound, gather_name,
                               gather_checked_first));
     plan->gather_identity = gathers == nullptr || host.gather_mismatch == 0 ? 1 : 0;
@@ -448,9 +455,31 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     return RELM_MP_OK;
 }
 
-size_t csr_total(int64_t num_keys, int64_t num_edges) {
-    return csr_layout(nullptr, num_keys, num_edges).bytes +
-           csr_scratch(nullptr, num_keys, num_edges).bytes;
+// Device scratch of relm_mp_fanin_reduce_noalloc (plan, sort buffers and hub
+// partials of one call), held by every device the library runs on until the
+// process ends.
+__device__ __align__(256) unsigned char scratch[RELM_MP_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call on
+// that device).
+int noalloc_scratch(void** out) {
+    int dev = 0;
+    RELM_HIP(hipGetDevice(&dev), "relm_mp device query");
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(RELM_MP_ERR_HIP, "relm_mp: device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        RELM_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "relm_mp scratch address");
+        if (ptr == nullptr) return set_error(RELM_MP_ERR_HIP, "relm_mp: scratch address is NULL");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return RELM_MP_OK;
 }
 
 }  // namespace
@@ -797,13 +826,9 @@ size_t relm_mp_fanin_reduce_workspace_size(int64_t num_edges, int64_t dim_size, 
     return plan + scratch;
 }
 
-// mp_ops.cpp:3327-3348 (mode router), 3168-3222 (sum), 3005-3036 (logsumexp);
-// the sum CPU loop 2863-2886 checks flat_src before dst_idx.
-int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int64_t emb,
-                         const int64_t* flat_src, const int64_t* dst_idx, int64_t num_edges,
-                         int64_t dim_size, int64_t mode, void* out, void* workspace,
-                         size_t workspace_bytes, relm_mp_stream_t stream) {
-    hipStream_t s = static_cast<hipStream_t>(stream);
+// Checks of relm_mp_fanin_reduce's arguments (the workspace aside).
+static int fanin_reduce_checks(int dtype, int64_t rel_rows, int64_t emb, int64_t num_edges,
+                               int64_t dim_size, int64_t mode) {
     RELM_TRY(check_dtype(dtype));
     RELM_TRY(check_rows(dim_size, "dim_size"));
     RELM_TRY(check_rows(rel_rows, "rel_rows"));
@@ -812,18 +837,69 @@ int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int6
     if (mode != RELM_MP_MODE_SUM && mode != RELM_MP_MODE_LOGSUMEXP)
         return set_error(RELM_MP_ERR_UNSUPPORTED_MODE,
                          "Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
+    return RELM_MP_OK;
+}
+
+// The body of relm_mp_fanin_reduce once the workspace is known to suffice.
+static int fanin_reduce_run(int dtype, const void* rel_flat, int64_t rel_rows, int64_t emb,
+                            const int64_t* flat_src, const int64_t* dst_idx, int64_t num_edges,
+                            int64_t dim_size, int64_t mode, void* out, void* workspace,
+                            size_t workspace_bytes, hipStream_t s, StatusPath path) {
     const double empty = mode == RELM_MP_MODE_SUM ? 0.0 : -__builtin_huge_val();
     if (num_edges == 0 || dim_size == 0) return compute_fill(dtype, out, dim_size * emb, empty, s);
-    const size_t need = relm_mp_fanin_reduce_workspace_size(num_edges, dim_size, emb, dtype);
-    if (workspace == nullptr || workspace_bytes < need)
-        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: workspace too small");
     const size_t plan_bytes = relm_mp_csr_plan_bytes(dim_size, num_edges);
     char* scratch = static_cast<char*>(workspace) + plan_bytes;
     relm_mp_plan plan;
     RELM_TRY(csr_build(dst_idx, dim_size, "dst_idx", flat_src, rel_rows, "flat_src", 1, num_edges,
-                       workspace, plan_bytes, scratch, workspace_bytes - plan_bytes, &plan, false, s));
+                       workspace, plan_bytes, scratch, workspace_bytes - plan_bytes, &plan, false, s,
+                       path));
     return compute_segment_reduce(dtype, plan, nullptr, rel_flat, emb, mode, out, scratch,
                                   workspace_bytes - plan_bytes, s);
+}
+
+// mp_ops.cpp:3327-3348 (mode router), 3168-3222 (sum), 3005-3036 (logsumexp);
+// the sum CPU loop 2863-2886 checks flat_src before dst_idx.
+int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int64_t emb,
+                         const int64_t* flat_src, const int64_t* dst_idx, int64_t num_edges,
+                         int64_t dim_size, int64_t mode, void* out, void* workspace,
+                         size_t workspace_bytes, relm_mp_stream_t stream) {
+    RELM_TRY(fanin_reduce_checks(dtype, rel_rows, emb, num_edges, dim_size, mode));
+    if (num_edges > 0 && dim_size > 0) {
+        const size_t need = relm_mp_fanin_reduce_workspace_size(num_edges, dim_size, emb, dtype);
+        if (workspace == nullptr || workspace_bytes < need)
+            return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: workspace too small");
+    }
+    return fanin_reduce_run(dtype, rel_flat, rel_rows, emb, flat_src, dst_idx, num_edges, dim_size,
+                            mode, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                            StatusPath::kPinnedSlot);
+}
+
+// relm_mp_fanin_reduce on the library's own device scratch: the array below,
+// one copy per device.  Host code never passes its name to a kernel or a copy
+// (there it names a host-side stand-in); the device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+int relm_mp_fanin_reduce_noalloc(int dtype, const void* rel_flat, int64_t rel_rows, int64_t emb,
+                                 const int64_t* flat_src, const int64_t* dst_idx,
+                                 int64_t num_edges, int64_t dim_size, int64_t mode, void* out,
+                                 relm_mp_stream_t stream) {
+    RELM_TRY(fanin_reduce_checks(dtype, rel_rows, emb, num_edges, dim_size, mode));
+    void* ws = nullptr;
+    if (num_edges > 0 && dim_size > 0) {
+        const size_t need = relm_mp_fanin_reduce_workspace_size(num_edges, dim_size, emb, dtype);
+        if (need > static_cast<size_t>(RELM_MP_NOALLOC_SCRATCH_BYTES)) {
+            char buf[256];
+            std::snprintf(buf, sizeof(buf),
+                          "relm_mp_fanin_reduce_noalloc: this call needs %zu bytes of scratch, more "
+                          "than the %lld the library reserves per device; use "
+                          "relm_mp_fanin_reduce with a workspace",
+                          need, static_cast<long long>(RELM_MP_NOALLOC_SCRATCH_BYTES));
+            return set_error(RELM_MP_ERR_WORKSPACE, buf);
+        }
+        RELM_TRY(noalloc_scratch(&ws));
+    }
+    return fanin_reduce_run(dtype, rel_flat, rel_rows, emb, flat_src, dst_idx, num_edges, dim_size,
+                            mode, out, ws, static_cast<size_t>(RELM_MP_NOALLOC_SCRATCH_BYTES),
+                            static_cast<hipStream_t>(stream), StatusPath::kStreamCopy);
 }
 
 size_t relm_mp_fanin_reduce_sum_backward_workspace_size(int64_t num_edges, int64_t rel_rows,
