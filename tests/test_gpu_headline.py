@@ -240,9 +240,9 @@ def _step_grads(C, model, batch, routing, enable: str, monkeypatch):
 def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     """One training step: the HIP lane (fp32) is at least as close to a float64
     run of the same step as the ATen lane (fp32) is - per parameter, the
-    relative L2 error of the gradient within twice the ATen lane's (plus 1e-7),
-    and the loss within twice the ATen lane's loss error (plus 1e-7
-    relative).  Sum and logsumexp; mean for C5."""
+    relative L2 error of the gradient within twice the ATen lane's, and the
+    loss within twice the ATen lane's loss error, each plus 8 fp32 ulps
+    (relative).  Sum and logsumexp; mean for C5."""
 
     import copy
 
@@ -267,14 +267,16 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
         loss64, g64 = _step_grads(C, m64, batch, routing, "0", monkeypatch)
         e_hip, e_aten = abs(loss_hip - loss64), abs(loss_aten - loss64)
         _log(f"  loss {loss64:.8g}: |hip - f64| {e_hip:.3g}, |aten - f64| {e_aten:.3g}")
-        assert e_hip <= 2 * e_aten + 1e-7 * abs(loss64), (mode, e_hip, e_aten)
+        # slack of a few fp32 ulps: the ATen lane's own error varies run to run
+        # (float atomics), the HIP lane's does not
+        assert e_hip <= 2 * e_aten + 8 * EPS32 * abs(loss64), (mode, e_hip, e_aten)
         worst = 0.0
         for k, ref in g64.items():
             nref = float(ref.norm())
             r_hip = float((g_hip[k].double() - ref).norm()) / max(nref, 1e-300)
             r_aten = float((g_aten[k].double() - ref).norm()) / max(nref, 1e-300)
             worst = max(worst, r_hip / max(r_aten, 1e-12))
-            assert r_hip <= 2 * r_aten + 1e-7, (mode, k, r_hip, r_aten)
+            assert r_hip <= 2 * r_aten + 8 * EPS32, (mode, k, r_hip, r_aten)
         _log(f"  gradients: worst ratio of relative L2 errors hip/aten {worst:.3g}")
         del m, m64, routing, g_hip, g_aten, g64
         torch.cuda.empty_cache()
