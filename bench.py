@@ -266,9 +266,12 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
     (CentralizedRelationalGNN, fused central layer): fp32 training step =
     forward + backward of mean(out^2) through relmo_amd.mp (HIP ops), index
     routing built once per batch as in the reference layers; graphs/sec =
-    graphs / time per step.  C5 runs 512 of its 2048 graphs: ten layers of
-    saved activations for 2048 graphs (about 40 GB per layer) exceed one
-    GPU's 288 GB."""
+    graphs / time per step.  C5 runs all 2048 graphs of its config (~5.1M
+    relation nodes): the central FiLM MLP's hidden activations (~40 GB per
+    layer, ten layers) are recomputed in the backward from the saved layer
+    input (activation checkpointing), which keeps the step under one GPU's
+    288 GB; the recompute is one extra central-MLP forward per layer, inside
+    the timed step."""
 
     from relmo_amd import consumers as C
 
@@ -277,13 +280,17 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
         batch = C.synthetic_c4(dev)
         make = lambda mode: C.RelationalGNN(32, 10, batch.relations, mode).to(dev)
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects, "emb": 32, "layers": 10}
+        modes = ((0, "sum"), (1, "logsumexp"))
     else:
-        batch = C.synthetic_c5(dev, num_graphs=512)
-        make = lambda mode: C.CentralizedRelationalGNN(128, 10, batch.relations, mode).to(dev)
-        cfg = {"graphs": batch.num_graphs, "graphs_in_config": 2048, "objects": batch.num_objects,
-               "emb": 128, "layers": 10}
+        batch = C.synthetic_c5(dev)
+        make = lambda mode: C.CentralizedRelationalGNN(128, 10, batch.relations, mode,
+                                                       recompute_central=True).to(dev)
+        cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects,
+               "relation_nodes": int(sum(a.size(0) for a in batch.atoms.values())), "emb": 128,
+               "layers": 10, "central_mlp": "recomputed in the backward (activation checkpointing)"}
+        modes = ((0, "sum"), (1, "logsumexp"), (2, "mean"))
     res = {"config": cfg}
-    for mode, name in ((0, "sum"), (1, "logsumexp")):
+    for mode, name in modes:
         torch.manual_seed(0)
         model = make(mode)
         routing = model.routing(batch)
@@ -555,13 +562,215 @@ def cpu_baseline(syn, torch) -> dict:
                         "sample": sample + f"; reference CPU lane (ATen sequences, mp_ops.cpp:2981-3036), "
                                            f"{threads} threads, median of {reps}, {t:.3f} s per fwd+bwd"}
         headline["variants"] = variants
+        headline["host"] = host_info(torch)
         return headline
     t0 = time.perf_counter()
     out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, K)
     oracle.fanin_reduce_logsumexp_backward(g, rel, flat_src, dst, out, E)
     t = time.perf_counter() - t0
     return {"value": round(gbs(nbytes, t), 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": sample + f"; C oracle, 1 thread, {t:.3f} s per fwd+bwd", "variants": variants}
+            "sample": sample + f"; C oracle, 1 thread, {t:.3f} s per fwd+bwd", "variants": variants,
+            "host": host_info(torch)}
+
+
+def host_info(torch) -> dict:
+    """The host the CPU baselines ran on."""
+
+    cpu = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        rocm = Path("/opt/rocm/.info/version").read_text().strip()
+    except OSError:
+        rocm = None
+    return {"cpu_model": cpu, "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "job_threads": host_threads(), "torch": torch.__version__, "hip": torch.version.hip,
+            "rocm": rocm}
+
+
+def cpu_full(torch, syn) -> dict:
+    """The full CPU baseline plan, on the host's cores (``--cpu-full``; minutes
+    of CPU work, so not part of the default run):
+
+      * C1 in full - the reference's CPU op library (oracle/_ref) per op,
+        median of 80 calls after 20 warmup (benchmark_mp_ops.py:74-117 with
+        one call per sample), and relmo's python_only ATen lane (forward, and
+        forward + autograd backward) - at 1 thread and at the job's share;
+      * C2 (logsumexp and sum) and C3 (fanout) at full size, once per thread
+        count, the same two lanes;
+      * C4 (512 graphs) and C5 (a 64-graph sample of its 2048) training steps
+        on the ATen model path (RELM_MP_ENABLE=0), at the job's share,
+        graphs/sec of one step after one warmup step."""
+
+    import numpy as np
+
+    from oracle import ref_runner
+    from relmo_amd import consumers as C
+    from relmo_amd import mp_pack
+
+    full = host_threads()
+    threads = (1, full)
+    have_ref = ref_runner.available()
+    res: dict = {"host": host_info(torch), "threads": list(threads), "reference_lane": have_ref}
+
+    def aten(fn, th, reps, warm):
+        saved = torch.get_num_threads()
+        torch.set_num_threads(th)
+        try:
+            for _ in range(warm):
+                fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+        finally:
+            torch.set_num_threads(saved)
+        return statistics.median(ts)
+
+    def ref(specs, arrays, reps, warm):
+        """{threads: {name: median seconds}} for the reference library's ops."""
+
+        calls = [{"op": op, "tensors": ts, "ints": ints, "repeat": reps, "warmup": warm, "threads": th,
+                  "keep": False} for th in threads for _name, op, ts, ints in specs]
+        out = ref_runner.run_reference(calls, arrays, timeout=1800.0)
+        got: dict = {}
+        for call, r in zip(calls, out):
+            if "error" in r:
+                raise RuntimeError(f"reference {call['op']}: {r['error']}")
+        i = 0
+        for th in threads:
+            got[th] = {}
+            for name, *_ in specs:
+                got[th][name] = statistics.median(out[i]["times"])
+                i += 1
+        return got
+
+    def grad_of(fn, leaf, g):
+        def step():
+            x = leaf.clone().requires_grad_(True)
+            torch.autograd.grad(fn(x), x, g)
+        return step
+
+    # ---- C1 ------------------------------------------------------------------------
+    log("CPU C1 ...")
+    d = syn.c1_ops("cpu")
+    objects, slots = d["objects"], d["slots"]
+    c1: dict = {"python_only_us": {}}
+    py = {
+        "fanout_scatter": lambda: mp_pack.fanout_scatter_python(d["x"], d["src"], d["flat_dst"], slots),
+        "fanout_scatter_fwd_bwd": grad_of(
+            lambda x: mp_pack.fanout_scatter_python(x, d["src"], d["flat_dst"], slots), d["x"], d["grad_slots"]),
+        "fanin_reduce_sum": lambda: mp_pack.fanin_reduce_python(d["rel"], d["flat_src"], d["dst"], objects, 0),
+        "fanin_reduce_sum_fwd_bwd": grad_of(
+            lambda r: mp_pack.fanin_reduce_python(r, d["flat_src"], d["dst"], objects, 0), d["rel"], d["grad_obj"]),
+    }
+    for th in threads:
+        c1["python_only_us"][th] = {k: round(aten(fn, th, 80, 20) * 1e6, 1) for k, fn in py.items()}
+    if have_ref:
+        arrays = {k: v.numpy() for k, v in d.items() if isinstance(v, torch.Tensor)}
+        specs = [("fanout_scatter", "fanout_scatter", ["x", "src", "flat_dst"], [slots]),
+                 ("fanout_scatter_backward", "fanout_scatter_backward", ["grad_slots", "src", "flat_dst"], [objects]),
+                 ("fanin_reduce_sum", "fanin_reduce", ["rel", "flat_src", "dst"], [objects, 0]),
+                 ("fanin_reduce_sum_backward", "fanin_reduce_sum_backward", ["grad_obj", "flat_src", "dst"], [slots])]
+        got = ref(specs, arrays, 80, 20)
+        c1["reference_us"] = {th: {k: round(v * 1e6, 1) for k, v in got[th].items()} for th in threads}
+    res["c1"] = c1
+
+    # ---- C2 ------------------------------------------------------------------------
+    log("CPU C2 ...")
+    d = syn.c2_fanin("cpu")
+    K, E, D = d["dim_size"], d["rel"].size(0), d["rel"].size(1)
+    lse_bytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_lse_bwd(E, D, K, E)
+    sum_bytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_sum_bwd(E, D, K, E)
+    c2: dict = {"bytes_lse_fwd_bwd": lse_bytes, "bytes_sum_fwd_bwd": sum_bytes, "python_only_s": {}}
+    for th in threads:
+        c2["python_only_s"][th] = {
+            mode: round(aten(grad_of(lambda r, m=m: mp_pack.fanin_reduce_python(r, d["flat_src"], d["dst"], K, m),
+                                     d["rel"], d["grad_out"]), th, 1, 0), 3)
+            for mode, m in (("logsumexp_fwd_bwd", 1), ("sum_fwd_bwd", 0))}
+    if have_ref:
+        out = mp_pack.fanin_reduce_python(d["rel"], d["flat_src"], d["dst"], K, 1)
+        arrays = {"rel": d["rel"].numpy(), "src": d["flat_src"].numpy(), "dst": d["dst"].numpy(),
+                  "g": d["grad_out"].numpy(), "out": out.numpy()}
+        specs = [("logsumexp_fwd", "fanin_reduce", ["rel", "src", "dst"], [K, 1]),
+                 ("logsumexp_bwd", "fanin_reduce_logsumexp_backward", ["g", "rel", "src", "dst", "out"], [E]),
+                 ("sum_fwd", "fanin_reduce", ["rel", "src", "dst"], [K, 0]),
+                 ("sum_bwd", "fanin_reduce_sum_backward", ["g", "src", "dst"], [E])]
+        got = ref(specs, arrays, 1, 0)
+        c2["reference_s"] = {th: {k: round(v, 3) for k, v in got[th].items()} for th in threads}
+        c2["reference_gbs"] = {th: {
+            "logsumexp_fwd_bwd": round(gbs(lse_bytes, got[th]["logsumexp_fwd"] + got[th]["logsumexp_bwd"]), 3),
+            "sum_fwd_bwd": round(gbs(sum_bytes, got[th]["sum_fwd"] + got[th]["sum_bwd"]), 3)} for th in threads}
+        del arrays, out
+    c2["python_only_gbs"] = {th: {"logsumexp_fwd_bwd": round(gbs(lse_bytes, v["logsumexp_fwd_bwd"]), 3),
+                                  "sum_fwd_bwd": round(gbs(sum_bytes, v["sum_fwd_bwd"]), 3)}
+                             for th, v in c2["python_only_s"].items()}
+    res["c2"] = c2
+    del d
+
+    # ---- C3 ------------------------------------------------------------------------
+    log("CPU C3 ...")
+    d = syn.c3_fanout("cpu")
+    R, D = d["x"].shape
+    S = d["out_rows"]
+    c3_bytes = syn.bytes_fanout_fwd(S, D, S) + syn.bytes_fanout_bwd(S, D, R)
+    c3: dict = {"bytes_fwd_bwd": c3_bytes, "python_only_s": {}}
+    for th in threads:
+        c3["python_only_s"][th] = round(aten(grad_of(
+            lambda x: mp_pack.fanout_scatter_python(x, d["src"], d["flat_dst"], S), d["x"], d["grad_out"]),
+            th, 1, 0), 3)
+    if have_ref:
+        arrays = {"x": d["x"].numpy(), "src": d["src"].numpy(), "flat": d["flat_dst"].numpy(),
+                  "g": d["grad_out"].numpy()}
+        specs = [("fanout_fwd", "fanout_scatter", ["x", "src", "flat"], [S]),
+                 ("fanout_bwd", "fanout_scatter_backward", ["g", "src", "flat"], [R])]
+        got = ref(specs, arrays, 1, 0)
+        c3["reference_s"] = {th: {k: round(v, 3) for k, v in got[th].items()} for th in threads}
+        c3["reference_gbs"] = {th: round(gbs(c3_bytes, got[th]["fanout_fwd"] + got[th]["fanout_bwd"]), 3)
+                               for th in threads}
+        del arrays
+    c3["python_only_gbs"] = {th: round(gbs(c3_bytes, v), 3) for th, v in c3["python_only_s"].items()}
+    res["c3"] = c3
+    del d
+
+    # ---- C4 / C5 on the ATen model path ---------------------------------------------
+    saved_env = os.environ.get("RELM_MP_ENABLE")
+    os.environ["RELM_MP_ENABLE"] = "0"
+    saved_threads = torch.get_num_threads()
+    torch.set_num_threads(full)
+    try:
+        for name, batch, make, modes in (
+            ("c4", C.synthetic_c4("cpu"), lambda b, m: C.RelationalGNN(32, 10, b.relations, m),
+             ((0, "sum"), (1, "logsumexp"))),
+            ("c5", C.synthetic_c5("cpu", num_graphs=64), lambda b, m: C.CentralizedRelationalGNN(128, 10, b.relations, m),
+             ((0, "sum"), (1, "logsumexp"), (2, "mean"))),
+        ):
+            log(f"CPU {name} ...")
+            entry: dict = {"graphs": batch.num_graphs, "objects": batch.num_objects, "threads": full}
+            for m, mode in modes:
+                torch.manual_seed(0)
+                model = make(batch, m)
+                routing = model.routing(batch)
+                C.train_step(model, batch, routing)
+                t0 = time.perf_counter()
+                C.train_step(model, batch, routing)
+                t = time.perf_counter() - t0
+                entry[mode] = {"s_step": round(t, 3), "graphs_per_sec": round(batch.num_graphs / t, 2)}
+            res[name] = entry
+    finally:
+        torch.set_num_threads(saved_threads)
+        if saved_env is None:
+            os.environ.pop("RELM_MP_ENABLE", None)
+        else:
+            os.environ["RELM_MP_ENABLE"] = saved_env
+    return res
 
 
 def main() -> int:
@@ -574,6 +783,8 @@ def main() -> int:
                     default=None,
                     help="run one workload only and print its figures (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="run the full CPU baseline plan (C1-C5 on the host's cores) and print it")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -585,6 +796,10 @@ def main() -> int:
 
     from relmo_amd import capi, mp
     from relmo_amd import synthetic as syn
+
+    if args.cpu_full:
+        print(json.dumps({"cpu_full": cpu_full(torch, syn)}), flush=True)
+        return 0
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

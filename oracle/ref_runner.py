@@ -49,11 +49,12 @@ def available() -> bool:
 
 def run_reference(calls: list[dict], arrays: dict[str, np.ndarray], timeout: float = 600.0) -> list[dict]:
     """Each call: {"op", "tensors": [names], "ints": [...], optional "repeat",
-    "warmup", "threads"}, or {"op", "args": [spec, ...]} with each spec one of
-    {"tensor": name}, {"tensors": [names]}, {"int": v}, {"ints": [v, ...]}.
+    "warmup", "threads", "keep"}, or {"op", "args": [spec, ...]} with each spec
+    one of {"tensor": name}, {"tensors": [names]}, {"int": v}, {"ints": [v, ...]}.
     Returns per call {"out": ndarray} ({"outs": [ndarray, ...]} for an op
-    returning a tuple) or {"error": str}, plus "times" (seconds per repetition)
-    when "repeat" is given."""
+    returning a tuple; neither with "keep": false, for timing runs) or
+    {"error": str}, plus "times" (seconds per repetition) when "repeat" is
+    given."""
 
     if not available():
         raise FileNotFoundError(f"{REF_LIB} is missing; run `make -C oracle ref` where the reference is present")
@@ -124,7 +125,9 @@ def _child(req_dir: Path) -> None:
             entry["error_type"] = type(exc).__name__
             meta.append(entry)
             continue
-        if isinstance(out, (tuple, list)):
+        if not call.get("keep", True):
+            pass
+        elif isinstance(out, (tuple, list)):
             entry["num_outs"] = len(out)
             for k, o in enumerate(out):
                 outputs[f"out_{i}_{k}"] = o.detach().numpy()

@@ -23,6 +23,7 @@ from dataclasses import dataclass
 
 import torch
 from torch import Tensor, nn
+from torch.utils.checkpoint import checkpoint
 
 from . import mp
 
@@ -240,9 +241,14 @@ class CentralizedRelationalGNN(nn.Module):
     layout, the same object update as RelationalGNN."""
 
     def __init__(self, embedding_size: int, num_layers: int, relations: dict[str, int], mode: int,
-                 condition_dim: int | None = None, slot_mask: bool = True):
+                 condition_dim: int | None = None, slot_mask: bool = True,
+                 recompute_central: bool = False):
         super().__init__()
         self.d = embedding_size
+        # keep only the central module's input per layer and run the module
+        # again in the backward (activation checkpointing): its hidden
+        # activations are ~4x the slot tensor, ~40 GB per layer at 2048 graphs
+        self.recompute_central = recompute_central
         self.num_layers = num_layers
         self.mode = mode
         self.relations = dict(relations)
@@ -298,7 +304,11 @@ class CentralizedRelationalGNN(nn.Module):
         context = torch.cat(ctx, dim=1)
         for _ in range(self.num_layers):
             # [context | argument slots]: the fanout writes into the slots directly
-            outputs = self.central(mp.fanout_concat(context, x, r["obj"], r["flat"], ma))
+            inp = mp.fanout_concat(context, x, r["obj"], r["flat"], ma)
+            if self.recompute_central and torch.is_grad_enabled():
+                outputs = checkpoint(self.central, inp, use_reentrant=False)
+            else:
+                outputs = self.central(inp)
             out_flat = outputs.reshape(nodes * ma, d)
             msgs = fanin_objects(self.mode, out_flat, r, batch.num_objects)
             x = x + self.updater(torch.cat([x, msgs], dim=1))

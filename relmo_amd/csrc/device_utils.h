@@ -135,6 +135,12 @@ __device__ __forceinline__ T neg_inf() { return -__builtin_huge_val(); }
 template <>
 __device__ __forceinline__ float neg_inf<float>() { return -__builtin_huge_valf(); }
 
+// Lowest finite value.
+template <typename T>
+__device__ __forceinline__ T lowest() { return -__DBL_MAX__; }
+template <>
+__device__ __forceinline__ float lowest<float>() { return -__FLT_MAX__; }
+
 template <typename T>
 __device__ __forceinline__ T quiet_nan() { return __builtin_nan(""); }
 template <>

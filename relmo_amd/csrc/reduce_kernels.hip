@@ -170,11 +170,13 @@ struct SumOp {
 #pragma unroll
         for (int i = 0; i < V; ++i) acc.v[i] = head ? T(0) : acc.v[i];
     }
-    __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
+    // Callers repeat the last valid index past `cnt`, so every lane loads a
+    // real row and no load needs a per-slot branch; rows past `cnt` are
+    // never accumulated.
+    __device__ __forceinline__ void load(const int32_t (&idx)[U], int) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + rows(idx[u], D) + col)
-                                      : pack_fill<T, V>(T(0));
+            x[u] = colok ? pack_load<T, V>(table + rows(idx[u], D) + col) : pack_fill<T, V>(T(0));
     }
     __device__ __forceinline__ void consume(int cnt) {
 #pragma unroll
@@ -208,18 +210,23 @@ struct LseOp {
         m = pack_fill<T, V>(neg_inf<T>());
         s = pack_fill<T, V>(T(0));
     }
+    // The walker's segments (restart / add / result) start m at the lowest
+    // finite value instead of -inf: a -inf message then gives exp(-inf) = 0
+    // with no guard (m - x is never -inf - -inf), and a first finite message
+    // still sets s = fma(0, e, 1) = 1 exactly.
     __device__ __forceinline__ void restart(bool head, int64_t) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
-            m.v[i] = head ? neg_inf<T>() : m.v[i];
+            m.v[i] = head ? lowest<T>() : m.v[i];
             s.v[i] = head ? T(0) : s.v[i];
         }
     }
-    __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
+    // as SumOp::load: indices past `cnt` repeat the last valid one
+    __device__ __forceinline__ void load(const int32_t (&idx)[U], int) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            x[u] = (u < cnt && colok) ? pack_load<T, V>(table + row_offset(idx[u], D) + col)
-                                      : pack_fill<T, V>(neg_inf<T>());
+            x[u] = colok ? pack_load<T, V>(table + row_offset(idx[u], D) + col)
+                         : pack_fill<T, V>(neg_inf<T>());
     }
     __device__ __forceinline__ void consume(int cnt) {
 #pragma unroll
@@ -249,27 +256,27 @@ struct LseOp {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             // exp(-|x - m|) is exp(m - x) when x raises the maximum, exp(x - m)
-            // otherwise; a -inf message adds 0 (its difference may be NaN)
+            // otherwise; m is finite or +inf, so a -inf message adds exp(-inf)
+            // = 0 and a NaN message makes s NaN
             const T xv = x[u].v[i];
             const bool up = xv > m.v[i];
             const T d = xv - m.v[i];
-            const T e = xv == neg_inf<T>() ? T(0) : fast_exp<T>(-fabs(d));
+            const T e = fast_exp<T>(-fabs(d));
             s.v[i] = up ? fma(s.v[i], e, T(1)) : s.v[i] + e;
             m.v[i] = up ? xv : m.v[i];
         }
     }
-    // A +inf message makes the reference's exp(x - max) NaN; so does a NaN
-    // message or a segment of -inf only.
-    __device__ __forceinline__ Pack<T, V> result(bool nonempty) const {
+    // Result of a walked segment.  A +inf message makes the reference's
+    // exp(x - max) NaN; so does a NaN message or a segment of -inf only.
+    // Those are exactly the cases where log(s) + m is infinite (m = +inf, or
+    // s = 0 with m the lowest finite value): otherwise m is finite and
+    // 1 <= s <= 65, so m + log(s) cannot round to an infinity.
+    __device__ __forceinline__ Pack<T, V> result(bool) const {
         Pack<T, V> r;
 #pragma unroll
         for (int i = 0; i < V; ++i) {
-            if (!nonempty)
-                r.v[i] = neg_inf<T>();
-            else if (__builtin_isinf(m.v[i]))
-                r.v[i] = quiet_nan<T>();
-            else
-                r.v[i] = dev_log<T>(s.v[i]) + m.v[i];
+            const T v = dev_log<T>(s.v[i]) + m.v[i];
+            r.v[i] = __builtin_isinf(v) ? quiet_nan<T>() : v;
         }
         return r;
     }
@@ -298,13 +305,13 @@ struct LseBwdOp {
     __device__ __forceinline__ void restart(bool head, int64_t key) {
         if (head) begin(key, true);
     }
-    __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
+    // as SumOp::load: indices past `cnt` repeat the last valid one
+    __device__ __forceinline__ void load(const int32_t (&idx)[U], int) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const bool ok = u < cnt && colok;
             const uint64_t off = row_offset(idx[u], D) + col;
-            g[u] = ok ? pack_load<T, V>(grad_out + off) : pack_fill<T, V>(T(0));
-            o[u] = ok ? pack_load<T, V>(out + off) : pack_fill<T, V>(T(0));
+            g[u] = colok ? pack_load<T, V>(grad_out + off) : pack_fill<T, V>(T(0));
+            o[u] = colok ? pack_load<T, V>(out + off) : pack_fill<T, V>(T(0));
         }
     }
     __device__ __forceinline__ void consume(int cnt) {
@@ -558,7 +565,7 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
                     op.restart(lab[u] != prev, key);
                     op.add(u);
                     if (next != lab[u] && op.colok)
-                        pack_store_stream<T, V>(out + key * D + op.col,
+                        pack_store_stream<T, V>(out + row_offset(key, D) + op.col,
                                                 epi(key, op.result(true), D, op.col));
                     prev = lab[u];
                 }

@@ -361,6 +361,27 @@ def test_model_consumers_cpu_lane_matches_aten(monkeypatch) -> None:
             assert torch.allclose(a, b, rtol=1e-5, atol=1e-7), (mode, float(a), float(b))
 
 
+def test_central_recompute_matches_stored_activations() -> None:
+    """Recomputing the central module in the backward (activation
+    checkpointing) gives the same loss and gradients as keeping its
+    activations."""
+
+    from relmo_amd import consumers as C
+
+    batch = C.synthetic_c5("cpu", seed=2, num_graphs=2)
+    for mode in (0, 1, 2):
+        grads = []
+        for recompute in (False, True):
+            torch.manual_seed(0)
+            model = C.CentralizedRelationalGNN(8, 2, batch.relations, mode, recompute_central=recompute)
+            loss = C.train_step(model, batch, model.routing(batch))
+            grads.append((loss, [p.grad.clone() for p in model.parameters()]))
+        (la, ga), (lb, gb) = grads
+        assert torch.equal(la, lb), mode
+        for a, b in zip(ga, gb):
+            torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-8)
+
+
 def test_model_fanin_masks_only_objects_without_messages(mp_env) -> None:
     """Objects without messages get 0 (PyG's aggregators); a NaN or +inf in an
     object's messages still reaches that object's aggregate."""
