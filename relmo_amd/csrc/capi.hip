@@ -414,7 +414,8 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->snap_gather_plain = gathers != nullptr ? l.snap_plain : nullptr;
     plan->max_degree = plan->num_hubs = plan->num_chunks = plan->num_multi_hubs = -1;
     plan->num_items = plan->num_short = -1;
-    RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
+    const SortZero zero = sort_zero_region(sc.sort, num_edges);
+    RELM_HIP(launch_status_init(l.status, s, zero.p, zero.n), "relm_mp status init");
     // The validation result is final after the first sort pass: copy it to
     // the host and mark the point, then enqueue the rest of the build.
     auto mark_validation = [&]() -> hipError_t {

@@ -43,6 +43,7 @@ constexpr int kItemSize = RELM_MP_ITEM_SIZE;
 constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys per block
+constexpr int kSortMaxPasses = 4;                     // 32-bit keys, <= 8-bit digits
 constexpr int kSortBins = 256;
 constexpr int kSnapTile = RELM_MP_SNAP_TILE;
 static_assert(kSnapTile == kSortTile, "the sort's first pass writes the snapshot tiles");
@@ -59,7 +60,9 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // ---- plan kernels (plan_kernels.hip) -------------------------------------
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
-hipError_t launch_status_init(DevStatus* st, hipStream_t s);
+// Resets the status; also zeroes `nclear` words at `clear` (sort_zero_region).
+hipError_t launch_status_init(DevStatus* st, hipStream_t s, uint32_t* clear = nullptr,
+                              int64_t nclear = 0);
 // Copies *st to pinned host memory through its device mapping; with `pc`,
 // also stores the inverse-plan statistics (collisions, identity) there.
 hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped,
@@ -95,6 +98,13 @@ struct SortBuffers {
 };
 int64_t sort_tiles(int64_t n);
 size_t sort_hist_words(int64_t n);
+// The words of buf.hist that must be zero when sort_by_key starts (the
+// counting kernels add their per-chunk digit sums there with atomics).
+struct SortZero {
+    uint32_t* p;
+    int64_t n;
+};
+SortZero sort_zero_region(const SortBuffers& buf, int64_t n);
 // after_validation (may be null) is called once the first pass is enqueued:
 // from then on, in stream order, `st` holds the validation result.
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,

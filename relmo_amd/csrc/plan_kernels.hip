@@ -31,7 +31,10 @@ __global__ __launch_bounds__(kThreads) void k_fill_i32(int32_t* __restrict__ p, 
         p[i] = value;
 }
 
-__global__ void k_status_init(DevStatus* st) {
+// Resets the status and zeroes `nclear` words (counters that later kernels
+// add to with atomics).
+__global__ void k_status_init(DevStatus* st, uint32_t* __restrict__ clear, int64_t nclear) {
+    for (int64_t i = threadIdx.x; i < nclear; i += blockDim.x) clear[i] = 0u;
     if (threadIdx.x == 0) {
         st->bad_key_edge = kNoEdge;
         st->bad_gather_edge = kNoEdge;
@@ -184,34 +187,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict
 // tile chunk [c * kColChunk, (c + 1) * kColChunk): for each tile those counts
 // are one 128-byte line, so every load is a full line (digit-major counts
 // written by concurrent tiles on different XCDs would be partial lines).
-// Thread t handles digit 32g + t % 32 over kColItems consecutive tiles.  Two
-// launches: the chunk sums (k_hist_chunk_sums), then each chunk adds the sums
-// of the chunks before it (k_scan_cols).
+// Thread t handles digit 32g + t % 32 over kColItems consecutive tiles.  The
+// chunk sums come from the counting kernels (atomics into chunk_sum); each
+// chunk adds the sums of the chunks before it.
 constexpr int kColDigits = 32;
 constexpr int kColItems = 16;
 constexpr int kColLanes = kScanThreads / kColDigits;  // tile lanes per digit
 constexpr int kColChunk = kColLanes * kColItems;      // tiles per workgroup
-
-__global__ __launch_bounds__(kScanThreads) void k_hist_chunk_sums(const uint32_t* __restrict__ hist,
-                                                                  int64_t ntiles,
-                                                                  uint32_t* __restrict__ chunk_sum) {
-    __shared__ uint32_t part[kColLanes][kColDigits];
-    const int dl = static_cast<int>(threadIdx.x) % kColDigits;
-    const int tl = static_cast<int>(threadIdx.x) / kColDigits;
-    const int64_t d = static_cast<int64_t>(blockIdx.x) * kColDigits + dl;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kColChunk + static_cast<int64_t>(tl) * kColItems;
-    uint32_t sum = 0;
-#pragma unroll
-    for (int i = 0; i < kColItems; ++i) sum += t0 + i < ntiles ? hist[(t0 + i) * kSortBins + d] : 0u;
-    part[tl][dl] = sum;
-    __syncthreads();
-    if (tl == 0) {
-        uint32_t total = 0;
-#pragma unroll
-        for (int l = 0; l < kColLanes; ++l) total += part[l][dl];
-        chunk_sum[static_cast<int64_t>(blockIdx.y) * kSortBins + d] = total;
-    }
-}
 
 __global__ __launch_bounds__(kScanThreads) void k_scan_cols(uint32_t* __restrict__ hist,
                                                             int64_t ntiles,
@@ -252,6 +234,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_cols(uint32_t* __restrict
 
 // ---- radix sort ----------------------------------------------------------
 
+// The tile's count of digit threadIdx.x: its row of the tile-major counts
+// and, when the tiles form more than one column chunk, the running sum of its
+// chunk (chunk_sum, zeroed before the sort).
+__device__ __forceinline__ void store_tile_counts(uint32_t* __restrict__ hist,
+                                                  uint32_t* __restrict__ chunk_sum, uint32_t t) {
+    hist[static_cast<int64_t>(blockIdx.x) * kSortBins + threadIdx.x] = t;
+    if (chunk_sum != nullptr && t != 0u)
+        atomicAdd(chunk_sum + static_cast<int64_t>(blockIdx.x / kColChunk) * kSortBins + threadIdx.x, t);
+}
+
 // Tile digit histogram in LDS: kSubHists copies per wave (lane & 3), so that
 // lanes holding the same digit - frequent for hub keys - rarely hit the same
 // address; plain LDS atomics, no cross-lane matching.
@@ -284,6 +276,7 @@ __device__ __forceinline__ uint32_t hist_total(const uint32_t* h) {
 // scatter generates its values.
 using i64x2 = int64_t __attribute__((ext_vector_type(2)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 
 // One index checked against its bound: the narrowed value (0 if bad), the
 // smallest bad edge so far.
@@ -298,7 +291,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
     const int64_t* __restrict__ keys, const int64_t* __restrict__ gathers, int64_t n, int shift,
     int bits, int64_t key_bound, int64_t gather_bound, uint32_t* __restrict__ keys32,
     uint32_t* __restrict__ vals32, uint32_t* __restrict__ tile_plain, uint32_t* __restrict__ hist,
-    int64_t nblocks, DevStatus* __restrict__ st) {
+    uint32_t* __restrict__ chunk_sum, int64_t nblocks, DevStatus* __restrict__ st) {
     __shared__ uint32_t h[(kSortThreads / kWave) * kSubHists * kSortBins];
     hist_clear(h);
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
@@ -379,7 +372,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
         if (any) atomicOr(&st->gather_mismatch, 1ull);
     }
     __syncthreads();
-    hist[static_cast<int64_t>(blockIdx.x) * kSortBins + threadIdx.x] = hist_total(h);
+    store_tile_counts(hist, chunk_sum, hist_total(h));
 }
 
 // Per-tile digit histogram of the narrowed keys, written tile-major:
@@ -391,23 +384,43 @@ template <int BITS>
 __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* __restrict__ keys,
                                                                 int64_t n, int shift,
                                                                 uint32_t* __restrict__ hist,
+                                                                uint32_t* __restrict__ chunk_sum,
                                                                 int64_t nblocks) {
     constexpr int kWaves = kSortThreads / kWave;
     __shared__ uint32_t h[kWaves * kSortBins];
     for (int i = static_cast<int>(threadIdx.x); i < kWaves * kSortBins; i += kSortThreads) h[i] = 0;
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
     constexpr uint32_t dmask = (1u << BITS) - 1u;
+    // Counting ignores the order, so a full tile is read as 16-byte loads
+    // (thread t holds elements 4 * (j * 256 + t) + {0..3}); a partial tile
+    // element by element, with the elements past n inactive.
     uint32_t key[kSortItems];
+    int valid = kSortItems;
+    if (base + kSortTile <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0) {
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
-        key[i] = p < n ? keys[p] : 0u;
+        for (int j = 0; j < kSortItems / 4; ++j) {
+            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                keys + base + 4 * (static_cast<int64_t>(j) * kSortThreads + threadIdx.x)));
+            key[4 * j] = v.x;
+            key[4 * j + 1] = v.y;
+            key[4 * j + 2] = v.z;
+            key[4 * j + 3] = v.w;
+        }
+    } else {
+        valid = 0;
+#pragma unroll
+        for (int i = 0; i < kSortItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
+            key[i] = p < n ? keys[p] : 0u;
+            valid += p < n ? 1 : 0;
+        }
     }
     __syncthreads();
     uint32_t* wh = h + (static_cast<int>(threadIdx.x) / kWave) * kSortBins;
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
-        const bool active = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x < n;
+        // partial tiles: thread t's valid elements are its first `valid`
+        const bool active = i < valid;
         const uint32_t d = (key[i] >> shift) & dmask;
         const unsigned long long peers = match_digit<BITS>(d, __ballot(active));
         if (active && (peers & lanemask_lt()) == 0) wh[d] += static_cast<uint32_t>(__popcll(peers));
@@ -416,7 +429,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
     uint32_t t = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) t += h[w * kSortBins + threadIdx.x];
-    hist[static_cast<int64_t>(blockIdx.x) * kSortBins + threadIdx.x] = t;
+    store_tile_counts(hist, chunk_sum, t);
 }
 
 // Stable scatter of one tile.  Wave w owns tile positions [w*1024, (w+1)*1024)
@@ -702,45 +715,64 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
             if (at >= 0 && at < chunk_capacity) chunk_hub[at] = static_cast<int32_t>(slot);
         }
     }
-    if (k > num_keys) return;
     // S[k]: short messages before k; W[k] = k + S[k]
+    const bool live = k <= num_keys;
     const int64_t hub_before = static_cast<int64_t>(counts[3 * stride + blockIdx.x]) + ie - f.hub_edges;
-    const int64_t S = static_cast<int64_t>(offsets[k]) - hub_before;
-    const int64_t W = k + S;
-    int64_t Wprev = -1;
-    if (k > 0) {
-        const int64_t dprev = static_cast<int64_t>(offsets[k]) - offsets[k - 1];
-        Wprev = W - 1 - (dprev > 0 && dprev <= kHubThreshold ? dprev : 0);
-    }
-    short_off[k] = static_cast<int32_t>(S);
-    // items j with Wprev < j * kItemSize <= W; the key past the end also closes
-    // the last used item (j = W / kItemSize + 1)
-    const int64_t j0 = Wprev < 0 ? 0 : Wprev / kItemSize + 1;
-    int64_t j1 = k == num_keys ? W / kItemSize + 1 : W / kItemSize;
-    if (j1 > item_capacity) j1 = item_capacity;
-    for (int64_t j = j0; j <= j1; ++j) {
-        item_first[j] = static_cast<int32_t>(k);
-        item_short[j] = static_cast<int32_t>(S);
-    }
-    if (k == num_keys) {
-        st->total_weight = static_cast<unsigned long long>(W);
-        pc->num_items = min(W / kItemSize + 1, item_capacity);
-        pc->num_short = W - num_keys;
-        return;
-    }
-    // the short segment's gathered rows, back to back in key order (without
-    // hubs that is gather_sorted itself: nothing to copy, the walker reads it)
-    if (totals[0] != 0 && f.deg > 0 && f.deg <= kHubThreshold) {
-        const int64_t b = offsets[k];
-        int64_t j = 0;
-        for (; j + 4 <= f.deg; j += 4) {
-            const int32_t a0 = gs[b + j], a1 = gs[b + j + 1], a2 = gs[b + j + 2], a3 = gs[b + j + 3];
-            short_gather[S + j] = a0;
-            short_gather[S + j + 1] = a1;
-            short_gather[S + j + 2] = a2;
-            short_gather[S + j + 3] = a3;
+    const int64_t S = live ? static_cast<int64_t>(offsets[k]) - hub_before : 0;
+    if (live) {
+        const int64_t W = k + S;
+        int64_t Wprev = -1;
+        if (k > 0) {
+            const int64_t dprev = static_cast<int64_t>(offsets[k]) - offsets[k - 1];
+            Wprev = W - 1 - (dprev > 0 && dprev <= kHubThreshold ? dprev : 0);
         }
-        for (; j < f.deg; ++j) short_gather[S + j] = gs[b + j];
+        short_off[k] = static_cast<int32_t>(S);
+        // items j with Wprev < j * kItemSize <= W; the key past the end also
+        // closes the last used item (j = W / kItemSize + 1)
+        const int64_t j0 = Wprev < 0 ? 0 : Wprev / kItemSize + 1;
+        int64_t j1 = k == num_keys ? W / kItemSize + 1 : W / kItemSize;
+        if (j1 > item_capacity) j1 = item_capacity;
+        for (int64_t j = j0; j <= j1; ++j) {
+            item_first[j] = static_cast<int32_t>(k);
+            item_short[j] = static_cast<int32_t>(S);
+        }
+        if (k == num_keys) {
+            st->total_weight = static_cast<unsigned long long>(W);
+            pc->num_items = min(W / kItemSize + 1, item_capacity);
+            pc->num_short = W - num_keys;
+        }
+    }
+    // The short segments' gathered rows, back to back in key order (without
+    // hubs that is gather_sorted itself: nothing to copy, the walker reads
+    // it).  The workgroup's keys own one contiguous range of short_gather;
+    // its threads copy that range position by position (coalesced), each
+    // finding its key among the workgroup's segment starts in LDS.
+    if (totals[0] == 0) return;  // uniform over the grid
+    __shared__ int32_t seg_start[kThreads + 1];
+    __shared__ int32_t seg_src[kThreads];
+    const bool short_key = live && k < num_keys && f.deg > 0 && f.deg <= kHubThreshold;
+    __shared__ int64_t blk_s0;  // S of the workgroup's first key (always live)
+    if (threadIdx.x == 0) blk_s0 = S;
+    __syncthreads();
+    const int64_t base = blk_s0;
+    seg_start[threadIdx.x] = static_cast<int32_t>(live ? S - base : 0);
+    seg_src[threadIdx.x] = short_key ? offsets[k] : 0;
+    // the end of the workgroup's range: the last live key's start plus its
+    // short messages
+    const int64_t last = min(static_cast<int64_t>(blockIdx.x) * kThreads + kThreads - 1, num_keys);
+    if (k == last) seg_start[kThreads] = static_cast<int32_t>(S - base + (short_key ? f.deg : 0));
+    __syncthreads();
+    const int nlive = static_cast<int>(last - static_cast<int64_t>(blockIdx.x) * kThreads + 1);
+    const int total = seg_start[kThreads];
+    for (int j = static_cast<int>(threadIdx.x); j < total; j += kThreads) {
+        // the last key whose start is <= j (a key of no short messages shares
+        // its start with the next key, so the last such key has messages)
+        int lo = 0, hi = nlive;  // seg_start[lo] <= j < seg_start[hi] (hi == nlive: the end)
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (seg_start[mid] <= j) lo = mid; else hi = mid;
+        }
+        short_gather[base + j] = gs[static_cast<int64_t>(seg_src[lo]) + (j - seg_start[lo])];
     }
 }
 
@@ -753,8 +785,8 @@ hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s) 
     return hipGetLastError();
 }
 
-hipError_t launch_status_init(DevStatus* st, hipStream_t s) {
-    hipLaunchKernelGGL(k_status_init, dim3(1), dim3(64), 0, s, st);
+hipError_t launch_status_init(DevStatus* st, hipStream_t s, uint32_t* clear, int64_t nclear) {
+    hipLaunchKernelGGL(k_status_init, dim3(1), dim3(256), 0, s, st, clear, nclear);
     return hipGetLastError();
 }
 
@@ -773,13 +805,22 @@ hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_
     return hipGetLastError();
 }
 
+SortZero sort_zero_region(const SortBuffers& buf, int64_t n) {
+    const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
+    const int64_t chunks = (nblocks + kColChunk - 1) / kColChunk;
+    if (n <= 0 || chunks <= 1) return {nullptr, 0};
+    return {buf.hist + static_cast<int64_t>(kSortBins) * (nblocks + 1),
+            static_cast<int64_t>(kSortBins) * kSortMaxPasses * chunks};
+}
+
 int64_t sort_tiles(int64_t n) { return std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile); }
 
 size_t sort_hist_words(int64_t n) {
     const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
     const int64_t chunks = (nblocks + kColChunk - 1) / kColChunk;
-    // per-tile digit counts, the digit totals, the per-chunk digit sums
-    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks + 1 + chunks);
+    // per-tile digit counts, the digit totals, the per-chunk digit sums of
+    // every pass (zeroed together before the sort)
+    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks + 1 + kSortMaxPasses * chunks);
 }
 
 namespace {
@@ -814,7 +855,8 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
     const int64_t hist_n = static_cast<int64_t>(kSortBins) * nblocks;
     uint32_t* digit_tot = buf.hist + hist_n;
     const int64_t col_chunks = (nblocks + kColChunk - 1) / kColChunk;
-    uint32_t* chunk_sum = digit_tot + kSortBins;
+    // per pass: the chunk sums (zeroed by launch_status_init; a single chunk
+    // has no chunks before it and needs none)
     // the narrowed input goes to the n buffers (the plan's snapshot); pass p
     // writes a, b, a, ... and the last pass the plan arrays
     const uint32_t* in_k = buf.keys_n;
@@ -826,14 +868,15 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         uint32_t* out_k = last ? keys_out : (p % 2 == 0 ? buf.keys_a : buf.keys_b);
         uint32_t* out_v = last ? vals_out : (p % 2 == 0 ? buf.vals_a : buf.vals_b);
         const dim3 grid(static_cast<unsigned>(nblocks)), block(kSortThreads);
+        uint32_t* chunk_sum = col_chunks > 1 ? digit_tot + kSortBins + p * col_chunks * kSortBins : nullptr;
         if (p == 0) {
             hipLaunchKernelGGL(k_radix_narrow, grid, block, 0, s, keys, gathers, n, shift, width,
                                key_bound, gather_bound, buf.keys_n, buf.vals_n, buf.tile_plain,
-                               buf.hist, nblocks, st);
+                               buf.hist, chunk_sum, nblocks, st);
         } else {
             with_digit_bits(width, [&](auto bt) {
                 hipLaunchKernelGGL((k_radix_upsweep<decltype(bt)::value>), grid, block, 0, s, in_k, n,
-                                   shift, buf.hist, nblocks);
+                                   shift, buf.hist, chunk_sum, nblocks);
             });
         }
         hipError_t err = hipGetLastError();
@@ -843,12 +886,6 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
             if (err != hipSuccess) return err;
         }
         const dim3 cgrid(kSortBins / kColDigits, static_cast<unsigned>(col_chunks));
-        if (col_chunks > 1) {  // a single chunk has no chunks before it
-            hipLaunchKernelGGL(k_hist_chunk_sums, cgrid, dim3(kScanThreads), 0, s,
-                               static_cast<const uint32_t*>(buf.hist), nblocks, chunk_sum);
-            err = hipGetLastError();
-            if (err != hipSuccess) return err;
-        }
         hipLaunchKernelGGL(k_scan_cols, cgrid, dim3(kScanThreads), 0, s, buf.hist, nblocks,
                            static_cast<const uint32_t*>(chunk_sum), digit_tot);
         err = hipGetLastError();
