@@ -594,7 +594,7 @@ def host_info(torch) -> dict:
             "rocm": rocm}
 
 
-def cpu_full(torch, syn) -> dict:
+def cpu_full(torch, syn, parts: set[str]) -> dict:
     """The full CPU baseline plan, on the host's cores (``--cpu-full``; minutes
     of CPU work, so not part of the default run):
 
@@ -608,11 +608,7 @@ def cpu_full(torch, syn) -> dict:
         on the ATen model path (RELM_MP_ENABLE=0), at the job's share,
         graphs/sec of one step after one warmup step."""
 
-    import numpy as np
-
     from oracle import ref_runner
-    from relmo_amd import consumers as C
-    from relmo_amd import mp_pack
 
     full = host_threads()
     threads = (1, full)
@@ -658,7 +654,20 @@ def cpu_full(torch, syn) -> dict:
             torch.autograd.grad(fn(x), x, g)
         return step
 
-    # ---- C1 ------------------------------------------------------------------------
+    if "c1" in parts:
+        res["c1"] = cpu_c1(torch, syn, aten, ref, grad_of, threads, have_ref)
+    if "c2" in parts:
+        res["c2"] = cpu_c2(torch, syn, ref, threads, have_ref)
+    if "c3" in parts:
+        res["c3"] = cpu_c3(torch, syn, ref, threads, have_ref)
+    if parts & {"c4", "c5"}:
+        res.update(cpu_models(torch, full, parts))
+    return res
+
+
+def cpu_c1(torch, syn, aten, ref, grad_of, threads, have_ref) -> dict:
+    from relmo_amd import mp_pack
+
     log("CPU C1 ...")
     d = syn.c1_ops("cpu")
     objects, slots = d["objects"], d["slots"]
@@ -681,20 +690,38 @@ def cpu_full(torch, syn) -> dict:
                  ("fanin_reduce_sum_backward", "fanin_reduce_sum_backward", ["grad_obj", "flat_src", "dst"], [slots])]
         got = ref(specs, arrays, 80, 20)
         c1["reference_us"] = {th: {k: round(v * 1e6, 1) for k, v in got[th].items()} for th in threads}
-    res["c1"] = c1
+    return c1
 
-    # ---- C2 ------------------------------------------------------------------------
+
+def cpu_c2(torch, syn, ref, threads, have_ref) -> dict:
+    from relmo_amd import mp_pack
+
     log("CPU C2 ...")
     d = syn.c2_fanin("cpu")
     K, E, D = d["dim_size"], d["rel"].size(0), d["rel"].size(1)
     lse_bytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_lse_bwd(E, D, K, E)
     sum_bytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_sum_bwd(E, D, K, E)
     c2: dict = {"bytes_lse_fwd_bwd": lse_bytes, "bytes_sum_fwd_bwd": sum_bytes, "python_only_s": {}}
+    saved = torch.get_num_threads()
     for th in threads:
-        c2["python_only_s"][th] = {
-            mode: round(aten(grad_of(lambda r, m=m: mp_pack.fanin_reduce_python(r, d["flat_src"], d["dst"], K, m),
-                                     d["rel"], d["grad_out"]), th, 1, 0), 3)
-            for mode, m in (("logsumexp_fwd_bwd", 1), ("sum_fwd_bwd", 0))}
+        c2["python_only_s"][th] = {}
+        torch.set_num_threads(th)
+        for mode, m in (("logsumexp", 1), ("sum", 0)):
+            # forward, then the autograd backward, each reported as it ends
+            r = d["rel"].clone().requires_grad_(True)
+            t0 = time.perf_counter()
+            out = mp_pack.fanin_reduce_python(r, d["flat_src"], d["dst"], K, m)
+            fwd = time.perf_counter() - t0
+            log(f"  python_only C2 {mode} forward, {th} threads: {fwd:.2f} s")
+            t0 = time.perf_counter()
+            torch.autograd.grad(out, r, d["grad_out"])
+            bwd = time.perf_counter() - t0
+            log(f"  python_only C2 {mode} backward, {th} threads: {bwd:.2f} s")
+            del r, out
+            c2["python_only_s"][th][f"{mode}_fwd"] = round(fwd, 3)
+            c2["python_only_s"][th][f"{mode}_bwd"] = round(bwd, 3)
+            c2["python_only_s"][th][f"{mode}_fwd_bwd"] = round(fwd + bwd, 3)
+    torch.set_num_threads(saved)
     if have_ref:
         out = mp_pack.fanin_reduce_python(d["rel"], d["flat_src"], d["dst"], K, 1)
         arrays = {"rel": d["rel"].numpy(), "src": d["flat_src"].numpy(), "dst": d["dst"].numpy(),
@@ -712,20 +739,33 @@ def cpu_full(torch, syn) -> dict:
     c2["python_only_gbs"] = {th: {"logsumexp_fwd_bwd": round(gbs(lse_bytes, v["logsumexp_fwd_bwd"]), 3),
                                   "sum_fwd_bwd": round(gbs(sum_bytes, v["sum_fwd_bwd"]), 3)}
                              for th, v in c2["python_only_s"].items()}
-    res["c2"] = c2
-    del d
+    return c2
 
-    # ---- C3 ------------------------------------------------------------------------
+
+def cpu_c3(torch, syn, ref, threads, have_ref) -> dict:
+    from relmo_amd import mp_pack
+
     log("CPU C3 ...")
     d = syn.c3_fanout("cpu")
     R, D = d["x"].shape
     S = d["out_rows"]
     c3_bytes = syn.bytes_fanout_fwd(S, D, S) + syn.bytes_fanout_bwd(S, D, R)
     c3: dict = {"bytes_fwd_bwd": c3_bytes, "python_only_s": {}}
+    saved = torch.get_num_threads()
     for th in threads:
-        c3["python_only_s"][th] = round(aten(grad_of(
-            lambda x: mp_pack.fanout_scatter_python(x, d["src"], d["flat_dst"], S), d["x"], d["grad_out"]),
-            th, 1, 0), 3)
+        torch.set_num_threads(th)
+        x = d["x"].clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        out = mp_pack.fanout_scatter_python(x, d["src"], d["flat_dst"], S)
+        fwd = time.perf_counter() - t0
+        log(f"  python_only C3 forward, {th} threads: {fwd:.2f} s")
+        t0 = time.perf_counter()
+        torch.autograd.grad(out, x, d["grad_out"])
+        bwd = time.perf_counter() - t0
+        log(f"  python_only C3 backward, {th} threads: {bwd:.2f} s")
+        del x, out
+        c3["python_only_s"][th] = round(fwd + bwd, 3)
+    torch.set_num_threads(saved)
     if have_ref:
         arrays = {"x": d["x"].numpy(), "src": d["src"].numpy(), "flat": d["flat_dst"].numpy(),
                   "g": d["grad_out"].numpy()}
@@ -737,22 +777,31 @@ def cpu_full(torch, syn) -> dict:
                                for th in threads}
         del arrays
     c3["python_only_gbs"] = {th: round(gbs(c3_bytes, v), 3) for th, v in c3["python_only_s"].items()}
-    res["c3"] = c3
-    del d
+    return c3
 
-    # ---- C4 / C5 on the ATen model path ---------------------------------------------
+
+def cpu_models(torch, full: int, parts: set[str]) -> dict:
+    """C4 / C5 training steps on the ATen model path at `full` threads."""
+
+    from relmo_amd import consumers as C
+
+    res = {}
     saved_env = os.environ.get("RELM_MP_ENABLE")
     os.environ["RELM_MP_ENABLE"] = "0"
     saved_threads = torch.get_num_threads()
     torch.set_num_threads(full)
     try:
-        for name, batch, make, modes in (
-            ("c4", C.synthetic_c4("cpu"), lambda b, m: C.RelationalGNN(32, 10, b.relations, m),
+        for name, batch_fn, make, modes in (
+            ("c4", lambda: C.synthetic_c4("cpu"), lambda b, m: C.RelationalGNN(32, 10, b.relations, m),
              ((0, "sum"), (1, "logsumexp"))),
-            ("c5", C.synthetic_c5("cpu", num_graphs=64), lambda b, m: C.CentralizedRelationalGNN(128, 10, b.relations, m),
+            ("c5", lambda: C.synthetic_c5("cpu", num_graphs=64),
+             lambda b, m: C.CentralizedRelationalGNN(128, 10, b.relations, m),
              ((0, "sum"), (1, "logsumexp"), (2, "mean"))),
         ):
+            if name not in parts:
+                continue
             log(f"CPU {name} ...")
+            batch = batch_fn()
             entry: dict = {"graphs": batch.num_graphs, "objects": batch.num_objects, "threads": full}
             for m, mode in modes:
                 torch.manual_seed(0)
@@ -763,6 +812,7 @@ def cpu_full(torch, syn) -> dict:
                 C.train_step(model, batch, routing)
                 t = time.perf_counter() - t0
                 entry[mode] = {"s_step": round(t, 3), "graphs_per_sec": round(batch.num_graphs / t, 2)}
+                log(f"  {name} {mode}: {t:.2f} s per step")
             res[name] = entry
     finally:
         torch.set_num_threads(saved_threads)
@@ -783,8 +833,9 @@ def main() -> int:
                     default=None,
                     help="run one workload only and print its figures (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-full", action="store_true",
-                    help="run the full CPU baseline plan (C1-C5 on the host's cores) and print it")
+    ap.add_argument("--cpu-full", nargs="?", const="c1,c2,c3,c4,c5", default=None, metavar="PARTS",
+                    help="run the full CPU baseline plan on the host's cores and print it: all of "
+                         "C1-C5, or the comma-separated parts named")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -798,7 +849,12 @@ def main() -> int:
     from relmo_amd import synthetic as syn
 
     if args.cpu_full:
-        print(json.dumps({"cpu_full": cpu_full(torch, syn)}), flush=True)
+        parts = {p.strip().lower() for p in args.cpu_full.split(",") if p.strip()}
+        unknown = parts - {"c1", "c2", "c3", "c4", "c5"}
+        if unknown:
+            print(f"--cpu-full: unknown parts {sorted(unknown)}", file=sys.stderr)
+            return 2
+        print(json.dumps({"cpu_full": cpu_full(torch, syn, parts)}), flush=True)
         return 0
 
     if not torch.cuda.is_available():

@@ -62,12 +62,13 @@ def run_reference(calls: list[dict], arrays: dict[str, np.ndarray], timeout: flo
         tmpd = Path(tmp)
         np.savez(tmpd / "inputs.npz", **arrays)
         (tmpd / "request.json").write_text(json.dumps(calls))
+        # the child's stderr passes through: timing runs report each call
         proc = subprocess.run(
             [sys.executable, str(Path(__file__).resolve()), str(tmpd)],
-            capture_output=True, text=True, timeout=timeout,
+            stdout=subprocess.PIPE, text=True, timeout=timeout,
         )
         if proc.returncode != 0:
-            raise RuntimeError(f"reference runner failed:\n{proc.stdout}\n{proc.stderr}")
+            raise RuntimeError(f"reference runner failed (exit {proc.returncode}):\n{proc.stdout}")
         meta = json.loads((tmpd / "result.json").read_text())
         outs = np.load(tmpd / "outputs.npz", allow_pickle=False)
         results = []
@@ -145,6 +146,8 @@ def _child(req_dir: Path) -> None:
                 fn(*tensors, *ints)
                 times.append(time.perf_counter() - t0)
             entry["times"] = times
+            print(f"reference {op}: {len(times)} timed calls at {entry['threads']} threads, "
+                  f"median {sorted(times)[len(times) // 2]:.4f} s", file=sys.stderr, flush=True)
         meta.append(entry)
     np.savez(req_dir / "outputs.npz", **outputs)
     (req_dir / "result.json").write_text(json.dumps(meta))
