@@ -5,8 +5,12 @@ the ``cpu_baseline`` leg of bench.py as the checker.  The product package
 (``relmo_amd``) never imports it.
 
 Each wrapper restates one reference CPU routine (see the C file for the
-file:line of relmo's ``src/_ops/mp/mp_ops.cpp`` it follows) and raises
-``OracleIndexError`` with the reference's message for an index out of range.
+file:line of relmo's ``src/_ops/mp/mp_ops.cpp`` it follows) and raises the
+reference's error for an index out of range: ``OracleIndexError`` with the
+loop message of the sum and copy ops, and for the logsumexp ops (ATen call
+sequences there) ATen's errors in call order - ``IndexError`` from
+index_select, ``OracleIndexError`` with ATen's message from scatter_reduce_ /
+index_add_.
 
 Parity status of each function (how it is pinned, see tests/test_oracle.py):
   fanout_scatter                  pinned: reference library (oracle/_ref) bit-exact,
@@ -172,11 +176,36 @@ def fanin_reduce_sum(rel_flat, flat_src, dst_idx, dim_size: int) -> np.ndarray:
     return out
 
 
+def _outside(idx: np.ndarray, size: int) -> np.ndarray:
+    return (idx < 0) | (idx >= size)
+
+
+def _aten_index_select_check(idx: np.ndarray, rows: int) -> None:
+    """ATen's index_select on the CPU: IndexError for any index outside the rows."""
+
+    if np.any(_outside(idx, rows)):
+        raise IndexError("index out of range in self")
+
+
+def _aten_scatter_check(idx: np.ndarray, size: int) -> None:
+    """ATen's scatter_reduce_ / index_add_ on the CPU: the first index outside
+    [0, size) in edge order."""
+
+    bad = np.flatnonzero(_outside(idx, size))
+    if bad.size:
+        raise OracleIndexError(f"index {int(idx[bad[0]])} is out of bounds for dimension 0 with size {size}")
+
+
 def fanin_reduce_logsumexp(rel_flat, flat_src, dst_idx, dim_size: int) -> np.ndarray:
-    """mp_ops.cpp:3019-3035 (the CPU ATen sequence, restated with libm exp/log)."""
+    """mp_ops.cpp:3019-3035 (the CPU ATen sequence, restated with libm exp/log).
+    An index out of range raises ATen's error of the call that meets it first:
+    index_select over flat_src, then scatter_reduce_ over dst_idx."""
 
     r = _vals(rel_flat)
     src, dst = _idx(flat_src), _idx(dst_idx)
+    if src.size and dim_size and r.shape[1]:
+        _aten_index_select_check(src, r.shape[0])
+        _aten_scatter_check(dst, int(dim_size))
     out = np.empty((int(dim_size), r.shape[1]), dtype=r.dtype)
     bad = _Bad()
     fn = getattr(lib(), "oracle_fanin_reduce_logsumexp_" + _suffix(r))
@@ -211,10 +240,18 @@ def fanin_reduce_sum_backward(grad_out, flat_src, dst_idx, rel_rows: int) -> np.
 
 
 def fanin_reduce_logsumexp_backward(grad_out, rel_flat, flat_src, dst_idx, out, rel_rows: int) -> np.ndarray:
-    """mp_ops.cpp:2981-3003 (ATen fallback sequence, edge order)."""
+    """mp_ops.cpp:2981-3003 (ATen fallback sequence, edge order).  An index out
+    of range raises ATen's error of the call that meets it first: index_select
+    of rel_flat rows (flat_src), of out and grad_out rows (dst_idx), then
+    index_add_ into the rel_rows gradient rows (flat_src)."""
 
     g, r, o = _vals(grad_out), _vals(rel_flat), _vals(out)
     src, dst = _idx(flat_src), _idx(dst_idx)
+    if src.size and rel_rows and g.shape[1]:
+        _aten_index_select_check(src, r.shape[0])
+        _aten_index_select_check(dst, o.shape[0])
+        _aten_index_select_check(dst, g.shape[0])
+        _aten_scatter_check(src, int(rel_rows))
     res = np.empty((int(rel_rows), g.shape[1]), dtype=r.dtype)
     bad = _Bad()
     fn = getattr(lib(), "oracle_fanin_reduce_logsumexp_backward_" + _suffix(r))

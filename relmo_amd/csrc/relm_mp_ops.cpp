@@ -105,8 +105,7 @@ Tensor byte_buffer(size_t bytes, const Tensor& like) {
 //
 // A plan (relm_mp.h) lives in a byte tensor on the device together with a
 // snapshot of the indices it was built from.  PlanRef holds it with the
-// stream that built it and an event recorded behind the build, so that work
-// on another stream can wait for the plan.
+// stream that built it, so that work on another stream can wait for the plan.
 //
 // The cache keeps recent plans.  A plan is served to a later call only when
 // that call's index arrays equal the plan's snapshot: one device pass compares
@@ -137,31 +136,32 @@ struct PlanRef : torch::CustomClassHolder {
     int device = -1;
     int64_t key_bound = 0;
     int64_t gather_bound = 0;
-    hipStream_t stream = nullptr;
-    hipEvent_t built = nullptr;
+    hipStream_t stream = nullptr;  // the stream the plan was built on
 
     PlanRef() = default;
     PlanRef(const PlanRef&) = delete;
     PlanRef& operator=(const PlanRef&) = delete;
-    ~PlanRef() {
-        if (built != nullptr) (void)hipEventDestroy(built);
-    }
 
     bool defined() const { return plan.kind != 0; }
 
-    // Records the end of the build on its stream (after the build's last
-    // kernel has been enqueued).
-    void mark_built() {
-        if (built == nullptr)
-            check_hip(hipEventCreateWithFlags(&built, hipEventDisableTiming), "plan event");
-        check_hip(hipEventRecord(built, stream), "plan event record");
-    }
-
     // Work enqueued on `s` from now on waits for the build, and the plan
-    // memory is not handed out again before that work has finished.
+    // memory is not handed out again before that work has finished.  The
+    // wait is on an event recorded on the build stream now, behind the
+    // build and whatever followed it there (no event is recorded at build
+    // time: a marker between the build and its own stream's next kernel
+    // would stall that stream).
     void use_on(hipStream_t s) const {
         if (s == stream || !mem.defined()) return;
-        check_hip(hipStreamWaitEvent(s, built, 0), "plan stream wait");
+        hipEvent_t ev = nullptr;
+        check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "plan event");
+        hipError_t err = hipEventRecord(ev, stream);
+        if (err == hipSuccess) err = hipStreamWaitEvent(s, ev, 0);
+        (void)hipEventDestroy(ev);  // released once the wait has been resolved
+        if (err != hipSuccess) {
+            // the build stream is gone: everything it ran has finished
+            (void)hipGetLastError();
+            check_hip(hipDeviceSynchronize(), "plan stream sync");
+        }
         c10::hip::HIPCachingAllocator::recordStream(
             mem.storage().data_ptr(), c10::hip::getStreamFromExternal(s, device));
     }
@@ -362,7 +362,6 @@ PlanPtr inverse_plan(const Tensor& key, int64_t key_bound, const char* key_name,
                                     gather.data_ptr<int64_t>(), gather_bound, gather_name,
                                     gather_first ? 1 : 0, key.numel(), flags, r->mem.data_ptr(),
                                     static_cast<size_t>(r->mem.numel()), &r->plan, s));
-    r->mark_built();
     cache.insert(r, key, &gather);
     return r;
 }
@@ -381,7 +380,6 @@ PlanPtr csr_build(int role, const Tensor& key, int64_t key_bound, const char* ke
         gather != nullptr ? gather->data_ptr<int64_t>() : nullptr, gather_bound, gather_name,
         gather_first ? 1 : 0, n, r->mem.data_ptr(), static_cast<size_t>(r->mem.numel()),
         scratch.data_ptr(), static_cast<size_t>(scratch.numel()), &r->plan, s));
-    r->mark_built();
     PlanCache::get().insert(r, key, gather);
     return r;
 }
@@ -432,7 +430,6 @@ void fanout_inverse(const Tensor& d_idx, int64_t out_rows, const Tensor& s_idx, 
     const int rc = gather(r->plan);
     raise_if(relm_mp_plan_validate(&r->plan));
     raise_if(rc);
-    r->mark_built();
     cache.insert(r, d_idx, &s_idx);
 }
 
@@ -531,6 +528,40 @@ Tensor fanout_scatter_backward_from_gpu(const Tensor& grad, const Tensor& src, c
 
 // fanin_reduce on the GPU; *plan_out (if given) receives the forward's CSR
 // plan (keys dst_idx, gathers flat_src) for the backward.
+// The reference's CPU lane computes logsumexp with ATen calls
+// (mp_ops.cpp:2981-3035), so an index out of range raises ATen's errors, in
+// the order of those calls: index_select raises IndexError "index out of
+// range in self"; scatter_reduce_ and index_add_ raise "index i is out of
+// bounds for dimension 0 with size n" for the first bad index in edge order.
+// The GPU lane validates on the device; when a logsumexp op's plan build
+// reports a bad index, these restate the reference's error for it.
+bool any_outside(const Tensor& idx, int64_t size) {
+    return ((idx < 0) | (idx >= size)).any().item<bool>();
+}
+
+void raise_first_outside(const Tensor& idx, int64_t size) {
+    const Tensor bad = ((idx < 0) | (idx >= size)).nonzero();
+    if (bad.numel() == 0) return;
+    const int64_t v = idx[bad[0][0].item<int64_t>()].item<int64_t>();
+    TORCH_CHECK(false, "index ", v, " is out of bounds for dimension 0 with size ", size);
+}
+
+// mp_ops.cpp:3019-3035: rel_flat.index_select(flat_src), then scatter_reduce_ over dst_idx.
+void raise_lse_forward_index_error(const Tensor& s_idx, int64_t rel_rows, const Tensor& d_idx,
+                                   int64_t dim_size) {
+    TORCH_CHECK_INDEX(!any_outside(s_idx, rel_rows), "index out of range in self");
+    raise_first_outside(d_idx, dim_size);
+}
+
+// mp_ops.cpp:2981-3003: rel_flat / out / grad_out index_select, then index_add_ into
+// the rel_rows gradient rows.
+void raise_lse_backward_index_error(const Tensor& s_idx, int64_t rel_flat_rows, const Tensor& d_idx,
+                                    int64_t out_rows, int64_t rel_rows) {
+    TORCH_CHECK_INDEX(!any_outside(s_idx, rel_flat_rows), "index out of range in self");
+    TORCH_CHECK_INDEX(!any_outside(d_idx, out_rows), "index out of range in self");
+    raise_first_outside(s_idx, rel_rows);
+}
+
 Tensor fanin_reduce_gpu(const Tensor& rel_flat, const Tensor& flat_src, const Tensor& dst_idx,
                         int64_t dim_size, int64_t mode, PlanPtr* plan_out = nullptr) {
     c10::OptionalDeviceGuard guard(rel_flat.device());
@@ -546,7 +577,13 @@ Tensor fanin_reduce_gpu(const Tensor& rel_flat, const Tensor& flat_src, const Te
     const Tensor s_idx = contiguous(flat_src);
     const Tensor d_idx = contiguous(dst_idx);
     hipStream_t stream = current_stream(rel);
-    PlanPtr gp = csr_plan(d_idx, dim_size, "dst_idx", s_idx, rel.size(0), "flat_src", true, stream);
+    PlanPtr gp;
+    try {
+        gp = csr_plan(d_idx, dim_size, "dst_idx", s_idx, rel.size(0), "flat_src", true, stream);
+    } catch (const c10::Error&) {
+        if (mode == kModeLogSumExp) raise_lse_forward_index_error(s_idx, rel.size(0), d_idx, dim_size);
+        throw;
+    }
     Tensor out = at::empty({dim_size, emb}, rel_flat.options());
     Tensor scratch = compute_scratch(gp->plan, emb, dtype_code(rel), mode, rel);
     raise_if(relm_mp_plan_segment_reduce(dtype_code(rel), &gp->plan, nullptr, rel.data_ptr(), emb,
@@ -645,15 +682,29 @@ Tensor fanin_reduce_logsumexp_backward_gpu(const Tensor& grad_out, const Tensor&
         return grad_rel;
     }
     if (key_bound < rel_rows) grad_rel.narrow(0, key_bound, rel_rows - key_bound).zero_();
-    PlanPtr inv = inverse_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true,
-                               stream);
+    const auto reference_error = [&]() {
+        raise_lse_backward_index_error(s_idx, rel.size(0), d_idx, o.size(0), rel_rows);
+    };
+    PlanPtr inv;
+    try {
+        inv = inverse_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true, stream);
+    } catch (const c10::Error&) {
+        reference_error();
+        throw;
+    }
     if (inv->plan.collisions == 0) {
         raise_if(relm_mp_plan_logsumexp_backward(dt, &inv->plan, d_idx.data_ptr<int64_t>(),
                                                  g.data_ptr(), o.data_ptr(), rel.data_ptr(), emb,
                                                  grad_rel.data_ptr(), nullptr, 0, stream));
         return grad_rel;
     }
-    PlanPtr gp = csr_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true, stream);
+    PlanPtr gp;
+    try {
+        gp = csr_plan(s_idx, key_bound, "flat_src", d_idx, g.size(0), "dst_idx", true, stream);
+    } catch (const c10::Error&) {
+        reference_error();
+        throw;
+    }
     Tensor scratch = compute_scratch(gp->plan, emb, dt, kModeSum, g);
     raise_if(relm_mp_plan_logsumexp_backward(dt, &gp->plan, nullptr, g.data_ptr(), o.data_ptr(),
                                              rel.data_ptr(), emb, grad_rel.data_ptr(),

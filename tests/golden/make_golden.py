@@ -204,6 +204,10 @@ def add_edge_cases(b: Builder) -> None:
     b.case("e7_err_fanout_bwd", "fanout_scatter_backward", ["t1_g", "e7_bad_src", "e7_bad_dst"], [7])
     b.case("e7_err_sum_bwd", "fanin_reduce_sum_backward", ["t3_g", "e7_neg", "e7_big_dst"], [10])
     b.case("e7_err_mode", "fanin_reduce", ["t3_rel", "t3_src", "t3_dst"], [4, 2])
+    # logsumexp runs as ATen calls in the reference's CPU lane: their errors, in call order
+    b.case("e7_err_lse_neg_src", "fanin_reduce", ["t3_rel", "e7_neg", "t3_dst"], [4, 1])
+    b.case("e7_err_lse_dst", "fanin_reduce", ["t3_rel", "t3_src", "e7_big_dst"], [4, 1])
+    b.case("e7_err_lse_both", "fanin_reduce", ["t3_rel", "e7_neg", "e7_big_dst"], [4, 1])
     # empty inputs
     b.arr("e8_empty_idx", np.zeros(0, dtype=np.int64))
     b.case("e8_fanout_empty", "fanout_scatter", ["t1_x", "e8_empty_idx", "e8_empty_idx"], [6])
@@ -237,6 +241,21 @@ def add_logsumexp_backward_cases(b: Builder, outputs: dict[str, np.ndarray]) -> 
         outputs["expected_" + case["name"]] = res["out"]
         case["expected"] = "expected_" + case["name"]
         b.cases.append(case)
+    # bad indices in the backward (e6: 16 rel rows, 3 objects, 6 messages): a
+    # message row past rel_flat, an object past out, a message row inside
+    # rel_flat but past rel_rows
+    b.idx("e9_src_past_rel", [4, 9, 1, 16, 0, 7])
+    b.idx("e9_dst_past_out", [0, 2, 3, 1, 0, 0])
+    errors = [
+        ("e9_err_lse_bwd_src", ["e6_lse_fwd_gout", "e6_rel", "e9_src_past_rel", "e6_dst", "e6_lse_fwd_out"], [16]),
+        ("e9_err_lse_bwd_dst", ["e6_lse_fwd_gout", "e6_rel", "e6_src", "e9_dst_past_out", "e6_lse_fwd_out"], [16]),
+        ("e9_err_lse_bwd_rows", ["e6_lse_fwd_gout", "e6_rel", "e6_src", "e6_dst", "e6_lse_fwd_out"], [8]),
+    ]
+    calls = [{"op": "fanin_reduce_logsumexp_backward", "tensors": t, "ints": i} for _n, t, i in errors]
+    for (name, tensors, ints), res in zip(errors, ref_runner.run_reference(calls, b.arrays)):
+        assert "error" in res, (name, res)
+        b.cases.append({"name": name, "op": "fanin_reduce_logsumexp_backward", "tensors": tensors,
+                        "ints": ints, "error": res["error"], "error_type": res["error_type"]})
 
 
 def main() -> None:

@@ -105,9 +105,10 @@ def _cpu_sum_parity(op: str, args: list, got: np.ndarray, want: np.ndarray, name
 def _check_case(fn, case: dict, arrays: dict, exact: bool) -> None:
     args = [torch.from_numpy(arrays[n]) for n in case["tensors"]] + list(case["ints"])
     if "error" in case:
-        with pytest.raises((RuntimeError, ValueError)) as info:
+        with pytest.raises((RuntimeError, ValueError, IndexError)) as info:
             fn(*args)
         assert str(info.value).splitlines()[0] == case["error"], case["name"]
+        assert (case.get("error_type") == "IndexError") == isinstance(info.value, IndexError), case["name"]
         return
     got = fn(*args).numpy()
     want = arrays[case["expected"]]

@@ -31,9 +31,10 @@ def test_oracle_matches_every_golden_case(golden) -> None:
         args = [arrays[n] for n in case["tensors"]] + list(case["ints"])
         fn = ORACLE_OPS[case["op"]]
         if "error" in case:
-            with pytest.raises((RuntimeError, ValueError)) as info:
+            with pytest.raises((RuntimeError, ValueError, IndexError)) as info:
                 fn(*args)
             assert str(info.value) == case["error"], case["name"]
+            assert (case.get("error_type") == "IndexError") == isinstance(info.value, IndexError), case["name"]
             continue
         got = fn(*args)
         want = arrays[case["expected"]]
