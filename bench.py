@@ -271,7 +271,10 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
     layer, ten layers) are recomputed in the backward from the saved layer
     input (activation checkpointing), which keeps the step under one GPU's
     288 GB; the recompute is one extra central-MLP forward per layer, inside
-    the timed step."""
+    the timed step.  The MLP's first Linear runs per object and is gathered
+    per relation node (CentralizedRelationalGNN._central_gathered: the same
+    function, a ninth of its multiply-adds at C5); the step on the assembled
+    input is reported beside it ("assembled_input")."""
 
     from relmo_amd import consumers as C
 
@@ -282,22 +285,30 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects, "emb": 32, "layers": 10}
         modes = ((0, "sum"), (1, "logsumexp"))
     else:
+        log("  generating the C5 batch (2048 graphs)")
         batch = C.synthetic_c5(dev)
-        make = lambda mode: C.CentralizedRelationalGNN(128, 10, batch.relations, mode,
-                                                       recompute_central=True).to(dev)
+        make = lambda mode: C.CentralizedRelationalGNN(128, 10, batch.relations, mode, recompute_central=True,
+                                                       gather_first_linear=True).to(dev)
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects,
                "relation_nodes": int(sum(a.size(0) for a in batch.atoms.values())), "emb": 128,
-               "layers": 10, "central_mlp": "recomputed in the backward (activation checkpointing)"}
+               "layers": 10, "central_mlp": "recomputed in the backward (activation checkpointing)",
+               "first_linear": "per object, gathered per relation node (fanin sum over the slot edges)"}
         modes = ((0, "sum"), (1, "logsumexp"), (2, "mean"))
     res = {"config": cfg}
-    for mode, name in modes:
+    variants = [(mode, name, True) for mode, name in modes]
+    if which == "c5":  # the module on the assembled input, for comparison (sum)
+        variants.append((0, "assembled_input_sum", False))
+    for mode, name, gathered in variants:
         torch.manual_seed(0)
         model = make(mode)
+        if which == "c5":
+            model.gather_first_linear = gathered
         routing = model.routing(batch)
         torch.cuda.reset_peak_memory_stats()
         t = timed(lambda: C.train_step(model, batch, routing), steps, warmup, torch.cuda.synchronize)
         res[name] = {"ms_step": t * 1e3, "graphs_per_sec": batch.num_graphs / t,
                      "peak_gb": torch.cuda.max_memory_allocated() / 1e9}
+        log(f"  {which} {name}: {t * 1e3:.1f} ms per step")
         del model, routing
         torch.cuda.empty_cache()
     if which == "c4":

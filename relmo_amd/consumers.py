@@ -242,9 +242,12 @@ class CentralizedRelationalGNN(nn.Module):
 
     def __init__(self, embedding_size: int, num_layers: int, relations: dict[str, int], mode: int,
                  condition_dim: int | None = None, slot_mask: bool = True,
-                 recompute_central: bool = False):
+                 recompute_central: bool = False, gather_first_linear: bool = False):
         super().__init__()
         self.d = embedding_size
+        # evaluate the central MLP's first Linear per object and gather it per
+        # relation node instead of assembling [cond | mask | slots] (_central_gathered)
+        self.gather_first_linear = gather_first_linear
         # keep only the central module's input per layer and run the module
         # again in the backward (activation checkpointing): its hidden
         # activations are ~4x the slot tensor, ~40 GB per layer at 2048 graphs
@@ -285,15 +288,75 @@ class CentralizedRelationalGNN(nn.Module):
                 flat.append(node * self.max_arity + pos)
                 obj.append(args[:, pos])
             start += n
-        obj_t = torch.cat(obj)
-        return {"meta": meta, "nodes": start, "flat": torch.cat(flat), "obj": obj_t,
-                "deg": _object_degrees(obj_t, batch.num_objects)}
+        obj_t, flat_t = torch.cat(obj), torch.cat(flat)
+        ma = self.max_arity
+        # the slot edges of the gathered first Linear: slot (node, pos) reads
+        # row obj * max_arity + pos of the per-object products
+        return {"meta": meta, "nodes": start, "flat": flat_t, "obj": obj_t,
+                "deg": _object_degrees(obj_t, batch.num_objects),
+                "slot_src": obj_t * ma + flat_t % ma, "slot_node": flat_t // ma}
+
+    def _central_gathered(self, x: Tensor, r: dict) -> Tensor:
+        """The central module on [cond | slot mask | slots] per relation node,
+        without assembling that input (fused.py:311-375 assembles it, then runs
+        the module).  Its first Linear is linear in each slot: the weight
+        columns of slot position a are applied once per object (x @ W_a^T for
+        all positions in one GEMM) and each node adds the products of the
+        objects in its slots - a fanin sum over the slot edges (at most
+        max_arity messages per node, in slot order).  The condition and mask
+        columns are constant per predicate, so their part of the Linear and
+        FiLM's gamma / beta are evaluated on the per-predicate table and
+        broadcast over each predicate's range of nodes (nodes are ordered by
+        predicate; a broadcast's backward is a sum over the range, where a
+        gather by node would accumulate millions of rows into a handful).
+        The result equals self.central(input) up to fp32 rounding (another
+        summation order)."""
+
+        film = self.central.module
+        ma, d, md = self.max_arity, self.d, self.mask_dim
+        lin = film.lins[0]
+        width = lin.out_features
+        nodes = r["nodes"]
+        table = self.cond.weight
+        w = lin.weight
+        if md:
+            const = torch.addmm(lin.bias, self.slot_mask, w[:, :md].t())  # [predicates, width]
+        else:
+            const = lin.bias.unsqueeze(0).expand(table.size(0), width)
+        w_slots = w[:, md:].reshape(width, ma, d).transpose(0, 1).reshape(ma * width, d)
+        per_object = (x @ w_slots.t()).view(-1, width)  # row obj * ma + a: x[obj] @ W_a^T
+        s = mp.fanin_reduce(per_object, r["slot_src"], r["slot_node"], nodes, 0)
+
+        def film_step(pre: Tensor, gamma: Tensor, beta: Tensor, add: Tensor | None) -> Tensor:
+            parts = []
+            for _p, start, n, _a, ci in r["meta"]:
+                v = pre[start:start + n]
+                parts.append(film.act(torch.addcmul(beta[ci], gamma[ci], v if add is None else v + add[ci])))
+            return torch.cat(parts) if len(parts) > 1 else parts[0]
+
+        h = film_step(s, film.gammas[0](table), film.betas[0](table), const)
+        for lin_k, g_k, b_k in zip(film.lins[1:], film.gammas[1:], film.betas[1:]):
+            h = film_step(lin_k(h), g_k(table), b_k(table), None)
+        out = film.out(h)
+        # Residual: the slots themselves (the fanout into a dense slot table)
+        slots = mp.fanout_scatter(x, r["obj"], r["flat"], nodes * ma).view(nodes, ma * d)
+        return slots + out
 
     def forward(self, batch: RelationalBatch, routing: dict | None = None) -> Tensor:
         r = routing or self.routing(batch)
         ref = self.cond.weight
         x = ref.new_zeros(batch.num_objects, self.d)
         nodes, ma, d = r["nodes"], self.max_arity, self.d
+        recompute = self.recompute_central and torch.is_grad_enabled()
+        if self.gather_first_linear:
+            for _ in range(self.num_layers):
+                if recompute:
+                    outputs = checkpoint(self._central_gathered, x, r, use_reentrant=False)
+                else:
+                    outputs = self._central_gathered(x, r)
+                msgs = fanin_objects(self.mode, outputs.reshape(nodes * ma, d), r, batch.num_objects)
+                x = x + self.updater(torch.cat([x, msgs], dim=1))
+            return x
         # context columns [cond | slot mask] per relation node, built once per
         # forward and shared by the layers (fused.py:311-340)
         cond_rows = torch.cat([torch.full((n,), ci, dtype=torch.long, device=ref.device)
@@ -305,7 +368,7 @@ class CentralizedRelationalGNN(nn.Module):
         for _ in range(self.num_layers):
             # [context | argument slots]: the fanout writes into the slots directly
             inp = mp.fanout_concat(context, x, r["obj"], r["flat"], ma)
-            if self.recompute_central and torch.is_grad_enabled():
+            if recompute:
                 outputs = checkpoint(self.central, inp, use_reentrant=False)
             else:
                 outputs = self.central(inp)

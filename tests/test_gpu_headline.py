@@ -236,13 +236,15 @@ def _step_grads(C, model, batch, routing, enable: str, monkeypatch):
                          if p.grad is not None}
 
 
-@pytest.mark.parametrize("model", ["c4", "c5"])
+@pytest.mark.parametrize("model", ["c4", "c5", "c5_gathered"])
 def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     """One training step: the HIP lane (fp32) is at least as close to a float64
     run of the same step as the ATen lane (fp32) is - per parameter, the
     relative L2 error of the gradient within twice the ATen lane's, and the
     loss within twice the ATen lane's loss error, each plus 8 fp32 ulps
-    (relative).  Sum and logsumexp; mean for C5."""
+    (relative).  Sum and logsumexp; mean for C5.  c5_gathered runs the central
+    MLP's first Linear per object and gathered (both fp32 lanes), against the
+    float64 run of the module on the assembled input."""
 
     import copy
 
@@ -254,7 +256,9 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
         modes = (0, 1)
     else:
         batch = C.synthetic_c5(DEV, seed=5, num_graphs=96)
-        make = lambda mode: C.CentralizedRelationalGNN(128, 10, batch.relations, mode).to(DEV)  # noqa: E731
+        gathered = model == "c5_gathered"
+        make = lambda mode: C.CentralizedRelationalGNN(  # noqa: E731
+            128, 10, batch.relations, mode, gather_first_linear=gathered).to(DEV)
         modes = (0, 1, 2)
     for mode in modes:
         _log(f"{model} mode={mode}: {batch.num_graphs} graphs, {batch.num_objects} objects")
@@ -264,6 +268,7 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
         loss_hip, g_hip = _step_grads(C, m, batch, routing, "1", monkeypatch)
         loss_aten, g_aten = _step_grads(C, m, batch, routing, "0", monkeypatch)
         m64 = copy.deepcopy(m).double()
+        m64.gather_first_linear = False
         loss64, g64 = _step_grads(C, m64, batch, routing, "0", monkeypatch)
         e_hip, e_aten = abs(loss_hip - loss64), abs(loss_aten - loss64)
         _log(f"  loss {loss64:.8g}: |hip - f64| {e_hip:.3g}, |aten - f64| {e_aten:.3g}")
