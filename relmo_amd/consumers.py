@@ -327,10 +327,13 @@ class CentralizedRelationalGNN(nn.Module):
         per_object = (x @ w_slots.t()).view(-1, width)  # row obj * ma + a: x[obj] @ W_a^T
         s = mp.fanin_reduce(per_object, r["slot_src"], r["slot_node"], nodes, 0)
 
+        sizes = [n for _p, _s, n, _a, _c in r["meta"]]
+
         def film_step(pre: Tensor, gamma: Tensor, beta: Tensor, add: Tensor | None) -> Tensor:
+            # torch.split, not slicing: the backward of a split is one
+            # concatenation, that of each slice a zero-filled full-size gradient
             parts = []
-            for _p, start, n, _a, ci in r["meta"]:
-                v = pre[start:start + n]
+            for v, (_p, _s, _n, _a, ci) in zip(torch.split(pre, sizes), r["meta"]):
                 parts.append(film.act(torch.addcmul(beta[ci], gamma[ci], v if add is None else v + add[ci])))
             return torch.cat(parts) if len(parts) > 1 else parts[0]
 

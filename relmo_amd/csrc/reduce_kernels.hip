@@ -946,13 +946,18 @@ struct Geometry {
     int64_t slices;
 };
 
+// Dense rows: the widest of kVecMax, kVecMax / 2 and 1 elements per lane that
+// divides D and keeps every row start aligned (rows of an even number of
+// floats that is not a multiple of 4 still move 8 bytes per lane).
 template <typename T>
 Geometry choose_geometry(int64_t D, std::initializer_list<const void*> ptrs) {
     constexpr int kVecMax = 16 / static_cast<int>(sizeof(T));
     int V = kVecMax;
-    if (D % V != 0) V = 1;
-    for (const void* p : ptrs) {
-        if (p != nullptr && reinterpret_cast<uintptr_t>(p) % (sizeof(T) * V) != 0) V = 1;
+    for (; V > 1; V /= 2) {
+        bool ok = D % V == 0;
+        for (const void* p : ptrs)
+            ok = ok && (p == nullptr || reinterpret_cast<uintptr_t>(p) % (sizeof(T) * V) == 0);
+        if (ok) break;
     }
     const int64_t vcols = (D + V - 1) / V;
     int G = 4;
@@ -976,6 +981,9 @@ int with_geometry(const Geometry& geo, F&& f) {
     };
     constexpr int kVecMax = 16 / static_cast<int>(sizeof(T));
     if (geo.V == kVecMax) return by_g(std::integral_constant<int, kVecMax>{});
+    if constexpr (kVecMax > 2) {
+        if (geo.V == kVecMax / 2) return by_g(std::integral_constant<int, kVecMax / 2>{});
+    }
     return by_g(std::integral_constant<int, 1>{});
 }
 

@@ -338,7 +338,7 @@ def _segments_bounded(keys: np.ndarray, bound: int = 64) -> bool:
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
-@pytest.mark.parametrize("emb", [1, 3, 4, 5, 32, 64, 128, 200, 300])
+@pytest.mark.parametrize("emb", [1, 2, 3, 4, 5, 6, 32, 64, 128, 200, 300, 398])
 def test_random_parity_all_ops(dtype, emb: int) -> None:
     from relmo_amd import capi
 
@@ -387,11 +387,15 @@ def _zipf_keys(rng, num_keys: int, n: int, s: float = 1.1) -> np.ndarray:
     return rng.permutation(num_keys)[np.minimum(r, num_keys - 1)]
 
 
-def test_hub_segments_against_float64_truth() -> None:
+@pytest.mark.parametrize("emb", [32, 6])
+def test_hub_segments_against_float64_truth(emb: int) -> None:
+    """emb 32 moves 16 bytes per lane, emb 6 (rows of an even number of floats
+    that is not a multiple of 4) 8 bytes."""
+
     from relmo_amd import capi
 
     rng = np.random.default_rng(12)
-    num_keys, n, emb = 20_000, 600_000, 32
+    num_keys, n = 20_000, 600_000
     dst = _zipf_keys(rng, num_keys, n)
     rel = (2.0 * rng.standard_normal((n, emb))).astype(np.float32)
     flat_src = rng.permutation(n)
