@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <string>
 
 #include "internal.h"
@@ -103,17 +104,55 @@ struct PendingCheck {
     int64_t gather_bound = 0;
     std::string gather_name;
     int gather_checked_first = 0;
+    int32_t gen = 0;           // the status publication to wait for
+    hipStream_t stream = nullptr;
 };
 
 struct HostSlot {
     int device = -1;
-    hipEvent_t ready = nullptr;
     DevStatus* status = nullptr;         // host address
     DevStatus* status_mapped = nullptr;  // the same memory as the device addresses it
     relm_mp_plan_counts* counts = nullptr;
-    int32_t* match = nullptr;  // host address, kMaxMatch flags
+    int32_t* match = nullptr;         // host address: kMaxMatch flags, then the generation word
+    int32_t* match_mapped = nullptr;  // the same words as the device addresses them
+    int32_t match_gen = 0;            // generation of the last plan match from this slot
+    int32_t* status_gen = nullptr;         // host address of the status publication word
+    int32_t* status_gen_mapped = nullptr;  // the same word as the device addresses it
+    int32_t status_issued = 0;             // generation of the last status publication
     PendingCheck pending;
+
+    // Enqueues the publication of `st` (and, with pc, the inverse-plan
+    // statistics) to this slot's host status; returns its generation.
+    hipError_t publish_status(const DevStatus* st, relm_mp_plan_counts* pc, hipStream_t s,
+                              int32_t* gen) {
+        *gen = static_cast<int32_t>(static_cast<uint32_t>(status_issued) + 1u);
+        status_issued = *gen;
+        return launch_status_publish(st, status_mapped, pc, status_gen_mapped, *gen, s);
+    }
 };
+
+// Waits until the device has stored `want` into *word (host memory mapped for
+// the device, written with a system-scope release behind the data it
+// guards).  Spins, checking the stream every 1024 polls: a failed stream, or
+// one that has drained without the store, is an error.
+int wait_host_word(const int32_t* word, int32_t want, hipStream_t s, const char* what) {
+    for (uint64_t spin = 1;; ++spin) {
+        if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == want) return RELM_MP_OK;
+        if ((spin & 1023) == 0) {
+            const hipError_t q = hipStreamQuery(s);
+            if (q == hipSuccess) {
+                if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == want) return RELM_MP_OK;
+                return set_error(RELM_MP_ERR_HIP, std::string(what) + ": the device did not publish its result");
+            }
+            if (q != hipErrorNotReady) {
+                (void)hipGetLastError();
+                return set_error(RELM_MP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(q));
+            }
+            if (spin > (1ull << 20)) std::this_thread::yield();
+        }
+        __builtin_ia32_pause();
+    }
+}
 
 int no_pending(const HostSlot* hs) {
     if (hs->pending.active)
@@ -135,13 +174,10 @@ int host_slot(HostSlot** out) {
     }
     for (HostSlot& h : slots) {
         if (h.device < 0) {
-            // default system-scope release on record: the status stores of
-            // the kernel before it are visible once the event has completed
-            RELM_HIP(hipEventCreateWithFlags(&h.ready, hipEventDisableTiming), "relm_mp event");
             void* mem = nullptr;
             RELM_HIP(hipHostMalloc(&mem,
                                    sizeof(DevStatus) + sizeof(relm_mp_plan_counts) +
-                                       kMaxMatch * sizeof(int32_t),
+                                       (kMaxMatch + 2) * sizeof(int32_t),
                                    hipHostMallocDefault),
                      "relm_mp pinned status");
             h.status = static_cast<DevStatus*>(mem);
@@ -150,6 +186,12 @@ int host_slot(HostSlot** out) {
             void* mapped = nullptr;
             RELM_HIP(hipHostGetDevicePointer(&mapped, mem, 0), "relm_mp pinned status mapping");
             h.status_mapped = static_cast<DevStatus*>(mapped);
+            h.match_mapped = reinterpret_cast<int32_t*>(static_cast<char*>(mapped) +
+                                                        (reinterpret_cast<char*>(h.match) - static_cast<char*>(mem)));
+            h.match[kMaxMatch] = 0;
+            h.status_gen = h.match + kMaxMatch + 1;
+            h.status_gen_mapped = h.match_mapped + kMaxMatch + 1;
+            *h.status_gen = 0;
             h.device = dev;
             *out = &h;
             return RELM_MP_OK;
@@ -323,8 +365,8 @@ int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     RELM_HIP(launch_inv_build(keys, key_bound, gathers, gather_bound, num_edges, l.inv, snap,
                               l.status, s),
              "relm_mp inverse plan kernel");
-    RELM_HIP(launch_status_publish(l.status, hs->status_mapped, l.counts, s), "relm_mp status publish");
-    RELM_HIP(hipEventRecord(hs->ready, s), "relm_mp status event");
+    int32_t gen = 0;
+    RELM_HIP(hs->publish_status(l.status, l.counts, s, &gen), "relm_mp status publish");
     if (!wait) {
         PendingCheck& p = hs->pending;
         p.active = true;
@@ -336,9 +378,11 @@ int inv_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
         p.gather_bound = gather_bound;
         p.gather_name = gather_name != nullptr ? gather_name : "index";
         p.gather_checked_first = gather_checked_first;
+        p.gen = gen;
+        p.stream = s;
         return RELM_MP_OK;
     }
-    RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
+    RELM_TRY(wait_host_word(hs->status_gen, gen, s, "relm_mp status wait"));
     const DevStatus host = *hs->status;
     RELM_TRY(check_validation(host, keys, key_bound, key_name, gathers, gather_bound, gather_name,
                               gather_checked_first));
@@ -353,7 +397,7 @@ int validate_pending(relm_mp_plan* plan) {
     PendingCheck& p = hs->pending;
     if (!p.active || p.plan_counts != plan->counts) return RELM_MP_OK;
     p.active = false;
-    RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
+    RELM_TRY(wait_host_word(hs->status_gen, p.gen, p.stream, "relm_mp status wait"));
     const DevStatus host = *hs->status;
     RELM_TRY(check_validation(host, p.keys, p.key_bound, p.key_name.c_str(), p.gathers,
                               p.gather_bound, p.gather_name.c_str(), p.gather_checked_first));
@@ -416,12 +460,12 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->num_items = plan->num_short = -1;
     const SortZero zero = sort_zero_region(sc.sort, num_edges);
     RELM_HIP(launch_status_init(l.status, s, zero.p, zero.n), "relm_mp status init");
-    // The validation result is final after the first sort pass: copy it to
-    // the host and mark the point, then enqueue the rest of the build.
+    // The validation result is final after the first sort pass: publish it
+    // to the host, then enqueue the rest of the build.
+    int32_t status_gen = 0;
     auto mark_validation = [&]() -> hipError_t {
         if (hs == nullptr) return hipSuccess;
-        hipError_t e = launch_status_publish(l.status, hs->status_mapped, nullptr, s);
-        return e != hipSuccess ? e : hipEventRecord(hs->ready, s);
+        return hs->publish_status(l.status, nullptr, s, &status_gen);
     };
     if (num_edges > 0) {
         RELM_HIP(sort_by_key(keys, key_bound, gathers, gather_bound, num_edges, sc.sort,
@@ -442,7 +486,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
              "relm_mp key index kernels");
     DevStatus host{};
     if (hs != nullptr) {
-        RELM_HIP(hipEventSynchronize(hs->ready), "relm_mp status wait");
+        RELM_TRY(wait_host_word(hs->status_gen, status_gen, s, "relm_mp status wait"));
         host = *hs->status;
     } else {
         RELM_HIP(hipMemcpyAsync(&host, l.status, sizeof(DevStatus), hipMemcpyDeviceToHost, s),
@@ -591,11 +635,13 @@ int relm_mp_plan_match(const int64_t* keys, const int64_t* gathers, int64_t n,
     RELM_TRY(host_slot(&hs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     int32_t* flags = static_cast<int32_t*>(workspace);
-    RELM_HIP(launch_plan_match(keys, gathers, n, cand, num, flags, s), "relm_mp plan match kernel");
-    RELM_HIP(hipMemcpyAsync(hs->match, flags, kMaxMatch * sizeof(int32_t), hipMemcpyDeviceToHost, s),
-             "relm_mp plan match copy");
-    RELM_HIP(hipStreamSynchronize(s), "relm_mp plan match sync");
-    for (int32_t j = 0; j < num; ++j) match[slot[j]] = hs->match[j] == 0 ? 1 : 0;
+    // a new generation per call (the previous one is still in the host word)
+    const int32_t gen = static_cast<int32_t>(static_cast<uint32_t>(hs->match_gen) + 1u);
+    hs->match_gen = gen;
+    RELM_HIP(launch_plan_match(keys, gathers, n, cand, num, flags, gen, hs->match_mapped, s),
+             "relm_mp plan match kernel");
+    RELM_TRY(wait_host_word(hs->match + kMaxMatch, gen, s, "relm_mp plan match"));
+    for (int32_t j = 0; j < num; ++j) match[slot[j]] = hs->match[j] == gen ? 0 : 1;
     return RELM_MP_OK;
 }
 

@@ -63,10 +63,13 @@ hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
 // Resets the status; also zeroes `nclear` words at `clear` (sort_zero_region).
 hipError_t launch_status_init(DevStatus* st, hipStream_t s, uint32_t* clear = nullptr,
                               int64_t nclear = 0);
-// Copies *st to pinned host memory through its device mapping; with `pc`,
-// also stores the inverse-plan statistics (collisions, identity) there.
+// Copies *st to pinned host memory through its device mapping, then stores
+// `gen` to *host_gen (also mapped host memory) with a system-scope release,
+// for the host to poll; with `pc`, also stores the inverse-plan statistics
+// (collisions, identity) there.
 hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped,
-                                 relm_mp_plan_counts* pc, hipStream_t s);
+                                 relm_mp_plan_counts* pc, int32_t* host_gen, int32_t gen,
+                                 hipStream_t s);
 // Index snapshot written by a plan build (relm_mp_plan::snap_*): int32 per
 // edge, tiles of kSnapTile edges whose values are their edge ids flagged in
 // the plain arrays and not stored.  Null members are not written.
@@ -143,12 +146,16 @@ hipError_t launch_pack_index(const relm_mp_index_part* parts, int num_parts, int
 
 // ---- content comparison (match_kernels.hip) -------------------------------
 constexpr int kMaxMatch = RELM_MP_MAX_MATCH;
-// mismatch[0..kMaxMatch) is cleared, then mismatch[c] != 0 iff the snapshot of
-// plans[c] differs from (keys, gathers) (gathers null: keys only; every plan
-// has num_edges == n).
+// After the launches mismatch[c] == gen iff the snapshot of plans[c] differs
+// from (keys, gathers) (gathers null: keys only; every plan has num_edges ==
+// n).  mismatch is not cleared first: a word left from an earlier call that
+// happens to equal gen only reads as a difference (a rebuild, never a stale
+// plan).  Then the num_plans words and, last, `gen` itself (a system-scope
+// release) are stored to host_words[0..num_plans] and host_words[kMaxMatch]:
+// host memory mapped for the device, which the host polls.
 hipError_t launch_plan_match(const int64_t* keys, const int64_t* gathers, int64_t n,
                              const relm_mp_plan* const* plans, int num_plans, int32_t* mismatch,
-                             hipStream_t s);
+                             int32_t gen, int32_t* host_words, hipStream_t s);
 
 // ---- compute kernels (reduce_kernels.hip) --------------------------------
 int compute_gather_last(int dtype, const relm_mp_plan& plan, const int64_t* gathers,

@@ -26,7 +26,7 @@ struct MatchLaunch {
 using i64x2 = int64_t __attribute__((ext_vector_type(2)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 
-// mismatch[c] becomes nonzero when plan c's snapshot differs from (keys,
+// mismatch[c] becomes gen when plan c's snapshot differs from (keys,
 // gathers) at some edge.  One snapshot tile per workgroup round (tile = block
 // + round * grid; the grid covers every tile once for up to 2^16 tiles).  A
 // workgroup first reads the flags of the candidates still live (device-scope
@@ -42,7 +42,7 @@ __global__ __launch_bounds__(kThreads) void k_plan_match(const int64_t* __restri
                                                          const int64_t* __restrict__ gathers,
                                                          int64_t n, MatchLaunch L,
                                                          int32_t* __restrict__ mismatch,
-                                                         int64_t spread) {
+                                                         int32_t gen, int64_t spread) {
     constexpr int kPairs = kPerThread / 2;
     __shared__ int s_live;
     __shared__ int s_diff;
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(kThreads) void k_plan_match(const int64_t* __restri
         if (threadIdx.x == 0) {
             int live = 0, plain = 0;
             for (int c = 0; c < L.num; ++c) {
-                if (__hip_atomic_load(mismatch + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+                if (__hip_atomic_load(mismatch + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen)
                     continue;
                 live |= 1 << c;
                 if (L.key_plain[c] != nullptr && L.key_plain[c][tile] != 0u) plain |= 1 << c;
@@ -130,16 +130,28 @@ __global__ __launch_bounds__(kThreads) void k_plan_match(const int64_t* __restri
         if (threadIdx.x == 0 && s_diff != 0) {
             const int dm = s_diff;
             for (int c = 0; c < L.num; ++c)
-                if ((dm >> c) & 1) atomicOr(mismatch + c, 1);
+                if ((dm >> c) & 1)
+                    __hip_atomic_store(mismatch + c, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+}
+
+// Copies the flags to host memory, then stores gen behind them: the host
+// polls host[kMaxMatch] and reads the flags once it equals gen.
+__global__ void k_match_publish(const int32_t* __restrict__ mismatch, int num, int32_t gen,
+                                int32_t* __restrict__ host) {
+    const int c = static_cast<int>(threadIdx.x);
+    if (c < num) host[c] = __hip_atomic_load(mismatch + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __threadfence_system();
+    __syncthreads();
+    if (c == 0) __hip_atomic_store(host + kMaxMatch, gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 }  // namespace
 
 hipError_t launch_plan_match(const int64_t* keys, const int64_t* gathers, int64_t n,
                              const relm_mp_plan* const* plans, int num_plans, int32_t* mismatch,
-                             hipStream_t s) {
+                             int32_t gen, int32_t* host_words, hipStream_t s) {
     MatchLaunch L{};
     L.num = num_plans;
     for (int c = 0; c < num_plans; ++c) {
@@ -149,21 +161,26 @@ hipError_t launch_plan_match(const int64_t* keys, const int64_t* gathers, int64_
                                           : nullptr;
         L.gather_plain[c] = gathers != nullptr ? plans[c]->snap_gather_plain : nullptr;
     }
-    hipError_t err = launch_fill_i32(mismatch, kMaxMatch, 0, s);
-    if (err != hipSuccess || n == 0 || num_plans == 0) return err;
+    hipError_t err = hipSuccess;
     const int64_t tiles = (n + kSnapTile - 1) / kSnapTile;
-    constexpr int64_t kProbe = 64;
-    if (tiles > 4 * kProbe) {
-        hipLaunchKernelGGL(k_plan_match, dim3(static_cast<unsigned>(kProbe)), dim3(kThreads), 0, s,
-                           keys, gathers, n, L, mismatch, tiles / kProbe);
+    if (tiles > 0 && num_plans > 0) {
+        constexpr int64_t kProbe = 64;
+        if (tiles > 4 * kProbe) {
+            hipLaunchKernelGGL(k_plan_match, dim3(static_cast<unsigned>(kProbe)), dim3(kThreads), 0,
+                               s, keys, gathers, n, L, mismatch, gen, tiles / kProbe);
+            err = hipGetLastError();
+            if (err != hipSuccess) return err;
+        }
+        // one workgroup per tile (a full comparison streams at HBM rate with
+        // several workgroups resident per CU), grid-stride beyond 2^16 tiles
+        const int64_t blocks = std::min<int64_t>(tiles, 65536);
+        hipLaunchKernelGGL(k_plan_match, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s,
+                           keys, gathers, n, L, mismatch, gen, int64_t{0});
         err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
-    // one workgroup per tile (a full comparison streams at HBM rate with
-    // several workgroups resident per CU), grid-stride beyond 2^16 tiles
-    const int64_t blocks = std::min<int64_t>(tiles, 65536);
-    hipLaunchKernelGGL(k_plan_match, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s,
-                       keys, gathers, n, L, mismatch, int64_t{0});
+    hipLaunchKernelGGL(k_match_publish, dim3(1), dim3(64), 0, s,
+                       static_cast<const int32_t*>(mismatch), num_plans, gen, host_words);
     return hipGetLastError();
 }
 

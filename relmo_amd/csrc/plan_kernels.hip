@@ -49,11 +49,12 @@ __global__ void k_status_init(DevStatus* st, uint32_t* __restrict__ clear, int64
     }
 }
 
-// Copies the status to host memory mapped for the device (vector stores).
-// The host reads it after an event recorded behind this kernel has
-// completed; the event's system-scope release makes the stores visible.
+// Copies the status to host memory mapped for the device (vector stores),
+// then stores `gen` behind it with a system-scope release: the host polls
+// *host_gen and reads the status once it equals gen.
 __global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __restrict__ host,
-                                 relm_mp_plan_counts* __restrict__ pc) {
+                                 relm_mp_plan_counts* __restrict__ pc, int32_t* __restrict__ host_gen,
+                                 int32_t gen) {
     constexpr int kWords = static_cast<int>(sizeof(DevStatus) / sizeof(unsigned long long));
     const int i = static_cast<int>(threadIdx.x);
     if (i < kWords)
@@ -62,6 +63,10 @@ __global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __
         pc->collisions = static_cast<int64_t>(st->collisions);
         pc->identity = st->key_mismatch == 0 ? 1 : 0;
     }
+    __threadfence_system();
+    __syncthreads();
+    if (i == 0 && host_gen != nullptr)
+        __hip_atomic_store(host_gen, gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // inv[k] = max e with keys[e] == k.  Every key and gathered index is checked;
@@ -791,8 +796,9 @@ hipError_t launch_status_init(DevStatus* st, hipStream_t s, uint32_t* clear, int
 }
 
 hipError_t launch_status_publish(const DevStatus* st, DevStatus* host_mapped,
-                                 relm_mp_plan_counts* pc, hipStream_t s) {
-    hipLaunchKernelGGL(k_status_publish, dim3(1), dim3(64), 0, s, st, host_mapped, pc);
+                                 relm_mp_plan_counts* pc, int32_t* host_gen, int32_t gen,
+                                 hipStream_t s) {
+    hipLaunchKernelGGL(k_status_publish, dim3(1), dim3(64), 0, s, st, host_mapped, pc, host_gen, gen);
     return hipGetLastError();
 }
 
