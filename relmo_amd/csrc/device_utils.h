@@ -130,6 +130,15 @@ __device__ __forceinline__ float dev_log<float>(float x) {
 template <>
 __device__ __forceinline__ double dev_log<double>(double x) { return log(x); }
 
+// log(s) + m: for float one rounding of log2(s) * ln 2 + m (the hardware
+// log2, then a fused multiply-add); for double the accurate log.
+template <typename T>
+__device__ __forceinline__ T log_add(T s, T m) { return log(s) + m; }
+template <>
+__device__ __forceinline__ float log_add<float>(float s, float m) {
+    return __builtin_fmaf(__builtin_amdgcn_logf(s), 0.693147180559945309f, m);
+}
+
 template <typename T>
 __device__ __forceinline__ T neg_inf() { return -__builtin_huge_val(); }
 template <>

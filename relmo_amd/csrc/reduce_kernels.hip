@@ -164,6 +164,9 @@ struct SumOp {
     Pack<T, V> acc;
     Rows rows;  // layout of the table rows
 
+    // The walker starts each segment by reset() after storing the previous one.
+    static constexpr bool kResetAtEnd = true;
+    __device__ __forceinline__ void reset() { acc = pack_fill<T, V>(T(0)); }
     __device__ __forceinline__ void begin(int64_t, bool) { acc = pack_fill<T, V>(T(0)); }
     // Starts a new segment when `head` (branch-free).
     __device__ __forceinline__ void restart(bool head, int64_t) {
@@ -210,10 +213,15 @@ struct LseOp {
         m = pack_fill<T, V>(neg_inf<T>());
         s = pack_fill<T, V>(T(0));
     }
-    // The walker's segments (restart / add / result) start m at the lowest
+    // The walker's segments (reset / add / result) start m at the lowest
     // finite value instead of -inf: a -inf message then gives exp(-inf) = 0
     // with no guard (m - x is never -inf - -inf), and a first finite message
     // still sets s = fma(0, e, 1) = 1 exactly.
+    static constexpr bool kResetAtEnd = true;
+    __device__ __forceinline__ void reset() {
+        m = pack_fill<T, V>(lowest<T>());
+        s = pack_fill<T, V>(T(0));
+    }
     __device__ __forceinline__ void restart(bool head, int64_t) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
@@ -275,7 +283,7 @@ struct LseOp {
         Pack<T, V> r;
 #pragma unroll
         for (int i = 0; i < V; ++i) {
-            const T v = dev_log<T>(s.v[i]) + m.v[i];
+            const T v = log_add<T>(s.v[i], m.v[i]);
             r.v[i] = __builtin_isinf(v) ? quiet_nan<T>() : v;
         }
         return r;
@@ -289,6 +297,8 @@ struct LseOp {
 template <typename T, int V, int U>
 struct LseBwdOp {
     using Partial = SumPartial<T, V>;
+    // a segment starts by loading its key's rel row: restart() at its head
+    static constexpr bool kResetAtEnd = false;
     const T* __restrict__ grad_out;
     const T* __restrict__ out;
     const T* __restrict__ rel;
@@ -430,8 +440,13 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
     constexpr int kPosCap = R * kItemSize + kHubThreshold + 1;
     constexpr int PI = (kPosCap + kThreads - 1) / kThreads;  // staged positions per thread
     constexpr int KI = (kKeyCap + kThreads - 1) / kThreads;
+    // a batch reads U + 1 positions from any message of an item on: the
+    // staged range is followed by at least U + 1 padding positions
+    static_assert(kThreads * PI >= kPosCap + U + 1, "walker staging leaves no padding");
+    constexpr uint16_t kNoLabel = 0xFFFF;  // label of the padding (keys are < kKeyCap)
+    static_assert(kKeyCap < kNoLabel, "walker labels fit 16 bits");
     __shared__ int32_t s_off[kKeyCap];
-    __shared__ int32_t s_idx[kPosCap];
+    __shared__ int32_t s_idx[kThreads * PI];   // gathered rows; row 0 as padding
     __shared__ uint16_t s_key[kThreads * PI];  // labels; thread t scans [t * PI, t * PI + PI)
     __shared__ uint32_t s_scan[kThreads / kWave];
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
@@ -479,11 +494,13 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
             const int i = static_cast<int>(threadIdx.x) + j * kThreads;
             if (i < nk) s_off[i] = tk[j];
         }
-        // labels start at 0; thread t owns positions [t * PI, t * PI + PI)
+        // labels start at 0; thread t owns positions [t * PI, t * PI + PI).
+        // Positions past the staged range read row 0, a valid row of every
+        // table the walker reads (it runs only when there are messages).
 #pragma unroll
         for (int j = 0; j < PI; ++j) {
             const int i = static_cast<int>(threadIdx.x) + j * kThreads;
-            if (i < np) s_idx[i] = tp[j];
+            s_idx[i] = i < np ? tp[j] : 0;
             s_key[static_cast<int>(threadIdx.x) * PI + j] = 0;
         }
         __syncthreads();
@@ -531,7 +548,8 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
 #pragma unroll
             for (int j = 0; j < PI; ++j) {
                 cur = v[j] > cur ? v[j] : cur;
-                s_key[static_cast<int>(threadIdx.x) * PI + j] = static_cast<uint16_t>(cur);
+                const int at = static_cast<int>(threadIdx.x) * PI + j;
+                s_key[at] = at < np ? static_cast<uint16_t>(cur) : kNoLabel;
             }
         }
         __syncthreads();
@@ -544,6 +562,11 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
         // the item's messages [sb, se), as staged positions [lb, le)
         const int lb = static_cast<int>(sb - bs0 < np ? sb - bs0 : np);
         const int le = static_cast<int>(se - bs0 < np ? se - bs0 : np);
+        // Positions past the item (q + u >= le) hold the next item's messages
+        // or the padding: valid rows to load, and labels that differ from
+        // the item's last key (items hold whole keys), so a message ends its
+        // segment exactly when the next position's label differs.
+        if constexpr (Op::kResetAtEnd) op.reset();
         int prev = -1;
         for (int q = lb; q < le; q += U) {
             const int cnt = le - q < U ? le - q : U;
@@ -551,22 +574,23 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
             int lab[U + 1];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int at = q + (u < cnt ? u : cnt - 1);
-                idx[u] = s_idx[at];
-                lab[u] = s_key[at];
+                idx[u] = s_idx[q + u];
+                lab[u] = s_key[q + u];
             }
-            lab[U] = q + cnt < le ? static_cast<int>(s_key[q + cnt]) : -1;
+            lab[U] = s_key[q + U];
             op.load(idx, cnt);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (u < cnt) {
-                    const int next = u + 1 < cnt ? lab[u + 1] : lab[U];
                     const int64_t key = bk0 + lab[u];
-                    op.restart(lab[u] != prev, key);
+                    if constexpr (!Op::kResetAtEnd) op.restart(lab[u] != prev, key);
                     op.add(u);
-                    if (next != lab[u] && op.colok)
-                        pack_store_stream<T, V>(out + row_offset(key, D) + op.col,
-                                                epi(key, op.result(true), D, op.col));
+                    if (lab[u + 1] != lab[u]) {
+                        if (op.colok)
+                            pack_store_stream<T, V>(out + row_offset(key, D) + op.col,
+                                                    epi(key, op.result(true), D, op.col));
+                        if constexpr (Op::kResetAtEnd) op.reset();
+                    }
                     prev = lab[u];
                 }
             }
