@@ -89,6 +89,75 @@ def synthetic_c5(device, seed: int = 0, num_graphs: int = 2048) -> RelationalBat
 # ---- modules (relmo/models/mlp.py, residual.py, film.py) ---------------------------------
 
 
+def weight_grad(grad_out: Tensor, inp: Tensor, chunk: int = 4096) -> Tensor:
+    """grad_out^T @ inp for a Linear's weight: [K, out] x [K, in] -> [out, in].
+
+    The weight gradients of these models reduce over all atoms or relation
+    nodes (K up to 5 M) into a few hundred columns.  For narrow weights the
+    library GEMM picks a handful of output tiles and walks all of K in each
+    (C4: about 0.5 ms per 96 x 96 weight); here K is split into chunks that
+    run as one batched product (chunk x out by chunk x in per batch entry),
+    then summed.  Another summation order than one GEMM: equal up to fp32
+    rounding."""
+
+    K = inp.size(0)
+    # wide weights already give the GEMM enough output tiles (C5's 398 x 384:
+    # measured no gain, and slower with the transposing copy at K = 5 M)
+    if K < 8 * chunk or grad_out.size(1) * inp.size(1) > 256 * 256:
+        return grad_out.t().matmul(inp)
+    b = K // chunk
+    main = b * chunk
+    out_f, in_f = grad_out.size(1), inp.size(1)
+    # the narrower operand is the one copied transposed (the other is read in
+    # place as the right operand)
+    if in_f <= out_f:
+        xt = inp[:main].reshape(b, chunk, in_f).transpose(1, 2).contiguous()
+        w = torch.bmm(xt, grad_out[:main].reshape(b, chunk, out_f)).sum(0).t()
+    else:
+        gt = grad_out[:main].reshape(b, chunk, out_f).transpose(1, 2).contiguous()
+        w = torch.bmm(gt, inp[:main].reshape(b, chunk, in_f)).sum(0)
+    if main < K:
+        w = w + grad_out[main:].t().matmul(inp[main:])
+    return w
+
+
+class _Linear(torch.autograd.Function):
+    """F.linear with the weight gradient of weight_grad."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return nn.functional.linear(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        x, weight = ctx.saved_tensors
+        # no copies: x may be a column slice of a wider matrix (the GEMMs take
+        # its row stride as it is)
+        g2 = grad.reshape(-1, grad.size(-1))
+        x2 = x.reshape(-1, x.size(-1))
+        gx = grad.matmul(weight) if ctx.needs_input_grad[0] else None
+        gw = weight_grad(g2, x2) if ctx.needs_input_grad[1] else None
+        gb = g2.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return gx, gw, gb
+
+
+def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """F.linear; on the GPU with the weight gradient of weight_grad."""
+
+    if torch.is_grad_enabled() and x.is_cuda:
+        return _Linear.apply(x, weight, bias)
+    return nn.functional.linear(x, weight, bias)
+
+
+class Linear(nn.Linear):
+    """nn.Linear whose weight gradient splits long reductions (weight_grad)."""
+
+    def forward(self, x: Tensor) -> Tensor:
+        return linear(x, self.weight, self.bias)
+
+
 class Residual(nn.Module):
     """x[..., -width:] + f(x) (residual.py:4-31 with truncate_right=False)."""
 
@@ -110,7 +179,7 @@ def arity_mlp(feature: int, arity: int, layers: int) -> nn.Module:
     mods: list[nn.Module] = []
     dims = [width] * (layers + 1) + [width]
     for i in range(len(dims) - 1):
-        mods.append(nn.Linear(dims[i], dims[i + 1]))
+        mods.append(Linear(dims[i], dims[i + 1]))
         if i < len(dims) - 2:
             mods.append(nn.Mish())
     return Residual(nn.Sequential(*mods), width)
@@ -119,7 +188,7 @@ def arity_mlp(feature: int, arity: int, layers: int) -> nn.Module:
 def simple_mlp(in_size: int, hidden: int, out_size: int) -> nn.Module:
     """SimpleMLP (mlp.py:50-79): Linear, Mish, Linear."""
 
-    return nn.Sequential(nn.Linear(in_size, hidden), nn.Mish(), nn.Linear(hidden, out_size))
+    return nn.Sequential(Linear(in_size, hidden), nn.Mish(), Linear(hidden, out_size))
 
 
 class FiLMConcatMLP(nn.Module):
@@ -134,11 +203,11 @@ class FiLMConcatMLP(nn.Module):
         self.betas = nn.ModuleList()
         prev = in_dim
         for h in hidden:
-            self.lins.append(nn.Linear(prev, h))
-            self.gammas.append(nn.Linear(cond_dim, h))
-            self.betas.append(nn.Linear(cond_dim, h))
+            self.lins.append(Linear(prev, h))
+            self.gammas.append(Linear(cond_dim, h))
+            self.betas.append(Linear(cond_dim, h))
             prev = h
-        self.out = nn.Linear(prev, out_dim)
+        self.out = Linear(prev, out_dim)
         self.act = nn.Mish()
 
     def forward(self, x: Tensor) -> Tensor:
@@ -324,7 +393,7 @@ class CentralizedRelationalGNN(nn.Module):
         else:
             const = lin.bias.unsqueeze(0).expand(table.size(0), width)
         w_slots = w[:, md:].reshape(width, ma, d).transpose(0, 1).reshape(ma * width, d)
-        per_object = (x @ w_slots.t()).view(-1, width)  # row obj * ma + a: x[obj] @ W_a^T
+        per_object = linear(x, w_slots).view(-1, width)  # row obj * ma + a: x[obj] @ W_a^T
         s = mp.fanin_reduce(per_object, r["slot_src"], r["slot_node"], nodes, 0)
 
         sizes = [n for _p, _s, n, _a, _c in r["meta"]]

@@ -409,6 +409,21 @@ def test_central_first_linear_gathered_per_object(dtype) -> None:
                 torch.testing.assert_close(b, a, rtol=tol[0], atol=tol[1])
 
 
+@pytest.mark.parametrize("K", [0, 5, 127, 128, 129, 1000])
+def test_split_weight_gradient(K: int) -> None:
+    """The chunked weight gradient equals grad_out^T @ inp (chunks of 16 rows
+    here, so every K above 128 takes the batched path, with and without a
+    remainder)."""
+
+    from relmo_amd.consumers import weight_grad
+
+    g = torch.Generator().manual_seed(K)
+    for out_f, in_f in ((7, 5), (5, 7)):  # either operand the narrower one
+        go = torch.randn(K, out_f, generator=g, dtype=torch.float64)
+        x = torch.randn(K, in_f + 3, generator=g, dtype=torch.float64)[:, 3:]  # a column slice
+        torch.testing.assert_close(weight_grad(go, x, chunk=16), go.t() @ x, rtol=1e-12, atol=1e-12)
+
+
 def test_model_fanin_masks_only_objects_without_messages(mp_env) -> None:
     """Objects without messages get 0 (PyG's aggregators); a NaN or +inf in an
     object's messages still reaches that object's aggregate."""
