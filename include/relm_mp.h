@@ -424,6 +424,36 @@ typedef struct relm_mp_index_part {
 int relm_mp_pack_index(const relm_mp_index_part* parts, int32_t num_parts, int64_t* out_a,
                        int64_t* out_b, relm_mp_stream_t stream);
 
+/* ---- FiLM step with Mish for central layers (no counterpart in the reference,
+ * which runs it as torch ops inside its central module: relmo/models/film.py
+ * conditioning, relational_gnn.py:757-787) ------------------------------------
+ * Rows [range_start[k], range_start[k + 1]) of s [rows, width] (float32,
+ * row-major) form range k and share row k of gamma, beta and add [num_ranges,
+ * width] (add may be NULL: zero):
+ *   y[r] = mish(beta[k] + gamma[k] * (s[r] + add[k])),  mish(u) = u tanh(softplus(u)).
+ * range_start: num_ranges + 1 ascending host values from 0 to rows,
+ * 1 <= num_ranges <= RELM_MP_FILM_MAX_RANGES. */
+#define RELM_MP_FILM_MAX_RANGES 16
+#define RELM_MP_FILM_ROWS_PER_BLOCK 512
+int relm_mp_film_mish(const float* s, int64_t rows, int64_t width, const int64_t* range_start,
+                      int32_t num_ranges, const float* gamma, const float* beta, const float* add,
+                      float* y, relm_mp_stream_t stream);
+
+/* Blocks of the backward's partial sums for these ranges (each range in blocks of
+ * RELM_MP_FILM_ROWS_PER_BLOCK rows); -1 for invalid ranges. */
+int64_t relm_mp_film_mish_blocks(const int64_t* range_start, int32_t num_ranges);
+
+/* Backward of relm_mp_film_mish given dy [rows, width]: ds = du * gamma[k] with
+ * du = dy * mish'(u), u = beta[k] + gamma[k] * (s + add[k]); partial [blocks, 2,
+ * width] receives per block (the blocks of range k are consecutive, in row order)
+ * the column sums of du * (s + add[k]) and of du over its rows: summed over range
+ * k's blocks they are the gradients of gamma[k] and of beta[k] (that of add[k] is
+ * gamma[k] times the latter).  partial_blocks >= relm_mp_film_mish_blocks(...). */
+int relm_mp_film_mish_backward(const float* s, const float* dy, int64_t rows, int64_t width,
+                               const int64_t* range_start, int32_t num_ranges, const float* gamma,
+                               const float* beta, const float* add, float* ds, float* partial,
+                               int64_t partial_blocks, relm_mp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

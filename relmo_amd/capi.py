@@ -64,6 +64,9 @@ EXPORTED_SYMBOLS = (
     "relm_mp_plan_segment_sum_scaled",
     "relm_mp_plan_gather_last_grouped",
     "relm_mp_plan_segment_sum_grouped",
+    "relm_mp_film_mish",
+    "relm_mp_film_mish_blocks",
+    "relm_mp_film_mish_backward",
 )
 
 
@@ -171,6 +174,10 @@ _SIGNATURES = {
     "relm_mp_plan_gather_last_grouped": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "relm_mp_plan_segment_sum_grouped": (
         _int, [_int, _PP, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "relm_mp_film_mish": (_int, [_vp, _i64, _i64, _vp, ctypes.c_int32, _vp, _vp, _vp, _vp, _vp]),
+    "relm_mp_film_mish_blocks": (_i64, [_vp, ctypes.c_int32]),
+    "relm_mp_film_mish_backward": (
+        _int, [_vp, _vp, _i64, _i64, _vp, ctypes.c_int32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "relm_mp_plan_match": (
         _int,
         [_vp, _vp, _i64, ctypes.POINTER(_PP), ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), _vp,
@@ -615,6 +622,36 @@ def pack_index(parts: list[tuple], write_b: bool = True) -> tuple[torch.Tensor, 
     out_b = torch.empty(total, dtype=torch.int64, device=like.device) if write_b else None
     check(lib().relm_mp_pack_index(descs, len(parts), _ptr(out_a), _ptr(out_b), _stream(like)))
     return out_a, out_b
+
+
+def _starts(range_start: list[int]):
+    arr = (ctypes.c_int64 * len(range_start))(*range_start)
+    return arr, len(range_start) - 1
+
+
+def film_mish(s: torch.Tensor, range_start: list[int], gamma: torch.Tensor, beta: torch.Tensor,
+              add: torch.Tensor | None = None) -> torch.Tensor:
+    """``relm_mp_film_mish`` on contiguous float32 device tensors."""
+
+    y = torch.empty_like(s)
+    starts, k = _starts(range_start)
+    check(lib().relm_mp_film_mish(_ptr(s), s.size(0), s.size(1), starts, k, _ptr(gamma), _ptr(beta),
+                                  _ptr(add) if add is not None else None, _ptr(y), _stream(s)))
+    return y
+
+
+def film_mish_backward(dy: torch.Tensor, s: torch.Tensor, range_start: list[int], gamma: torch.Tensor,
+                       beta: torch.Tensor, add: torch.Tensor | None = None):
+    """``relm_mp_film_mish_backward``: (ds, per-block partial sums [blocks, 2, width])."""
+
+    starts, k = _starts(range_start)
+    blocks = lib().relm_mp_film_mish_blocks(starts, k)
+    ds = torch.empty_like(s)
+    partial = torch.empty(max(blocks, 1), 2, s.size(1), dtype=s.dtype, device=s.device)
+    check(lib().relm_mp_film_mish_backward(_ptr(s), _ptr(dy), s.size(0), s.size(1), starts, k,
+                                           _ptr(gamma), _ptr(beta), _ptr(add) if add is not None else None,
+                                           _ptr(ds), _ptr(partial), blocks, _stream(s)))
+    return ds, partial[:blocks]
 
 
 def plan_match(keys: torch.Tensor, gathers: torch.Tensor | None, plans: list[BuiltPlan]) -> list[bool]:

@@ -26,6 +26,7 @@ from torch import Tensor, nn
 from torch.utils.checkpoint import checkpoint
 
 from . import mp
+from .mp_dispatch import library_op
 
 
 @dataclass
@@ -149,6 +150,26 @@ def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
     if torch.is_grad_enabled() and x.is_cuda:
         return _Linear.apply(x, weight, bias)
     return nn.functional.linear(x, weight, bias)
+
+
+class _FilmMish(torch.autograd.Function):
+    """mish(beta[k] + gamma[k] * (s + add[k])) over the row ranges k of s (range
+    k = rows [starts[k], starts[k + 1])), in one pass of the library's kernel
+    (torch.ops.relm_mp.film_mish); the backward reads s and the gradient once
+    (film_mish_backward), and the gradient of add is gamma times beta's."""
+
+    @staticmethod
+    def forward(ctx, s: Tensor, gamma: Tensor, beta: Tensor, add: Tensor | None, starts: list[int]) -> Tensor:
+        ctx.starts = starts
+        ctx.save_for_backward(s, gamma, beta, add)
+        return torch.ops.relm_mp.film_mish(s, starts, gamma, beta, add)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        s, gamma, beta, add = ctx.saved_tensors
+        ds, dg, db = torch.ops.relm_mp.film_mish_backward(grad, s, ctx.starts, gamma, beta, add)
+        da = gamma * db if add is not None and ctx.needs_input_grad[3] else None
+        return ds, dg, db, da, None
 
 
 class Linear(nn.Linear):
@@ -377,7 +398,9 @@ class CentralizedRelationalGNN(nn.Module):
         FiLM's gamma / beta are evaluated on the per-predicate table and
         broadcast over each predicate's range of nodes (nodes are ordered by
         predicate; a broadcast's backward is a sum over the range, where a
-        gather by node would accumulate millions of rows into a handful).
+        gather by node would accumulate millions of rows into a handful).  On
+        the GPU in float32 each FiLM step with its Mish is one kernel over all
+        ranges (torch.ops.relm_mp.film_mish, _FilmMish).
         The result equals self.central(input) up to fp32 rounding (another
         summation order)."""
 
@@ -397,6 +420,19 @@ class CentralizedRelationalGNN(nn.Module):
         s = mp.fanin_reduce(per_object, r["slot_src"], r["slot_node"], nodes, 0)
 
         sizes = [n for _p, _s, n, _a, _c in r["meta"]]
+        fused = (s.dtype == torch.float32 and len(sizes) <= 16
+                 and library_op("film_mish", tensor=s, gpu_only=True) is not None)
+        if fused:
+            # the FiLM steps as one kernel each: tables in range order
+            order = torch.tensor([ci for _p, _s, _n, _a, ci in r["meta"]], device=s.device)
+            starts = [st for _p, st, _n, _a, _c in r["meta"]] + [nodes]
+            h = _FilmMish.apply(s, film.gammas[0](table)[order], film.betas[0](table)[order],
+                                const[order], starts)
+            for lin_k, g_k, b_k in zip(film.lins[1:], film.gammas[1:], film.betas[1:]):
+                h = _FilmMish.apply(lin_k(h), g_k(table)[order], b_k(table)[order], None, starts)
+            out = film.out(h)
+            slots = mp.fanout_scatter(x, r["obj"], r["flat"], nodes * ma).view(nodes, ma * d)
+            return slots + out
 
         def film_step(pre: Tensor, gamma: Tensor, beta: Tensor, add: Tensor | None) -> Tensor:
             # torch.split, not slicing: the backward of a split is one

@@ -645,6 +645,60 @@ int relm_mp_plan_match(const int64_t* keys, const int64_t* gathers, int64_t n,
     return RELM_MP_OK;
 }
 
+static int check_film_ranges(const int64_t* range_start, int32_t num_ranges, int64_t rows) {
+    if (num_ranges < 1 || num_ranges > kFilmMaxRanges || range_start == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: 1 to 16 row ranges expected");
+    if (range_start[0] != 0 || range_start[num_ranges] != rows)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: the ranges must cover the rows");
+    for (int32_t k = 0; k < num_ranges; ++k)
+        if (range_start[k + 1] < range_start[k])
+            return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: the ranges must be ascending");
+    if (relm_mp_film_mish_blocks(range_start, num_ranges) > 0x7fffffff)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: too many rows");
+    return RELM_MP_OK;
+}
+
+int64_t relm_mp_film_mish_blocks(const int64_t* range_start, int32_t num_ranges) {
+    if (num_ranges < 1 || num_ranges > kFilmMaxRanges || range_start == nullptr) return -1;
+    int64_t blocks = 0;
+    for (int32_t k = 0; k < num_ranges; ++k) blocks += film_range_blocks(range_start[k + 1] - range_start[k]);
+    return blocks;
+}
+
+int relm_mp_film_mish(const float* s, int64_t rows, int64_t width, const int64_t* range_start,
+                      int32_t num_ranges, const float* gamma, const float* beta, const float* add,
+                      float* y, relm_mp_stream_t stream) {
+    RELM_TRY(check_rows(rows, "rows"));
+    if (width < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "width must be >= 0.");
+    RELM_TRY(check_film_ranges(range_start, num_ranges, rows));
+    if (rows == 0 || width == 0) return RELM_MP_OK;
+    if (s == nullptr || gamma == nullptr || beta == nullptr || y == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: NULL array");
+    RELM_HIP(launch_film_mish(s, width, range_start, num_ranges, gamma, beta, add, y,
+                              static_cast<hipStream_t>(stream)),
+             "relm_mp film kernel");
+    return RELM_MP_OK;
+}
+
+int relm_mp_film_mish_backward(const float* s, const float* dy, int64_t rows, int64_t width,
+                               const int64_t* range_start, int32_t num_ranges, const float* gamma,
+                               const float* beta, const float* add, float* ds, float* partial,
+                               int64_t partial_blocks, relm_mp_stream_t stream) {
+    RELM_TRY(check_rows(rows, "rows"));
+    if (width < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "width must be >= 0.");
+    RELM_TRY(check_film_ranges(range_start, num_ranges, rows));
+    if (rows == 0 || width == 0) return RELM_MP_OK;
+    if (partial_blocks < relm_mp_film_mish_blocks(range_start, num_ranges))
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp film: partial sums too small");
+    if (s == nullptr || dy == nullptr || gamma == nullptr || beta == nullptr || ds == nullptr ||
+        partial == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: NULL array");
+    RELM_HIP(launch_film_mish_backward(s, dy, width, range_start, num_ranges, gamma, beta, add, ds,
+                                       partial, static_cast<hipStream_t>(stream)),
+             "relm_mp film backward kernel");
+    return RELM_MP_OK;
+}
+
 int relm_mp_pack_index(const relm_mp_index_part* parts, int32_t num_parts, int64_t* out_a,
                        int64_t* out_b, relm_mp_stream_t stream) {
     if (num_parts < 0 || (num_parts > 0 && parts == nullptr))

@@ -144,6 +144,22 @@ inline int64_t max_chunks(int64_t num_edges) {
 hipError_t launch_pack_index(const relm_mp_index_part* parts, int num_parts, int64_t* out_a,
                              int64_t* out_b, hipStream_t s);
 
+// ---- FiLM step with Mish (film_kernels.hip) ---------------------------------
+constexpr int kFilmMaxRanges = RELM_MP_FILM_MAX_RANGES;
+// Blocks of RELM_MP_FILM_ROWS_PER_BLOCK rows of a range of `rows` rows.
+inline int64_t film_range_blocks(int64_t rows) {
+    return rows <= 0 ? 0 : (rows + RELM_MP_FILM_ROWS_PER_BLOCK - 1) / RELM_MP_FILM_ROWS_PER_BLOCK;
+}
+// range_start: num_ranges + 1 ascending host values from 0 to the row count
+// (checked by the caller).
+hipError_t launch_film_mish(const float* s, int64_t width, const int64_t* range_start,
+                            int32_t num_ranges, const float* gamma, const float* beta,
+                            const float* add, float* y, hipStream_t st);
+hipError_t launch_film_mish_backward(const float* s, const float* dy, int64_t width,
+                                     const int64_t* range_start, int32_t num_ranges,
+                                     const float* gamma, const float* beta, const float* add,
+                                     float* ds, float* partial, hipStream_t st);
+
 // ---- content comparison (match_kernels.hip) -------------------------------
 constexpr int kMaxMatch = RELM_MP_MAX_MATCH;
 // After the launches mismatch[c] == gen iff the snapshot of plans[c] differs

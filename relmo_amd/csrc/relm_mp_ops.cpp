@@ -1640,6 +1640,90 @@ int64_t plan_cache_size() { return PlanCache::get().size(); }
 
 std::vector<int64_t> plan_cache_stats() { return PlanCache::get().stats(); }
 
+// ---- fused FiLM step with Mish (no counterpart in the reference) ---------------
+//
+// y = mish(beta[k] + gamma[k] * (s + add[k])) over row ranges k of s (one
+// range per predicate in a central layer); float32 GPU tensors, the tables
+// [ranges, width].  The backward returns (ds, dgamma, dbeta): the gradient of
+// add is gamma * dbeta.
+
+namespace {
+
+struct FilmArgs {
+    Tensor s, gamma, beta, add;
+    std::vector<int64_t> starts;
+};
+
+FilmArgs film_args(const Tensor& s, at::IntArrayRef range_start, const Tensor& gamma, const Tensor& beta,
+                   const std::optional<Tensor>& add) {
+    TORCH_CHECK(s.dim() == 2 && s.is_cuda() && s.scalar_type() == at::kFloat,
+                "film_mish: s must be a 2-D float32 GPU tensor.");
+    const int64_t k = static_cast<int64_t>(range_start.size()) - 1;
+    TORCH_CHECK(k >= 1 && k <= RELM_MP_FILM_MAX_RANGES, "film_mish: 1 to ", RELM_MP_FILM_MAX_RANGES,
+                " row ranges expected.");
+    for (const Tensor* t : {&gamma, &beta}) {
+        TORCH_CHECK(t->dim() == 2 && t->size(0) == k && t->size(1) == s.size(1) &&
+                        t->scalar_type() == at::kFloat && t->device() == s.device(),
+                    "film_mish: gamma and beta must be float32 [ranges, width] on the device of s.");
+    }
+    FilmArgs a{contiguous(s), contiguous(gamma), contiguous(beta), Tensor(),
+               std::vector<int64_t>(range_start.begin(), range_start.end())};
+    if (add.has_value() && add->defined()) {
+        TORCH_CHECK(add->sizes() == gamma.sizes() && add->scalar_type() == at::kFloat &&
+                        add->device() == s.device(),
+                    "film_mish: add must be float32 [ranges, width] on the device of s.");
+        a.add = contiguous(*add);
+    }
+    return a;
+}
+
+const float* fptr(const Tensor& t) { return t.defined() ? t.data_ptr<float>() : nullptr; }
+
+}  // namespace
+
+Tensor film_mish(const Tensor& s, at::IntArrayRef range_start, const Tensor& gamma, const Tensor& beta,
+                 const std::optional<Tensor>& add) {
+    const FilmArgs a = film_args(s, range_start, gamma, beta, add);
+    c10::OptionalDeviceGuard guard(s.device());
+    Tensor y = at::empty_like(a.s);
+    raise_if(relm_mp_film_mish(fptr(a.s), a.s.size(0), a.s.size(1), a.starts.data(),
+                               static_cast<int32_t>(a.starts.size() - 1), fptr(a.gamma), fptr(a.beta),
+                               fptr(a.add), y.data_ptr<float>(), current_stream(a.s)));
+    return y;
+}
+
+std::tuple<Tensor, Tensor, Tensor> film_mish_backward(const Tensor& grad, const Tensor& s,
+                                                      at::IntArrayRef range_start, const Tensor& gamma,
+                                                      const Tensor& beta,
+                                                      const std::optional<Tensor>& add) {
+    const FilmArgs a = film_args(s, range_start, gamma, beta, add);
+    TORCH_CHECK(grad.sizes() == s.sizes() && grad.scalar_type() == at::kFloat &&
+                    grad.device() == s.device(),
+                "film_mish_backward: grad must match s.");
+    c10::OptionalDeviceGuard guard(s.device());
+    const Tensor g = contiguous(grad);
+    const int32_t k = static_cast<int32_t>(a.starts.size() - 1);
+    const int64_t width = a.s.size(1);
+    const int64_t blocks = relm_mp_film_mish_blocks(a.starts.data(), k);
+    TORCH_CHECK(blocks >= 0, "film_mish_backward: bad row ranges.");
+    Tensor ds = at::empty_like(a.s);
+    Tensor partial = at::empty({std::max<int64_t>(blocks, 1), 2, width}, a.s.options());
+    raise_if(relm_mp_film_mish_backward(fptr(a.s), g.data_ptr<float>(), a.s.size(0), width,
+                                        a.starts.data(), k, fptr(a.gamma), fptr(a.beta), fptr(a.add),
+                                        ds.data_ptr<float>(), partial.data_ptr<float>(), blocks,
+                                        current_stream(a.s)));
+    // per range, the sums of its blocks (consecutive, RELM_MP_FILM_ROWS_PER_BLOCK rows each)
+    Tensor sums = at::zeros({k, 2, width}, a.s.options());
+    int64_t b0 = 0;
+    for (int32_t r = 0; r < k; ++r) {
+        const int64_t rows = a.starts[r + 1] - a.starts[r];
+        const int64_t nb = rows <= 0 ? 0 : (rows + RELM_MP_FILM_ROWS_PER_BLOCK - 1) / RELM_MP_FILM_ROWS_PER_BLOCK;
+        if (nb > 0) sums[r].copy_(partial.narrow(0, b0, nb).sum(0));
+        b0 += nb;
+    }
+    return {ds, sums.select(1, 0), sums.select(1, 1)};
+}
+
 }  // namespace relm_amd
 
 TORCH_LIBRARY(relm_mp, m) {
@@ -1668,6 +1752,8 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("plan_cache_clear() -> ()");
     m.def("plan_cache_size() -> int");
     m.def("plan_cache_stats() -> int[]");
+    m.def("film_mish(Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> Tensor");
+    m.def("film_mish_backward(Tensor grad, Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> (Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
@@ -1694,4 +1780,6 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
     m.impl("plan_cache_size", relm_amd::plan_cache_size);
     m.impl("plan_cache_stats", relm_amd::plan_cache_stats);
+    m.impl("film_mish", relm_amd::film_mish);
+    m.impl("film_mish_backward", relm_amd::film_mish_backward);
 }

@@ -1,0 +1,105 @@
+"""GPU tests of the fused FiLM step with Mish (torch.ops.relm_mp.film_mish and
+its backward; C ABI relm_mp_film_mish*): against the same function in float64
+through torch autograd."""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    os.environ["RELM_MP_FALLBACK"] = "error"
+    from relmo_amd import mp_runtime
+
+    mp_runtime.ensure_loaded()
+
+
+def _reference(s, gamma, beta, add, starts):
+    """float64: mish(beta[k] + gamma[k] * (s + add[k])) per range, through autograd."""
+
+    parts = []
+    for k in range(len(starts) - 1):
+        v = s[starts[k]:starts[k + 1]]
+        t = v + add[k] if add is not None else v
+        parts.append(torch.nn.functional.mish(beta[k] + gamma[k] * t))
+    return torch.cat(parts)
+
+
+@pytest.mark.parametrize("width,starts,with_add", [
+    (398, [0, 1000, 1000, 5123, 6000], True),   # an empty range; 8-byte lanes
+    (398, [0, 513], False),                     # one range, one block plus a row
+    (7, [0, 3, 700, 1536, 1537], True),         # odd width: 4-byte lanes
+    (600, [0, 2048, 4096], True),               # more than 256 column pairs per row
+])
+def test_film_mish_against_float64(width, starts, with_add) -> None:
+    from relmo_amd import capi
+
+    _log(f"film_mish width={width} starts={starts} add={with_add}")
+    g = torch.Generator(device=DEV).manual_seed(width + len(starts))
+    k, rows = len(starts) - 1, starts[-1]
+    s = 2.0 * torch.randn(rows, width, device=DEV, generator=g)
+    gamma = torch.randn(k, width, device=DEV, generator=g)
+    beta = torch.randn(k, width, device=DEV, generator=g)
+    add = torch.randn(k, width, device=DEV, generator=g) if with_add else None
+    dy = torch.randn(rows, width, device=DEV, generator=g)
+
+    ops = torch.ops.relm_mp
+    y = ops.film_mish(s, starts, gamma, beta, add)
+    ds, dg, db = ops.film_mish_backward(dy, s, starts, gamma, beta, add)
+
+    leaves = [t.double().requires_grad_(True) for t in (s, gamma, beta) + ((add,) if with_add else ())]
+    y64 = _reference(leaves[0], leaves[1], leaves[2], leaves[3] if with_add else None, starts)
+    grads = torch.autograd.grad(y64, leaves, dy.double())
+    torch.testing.assert_close(y.double(), y64.detach(), rtol=2e-6, atol=2e-6)
+    torch.testing.assert_close(ds.double(), grads[0], rtol=1e-5, atol=1e-5)
+    # per-range column sums over up to thousands of rows: fp32 accumulation
+    torch.testing.assert_close(dg.double(), grads[1], rtol=1e-4, atol=1e-3)
+    torch.testing.assert_close(db.double(), grads[2], rtol=1e-4, atol=1e-3)
+    if with_add:
+        torch.testing.assert_close((gamma * db).double(), grads[3], rtol=1e-4, atol=1e-3)
+
+    # the C ABI gives the same bits as the torch op
+    assert torch.equal(capi.film_mish(s, starts, gamma, beta, add), y)
+    ds2, partial = capi.film_mish_backward(dy, s, starts, gamma, beta, add)
+    assert torch.equal(ds2, ds)
+    b0 = 0
+    for r in range(k):
+        nb = -(-(starts[r + 1] - starts[r]) // 512)
+        if nb:
+            torch.testing.assert_close(partial[b0:b0 + nb, 1].sum(0), db[r])
+        b0 += nb
+
+
+def test_film_mish_extremes_and_errors() -> None:
+    """Large and very negative pre-activations (Mish is u and 0 there), and
+    ranges that do not cover the rows."""
+
+    ops = torch.ops.relm_mp
+    u = torch.tensor([[-200.0, -30.0, -5.0, 0.0, 5.0, 19.0, 21.0, 300.0]], device=DEV)
+    one = torch.ones(1, 8, device=DEV)
+    y = ops.film_mish(u, [0, 1], one, torch.zeros(1, 8, device=DEV), None)
+    want = torch.nn.functional.mish(u.double())
+    torch.testing.assert_close(y.double(), want, rtol=2e-6, atol=1e-12)
+    ds, _, _ = ops.film_mish_backward(torch.ones_like(u), u, [0, 1], one, torch.zeros(1, 8, device=DEV), None)
+    x = u.double().requires_grad_(True)
+    (gx,) = torch.autograd.grad(torch.nn.functional.mish(x).sum(), x)
+    torch.testing.assert_close(ds.double(), gx, rtol=1e-5, atol=1e-7)
+    with pytest.raises(RuntimeError, match="cover the rows"):
+        ops.film_mish(u, [0, 2], one, one, None)
+    with pytest.raises(RuntimeError, match="row ranges"):
+        ops.film_mish(u, [0], one, one, None)

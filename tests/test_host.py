@@ -26,7 +26,7 @@ EPS32 = float(np.finfo(np.float32).eps)
 
 def _declared_functions() -> set[str]:
     text = HEADER.read_text()
-    return set(re.findall(r"^(?:size_t|int|const char\*)\s+(relm_mp_\w+)\s*\(", text, re.M))
+    return set(re.findall(r"^(?:size_t|int|int64_t|const char\*)\s+(relm_mp_\w+)\s*\(", text, re.M))
 
 
 def _hip_library():
