@@ -267,14 +267,15 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
     forward + backward of mean(out^2) through relmo_amd.mp (HIP ops), index
     routing built once per batch as in the reference layers; graphs/sec =
     graphs / time per step.  C5 runs all 2048 graphs of its config (~5.1M
-    relation nodes): the central FiLM MLP's hidden activations (~40 GB per
-    layer, ten layers) are recomputed in the backward from the saved layer
-    input (activation checkpointing), which keeps the step under one GPU's
-    288 GB; the recompute is one extra central-MLP forward per layer, inside
-    the timed step.  The MLP's first Linear runs per object and is gathered
+    relation nodes).  The MLP's first Linear runs per object and is gathered
     per relation node (CentralizedRelationalGNN._central_gathered: the same
-    function, a ninth of its multiply-adds at C5); the step on the assembled
-    input is reported beside it ("assembled_input")."""
+    function, a ninth of its multiply-adds at C5); the FiLM step with its
+    Mish and the Linear after it keep only the gathered sums (8 GB per
+    layer) and recompute the Mish output in the backward with the fused
+    kernel, which keeps the step under one GPU's 288 GB.  The step on the
+    assembled input is reported beside it ("assembled_input_sum"), with the
+    whole central module recomputed in the backward (activation
+    checkpointing)."""
 
     from relmo_amd import consumers as C
 
@@ -292,7 +293,8 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
                                                        gather_first_linear=True).to(dev)
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects,
                "relation_nodes": int(sum(a.size(0) for a in batch.atoms.values())), "emb": 128,
-               "layers": 10, "central_mlp": "recomputed in the backward (activation checkpointing)",
+               "layers": 10,
+               "central_mlp": "FiLM step + Mish + Linear keep the gathered sums, Mish output recomputed in the backward",
                "first_linear": "per object, gathered per relation node (fanin sum over the slot edges)"}
         modes = ((0, "sum"), (1, "logsumexp"), (2, "mean"))
     res = {"config": cfg}

@@ -172,6 +172,35 @@ class _FilmMish(torch.autograd.Function):
         return ds, dg, db, da, None
 
 
+class _FilmMishLinear(torch.autograd.Function):
+    """out(film_mish(s)): the FiLM step with Mish and the Linear after it,
+    keeping only s for the backward - the Mish output that the Linear's weight
+    gradient needs is recomputed there by one more pass of the fused kernel
+    (selective recomputation: the step's other activations are never kept)."""
+
+    @staticmethod
+    def forward(ctx, s: Tensor, gamma: Tensor, beta: Tensor, add: Tensor | None, starts: list[int],
+                weight: Tensor, bias: Tensor | None) -> Tensor:
+        ctx.starts = starts
+        ctx.has_bias = bias is not None
+        ctx.save_for_backward(s, gamma, beta, add, weight)
+        h = torch.ops.relm_mp.film_mish(s, starts, gamma, beta, add)
+        return nn.functional.linear(h, weight, bias)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        s, gamma, beta, add, weight = ctx.saved_tensors
+        h = torch.ops.relm_mp.film_mish(s, ctx.starts, gamma, beta, add)
+        g2 = grad.reshape(-1, grad.size(-1))
+        gw = weight_grad(g2, h) if ctx.needs_input_grad[5] else None
+        gb = g2.sum(0) if ctx.has_bias and ctx.needs_input_grad[6] else None
+        del h
+        ds, dg, db = torch.ops.relm_mp.film_mish_backward(grad.matmul(weight), s, ctx.starts, gamma, beta,
+                                                          add)
+        da = gamma * db if add is not None and ctx.needs_input_grad[3] else None
+        return ds, dg, db, da, None, gw, gb
+
+
 class Linear(nn.Linear):
     """nn.Linear whose weight gradient splits long reductions (weight_grad)."""
 
@@ -338,9 +367,10 @@ class CentralizedRelationalGNN(nn.Module):
         # evaluate the central MLP's first Linear per object and gather it per
         # relation node instead of assembling [cond | mask | slots] (_central_gathered)
         self.gather_first_linear = gather_first_linear
-        # keep only the central module's input per layer and run the module
-        # again in the backward (activation checkpointing): its hidden
-        # activations are ~4x the slot tensor, ~40 GB per layer at 2048 graphs
+        # recompute the central module's hidden activations in the backward
+        # (~4x the slot tensor, ~40 GB per layer at 2048 graphs): with the
+        # fused FiLM step only its Mish output (_FilmMishLinear), otherwise the
+        # whole module from its saved input (activation checkpointing)
         self.recompute_central = recompute_central
         self.num_layers = num_layers
         self.mode = mode
@@ -386,6 +416,13 @@ class CentralizedRelationalGNN(nn.Module):
                 "deg": _object_degrees(obj_t, batch.num_objects),
                 "slot_src": obj_t * ma + flat_t % ma, "slot_node": flat_t // ma}
 
+    def _film_fused(self, t: Tensor, r: dict) -> bool:
+        """Whether the FiLM steps run on the library's fused kernel (float32 on
+        the GPU, at most 16 predicate ranges)."""
+
+        return (t.dtype == torch.float32 and len(r["meta"]) <= 16
+                and library_op("film_mish", tensor=t, gpu_only=True) is not None)
+
     def _central_gathered(self, x: Tensor, r: dict) -> Tensor:
         """The central module on [cond | slot mask | slots] per relation node,
         without assembling that input (fused.py:311-375 assembles it, then runs
@@ -420,17 +457,19 @@ class CentralizedRelationalGNN(nn.Module):
         s = mp.fanin_reduce(per_object, r["slot_src"], r["slot_node"], nodes, 0)
 
         sizes = [n for _p, _s, n, _a, _c in r["meta"]]
-        fused = (s.dtype == torch.float32 and len(sizes) <= 16
-                 and library_op("film_mish", tensor=s, gpu_only=True) is not None)
-        if fused:
+        if self._film_fused(s, r):
             # the FiLM steps as one kernel each: tables in range order
             order = torch.tensor([ci for _p, _s, _n, _a, ci in r["meta"]], device=s.device)
             starts = [st for _p, st, _n, _a, _c in r["meta"]] + [nodes]
-            h = _FilmMish.apply(s, film.gammas[0](table)[order], film.betas[0](table)[order],
-                                const[order], starts)
-            for lin_k, g_k, b_k in zip(film.lins[1:], film.gammas[1:], film.betas[1:]):
-                h = _FilmMish.apply(lin_k(h), g_k(table)[order], b_k(table)[order], None, starts)
-            out = film.out(h)
+            gamma, beta = film.gammas[0](table)[order], film.betas[0](table)[order]
+            if self.recompute_central and len(film.lins) == 1 and torch.is_grad_enabled():
+                out = _FilmMishLinear.apply(s, gamma, beta, const[order], starts, film.out.weight,
+                                            film.out.bias)
+            else:
+                h = _FilmMish.apply(s, gamma, beta, const[order], starts)
+                for lin_k, g_k, b_k in zip(film.lins[1:], film.gammas[1:], film.betas[1:]):
+                    h = _FilmMish.apply(lin_k(h), g_k(table)[order], b_k(table)[order], None, starts)
+                out = film.out(h)
             slots = mp.fanout_scatter(x, r["obj"], r["flat"], nodes * ma).view(nodes, ma * d)
             return slots + out
 
@@ -458,7 +497,10 @@ class CentralizedRelationalGNN(nn.Module):
         recompute = self.recompute_central and torch.is_grad_enabled()
         if self.gather_first_linear:
             for _ in range(self.num_layers):
-                if recompute:
+                # with the fused FiLM step the recomputation is selective
+                # (_FilmMishLinear keeps the gathered sums only); otherwise the
+                # whole central module is recomputed in the backward
+                if recompute and not self._film_fused(x, r):
                     outputs = checkpoint(self._central_gathered, x, r, use_reentrant=False)
                 else:
                     outputs = self._central_gathered(x, r)

@@ -103,3 +103,31 @@ def test_film_mish_extremes_and_errors() -> None:
         ops.film_mish(u, [0, 2], one, one, None)
     with pytest.raises(RuntimeError, match="row ranges"):
         ops.film_mish(u, [0], one, one, None)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_selective_recompute_matches_stored_activations(mode: int, monkeypatch) -> None:
+    """The gathered central module with recomputation (the fused FiLM step and
+    the Linear after it keep only the gathered sums; the Mish output is
+    recomputed in the backward) gives the loss and gradients of the same
+    module that keeps its activations."""
+
+    from relmo_amd import consumers as C
+
+    monkeypatch.setenv("RELM_MP_ENABLE", "1")
+    batch = C.synthetic_c5(DEV, seed=11, num_graphs=64)
+    results = []
+    for recompute in (False, True):
+        _log(f"central module mode={mode} recompute={recompute}: {batch.num_objects} objects")
+        torch.manual_seed(0)
+        m = C.CentralizedRelationalGNN(128, 4, batch.relations, mode, gather_first_linear=True,
+                                       recompute_central=recompute).to(DEV)
+        routing = m.routing(batch)
+        loss = float(C.train_step(m, batch, routing))
+        grads = {k: p.grad.detach().clone() for k, p in m.named_parameters() if p.grad is not None}
+        results.append((loss, grads))
+    (l0, g0), (l1, g1) = results
+    assert l0 == l1
+    assert g0.keys() == g1.keys()
+    for k in g0:
+        torch.testing.assert_close(g1[k], g0[k], rtol=1e-6, atol=1e-7, msg=lambda m, k=k: f"{k}: {m}")

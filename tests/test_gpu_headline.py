@@ -236,7 +236,7 @@ def _step_grads(C, model, batch, routing, enable: str, monkeypatch):
                          if p.grad is not None}
 
 
-@pytest.mark.parametrize("model", ["c4", "c5", "c5_gathered"])
+@pytest.mark.parametrize("model", ["c4", "c5", "c5_gathered", "c5_gathered_recompute"])
 def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     """One training step: the HIP lane (fp32) is at least as close to a float64
     run of the same step as the ATen lane (fp32) is - per parameter, the
@@ -244,7 +244,10 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     loss within twice the ATen lane's loss error, each plus 8 fp32 ulps
     (relative).  Sum and logsumexp; mean for C5.  c5_gathered runs the central
     MLP's first Linear per object and gathered (both fp32 lanes), against the
-    float64 run of the module on the assembled input."""
+    float64 run of the module on the assembled input; c5_gathered_recompute
+    adds the recomputation of the central activations (on the HIP lane the
+    FiLM step's Mish output is recomputed by its fused kernel in the
+    backward, on the ATen lane the whole central module is checkpointed)."""
 
     import copy
 
@@ -256,9 +259,11 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
         modes = (0, 1)
     else:
         batch = C.synthetic_c5(DEV, seed=5, num_graphs=96)
-        gathered = model == "c5_gathered"
+        gathered = model.startswith("c5_gathered")
+        recompute = model.endswith("_recompute")
         make = lambda mode: C.CentralizedRelationalGNN(  # noqa: E731
-            128, 10, batch.relations, mode, gather_first_linear=gathered).to(DEV)
+            128, 10, batch.relations, mode, gather_first_linear=gathered,
+            recompute_central=recompute).to(DEV)
         modes = (0, 1, 2)
     for mode in modes:
         _log(f"{model} mode={mode}: {batch.num_graphs} graphs, {batch.num_objects} objects")
@@ -269,6 +274,7 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
         loss_aten, g_aten = _step_grads(C, m, batch, routing, "0", monkeypatch)
         m64 = copy.deepcopy(m).double()
         m64.gather_first_linear = False
+        m64.recompute_central = False
         loss64, g64 = _step_grads(C, m64, batch, routing, "0", monkeypatch)
         e_hip, e_aten = abs(loss_hip - loss64), abs(loss_aten - loss64)
         _log(f"  loss {loss64:.8g}: |hip - f64| {e_hip:.3g}, |aten - f64| {e_aten:.3g}")
