@@ -113,7 +113,9 @@ __global__ __launch_bounds__(kThreads) void k_film_mish(const float* __restrict_
 
 // ds = dy * mish'(u) * gamma; partial[block][0][col] = sum over the block's
 // rows of du * (s + add), partial[block][1][col] = sum of du, du = dy *
-// mish'(u), in row order.
+// mish'(u), each term rounded to fp32 and added in row order in fp64 (the
+// sum of a block is rounded once: a per-range sum over tens of thousands of
+// rows keeps about the accuracy of a tree reduction).
 template <int V>
 __global__ __launch_bounds__(kThreads) void k_film_mish_backward(
     const float* __restrict__ s, const float* __restrict__ dy, int64_t width, FilmRanges R,
@@ -128,7 +130,9 @@ __global__ __launch_bounds__(kThreads) void k_film_mish_backward(
         const Vec<V> b = pack_load<float, V>(beta + br.k * width + col);
         const Vec<V> a = add != nullptr ? pack_load<float, V>(add + br.k * width + col)
                                         : pack_fill<float, V>(0.0f);
-        Vec<V> sum_t = pack_fill<float, V>(0.0f), sum_u = pack_fill<float, V>(0.0f);
+        double sum_t[V], sum_u[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) sum_t[i] = sum_u[i] = 0.0;
         auto step = [&](const Vec<V>& x, const Vec<V>& d, int64_t r) {
             Vec<V> o;
 #pragma unroll
@@ -136,8 +140,8 @@ __global__ __launch_bounds__(kThreads) void k_film_mish_backward(
                 const float t = x.v[i] + a.v[i];
                 const float du = d.v[i] * mish_grad(b.v[i] + g.v[i] * t);
                 o.v[i] = du * g.v[i];
-                sum_t.v[i] = sum_t.v[i] + du * t;
-                sum_u.v[i] = sum_u.v[i] + du;
+                sum_t[i] += static_cast<double>(du * t);
+                sum_u[i] += static_cast<double>(du);
             }
             pack_store_stream<float, V>(ds + r * width + col, o);
         };
@@ -155,8 +159,14 @@ __global__ __launch_bounds__(kThreads) void k_film_mish_backward(
         for (; r < br.r1; ++r)
             step(pack_load_stream<float, V>(s + r * width + col),
                  pack_load_stream<float, V>(dy + r * width + col), r);
-        pack_store<float, V>(part + col, sum_t);
-        pack_store<float, V>(part + width + col, sum_u);
+        Vec<V> pt, pu;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            pt.v[i] = static_cast<float>(sum_t[i]);
+            pu.v[i] = static_cast<float>(sum_u[i]);
+        }
+        pack_store<float, V>(part + col, pt);
+        pack_store<float, V>(part + width + col, pu);
     }
 }
 

@@ -67,11 +67,12 @@ def test_film_mish_against_float64(width, starts, with_add) -> None:
     grads = torch.autograd.grad(y64, leaves, dy.double())
     torch.testing.assert_close(y.double(), y64.detach(), rtol=2e-6, atol=2e-6)
     torch.testing.assert_close(ds.double(), grads[0], rtol=1e-5, atol=1e-5)
-    # per-range column sums over up to thousands of rows: fp32 accumulation
-    torch.testing.assert_close(dg.double(), grads[1], rtol=1e-4, atol=1e-3)
-    torch.testing.assert_close(db.double(), grads[2], rtol=1e-4, atol=1e-3)
+    # per-range column sums over up to thousands of rows: fp32 terms added in
+    # fp64 within each 512-row block, the blocks summed in fp32
+    torch.testing.assert_close(dg.double(), grads[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(db.double(), grads[2], rtol=1e-5, atol=1e-4)
     if with_add:
-        torch.testing.assert_close((gamma * db).double(), grads[3], rtol=1e-4, atol=1e-3)
+        torch.testing.assert_close((gamma * db).double(), grads[3], rtol=1e-5, atol=1e-4)
 
     # the C ABI gives the same bits as the torch op
     assert torch.equal(capi.film_mish(s, starts, gamma, beta, add), y)
