@@ -90,25 +90,36 @@ def synthetic_c5(device, seed: int = 0, num_graphs: int = 2048) -> RelationalBat
 # ---- modules (relmo/models/mlp.py, residual.py, film.py) ---------------------------------
 
 
-def weight_grad(grad_out: Tensor, inp: Tensor, chunk: int = 4096) -> Tensor:
+def weight_grad(grad_out: Tensor, inp: Tensor, chunk: int | None = None) -> Tensor:
     """grad_out^T @ inp for a Linear's weight: [K, out] x [K, in] -> [out, in].
 
     The weight gradients of these models reduce over all atoms or relation
-    nodes (K up to 5 M) into a few hundred columns.  For narrow weights the
-    library GEMM picks a handful of output tiles and walks all of K in each
-    (C4: about 0.5 ms per 96 x 96 weight); here K is split into chunks that
-    run as one batched product (chunk x out by chunk x in per batch entry),
-    then summed.  Another summation order than one GEMM: equal up to fp32
-    rounding."""
+    nodes (K up to 5 M) into a few hundred columns.  The library GEMM picks a
+    handful of output tiles and walks all of K in each (C4: about 0.5 ms per
+    96 x 96 weight; C5's 384 x 398 weight over 5 M rows: 21 ms, 73 TFLOP/s);
+    here K is split into chunks that run as one batched product (chunk x out
+    by chunk x in per batch entry), then summed: C5's weight in 14 ms.
+    Another summation order than one GEMM: equal up to fp32 rounding.
+    Chunks default to 4096 rows for weights of at most 256 x 256 entries,
+    32768 above."""
 
     K = inp.size(0)
-    # wide weights already give the GEMM enough output tiles (C5's 398 x 384:
-    # measured no gain, and slower with the transposing copy at K = 5 M)
-    if K < 8 * chunk or grad_out.size(1) * inp.size(1) > 256 * 256:
+    out_f, in_f = grad_out.size(1), inp.size(1)
+    wide = out_f * in_f > 256 * 256
+    if chunk is None:
+        chunk = 32768 if wide else 4096
+    # a wide weight reads the input's chunks in place (a transposed view as the
+    # left operand): only a contiguous input can be viewed so
+    if K < 8 * chunk or (wide and not (inp.is_contiguous() and grad_out.is_contiguous())):
         return grad_out.t().matmul(inp)
     b = K // chunk
     main = b * chunk
-    out_f, in_f = grad_out.size(1), inp.size(1)
+    if wide:
+        w = torch.bmm(inp[:main].view(b, chunk, in_f).transpose(1, 2),
+                      grad_out[:main].view(b, chunk, out_f)).sum(0).t()
+        if main < K:
+            w = w + grad_out[main:].t().matmul(inp[main:])
+        return w
     # the narrower operand is the one copied transposed (the other is read in
     # place as the right operand)
     if in_f <= out_f:
