@@ -669,7 +669,8 @@ int relm_mp_film_mish(const float* s, int64_t rows, int64_t width, const int64_t
                       int32_t num_ranges, const float* gamma, const float* beta, const float* add,
                       float* y, relm_mp_stream_t stream) {
     RELM_TRY(check_rows(rows, "rows"));
-    if (width < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "width must be >= 0.");
+    if (width < 0 || width > 0x7fffffff)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: width must be in [0, 2^31).");
     RELM_TRY(check_film_ranges(range_start, num_ranges, rows));
     if (rows == 0 || width == 0) return RELM_MP_OK;
     if (s == nullptr || gamma == nullptr || beta == nullptr || y == nullptr)
@@ -685,7 +686,8 @@ int relm_mp_film_mish_backward(const float* s, const float* dy, int64_t rows, in
                                const float* beta, const float* add, float* ds, float* partial,
                                int64_t partial_blocks, relm_mp_stream_t stream) {
     RELM_TRY(check_rows(rows, "rows"));
-    if (width < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "width must be >= 0.");
+    if (width < 0 || width > 0x7fffffff)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp film: width must be in [0, 2^31).");
     RELM_TRY(check_film_ranges(range_start, num_ranges, rows));
     if (rows == 0 || width == 0) return RELM_MP_OK;
     if (partial_blocks < relm_mp_film_mish_blocks(range_start, num_ranges))

@@ -19,7 +19,7 @@ namespace relm_mp {
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kMaxThreads = 1024;
 constexpr int kMaxRanges = RELM_MP_FILM_MAX_RANGES;
 constexpr int kRowsPerBlock = RELM_MP_FILM_ROWS_PER_BLOCK;
 
@@ -71,37 +71,51 @@ __device__ __forceinline__ BlockRows block_rows(const FilmRanges& R) {
     return {k, r0, r1};
 }
 
-// One workgroup per block of rows; thread t handles column units t, t + 256,
-// ... (V floats each) of every row of the block.
+// Thread layout of both kernels: `phases` groups of `units` threads (one per
+// column unit of V floats); thread t owns unit t % units and, within the
+// workgroup's block of rows, the rows r0 + p, r0 + p + phases, ... (p = t /
+// units).  Several phases keep the lanes busy where a row has fewer units
+// than the workgroup threads (C5: 199 pairs of floats per row, 4 phases over
+// 832 threads); with one phase the threads loop over the units instead (rows
+// wider than the workgroup).  A thread keeps its columns, so the backward's
+// column sums need no atomics.
+struct FilmLayout {
+    int units;   // column units per row
+    int phases;  // row phases
+};
+
 template <int V>
-__global__ __launch_bounds__(kThreads) void k_film_mish(const float* __restrict__ s,
-                                                         int64_t width, FilmRanges R,
-                                                         const float* __restrict__ gamma,
-                                                         const float* __restrict__ beta,
-                                                         const float* __restrict__ add,
-                                                         float* __restrict__ y) {
+__global__ __launch_bounds__(kMaxThreads) void k_film_mish(const float* __restrict__ s,
+                                                           int64_t width, FilmRanges R, FilmLayout L,
+                                                           const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta,
+                                                           const float* __restrict__ add,
+                                                           float* __restrict__ y) {
     const BlockRows br = block_rows(R);
-    const int64_t units = width / V;
-    for (int64_t c = threadIdx.x; c < units; c += kThreads) {
+    const int t = static_cast<int>(threadIdx.x);
+    const int ph = L.phases > 1 ? t / L.units : 0;
+    if (ph >= L.phases) return;
+    const int step = L.phases;
+    for (int64_t c = L.phases > 1 ? t % L.units : t; c < L.units; c += L.phases > 1 ? L.units : blockDim.x) {
         const int64_t col = c * V;
         const Vec<V> g = pack_load<float, V>(gamma + br.k * width + col);
         const Vec<V> b = pack_load<float, V>(beta + br.k * width + col);
         const Vec<V> a = add != nullptr ? pack_load<float, V>(add + br.k * width + col)
                                         : pack_fill<float, V>(0.0f);
-        int64_t r = br.r0;
-        for (; r + 4 <= br.r1; r += 4) {
+        int64_t r = br.r0 + ph;
+        for (; r + 3 * step < br.r1; r += 4 * step) {
             Vec<V> x[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) x[j] = pack_load_stream<float, V>(s + (r + j) * width + col);
+            for (int j = 0; j < 4; ++j) x[j] = pack_load_stream<float, V>(s + (r + j * step) * width + col);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 Vec<V> o;
 #pragma unroll
                 for (int i = 0; i < V; ++i) o.v[i] = mish(b.v[i] + g.v[i] * (x[j].v[i] + a.v[i]));
-                pack_store_stream<float, V>(y + (r + j) * width + col, o);
+                pack_store_stream<float, V>(y + (r + j * step) * width + col, o);
             }
         }
-        for (; r < br.r1; ++r) {
+        for (; r < br.r1; r += step) {
             const Vec<V> x = pack_load_stream<float, V>(s + r * width + col);
             Vec<V> o;
 #pragma unroll
@@ -113,18 +127,25 @@ __global__ __launch_bounds__(kThreads) void k_film_mish(const float* __restrict_
 
 // ds = dy * mish'(u) * gamma; partial[block][0][col] = sum over the block's
 // rows of du * (s + add), partial[block][1][col] = sum of du, du = dy *
-// mish'(u), each term rounded to fp32 and added in row order in fp64 (the
-// sum of a block is rounded once: a per-range sum over tens of thousands of
-// rows keeps about the accuracy of a tree reduction).
+// mish'(u), each term rounded to fp32 and added in fp64: by each thread over
+// its rows in row order, then the phases in order (the sum of a block is
+// rounded once: a per-range sum over tens of thousands of rows keeps about the
+// accuracy of a tree reduction).  With several phases, `lds` holds
+// phases * units * V * 2 doubles.
 template <int V>
-__global__ __launch_bounds__(kThreads) void k_film_mish_backward(
+__global__ __launch_bounds__(kMaxThreads) void k_film_mish_backward(
     const float* __restrict__ s, const float* __restrict__ dy, int64_t width, FilmRanges R,
-    const float* __restrict__ gamma, const float* __restrict__ beta,
+    FilmLayout L, const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ add, float* __restrict__ ds, float* __restrict__ partial) {
+    extern __shared__ double lds[];
     const BlockRows br = block_rows(R);
-    const int64_t units = width / V;
+    const int t = static_cast<int>(threadIdx.x);
+    const int ph = L.phases > 1 ? t / L.units : 0;
+    const int step = L.phases;
     float* __restrict__ part = partial + static_cast<int64_t>(blockIdx.x) * 2 * width;
-    for (int64_t c = threadIdx.x; c < units; c += kThreads) {
+    const bool active = ph < L.phases;
+    for (int64_t c = L.phases > 1 ? t % L.units : t; active && c < L.units;
+         c += L.phases > 1 ? L.units : blockDim.x) {
         const int64_t col = c * V;
         const Vec<V> g = pack_load<float, V>(gamma + br.k * width + col);
         const Vec<V> b = pack_load<float, V>(beta + br.k * width + col);
@@ -133,40 +154,73 @@ __global__ __launch_bounds__(kThreads) void k_film_mish_backward(
         double sum_t[V], sum_u[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) sum_t[i] = sum_u[i] = 0.0;
-        auto step = [&](const Vec<V>& x, const Vec<V>& d, int64_t r) {
+        auto stp = [&](const Vec<V>& x, const Vec<V>& d, int64_t r) {
             Vec<V> o;
 #pragma unroll
             for (int i = 0; i < V; ++i) {
-                const float t = x.v[i] + a.v[i];
-                const float du = d.v[i] * mish_grad(b.v[i] + g.v[i] * t);
+                const float tt = x.v[i] + a.v[i];
+                const float du = d.v[i] * mish_grad(b.v[i] + g.v[i] * tt);
                 o.v[i] = du * g.v[i];
-                sum_t[i] += static_cast<double>(du * t);
+                sum_t[i] += static_cast<double>(du * tt);
                 sum_u[i] += static_cast<double>(du);
             }
             pack_store_stream<float, V>(ds + r * width + col, o);
         };
-        int64_t r = br.r0;
-        for (; r + 4 <= br.r1; r += 4) {
+        int64_t r = br.r0 + ph;
+        for (; r + 3 * step < br.r1; r += 4 * step) {
             Vec<V> x[4], d[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                x[j] = pack_load_stream<float, V>(s + (r + j) * width + col);
-                d[j] = pack_load_stream<float, V>(dy + (r + j) * width + col);
+                x[j] = pack_load_stream<float, V>(s + (r + j * step) * width + col);
+                d[j] = pack_load_stream<float, V>(dy + (r + j * step) * width + col);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) step(x[j], d[j], r + j);
+            for (int j = 0; j < 4; ++j) stp(x[j], d[j], r + j * step);
         }
-        for (; r < br.r1; ++r)
-            step(pack_load_stream<float, V>(s + r * width + col),
-                 pack_load_stream<float, V>(dy + r * width + col), r);
-        Vec<V> pt, pu;
+        for (; r < br.r1; r += step)
+            stp(pack_load_stream<float, V>(s + r * width + col),
+                pack_load_stream<float, V>(dy + r * width + col), r);
+        if (L.phases > 1) {
+            // this thread's sums into LDS: [phase][unit][V] for t, then for u
+            double* lt = lds + (static_cast<int64_t>(ph) * L.units + c) * V;
+            double* lu = lt + static_cast<int64_t>(L.phases) * L.units * V;
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-            pt.v[i] = static_cast<float>(sum_t[i]);
-            pu.v[i] = static_cast<float>(sum_u[i]);
+            for (int i = 0; i < V; ++i) {
+                lt[i] = sum_t[i];
+                lu[i] = sum_u[i];
+            }
+        } else {
+            Vec<V> pt, pu;
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                pt.v[i] = static_cast<float>(sum_t[i]);
+                pu.v[i] = static_cast<float>(sum_u[i]);
+            }
+            pack_store<float, V>(part + col, pt);
+            pack_store<float, V>(part + width + col, pu);
         }
-        pack_store<float, V>(part + col, pt);
-        pack_store<float, V>(part + width + col, pu);
+    }
+    if (L.phases > 1) {
+        __syncthreads();
+        // phase 0's threads add the phases in order
+        if (active && ph == 0) {
+            const int c = t;
+            const int64_t col = static_cast<int64_t>(c) * V;
+            Vec<V> pt, pu;
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                double at = 0.0, au = 0.0;
+                for (int p = 0; p < L.phases; ++p) {
+                    const double* lt = lds + (static_cast<int64_t>(p) * L.units + c) * V;
+                    at += lt[i];
+                    au += lt[static_cast<int64_t>(L.phases) * L.units * V + i];
+                }
+                pt.v[i] = static_cast<float>(at);
+                pu.v[i] = static_cast<float>(au);
+            }
+            pack_store<float, V>(part + col, pt);
+            pack_store<float, V>(part + width + col, pu);
+        }
     }
 }
 
@@ -193,6 +247,23 @@ FilmRanges film_ranges(const int64_t* range_start, int32_t num_ranges) {
     return R;
 }
 
+// Most phases whose threads fit one workgroup (at most 4), and the workgroup
+// size: a multiple of the wave.
+FilmLayout film_layout(int64_t units) {
+    FilmLayout L{static_cast<int>(units), 1};
+    if (units <= kMaxThreads / 2) L.phases = static_cast<int>(std::min<int64_t>(4, kMaxThreads / units));
+    return L;
+}
+
+int film_threads(const FilmLayout& L) {
+    const int n = L.units * L.phases;
+    return std::min(kMaxThreads, (n + 63) / 64 * 64);
+}
+
+size_t film_lds_bytes(const FilmLayout& L, int V) {
+    return L.phases > 1 ? static_cast<size_t>(L.phases) * L.units * V * 2 * sizeof(double) : 0;
+}
+
 }  // namespace
 
 hipError_t launch_film_mish(const float* s, int64_t width, const int64_t* range_start,
@@ -201,12 +272,15 @@ hipError_t launch_film_mish(const float* s, int64_t width, const int64_t* range_
     const FilmRanges R = film_ranges(range_start, num_ranges);
     const int64_t blocks = R.first_block[kMaxRanges];
     if (blocks == 0 || width == 0) return hipSuccess;
-    if (film_vec(width, {s, gamma, beta, add, y}) == 2)
-        hipLaunchKernelGGL(k_film_mish<2>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, s,
-                           width, R, gamma, beta, add, y);
-    else
-        hipLaunchKernelGGL(k_film_mish<1>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, s,
-                           width, R, gamma, beta, add, y);
+    if (film_vec(width, {s, gamma, beta, add, y}) == 2) {
+        const FilmLayout L = film_layout(width / 2);
+        hipLaunchKernelGGL(k_film_mish<2>, dim3(static_cast<unsigned>(blocks)), dim3(film_threads(L)), 0, st,
+                           s, width, R, L, gamma, beta, add, y);
+    } else {
+        const FilmLayout L = film_layout(width);
+        hipLaunchKernelGGL(k_film_mish<1>, dim3(static_cast<unsigned>(blocks)), dim3(film_threads(L)), 0, st,
+                           s, width, R, L, gamma, beta, add, y);
+    }
     return hipGetLastError();
 }
 
@@ -217,12 +291,17 @@ hipError_t launch_film_mish_backward(const float* s, const float* dy, int64_t wi
     const FilmRanges R = film_ranges(range_start, num_ranges);
     const int64_t blocks = R.first_block[kMaxRanges];
     if (blocks == 0 || width == 0) return hipSuccess;
-    if (film_vec(width, {s, dy, gamma, beta, add, ds, partial}) == 2)
-        hipLaunchKernelGGL(k_film_mish_backward<2>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                           st, s, dy, width, R, gamma, beta, add, ds, partial);
-    else
-        hipLaunchKernelGGL(k_film_mish_backward<1>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                           st, s, dy, width, R, gamma, beta, add, ds, partial);
+    if (film_vec(width, {s, dy, gamma, beta, add, ds, partial}) == 2) {
+        const FilmLayout L = film_layout(width / 2);
+        hipLaunchKernelGGL(k_film_mish_backward<2>, dim3(static_cast<unsigned>(blocks)),
+                           dim3(film_threads(L)), film_lds_bytes(L, 2), st, s, dy, width, R, L, gamma,
+                           beta, add, ds, partial);
+    } else {
+        const FilmLayout L = film_layout(width);
+        hipLaunchKernelGGL(k_film_mish_backward<1>, dim3(static_cast<unsigned>(blocks)),
+                           dim3(film_threads(L)), film_lds_bytes(L, 1), st, s, dy, width, R, L, gamma,
+                           beta, add, ds, partial);
+    }
     return hipGetLastError();
 }
 

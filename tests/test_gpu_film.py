@@ -44,7 +44,8 @@ def _reference(s, gamma, beta, add, starts):
     (398, [0, 1000, 1000, 5123, 6000], True),   # an empty range; 8-byte lanes
     (398, [0, 513], False),                     # one range, one block plus a row
     (7, [0, 3, 700, 1536, 1537], True),         # odd width: 4-byte lanes
-    (600, [0, 2048, 4096], True),               # more than 256 column pairs per row
+    (600, [0, 2048, 4096], True),               # 300 column pairs: 3 row phases
+    (2500, [0, 700, 701, 1500], True),          # more column pairs than threads: one phase, looped
 ])
 def test_film_mish_against_float64(width, starts, with_add) -> None:
     from relmo_amd import capi
