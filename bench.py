@@ -284,7 +284,7 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
         batch = C.synthetic_c4(dev)
         make = lambda mode: C.RelationalGNN(32, 10, batch.relations, mode).to(dev)
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects, "emb": 32, "layers": 10,
-               "weight_gradients": "reductions over atoms split into 4096-row chunks (consumers.weight_grad)"}
+               "weight_gradients": "reductions over atoms split into 2048/4096-row chunks read in place (consumers.weight_grad)"}
         modes = ((0, "sum"), (1, "logsumexp"))
     else:
         log("  generating the C5 batch (2048 graphs)")

@@ -95,39 +95,28 @@ def weight_grad(grad_out: Tensor, inp: Tensor, chunk: int | None = None) -> Tens
 
     The weight gradients of these models reduce over all atoms or relation
     nodes (K up to 5 M) into a few hundred columns.  The library GEMM picks a
-    handful of output tiles and walks all of K in each (C4: about 0.5 ms per
-    96 x 96 weight; C5's 384 x 398 weight over 5 M rows: 21 ms, 73 TFLOP/s);
-    here K is split into chunks that run as one batched product (chunk x out
-    by chunk x in per batch entry), then summed: C5's weight in 14 ms.
-    Another summation order than one GEMM: equal up to fp32 rounding.
-    Chunks default to 4096 rows for weights of at most 256 x 256 entries,
-    32768 above."""
+    handful of output tiles and walks all of K in each (C4: 0.40-0.53 ms per
+    weight of 32 x 32 to 96 x 96 over 204,800 atoms; C5's 384 x 398 weight
+    over 5 M nodes: 21 ms); here K is split into chunks that run as one
+    batched product (chunk x in by chunk x out per batch entry), then summed:
+    31-61 us for C4's weights, 14 ms for C5's.  The input's chunks are read in
+    place as transposed views (the left operand), the gradient's as they are
+    (column slices of wider matrices included: only unit column strides are
+    needed).  Another summation order than one GEMM: equal up to fp32
+    rounding.  Chunks default to 2048 rows for weights of at most 64 x 64
+    entries, 4096 up to 256 x 256, 32768 above."""
 
     K = inp.size(0)
     out_f, in_f = grad_out.size(1), inp.size(1)
-    wide = out_f * in_f > 256 * 256
     if chunk is None:
-        chunk = 32768 if wide else 4096
-    # a wide weight reads the input's chunks in place (a transposed view as the
-    # left operand): only a contiguous input can be viewed so
-    if K < 8 * chunk or (wide and not (inp.is_contiguous() and grad_out.is_contiguous())):
+        entries = out_f * in_f
+        chunk = 2048 if entries <= 64 * 64 else (4096 if entries <= 256 * 256 else 32768)
+    if K < 8 * chunk or inp.stride(1) != 1 or grad_out.stride(1) != 1:
         return grad_out.t().matmul(inp)
     b = K // chunk
     main = b * chunk
-    if wide:
-        w = torch.bmm(inp[:main].view(b, chunk, in_f).transpose(1, 2),
-                      grad_out[:main].view(b, chunk, out_f)).sum(0).t()
-        if main < K:
-            w = w + grad_out[main:].t().matmul(inp[main:])
-        return w
-    # the narrower operand is the one copied transposed (the other is read in
-    # place as the right operand)
-    if in_f <= out_f:
-        xt = inp[:main].reshape(b, chunk, in_f).transpose(1, 2).contiguous()
-        w = torch.bmm(xt, grad_out[:main].reshape(b, chunk, out_f)).sum(0).t()
-    else:
-        gt = grad_out[:main].reshape(b, chunk, out_f).transpose(1, 2).contiguous()
-        w = torch.bmm(gt, inp[:main].reshape(b, chunk, in_f)).sum(0)
+    w = torch.bmm(inp[:main].unflatten(0, (b, chunk)).transpose(1, 2),
+                  grad_out[:main].unflatten(0, (b, chunk))).sum(0).t()
     if main < K:
         w = w + grad_out[main:].t().matmul(inp[main:])
     return w

@@ -34,19 +34,22 @@ struct FilmRanges {
 
 // Mish and its derivative through n = e^u (e^u + 2): tanh(softplus(u)) =
 // n / (n + 2), and d/du [u tanh(softplus(u))] = n / (n + 2) + 4 u e^u (1 +
-// e^u) / (n + 2)^2.  Above u = 20, tanh(softplus(u)) is 1 in fp32.
+// e^u) / (n + 2)^2.  Above u = 20, tanh(softplus(u)) is 1 in fp32.  The
+// accurate expf and an IEEE division (the kernels are bound by memory): the
+// per-predicate sums of the backward add tens of thousands of these terms,
+// where the bias of approximate ones would show.
 __device__ __forceinline__ float mish(float u) {
     if (u > 20.0f) return u;
-    const float e = __expf(u);
+    const float e = expf(u);
     const float n = e * (e + 2.0f);
-    return u * n * __builtin_amdgcn_rcpf(n + 2.0f);
+    return u * n / (n + 2.0f);
 }
 
 __device__ __forceinline__ float mish_grad(float u) {
     if (u > 20.0f) return 1.0f;
-    const float e = __expf(u);
+    const float e = expf(u);
     const float n = e * (e + 2.0f);
-    const float r = __builtin_amdgcn_rcpf(n + 2.0f);
+    const float r = 1.0f / (n + 2.0f);
     return n * r + 4.0f * u * e * (1.0f + e) * r * r;
 }
 

@@ -422,13 +422,17 @@ def test_split_weight_gradient(K: int) -> None:
         go = torch.randn(K, out_f, generator=g, dtype=torch.float64)
         x = torch.randn(K, in_f + 3, generator=g, dtype=torch.float64)[:, 3:]  # a column slice
         torch.testing.assert_close(weight_grad(go, x, chunk=16), go.t() @ x, rtol=1e-12, atol=1e-12)
-    # weights of more than 256 x 256 entries: the input's chunks as transposed
-    # views (contiguous input), or one product (a column slice)
+    # weights of more than 256 x 256 entries, contiguous input or a column slice
     go = torch.randn(K, 300, generator=g, dtype=torch.float64)
     x = torch.randn(K, 260, generator=g, dtype=torch.float64)
     torch.testing.assert_close(weight_grad(go, x, chunk=16), go.t() @ x, rtol=1e-12, atol=1e-12)
     xs = torch.randn(K, 263, generator=g, dtype=torch.float64)[:, 3:]
     torch.testing.assert_close(weight_grad(go, xs, chunk=16), go.t() @ xs, rtol=1e-12, atol=1e-12)
+    # a column-strided gradient, and one whose columns are not contiguous
+    gs = torch.randn(K, 305, generator=g, dtype=torch.float64)[:, 5:]
+    torch.testing.assert_close(weight_grad(gs, xs, chunk=16), gs.t() @ xs, rtol=1e-12, atol=1e-12)
+    gt = torch.randn(300, K, generator=g, dtype=torch.float64).t()
+    torch.testing.assert_close(weight_grad(gt, x, chunk=16), gt.t() @ x, rtol=1e-12, atol=1e-12)
 
 
 def test_model_fanin_masks_only_objects_without_messages(mp_env) -> None:
