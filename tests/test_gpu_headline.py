@@ -240,9 +240,9 @@ def _step_grads(C, model, batch, routing, enable: str, monkeypatch):
 def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     """One training step: the HIP lane (fp32) is at least as close to a float64
     run of the same step as the ATen lane (fp32) is - per parameter, the
-    relative L2 error of the gradient within twice the ATen lane's, and the
-    loss within twice the ATen lane's loss error, each plus 8 fp32 ulps
-    (relative).  Sum and logsumexp; mean for C5.  c5_gathered runs the central
+    relative L2 error of the gradient within twice the ATen lane's plus 32
+    fp32 ulps, and the loss within twice the ATen lane's loss error plus 8
+    fp32 ulps (relative).  Sum and logsumexp; mean for C5.  c5_gathered runs the central
     MLP's first Linear per object and gathered (both fp32 lanes), against the
     float64 run of the module on the assembled input; c5_gathered_recompute
     adds the recomputation of the central activations (on the HIP lane the
@@ -288,7 +288,11 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
             r_aten = float((g_aten[k].double() - ref).norm()) / max(nref, 1e-300)
             if r_hip / max(r_aten, 1e-12) > worst:
                 worst, worst_k = r_hip / max(r_aten, 1e-12), f"{k} ({r_hip:.3g} against {r_aten:.3g})"
-            assert r_hip <= 2 * r_aten + 8 * EPS32, (mode, k, r_hip, r_aten)
+            # a gradient summed over ~1e5 relation nodes in each of ten layers
+            # keeps a few 1e-6 of relative fp32 error however it is ordered
+            # (a dropped or doubled term gives O(1)); the ATen lane's draws
+            # vary with its float atomics
+            assert r_hip <= 2 * r_aten + 32 * EPS32, (mode, k, r_hip, r_aten)
         _log(f"  gradients: worst ratio of relative L2 errors hip/aten {worst:.3g}: {worst_k}")
         del m, m64, routing, g_hip, g_aten, g64
         torch.cuda.empty_cache()
