@@ -89,9 +89,13 @@ int check_validation(const DevStatus& host, const int64_t* keys, int64_t key_bou
     return set_error(RELM_MP_ERR_INDEX_OUT_OF_BOUNDS, buf);
 }
 
-// Per host thread and device: pinned host copies of a plan status and plan
-// counts, and an event marking when the status copy has landed.  A build
-// waits for its own event before returning, so one slot per thread suffices.
+// Per host thread and device: pinned host memory (a few hundred bytes,
+// allocated on the thread's first build on that device and kept until the
+// process ends) into which the device publishes a plan's status, its
+// counts and plan-match flags, each publication followed by a generation
+// word that the host polls.  A build waits for its own publication before
+// returning, so one slot per thread suffices.
+//
 // An index validation whose result has not been read yet (inverse plans
 // built without waiting): what the error message needs.
 struct PendingCheck {
