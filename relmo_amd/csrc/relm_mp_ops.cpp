@@ -312,8 +312,11 @@ class PlanCache {
         if (mb != nullptr) limit_ = static_cast<size_t>(std::strtoull(mb, nullptr, 10)) << 20;
     }
 
+    // Inference tensors keep no version counter (reading it throws); the
+    // version is only an ordering hint here, every candidate's content is
+    // compared.
     static uint32_t version(const Tensor& t) {
-        return t.unsafeGetTensorImpl()->version_counter().current_version();
+        return t.is_inference() ? 0u : t.unsafeGetTensorImpl()->version_counter().current_version();
     }
 
     static void note_tensors(Entry& e, const Tensor& key, const Tensor* gather) {

@@ -267,3 +267,29 @@ def test_cache_memory_stays_bounded(mp_env) -> None:
     entries, _, _, _, kept, peak = ns.plan_cache_stats()
     limit = int(os.environ.get("RELM_MP_PLAN_CACHE_MB", "2048")) << 20
     assert 0 < kept <= peak <= limit and entries >= 1
+
+
+def test_inference_mode_indices(mp_env) -> None:
+    """Index tensors made under torch.inference_mode() keep no version counter:
+    the cache builds, keeps and serves plans for them as for other tensors
+    (fanin sum and fanout, the second call of each a content hit)."""
+
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    ns.plan_cache_clear()
+    rel, src, dst, K = _fanin_case(3)
+    with torch.inference_mode():
+        s2, d2 = src.clone(), dst.clone()
+        before = _stats()
+        a = mp.fanin_reduce(rel, s2, d2, K, 0)
+        b = mp.fanin_reduce(rel, s2, d2, K, 0)
+        f1 = mp.fanout_scatter(rel, s2, d2, K)
+        f2 = mp.fanout_scatter(rel, s2, d2, K)
+        d = _delta(before, _stats())
+    _log(f"inference-mode indices: {d}")
+    assert d["hits"] >= 2, d
+    assert torch.equal(a, b) and torch.equal(f1, f2)
+    assert np.array_equal(a.cpu().numpy(), _want_sum(rel, src, dst, K))
+    want = oracle.fanout_scatter(rel.cpu().numpy(), src.cpu().numpy(), dst.cpu().numpy(), K)
+    assert np.array_equal(f1.cpu().numpy(), want)
