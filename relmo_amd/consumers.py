@@ -281,10 +281,13 @@ def fanin_objects(mode: int, rel_flat: Tensor, r: dict, num_objects: int) -> Ten
     (the op's logsumexp leaves -inf there, which is replaced - NaN and +inf
     results of objects with messages pass through unchanged)."""
 
+    # the fanin edge list: the fanout's (slot, object) pairs unless the routing
+    # packed its own (RelationalGNN's batched lane)
+    src, dst = r.get("fanin_src", r["flat"]), r.get("fanin_dst", r["obj"])
     if mode == mp.MODE_MEAN:
-        total = mp.fanin_reduce(rel_flat, r["flat"], r["obj"], num_objects, mp.MODE_SUM)
+        total = mp.fanin_reduce(rel_flat, src, dst, num_objects, mp.MODE_SUM)
         return total / r["deg"].clamp_min(1).to(total.dtype).unsqueeze(1)
-    msgs = mp.fanin_reduce(rel_flat, r["flat"], r["obj"], num_objects, mode)
+    msgs = mp.fanin_reduce(rel_flat, src, dst, num_objects, mode)
     if mode == mp.MODE_LOGSUMEXP:
         msgs = msgs.masked_fill((r["deg"] == 0).unsqueeze(1), 0.0)
     return msgs
@@ -297,11 +300,21 @@ class RelationalGNN(nn.Module):
     """RelationalGNN with the fast fused relation layer: per layer, gather the
     argument embeddings of every atom into slots (fanout_scatter), apply the
     predicate's residual MLP, reduce the slot outputs back to objects
-    (fanin_reduce: sum or logsumexp), update X <- X + updater([X, m])."""
+    (fanin_reduce: sum or logsumexp), update X <- X + updater([X, m]).
+
+    ``lane="batched"`` routes as the batched_cached lane (BatchedFanOutMP /
+    BatchedFanInMP with the pack ops enabled): the slot and object indices of
+    both ops come from ``fanout_pack_from_edges`` and
+    ``fanin_pack_from_edges`` over per-(predicate, position) edge lists, made
+    once per batch and reused by every layer.  The two lanes route the same
+    edges in the same order, so their indices and steps agree exactly."""
 
     def __init__(self, embedding_size: int, num_layers: int, relations: dict[str, int], mode: int,
-                 mlp_layers: int = 2):
+                 mlp_layers: int = 2, lane: str = "fast_fused"):
         super().__init__()
+        if lane not in ("fast_fused", "batched"):
+            raise ValueError(f"unknown RelationalGNN lane {lane!r} (fast_fused or batched)")
+        self.lane = lane
         self.d = embedding_size
         self.num_layers = num_layers
         self.mode = mode
@@ -315,6 +328,8 @@ class RelationalGNN(nn.Module):
         (atom, pos) = offset + atom * arity + pos; fanout edges listed per
         predicate then position, fanin edges the same way."""
 
+        if self.lane == "batched":
+            return self._routing_batched(batch)
         meta, flat, obj = [], [], []
         total = 0
         for pred in sorted(self.relations):
@@ -333,6 +348,48 @@ class RelationalGNN(nn.Module):
         # the fanin pair (flat_src, dst) is the same edge list as the fanout pair
         return {"meta": meta, "total": total, "flat": flat_t, "obj": obj_t,
                 "deg": _object_degrees(obj_t, batch.num_objects)}
+
+    def _routing_batched(self, batch: RelationalBatch) -> dict:
+        """batched.py:121-257 (the fanout's packed plan) and the relation lane
+        of BatchedFanInMP (its packed fanin plan): one edge list per
+        (predicate, position) - argument object -> atom for the fanout, atom ->
+        object for the fanin - packed by the pack ops into the operands of
+        fanout_scatter (object row, slot_offset + atom * arity + pos) and of
+        fanin_reduce (relation row atom * arity + pos after the predicate's
+        rows, object).  Only the index outputs are kept: the reference packs
+        with the layer's tensors, whose values the layers pass again."""
+
+        meta, objs, atoms, part_of, arities, positions, offsets = [], [], [], [], [], [], []
+        total = 0
+        for pred in sorted(self.relations):
+            args = batch.atoms.get(pred)
+            if args is None or args.numel() == 0:
+                continue
+            n, arity = int(args.size(0)), self.relations[pred]
+            atom = torch.arange(n, device=args.device)
+            for pos in range(arity):
+                objs.append(args[:, pos])
+                atoms.append(atom)
+                part_of.append(len(meta))
+                arities.append(arity)
+                positions.append(pos)
+                offsets.append(total)
+            meta.append((pred, n, arity, total))
+            total += n * arity
+        dev = next(iter(self.updater.parameters())).device
+        if not meta:
+            empty = torch.zeros(0, dtype=torch.long, device=dev)
+            return {"meta": meta, "total": 0, "flat": empty, "obj": empty, "fanin_src": empty,
+                    "fanin_dst": empty, "deg": torch.zeros(batch.num_objects, dtype=torch.long, device=dev)}
+        # index computations only: one-column stand-ins for the value parts
+        x_stub = torch.zeros(batch.num_objects, 1, device=dev)
+        rel_stubs = [torch.zeros(n * arity, 1, device=dev) for _p, n, arity, _o in meta]
+        _x, obj_t, flat_t = mp.fanout_pack_from_edges([x_stub], objs, atoms, [0] * len(objs), arities,
+                                                      positions, offsets)
+        _r, fanin_src, fanin_dst = mp.fanin_pack_from_edges(rel_stubs, atoms, objs, part_of, arities,
+                                                            positions, 0)
+        return {"meta": meta, "total": total, "flat": flat_t, "obj": obj_t, "fanin_src": fanin_src,
+                "fanin_dst": fanin_dst, "deg": _object_degrees(fanin_dst, batch.num_objects)}
 
     def forward(self, batch: RelationalBatch, routing: dict | None = None) -> Tensor:
         r = routing or self.routing(batch)

@@ -299,3 +299,33 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
         _log(f"  gradients: worst ratio of relative L2 errors hip/aten {worst:.3g}: {worst_k}")
         del m, m64, routing, g_hip, g_aten, g_aten2, g64
         torch.cuda.empty_cache()
+
+
+def test_c4_batched_lane_matches_fast_fused(monkeypatch) -> None:
+    """C4 at its configured size through the batched lane: the routing packed on
+    the GPU by fanout_pack_from_edges / fanin_pack_from_edges equals the fast
+    fused lane's index for index, and a training step of each lane gives the
+    same loss and gradients bit for bit (sum and logsumexp)."""
+
+    from relmo_amd import consumers as C
+
+    monkeypatch.setenv("RELM_MP_ENABLE", "1")
+    batch = C.synthetic_c4(DEV, seed=5, num_graphs=512)
+    for mode in (0, 1):
+        _log(f"c4 batched lane mode={mode}: {batch.num_graphs} graphs")
+        runs = []
+        for lane in ("fast_fused", "batched"):
+            torch.manual_seed(0)
+            m = C.RelationalGNN(32, 10, batch.relations, mode, lane=lane).to(DEV)
+            r = m.routing(batch)
+            loss = C.train_step(m, batch, r)
+            runs.append((r, loss, {k: p.grad.detach().clone() for k, p in m.named_parameters()}))
+        (ra, la, ga), (rb, lb, gb) = runs
+        for key in ("flat", "obj", "deg"):
+            assert torch.equal(ra[key], rb[key]), key
+        assert torch.equal(rb["fanin_src"], ra["flat"]) and torch.equal(rb["fanin_dst"], ra["obj"])
+        assert torch.equal(la, lb), mode
+        for k in ga:
+            assert torch.equal(ga[k], gb[k]), (mode, k)
+        del runs, ra, rb, ga, gb
+        torch.cuda.empty_cache()

@@ -362,6 +362,37 @@ def test_model_consumers_cpu_lane_matches_aten(monkeypatch) -> None:
             assert torch.allclose(a, b, rtol=1e-5, atol=1e-7), (mode, float(a), float(b))
 
 
+@pytest.mark.parametrize("enable", ["1", "0"])
+def test_relational_gnn_batched_lane(monkeypatch, enable: str) -> None:
+    """The batched lane's routing, packed by fanout_pack_from_edges and
+    fanin_pack_from_edges (the library's CPU lane, or the Python fallbacks with
+    the library off), equals the fast fused lane's index for index, and one
+    training step of either lane gives the same loss and gradients bit for bit
+    (sum, logsumexp, mean)."""
+
+    from relmo_amd import consumers as C
+
+    monkeypatch.setenv("RELM_MP_ENABLE", enable)
+    batch = C.synthetic_c4("cpu", seed=2, num_graphs=3)
+    for mode in (0, 1, 2):
+        runs = []
+        for lane in ("fast_fused", "batched"):
+            torch.manual_seed(0)
+            model = C.RelationalGNN(16, 2, batch.relations, mode, lane=lane)
+            r = model.routing(batch)
+            loss = C.train_step(model, batch, r)
+            runs.append((r, loss, {k: p.grad.clone() for k, p in model.named_parameters()}))
+        (ra, la, ga), (rb, lb, gb) = runs
+        for key in ("flat", "obj", "deg"):
+            assert torch.equal(ra[key], rb[key]), key
+        assert torch.equal(rb["fanin_src"], ra["flat"]) and torch.equal(rb["fanin_dst"], ra["obj"])
+        assert torch.equal(la, lb), mode
+        for k in ga:
+            assert torch.equal(ga[k], gb[k]), (mode, k)
+    with pytest.raises(ValueError, match="lane"):
+        C.RelationalGNN(16, 2, batch.relations, 0, lane="modular")
+
+
 def test_central_recompute_matches_stored_activations() -> None:
     """Recomputing the central module in the backward (activation
     checkpointing) gives the same loss and gradients as keeping its
