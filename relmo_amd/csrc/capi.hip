@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -137,22 +138,33 @@ struct HostSlot {
 
 // Waits until the device has stored `want` into *word (host memory mapped for
 // the device, written with a system-scope release behind the data it
-// guards).  Spins, checking the stream every 1024 polls: a failed stream, or
-// one that has drained without the store, is an error.
+// guards).  Spins; after 2 ms without the store, and every millisecond from
+// then on, asks whether the stream has failed or drained without storing it
+// (either is an error).  Not earlier: a stream query can leave a marker in
+// the stream, a pause of several microseconds between the kernels around it,
+// and most waits end within a few hundred microseconds.
 int wait_host_word(const int32_t* word, int32_t want, hipStream_t s, const char* what) {
+    using Clock = std::chrono::steady_clock;
+    const Clock::time_point start = Clock::now();
+    Clock::time_point next_query = start + std::chrono::milliseconds(2);
     for (uint64_t spin = 1;; ++spin) {
         if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == want) return RELM_MP_OK;
-        if ((spin & 1023) == 0) {
-            const hipError_t q = hipStreamQuery(s);
-            if (q == hipSuccess) {
-                if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == want) return RELM_MP_OK;
-                return set_error(RELM_MP_ERR_HIP, std::string(what) + ": the device did not publish its result");
+        if ((spin & 255) == 0) {
+            const Clock::time_point now = Clock::now();
+            if (now >= next_query) {
+                next_query = now + std::chrono::milliseconds(1);
+                const hipError_t q = hipStreamQuery(s);
+                if (q == hipSuccess) {
+                    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == want) return RELM_MP_OK;
+                    return set_error(RELM_MP_ERR_HIP,
+                                     std::string(what) + ": the device did not publish its result");
+                }
+                if (q != hipErrorNotReady) {
+                    (void)hipGetLastError();
+                    return set_error(RELM_MP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(q));
+                }
             }
-            if (q != hipErrorNotReady) {
-                (void)hipGetLastError();
-                return set_error(RELM_MP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(q));
-            }
-            if (spin > (1ull << 20)) std::this_thread::yield();
+            if (now - start > std::chrono::milliseconds(20)) std::this_thread::yield();
         }
         __builtin_ia32_pause();
     }
