@@ -35,7 +35,11 @@ namespace relm_mp {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsInFlight = 4;          // rows per row group per iteration (inverse plans)
+// Rows per row group per iteration of the inverse-plan row kernels (the best
+// of 2..8 measured at the bench sizes: the gather moves one row per row, the
+// logsumexp backward reads three).
+constexpr int kGatherRowsInFlight = 2;
+constexpr int kLseRowsInFlight = 4;
 constexpr int64_t kMaxBlocksX = 1 << 22;  // keeps blocks * 1024 threads below 2^32
 // Largest pair of arrays read into the memory-side cache (256 MB on MI355X)
 // ahead of a write-dominated kernel.
@@ -785,8 +789,12 @@ __device__ __forceinline__ int32_t inverse_edge(const int32_t* __restrict__ inv,
 }
 
 // out[r] = table[gathers[inv[r]]] or 0 (inverse plans: fanout forward and
-// injective sum backward).  Each row group keeps kRowsInFlight rows in flight:
-// rows key0 + j * ngroups, so neighbouring groups touch neighbouring rows.
+// injective sum backward).  Each row group keeps kGatherRowsInFlight rows in
+// flight.
+// A workgroup takes R * RU consecutive rows at a time (row j * R + group of
+// its chunk for the group's j-th row): all resident workgroups stream one
+// contiguous region.  (Rows a grid apart instead - RU regions at once, a
+// power-of-two distance apart at the bench sizes - ran up to 10% slower.)
 // The identity (keys[e] == e for every edge): plans read back by the host
 // have inv == NULL; plans still being validated carry the flag in counts.
 __device__ __forceinline__ const int32_t* inverse_map(const int32_t* inv,
@@ -804,17 +812,18 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
                                                          int64_t num_keys, int64_t D,
                                                          T* __restrict__ out, Rows out_rows) {
     constexpr int R = kThreads / G;
-    constexpr int RU = kRowsInFlight;
+    constexpr int RU = kGatherRowsInFlight;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
     const int32_t* inv = inverse_map(inv_in, pc);
-    const int64_t ngroups = static_cast<int64_t>(gridDim.x) * R;
-    for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key0 < num_keys;
-         key0 += ngroups * RU) {
+    const int64_t chunk = static_cast<int64_t>(R) * RU;
+    const int64_t grp = threadIdx.x / G;
+    for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * chunk + grp; key0 < num_keys;
+         key0 += static_cast<int64_t>(gridDim.x) * chunk) {
         int32_t e[RU];
 #pragma unroll
-        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * ngroups, num_keys, num_edges);
+        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * R, num_keys, num_edges);
         int64_t g[RU];
 #pragma unroll
         for (int j = 0; j < RU; ++j) g[j] = e[j] >= 0 ? gathers[e[j]] : -1;
@@ -827,7 +836,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
         }
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
-            const int64_t key = key0 + j * ngroups;
+            const int64_t key = key0 + j * R;
             if (key < num_keys) pack_store_stream<T, V>(out + out_rows(key, D) + col, v[j]);
         }
     }
@@ -920,17 +929,18 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
     const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
     int64_t num_keys, int64_t D, T* __restrict__ grad_rel) {
     constexpr int R = kThreads / G;
-    constexpr int RU = kRowsInFlight;
+    constexpr int RU = kLseRowsInFlight;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
     const int32_t* inv = inverse_map(inv_in, pc);
-    const int64_t ngroups = static_cast<int64_t>(gridDim.x) * R;
-    for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; key0 < num_keys;
-         key0 += ngroups * RU) {
+    const int64_t chunk = static_cast<int64_t>(R) * RU;
+    const int64_t grp = threadIdx.x / G;
+    for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * chunk + grp; key0 < num_keys;
+         key0 += static_cast<int64_t>(gridDim.x) * chunk) {
         int32_t e[RU];
 #pragma unroll
-        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * ngroups, num_keys, num_edges);
+        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * R, num_keys, num_edges);
         int64_t d[RU];
 #pragma unroll
         for (int j = 0; j < RU; ++j) d[j] = e[j] >= 0 ? gathers[e[j]] : -1;
@@ -938,14 +948,14 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
             const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
-            const int64_t key = key0 + j * ngroups;
+            const int64_t key = key0 + j * R;
             x[j] = ok ? pack_load_stream<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
             g[j] = ok ? pack_load<T, V>(grad_out + row_offset(d[j], D) + col) : pack_fill<T, V>(T(0));
             o[j] = ok ? pack_load<T, V>(out + row_offset(d[j], D) + col) : pack_fill<T, V>(T(0));
         }
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
-            const int64_t key = key0 + j * ngroups;
+            const int64_t key = key0 + j * R;
             if (key >= num_keys) continue;
             const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
             Pack<T, V> r = pack_fill<T, V>(T(0));
@@ -1150,7 +1160,7 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
         using Rows = decltype(rows);
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
             hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows>),
-                               row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
+                               row_grid(plan.num_keys, G, geo.slices, kGatherRowsInFlight),
                                dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
                                gathers, plan.num_gather, table, plan.num_keys, emb, out, rows);
         } else {
@@ -1255,7 +1265,7 @@ int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void*
         constexpr int U = batch_rows<G>();
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
             hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G>),
-                               row_grid(plan.num_keys, G, geo.slices, kRowsInFlight),
+                               row_grid(plan.num_keys, G, geo.slices, kLseRowsInFlight),
                                dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
                                gathers, plan.num_gather, grad_out, out, rel, plan.num_keys, emb,
                                grad_rel);
