@@ -35,10 +35,13 @@ namespace relm_mp {
 namespace {
 
 constexpr int kThreads = 256;
-// Rows per row group per iteration of the inverse-plan row kernels (the best
-// of 2..8 measured at the bench sizes: the gather moves one row per row, the
-// logsumexp backward reads three).
-constexpr int kGatherRowsInFlight = 2;
+// Rows per row group per iteration of the inverse-plan row kernels, the best
+// of 1..8 measured: the gather of 16-byte lanes (C3, D = 64; edge order,
+// D = 32) keeps 2 rows in flight, of narrower lanes (argument slots of 128
+// columns at an 8-byte aligned offset) 8; the logsumexp backward, which
+// reads three rows per row, 4.
+template <typename T, int V>
+constexpr int gather_rows_in_flight() { return sizeof(T) * V >= 16 ? 2 : 8; }
 constexpr int kLseRowsInFlight = 4;
 constexpr int64_t kMaxBlocksX = 1 << 22;  // keeps blocks * 1024 threads below 2^32
 // Largest pair of arrays read into the memory-side cache (256 MB on MI355X)
@@ -789,8 +792,8 @@ __device__ __forceinline__ int32_t inverse_edge(const int32_t* __restrict__ inv,
 }
 
 // out[r] = table[gathers[inv[r]]] or 0 (inverse plans: fanout forward and
-// injective sum backward).  Each row group keeps kGatherRowsInFlight rows in
-// flight.
+// injective sum backward).  Each row group keeps gather_rows_in_flight<T, V>() rows
+// in flight.
 // A workgroup takes R * RU consecutive rows at a time (row j * R + group of
 // its chunk for the group's j-th row): all resident workgroups stream one
 // contiguous region.  (Rows a grid apart instead - RU regions at once, a
@@ -812,7 +815,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
                                                          int64_t num_keys, int64_t D,
                                                          T* __restrict__ out, Rows out_rows) {
     constexpr int R = kThreads / G;
-    constexpr int RU = kGatherRowsInFlight;
+    constexpr int RU = gather_rows_in_flight<T, V>();
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
@@ -1160,7 +1163,7 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
         using Rows = decltype(rows);
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
             hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows>),
-                               row_grid(plan.num_keys, G, geo.slices, kGatherRowsInFlight),
+                               row_grid(plan.num_keys, G, geo.slices, gather_rows_in_flight<T, V>()),
                                dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
                                gathers, plan.num_gather, table, plan.num_keys, emb, out, rows);
         } else {
