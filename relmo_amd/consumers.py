@@ -208,6 +208,77 @@ class Linear(nn.Linear):
         return linear(x, self.weight, self.bias)
 
 
+_UNIT_FILM: dict[tuple[torch.device, int], tuple[Tensor, Tensor]] = {}
+
+
+def _unit_film(like: Tensor) -> tuple[Tensor, Tensor]:
+    """gamma = 1 and beta = 0 for one row range of like's width: the fused
+    FiLM kernel then computes plain Mish (0 + 1 * u == u exactly)."""
+
+    key = (like.device, like.size(-1))
+    pair = _UNIT_FILM.get(key)
+    if pair is None:
+        pair = (torch.ones(1, like.size(-1), device=like.device),
+                torch.zeros(1, like.size(-1), device=like.device))
+        _UNIT_FILM[key] = pair
+    return pair
+
+
+class _LinearMish(torch.autograd.Function):
+    """mish(linear(x, weight, bias)) with Mish in the library's fused FiLM
+    kernel (one row range, unit scale, zero shift; torch.ops.relm_mp.film_mish).
+    The pre-activation u is kept; the backward reads it and the gradient once
+    (film_mish_backward), which also yields the bias gradient - the column
+    sums of the gradient at u - so no separate reduction runs for it."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+        u = nn.functional.linear(x, weight, bias)
+        u2 = u.reshape(-1, u.size(-1))
+        one, zero = _unit_film(u2)
+        ctx.has_bias = bias is not None
+        ctx.save_for_backward(x, weight, u)
+        return torch.ops.relm_mp.film_mish(u2, [0, u2.size(0)], one, zero, None).view_as(u)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        x, weight, u = ctx.saved_tensors
+        u2 = u.reshape(-1, u.size(-1))
+        one, zero = _unit_film(u2)
+        du, _dg, db = torch.ops.relm_mp.film_mish_backward(grad.reshape(u2.shape), u2, [0, u2.size(0)],
+                                                           one, zero, None)
+        x2 = x.reshape(-1, x.size(-1))
+        gx = du.matmul(weight).view(*x.shape[:-1], weight.size(1)) if ctx.needs_input_grad[0] else None
+        gw = weight_grad(du, x2) if ctx.needs_input_grad[1] else None
+        gb = db[0] if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return gx, gw, gb
+
+
+class MishMLP(nn.Sequential):
+    """nn.Sequential of Linear and Mish layers (mlp.py's layer order and
+    parameter names) where, in float32 on the GPU with the library loaded, a
+    Linear followed by Mish runs as one autograd node (_LinearMish): torch's
+    Mish costs three transcendental functions per element and its backward
+    more, the fused kernel one exp and one division, and the bias gradient
+    comes with the Mish backward."""
+
+    def forward(self, x: Tensor) -> Tensor:
+        mods = list(self)
+        fused = (x.is_cuda and x.dtype == torch.float32
+                 and library_op("film_mish", tensor=x, gpu_only=True) is not None)
+        i = 0
+        while i < len(mods):
+            m = mods[i]
+            if (fused and isinstance(m, nn.Linear) and i + 1 < len(mods)
+                    and isinstance(mods[i + 1], nn.Mish) and x.size(-1) == m.in_features):
+                x = _LinearMish.apply(x, m.weight, m.bias)
+                i += 2
+            else:
+                x = m(x)
+                i += 1
+        return x
+
+
 class Residual(nn.Module):
     """x[..., -width:] + f(x) (residual.py:4-31 with truncate_right=False)."""
 
@@ -232,13 +303,13 @@ def arity_mlp(feature: int, arity: int, layers: int) -> nn.Module:
         mods.append(Linear(dims[i], dims[i + 1]))
         if i < len(dims) - 2:
             mods.append(nn.Mish())
-    return Residual(nn.Sequential(*mods), width)
+    return Residual(MishMLP(*mods), width)
 
 
 def simple_mlp(in_size: int, hidden: int, out_size: int) -> nn.Module:
     """SimpleMLP (mlp.py:50-79): Linear, Mish, Linear."""
 
-    return nn.Sequential(Linear(in_size, hidden), nn.Mish(), Linear(hidden, out_size))
+    return MishMLP(Linear(in_size, hidden), nn.Mish(), Linear(hidden, out_size))
 
 
 class FiLMConcatMLP(nn.Module):
@@ -397,9 +468,13 @@ class RelationalGNN(nn.Module):
         x = ref.new_zeros(batch.num_objects, self.d)
         for _ in range(self.num_layers):
             args = mp.fanout_scatter(x, r["obj"], r["flat"], r["total"])
+            # split, not slices: the backward of split concatenates the parts'
+            # gradients once, where each slice's would be a zero-filled full
+            # copy, summed over the predicates
+            parts = args.split([n * arity for _p, n, arity, _o in r["meta"]])
             outs = []
-            for pred, n, arity, off in r["meta"]:
-                feat = args[off: off + n * arity].view(n, arity * self.d)
+            for (pred, n, arity, _off), part in zip(r["meta"], parts):
+                feat = part.view(n, arity * self.d)
                 outs.append(self.rel_mlps[pred](feat).view(n * arity, self.d))
             rel_flat = torch.cat(outs) if len(outs) > 1 else outs[0]
             msgs = fanin_objects(self.mode, rel_flat, r, batch.num_objects)

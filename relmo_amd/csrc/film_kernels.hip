@@ -78,8 +78,8 @@ __device__ __forceinline__ BlockRows block_rows(const FilmRanges& R) {
 // column unit of V floats); thread t owns unit t % units and, within the
 // workgroup's block of rows, the rows r0 + p, r0 + p + phases, ... (p = t /
 // units).  Several phases keep the lanes busy where a row has fewer units
-// than the workgroup threads (C5: 199 pairs of floats per row, 4 phases over
-// 832 threads); with one phase the threads loop over the units instead (rows
+// than the workgroup threads (C5: 199 pairs of floats per row, 5 phases over
+// 1024 threads); with one phase the threads loop over the units instead (rows
 // wider than the workgroup).  A thread keeps its columns, so the backward's
 // column sums need no atomics.
 struct FilmLayout {
@@ -250,11 +250,15 @@ FilmRanges film_ranges(const int64_t* range_start, int32_t num_ranges) {
     return R;
 }
 
-// Most phases whose threads fit one workgroup (at most 4), and the workgroup
-// size: a multiple of the wave.
+// Most phases whose threads fit one workgroup (at most kMaxPhases), and the
+// workgroup size: a multiple of the wave.  Narrow rows take many phases, so
+// that a block of kRowsPerBlock rows still fills a workgroup (rows of 32
+// floats: 16 column pairs x 64 phases of 8 rows each).
+constexpr int kMaxPhases = 64;
 FilmLayout film_layout(int64_t units) {
     FilmLayout L{static_cast<int>(units), 1};
-    if (units <= kMaxThreads / 2) L.phases = static_cast<int>(std::min<int64_t>(4, kMaxThreads / units));
+    if (units <= kMaxThreads / 2)
+        L.phases = static_cast<int>(std::min<int64_t>(kMaxPhases, kMaxThreads / units));
     return L;
 }
 
