@@ -122,13 +122,46 @@ def weight_grad(grad_out: Tensor, inp: Tensor, chunk: int | None = None) -> Tens
     return w
 
 
+def _narrow_nt(t: Tensor, inner: int, cols: int) -> bool:
+    """Whether t @ b^T (inner size `inner`, `cols` output columns) goes to the
+    library's mm_nt (rocBLAS): float32 on the GPU with 64 to 128 inner and at
+    most 128 output columns, where rocBLAS streams at about the HBM rate and
+    hipBLASLt runs 2-3x slower (C4's relation MLPs: 23 against 55 us for a
+    204,800 x 64 by 64 x 64 product, 43 against 85 us at 96).  With fewer than
+    64 inner columns rocBLAS is the slower one."""
+
+    return (64 <= inner <= 128 and cols <= 128 and t.dtype == torch.float32
+            and library_op("mm_nt", tensor=t, gpu_only=True) is not None)
+
+
+def matmul_nt(a: Tensor, b: Tensor) -> Tensor:
+    """a @ b^T for a [M, K], b [N, K] (_narrow_nt picks the library)."""
+
+    if _narrow_nt(a, a.size(1), b.size(0)):
+        return torch.ops.relm_mp.mm_nt(a, b)
+    return a.matmul(b.t())
+
+
+def _input_grad(grad: Tensor, weight: Tensor, x: Tensor) -> Tensor:
+    """grad @ weight ([M, out] x [out, in]) shaped as x."""
+
+    g2 = grad.reshape(-1, grad.size(-1))
+    if _narrow_nt(g2, weight.size(0), weight.size(1)):
+        return torch.ops.relm_mp.mm_nt(g2, weight.t().contiguous()).view(*x.shape[:-1], weight.size(1))
+    return grad.matmul(weight)
+
+
 class _Linear(torch.autograd.Function):
-    """F.linear with the weight gradient of weight_grad."""
+    """F.linear with the weight gradient of weight_grad; narrow products
+    through matmul_nt (the bias then added in place)."""
 
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
         ctx.save_for_backward(x, weight)
         ctx.has_bias = bias is not None
+        if x.dim() == 2 and _narrow_nt(x, weight.size(1), weight.size(0)):
+            y = torch.ops.relm_mp.mm_nt(x, weight)
+            return y.add_(bias) if bias is not None else y
         return nn.functional.linear(x, weight, bias)
 
     @staticmethod
@@ -138,7 +171,7 @@ class _Linear(torch.autograd.Function):
         # its row stride as it is)
         g2 = grad.reshape(-1, grad.size(-1))
         x2 = x.reshape(-1, x.size(-1))
-        gx = grad.matmul(weight) if ctx.needs_input_grad[0] else None
+        gx = _input_grad(grad, weight, x) if ctx.needs_input_grad[0] else None
         gw = weight_grad(g2, x2) if ctx.needs_input_grad[1] else None
         gb = g2.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
         return gx, gw, gb
@@ -226,29 +259,37 @@ def _unit_film(like: Tensor) -> tuple[Tensor, Tensor]:
 
 class _LinearMish(torch.autograd.Function):
     """mish(linear(x, weight, bias)) with Mish in the library's fused FiLM
-    kernel (one row range, unit scale, zero shift; torch.ops.relm_mp.film_mish).
-    The pre-activation u is kept; the backward reads it and the gradient once
-    (film_mish_backward), which also yields the bias gradient - the column
-    sums of the gradient at u - so no separate reduction runs for it."""
+    kernel (one row range, unit scale; torch.ops.relm_mp.film_mish).  Narrow
+    products run through mm_nt without the bias, which the kernel then adds
+    as its shift (mish(bias + u)); otherwise the GEMM adds it and the shift is
+    zero.  The pre-activation u is kept; the backward reads it and the
+    gradient once (film_mish_backward), which also yields the bias gradient -
+    the column sums of the gradient at the Mish input - so no separate
+    reduction runs for it."""
 
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
-        u = nn.functional.linear(x, weight, bias)
-        u2 = u.reshape(-1, u.size(-1))
-        one, zero = _unit_film(u2)
+        x2 = x.reshape(-1, x.size(-1))
+        one, zero = _unit_film(weight[:, 0])
+        if _narrow_nt(x2, weight.size(1), weight.size(0)):
+            u = torch.ops.relm_mp.mm_nt(x2, weight)
+            shift = bias.unsqueeze(0) if bias is not None else zero
+        else:
+            u = nn.functional.linear(x2, weight, bias)
+            shift = zero
         ctx.has_bias = bias is not None
-        ctx.save_for_backward(x, weight, u)
-        return torch.ops.relm_mp.film_mish(u2, [0, u2.size(0)], one, zero, None).view_as(u)
+        ctx.save_for_backward(x, weight, u, shift)
+        y = torch.ops.relm_mp.film_mish(u, [0, u.size(0)], one, shift, None)
+        return y.view(*x.shape[:-1], weight.size(0))
 
     @staticmethod
     def backward(ctx, grad: Tensor):
-        x, weight, u = ctx.saved_tensors
-        u2 = u.reshape(-1, u.size(-1))
-        one, zero = _unit_film(u2)
-        du, _dg, db = torch.ops.relm_mp.film_mish_backward(grad.reshape(u2.shape), u2, [0, u2.size(0)],
-                                                           one, zero, None)
+        x, weight, u, shift = ctx.saved_tensors
+        one, _zero = _unit_film(weight[:, 0])
+        du, _dg, db = torch.ops.relm_mp.film_mish_backward(grad.reshape(u.shape), u, [0, u.size(0)],
+                                                           one, shift, None)
         x2 = x.reshape(-1, x.size(-1))
-        gx = du.matmul(weight).view(*x.shape[:-1], weight.size(1)) if ctx.needs_input_grad[0] else None
+        gx = _input_grad(du, weight, x) if ctx.needs_input_grad[0] else None
         gw = weight_grad(du, x2) if ctx.needs_input_grad[1] else None
         gb = db[0] if ctx.has_bias and ctx.needs_input_grad[2] else None
         return gx, gw, gb

@@ -105,6 +105,7 @@ def build_torch_ext(verbose: bool = False) -> Path:
         "-ltorch_hip",
         "-lc10",
         "-lc10_hip",
+        "-lhipblas",
         "-Wl,-rpath,$ORIGIN",
         f"-Wl,-rpath,{tdir / 'lib'}",
         "-o",

@@ -13,6 +13,7 @@
 //     (mp_ops.cpp:2913-3003).
 // GPU tensors never take the CPU lane.
 #include <ATen/ATen.h>
+#include <ATen/hip/HIPContext.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <c10/util/intrusive_ptr.h>
@@ -1727,6 +1728,44 @@ std::tuple<Tensor, Tensor, Tensor> film_mish_backward(const Tensor& grad, const 
     return {ds, sums.select(1, 0), sums.select(1, 1)};
 }
 
+// ---- a @ b^T for the models' narrow Linears (no counterpart in the reference) ----
+//
+// a [M, K], b [N, K], float32 on one GPU, unit column strides: a @ b^T as a
+// new [M, N] tensor, through hipBLAS (rocBLAS) on torch's handle for the
+// current stream.  For the tall, narrow products of the relation MLPs (M in
+// the hundreds of thousands, K and N of 64 to 128) rocBLAS streams at about
+// the HBM rate where the library GEMM torch picks (hipBLASLt) runs 2-3x
+// slower; the caller chooses which shapes come here.
+Tensor mm_nt(const Tensor& a, const Tensor& b) {
+    TORCH_CHECK(a.dim() == 2 && b.dim() == 2 && a.size(1) == b.size(1),
+                "mm_nt: a [M, K] and b [N, K] expected.");
+    TORCH_CHECK(a.is_cuda() && b.device() == a.device() && a.scalar_type() == at::kFloat &&
+                    b.scalar_type() == at::kFloat,
+                "mm_nt: float32 tensors on one GPU expected.");
+    const int64_t M = a.size(0), K = a.size(1), N = b.size(0);
+    const int64_t lim = std::numeric_limits<int>::max();
+    TORCH_CHECK(M <= lim && N <= lim && K <= lim, "mm_nt: sizes must fit 32 bits.");
+    const Tensor A = (a.stride(1) == 1 && a.stride(0) >= std::max<int64_t>(K, 1)) ? a : a.contiguous();
+    const Tensor B = (b.stride(1) == 1 && b.stride(0) >= std::max<int64_t>(K, 1)) ? b : b.contiguous();
+    TORCH_CHECK(A.stride(0) <= lim && B.stride(0) <= lim, "mm_nt: row strides must fit 32 bits.");
+    c10::OptionalDeviceGuard guard(a.device());
+    Tensor out = at::empty({M, N}, a.options());
+    if (M == 0 || N == 0) return out;
+    if (K == 0) return out.zero_();
+    // column-major view: out^T [N, M] = op(B) [N, K] x A^T [K, M], with B read
+    // as a K x N column-major matrix (ld = its row stride) and transposed
+    const float one = 1.0f, zero = 0.0f;
+    hipblasHandle_t handle = at::cuda::getCurrentCUDABlasHandle();
+    const hipblasStatus_t st =
+        hipblasSgemm(handle, HIPBLAS_OP_T, HIPBLAS_OP_N, static_cast<int>(N), static_cast<int>(M),
+                     static_cast<int>(K), &one, B.data_ptr<float>(), static_cast<int>(B.stride(0)),
+                     A.data_ptr<float>(), static_cast<int>(A.stride(0)), &zero, out.data_ptr<float>(),
+                     static_cast<int>(N));
+    TORCH_CHECK(st == HIPBLAS_STATUS_SUCCESS, "mm_nt: hipblasSgemm failed (status ", static_cast<int>(st),
+                ").");
+    return out;
+}
+
 }  // namespace relm_amd
 
 TORCH_LIBRARY(relm_mp, m) {
@@ -1757,6 +1796,7 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("plan_cache_stats() -> int[]");
     m.def("film_mish(Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> Tensor");
     m.def("film_mish_backward(Tensor grad, Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> (Tensor, Tensor, Tensor)");
+    m.def("mm_nt(Tensor a, Tensor b) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
@@ -1785,4 +1825,5 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("plan_cache_stats", relm_amd::plan_cache_stats);
     m.impl("film_mish", relm_amd::film_mish);
     m.impl("film_mish_backward", relm_amd::film_mish_backward);
+    m.impl("mm_nt", relm_amd::mm_nt);
 }

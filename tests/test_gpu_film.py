@@ -186,3 +186,30 @@ def test_linear_mish_against_float64(width: int, rows: int) -> None:
         _log(f"  {name}: fused {e_fused:.3g} torch {e_plain:.3g} (scale {scale:.3g})")
         assert e_fused <= 8 * e_plain + 32 * 1.2e-7 * scale, name
 
+
+
+@pytest.mark.parametrize("m,k,n,slice_cols", [(204800, 64, 64, False), (20000, 96, 96, False),
+                                              (5000, 128, 32, False), (3001, 64, 128, True),
+                                              (0, 64, 64, False), (7, 0, 5, False)])
+def test_mm_nt_against_float64(m: int, k: int, n: int, slice_cols: bool) -> None:
+    """torch.ops.relm_mp.mm_nt (a @ b^T through hipBLAS on torch's handle):
+    against float64, the same bits on a second call, and a column slice of a
+    wider matrix read in place."""
+
+    _log(f"mm_nt m={m} k={k} n={n} slice={slice_cols}")
+    g = torch.Generator(device=DEV).manual_seed(m + k + n)
+    if slice_cols:
+        wide = torch.randn(m, k + 14, device=DEV, generator=g)
+        a = wide[:, 14:]
+        assert a.stride(0) == k + 14
+    else:
+        a = torch.randn(m, k, device=DEV, generator=g)
+    b = torch.randn(n, k, device=DEV, generator=g)
+    out = torch.ops.relm_mp.mm_nt(a, b)
+    assert out.shape == (m, n) and out.is_contiguous()
+    want = a.double() @ b.double().t()
+    # fp32 products and sums over k terms of |a||b| ~ 1
+    torch.testing.assert_close(out.double(), want, rtol=0, atol=4 * 1.2e-7 * max(k, 1) * 4)
+    assert torch.equal(torch.ops.relm_mp.mm_nt(a, b), out)
+    with pytest.raises(RuntimeError, match="mm_nt"):
+        torch.ops.relm_mp.mm_nt(a, b[:, :-1] if k > 0 else torch.zeros(n, 1, device=DEV))
