@@ -703,12 +703,16 @@ class CentralizedRelationalGNN(nn.Module):
 
 def train_step(model: nn.Module, batch: RelationalBatch, routing: dict) -> Tensor:
     """Forward + backward of loss = mean(out^2), as the reference's benchmark
-    (scripts/benchmark_relational_models.py:287-295)."""
+    (scripts/benchmark_relational_models.py:287-295).  The routing's index
+    tensors are built once per batch and never written during the step, so
+    the step runs in one mp.plan_scope: each layer after the first reuses
+    the index plans of the first without comparing the indices again."""
 
     model.zero_grad(set_to_none=True)
-    out = model(batch, routing)
-    loss = out.square().mean()
-    loss.backward()
+    with mp.plan_scope():
+        out = model(batch, routing)
+        loss = out.square().mean()
+        loss.backward()
     return loss.detach()
 
 

@@ -185,6 +185,10 @@ class PlanCache {
     PlanPtr lookup(int role, const Tensor& key, const Tensor* gather, int64_t key_bound,
                    int64_t gather_bound, hipStream_t s) {
         if (!enabled_) return PlanPtr();
+        if (PlanPtr t = trusted(role, key, gather, key_bound, gather_bound)) {
+            t->use_on(s);
+            return t;
+        }
         struct Cand {
             PlanPtr ref;
             bool same;
@@ -236,6 +240,7 @@ class PlanCache {
                 note_tensors(e, key, gather);
             }
             ++(cand[j].same ? same_hits_ : other_hits_);
+            remember(cand[j].ref, key, gather);
             return cand[j].ref;
         }
         ++misses_;
@@ -249,6 +254,7 @@ class PlanCache {
         const size_t bytes = static_cast<size_t>(ref->mem.numel());
         if (bytes > limit_) return;
         std::lock_guard<std::mutex> lock(mu_);
+        remember(ref, key, gather);
         Entry e;
         e.ref = ref;
         e.bytes = bytes;
@@ -269,15 +275,33 @@ class PlanCache {
     void clear() {
         std::lock_guard<std::mutex> lock(mu_);
         entries_.clear();
+        trusted_.clear();
         total_ = 0;
     }
 
+    // Trust scopes (plan_trust_enter / plan_trust_exit, nestable, process
+    // wide): while one is open, the caller promises that no index tensor is
+    // written, so a plan built or compared equal in the scope is served again
+    // for the very same tensors (same TensorImpl, version, data pointer and
+    // size) without comparing them.  Closing the outermost scope forgets
+    // those tensors.
+    void trust_enter() {
+        std::lock_guard<std::mutex> lock(mu_);
+        ++trust_depth_;
+    }
+
+    void trust_exit() {
+        std::lock_guard<std::mutex> lock(mu_);
+        if (trust_depth_ > 0 && --trust_depth_ == 0) trusted_.clear();
+    }
+
     // entries, hits with the same tensors, hits with other tensors of equal
-    // content, misses (lookups that found no equal plan), bytes kept, peak bytes
+    // content, misses (lookups that found no equal plan), bytes kept, peak
+    // bytes, plans served in trust scopes without a comparison
     std::vector<int64_t> stats() {
         std::lock_guard<std::mutex> lock(mu_);
         return {static_cast<int64_t>(entries_.size()), same_hits_, other_hits_, misses_,
-                static_cast<int64_t>(total_), static_cast<int64_t>(peak_)};
+                static_cast<int64_t>(total_), static_cast<int64_t>(peak_), trusted_hits_};
     }
 
     int64_t size() {
@@ -287,6 +311,55 @@ class PlanCache {
 
    private:
     static constexpr size_t kMaxEntries = 64;
+    static constexpr size_t kMaxTrusted = 64;
+
+    // A plan and the tensors it was built or verified for in the open trust
+    // scope; the references keep the TensorImpl addresses from being reused.
+    struct Trusted {
+        PlanPtr ref;
+        Tensor key;
+        Tensor gather;
+        uint32_t key_ver = 0;
+        uint32_t gather_ver = 0;
+    };
+
+    static bool same_tensor(const Tensor& held, uint32_t ver, const Tensor& t) {
+        return held.unsafeGetTensorImpl() == t.unsafeGetTensorImpl() && version(t) == ver &&
+               held.data_ptr() == t.data_ptr() && held.numel() == t.numel();
+    }
+
+    PlanPtr trusted(int role, const Tensor& key, const Tensor* gather, int64_t key_bound,
+                    int64_t gather_bound) {
+        std::lock_guard<std::mutex> lock(mu_);
+        if (trust_depth_ == 0) return PlanPtr();
+        for (const Trusted& t : trusted_) {
+            const PlanRef& r = *t.ref;
+            if (r.role != role || r.key_bound != key_bound ||
+                (gather_bound >= 0 && r.gather_bound != gather_bound) ||
+                !same_tensor(t.key, t.key_ver, key) || t.gather.defined() != (gather != nullptr) ||
+                (gather != nullptr && !same_tensor(t.gather, t.gather_ver, *gather)))
+                continue;
+            ++trusted_hits_;
+            return t.ref;
+        }
+        return PlanPtr();
+    }
+
+    // Records (ref, key, gather) for the open trust scope; mu_ held.
+    void remember(const PlanPtr& ref, const Tensor& key, const Tensor* gather) {
+        if (trust_depth_ == 0) return;
+        if (trusted_.size() >= kMaxTrusted) trusted_.erase(trusted_.begin());
+        Trusted t;
+        t.ref = ref;
+        t.key = key;
+        t.key_ver = version(key);
+        if (gather != nullptr) {
+            t.gather = *gather;
+            t.gather_ver = version(*gather);
+        }
+        trusted_.push_back(std::move(t));
+    }
+
 
     // The tensors a plan was last used with, kept only as a hint for ordering
     // the candidates: the address may belong to a later tensor by now, which
@@ -336,6 +409,9 @@ class PlanCache {
     int64_t same_hits_ = 0;
     int64_t other_hits_ = 0;
     int64_t misses_ = 0;
+    int64_t trusted_hits_ = 0;
+    int trust_depth_ = 0;
+    std::vector<Trusted> trusted_;
     bool enabled_ = true;
     bool identity_only_ = false;
 };
@@ -1644,6 +1720,10 @@ int64_t plan_cache_size() { return PlanCache::get().size(); }
 
 std::vector<int64_t> plan_cache_stats() { return PlanCache::get().stats(); }
 
+void plan_trust_enter() { PlanCache::get().trust_enter(); }
+
+void plan_trust_exit() { PlanCache::get().trust_exit(); }
+
 // ---- fused FiLM step with Mish (no counterpart in the reference) ---------------
 //
 // y = mish(beta[k] + gamma[k] * (s + add[k])) over row ranges k of s (one
@@ -1717,6 +1797,10 @@ std::tuple<Tensor, Tensor, Tensor> film_mish_backward(const Tensor& grad, const 
                                         ds.data_ptr<float>(), partial.data_ptr<float>(), blocks,
                                         current_stream(a.s)));
     // per range, the sums of its blocks (consecutive, RELM_MP_FILM_ROWS_PER_BLOCK rows each)
+    if (k == 1 && blocks > 0) {
+        const Tensor sum = partial.sum(0);  // [2, width]
+        return {ds, sum.narrow(0, 0, 1), sum.narrow(0, 1, 1)};
+    }
     Tensor sums = at::zeros({k, 2, width}, a.s.options());
     int64_t b0 = 0;
     for (int32_t r = 0; r < k; ++r) {
@@ -1794,6 +1878,8 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("plan_cache_clear() -> ()");
     m.def("plan_cache_size() -> int");
     m.def("plan_cache_stats() -> int[]");
+    m.def("plan_trust_enter() -> ()");
+    m.def("plan_trust_exit() -> ()");
     m.def("film_mish(Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> Tensor");
     m.def("film_mish_backward(Tensor grad, Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> (Tensor, Tensor, Tensor)");
     m.def("mm_nt(Tensor a, Tensor b) -> Tensor");
@@ -1823,6 +1909,8 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("plan_cache_clear", relm_amd::plan_cache_clear);
     m.impl("plan_cache_size", relm_amd::plan_cache_size);
     m.impl("plan_cache_stats", relm_amd::plan_cache_stats);
+    m.impl("plan_trust_enter", relm_amd::plan_trust_enter);
+    m.impl("plan_trust_exit", relm_amd::plan_trust_exit);
     m.impl("film_mish", relm_amd::film_mish);
     m.impl("film_mish_backward", relm_amd::film_mish_backward);
     m.impl("mm_nt", relm_amd::mm_nt);

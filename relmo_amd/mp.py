@@ -13,6 +13,8 @@ otherwise.
 
 from __future__ import annotations
 
+import contextlib
+
 from .mp_autograd import (
     _FaninReduceLogSumExpFunction,
     _FaninReduceSumFunction,
@@ -31,7 +33,7 @@ from .mp_pack import (
     fanout_pack_multi_python,
     fanout_scatter_python,
 )
-from .mp_runtime import TORCH_IMPORT_ERROR, assert_runtime_compat, available, require_torch, torch
+from .mp_runtime import TORCH_IMPORT_ERROR, assert_runtime_compat, available, ops_namespace, require_torch, torch
 
 
 def _first(parts):
@@ -199,6 +201,34 @@ def _lgan_relation_graph_step(relation_pair_x, rr_src, rr_dst, tn_rel, tn_ent, n
     )
 
 
+@contextlib.contextmanager
+def plan_scope():
+    """Trust scope for the library's index plans (no counterpart in relmo).
+
+    Every op call compares its index tensors with the plans it could reuse
+    (a device pass over the indices), so that a plan is never served for
+    indices that changed - also through ``.data`` or a raw pointer, which
+    leave the tensor's version unchanged.  Inside this scope the caller
+    promises that no index tensor passed to the ops is written; a plan built
+    or compared equal in the scope is then served again for the very same
+    tensors (same tensor object, version, data pointer and size) without the
+    comparison, and the tensors are released when the outermost scope closes.
+    Scopes nest and hold for the whole process (the backward's calls on
+    autograd's threads included).  Without the library loaded the scope does
+    nothing."""
+
+    ns = ops_namespace() if library_ready("plan_trust_enter") else None
+    enter = getattr(ns, "plan_trust_enter", None) if ns is not None else None
+    if enter is None:
+        yield
+        return
+    enter()
+    try:
+        yield
+    finally:
+        ns.plan_trust_exit()
+
+
 __all__ = [
     "MODE_LOGSUMEXP",
     "MODE_MEAN",
@@ -214,4 +244,5 @@ __all__ = [
     "fanout_pack_from_edges",
     "fanout_pack_multi",
     "fanout_scatter",
+    "plan_scope",
 ]

@@ -42,8 +42,9 @@ def _stats() -> dict[str, int]:
     "same" (last used with the same tensor objects) or "other" is only the
     cache's ordering hint: a new tensor can occupy a freed tensor's address."""
 
-    entries, same, other, misses, kept, peak = torch.ops.relm_mp.plan_cache_stats()
-    return {"entries": entries, "same": same, "other": other, "hits": same + other, "misses": misses}
+    entries, same, other, misses, kept, peak, trusted = torch.ops.relm_mp.plan_cache_stats()
+    return {"entries": entries, "same": same, "other": other, "hits": same + other, "misses": misses,
+            "trusted": trusted}
 
 
 def _delta(before: dict, after: dict) -> dict:
@@ -264,7 +265,7 @@ def test_cache_memory_stays_bounded(mp_env) -> None:
     for seed in range(12):
         rel, src, dst, K = _fanin_case(100 + seed)
         mp.fanin_reduce(rel, src, dst, K, 0)
-    entries, _, _, _, kept, peak = ns.plan_cache_stats()
+    entries, _, _, _, kept, peak, _trusted = ns.plan_cache_stats()
     limit = int(os.environ.get("RELM_MP_PLAN_CACHE_MB", "2048")) << 20
     assert 0 < kept <= peak <= limit and entries >= 1
 
@@ -293,3 +294,61 @@ def test_inference_mode_indices(mp_env) -> None:
     assert np.array_equal(a.cpu().numpy(), _want_sum(rel, src, dst, K))
     want = oracle.fanout_scatter(rel.cpu().numpy(), src.cpu().numpy(), dst.cpu().numpy(), K)
     assert np.array_equal(f1.cpu().numpy(), want)
+
+
+def test_trust_scope_serves_the_same_tensors_without_comparing(mp_env) -> None:
+    """In an mp.plan_scope the plan of a call is served again for the very same
+    index tensors without the device comparison (counted as "trusted"); new
+    tensors of equal content are still compared, and after the scope a write
+    through .data is seen again."""
+
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    ns.plan_cache_clear()
+    rel, src, dst, K = _fanin_case(7)
+    want = _want_sum(rel, src, dst, K)
+    with mp.plan_scope():
+        with mp.plan_scope():  # nested: the outer scope keeps the records
+            before = _stats()
+            first = mp.fanin_reduce(rel, src, dst, K, 0)
+            d = _delta(before, _stats())
+            assert d["trusted"] == 0 and d["misses"] == 1, d
+        for rep in range(3):
+            before = _stats()
+            out = mp.fanin_reduce(rel, src, dst, K, 0)
+            d = _delta(before, _stats())
+            _log(f"trust scope call {rep}: {d}")
+            assert d["trusted"] == 1 and d["hits"] == 0 and d["misses"] == 0, d
+            assert torch.equal(out, first)
+        before = _stats()
+        out = mp.fanin_reduce(rel, src.clone(), dst.clone(), K, 0)
+        d = _delta(before, _stats())
+        assert d["trusted"] == 0 and d["hits"] == 1, d
+        assert torch.equal(out, first)
+    assert np.array_equal(first.cpu().numpy(), want)
+    # scope closed: the same tensors are compared again, so an untracked write is seen
+    new_dst = torch.flip(dst, [0]).contiguous()
+    dst.data[:] = new_dst
+    before = _stats()
+    out = mp.fanin_reduce(rel, src, dst, K, 0)
+    d = _delta(before, _stats())
+    assert d["trusted"] == 0 and d["misses"] == 1, d
+    assert np.array_equal(out.cpu().numpy(), _want_sum(rel, src, new_dst, K))
+
+
+def test_trust_scope_closes_on_error(mp_env) -> None:
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    ns.plan_cache_clear()
+    rel, src, dst, K = _fanin_case(8)
+    with pytest.raises(ValueError, match="boom"):
+        with mp.plan_scope():
+            mp.fanin_reduce(rel, src, dst, K, 0)
+            raise ValueError("boom")
+    before = _stats()
+    mp.fanin_reduce(rel, src, dst, K, 0)
+    d = _delta(before, _stats())
+    assert d["trusted"] == 0 and d["hits"] == 1, d
+

@@ -783,3 +783,21 @@ def test_planned_ops_on_the_cpu_lane(ops) -> None:
         assert torch.equal(got, want)
     with pytest.raises((RuntimeError, ValueError), match="Unsupported fanin_reduce mode"):
         ops.fanin_reduce_planned(rel, src, dst, 4, 2)
+
+
+def test_plan_scope_nests_and_survives_errors() -> None:
+    """mp.plan_scope enters and leaves the library's trust scope (CPU: nothing
+    is served from it; the calls only have to balance)."""
+
+    import torch
+
+    from relmo_amd import mp
+
+    with mp.plan_scope():
+        with mp.plan_scope():
+            pass
+    with pytest.raises(KeyError):
+        with mp.plan_scope():
+            raise KeyError("x")
+    stats = torch.ops.relm_mp.plan_cache_stats()
+    assert len(stats) == 7 and stats[6] == 0
