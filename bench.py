@@ -272,10 +272,14 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
     function, a ninth of its multiply-adds at C5); the FiLM step with its
     Mish and the Linear after it keep only the gathered sums (8 GB per
     layer) and recompute the Mish output in the backward with the fused
-    kernel, which keeps the step under one GPU's 288 GB.  The step on the
-    assembled input is reported beside it ("assembled_input_sum"), with the
-    whole central module recomputed in the backward (activation
-    checkpointing)."""
+    kernel, which keeps the step under one GPU's 288 GB.  With sum and mean
+    the hidden rows are added up per (object, slot position) before the
+    output Linear (CentralizedRelationalGNN._central_messages: the output
+    Linear over 0.59 M objects instead of 5.07 M nodes); logsumexp is not
+    linear and keeps the per-node outputs.  Reported beside them: sum with
+    the per-node outputs ("gathered_sum") and the step on the assembled input
+    ("assembled_input_sum", the whole central module recomputed in the
+    backward by activation checkpointing)."""
 
     from relmo_amd import consumers as C
 
@@ -290,22 +294,24 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
         log("  generating the C5 batch (2048 graphs)")
         batch = C.synthetic_c5(dev)
         make = lambda mode: C.CentralizedRelationalGNN(128, 10, batch.relations, mode, recompute_central=True,
-                                                       gather_first_linear=True).to(dev)
+                                                       gather_first_linear=True, sum_before_output=True).to(dev)
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects,
                "relation_nodes": int(sum(a.size(0) for a in batch.atoms.values())), "emb": 128,
                "layers": 10,
                "central_mlp": "FiLM step + Mish + Linear keep the gathered sums, Mish output recomputed in the backward",
-               "first_linear": "per object, gathered per relation node (fanin sum over the slot edges)"}
+               "first_linear": "per object, gathered per relation node (fanin sum over the slot edges)",
+               "output_linear": "sum / mean: on the hidden rows summed per (object, slot position)"}
         modes = ((0, "sum"), (1, "logsumexp"), (2, "mean"))
     res = {"config": cfg}
-    variants = [(mode, name, True) for mode, name in modes]
-    if which == "c5":  # the module on the assembled input, for comparison (sum)
-        variants.append((0, "assembled_input_sum", False))
-    for mode, name, gathered in variants:
+    variants = [(mode, name, True, True) for mode, name in modes]
+    if which == "c5":  # per-node outputs, and the module on the assembled input (sum)
+        variants += [(0, "gathered_sum", True, False), (0, "assembled_input_sum", False, False)]
+    for mode, name, gathered, summed in variants:
         torch.manual_seed(0)
         model = make(mode)
         if which == "c5":
             model.gather_first_linear = gathered
+            model.sum_before_output = summed
         routing = model.routing(batch)
         torch.cuda.reset_peak_memory_stats()
         t = timed(lambda: C.train_step(model, batch, routing), steps, warmup, torch.cuda.synchronize)

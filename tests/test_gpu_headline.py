@@ -236,7 +236,7 @@ def _step_grads(C, model, batch, routing, enable: str, monkeypatch):
                          if p.grad is not None}
 
 
-@pytest.mark.parametrize("model", ["c4", "c5", "c5_gathered", "c5_gathered_recompute"])
+@pytest.mark.parametrize("model", ["c4", "c5", "c5_gathered", "c5_gathered_recompute", "c5_summed"])
 def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     """One training step: the HIP lane (fp32) is about as close to a float64
     run of the same step as the ATen lane (fp32) is - per parameter, the
@@ -250,7 +250,9 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     float64 run of the module on the assembled input; c5_gathered_recompute
     adds the recomputation of the central activations (on the HIP lane the
     FiLM step's Mish output is recomputed by its fused kernel in the
-    backward, on the ATen lane the whole central module is checkpointed)."""
+    backward, on the ATen lane the whole central module is checkpointed);
+    c5_summed adds up the hidden rows per (object, slot) before the output
+    Linear for sum and mean (logsumexp keeps the gathered path)."""
 
     import copy
 
@@ -262,11 +264,12 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
         modes = (0, 1)
     else:
         batch = C.synthetic_c5(DEV, seed=5, num_graphs=96)
-        gathered = model.startswith("c5_gathered")
-        recompute = model.endswith("_recompute")
+        gathered = model.startswith(("c5_gathered", "c5_summed"))
+        recompute = model.endswith(("_recompute", "_summed"))
+        summed = model == "c5_summed"
         make = lambda mode: C.CentralizedRelationalGNN(  # noqa: E731
             128, 10, batch.relations, mode, gather_first_linear=gathered,
-            recompute_central=recompute).to(DEV)
+            recompute_central=recompute, sum_before_output=summed).to(DEV)
         modes = (0, 1, 2)
     for mode in modes:
         _log(f"{model} mode={mode}: {batch.num_graphs} graphs, {batch.num_objects} objects")

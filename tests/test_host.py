@@ -419,7 +419,9 @@ def test_central_first_linear_gathered_per_object(dtype) -> None:
     """The central MLP with its first Linear evaluated per object and gathered
     per relation node equals the module run on the assembled input: float64
     to 1e-12, float32 to a few ulps of the activations, for every mode, with
-    and without recomputation in the backward."""
+    and without recomputation in the backward; so does the path that adds up
+    the hidden rows per (object, slot) before the output Linear (sum and mean;
+    logsumexp keeps the gathered path)."""
 
     from relmo_amd import consumers as C
 
@@ -427,10 +429,12 @@ def test_central_first_linear_gathered_per_object(dtype) -> None:
     tol = {torch.float64: (1e-10, 1e-12), torch.float32: (2e-4, 1e-6)}[dtype]
     for mode in (0, 1, 2):
         runs = []
-        for gathered, recompute in ((False, False), (True, False), (True, True)):
+        for gathered, recompute, summed in ((False, False, False), (True, False, False), (True, True, False),
+                                            (True, False, True), (True, True, True)):
             torch.manual_seed(0)
             model = C.CentralizedRelationalGNN(8, 2, batch.relations, mode, recompute_central=recompute,
-                                               gather_first_linear=gathered).to(dtype)
+                                               gather_first_linear=gathered,
+                                               sum_before_output=summed).to(dtype)
             loss = C.train_step(model, batch, model.routing(batch))
             runs.append((loss, [p.grad.clone() for p in model.parameters()]))
         (la, ga), *others = runs
