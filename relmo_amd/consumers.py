@@ -251,8 +251,8 @@ def _unit_film(like: Tensor) -> tuple[Tensor, Tensor]:
     key = (like.device, like.size(-1))
     pair = _UNIT_FILM.get(key)
     if pair is None:
-        pair = (torch.ones(1, like.size(-1), device=like.device),
-                torch.zeros(1, like.size(-1), device=like.device))
+        pair = (torch.ones(1, like.size(-1), device=like.device, dtype=torch.float32),
+                torch.zeros(1, like.size(-1), device=like.device, dtype=torch.float32))
         _UNIT_FILM[key] = pair
     return pair
 
