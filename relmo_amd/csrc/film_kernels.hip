@@ -227,11 +227,15 @@ __global__ __launch_bounds__(kMaxThreads) void k_film_mish_backward(
     }
 }
 
+// Floats per lane: 4 where the width and every table are 16-byte aligned,
+// else 2 where they are 8-byte aligned, else 1.
 int film_vec(int64_t width, std::initializer_list<const void*> ptrs) {
-    if (width % 2 != 0) return 1;
-    for (const void* p : ptrs)
-        if (p != nullptr && reinterpret_cast<uintptr_t>(p) % 8 != 0) return 1;
-    return 2;
+    for (int v : {4, 2}) {
+        bool ok = width % v == 0;
+        for (const void* p : ptrs) ok = ok && (p == nullptr || reinterpret_cast<uintptr_t>(p) % (4 * v) == 0);
+        if (ok) return v;
+    }
+    return 1;
 }
 
 FilmRanges film_ranges(const int64_t* range_start, int32_t num_ranges) {
@@ -253,12 +257,14 @@ FilmRanges film_ranges(const int64_t* range_start, int32_t num_ranges) {
 // Most phases whose threads fit one workgroup (at most kMaxPhases), and the
 // workgroup size: a multiple of the wave.  Narrow rows take many phases, so
 // that a block of kRowsPerBlock rows still fills a workgroup (rows of 32
-// floats: 16 column pairs x 64 phases of 8 rows each).
+// floats: 16 column pairs x 64 phases of 8 rows each).  With 4 floats per
+// lane the phases' threads stay within 768, so that the backward's fp64
+// phase sums (phases * units * V * 16 bytes) fit 48 KB of LDS.
 constexpr int kMaxPhases = 64;
-FilmLayout film_layout(int64_t units) {
+FilmLayout film_layout(int64_t units, int V) {
+    const int64_t cap = V >= 4 ? 768 : kMaxThreads;
     FilmLayout L{static_cast<int>(units), 1};
-    if (units <= kMaxThreads / 2)
-        L.phases = static_cast<int>(std::min<int64_t>(kMaxPhases, kMaxThreads / units));
+    if (units <= cap / 2) L.phases = static_cast<int>(std::min<int64_t>(kMaxPhases, cap / units));
     return L;
 }
 
@@ -279,15 +285,15 @@ hipError_t launch_film_mish(const float* s, int64_t width, const int64_t* range_
     const FilmRanges R = film_ranges(range_start, num_ranges);
     const int64_t blocks = R.first_block[kMaxRanges];
     if (blocks == 0 || width == 0) return hipSuccess;
-    if (film_vec(width, {s, gamma, beta, add, y}) == 2) {
-        const FilmLayout L = film_layout(width / 2);
-        hipLaunchKernelGGL(k_film_mish<2>, dim3(static_cast<unsigned>(blocks)), dim3(film_threads(L)), 0, st,
-                           s, width, R, L, gamma, beta, add, y);
-    } else {
-        const FilmLayout L = film_layout(width);
-        hipLaunchKernelGGL(k_film_mish<1>, dim3(static_cast<unsigned>(blocks)), dim3(film_threads(L)), 0, st,
-                           s, width, R, L, gamma, beta, add, y);
-    }
+    const int V = film_vec(width, {s, gamma, beta, add, y});
+    const FilmLayout L = film_layout(width / V, V);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(film_threads(L)), 0, st, s,
+                           width, R, L, gamma, beta, add, y);
+    };
+    if (V == 4) launch(k_film_mish<4>);
+    else if (V == 2) launch(k_film_mish<2>);
+    else launch(k_film_mish<1>);
     return hipGetLastError();
 }
 
@@ -298,17 +304,15 @@ hipError_t launch_film_mish_backward(const float* s, const float* dy, int64_t wi
     const FilmRanges R = film_ranges(range_start, num_ranges);
     const int64_t blocks = R.first_block[kMaxRanges];
     if (blocks == 0 || width == 0) return hipSuccess;
-    if (film_vec(width, {s, dy, gamma, beta, add, ds, partial}) == 2) {
-        const FilmLayout L = film_layout(width / 2);
-        hipLaunchKernelGGL(k_film_mish_backward<2>, dim3(static_cast<unsigned>(blocks)),
-                           dim3(film_threads(L)), film_lds_bytes(L, 2), st, s, dy, width, R, L, gamma,
-                           beta, add, ds, partial);
-    } else {
-        const FilmLayout L = film_layout(width);
-        hipLaunchKernelGGL(k_film_mish_backward<1>, dim3(static_cast<unsigned>(blocks)),
-                           dim3(film_threads(L)), film_lds_bytes(L, 1), st, s, dy, width, R, L, gamma,
-                           beta, add, ds, partial);
-    }
+    const int V = film_vec(width, {s, dy, gamma, beta, add, ds, partial});
+    const FilmLayout L = film_layout(width / V, V);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(film_threads(L)),
+                           film_lds_bytes(L, V), st, s, dy, width, R, L, gamma, beta, add, ds, partial);
+    };
+    if (V == 4) launch(k_film_mish_backward<4>);
+    else if (V == 2) launch(k_film_mish_backward<2>);
+    else launch(k_film_mish_backward<1>);
     return hipGetLastError();
 }
 
