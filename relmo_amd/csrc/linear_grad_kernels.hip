@@ -1,0 +1,244 @@
+// Weight and bias gradients of a Linear with few columns over many rows:
+//
+//   dw[o][i] = sum_r g[r][o] * x[r][i],   db[o] = sum_r g[r][o]
+//
+// for g [M, O] (the gradient at the Linear's output) and x [M, I] (its input),
+// O and I at most 96, M up to millions (the relation MLPs of a RelationalGNN
+// step reduce over all atoms).  A library GEMM walks all of M in a few output
+// tiles for such shapes; here each wave reduces its own run of rows with the
+// fp32 matrix cores (v_mfma_f32_32x32x2f32: two rows per instruction into a
+// 32 x 32 tile of dw), the four waves of a workgroup add their tiles in LDS
+// in wave order, every workgroup stores one partial, and a second kernel adds
+// the partials in workgroup order: a fixed summation order, so the result is
+// the same on every run.
+//
+// Operand layout of v_mfma_f32_32x32x2f32 (one block): lane l supplies
+// A[l % 32][l / 32] and B[l / 32][l % 32]; accumulator register j of lane l
+// holds D[8 (j / 4) + 4 (l / 32) + j % 4][l % 32].  With A = g^T (row o of
+// the tile, k = the row of g) and B = x, lane l loads g[r + l / 32][o0 + l %
+// 32] and x[r + l / 32][i0 + l % 32]: two rows of 128 contiguous bytes per
+// operand and instruction.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "internal.h"
+
+namespace relm_mp {
+
+namespace {
+
+constexpr int kWgThreads = 256;
+constexpr int kWgWaves = kWgThreads / 64;
+constexpr int kMaxTiles = 3;  // O, I <= 96
+
+// Row pairs per iteration: the loads of the next iteration are issued before
+// this one's products, so 2 * U row pairs of operands are in flight per wave.
+template <int TO, int TI>
+constexpr int wgrad_unroll() { return TO * TI <= 1 ? 8 : (TO * TI <= 4 ? 4 : 2); }
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Row (within a 32 x 32 tile) of accumulator register j of lane l.
+__device__ __forceinline__ int acc_row(int lane, int j) { return 8 * (j / 4) + 4 * (lane / 32) + (j % 4); }
+
+// Partial of workgroup b: O * I entries of dw (row-major), then O of db.
+template <int TO, int TI>
+__global__ __launch_bounds__(kWgThreads) void k_linear_wgrad(const float* __restrict__ g, int64_t ldg,
+                                                             const float* __restrict__ x, int64_t ldx,
+                                                             int64_t M, int O, int I, int64_t rows_per_wg,
+                                                             float* __restrict__ partial) {
+    constexpr int T = TO * TI;
+    __shared__ float red[T * 1024 + TO * 32];
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    // this wave's rows: a quarter of the workgroup's, an even count
+    const int64_t per_wave = rows_per_wg / kWgWaves;
+    const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * rows_per_wg + wave * per_wave;
+    const int64_t r_end = min(M, r_begin + per_wave);
+
+    v16f acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = v16f{};
+    float bsum[TO];
+#pragma unroll
+    for (int t = 0; t < TO; ++t) bsum[t] = 0.0f;
+    bool o_ok[TO], i_ok[TI];
+#pragma unroll
+    for (int t = 0; t < TO; ++t) o_ok[t] = t * 32 + col < O;
+#pragma unroll
+    for (int t = 0; t < TI; ++t) i_ok[t] = t * 32 + col < I;
+
+    constexpr int U = wgrad_unroll<TO, TI>();
+    float a[U][TO], b[U][TI];
+    auto load = [&](int64_t r0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t row = r0 + 2 * u + half;
+            const bool rv = row < r_end;
+#pragma unroll
+            for (int t = 0; t < TO; ++t) a[u][t] = rv && o_ok[t] ? g[row * ldg + t * 32 + col] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < TI; ++t) b[u][t] = rv && i_ok[t] ? x[row * ldx + t * 32 + col] : 0.0f;
+        }
+    };
+    load(r_begin);
+    for (int64_t r0 = r_begin; r0 < r_end; r0 += 2 * U) {
+        float ca[U][TO], cb[U][TI];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int t = 0; t < TO; ++t) ca[u][t] = a[u][t];
+#pragma unroll
+            for (int t = 0; t < TI; ++t) cb[u][t] = b[u][t];
+        }
+        if (r0 + 2 * U < r_end) load(r0 + 2 * U);  // next iteration's rows, in flight meanwhile
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int to = 0; to < TO; ++to) {
+                bsum[to] += ca[u][to];
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti)
+                    acc[to * TI + ti] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[u][to], cb[u][ti],
+                                                                            acc[to * TI + ti], 0, 0, 0);
+            }
+        }
+    }
+    // bias: the two halves of the wave hold alternate rows
+#pragma unroll
+    for (int t = 0; t < TO; ++t) bsum[t] += __shfl_xor(bsum[t], 32, 64);
+
+    // waves add their tiles into LDS in wave order (wave 0 stores)
+    for (int w = 0; w < kWgWaves; ++w) {
+        if (wave == w) {
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    float& slot = red[t * 1024 + lane * 16 + j];
+                    slot = w == 0 ? acc[t][j] : slot + acc[t][j];
+                }
+            if (lane < 32) {
+#pragma unroll
+                for (int t = 0; t < TO; ++t) {
+                    float& slot = red[T * 1024 + t * 32 + lane];
+                    slot = w == 0 ? bsum[t] : slot + bsum[t];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    // the workgroup's partial in row-major order
+    float* out = partial + static_cast<int64_t>(blockIdx.x) * (static_cast<int64_t>(O) * I + O);
+    for (int e = static_cast<int>(threadIdx.x); e < O * I; e += kWgThreads) {
+        const int o = e / I, i = e % I;
+        const int t = (o / 32) * TI + i / 32;
+        const int ro = o % 32;
+        const int l = (i % 32) + 32 * ((ro / 4) % 2);
+        const int j = (ro / 8) * 4 + ro % 4;
+        out[e] = red[t * 1024 + l * 16 + j];
+    }
+    for (int o = static_cast<int>(threadIdx.x); o < O; o += kWgThreads)
+        out[static_cast<int64_t>(O) * I + o] = red[T * 1024 + (o / 32) * 32 + o % 32];
+}
+
+constexpr int kSumGroup = 32;  // partials added per thread in the first summing pass
+
+// First pass: sums[q][e] = partial[32 q][e] + ... + partial[32 q + 31][e] (in
+// that order; blockIdx.y = q), so that many threads share the adding up.
+__global__ __launch_bounds__(kWgThreads) void k_linear_wgrad_group(const float* __restrict__ partial,
+                                                                   int64_t wgs, int64_t n,
+                                                                   float* __restrict__ sums) {
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kWgThreads + threadIdx.x;
+    if (e >= n) return;
+    const int64_t b0 = static_cast<int64_t>(blockIdx.y) * kSumGroup;
+    float v[kSumGroup];
+#pragma unroll
+    for (int k = 0; k < kSumGroup; ++k) v[k] = b0 + k < wgs ? partial[(b0 + k) * n + e] : 0.0f;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kSumGroup; ++k) s += v[k];
+    sums[static_cast<int64_t>(blockIdx.y) * n + e] = s;
+}
+
+// dw[o][i] (row stride ldw) and db[o]: the group sums added in group order.
+__global__ __launch_bounds__(kWgThreads) void k_linear_wgrad_sum(const float* __restrict__ sums,
+                                                                 int64_t groups, int O, int I,
+                                                                 float* __restrict__ dw, int64_t ldw,
+                                                                 float* __restrict__ db) {
+    const int64_t n = static_cast<int64_t>(O) * I + O;
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kWgThreads + threadIdx.x;
+    if (e >= n) return;
+    float s = 0.0f;
+    for (int64_t q = 0; q < groups; ++q) s += sums[q * n + e];
+    if (e < static_cast<int64_t>(O) * I) {
+        dw[(e / I) * ldw + e % I] = s;
+    } else if (db != nullptr) {
+        db[e - static_cast<int64_t>(O) * I] = s;
+    }
+}
+
+// Workgroups: about 32 row pairs per wave, at most 2048 workgroups (fewer for
+// wide outputs, whose partials cost more to write and add up).
+int64_t wgrad_wgs(int64_t M, int64_t O, int64_t I) {
+    const int64_t rows = 2 * 32 * kWgWaves;
+    const int64_t cap = O * I <= 32 * 32 ? 2048 : (O * I <= 64 * 64 ? 1024 : 512);
+    return std::max<int64_t>(1, std::min<int64_t>(cap, (M + rows - 1) / rows));
+}
+
+}  // namespace
+
+// Partials of every workgroup, then the sums of the groups of kSumGroup.
+size_t linear_wgrad_scratch_bytes(int64_t M, int64_t O, int64_t I) {
+    const int64_t wgs = wgrad_wgs(M, O, I);
+    const int64_t groups = (wgs + kSumGroup - 1) / kSumGroup;
+    return static_cast<size_t>(wgs + groups) * static_cast<size_t>(O * I + O) * sizeof(float);
+}
+
+bool linear_wgrad_supported(int64_t O, int64_t I) {
+    return O >= 1 && I >= 1 && O <= kMaxTiles * 32 && I <= kMaxTiles * 32;
+}
+
+hipError_t launch_linear_wgrad(const float* g, int64_t ldg, const float* x, int64_t ldx, int64_t M,
+                               int64_t O, int64_t I, float* dw, int64_t ldw, float* db, float* scratch,
+                               hipStream_t s) {
+    const int64_t wgs = wgrad_wgs(M, O, I);
+    // rows per workgroup: a multiple of 2 * waves, covering M
+    const int64_t step = 2 * kWgWaves;
+    const int64_t rows_per_wg = ((M + wgs - 1) / wgs + step - 1) / step * step;
+    const int to = static_cast<int>((O + 31) / 32), ti = static_cast<int>((I + 31) / 32);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(kWgThreads), 0, s, g, ldg, x, ldx,
+                           M, static_cast<int>(O), static_cast<int>(I), rows_per_wg, scratch);
+    };
+    switch (to * 4 + ti) {
+        case 1 * 4 + 1: launch(k_linear_wgrad<1, 1>); break;
+        case 1 * 4 + 2: launch(k_linear_wgrad<1, 2>); break;
+        case 1 * 4 + 3: launch(k_linear_wgrad<1, 3>); break;
+        case 2 * 4 + 1: launch(k_linear_wgrad<2, 1>); break;
+        case 2 * 4 + 2: launch(k_linear_wgrad<2, 2>); break;
+        case 2 * 4 + 3: launch(k_linear_wgrad<2, 3>); break;
+        case 3 * 4 + 1: launch(k_linear_wgrad<3, 1>); break;
+        case 3 * 4 + 2: launch(k_linear_wgrad<3, 2>); break;
+        case 3 * 4 + 3: launch(k_linear_wgrad<3, 3>); break;
+        default: return hipErrorInvalidValue;
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int64_t n = O * I + O;
+    const int64_t groups = (wgs + kSumGroup - 1) / kSumGroup;
+    float* sums = scratch + wgs * n;
+    const unsigned eblocks = static_cast<unsigned>((n + kWgThreads - 1) / kWgThreads);
+    hipLaunchKernelGGL(k_linear_wgrad_group, dim3(eblocks, static_cast<unsigned>(groups)), dim3(kWgThreads), 0, s,
+                       scratch, wgs, n, sums);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_linear_wgrad_sum, dim3(eblocks), dim3(kWgThreads), 0, s, sums, groups,
+                       static_cast<int>(O), static_cast<int>(I), dw, ldw, db);
+    return hipGetLastError();
+}
+
+}  // namespace relm_mp
