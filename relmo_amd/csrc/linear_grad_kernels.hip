@@ -7,10 +7,9 @@
 // step reduce over all atoms).  A library GEMM walks all of M in a few output
 // tiles for such shapes; here each wave reduces its own run of rows with the
 // fp32 matrix cores (v_mfma_f32_32x32x2f32: two rows per instruction into a
-// 32 x 32 tile of dw), the four waves of a workgroup add their tiles in LDS
-// in wave order, every workgroup stores one partial, and a second kernel adds
-// the partials in workgroup order: a fixed summation order, so the result is
-// the same on every run.
+// 32 x 32 tile of dw), every workgroup stores one partial, and two more
+// kernels add the partials up in workgroup order: a fixed summation order, so
+// the result is the same on every run.
 //
 // Operand layout of v_mfma_f32_32x32x2f32 (one block): lane l supplies
 // A[l % 32][l / 32] and B[l / 32][l % 32]; accumulator register j of lane l
@@ -35,12 +34,20 @@ constexpr int kMaxTiles = 3;  // O, I <= 96
 // Row pairs per iteration: the loads of the next iteration are issued before
 // this one's products, so 2 * U row pairs of operands are in flight per wave.
 template <int TO, int TI>
-constexpr int wgrad_unroll() { return TO * TI <= 1 ? 8 : (TO * TI <= 4 ? 4 : 2); }
+constexpr int wgrad_unroll() { return TO * TI <= 4 ? 8 : 4; }
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 // Row (within a 32 x 32 tile) of accumulator register j of lane l.
 __device__ __forceinline__ int acc_row(int lane, int j) { return 8 * (j / 4) + 4 * (lane / 32) + (j % 4); }
+
+// Work of the four waves of a workgroup: with T = TO * TI output tiles of
+// 32 x 32, T < 4 tiles are each taken by 4 / T waves over disjoint quarters or
+// halves of the workgroup's rows (T = 3: three waves, one idle); T >= 4 tiles
+// are dealt out to the waves (tile t to wave t % 4) over all of its rows, so
+// that a wave holds at most three accumulators.
+template <int T>
+constexpr int wgrad_subsets() { return T == 1 ? 4 : (T == 2 ? 2 : 1); }
 
 // Partial of workgroup b: O * I entries of dw (row-major), then O of db.
 template <int TO, int TI>
@@ -49,100 +56,112 @@ __global__ __launch_bounds__(kWgThreads) void k_linear_wgrad(const float* __rest
                                                              int64_t M, int O, int I, int64_t rows_per_wg,
                                                              float* __restrict__ partial) {
     constexpr int T = TO * TI;
-    __shared__ float red[T * 1024 + TO * 32];
+    constexpr int S = wgrad_subsets<T>();
+    constexpr int MT = S > 1 ? 1 : (T + kWgWaves - 1) / kWgWaves;  // tiles per wave
+    constexpr int U = wgrad_unroll<TO, TI>();
+    __shared__ float red[S > 1 ? (S - 1) * T * 1024 + (S - 1) * TO * 32 : 1];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int col = lane & 31;
     const int half = lane >> 5;
-    // this wave's rows: a quarter of the workgroup's, an even count
-    const int64_t per_wave = rows_per_wg / kWgWaves;
-    const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * rows_per_wg + wave * per_wave;
-    const int64_t r_end = min(M, r_begin + per_wave);
+    const int sub = S > 1 ? wave / T : 0;
+    const int64_t per = rows_per_wg / S;  // even
+    const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * rows_per_wg + sub * per;
+    const int64_t r_end = min(M, r_begin + per);
 
-    v16f acc[T];
+    // this wave's tiles: t_k = first + k * 4 (S == 1) or the single t = wave % T
+    const int first = S > 1 ? wave % T : wave;
+    int to_k[MT], ti_k[MT];
+    bool own[MT], o_ok[MT], i_ok[MT];
 #pragma unroll
-    for (int t = 0; t < T; ++t) acc[t] = v16f{};
-    float bsum[TO];
+    for (int k = 0; k < MT; ++k) {
+        const int t = first + k * kWgWaves;
+        own[k] = (S > 1 ? wave < S * T : true) && t < T;
+        to_k[k] = own[k] ? t / TI : 0;
+        ti_k[k] = own[k] ? t % TI : 0;
+        o_ok[k] = own[k] && to_k[k] * 32 + col < O;
+        i_ok[k] = own[k] && ti_k[k] * 32 + col < I;
+    }
+    v16f acc[MT];
+    float bsum[MT];
 #pragma unroll
-    for (int t = 0; t < TO; ++t) bsum[t] = 0.0f;
-    bool o_ok[TO], i_ok[TI];
-#pragma unroll
-    for (int t = 0; t < TO; ++t) o_ok[t] = t * 32 + col < O;
-#pragma unroll
-    for (int t = 0; t < TI; ++t) i_ok[t] = t * 32 + col < I;
+    for (int k = 0; k < MT; ++k) {
+        acc[k] = v16f{};
+        bsum[k] = 0.0f;
+    }
 
-    constexpr int U = wgrad_unroll<TO, TI>();
-    float a[U][TO], b[U][TI];
+    float a[U][MT], b[U][MT];
     auto load = [&](int64_t r0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t row = r0 + 2 * u + half;
             const bool rv = row < r_end;
 #pragma unroll
-            for (int t = 0; t < TO; ++t) a[u][t] = rv && o_ok[t] ? g[row * ldg + t * 32 + col] : 0.0f;
-#pragma unroll
-            for (int t = 0; t < TI; ++t) b[u][t] = rv && i_ok[t] ? x[row * ldx + t * 32 + col] : 0.0f;
+            for (int k = 0; k < MT; ++k) {
+                a[u][k] = rv && o_ok[k] ? g[row * ldg + to_k[k] * 32 + col] : 0.0f;
+                b[u][k] = rv && i_ok[k] ? x[row * ldx + ti_k[k] * 32 + col] : 0.0f;
+            }
         }
     };
     load(r_begin);
     for (int64_t r0 = r_begin; r0 < r_end; r0 += 2 * U) {
-        float ca[U][TO], cb[U][TI];
+        float ca[U][MT], cb[U][MT];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int t = 0; t < TO; ++t) ca[u][t] = a[u][t];
-#pragma unroll
-            for (int t = 0; t < TI; ++t) cb[u][t] = b[u][t];
-        }
+            for (int k = 0; k < MT; ++k) {
+                ca[u][k] = a[u][k];
+                cb[u][k] = b[u][k];
+            }
         if (r0 + 2 * U < r_end) load(r0 + 2 * U);  // next iteration's rows, in flight meanwhile
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int to = 0; to < TO; ++to) {
-                bsum[to] += ca[u][to];
-#pragma unroll
-                for (int ti = 0; ti < TI; ++ti)
-                    acc[to * TI + ti] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[u][to], cb[u][ti],
-                                                                            acc[to * TI + ti], 0, 0, 0);
+            for (int k = 0; k < MT; ++k) {
+                bsum[k] += ca[u][k];
+                acc[k] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[u][k], cb[u][k], acc[k], 0, 0, 0);
             }
-        }
     }
-    // bias: the two halves of the wave hold alternate rows
+    // bias of o-tile to_k: kept by the wave of tile (to_k, 0); the two halves
+    // of the wave hold alternate rows
 #pragma unroll
-    for (int t = 0; t < TO; ++t) bsum[t] += __shfl_xor(bsum[t], 32, 64);
+    for (int k = 0; k < MT; ++k) bsum[k] += __shfl_xor(bsum[k], 32, 64);
 
-    // waves add their tiles into LDS in wave order (wave 0 stores)
-    for (int w = 0; w < kWgWaves; ++w) {
-        if (wave == w) {
+    if constexpr (S > 1) {
+        // waves of the later row subsets leave their tiles in LDS; the first
+        // subset's wave adds them in subset order
+        if (sub > 0 && wave < S * T) {
+            float* dst = red + ((sub - 1) * T + first) * 1024 + lane * 16;
 #pragma unroll
-            for (int t = 0; t < T; ++t)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    float& slot = red[t * 1024 + lane * 16 + j];
-                    slot = w == 0 ? acc[t][j] : slot + acc[t][j];
-                }
-            if (lane < 32) {
-#pragma unroll
-                for (int t = 0; t < TO; ++t) {
-                    float& slot = red[T * 1024 + t * 32 + lane];
-                    slot = w == 0 ? bsum[t] : slot + bsum[t];
-                }
-            }
+            for (int j = 0; j < 16; ++j) dst[j] = acc[0][j];
+            if (ti_k[0] == 0 && lane < 32) red[(S - 1) * T * 1024 + ((sub - 1) * TO + to_k[0]) * 32 + lane] = bsum[0];
         }
         __syncthreads();
+        if (sub == 0) {
+            for (int q = 1; q < S; ++q) {
+                const float* src = red + ((q - 1) * T + first) * 1024 + lane * 16;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[0][j] += src[j];
+                if (ti_k[0] == 0) bsum[0] += red[(S - 1) * T * 1024 + ((q - 1) * TO + to_k[0]) * 32 + col];
+            }
+        }
     }
-    // the workgroup's partial in row-major order
+    // the owning waves store the workgroup's partial in row-major order
     float* out = partial + static_cast<int64_t>(blockIdx.x) * (static_cast<int64_t>(O) * I + O);
-    for (int e = static_cast<int>(threadIdx.x); e < O * I; e += kWgThreads) {
-        const int o = e / I, i = e % I;
-        const int t = (o / 32) * TI + i / 32;
-        const int ro = o % 32;
-        const int l = (i % 32) + 32 * ((ro / 4) % 2);
-        const int j = (ro / 8) * 4 + ro % 4;
-        out[e] = red[t * 1024 + l * 16 + j];
+    if (sub == 0) {
+#pragma unroll
+        for (int k = 0; k < MT; ++k) {
+            if (!own[k]) continue;
+            const int i = ti_k[k] * 32 + col;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int o = to_k[k] * 32 + acc_row(lane, j);
+                if (o < O && i < I) out[static_cast<int64_t>(o) * I + i] = acc[k][j];
+            }
+            if (ti_k[k] == 0 && lane < 32 && to_k[k] * 32 + lane < O)
+                out[static_cast<int64_t>(O) * I + to_k[k] * 32 + lane] = bsum[k];
+        }
     }
-    for (int o = static_cast<int>(threadIdx.x); o < O; o += kWgThreads)
-        out[static_cast<int64_t>(O) * I + o] = red[T * 1024 + (o / 32) * 32 + o % 32];
 }
 
 constexpr int kSumGroup = 32;  // partials added per thread in the first summing pass
