@@ -288,7 +288,9 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
         batch = C.synthetic_c4(dev)
         make = lambda mode: C.RelationalGNN(32, 10, batch.relations, mode).to(dev)
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects, "emb": 32, "layers": 10,
-               "weight_gradients": "reductions over atoms split into 2048/4096-row chunks read in place (consumers.weight_grad)"}
+               "weight_gradients": ("up to 64 x 64 entries on the matrix cores (relm_mp::linear_weight_grad), "
+                                    "96 x 96 as 4096-row chunks read in place (consumers.weight_grad)"),
+               "narrow_products": "64-128 inner columns through rocBLAS (relm_mp::mm_nt)"}
         modes = ((0, "sum"), (1, "logsumexp"))
     else:
         log("  generating the C5 batch (2048 graphs)")
@@ -298,7 +300,8 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects,
                "relation_nodes": int(sum(a.size(0) for a in batch.atoms.values())), "emb": 128,
                "layers": 10,
-               "central_mlp": "FiLM step + Mish + Linear keep the gathered sums, Mish output recomputed in the backward",
+               "central_mlp": ("hidden width padded 398 -> 400 (zero columns); logsumexp: FiLM step + Mish + Linear "
+                               "keep the gathered sums, Mish output recomputed in the backward"),
                "first_linear": "per object, gathered per relation node (fanin sum over the slot edges)",
                "output_linear": "sum / mean: on the hidden rows summed per (object, slot position)"}
         modes = ((0, "sum"), (1, "logsumexp"), (2, "mean"))
