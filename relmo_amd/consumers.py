@@ -18,6 +18,7 @@ skipped, as in relational_gnn.py:322-326).
 
 from __future__ import annotations
 
+import contextlib
 import math
 from dataclasses import dataclass
 
@@ -144,12 +145,47 @@ def matmul_nt(a: Tensor, b: Tensor) -> Tensor:
     return a.matmul(b.t())
 
 
+# Contiguous transposes of the weights, shared by the layers of one training
+# step (shared_weight_transposes): {id(weight): (weight, version, transpose)}.
+_TRANSPOSES: dict | None = None
+
+
+@contextlib.contextmanager
+def shared_weight_transposes():
+    """Within the block, the input gradients of the narrow products reuse one
+    contiguous transpose per weight (the layers of a RelationalGNN share their
+    MLPs: ten layers, one transpose each instead of ten).  An entry is used
+    only for the same weight object at the same version; the block holds
+    them until it ends.  Process wide, like mp.plan_scope, so that the
+    backward's calls on autograd's threads see it."""
+
+    global _TRANSPOSES
+    prev = _TRANSPOSES
+    _TRANSPOSES = {}
+    try:
+        yield
+    finally:
+        _TRANSPOSES = prev
+
+
+def _transposed(weight: Tensor) -> Tensor:
+    cache = _TRANSPOSES
+    if cache is None:
+        return weight.t().contiguous()
+    hit = cache.get(id(weight))
+    if hit is not None and hit[0] is weight and hit[1] == weight._version:
+        return hit[2]
+    wt = weight.detach().t().contiguous()
+    cache[id(weight)] = (weight, weight._version, wt)
+    return wt
+
+
 def _input_grad(grad: Tensor, weight: Tensor, x: Tensor) -> Tensor:
     """grad @ weight ([M, out] x [out, in]) shaped as x."""
 
     g2 = grad.reshape(-1, grad.size(-1))
     if _narrow_nt(g2, weight.size(0), weight.size(1)):
-        return torch.ops.relm_mp.mm_nt(g2, weight.t().contiguous()).view(*x.shape[:-1], weight.size(1))
+        return torch.ops.relm_mp.mm_nt(g2, _transposed(weight)).view(*x.shape[:-1], weight.size(1))
     return grad.matmul(weight)
 
 
@@ -349,6 +385,34 @@ class MishMLP(nn.Sequential):
         return x
 
 
+class _ResidualConcat(torch.autograd.Function):
+    """cat_i(bases[i] + ys[i]) along the rows: each part's residual addition
+    written straight into its rows of the result (the per-predicate relation
+    outputs without a separate concatenation pass); the backward hands each
+    part's rows of the gradient to both of its inputs.  bases[i] and ys[i]
+    are [n_i, w_i] with w_i a multiple of the result's width d."""
+
+    @staticmethod
+    def forward(ctx, d: int, n: int, *parts: Tensor) -> Tensor:
+        bases, ys = parts[:n], parts[n:]
+        rows = [b.numel() // d for b in bases]
+        ctx.d, ctx.shapes, ctx.rows = d, [b.shape for b in bases], rows
+        out = bases[0].new_empty(sum(rows), d)
+        off = 0
+        for b, y, r in zip(bases, ys, rows):
+            torch.add(b, y, out=out[off:off + r].view(b.shape))
+            off += r
+        return out
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        grads, off = [], 0
+        for shape, r in zip(ctx.shapes, ctx.rows):
+            grads.append(grad[off:off + r].reshape(shape))
+            off += r
+        return (None, None, *grads, *grads)
+
+
 class Residual(nn.Module):
     """x[..., -width:] + f(x) (residual.py:4-31 with truncate_right=False)."""
 
@@ -542,11 +606,11 @@ class RelationalGNN(nn.Module):
             # gradients once, where each slice's would be a zero-filled full
             # copy, summed over the predicates
             parts = args.split([n * arity for _p, n, arity, _o in r["meta"]])
-            outs = []
-            for (pred, n, arity, _off), part in zip(r["meta"], parts):
-                feat = part.view(n, arity * self.d)
-                outs.append(self.rel_mlps[pred](feat).view(n * arity, self.d))
-            rel_flat = torch.cat(outs) if len(outs) > 1 else outs[0]
+            # each predicate's residual MLP, its residual addition written
+            # straight into the relation rows (_ResidualConcat)
+            feats = [part.view(n, arity * self.d) for (_p, n, arity, _o), part in zip(r["meta"], parts)]
+            ys = [self.rel_mlps[pred].module(feat) for (pred, _n, _a, _o), feat in zip(r["meta"], feats)]
+            rel_flat = _ResidualConcat.apply(self.d, len(feats), *feats, *ys)
             msgs = fanin_objects(self.mode, rel_flat, r, batch.num_objects)
             x = x + self.updater(torch.cat([x, msgs], dim=1))
         return x
@@ -817,10 +881,11 @@ def train_step(model: nn.Module, batch: RelationalBatch, routing: dict) -> Tenso
     (scripts/benchmark_relational_models.py:287-295).  The routing's index
     tensors are built once per batch and never written during the step, so
     the step runs in one mp.plan_scope: each layer after the first reuses
-    the index plans of the first without comparing the indices again."""
+    the index plans of the first without comparing the indices again; the
+    layers' shared MLP weights are transposed once (shared_weight_transposes)."""
 
     model.zero_grad(set_to_none=True)
-    with mp.plan_scope():
+    with mp.plan_scope(), shared_weight_transposes():
         out = model(batch, routing)
         loss = out.square().mean()
         loss.backward()

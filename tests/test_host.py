@@ -805,3 +805,40 @@ def test_plan_scope_nests_and_survives_errors() -> None:
             raise KeyError("x")
     stats = torch.ops.relm_mp.plan_cache_stats()
     assert len(stats) == 7 and stats[6] == 0
+
+
+def test_relational_gnn_residual_concat_matches_modules() -> None:
+    """RelationalGNN writes each predicate's residual MLP output straight into
+    the relation rows (_ResidualConcat): the same loss and gradients as
+    calling the Residual modules and concatenating their outputs (float64,
+    CPU, sum and logsumexp)."""
+
+    import torch
+
+    from relmo_amd import consumers as C
+    from relmo_amd import mp
+
+    batch = C.synthetic_c4("cpu", seed=2, num_graphs=3)
+    for mode in (0, 1):
+        torch.manual_seed(0)
+        model = C.RelationalGNN(8, 2, batch.relations, mode).double()
+        r = model.routing(batch)
+        loss = C.train_step(model, batch, r)
+        got = {k: p.grad.clone() for k, p in model.named_parameters()}
+
+        def reference_forward():
+            x = torch.zeros(batch.num_objects, model.d, dtype=torch.float64)
+            for _ in range(model.num_layers):
+                args = mp.fanout_scatter(x, r["obj"], r["flat"], r["total"])
+                outs = [model.rel_mlps[pred](args[off:off + n * a].view(n, a * model.d)).view(n * a, model.d)
+                        for pred, n, a, off in r["meta"]]
+                msgs = C.fanin_objects(mode, torch.cat(outs), r, batch.num_objects)
+                x = x + model.updater(torch.cat([x, msgs], dim=1))
+            return x
+
+        model.zero_grad(set_to_none=True)
+        ref_loss = reference_forward().square().mean()
+        ref_loss.backward()
+        torch.testing.assert_close(loss, ref_loss.detach(), rtol=1e-12, atol=1e-14)
+        for k, p in model.named_parameters():
+            torch.testing.assert_close(got[k], p.grad, rtol=1e-10, atol=1e-13, msg=lambda m, k=k: f"{k}: {m}")
