@@ -288,8 +288,7 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
         batch = C.synthetic_c4(dev)
         make = lambda mode: C.RelationalGNN(32, 10, batch.relations, mode).to(dev)
         cfg = {"graphs": batch.num_graphs, "objects": batch.num_objects, "emb": 32, "layers": 10,
-               "weight_gradients": ("up to 64 x 64 entries on the matrix cores (relm_mp::linear_weight_grad), "
-                                    "96 x 96 as 4096-row chunks read in place (consumers.weight_grad)"),
+               "weight_gradients": "reductions over atoms split into 2048/4096-row chunks read in place (consumers.weight_grad)",
                "narrow_products": "64-128 inner columns through rocBLAS (relm_mp::mm_nt)"}
         modes = ((0, "sum"), (1, "logsumexp"))
     else:

@@ -454,20 +454,6 @@ int relm_mp_film_mish_backward(const float* s, const float* dy, int64_t rows, in
                                const float* beta, const float* add, float* ds, float* partial,
                                int64_t partial_blocks, relm_mp_stream_t stream);
 
-/* ---- Weight and bias gradients of a narrow Linear (no counterpart in the
- * reference, whose models take them from the library GEMM through autograd) --
- * dw [out, in] = g^T x and db [out] = the column sums of g, for g [rows, out]
- * (the gradient at the Linear's output) and x [rows, in] (its input), float32,
- * row strides ldg >= out, ldx >= in, ldw >= in; 1 <= out, in <= 96; db may be
- * NULL.  The rows are reduced by the matrix cores in a fixed order (the result
- * does not change from run to run); workspace: at least
- * relm_mp_linear_weight_grad_workspace_size(rows, out, in) bytes of device
- * memory. */
-size_t relm_mp_linear_weight_grad_workspace_size(int64_t rows, int64_t out, int64_t in);
-int relm_mp_linear_weight_grad(const float* g, int64_t ldg, const float* x, int64_t ldx, int64_t rows,
-                               int64_t out, int64_t in, float* dw, int64_t ldw, float* db,
-                               void* workspace, size_t workspace_bytes, relm_mp_stream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

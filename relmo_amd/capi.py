@@ -67,8 +67,6 @@ EXPORTED_SYMBOLS = (
     "relm_mp_film_mish",
     "relm_mp_film_mish_blocks",
     "relm_mp_film_mish_backward",
-    "relm_mp_linear_weight_grad_workspace_size",
-    "relm_mp_linear_weight_grad",
 )
 
 
@@ -180,8 +178,6 @@ _SIGNATURES = {
     "relm_mp_film_mish_blocks": (_i64, [_vp, ctypes.c_int32]),
     "relm_mp_film_mish_backward": (
         _int, [_vp, _vp, _i64, _i64, _vp, ctypes.c_int32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
-    "relm_mp_linear_weight_grad_workspace_size": (_sz, [_i64, _i64, _i64]),
-    "relm_mp_linear_weight_grad": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_match": (
         _int,
         [_vp, _vp, _i64, ctypes.POINTER(_PP), ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), _vp,
@@ -642,21 +638,6 @@ def film_mish(s: torch.Tensor, range_start: list[int], gamma: torch.Tensor, beta
     check(lib().relm_mp_film_mish(_ptr(s), s.size(0), s.size(1), starts, k, _ptr(gamma), _ptr(beta),
                                   _ptr(add) if add is not None else None, _ptr(y), _stream(s)))
     return y
-
-
-def linear_weight_grad(g: torch.Tensor, x: torch.Tensor, bias: bool = True):
-    """``relm_mp_linear_weight_grad``: (g^T x [out, in], column sums of g [out] or None)."""
-
-    assert g.dim() == 2 and x.dim() == 2 and g.stride(1) == 1 and x.stride(1) == 1
-    out_f, in_f = g.size(1), x.size(1)
-    dw = torch.empty(out_f, in_f, dtype=g.dtype, device=g.device)
-    db = torch.empty(out_f, dtype=g.dtype, device=g.device) if bias else None
-    n = lib().relm_mp_linear_weight_grad_workspace_size(g.size(0), out_f, in_f)
-    ws = _bytes(max(n, 1), g)
-    # g and x may be column slices of wider matrices: their row strides are passed on
-    check(lib().relm_mp_linear_weight_grad(g.data_ptr(), g.stride(0), x.data_ptr(), x.stride(0), g.size(0), out_f,
-                                           in_f, _ptr(dw), in_f, _ptr(db), _ptr(ws), n, _stream(g)))
-    return dw, db
 
 
 def film_mish_backward(dy: torch.Tensor, s: torch.Tensor, range_start: list[int], gamma: torch.Tensor,

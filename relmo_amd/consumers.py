@@ -107,8 +107,6 @@ def weight_grad(grad_out: Tensor, inp: Tensor, chunk: int | None = None) -> Tens
     rounding.  Chunks default to 2048 rows for weights of at most 64 x 64
     entries, 4096 up to 256 x 256, 32768 above."""
 
-    if chunk is None and _wgrad_kernel(grad_out, inp):
-        return torch.ops.relm_mp.linear_weight_grad(grad_out, inp, False)[0]
     K = inp.size(0)
     out_f, in_f = grad_out.size(1), inp.size(1)
     if chunk is None:
@@ -189,29 +187,6 @@ def _input_grad(grad: Tensor, weight: Tensor, x: Tensor) -> Tensor:
     return grad.matmul(weight)
 
 
-def _wgrad_kernel(grad_out: Tensor, inp: Tensor) -> bool:
-    """Whether the library's weight-gradient kernel serves grad_out^T @ inp
-    (relm_mp::linear_weight_grad: the rows reduced on the matrix cores, the
-    bias gradient alongside): float32 on the GPU with at most 64 x 64 weight
-    entries, where it beats the chunked batched product (C4: 25 against 45 us
-    for 32 x 32 over 204,800 rows, 24-32 against 41-58 us for the update MLP's
-    weights over 102,400 objects); at 96 x 96 it does not."""
-
-    return (grad_out.dtype == torch.float32 and inp.dtype == torch.float32
-            and grad_out.size(1) * inp.size(1) <= 64 * 64
-            and library_op("linear_weight_grad", tensor=grad_out, gpu_only=True) is not None)
-
-
-def weight_and_bias_grad(grad_out: Tensor, inp: Tensor, bias: bool) -> tuple[Tensor, Tensor | None]:
-    """weight_grad and, with bias, the column sums of grad_out - from one
-    kernel where _wgrad_kernel allows."""
-
-    if _wgrad_kernel(grad_out, inp):
-        gw, gb = torch.ops.relm_mp.linear_weight_grad(grad_out, inp, bias)
-        return gw, (gb if bias else None)
-    return weight_grad(grad_out, inp), (grad_out.sum(0) if bias else None)
-
-
 class _Linear(torch.autograd.Function):
     """F.linear with the weight gradient of weight_grad; narrow products
     through matmul_nt (the bias then added in place)."""
@@ -233,12 +208,8 @@ class _Linear(torch.autograd.Function):
         g2 = grad.reshape(-1, grad.size(-1))
         x2 = x.reshape(-1, x.size(-1))
         gx = _input_grad(grad, weight, x) if ctx.needs_input_grad[0] else None
-        need_b = ctx.has_bias and ctx.needs_input_grad[2]
-        gw, gb = None, None
-        if ctx.needs_input_grad[1]:
-            gw, gb = weight_and_bias_grad(g2, x2, need_b)
-        elif need_b:
-            gb = g2.sum(0)
+        gw = weight_grad(g2, x2) if ctx.needs_input_grad[1] else None
+        gb = g2.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
         return gx, gw, gb
 
 

@@ -25,7 +25,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("RELM_MP_OFFLOAD_ARCH", "gfx950")
 
 HIP_SOURCES = ["plan_kernels.hip", "reduce_kernels.hip", "pack_kernels.hip", "match_kernels.hip",
-               "film_kernels.hip", "linear_grad_kernels.hip",
+               "film_kernels.hip",
                "capi.hip"]
 HIP_LIB = PKG_DIR / "librelm_mp_hip.so"
 TORCH_EXT = PKG_DIR / "relm_mp_ops.so"

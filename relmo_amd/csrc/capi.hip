@@ -717,30 +717,6 @@ int relm_mp_film_mish_backward(const float* s, const float* dy, int64_t rows, in
     return RELM_MP_OK;
 }
 
-size_t relm_mp_linear_weight_grad_workspace_size(int64_t rows, int64_t out, int64_t in) {
-    if (rows < 0 || !linear_wgrad_supported(out, in)) return 0;
-    return linear_wgrad_scratch_bytes(rows, out, in);
-}
-
-int relm_mp_linear_weight_grad(const float* g, int64_t ldg, const float* x, int64_t ldx, int64_t rows,
-                               int64_t out, int64_t in, float* dw, int64_t ldw, float* db,
-                               void* workspace, size_t workspace_bytes, relm_mp_stream_t stream) {
-    RELM_TRY(check_rows(rows, "rows"));
-    if (!linear_wgrad_supported(out, in))
-        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
-                         "relm_mp linear weight gradient: out and in must be in [1, 96]");
-    if (ldg < out || ldx < in || ldw < in)
-        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp linear weight gradient: row stride too small");
-    if (dw == nullptr || (rows > 0 && (g == nullptr || x == nullptr)))
-        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp linear weight gradient: NULL array");
-    if (workspace == nullptr || workspace_bytes < linear_wgrad_scratch_bytes(rows, out, in))
-        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp linear weight gradient: workspace too small");
-    RELM_HIP(launch_linear_wgrad(g, ldg, x, ldx, rows, out, in, dw, ldw, db, static_cast<float*>(workspace),
-                                 static_cast<hipStream_t>(stream)),
-             "relm_mp linear weight gradient kernels");
-    return RELM_MP_OK;
-}
-
 int relm_mp_pack_index(const relm_mp_index_part* parts, int32_t num_parts, int64_t* out_a,
                        int64_t* out_b, relm_mp_stream_t stream) {
     if (num_parts < 0 || (num_parts > 0 && parts == nullptr))

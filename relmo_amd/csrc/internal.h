@@ -160,17 +160,6 @@ hipError_t launch_film_mish_backward(const float* s, const float* dy, int64_t wi
                                      const float* gamma, const float* beta, const float* add,
                                      float* ds, float* partial, hipStream_t st);
 
-// ---- Linear weight gradients (linear_grad_kernels.hip) ------------------------
-// dw [O, I] (row stride ldw) = g^T x and db [O] = column sums of g (db may be
-// null) for g [M, O] (row stride ldg) and x [M, I] (row stride ldx), float32,
-// O and I in [1, 96] (linear_wgrad_supported); scratch holds
-// linear_wgrad_scratch_bytes(M, O, I) bytes of per-workgroup partials.
-bool linear_wgrad_supported(int64_t O, int64_t I);
-size_t linear_wgrad_scratch_bytes(int64_t M, int64_t O, int64_t I);
-hipError_t launch_linear_wgrad(const float* g, int64_t ldg, const float* x, int64_t ldx, int64_t M,
-                               int64_t O, int64_t I, float* dw, int64_t ldw, float* db, float* scratch,
-                               hipStream_t s);
-
 // ---- content comparison (match_kernels.hip) -------------------------------
 constexpr int kMaxMatch = RELM_MP_MAX_MATCH;
 // After the launches mismatch[c] == gen iff the snapshot of plans[c] differs

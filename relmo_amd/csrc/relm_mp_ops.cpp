@@ -1850,31 +1850,6 @@ Tensor mm_nt(const Tensor& a, const Tensor& b) {
     return out;
 }
 
-// Weight and bias gradients of a narrow Linear (no counterpart in the
-// reference): grad [M, O] and input [M, I] float32 on one GPU, unit column
-// strides, 1 <= O, I <= 96 -> (grad^T input [O, I], column sums of grad [O],
-// or an empty tensor without bias) through relm_mp_linear_weight_grad.
-std::tuple<Tensor, Tensor> linear_weight_grad(const Tensor& grad, const Tensor& input, bool bias) {
-    TORCH_CHECK(grad.dim() == 2 && input.dim() == 2 && grad.size(0) == input.size(0),
-                "linear_weight_grad: grad [M, O] and input [M, I] expected.");
-    TORCH_CHECK(grad.is_cuda() && input.device() == grad.device() && grad.scalar_type() == at::kFloat &&
-                    input.scalar_type() == at::kFloat,
-                "linear_weight_grad: float32 tensors on one GPU expected.");
-    const int64_t M = grad.size(0), O = grad.size(1), I = input.size(1);
-    TORCH_CHECK(O >= 1 && O <= 96 && I >= 1 && I <= 96, "linear_weight_grad: O and I must be in [1, 96].");
-    const Tensor G = (grad.stride(1) == 1 && grad.stride(0) >= O) ? grad : grad.contiguous();
-    const Tensor X = (input.stride(1) == 1 && input.stride(0) >= I) ? input : input.contiguous();
-    c10::OptionalDeviceGuard guard(grad.device());
-    Tensor dw = at::empty({O, I}, grad.options());
-    Tensor db = bias ? at::empty({O}, grad.options()) : at::empty({0}, grad.options());
-    const size_t ws_bytes = relm_mp_linear_weight_grad_workspace_size(M, O, I);
-    Tensor ws = byte_buffer(ws_bytes, grad);
-    raise_if(relm_mp_linear_weight_grad(G.data_ptr<float>(), G.stride(0), X.data_ptr<float>(), X.stride(0), M, O,
-                                        I, dw.data_ptr<float>(), I, bias ? db.data_ptr<float>() : nullptr,
-                                        ws.data_ptr(), ws_bytes, current_stream(G)));
-    return {dw, db};
-}
-
 }  // namespace relm_amd
 
 TORCH_LIBRARY(relm_mp, m) {
@@ -1908,7 +1883,6 @@ TORCH_LIBRARY(relm_mp, m) {
     m.def("film_mish(Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> Tensor");
     m.def("film_mish_backward(Tensor grad, Tensor s, int[] range_start, Tensor gamma, Tensor beta, Tensor? add) -> (Tensor, Tensor, Tensor)");
     m.def("mm_nt(Tensor a, Tensor b) -> Tensor");
-    m.def("linear_weight_grad(Tensor grad, Tensor input, bool bias) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
@@ -1940,5 +1914,4 @@ TORCH_LIBRARY_IMPL(relm_mp, CompositeImplicitAutograd, m) {
     m.impl("film_mish", relm_amd::film_mish);
     m.impl("film_mish_backward", relm_amd::film_mish_backward);
     m.impl("mm_nt", relm_amd::mm_nt);
-    m.impl("linear_weight_grad", relm_amd::linear_weight_grad);
 }

@@ -213,37 +213,3 @@ def test_mm_nt_against_float64(m: int, k: int, n: int, slice_cols: bool) -> None
     assert torch.equal(torch.ops.relm_mp.mm_nt(a, b), out)
     with pytest.raises(RuntimeError, match="mm_nt"):
         torch.ops.relm_mp.mm_nt(a, b[:, :-1] if k > 0 else torch.zeros(n, 1, device=DEV))
-
-
-@pytest.mark.parametrize("m,o,i,slice_cols", [(204800, 32, 32, False), (102400, 64, 64, True), (5003, 96, 96, False),
-                                              (777, 1, 33, False), (1, 64, 31, False), (0, 7, 9, False)])
-def test_linear_weight_grad_against_float64(m: int, o: int, i: int, slice_cols: bool) -> None:
-    """torch.ops.relm_mp.linear_weight_grad (grad^T input and the column sums of
-    grad on the matrix cores): against float64 within the fp32 bound of the
-    sums (a few eps times sqrt(m) for unit normal terms), the same bits on a
-    second call, a column slice of a wider matrix read in place, and the shape
-    checks."""
-
-    _log(f"linear_weight_grad m={m} o={o} i={i} slice={slice_cols}")
-    g = torch.Generator(device=DEV).manual_seed(m + 7 * o + i)
-    grad = torch.randn(m, o, device=DEV, generator=g)
-    if slice_cols:
-        wide = torch.randn(m, i + 5, device=DEV, generator=g)
-        inp = wide[:, 5:]
-    else:
-        inp = torch.randn(m, i, device=DEV, generator=g)
-    dw, db = torch.ops.relm_mp.linear_weight_grad(grad, inp, True)
-    assert dw.shape == (o, i) and db.shape == (o,)
-    want_w = grad.double().t() @ inp.double()
-    want_b = grad.double().sum(0)
-    tol = 64 * 1.2e-7 * max(m, 1) ** 0.5 * 4
-    torch.testing.assert_close(dw.double(), want_w, rtol=0, atol=tol)
-    torch.testing.assert_close(db.double(), want_b, rtol=0, atol=tol)
-    dw2, empty = torch.ops.relm_mp.linear_weight_grad(grad, inp, False)
-    assert torch.equal(dw2, dw) and empty.numel() == 0
-    from relmo_amd import capi
-
-    dw3, db3 = capi.linear_weight_grad(grad, inp, True)  # the C ABI gives the op's bits
-    assert torch.equal(dw3, dw) and torch.equal(db3, db)
-    with pytest.raises(RuntimeError, match="linear_weight_grad"):
-        torch.ops.relm_mp.linear_weight_grad(torch.zeros(m, 97, device=DEV), inp, True)
