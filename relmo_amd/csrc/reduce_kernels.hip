@@ -922,12 +922,27 @@ __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __r
     }
 }
 
+// The gathered index of edge e: the caller's int64 array, or a plan's int32
+// snapshot of it (tiles flagged plain hold the edge ids and are not stored) -
+// half the index bytes.
+struct GathersI64 {
+    const int64_t* __restrict__ p;
+    __device__ __forceinline__ int64_t operator()(int64_t e) const { return p[e]; }
+};
+struct GathersSnap {
+    const int32_t* __restrict__ p;
+    const uint32_t* __restrict__ plain;
+    __device__ __forceinline__ int64_t operator()(int64_t e) const {
+        return plain != nullptr && plain[e / RELM_MP_SNAP_TILE] != 0u ? e : static_cast<int64_t>(p[e]);
+    }
+};
+
 // Logsumexp backward with an inverse plan (injective keys):
-// grad_rel[r] = grad_out[d] * exp(rel[r] - out[d]), d = gathers[inv[r]], or 0.
-template <typename T, int V, int G>
+// grad_rel[r] = grad_out[d] * exp(rel[r] - out[d]), d = gathers(inv[r]), or 0.
+template <typename T, int V, int G, class Src>
 __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
     const int32_t* __restrict__ inv_in, const relm_mp_plan_counts* __restrict__ pc,
-    int64_t num_edges, const int64_t* __restrict__ gathers,
+    int64_t num_edges, Src gathers,
     int64_t num_gather,
     const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
     int64_t num_keys, int64_t D, T* __restrict__ grad_rel) {
@@ -946,7 +961,7 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
         for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * R, num_keys, num_edges);
         int64_t d[RU];
 #pragma unroll
-        for (int j = 0; j < RU; ++j) d[j] = e[j] >= 0 ? gathers[e[j]] : -1;
+        for (int j = 0; j < RU; ++j) d[j] = e[j] >= 0 ? gathers(e[j]) : -1;
         Pack<T, V> x[RU], g[RU], o[RU];
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
@@ -1255,7 +1270,7 @@ int segment_sum_scaled_t(const relm_mp_plan& plan, const void* table_v, int64_t 
 template <typename T>
 int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void* grad_out_v,
                    const void* out_v, const void* rel_v, int64_t emb, void* grad_rel_v,
-                   void* scratch, hipStream_t s) {
+                   void* scratch, hipStream_t s, const relm_mp_plan* snap = nullptr) {
     const T* grad_out = static_cast<const T*>(grad_out_v);
     const T* out = static_cast<const T*>(out_v);
     const T* rel = static_cast<const T*>(rel_v);
@@ -1267,11 +1282,17 @@ int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void*
         constexpr int G = decltype(gt)::value;
         constexpr int U = batch_rows<G>();
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
-            hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G>),
-                               row_grid(plan.num_keys, G, geo.slices, kLseRowsInFlight),
-                               dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
-                               gathers, plan.num_gather, grad_out, out, rel, plan.num_keys, emb,
-                               grad_rel);
+            const dim3 grid = row_grid(plan.num_keys, G, geo.slices, kLseRowsInFlight);
+            if (snap != nullptr) {
+                hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G, GathersSnap>), grid, dim3(kThreads), 0, s,
+                                   plan.inv, plan.counts, plan.num_edges,
+                                   GathersSnap{snap->snap_keys, snap->snap_key_plain}, plan.num_gather,
+                                   grad_out, out, rel, plan.num_keys, emb, grad_rel);
+            } else {
+                hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G, GathersI64>), grid, dim3(kThreads), 0, s,
+                                   plan.inv, plan.counts, plan.num_edges, GathersI64{gathers},
+                                   plan.num_gather, grad_out, out, rel, plan.num_keys, emb, grad_rel);
+            }
             return hip_error(hipGetLastError(), "relm_mp logsumexp backward kernel");
         }
         LseBwdOp<T, V, U> op{};
@@ -1474,8 +1495,13 @@ int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* 
         }
         return compute_gather_last(dtype, ident, dst_idx, grad_out, emb, grad_rel, s);
     }
-    return compute_logsumexp_backward(dtype, ident, dst_idx, grad_out, out, rel_flat, emb, grad_rel,
-                                      nullptr, 0, s);
+    // the destinations as the forward's plan keeps them (int32 snapshot, when
+    // it keeps one): half the index bytes of dst_idx
+    const relm_mp_plan* snap = plan.snap_keys != nullptr ? &plan : nullptr;
+    if (rel_rows == 0 || emb == 0) return RELM_MP_OK;
+    return dtype == RELM_MP_F64
+               ? lse_backward_t<double>(ident, dst_idx, grad_out, out, rel_flat, emb, grad_rel, nullptr, s, snap)
+               : lse_backward_t<float>(ident, dst_idx, grad_out, out, rel_flat, emb, grad_rel, nullptr, s, snap);
 }
 
 }  // namespace relm_mp
