@@ -805,11 +805,25 @@ __device__ __forceinline__ const int32_t* inverse_map(const int32_t* inv,
     return pc != nullptr && pc->identity != 0 ? nullptr : inv;
 }
 
-template <typename T, int V, int G, class Rows>
+// The gathered index of edge e: the caller's int64 array, or a plan's int32
+// snapshot of it (tiles flagged plain hold the edge ids and are not stored) -
+// half the index bytes.
+struct GathersI64 {
+    const int64_t* __restrict__ p;
+    __device__ __forceinline__ int64_t operator()(int64_t e) const { return p[e]; }
+};
+struct GathersSnap {
+    const int32_t* __restrict__ p;
+    const uint32_t* __restrict__ plain;
+    __device__ __forceinline__ int64_t operator()(int64_t e) const {
+        return plain != nullptr && plain[e / RELM_MP_SNAP_TILE] != 0u ? e : static_cast<int64_t>(p[e]);
+    }
+};
+
+template <typename T, int V, int G, class Rows, class Src>
 __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restrict__ inv_in,
                                                          const relm_mp_plan_counts* __restrict__ pc,
-                                                         int64_t num_edges,
-                                                         const int64_t* __restrict__ gathers,
+                                                         int64_t num_edges, Src gathers,
                                                          int64_t num_gather,
                                                          const T* __restrict__ table,
                                                          int64_t num_keys, int64_t D,
@@ -829,7 +843,7 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
         for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * R, num_keys, num_edges);
         int64_t g[RU];
 #pragma unroll
-        for (int j = 0; j < RU; ++j) g[j] = e[j] >= 0 ? gathers[e[j]] : -1;
+        for (int j = 0; j < RU; ++j) g[j] = e[j] >= 0 ? gathers(e[j]) : -1;
         Pack<T, V> v[RU];
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
@@ -921,21 +935,6 @@ __global__ __launch_bounds__(kThreads) void k_gather_last_csr(const int32_t* __r
         pack_store_stream<T, V>(out + out_rows(key, D) + col, v);
     }
 }
-
-// The gathered index of edge e: the caller's int64 array, or a plan's int32
-// snapshot of it (tiles flagged plain hold the edge ids and are not stored) -
-// half the index bytes.
-struct GathersI64 {
-    const int64_t* __restrict__ p;
-    __device__ __forceinline__ int64_t operator()(int64_t e) const { return p[e]; }
-};
-struct GathersSnap {
-    const int32_t* __restrict__ p;
-    const uint32_t* __restrict__ plain;
-    __device__ __forceinline__ int64_t operator()(int64_t e) const {
-        return plain != nullptr && plain[e / RELM_MP_SNAP_TILE] != 0u ? e : static_cast<int64_t>(p[e]);
-    }
-};
 
 // Logsumexp backward with an inverse plan (injective keys):
 // grad_rel[r] = grad_out[d] * exp(rel[r] - out[d]), d = gathers(inv[r]), or 0.
@@ -1169,7 +1168,8 @@ int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, 
 // group > 0: the output rows are grouped (GroupedRows{group, group_stride}).
 template <typename T>
 int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* table_v,
-                  int64_t emb, void* out_v, int64_t group, int64_t group_stride, hipStream_t s) {
+                  int64_t emb, void* out_v, int64_t group, int64_t group_stride, hipStream_t s,
+                  const relm_mp_plan* snap = nullptr) {
     const T* table = static_cast<const T*>(table_v);
     T* out = static_cast<T*>(out_v);
     auto launch = [&](auto vt, auto gt, const Geometry& geo, auto rows) -> int {
@@ -1177,10 +1177,17 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
         constexpr int G = decltype(gt)::value;
         using Rows = decltype(rows);
         if (plan.kind == RELM_MP_PLAN_INVERSE) {
-            hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows>),
-                               row_grid(plan.num_keys, G, geo.slices, gather_rows_in_flight<T, V>()),
-                               dim3(kThreads), 0, s, plan.inv, plan.counts, plan.num_edges,
-                               gathers, plan.num_gather, table, plan.num_keys, emb, out, rows);
+            const dim3 grid = row_grid(plan.num_keys, G, geo.slices, gather_rows_in_flight<T, V>());
+            if (snap != nullptr) {
+                hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows, GathersSnap>), grid, dim3(kThreads), 0, s,
+                                   plan.inv, plan.counts, plan.num_edges,
+                                   GathersSnap{snap->snap_keys, snap->snap_key_plain}, plan.num_gather,
+                                   table, plan.num_keys, emb, out, rows);
+            } else {
+                hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows, GathersI64>), grid, dim3(kThreads), 0, s,
+                                   plan.inv, plan.counts, plan.num_edges, GathersI64{gathers},
+                                   plan.num_gather, table, plan.num_keys, emb, out, rows);
+            }
         } else {
             hipLaunchKernelGGL((k_gather_last_csr<T, V, G, Rows>),
                                row_grid(plan.num_keys, G, geo.slices), dim3(kThreads), 0, s,
@@ -1473,6 +1480,10 @@ int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* 
     ident.num_keys = rel_rows;
     ident.num_edges = plan.num_edges;
     ident.num_gather = plan.num_keys;
+    // the destinations as the forward's plan keeps them (int32 snapshot, when
+    // it keeps one): half the index bytes of dst_idx
+    const relm_mp_plan* snap = plan.snap_keys != nullptr ? &plan : nullptr;
+    if (rel_rows == 0 || emb == 0) return RELM_MP_OK;
     if (mode == RELM_MP_MODE_SUM) {
         // The sum backward writes every message row and reads only the
         // destination rows and dst_idx.  HBM sustains a pure write stream far
@@ -1481,24 +1492,23 @@ int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* 
         // fit the memory-side cache they are read into it first.
         const size_t elem = dtype == RELM_MP_F64 ? 8 : 4;
         const size_t tb = static_cast<size_t>(plan.num_keys) * static_cast<size_t>(emb) * elem;
-        const size_t ib = static_cast<size_t>(plan.num_edges) * sizeof(int64_t);
+        const void* idx = snap != nullptr ? static_cast<const void*>(plan.snap_keys) : dst_idx;
+        const size_t ib = static_cast<size_t>(plan.num_edges) * (snap != nullptr ? sizeof(int32_t) : sizeof(int64_t));
         if (tb + ib <= kPrefetchMaxBytes && tb % 16 == 0 && ib % 16 == 0 &&
-            (reinterpret_cast<uintptr_t>(grad_out) | reinterpret_cast<uintptr_t>(dst_idx)) % 16 == 0) {
+            (reinterpret_cast<uintptr_t>(grad_out) | reinterpret_cast<uintptr_t>(idx)) % 16 == 0) {
             const int64_t units = static_cast<int64_t>((tb + ib) / 16);
             const int64_t blocks = std::min<int64_t>((units + kThreads * 8 - 1) / (kThreads * 8), 4096);
             hipLaunchKernelGGL(k_touch, dim3(static_cast<unsigned>(std::max<int64_t>(blocks, 1))),
                                dim3(kThreads), 0, s, static_cast<const uint4*>(grad_out),
-                               static_cast<int64_t>(tb / 16),
-                               reinterpret_cast<const uint4*>(dst_idx), static_cast<int64_t>(ib / 16));
+                               static_cast<int64_t>(tb / 16), static_cast<const uint4*>(idx),
+                               static_cast<int64_t>(ib / 16));
             const int rc = hip_error(hipGetLastError(), "relm_mp prefetch kernel");
             if (rc != RELM_MP_OK) return rc;
         }
-        return compute_gather_last(dtype, ident, dst_idx, grad_out, emb, grad_rel, s);
+        return dtype == RELM_MP_F64
+                   ? gather_last_t<double>(ident, dst_idx, grad_out, emb, grad_rel, 0, 0, s, snap)
+                   : gather_last_t<float>(ident, dst_idx, grad_out, emb, grad_rel, 0, 0, s, snap);
     }
-    // the destinations as the forward's plan keeps them (int32 snapshot, when
-    // it keeps one): half the index bytes of dst_idx
-    const relm_mp_plan* snap = plan.snap_keys != nullptr ? &plan : nullptr;
-    if (rel_rows == 0 || emb == 0) return RELM_MP_OK;
     return dtype == RELM_MP_F64
                ? lse_backward_t<double>(ident, dst_idx, grad_out, out, rel_flat, emb, grad_rel, nullptr, s, snap)
                : lse_backward_t<float>(ident, dst_idx, grad_out, out, rel_flat, emb, grad_rel, nullptr, s, snap);
