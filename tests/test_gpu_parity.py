@@ -530,6 +530,35 @@ def test_backward_by_dst_over_the_forward_plan(emb: int) -> None:
         capi.plan_fanin_backward_by_dst(bp2, _t(dst), 0, _t(g), rel_rows)
 
 
+def test_backward_by_dst_with_plain_snapshot_tiles() -> None:
+    """The backward over the forward's CSR plan reads the destinations from the
+    plan's int32 snapshot, where tiles of 4096 edges whose destinations are the
+    edge ids are flagged instead of stored: destinations equal to the edge ids
+    except in one tile and the partial last one give the same results as the
+    int64 lane and the oracle."""
+
+    from relmo_amd import capi
+
+    rng = np.random.default_rng(77)
+    n, num_keys, emb = 50_000, 60_000, 32
+    dst = np.arange(n)
+    dst[3 * 4096:4 * 4096] = rng.integers(0, num_keys, 4096)
+    dst[-100:] = rng.integers(0, num_keys, 100)
+    flat_src = np.arange(n)
+    rel = (2.0 * rng.standard_normal((n, emb))).astype(np.float32)
+    g = rng.standard_normal((num_keys, emb)).astype(np.float32)
+    bp = capi.csr_plan(_t(dst), num_keys, _t(flat_src), n, "dst_idx", "flat_src", True)
+    assert bp.plan.gather_identity == 1
+    got = _np(capi.plan_fanin_backward_by_dst(bp, _t(dst), 0, _t(g), n))
+    assert np.array_equal(got, oracle.fanin_reduce_sum_backward(g, flat_src, dst, n))
+    out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, num_keys)
+    got = _np(capi.plan_fanin_backward_by_dst(bp, _t(dst), 1, _t(g), n, _t(out), _t(rel)))
+    ident = capi.identity_inv_plan(n, n, num_keys)
+    assert np.array_equal(got, _np(capi.plan_logsumexp_backward(ident, _t(g), _t(out), _t(rel), _t(dst))))
+    np.testing.assert_allclose(got, oracle.fanin_reduce_logsumexp_backward(g, rel, flat_src, dst, out, n),
+                               rtol=1e-4, atol=1e-6)
+
+
 def test_facade_backward_reuses_forward_plan(mp_env) -> None:
     """Autograd through the facade with flat_src = arange: the backward finds the
     forward's plan in the cache; results equal those computed without it."""
