@@ -60,9 +60,10 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // ---- plan kernels (plan_kernels.hip) -------------------------------------
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
-// Resets the status; also zeroes `nclear` words at `clear` (sort_zero_region).
+// Resets the status; also zeroes `nclear` words at `clear` (sort_zero_region)
+// and `nclear2` words at `clear2` (key_index_zero_region).
 hipError_t launch_status_init(DevStatus* st, hipStream_t s, uint32_t* clear = nullptr,
-                              int64_t nclear = 0);
+                              int64_t nclear = 0, uint32_t* clear2 = nullptr, int64_t nclear2 = 0);
 // Copies *st to pinned host memory through its device mapping, then stores
 // `gen` to *host_gen (also mapped host memory) with a system-scope release,
 // for the host to poll; with `pc`, also stores the inverse-plan statistics
@@ -126,6 +127,9 @@ hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, in
 // item_first and item_short have item_capacity + 1 entries
 // (item_capacity_for(num_keys)).
 size_t key_index_words(int64_t num_keys);
+// The words of the key-index scratch that must be zero when launch_key_index
+// starts (chunk sums added with atomics).
+SortZero key_index_zero_region(uint32_t* scratch, int64_t num_keys);
 int64_t item_capacity_for(int64_t num_keys);
 hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted, int64_t num_keys,
                             uint32_t* scratch, int32_t* hub_key, int32_t* hub_chunk_base,

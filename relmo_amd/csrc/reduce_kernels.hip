@@ -167,6 +167,7 @@ struct SumOp {
     int64_t D;
     int64_t col;
     bool colok;
+    int64_t lcol;  // column the lane loads: col, or 0 past the row (value unused)
     Pack<T, V> x[U];
     Pack<T, V> acc;
     Rows rows;  // layout of the table rows
@@ -180,20 +181,25 @@ struct SumOp {
 #pragma unroll
         for (int i = 0; i < V; ++i) acc.v[i] = head ? T(0) : acc.v[i];
     }
-    // Callers repeat the last valid index past `cnt`, so every lane loads a
-    // real row and no load needs a per-slot branch; rows past `cnt` are
-    // never accumulated.
+    // Callers pass valid rows past `cnt` (the last valid index repeated, or
+    // the next messages), and lanes past the row read its first columns, so
+    // every load is unconditional: the compiler keeps all U in flight and
+    // waits for each only where it is consumed.  Rows past `cnt` are never
+    // accumulated, lanes past the row never stored.
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            x[u] = colok ? pack_load<T, V>(table + rows(idx[u], D) + col) : pack_fill<T, V>(T(0));
+        for (int u = 0; u < U; ++u) x[u] = pack_load<T, V>(table + rows(idx[u], D) + lcol);
     }
+    // Rows u >= cnt (or !valid) leave the accumulator as it is: selects, not
+    // branches, so the loads stay unconditional.
     __device__ __forceinline__ void consume(int cnt) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (u < cnt) pack_add(acc, x[u]);
+        for (int u = 0; u < U; ++u) add(u, u < cnt);
     }
-    __device__ __forceinline__ void add(int u) { pack_add(acc, x[u]); }
+    __device__ __forceinline__ void add(int u, bool valid) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc.v[i] = valid ? acc.v[i] + x[u].v[i] : acc.v[i];
+    }
     __device__ __forceinline__ Pack<T, V> result(bool) const { return acc; }
     __device__ __forceinline__ Pack<T, V> empty() const { return pack_fill<T, V>(T(0)); }
     __device__ __forceinline__ Partial partial() const { return {acc}; }
@@ -213,6 +219,7 @@ struct LseOp {
     int64_t D;
     int64_t col;
     bool colok;
+    int64_t lcol;  // as SumOp::lcol
     Pack<T, V> x[U];
     Pack<T, V> m, s;
 
@@ -236,48 +243,49 @@ struct LseOp {
             s.v[i] = head ? T(0) : s.v[i];
         }
     }
-    // as SumOp::load: indices past `cnt` repeat the last valid one
+    // as SumOp::load
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            x[u] = colok ? pack_load<T, V>(table + row_offset(idx[u], D) + col)
-                         : pack_fill<T, V>(neg_inf<T>());
+        for (int u = 0; u < U; ++u) x[u] = pack_load<T, V>(table + row_offset(idx[u], D) + lcol);
     }
+    // Batch maximum, then the rescaled sum; rows u >= cnt are masked by
+    // selects (no branch, so the loads stay unconditional).  While the maximum
+    // is -inf (messages -inf or NaN only) m stays -inf and a NaN message
+    // makes s NaN.
     __device__ __forceinline__ void consume(int cnt) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             T mb = neg_inf<T>();
 #pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (u < cnt) mb = max_num(mb, x[u].v[i]);
+            for (int u = 0; u < U; ++u) mb = u < cnt ? max_num(mb, x[u].v[i]) : mb;
             const T nm = max_num(m.v[i], mb);
-            if (nm != neg_inf<T>()) {
-                T acc = s.v[i] * fast_exp<T>(m.v[i] - nm);
+            T acc = s.v[i] * fast_exp<T>(m.v[i] - nm);
+            T snan = s.v[i];
 #pragma unroll
-                for (int u = 0; u < U; ++u)
-                    if (u < cnt) acc = acc + fast_exp<T>(x[u].v[i] - nm);
-                s.v[i] = acc;
-                m.v[i] = nm;
-            } else {
-#pragma unroll
-                for (int u = 0; u < U; ++u)
-                    if (u < cnt && x[u].v[i] != x[u].v[i]) s.v[i] = quiet_nan<T>();
+            for (int u = 0; u < U; ++u) {
+                acc = u < cnt ? acc + fast_exp<T>(x[u].v[i] - nm) : acc;
+                snan = (u < cnt && x[u].v[i] != x[u].v[i]) ? quiet_nan<T>() : snan;
             }
+            const bool fin = nm != neg_inf<T>();
+            s.v[i] = fin ? acc : snan;
+            m.v[i] = fin ? nm : m.v[i];
         }
     }
     // One message at a time (segments whose batches mix keys): the running
-    // maximum only moves up, so each message costs one exp.
-    __device__ __forceinline__ void add(int u) {
+    // maximum only moves up, so each message costs one exp.  An invalid row
+    // (past the batch) changes nothing.
+    __device__ __forceinline__ void add(int u, bool valid) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             // exp(-|x - m|) is exp(m - x) when x raises the maximum, exp(x - m)
             // otherwise; m is finite or +inf, so a -inf message adds exp(-inf)
             // = 0 and a NaN message makes s NaN
             const T xv = x[u].v[i];
-            const bool up = xv > m.v[i];
+            const bool up = valid && xv > m.v[i];
             const T d = xv - m.v[i];
             const T e = fast_exp<T>(-fabs(d));
-            s.v[i] = up ? fma(s.v[i], e, T(1)) : s.v[i] + e;
+            const T sn = up ? fma(s.v[i], e, T(1)) : s.v[i] + e;
+            s.v[i] = valid ? sn : s.v[i];
             m.v[i] = up ? xv : m.v[i];
         }
     }
@@ -312,44 +320,37 @@ struct LseBwdOp {
     int64_t D;
     int64_t col;
     bool colok;
+    int64_t lcol;  // as SumOp::lcol
     Pack<T, V> g[U], o[U];
     Pack<T, V> xr, acc;
 
-    __device__ __forceinline__ void begin(int64_t key, bool nonempty) {
+    // key is a valid rel row (hub chunks outside the plan pass row 0)
+    __device__ __forceinline__ void begin(int64_t key, bool) {
         acc = pack_fill<T, V>(T(0));
-        xr = (colok && nonempty) ? pack_load<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
+        xr = pack_load<T, V>(rel + key * D + lcol);
     }
     __device__ __forceinline__ void restart(bool head, int64_t key) {
         if (head) begin(key, true);
     }
-    // as SumOp::load: indices past `cnt` repeat the last valid one
+    // as SumOp::load
     __device__ __forceinline__ void load(const int32_t (&idx)[U], int) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint64_t off = row_offset(idx[u], D) + col;
-            g[u] = colok ? pack_load<T, V>(grad_out + off) : pack_fill<T, V>(T(0));
-            o[u] = colok ? pack_load<T, V>(out + off) : pack_fill<T, V>(T(0));
+            const uint64_t off = row_offset(idx[u], D) + lcol;
+            g[u] = pack_load<T, V>(grad_out + off);
+            o[u] = pack_load<T, V>(out + off);
         }
     }
     __device__ __forceinline__ void consume(int cnt) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (u < cnt) {
-#pragma unroll
-                for (int i = 0; i < V; ++i) {
-                    const T w = fast_exp<T>(xr.v[i] - o[u].v[i]);
-                    const T c = g[u].v[i] * w;
-                    acc.v[i] = acc.v[i] + c;
-                }
-            }
-        }
+        for (int u = 0; u < U; ++u) add(u, u < cnt);
     }
-    __device__ __forceinline__ void add(int u) {
+    __device__ __forceinline__ void add(int u, bool valid) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             const T w = fast_exp<T>(xr.v[i] - o[u].v[i]);
             const T c = g[u].v[i] * w;
-            acc.v[i] = acc.v[i] + c;
+            acc.v[i] = valid ? acc.v[i] + c : acc.v[i];
         }
     }
     __device__ __forceinline__ Pack<T, V> result(bool) const { return acc; }
@@ -460,6 +461,7 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
     const int grp = static_cast<int>(threadIdx.x) / G;
     op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     op.colok = op.col < op.D;
+    op.lcol = op.colok ? op.col : 0;
     const int64_t D = op.D;
     const int64_t num_items = pc->num_items;
     const int64_t num_short = pc->num_short;
@@ -586,20 +588,25 @@ __global__ __launch_bounds__(kThreads) void k_walk_items(
             }
             lab[U] = s_key[q + U];
             op.load(idx, cnt);
+            // Rows past cnt are masked in the arithmetic (no branch around
+            // it, so the compiler keeps the loads unconditional and waits
+            // for each row only where it is consumed); only a segment's
+            // store is under a branch.
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                if (u < cnt) {
-                    const int64_t key = bk0 + lab[u];
-                    if constexpr (!Op::kResetAtEnd) op.restart(lab[u] != prev, key);
-                    op.add(u);
-                    if (lab[u + 1] != lab[u]) {
-                        if (op.colok)
-                            pack_store_stream<T, V>(out + row_offset(key, D) + op.col,
-                                                    epi(key, op.result(true), D, op.col));
-                        if constexpr (Op::kResetAtEnd) op.reset();
-                    }
-                    prev = lab[u];
+                const bool valid = u < cnt;
+                const int64_t key = bk0 + lab[u];
+                if constexpr (!Op::kResetAtEnd) {
+                    if (valid) op.restart(lab[u] != prev, key);
                 }
+                op.add(u, valid);
+                if (valid && lab[u + 1] != lab[u]) {
+                    if (op.colok)
+                        pack_store_stream<T, V>(out + row_offset(key, D) + op.col,
+                                                epi(key, op.result(true), D, op.col));
+                    if constexpr (Op::kResetAtEnd) op.reset();
+                }
+                prev = valid ? lab[u] : prev;
             }
         }
     }
@@ -656,6 +663,7 @@ __global__ __launch_bounds__(kThreads) void k_hub_chunks(
     const int grp = static_cast<int>(threadIdx.x) / G;
     op.col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     op.colok = op.col < op.D;
+    op.lcol = op.colok ? op.col : 0;
     const int64_t D = op.D;
     const int64_t num_hubs = pc->num_hubs;
     const int64_t num_chunks = pc->num_chunks;
@@ -782,15 +790,6 @@ __global__ __launch_bounds__(kThreads) void k_hub_combine(
     }
 }
 
-// Edge of key k under an inverse plan: inv[k], or k itself (k < num_edges)
-// when the plan is the identity (inv == nullptr).
-__device__ __forceinline__ int32_t inverse_edge(const int32_t* __restrict__ inv, int64_t key,
-                                                int64_t num_keys, int64_t num_edges) {
-    if (key >= num_keys) return -1;
-    if (inv != nullptr) return inv[key];
-    return key < num_edges ? static_cast<int32_t>(key) : -1;
-}
-
 // out[r] = table[gathers[inv[r]]] or 0 (inverse plans: fanout forward and
 // injective sum backward).  Each row group keeps gather_rows_in_flight<T, V>() rows
 // in flight.
@@ -805,20 +804,88 @@ __device__ __forceinline__ const int32_t* inverse_map(const int32_t* inv,
     return pc != nullptr && pc->identity != 0 ? nullptr : inv;
 }
 
-// The gathered index of edge e: the caller's int64 array, or a plan's int32
-// snapshot of it (tiles flagged plain hold the edge ids and are not stored) -
-// half the index bytes.
+// The gathered index of edge e (0 <= e < num_edges): the caller's int64
+// array, or a plan's int32 snapshot of it (tiles flagged plain hold the edge
+// ids and are not stored) - half the index bytes.  fetch() issues the loads,
+// value() combines them, so the loads of several edges are in flight at once:
+// the snapshot word is read whether or not the tile is plain (it is
+// allocated for every edge), and a snapshot without plain flags reads a zero
+// word instead of a flag.
+__device__ uint32_t g_plain_none = 0u;
+
 struct GathersI64 {
     const int64_t* __restrict__ p;
-    __device__ __forceinline__ int64_t operator()(int64_t e) const { return p[e]; }
+    struct Raw {
+        int64_t v;
+    };
+    __device__ __forceinline__ Raw fetch(int64_t e) const { return {p[e]}; }
+    __device__ __forceinline__ int64_t value(int64_t, const Raw& r) const { return r.v; }
 };
 struct GathersSnap {
     const int32_t* __restrict__ p;
     const uint32_t* __restrict__ plain;
-    __device__ __forceinline__ int64_t operator()(int64_t e) const {
-        return plain != nullptr && plain[e / RELM_MP_SNAP_TILE] != 0u ? e : static_cast<int64_t>(p[e]);
+    struct Raw {
+        int32_t v;
+        uint32_t flag;
+    };
+    __device__ __forceinline__ Raw fetch(int64_t e) const {
+        const bool has = plain != nullptr;
+        const uint32_t* f = has ? plain + e / RELM_MP_SNAP_TILE : &g_plain_none;
+        return {p[e], *f};
+    }
+    __device__ __forceinline__ int64_t value(int64_t e, const Raw& r) const {
+        return r.flag != 0u ? e : static_cast<int64_t>(r.v);
     }
 };
+
+// Row kernels over inverse plans issue every load of an iteration without a
+// branch: a row past num_keys, an edge without a key and an invalid gathered
+// index read row 0 / edge 0 instead (the kernels run only with at least one
+// edge and one gathered row) and their values are discarded.  With the loads
+// under branches the compiler waits for each index before the next.
+struct InvRow {
+    int64_t key;   // the row, or 0 past num_keys
+    bool live;     // key < num_keys
+    int64_t g;     // gathered row, or 0
+    bool ok;       // the row has an edge whose gathered index is in [0, num_gather)
+};
+
+template <int RU, class Src>
+__device__ __forceinline__ void inverse_rows(InvRow (&r)[RU], int64_t key0, int64_t stride,
+                                             const int32_t* __restrict__ inv, int64_t num_keys,
+                                             int64_t num_edges, const Src& gathers,
+                                             int64_t num_gather) {
+    int64_t e[RU];
+#pragma unroll
+    for (int j = 0; j < RU; ++j) {
+        const int64_t key = key0 + j * stride;
+        r[j].live = key < num_keys;
+        r[j].key = r[j].live ? key : 0;
+    }
+    if (inv != nullptr) {
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            const int32_t iv = inv[r[j].key];
+            e[j] = r[j].live ? static_cast<int64_t>(iv) : -1;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < RU; ++j) e[j] = r[j].live && r[j].key < num_edges ? r[j].key : -1;
+    }
+    typename Src::Raw raw[RU];
+#pragma unroll
+    for (int j = 0; j < RU; ++j) {
+        const bool has = e[j] >= 0 && e[j] < num_edges;
+        e[j] = has ? e[j] : -1;
+        raw[j] = gathers.fetch(has ? e[j] : 0);
+    }
+#pragma unroll
+    for (int j = 0; j < RU; ++j) {
+        const int64_t d = gathers.value(e[j] >= 0 ? e[j] : 0, raw[j]);
+        r[j].ok = e[j] >= 0 && static_cast<uint64_t>(d) < static_cast<uint64_t>(num_gather);
+        r[j].g = r[j].ok ? d : 0;
+    }
+}
 
 template <typename T, int V, int G, class Rows, class Src>
 __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restrict__ inv_in,
@@ -838,23 +905,22 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
     const int64_t grp = threadIdx.x / G;
     for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * chunk + grp; key0 < num_keys;
          key0 += static_cast<int64_t>(gridDim.x) * chunk) {
-        int32_t e[RU];
+        if (num_edges <= 0 || num_gather <= 0) {  // uniform: no row to gather
 #pragma unroll
-        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * R, num_keys, num_edges);
-        int64_t g[RU];
-#pragma unroll
-        for (int j = 0; j < RU; ++j) g[j] = e[j] >= 0 ? gathers(e[j]) : -1;
+            for (int j = 0; j < RU; ++j)
+                if (key0 + j * R < num_keys)
+                    pack_store_stream<T, V>(out + out_rows(key0 + j * R, D) + col, pack_fill<T, V>(T(0)));
+            continue;
+        }
+        InvRow r[RU];
+        inverse_rows<RU>(r, key0, R, inv, num_keys, num_edges, gathers, num_gather);
         Pack<T, V> v[RU];
 #pragma unroll
-        for (int j = 0; j < RU; ++j) {
-            v[j] = pack_fill<T, V>(T(0));
-            if (static_cast<uint64_t>(g[j]) < static_cast<uint64_t>(num_gather))
-                v[j] = pack_load<T, V>(table + row_offset(g[j], D) + col);
-        }
+        for (int j = 0; j < RU; ++j) v[j] = pack_load<T, V>(table + row_offset(r[j].g, D) + col);
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
-            const int64_t key = key0 + j * R;
-            if (key < num_keys) pack_store_stream<T, V>(out + out_rows(key, D) + col, v[j]);
+            if (!r[j].ok) v[j] = pack_fill<T, V>(T(0));
+            if (r[j].live) pack_store_stream<T, V>(out + out_rows(r[j].key, D) + col, v[j]);
         }
     }
 }
@@ -955,36 +1021,32 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
     const int64_t grp = threadIdx.x / G;
     for (int64_t key0 = static_cast<int64_t>(blockIdx.x) * chunk + grp; key0 < num_keys;
          key0 += static_cast<int64_t>(gridDim.x) * chunk) {
-        int32_t e[RU];
+        if (num_edges <= 0 || num_gather <= 0) {  // uniform: no row to gather
 #pragma unroll
-        for (int j = 0; j < RU; ++j) e[j] = inverse_edge(inv, key0 + j * R, num_keys, num_edges);
-        int64_t d[RU];
-#pragma unroll
-        for (int j = 0; j < RU; ++j) d[j] = e[j] >= 0 ? gathers(e[j]) : -1;
+            for (int j = 0; j < RU; ++j)
+                if (key0 + j * R < num_keys)
+                    pack_store_stream<T, V>(grad_rel + (key0 + j * R) * D + col, pack_fill<T, V>(T(0)));
+            continue;
+        }
+        InvRow r[RU];
+        inverse_rows<RU>(r, key0, R, inv, num_keys, num_edges, gathers, num_gather);
         Pack<T, V> x[RU], g[RU], o[RU];
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
-            const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
-            const int64_t key = key0 + j * R;
-            x[j] = ok ? pack_load_stream<T, V>(rel + key * D + col) : pack_fill<T, V>(T(0));
-            g[j] = ok ? pack_load<T, V>(grad_out + row_offset(d[j], D) + col) : pack_fill<T, V>(T(0));
-            o[j] = ok ? pack_load<T, V>(out + row_offset(d[j], D) + col) : pack_fill<T, V>(T(0));
+            x[j] = pack_load_stream<T, V>(rel + r[j].key * D + col);
+            g[j] = pack_load<T, V>(grad_out + row_offset(r[j].g, D) + col);
+            o[j] = pack_load<T, V>(out + row_offset(r[j].g, D) + col);
         }
 #pragma unroll
         for (int j = 0; j < RU; ++j) {
-            const int64_t key = key0 + j * R;
-            if (key >= num_keys) continue;
-            const bool ok = static_cast<uint64_t>(d[j]) < static_cast<uint64_t>(num_gather);
-            Pack<T, V> r = pack_fill<T, V>(T(0));
-            if (ok) {
+            Pack<T, V> res;
 #pragma unroll
-                for (int i = 0; i < V; ++i) {
-                    const T w = fast_exp<T>(x[j].v[i] - o[j].v[i]);
-                    const T c = g[j].v[i] * w;
-                    r.v[i] = T(0) + c;
-                }
+            for (int i = 0; i < V; ++i) {
+                const T w = fast_exp<T>(x[j].v[i] - o[j].v[i]);
+                const T c = g[j].v[i] * w;
+                res.v[i] = r[j].ok ? T(0) + c : T(0);
             }
-            pack_store_stream<T, V>(grad_rel + key * D + col, r);
+            if (r[j].live) pack_store_stream<T, V>(grad_rel + r[j].key * D + col, res);
         }
     }
 }
