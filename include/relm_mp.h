@@ -445,13 +445,14 @@ int64_t relm_mp_film_mish_blocks(const int64_t* range_start, int32_t num_ranges)
 
 /* Backward of relm_mp_film_mish given dy [rows, width]: ds = du * gamma[k] with
  * du = dy * mish'(u), u = beta[k] + gamma[k] * (s + add[k]); partial [blocks, 2,
- * width] receives per block (the blocks of range k are consecutive, in row order)
- * the column sums of du * (s + add[k]) and of du over its rows: summed over range
- * k's blocks they are the gradients of gamma[k] and of beta[k] (that of add[k] is
- * gamma[k] times the latter).  partial_blocks >= relm_mp_film_mish_blocks(...). */
+ * width] (float64) receives per block (the blocks of range k are consecutive, in
+ * row order) the column sums of du * (s + add[k]) and of du over its rows, each
+ * fp32 term added in fp64: summed over range k's blocks they are the gradients of
+ * gamma[k] and of beta[k] (that of add[k] is gamma[k] times the latter).
+ * partial_blocks >= relm_mp_film_mish_blocks(...). */
 int relm_mp_film_mish_backward(const float* s, const float* dy, int64_t rows, int64_t width,
                                const int64_t* range_start, int32_t num_ranges, const float* gamma,
-                               const float* beta, const float* add, float* ds, float* partial,
+                               const float* beta, const float* add, float* ds, double* partial,
                                int64_t partial_blocks, relm_mp_stream_t stream);
 
 #ifdef __cplusplus

@@ -642,12 +642,12 @@ def film_mish(s: torch.Tensor, range_start: list[int], gamma: torch.Tensor, beta
 
 def film_mish_backward(dy: torch.Tensor, s: torch.Tensor, range_start: list[int], gamma: torch.Tensor,
                        beta: torch.Tensor, add: torch.Tensor | None = None):
-    """``relm_mp_film_mish_backward``: (ds, per-block partial sums [blocks, 2, width])."""
+    """``relm_mp_film_mish_backward``: (ds, per-block partial sums [blocks, 2, width], float64)."""
 
     starts, k = _starts(range_start)
     blocks = lib().relm_mp_film_mish_blocks(starts, k)
     ds = torch.empty_like(s)
-    partial = torch.empty(max(blocks, 1), 2, s.size(1), dtype=s.dtype, device=s.device)
+    partial = torch.empty(max(blocks, 1), 2, s.size(1), dtype=torch.float64, device=s.device)
     check(lib().relm_mp_film_mish_backward(_ptr(s), _ptr(dy), s.size(0), s.size(1), starts, k,
                                            _ptr(gamma), _ptr(beta), _ptr(add) if add is not None else None,
                                            _ptr(ds), _ptr(partial), blocks, _stream(s)))

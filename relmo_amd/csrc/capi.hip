@@ -700,7 +700,7 @@ int relm_mp_film_mish(const float* s, int64_t rows, int64_t width, const int64_t
 
 int relm_mp_film_mish_backward(const float* s, const float* dy, int64_t rows, int64_t width,
                                const int64_t* range_start, int32_t num_ranges, const float* gamma,
-                               const float* beta, const float* add, float* ds, float* partial,
+                               const float* beta, const float* add, float* ds, double* partial,
                                int64_t partial_blocks, relm_mp_stream_t stream) {
     RELM_TRY(check_rows(rows, "rows"));
     if (width < 0 || width > 0x7fffffff)

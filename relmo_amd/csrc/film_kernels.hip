@@ -7,7 +7,8 @@
 // One pass over s replaces torch's add, addcmul, Mish and the concatenation of
 // the per-range results; the backward reads s and the upstream gradient once,
 // writes ds and leaves per-block column sums of du * (s + add) and du (du the
-// gradient at the Mish input) for the per-range gamma / beta gradients.
+// gradient at the Mish input), in fp64, for the per-range gamma / beta
+// gradients.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -131,21 +132,21 @@ __global__ __launch_bounds__(kMaxThreads) void k_film_mish(const float* __restri
 // ds = dy * mish'(u) * gamma; partial[block][0][col] = sum over the block's
 // rows of du * (s + add), partial[block][1][col] = sum of du, du = dy *
 // mish'(u), each term rounded to fp32 and added in fp64: by each thread over
-// its rows in row order, then the phases in order (the sum of a block is
-// rounded once: a per-range sum over tens of thousands of rows keeps about the
-// accuracy of a tree reduction).  With several phases, `lds` holds
-// phases * units * V * 2 doubles.
+// its rows in row order, then the phases in order.  The block sums stay fp64
+// (the caller adds a range's blocks in fp64 and rounds once), so a per-range
+// sum over tens of thousands of rows carries only the rounding of its terms.
+// With several phases, `lds` holds phases * units * V * 2 doubles.
 template <int V>
 __global__ __launch_bounds__(kMaxThreads) void k_film_mish_backward(
     const float* __restrict__ s, const float* __restrict__ dy, int64_t width, FilmRanges R,
     FilmLayout L, const float* __restrict__ gamma, const float* __restrict__ beta,
-    const float* __restrict__ add, float* __restrict__ ds, float* __restrict__ partial) {
+    const float* __restrict__ add, float* __restrict__ ds, double* __restrict__ partial) {
     extern __shared__ double lds[];
     const BlockRows br = block_rows(R);
     const int t = static_cast<int>(threadIdx.x);
     const int ph = L.phases > 1 ? t / L.units : 0;
     const int step = L.phases;
-    float* __restrict__ part = partial + static_cast<int64_t>(blockIdx.x) * 2 * width;
+    double* __restrict__ part = partial + static_cast<int64_t>(blockIdx.x) * 2 * width;
     const bool active = ph < L.phases;
     for (int64_t c = L.phases > 1 ? t % L.units : t; active && c < L.units;
          c += L.phases > 1 ? L.units : blockDim.x) {
@@ -193,14 +194,11 @@ __global__ __launch_bounds__(kMaxThreads) void k_film_mish_backward(
                 lu[i] = sum_u[i];
             }
         } else {
-            Vec<V> pt, pu;
 #pragma unroll
             for (int i = 0; i < V; ++i) {
-                pt.v[i] = static_cast<float>(sum_t[i]);
-                pu.v[i] = static_cast<float>(sum_u[i]);
+                part[col + i] = sum_t[i];
+                part[width + col + i] = sum_u[i];
             }
-            pack_store<float, V>(part + col, pt);
-            pack_store<float, V>(part + width + col, pu);
         }
     }
     if (L.phases > 1) {
@@ -209,7 +207,6 @@ __global__ __launch_bounds__(kMaxThreads) void k_film_mish_backward(
         if (active && ph == 0) {
             const int c = t;
             const int64_t col = static_cast<int64_t>(c) * V;
-            Vec<V> pt, pu;
 #pragma unroll
             for (int i = 0; i < V; ++i) {
                 double at = 0.0, au = 0.0;
@@ -218,11 +215,9 @@ __global__ __launch_bounds__(kMaxThreads) void k_film_mish_backward(
                     at += lt[i];
                     au += lt[static_cast<int64_t>(L.phases) * L.units * V + i];
                 }
-                pt.v[i] = static_cast<float>(at);
-                pu.v[i] = static_cast<float>(au);
+                part[col + i] = at;
+                part[width + col + i] = au;
             }
-            pack_store<float, V>(part + col, pt);
-            pack_store<float, V>(part + width + col, pu);
         }
     }
 }
@@ -300,7 +295,7 @@ hipError_t launch_film_mish(const float* s, int64_t width, const int64_t* range_
 hipError_t launch_film_mish_backward(const float* s, const float* dy, int64_t width,
                                      const int64_t* range_start, int32_t num_ranges,
                                      const float* gamma, const float* beta, const float* add,
-                                     float* ds, float* partial, hipStream_t st) {
+                                     float* ds, double* partial, hipStream_t st) {
     const FilmRanges R = film_ranges(range_start, num_ranges);
     const int64_t blocks = R.first_block[kMaxRanges];
     if (blocks == 0 || width == 0) return hipSuccess;

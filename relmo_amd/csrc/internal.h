@@ -162,7 +162,7 @@ hipError_t launch_film_mish(const float* s, int64_t width, const int64_t* range_
 hipError_t launch_film_mish_backward(const float* s, const float* dy, int64_t width,
                                      const int64_t* range_start, int32_t num_ranges,
                                      const float* gamma, const float* beta, const float* add,
-                                     float* ds, float* partial, hipStream_t st);
+                                     float* ds, double* partial, hipStream_t st);
 
 // ---- content comparison (match_kernels.hip) -------------------------------
 constexpr int kMaxMatch = RELM_MP_MAX_MATCH;

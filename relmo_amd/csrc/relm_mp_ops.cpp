@@ -1791,17 +1791,18 @@ std::tuple<Tensor, Tensor, Tensor> film_mish_backward(const Tensor& grad, const 
     const int64_t blocks = relm_mp_film_mish_blocks(a.starts.data(), k);
     TORCH_CHECK(blocks >= 0, "film_mish_backward: bad row ranges.");
     Tensor ds = at::empty_like(a.s);
-    Tensor partial = at::empty({std::max<int64_t>(blocks, 1), 2, width}, a.s.options());
+    Tensor partial = at::empty({std::max<int64_t>(blocks, 1), 2, width}, a.s.options().dtype(at::kDouble));
     raise_if(relm_mp_film_mish_backward(fptr(a.s), g.data_ptr<float>(), a.s.size(0), width,
                                         a.starts.data(), k, fptr(a.gamma), fptr(a.beta), fptr(a.add),
-                                        ds.data_ptr<float>(), partial.data_ptr<float>(), blocks,
+                                        ds.data_ptr<float>(), partial.data_ptr<double>(), blocks,
                                         current_stream(a.s)));
-    // per range, the sums of its blocks (consecutive, RELM_MP_FILM_ROWS_PER_BLOCK rows each)
+    // per range, the sums of its blocks (consecutive, RELM_MP_FILM_ROWS_PER_BLOCK
+    // rows each) in fp64, rounded to fp32 once
     if (k == 1 && blocks > 0) {
-        const Tensor sum = partial.sum(0);  // [2, width]
+        const Tensor sum = partial.sum(0).to(at::kFloat);  // [2, width]
         return {ds, sum.narrow(0, 0, 1), sum.narrow(0, 1, 1)};
     }
-    Tensor sums = at::zeros({k, 2, width}, a.s.options());
+    Tensor sums = at::zeros({k, 2, width}, partial.options());
     int64_t b0 = 0;
     for (int32_t r = 0; r < k; ++r) {
         const int64_t rows = a.starts[r + 1] - a.starts[r];
@@ -1809,7 +1810,8 @@ std::tuple<Tensor, Tensor, Tensor> film_mish_backward(const Tensor& grad, const 
         if (nb > 0) sums[r].copy_(partial.narrow(0, b0, nb).sum(0));
         b0 += nb;
     }
-    return {ds, sums.select(1, 0), sums.select(1, 1)};
+    const Tensor sums32 = sums.to(at::kFloat);
+    return {ds, sums32.select(1, 0), sums32.select(1, 1)};
 }
 
 // ---- a @ b^T for the models' narrow Linears (no counterpart in the reference) ----

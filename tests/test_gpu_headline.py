@@ -240,12 +240,13 @@ def _step_grads(C, model, batch, routing, enable: str, monkeypatch):
 def test_model_step_at_config_width(model: str, monkeypatch) -> None:
     """One training step: the HIP lane (fp32) is about as close to a float64
     run of the same step as the ATen lane (fp32) is - per parameter, the
-    relative L2 error of the gradient within 8 times the ATen lane's (the
-    larger of two ATen runs: its float atomics move its error over a factor
-    of ~5 from run to run, the HIP lane's does not move) plus 32 fp32 ulps,
-    and the loss within twice the ATen lane's loss error plus 8 fp32 ulps
+    relative L2 error of the gradient within twice the ATen lane's (the
+    larger of two ATen runs: its float atomics move its error from run to
+    run, the HIP lane's does not move) plus 8 fp32 ulps, and below a fixed
+    1e-4 (C5's sum layers grow activations to ~1e20, where both lanes keep
+    ~1e-5); the loss within twice the ATen lane's loss error plus 8 fp32 ulps
     (relative).  A dropped, doubled or misplaced term gives errors of order
-    one.  Sum and logsumexp; mean for C5.  c5_gathered runs the central
+    one, a biased reduction errors far above the ATen lane's.  Sum and logsumexp; mean for C5.  c5_gathered runs the central
     MLP's first Linear per object and gathered (both fp32 lanes), against the
     float64 run of the module on the assembled input; c5_gathered_recompute
     adds the recomputation of the central activations (on the HIP lane the
@@ -296,12 +297,60 @@ def test_model_step_at_config_width(model: str, monkeypatch) -> None:
                          float((g_aten2[k].double() - ref).norm())) / max(nref, 1e-300)
             if r_hip / max(r_aten, 1e-12) > worst:
                 worst, worst_k = r_hip / max(r_aten, 1e-12), f"{k} ({r_hip:.3g} against {r_aten:.3g})"
-            # a gradient summed over ~1e5 relation nodes in each of ten layers
-            # keeps 1e-6..1e-5 of relative fp32 error however it is ordered
-            assert r_hip <= 8 * r_aten + 32 * EPS32, (mode, k, r_hip, r_aten)
+            assert r_hip <= 2 * r_aten + 8 * EPS32, (mode, k, r_hip, r_aten)
+            assert r_hip <= 1e-4, (mode, k, r_hip)
         _log(f"  gradients: worst ratio of relative L2 errors hip/aten {worst:.3g}: {worst_k}")
         del m, m64, routing, g_hip, g_aten, g_aten2, g64
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("mode,graphs,reference", [
+    (0, 2048, "assembled"), (1, 2048, "same"), (2, 2048, "same"), (1, 1024, "assembled"), (2, 1024, "assembled")])
+def test_c5_large_batch_hip_lane_against_aten_lane(mode: int, graphs: int, reference: str, monkeypatch) -> None:
+    """C5 at the 2048 graphs bench.py times: one training step of the HIP lane
+    as the bench runs it (the central MLP's first Linear per object and
+    gathered, the output Linear on the hidden rows summed per (object, slot)
+    for sum and mean, the central activations recomputed in the backward)
+    against an fp32 ATen lane with the same weights and batch: the module on
+    the assembled input (the reference's structure, checkpointed) where it
+    fits the GPU - sum at 2048 graphs, logsumexp and mean at 1024 - and the
+    same restructured module on ATen ops at 2048.  No float64 run fits at these
+    sizes; the two fp32 lanes differ by their rounding alone (measured: at most
+    1.2e-5 of a gradient's L2 norm and 5e-7 of the loss, the sum layers growing
+    activations to ~1e20), while a dropped, doubled or misplaced term moves a
+    loss or a gradient by order one."""
+
+    import gc
+
+    from relmo_amd import consumers as C
+
+    gc.collect()
+    torch.cuda.empty_cache()
+    batch = C.synthetic_c5(DEV, num_graphs=graphs)
+    torch.manual_seed(0)
+    m = C.CentralizedRelationalGNN(128, 10, batch.relations, mode, recompute_central=True,
+                                   gather_first_linear=True, sum_before_output=True).to(DEV)
+    routing = m.routing(batch)
+    _log(f"c5 mode={mode}: {batch.num_graphs} graphs, {batch.num_objects} objects, against {reference}")
+    loss_hip, g_hip = _step_grads(C, m, batch, routing, "1", monkeypatch)
+    if reference == "assembled":
+        m.gather_first_linear = False
+        m.sum_before_output = False
+    try:
+        loss_ref, g_ref = _step_grads(C, m, batch, routing, "0", monkeypatch)
+    finally:
+        m.zero_grad(set_to_none=True)
+    rel_loss = abs(loss_hip - loss_ref) / abs(loss_ref)
+    worst, worst_k = 0.0, ""
+    for k, ref in g_ref.items():
+        d = float((g_hip[k] - ref).double().norm()) / max(float(ref.double().norm()), 1e-300)
+        if d > worst:
+            worst, worst_k = d, k
+    _log(f"  loss {loss_ref:.8g}: relative difference {rel_loss:.3g}; "
+         f"largest relative L2 gradient difference {worst:.3g} ({worst_k})")
+    assert set(g_hip) == set(g_ref)
+    assert rel_loss <= 1e-5, rel_loss
+    assert worst <= 1e-4, (worst_k, worst)
 
 
 def test_c4_batched_lane_matches_fast_fused(monkeypatch) -> None:

@@ -387,10 +387,17 @@ def _zipf_keys(rng, num_keys: int, n: int, s: float = 1.1) -> np.ndarray:
     return rng.permutation(num_keys)[np.minimum(r, num_keys - 1)]
 
 
-@pytest.mark.parametrize("emb", [32, 6])
+def _chunk_size() -> int:
+    return int(re.search(r"#define RELM_MP_CHUNK_SIZE (\d+)", (REPO / "include" / "relm_mp.h").read_text()).group(1))
+
+
+@pytest.mark.parametrize("emb", [32, 6, 64, 128])
 def test_hub_segments_against_float64_truth(emb: int) -> None:
-    """emb 32 moves 16 bytes per lane, emb 6 (rows of an even number of floats
-    that is not a multiple of 4) 8 bytes."""
+    """Hubs of many chunks (the chunk kernel, then the combine kernel) against
+    float64 truth at every row geometry the hub kernels are built for: emb 32
+    (8 lanes of 16 bytes per row), 64 (16 lanes), 128 (32 lanes), and emb 6
+    (rows of an even number of floats that is not a multiple of 4: 8 bytes per
+    lane)."""
 
     from relmo_amd import capi
 
@@ -400,8 +407,10 @@ def test_hub_segments_against_float64_truth(emb: int) -> None:
     rel = (2.0 * rng.standard_normal((n, emb))).astype(np.float32)
     flat_src = rng.permutation(n)
     deg = np.bincount(dst, minlength=num_keys)
-    assert deg.max() > 10_000
+    chunk = _chunk_size()
+    assert (deg > 3 * chunk).sum() >= 3, "several hubs of more than three chunks"
     short = deg <= 64
+    hub = deg > 64
     got = _np(capi.fanin_reduce(_t(rel), _t(flat_src), _t(dst), num_keys, 0))
     want = oracle.fanin_reduce_sum(rel, flat_src, dst, num_keys)
     truth, absum = oracle.segment_sum_truth(rel, flat_src, dst, num_keys)
@@ -411,8 +420,11 @@ def test_hub_segments_against_float64_truth(emb: int) -> None:
     lse_truth = oracle.fanin_logsumexp_truth(rel, flat_src, dst, num_keys)
     _assert_lse_close(lse, lse_truth.astype(np.float32), "lse vs truth")
     _assert_lse_close(lse, oracle.fanin_reduce_logsumexp(rel, flat_src, dst, num_keys), "lse vs oracle")
+    # hub rows alone, ten times tighter than the op tolerance
+    np.testing.assert_allclose(lse[hub], lse_truth[hub], rtol=1e-5, atol=1e-6, err_msg="lse hubs vs truth")
     # fanout backward with hub rows on the source side
     src = _zipf_keys(rng, 5000, n)
+    assert (np.bincount(src, minlength=5000) > 3 * chunk).sum() >= 3
     g = rng.standard_normal((n, emb)).astype(np.float32)
     slots = np.arange(n)
     got = _np(capi.fanout_scatter_backward(_t(g), _t(src), _t(slots), 5000))
