@@ -111,16 +111,19 @@ int relm_mp_fanin_reduce(int dtype, const void* rel_flat, int64_t rel_rows, int6
 
 /* relm_mp_fanin_reduce without a workspace and without allocating: no
  * counterpart in the reference.  For callers that cannot allocate device or
- * pinned host memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  The plan, sort buffers and hub partials
- * live in a device array of RELM_MP_NOALLOC_SCRATCH_BYTES that the library
- * holds on every device it runs on until the process ends; a call whose
- * relm_mp_fanin_reduce_workspace_size exceeds it fails with
+ * pinned host memory (tight serving loops, harnesses that forbid hipMalloc).
+ * It cannot run under HIP graph capture: it synchronises `stream` once (the
+ * index check), like relm_mp_fanin_reduce.  The plan, sort buffers and hub
+ * partials live in a device array of RELM_MP_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every device it runs on until the process ends; a call
+ * whose relm_mp_fanin_reduce_workspace_size exceeds it fails with
  * RELM_MP_ERR_WORKSPACE before launching anything (64 MiB: about 1.5 million
- * messages at emb 32).  All calls on one device share that array, so calls
- * that overlap on one device (other host threads, other streams) race; the
- * array keeps the last call's contents, and every call writes what it reads.
- * Synchronises `stream` once (the index check), like relm_mp_fanin_reduce. */
+ * messages at emb 32).  All calls on one device share that array, so they are
+ * serialised: host threads one at a time, and on the device each call's
+ * kernels wait for the previous call's (an event per device, recorded behind
+ * every call, which the next call's stream waits on), whatever streams the
+ * calls use.  The array keeps the last call's contents, and every call writes
+ * what it reads. */
 #define RELM_MP_NOALLOC_SCRATCH_BYTES (64LL << 20)
 int relm_mp_fanin_reduce_noalloc(int dtype, const void* rel_flat, int64_t rel_rows, int64_t emb,
                                  const int64_t* flat_src, const int64_t* dst_idx,

@@ -525,6 +525,12 @@ __device__ __align__(256) unsigned char scratch[RELM_MP_NOALLOC_SCRATCH_BYTES];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+// Calls of one device run one at a time (host side), and each call's work on
+// the device waits for the previous call's through an event recorded behind
+// it (events hold no device memory).
+std::mutex g_noalloc_mu[kMaxDevices];
+hipEvent_t g_noalloc_done[kMaxDevices] = {};
+bool g_noalloc_recorded[kMaxDevices] = {};
 
 // The current device's address of `scratch` (looked up on the first call on
 // that device).
@@ -1017,9 +1023,26 @@ int relm_mp_fanin_reduce_noalloc(int dtype, const void* rel_flat, int64_t rel_ro
         }
         RELM_TRY(noalloc_scratch(&ws));
     }
-    return fanin_reduce_run(dtype, rel_flat, rel_rows, emb, flat_src, dst_idx, num_edges, dim_size,
-                            mode, out, ws, static_cast<size_t>(RELM_MP_NOALLOC_SCRATCH_BYTES),
-                            static_cast<hipStream_t>(stream), StatusPath::kStreamCopy);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    RELM_HIP(hipGetDevice(&dev), "relm_mp device query");
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(RELM_MP_ERR_HIP, "relm_mp: device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu[dev]);
+    if (g_noalloc_done[dev] == nullptr)
+        RELM_HIP(hipEventCreateWithFlags(&g_noalloc_done[dev], hipEventDisableTiming),
+                 "relm_mp noalloc event");
+    if (g_noalloc_recorded[dev])
+        RELM_HIP(hipStreamWaitEvent(s, g_noalloc_done[dev], 0), "relm_mp noalloc wait");
+    const int rc = fanin_reduce_run(dtype, rel_flat, rel_rows, emb, flat_src, dst_idx, num_edges,
+                                    dim_size, mode, out, ws,
+                                    static_cast<size_t>(RELM_MP_NOALLOC_SCRATCH_BYTES), s,
+                                    StatusPath::kStreamCopy);
+    // recorded whatever the outcome: kernels of a failed call may still be queued
+    const hipError_t rec = hipEventRecord(g_noalloc_done[dev], s);
+    if (rec == hipSuccess) g_noalloc_recorded[dev] = true;
+    if (rc != RELM_MP_OK) return rc;
+    return hip_error(rec, "relm_mp noalloc event record");
 }
 
 size_t relm_mp_fanin_reduce_sum_backward_workspace_size(int64_t num_edges, int64_t rel_rows,

@@ -1,8 +1,9 @@
 """GPU test of relm_mp_fanin_reduce_noalloc, the entry point that allocates
 nothing: through the C ABI, its results equal relm_mp_fanin_reduce's (the
 workspace entry point, same kernels) bit for bit, on consecutive calls that
-reuse the library's device scratch with a smaller input second, and a call
-beyond the scratch size is refused before anything is launched."""
+reuse the library's device scratch with a smaller input second, on two
+streams back to back, and a call beyond the scratch size is refused before
+anything is launched."""
 
 from __future__ import annotations
 
@@ -62,17 +63,43 @@ def test_noalloc_matches_the_workspace_entry_point() -> None:
         assert torch.equal(got, want), (seed, (got - want).abs().max().item())
 
 
+def test_noalloc_calls_on_two_streams_are_ordered() -> None:
+    """A call on one stream returns with its kernels still queued; the next
+    call, on another stream, builds its plan in the same device scratch.  The
+    library orders the second behind the first (an event per device), so both
+    results equal the workspace entry point's."""
+
+    from relmo_amd import capi
+
+    a = _case(4, 60_000, 1_200_000, 32, torch.float32, 200_000)
+    b = _case(5, 3_000, 50_000, 32, torch.float32, 5_000)
+    want_a = capi.fanin_reduce(*a, 60_000, 1)
+    want_b = capi.fanin_reduce(*b, 3_000, 1)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            got_a = capi.fanin_reduce_noalloc(*a, 60_000, 1)
+        with torch.cuda.stream(s2):
+            got_b = capi.fanin_reduce_noalloc(*b, 3_000, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(got_a, want_a)
+        assert torch.equal(got_b, want_b)
+
+
 def test_noalloc_refuses_calls_beyond_its_scratch() -> None:
     from relmo_amd import capi
 
     E, K, D = 4_000_000, 1_000, 32
     need = capi.lib().relm_mp_fanin_reduce_workspace_size(E, K, D, capi.F32)
     assert need > capi.NOALLOC_SCRATCH_BYTES
-    rel = torch.zeros(1, D, device=DEV)  # never read: the call is refused first
-    idx = torch.zeros(1, dtype=torch.int64, device=DEV)
+    # valid arguments of the claimed sizes (every index in bounds), so that a
+    # call that is not refused shows up as a changed `out`, never as a fault
+    rel = torch.zeros(1, D, device=DEV)
+    idx = torch.zeros(E, dtype=torch.int64, device=DEV)
     out = torch.full((K, D), 5.0, device=DEV)
     rc = capi.lib().relm_mp_fanin_reduce_noalloc(
-        capi.F32, rel.data_ptr(), E, D, idx.data_ptr(), idx.data_ptr(), E, K, 0, out.data_ptr(),
+        capi.F32, rel.data_ptr(), rel.size(0), D, idx.data_ptr(), idx.data_ptr(), E, K, 0, out.data_ptr(),
         capi._stream(rel))
     assert rc == capi.ERR_WORKSPACE
     assert "relm_mp_fanin_reduce_noalloc" in capi.last_error() and "workspace" in capi.last_error()
