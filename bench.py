@@ -13,15 +13,16 @@ The JSON line also carries
                   is the identity, so no index plan; one launch per step) timed
                   with HIP events on its stream around each timed step's
                   backward;
-  cpu_baseline  - the reference's own CPU op library (oracle/_ref) on a
-                  bounded 1/8-scale sample of C2, on the host's cores;
+  cpu_baseline  - the reference's own CPU op library (oracle/_ref) on the
+                  full C2 inputs (the job's thread share; 1 thread and a
+                  1/8-scale sample of both CPU lanes in its variants);
   extra         - kernel-only rates with cached plans, C2 with sum, C3 fanout
                   forward + backward, C1 latencies, the pack ops (index
                   preparation) and the LGAN pooling step against their ATen
                   formulation, C4 / C5 model training steps (graphs/sec).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--only c2|c2sum|c3|c1|c4|c5|pack|lgan|copy]
+                       [--only c2|c2sum|c2perm|c3|c1|c4|c5|pack|lgan|copy]
 """
 
 from __future__ import annotations
@@ -140,9 +141,25 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         out = mp.fanin_reduce(rel, flat_src, next(shifted), K, mode)
         torch.autograd.grad(out, rel, grad_out)
 
+    # The callers' layout (fused.py:183-190): message e is read from rel row
+    # flat_src[e], an injective map that is not the identity (a seeded
+    # permutation here).  Plans rebuilt every step: the forward's CSR plan,
+    # and in the backward an inverse plan of flat_src (k_inv_build) for
+    # k_lse_bwd_inv / k_gather_inv over it.
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    flat_perm = torch.randperm(E, device=dev, generator=gen)
+
+    def step_permuted():
+        ns.plan_cache_clear()
+        out = mp.fanin_reduce(rel, flat_perm, dst, K, mode)
+        torch.autograd.grad(out, rel, grad_out)
+
     sync = torch.cuda.synchronize
     t_step = timed(step_uncached, steps, warmup, sync)
     t_bwd_step = statistics.fmean(a.elapsed_time(b) for a, b in bwd_events[-steps:]) / 1e3
+    t_perm = timed(step_permuted, steps, warmup, sync)
+    del flat_perm
     t_cached = timed(step_cached, steps, warmup, sync)
     stats0 = ns.plan_cache_stats()
     t_same = timed(step_same_topology, steps, warmup, sync)
@@ -184,6 +201,8 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         "ms_step_same_topology_new_tensors": t_same * 1e3,
         "gbs_step_same_topology_new_tensors": gbs(b_fwd + b_bwd, t_same),
         "content_hits_same_topology": content_hits,
+        "ms_step_permuted_flat_src": t_perm * 1e3, "gbs_step_permuted_flat_src": gbs(b_fwd + b_bwd, t_perm),
+        "frac_step_permuted_flat_src": gbs(b_fwd + b_bwd, t_perm) / PEAK_HBM_GBS,
         "ms_step_new_topology_cache_kept": t_new * 1e3,
         "gbs_step_new_topology_cache_kept": gbs(b_fwd + b_bwd, t_new),
         "misses_new_topology": stats1[3] - stats0[3],
@@ -198,6 +217,36 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
     del d, rel, grad_out
     torch.cuda.empty_cache()
     return res
+
+
+def bench_c2_permuted(torch, mp, syn, steps: int, warmup: int, mode: int) -> dict:
+    """C2 with the callers' flat_src layout only (a seeded permutation, plans
+    rebuilt every step): the workload of ``--only c2perm``, for kernel traces
+    of that step alone."""
+
+    dev = torch.device("cuda", 0)
+    d = syn.c2_fanin(dev)
+    rel, dst, grad_out, K = d["rel"], d["dst"], d["grad_out"], d["dim_size"]
+    E, D = rel.shape
+    ns = torch.ops.relm_mp
+    rel.requires_grad_(True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    flat_perm = torch.randperm(E, device=dev, generator=gen)
+    if mode == 1:
+        nbytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_lse_bwd(E, D, K, E)
+    else:
+        nbytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_sum_bwd(E, D, K, E)
+
+    def step():
+        ns.plan_cache_clear()
+        out = mp.fanin_reduce(rel, flat_perm, dst, K, mode)
+        torch.autograd.grad(out, rel, grad_out)
+
+    t = timed(step, steps, warmup, torch.cuda.synchronize)
+    del d, rel, grad_out, flat_perm
+    torch.cuda.empty_cache()
+    return {"mode": mode, "ms_step": t * 1e3, "gbs_step": gbs(nbytes, t), "frac_of_peak": gbs(nbytes, t) / PEAK_HBM_GBS}
 
 
 def bench_c3(torch, mp, capi, syn, steps: int, warmup: int) -> dict:
@@ -305,6 +354,16 @@ def bench_models(torch, which: str, steps: int, warmup: int) -> dict:
                "output_linear": "sum / mean: on the hidden rows summed per (object, slot position)"}
         modes = ((0, "sum"), (1, "logsumexp"), (2, "mean"))
     res = {"config": cfg}
+    if which == "c5":
+        res["structure"] = {
+            "sum, logsumexp, mean": ("restructured central layer (this repository's): the first Linear per "
+                                     "object, gathered per relation node; for sum / mean the output Linear on "
+                                     "the hidden rows summed per (object, slot); logsumexp keeps per-node "
+                                     "outputs"),
+            "gathered_sum": "first Linear per object and gathered, per-node output Linear",
+            "assembled_input_sum": ("the reference's CentralFusedLayerMP structure (fused.py:311-375): the "
+                                    "central module on the assembled input - the like-for-like figure"),
+        }
     variants = [(mode, name, True, True) for mode, name in modes]
     if which == "c5":  # per-node outputs, and the module on the assembled input (sum)
         variants += [(0, "gathered_sum", True, False), (0, "assembled_input_sum", False, False)]
@@ -515,19 +574,61 @@ def host_threads() -> int:
 
 
 def cpu_baseline(syn, torch) -> dict:
-    """CPU baselines on a 1/8-scale C2 sample (same generator: 131,072 objects,
-    2,097,152 messages), logsumexp forward + backward, on the host's cores:
-      * the reference's own CPU op library (oracle/_ref, built from mp_ops.cpp),
-        at 1 thread and at the job's thread share - the headline baseline;
-      * relmo's python_only path (ATen index_select / scatter_reduce / exp /
-        scatter_add / log and autograd, mirrored by relmo_amd.mp_pack) at the
-        same two thread counts.
-    Falls back to the C oracle (1 thread) where oracle/_ref is absent."""
+    """CPU baseline of the headline workload, logsumexp forward + backward on
+    the host's cores:
+      * headline: the reference's own CPU op library (oracle/_ref, built from
+        mp_ops.cpp) on the full C2 inputs ``value`` is measured on (the same
+        seeded tensors, generated on the GPU and copied to the host), once at
+        the job's thread share and once at 1 thread, as the reference's bench
+        pins (benchmark_mp_ops.py:634-638);
+      * variants: the same library and relmo's python_only path (ATen
+        index_select / scatter_reduce / exp / scatter_add / log and autograd,
+        mirrored by relmo_amd.mp_pack) on a 1/8-scale C2 sample (131,072
+        objects, 2,097,152 messages) at 1 thread and at the job's share.
+    Falls back to the C oracle (1 thread, 1/8 sample) where oracle/_ref is
+    absent."""
 
     import numpy as np
 
     from oracle import oracle, ref_runner
+    from relmo_amd import mp
     from relmo_amd import mp_pack
+
+    full = host_threads()
+    variants = []
+    headline = None
+    if ref_runner.available():
+        d = syn.c2_fanin(torch.device("cuda", 0))
+        Kf, (Ef, Df) = d["dim_size"], d["rel"].shape
+        out_f = mp.fanin_reduce(d["rel"], d["flat_src"], d["dst"], Kf, 1)
+        arrays = {"rel": d["rel"].cpu().numpy(), "src": d["flat_src"].cpu().numpy(),
+                  "dst": d["dst"].cpu().numpy(), "g": d["grad_out"].cpu().numpy(), "out": out_f.cpu().numpy()}
+        del d, out_f
+        torch.cuda.empty_cache()
+        nbytes_f = syn.bytes_fanin_fwd(Ef, Df, Kf) + syn.bytes_fanin_lse_bwd(Ef, Df, Kf, Ef)
+        calls = []
+        for th in (full, 1):
+            calls += [{"op": "fanin_reduce", "tensors": ["rel", "src", "dst"], "ints": [Kf, 1], "repeat": 1,
+                       "warmup": 0, "threads": th, "keep": False},
+                      {"op": "fanin_reduce_logsumexp_backward", "tensors": ["g", "rel", "src", "dst", "out"],
+                       "ints": [Ef], "repeat": 1, "warmup": 0, "threads": th, "keep": False}]
+        res = ref_runner.run_reference(calls, arrays, timeout=900.0)
+        del arrays
+        for i in (0, 2):
+            if "error" in res[i] or "error" in res[i + 1]:
+                raise RuntimeError(f"reference library: {res[i].get('error') or res[i + 1].get('error')}")
+            t = res[i]["times"][0] + res[i + 1]["times"][0]
+            threads = res[i]["threads"]
+            entry = {"kind": "reference relm_mp_ops CPU lane, full C2", "threads": threads,
+                     "seconds": round(t, 4), "value": round(gbs(nbytes_f, t), 3)}
+            if headline is None:
+                headline = {"value": entry["value"], "unit": "GB/s", "cores": threads, "kind": "reference",
+                            "sample": (f"C2 in full, the inputs value is measured on (K={Kf}, E={Ef}, D={Df}, "
+                                       f"Zipf(1.1) dst), logsumexp fwd+bwd; reference CPU lane (ATen "
+                                       f"sequences, mp_ops.cpp:2981-3036), {threads} threads, one run, "
+                                       f"{t:.3f} s per fwd+bwd")}
+            else:
+                variants.append(entry)
 
     K, E, D = 1 << 17, 1 << 21, 32
     rng = np.random.default_rng(0)
@@ -540,8 +641,6 @@ def cpu_baseline(syn, torch) -> dict:
     g = rng.standard_normal((K, D)).astype(np.float32)
     nbytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_lse_bwd(E, D, K, E)
     sample = f"C2 at 1/8 scale: K={K}, E={E}, D={D}, Zipf(1.1) dst, logsumexp fwd+bwd"
-    full = host_threads()
-    variants = []
 
     # python_only: ATen forward + autograd backward, in this process on CPU tensors
     rel_t = torch.from_numpy(rel)
@@ -560,14 +659,13 @@ def cpu_baseline(syn, torch) -> dict:
         t0 = time.perf_counter()
         aten_step()
         t = time.perf_counter() - t0
-        variants.append({"kind": "python_only (ATen)", "threads": th, "seconds": round(t, 4),
+        variants.append({"kind": "python_only (ATen), 1/8 C2", "threads": th, "seconds": round(t, 4),
                          "value": round(gbs(nbytes, t), 3)})
     torch.set_num_threads(saved)
 
-    if ref_runner.available():
+    if headline is not None:
         out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, K)
         arrays = {"rel": rel, "src": flat_src, "dst": dst, "g": g, "out": out}
-        headline = None
         for th, reps, warm in ((1, 1, 0), (full, 3, 1)):
             calls = [
                 {"op": "fanin_reduce", "tensors": ["rel", "src", "dst"], "ints": [K, 1], "repeat": reps,
@@ -577,13 +675,10 @@ def cpu_baseline(syn, torch) -> dict:
             ]
             res = ref_runner.run_reference(calls, arrays)
             t = statistics.median(res[0]["times"]) + statistics.median(res[1]["times"])
-            threads = res[0]["threads"]
-            variants.append({"kind": "reference relm_mp_ops CPU lane", "threads": threads,
+            variants.append({"kind": "reference relm_mp_ops CPU lane, 1/8 C2", "threads": res[0]["threads"],
                              "seconds": round(t, 4), "value": round(gbs(nbytes, t), 3)})
-            headline = {"value": round(gbs(nbytes, t), 3), "unit": "GB/s", "cores": threads, "kind": "reference",
-                        "sample": sample + f"; reference CPU lane (ATen sequences, mp_ops.cpp:2981-3036), "
-                                           f"{threads} threads, median of {reps}, {t:.3f} s per fwd+bwd"}
         headline["variants"] = variants
+        headline["sample_1_8"] = sample
         headline["host"] = host_info(torch)
         return headline
     t0 = time.perf_counter()
@@ -850,7 +945,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["c2", "c2sum", "c3", "c1", "c4", "c5", "pack", "lgan", "slots",
+    ap.add_argument("--only", choices=["c2", "c2sum", "c2perm", "c3", "c1", "c4", "c5", "pack", "lgan", "slots",
                                        "copy"],
                     default=None,
                     help="run one workload only and print its figures (for profiling)")
@@ -888,6 +983,7 @@ def main() -> int:
     if args.only:
         fn = {"c2": lambda: bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 1),
               "c2sum": lambda: bench_c2(torch, mp, capi, syn, args.steps, args.warmup, 0),
+              "c2perm": lambda: bench_c2_permuted(torch, mp, syn, args.steps, args.warmup, 1),
               "c3": lambda: bench_c3(torch, mp, capi, syn, args.steps, args.warmup),
               "c1": lambda: bench_c1(torch, mp, syn),
               "c4": lambda: bench_models(torch, "c4", args.steps, args.warmup),
