@@ -319,6 +319,30 @@ int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
                                        const void* grad_out, const void* out,
                                        const void* rel_flat, int64_t emb, void* grad_rel,
                                        int64_t rel_rows, relm_mp_stream_t stream);
+/* Backward of fanin_reduce over the FORWARD's CSR plan when flat_src is not the
+ * identity: the inverse map of flat_src (rows of grad_rel -> edges) is built
+ * from the plan's int32 snapshot of flat_src (validated by the plan's build)
+ * with plain stores - no atomics, no second validation - and a second pass
+ * counts the edges whose row another edge also reads (collisions).  The
+ * backward kernel is queued right after and does nothing on the device when
+ * that count is nonzero; the call then waits for the count and stores it in
+ * *collisions.  0: grad_rel [rel_rows, emb] holds what
+ * relm_mp_fanin_reduce_sum_backward (mode 0) / _logsumexp_backward (mode 1)
+ * give for the same tensors (rows no edge reads are 0).  Nonzero: flat_src
+ * repeats and grad_rel is unspecified (use a CSR plan keyed by flat_src).
+ * Requires rel_rows >= dst_plan->num_gather; rel_flat has rel_rows rows (read
+ * in mode 1 only).  inv_mem holds relm_mp_inv_plan_bytes(rel_rows,
+ * dst_plan->num_edges, 0) bytes.  map_ready != 0: inv_mem already holds the
+ * map an earlier call built for this dst_plan and rel_rows with no collision
+ * (that call's work on `stream` precedes this one); only the backward kernel is
+ * launched, without waiting, and *collisions is 0.  No reference counterpart:
+ * it replaces the inverse-plan build of the backward ops (mp_ops.cpp:3224-3325
+ * take flat_src and dst_idx afresh) for callers that hold the forward's plan. */
+int relm_mp_plan_fanin_backward_by_src(int dtype, const relm_mp_plan* dst_plan, int64_t mode,
+                                       const void* grad_out, const void* out, const void* rel_flat,
+                                       int64_t emb, void* grad_rel, int64_t rel_rows, void* inv_mem,
+                                       size_t inv_bytes, int map_ready, int64_t* collisions,
+                                       relm_mp_stream_t stream);
 
 /* ---- row epilogues (the LGAN indexed reductions) ------------------------- */
 

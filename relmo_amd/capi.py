@@ -57,6 +57,7 @@ EXPORTED_SYMBOLS = (
     "relm_mp_plan_segment_reduce",
     "relm_mp_plan_logsumexp_backward",
     "relm_mp_plan_fanin_backward_by_dst",
+    "relm_mp_plan_fanin_backward_by_src",
     "relm_mp_pack_index",
     "relm_mp_plan_match_workspace_size",
     "relm_mp_plan_match",
@@ -167,6 +168,9 @@ _SIGNATURES = {
     "relm_mp_plan_segment_reduce": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_logsumexp_backward": (_int, [_int, _PP, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_fanin_backward_by_dst": (_int, [_int, _PP, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "relm_mp_plan_fanin_backward_by_src": (
+        _int, [_int, _PP, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _sz, _int, ctypes.POINTER(ctypes.c_int64),
+               _vp]),
     "relm_mp_pack_index": (_int, [ctypes.POINTER(IndexPart), ctypes.c_int32, _vp, _vp, _vp]),
     "relm_mp_plan_match_workspace_size": (_sz, []),
     "relm_mp_rows_scale": (_int, [_int, _vp, _vp, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
@@ -536,6 +540,26 @@ def plan_fanin_backward_by_dst(bp: BuiltPlan, dst_idx: torch.Tensor, mode: int, 
         )
     )
     return grad_rel
+
+
+def plan_fanin_backward_by_src(bp: BuiltPlan, mode: int, grad_out: torch.Tensor, rel_rows: int,
+                               out: torch.Tensor | None = None,
+                               rel_flat: torch.Tensor | None = None) -> tuple[torch.Tensor, int]:
+    """Backward of fanin_reduce over the forward's CSR plan when flat_src is not
+    the identity: (grad_rel, collisions); grad_rel is the result when
+    collisions == 0."""
+
+    emb = grad_out.size(1)
+    grad_rel = torch.empty(rel_rows, emb, dtype=grad_out.dtype, device=grad_out.device)
+    mem = _bytes(lib().relm_mp_inv_plan_bytes(rel_rows, bp.plan.num_edges, 0), grad_out)
+    collisions = ctypes.c_int64(-1)
+    check(
+        lib().relm_mp_plan_fanin_backward_by_src(
+            _dtype(grad_out), ctypes.byref(bp.plan), mode, _ptr(grad_out), _ptr(out), _ptr(rel_flat), emb,
+            _ptr(grad_rel), rel_rows, _ptr(mem), mem.numel(), 0, ctypes.byref(collisions), _stream(grad_out),
+        )
+    )
+    return grad_rel, collisions.value
 
 
 def identity_inv_plan(num_keys: int, num_edges: int, num_gather: int) -> BuiltPlan:

@@ -880,6 +880,59 @@ int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
                                    grad_rel, rel_rows, static_cast<hipStream_t>(stream));
 }
 
+int relm_mp_plan_fanin_backward_by_src(int dtype, const relm_mp_plan* dst_plan, int64_t mode,
+                                       const void* grad_out, const void* out, const void* rel_flat,
+                                       int64_t emb, void* grad_rel, int64_t rel_rows, void* inv_mem,
+                                       size_t inv_bytes, int map_ready, int64_t* collisions,
+                                       relm_mp_stream_t stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RELM_TRY(check_dtype(dtype));
+    RELM_TRY(check_rows(rel_rows, "rel_rows"));
+    if (dst_plan == nullptr || collisions == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan or collisions is NULL");
+    if (emb < 0) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "emb must be >= 0.");
+    if (mode != RELM_MP_MODE_SUM && mode != RELM_MP_MODE_LOGSUMEXP)
+        return set_error(RELM_MP_ERR_UNSUPPORTED_MODE,
+                         "Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
+    const relm_mp_plan& fwd = *dst_plan;
+    if (fwd.kind != RELM_MP_PLAN_CSR || fwd.snap_gathers == nullptr || fwd.snap_keys == nullptr)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: backward by source needs a CSR plan built with a gather array");
+    if (rel_rows < fwd.num_gather)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT,
+                         "relm_mp: backward by source needs rel_rows >= the plan's num_gather");
+    *collisions = 0;
+    if (rel_rows == 0 || emb == 0) return RELM_MP_OK;
+    const InvLayout l = inv_layout(inv_mem, rel_rows, fwd.num_edges, 0);
+    if (inv_mem == nullptr || inv_bytes < l.bytes)
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: inverse plan memory too small");
+    relm_mp_plan inv{};
+    inv.kind = RELM_MP_PLAN_INVERSE;
+    inv.num_keys = rel_rows;
+    inv.num_edges = fwd.num_edges;
+    inv.num_gather = fwd.num_keys;
+    inv.inv = l.inv;
+    inv.counts = l.counts;
+    inv.collisions = -1;
+    if (map_ready != 0)  // the map and its device counts from an earlier call
+        return compute_backward_by_src(dtype, fwd, inv, mode, grad_out, out, rel_flat, emb, grad_rel, s);
+    HostSlot* hs = nullptr;
+    RELM_TRY(host_slot(&hs));
+    RELM_TRY(no_pending(hs));
+    RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
+    RELM_HIP(launch_fill_i32(l.inv, rel_rows, -1, s), "relm_mp fill");
+    RELM_HIP(launch_inv_from_snapshot(fwd.snap_gathers, fwd.snap_gather_plain, fwd.num_edges, rel_rows,
+                                      l.inv, l.status, s),
+             "relm_mp inverse map kernels");
+    int32_t gen = 0;
+    RELM_HIP(hs->publish_status(l.status, l.counts, s, &gen), "relm_mp status publish");
+    // queued before the host reads the count: the kernels check it on the device
+    RELM_TRY(compute_backward_by_src(dtype, fwd, inv, mode, grad_out, out, rel_flat, emb, grad_rel, s));
+    RELM_TRY(wait_host_word(hs->status_gen, gen, s, "relm_mp status wait"));
+    *collisions = static_cast<int64_t>(hs->status->collisions);
+    return RELM_MP_OK;
+}
+
 /* ---- op-level entry points -------------------------------------------- */
 
 size_t relm_mp_fanout_scatter_workspace_size(int64_t num_edges, int64_t out_rows) {

@@ -83,6 +83,12 @@ struct SnapOut {
 hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                             int64_t gather_bound, int64_t n, int32_t* inv, const SnapOut& snap,
                             DevStatus* st, hipStream_t s);
+// inv (filled with -1 before) [g(e)] = e for the n edges of a plan's int32
+// snapshot (g(e) = e on tiles flagged in `plain`, which may be null), with plain
+// stores; then st->collisions counts the edges whose row another edge took or
+// whose index is >= key_bound, and st->key_mismatch flags g(e) != e.
+hipError_t launch_inv_from_snapshot(const int32_t* snap, const uint32_t* plain, int64_t n,
+                                    int64_t key_bound, int32_t* inv, DevStatus* st, hipStream_t s);
 
 
 // Stable LSD radix sort of (key, value) by key.  The first pass reads the
@@ -209,6 +215,14 @@ int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* 
                             int64_t mode, const void* grad_out, const void* out,
                             const void* rel_flat, int64_t emb, void* grad_rel, int64_t rel_rows,
                             hipStream_t s);
+// Backward of fanin_reduce (mode 0 / 1) by rows of grad_rel through inv_plan
+// (an inverse map of flat_src built without atomics, launch_inv_from_snapshot:
+// the kernels do nothing on the device when its count of collisions is
+// nonzero), each row's destination from dst_plan's int32 snapshot of dst_idx
+// (dst_plan: the forward's CSR plan).
+int compute_backward_by_src(int dtype, const relm_mp_plan& dst_plan, const relm_mp_plan& inv_plan,
+                            int64_t mode, const void* grad_out, const void* out,
+                            const void* rel_flat, int64_t emb, void* grad_rel, hipStream_t s);
 size_t hub_partial_bytes(const relm_mp_plan& plan, int64_t emb, int dtype, int64_t mode);
 
 }  // namespace relm_mp

@@ -148,7 +148,65 @@ __global__ __launch_bounds__(kThreads) void k_inv_build(const int64_t* __restric
     if (bad_k != kNoEdge) atomicMin(&st->bad_key_edge, bad_k);
     if (bad_g != kNoEdge) atomicMin(&st->bad_gather_edge, bad_g);
     if (lane_id() == 0 && collisions != 0) atomicAdd(&st->collisions, collisions);
-    if (__ballot(key_mismatch != 0) != 0 && lane_id() == 0) atomicOr(&st->key_mismatch, 1ull);
+    // a flag that only ever becomes 1: a plain store from one thread per
+    // workgroup (atomics on one word from thousands of workgroups serialise)
+    if (__syncthreads_or(key_mismatch) && threadIdx.x == 0) st->key_mismatch = 1ull;
+}
+
+// Inverse map of a CSR plan's gathered indices, from the plan's int32
+// snapshot of them (tiles flagged plain hold the edge ids): inv[g(e)] = e with
+// plain stores.  The snapshot was validated by the plan's build; an index at
+// or past key_bound is skipped here and counted by k_inv_verify.  With
+// repeated indices one writer wins per row; k_inv_verify finds the others.
+__device__ __forceinline__ int64_t snap_index(const int32_t* __restrict__ snap,
+                                              const uint32_t* __restrict__ plain, int64_t e) {
+    return plain != nullptr && plain[e / kSnapTile] != 0u ? e : static_cast<int64_t>(snap[e]);
+}
+
+__global__ __launch_bounds__(kThreads) void k_inv_scatter(const int32_t* __restrict__ snap,
+                                                          const uint32_t* __restrict__ plain,
+                                                          int64_t n, int64_t key_bound,
+                                                          int32_t* __restrict__ inv) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+        const int64_t r = snap_index(snap, plain, e);
+        if (static_cast<uint64_t>(r) < static_cast<uint64_t>(key_bound)) inv[r] = static_cast<int32_t>(e);
+    }
+}
+
+// Counts the edges e with inv[g(e)] != e (g(e) read by another edge too, or
+// out of range) into st->collisions, and flags g(e) != e in st->key_mismatch.
+__global__ __launch_bounds__(kThreads) void k_inv_verify(const int32_t* __restrict__ snap,
+                                                         const uint32_t* __restrict__ plain,
+                                                         int64_t n, int64_t key_bound,
+                                                         const int32_t* __restrict__ inv,
+                                                         DevStatus* __restrict__ st) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    unsigned long long lost = 0;
+    int mismatch = 0;
+    for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * blockDim.x; e0 < n; e0 += stride) {
+        const int64_t e = e0 + threadIdx.x;
+        bool bad = false;
+        if (e < n) {
+            const int64_t r = snap_index(snap, plain, e);
+            const bool in = static_cast<uint64_t>(r) < static_cast<uint64_t>(key_bound);
+            bad = !in || inv[in ? r : 0] != static_cast<int32_t>(e);
+            mismatch |= r != e ? 1 : 0;
+        }
+        lost += __popcll(__ballot(bad));
+    }
+    // one atomic per workgroup that lost edges; the mismatch flag (only ever 1)
+    // as a plain store - atomics on one word from thousands of workgroups
+    // serialise
+    __shared__ unsigned long long s_lost;
+    if (threadIdx.x == 0) s_lost = 0;
+    __syncthreads();
+    if (lane_id() == 0 && lost != 0) atomicAdd(&s_lost, lost);
+    const int any_mismatch = __syncthreads_or(mismatch);
+    if (threadIdx.x == 0) {
+        if (s_lost != 0) atomicAdd(&st->collisions, s_lost);
+        if (any_mismatch) st->key_mismatch = 1ull;
+    }
 }
 
 // ---- scan ----------------------------------------------------------------
@@ -341,7 +399,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
     if (bad_g != kNoEdge) atomicMin(&st->bad_gather_edge, bad_g);
     if (threadIdx.x == 0) {
         tile_plain[blockIdx.x] = any ? 0u : 1u;
-        if (any) atomicOr(&st->gather_mismatch, 1ull);
+        if (any) st->gather_mismatch = 1ull;  // only ever 1: a plain store, no atomic
     }
     __syncthreads();
     store_tile_counts(hist, chunk_sum, hist_total(h));
@@ -921,6 +979,18 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         shift += width;
     }
     return hipSuccess;
+}
+
+hipError_t launch_inv_from_snapshot(const int32_t* snap, const uint32_t* plain, int64_t n,
+                                    int64_t key_bound, int32_t* inv, DevStatus* st, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid(grid_1d(n, kThreads * 8, 1 << 16));
+    hipLaunchKernelGGL(k_inv_scatter, grid, dim3(kThreads), 0, s, snap, plain, n, key_bound, inv);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_inv_verify, grid, dim3(kThreads), 0, s, snap, plain, n, key_bound,
+                       static_cast<const int32_t*>(inv), st);
+    return hipGetLastError();
 }
 
 hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,

@@ -894,9 +894,12 @@ __global__ __launch_bounds__(kThreads) void k_gather_inv(const int32_t* __restri
                                                          int64_t num_gather,
                                                          const T* __restrict__ table,
                                                          int64_t num_keys, int64_t D,
-                                                         T* __restrict__ out, Rows out_rows) {
+                                                         T* __restrict__ out, Rows out_rows,
+                                                         bool skip_on_collision) {
     constexpr int R = kThreads / G;
     constexpr int RU = gather_rows_in_flight<T, V>();
+    // an inverse map built without atomics is only used when no row repeats
+    if (skip_on_collision && pc->collisions != 0) return;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
@@ -1010,9 +1013,11 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
     int64_t num_edges, Src gathers,
     int64_t num_gather,
     const T* __restrict__ grad_out, const T* __restrict__ out, const T* __restrict__ rel,
-    int64_t num_keys, int64_t D, T* __restrict__ grad_rel) {
+    int64_t num_keys, int64_t D, T* __restrict__ grad_rel, bool skip_on_collision) {
     constexpr int R = kThreads / G;
     constexpr int RU = kLseRowsInFlight;
+    // an inverse map built without atomics is only used when no row repeats
+    if (skip_on_collision && pc->collisions != 0) return;
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
@@ -1231,7 +1236,7 @@ int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, 
 template <typename T>
 int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* table_v,
                   int64_t emb, void* out_v, int64_t group, int64_t group_stride, hipStream_t s,
-                  const relm_mp_plan* snap = nullptr) {
+                  const relm_mp_plan* snap = nullptr, bool skip_on_collision = false) {
     const T* table = static_cast<const T*>(table_v);
     T* out = static_cast<T*>(out_v);
     auto launch = [&](auto vt, auto gt, const Geometry& geo, auto rows) -> int {
@@ -1244,11 +1249,11 @@ int gather_last_t(const relm_mp_plan& plan, const int64_t* gathers, const void* 
                 hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows, GathersSnap>), grid, dim3(kThreads), 0, s,
                                    plan.inv, plan.counts, plan.num_edges,
                                    GathersSnap{snap->snap_keys, snap->snap_key_plain}, plan.num_gather,
-                                   table, plan.num_keys, emb, out, rows);
+                                   table, plan.num_keys, emb, out, rows, skip_on_collision);
             } else {
                 hipLaunchKernelGGL((k_gather_inv<T, V, G, Rows, GathersI64>), grid, dim3(kThreads), 0, s,
                                    plan.inv, plan.counts, plan.num_edges, GathersI64{gathers},
-                                   plan.num_gather, table, plan.num_keys, emb, out, rows);
+                                   plan.num_gather, table, plan.num_keys, emb, out, rows, skip_on_collision);
             }
         } else {
             hipLaunchKernelGGL((k_gather_last_csr<T, V, G, Rows>),
@@ -1339,7 +1344,8 @@ int segment_sum_scaled_t(const relm_mp_plan& plan, const void* table_v, int64_t 
 template <typename T>
 int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void* grad_out_v,
                    const void* out_v, const void* rel_v, int64_t emb, void* grad_rel_v,
-                   void* scratch, hipStream_t s, const relm_mp_plan* snap = nullptr) {
+                   void* scratch, hipStream_t s, const relm_mp_plan* snap = nullptr,
+                   bool skip_on_collision = false) {
     const T* grad_out = static_cast<const T*>(grad_out_v);
     const T* out = static_cast<const T*>(out_v);
     const T* rel = static_cast<const T*>(rel_v);
@@ -1356,11 +1362,12 @@ int lse_backward_t(const relm_mp_plan& plan, const int64_t* gathers, const void*
                 hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G, GathersSnap>), grid, dim3(kThreads), 0, s,
                                    plan.inv, plan.counts, plan.num_edges,
                                    GathersSnap{snap->snap_keys, snap->snap_key_plain}, plan.num_gather,
-                                   grad_out, out, rel, plan.num_keys, emb, grad_rel);
+                                   grad_out, out, rel, plan.num_keys, emb, grad_rel, skip_on_collision);
             } else {
                 hipLaunchKernelGGL((k_lse_bwd_inv<T, V, G, GathersI64>), grid, dim3(kThreads), 0, s,
                                    plan.inv, plan.counts, plan.num_edges, GathersI64{gathers},
-                                   plan.num_gather, grad_out, out, rel, plan.num_keys, emb, grad_rel);
+                                   plan.num_gather, grad_out, out, rel, plan.num_keys, emb, grad_rel,
+                                   skip_on_collision);
             }
             return hip_error(hipGetLastError(), "relm_mp logsumexp backward kernel");
         }
@@ -1516,6 +1523,42 @@ int compute_logsumexp_backward(int dtype, const relm_mp_plan& plan, const int64_
     return dtype == RELM_MP_F64
                ? lse_backward_t<double>(plan, gathers, grad_out, out, rel_flat, emb, grad_rel, scratch, s)
                : lse_backward_t<float>(plan, gathers, grad_out, out, rel_flat, emb, grad_rel, scratch, s);
+}
+
+int compute_backward_by_src(int dtype, const relm_mp_plan& dst_plan, const relm_mp_plan& inv_plan,
+                            int64_t mode, const void* grad_out, const void* out,
+                            const void* rel_flat, int64_t emb, void* grad_rel, hipStream_t s) {
+    if (inv_plan.num_keys == 0 || emb == 0) return RELM_MP_OK;
+    if (mode != RELM_MP_MODE_SUM && mode != RELM_MP_MODE_LOGSUMEXP)
+        return set_error(RELM_MP_ERR_UNSUPPORTED_MODE,
+                         "Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
+    // rows in order through the inverse map; each row's destination from the
+    // forward plan's int32 snapshot of dst_idx
+    const relm_mp_plan* snap = &dst_plan;
+    if (mode == RELM_MP_MODE_SUM) {
+        // as the edge-order sum backward: grad_out and the destinations read
+        // into the memory-side cache first when they fit
+        const size_t elem = dtype == RELM_MP_F64 ? 8 : 4;
+        const size_t tb = static_cast<size_t>(dst_plan.num_keys) * static_cast<size_t>(emb) * elem;
+        const size_t ib = static_cast<size_t>(dst_plan.num_edges) * sizeof(int32_t);
+        if (tb + ib <= kPrefetchMaxBytes && tb % 16 == 0 && ib % 16 == 0 &&
+            (reinterpret_cast<uintptr_t>(grad_out) | reinterpret_cast<uintptr_t>(dst_plan.snap_keys)) % 16 == 0) {
+            const int64_t units = static_cast<int64_t>((tb + ib) / 16);
+            const int64_t blocks = std::min<int64_t>((units + kThreads * 8 - 1) / (kThreads * 8), 4096);
+            hipLaunchKernelGGL(k_touch, dim3(static_cast<unsigned>(std::max<int64_t>(blocks, 1))),
+                               dim3(kThreads), 0, s, static_cast<const uint4*>(grad_out),
+                               static_cast<int64_t>(tb / 16), reinterpret_cast<const uint4*>(dst_plan.snap_keys),
+                               static_cast<int64_t>(ib / 16));
+            const int rc = hip_error(hipGetLastError(), "relm_mp prefetch kernel");
+            if (rc != RELM_MP_OK) return rc;
+        }
+        return dtype == RELM_MP_F64
+                   ? gather_last_t<double>(inv_plan, nullptr, grad_out, emb, grad_rel, 0, 0, s, snap, true)
+                   : gather_last_t<float>(inv_plan, nullptr, grad_out, emb, grad_rel, 0, 0, s, snap, true);
+    }
+    return dtype == RELM_MP_F64
+               ? lse_backward_t<double>(inv_plan, nullptr, grad_out, out, rel_flat, emb, grad_rel, nullptr, s, snap, true)
+               : lse_backward_t<float>(inv_plan, nullptr, grad_out, out, rel_flat, emb, grad_rel, nullptr, s, snap, true);
 }
 
 int compute_backward_by_key(int dtype, const relm_mp_plan& plan, const int64_t* dst_idx,

@@ -138,6 +138,14 @@ struct PlanRef : torch::CustomClassHolder {
     int64_t key_bound = 0;
     int64_t gather_bound = 0;
     hipStream_t stream = nullptr;  // the stream the plan was built on
+    // CSR plans of a fanin forward: the inverse map of their gathered indices
+    // (flat_src), built by the first backward that needs it
+    // (relm_mp_plan_fanin_backward_by_src) and kept for later backward calls
+    // on the same stream with the same row count; inv_rows < 0: none.
+    std::mutex inv_mu;
+    Tensor inv_mem;
+    int64_t inv_rows = -1;
+    hipStream_t inv_stream = nullptr;
 
     PlanRef() = default;
     PlanRef(const PlanRef&) = delete;
@@ -688,6 +696,34 @@ PlanPtr fanin_forward_plan(const PlanRef* handoff, const Tensor& d_idx, const Te
     return PlanCache::get().lookup(kRoleCsr, d_idx, &s_idx, dim_size, -1, stream);
 }
 
+// The backward through the forward's CSR plan when flat_src is injective but
+// not the identity (the callers' layout): the inverse map of flat_src comes
+// from the plan's snapshot of it without atomics, and the kernel is queued
+// before the host learns whether flat_src repeats.  False (nothing to use)
+// when there is no such plan or flat_src repeats: the caller then builds its
+// own plans.  Rows [0, rows) of grad_rel are written.
+bool backward_by_src(const PlanPtr& fwd, int64_t mode, const Tensor& g, const void* out,
+                     const void* rel, int64_t emb, Tensor& grad_rel, int64_t rows, hipStream_t stream) {
+    if (!fwd || fwd->plan.gather_identity != 0 || fwd->plan.snap_gathers == nullptr ||
+        rows < fwd->plan.num_gather)
+        return false;
+    PlanRef& ref = *fwd;
+    std::lock_guard<std::mutex> lock(ref.inv_mu);
+    const bool ready = ref.inv_rows == rows && ref.inv_stream == stream && ref.inv_mem.defined();
+    Tensor mem = ready ? ref.inv_mem : byte_buffer(relm_mp_inv_plan_bytes(rows, fwd->plan.num_edges, 0), g);
+    int64_t collisions = 0;
+    raise_if(relm_mp_plan_fanin_backward_by_src(dtype_code(g), &fwd->plan, mode, g.data_ptr(), out, rel, emb,
+                                                grad_rel.data_ptr(), rows, mem.data_ptr(),
+                                                static_cast<size_t>(mem.numel()), ready ? 1 : 0, &collisions,
+                                                stream));
+    if (!ready && collisions == 0) {
+        ref.inv_mem = mem;
+        ref.inv_rows = rows;
+        ref.inv_stream = stream;
+    }
+    return collisions == 0;
+}
+
 Tensor fanin_reduce_sum_backward_gpu(const Tensor& grad_out, const Tensor& flat_src,
                                      const Tensor& dst_idx, int64_t rel_rows,
                                      const PlanRef* handoff = nullptr) {
@@ -712,6 +748,8 @@ Tensor fanin_reduce_sum_backward_gpu(const Tensor& grad_out, const Tensor& flat_
                                                     grad_rel.data_ptr(), rel_rows, stream));
         return grad_rel;
     }
+    if (backward_by_src(fwd, kModeSum, g, nullptr, nullptr, emb, grad_rel, rel_rows, stream))
+        return grad_rel;
     PlanPtr inv = inverse_plan(s_idx, rel_rows, "flat_src", d_idx, g.size(0), "dst_idx", false,
                                stream);
     if (inv->plan.collisions == 0) {
@@ -762,6 +800,9 @@ Tensor fanin_reduce_logsumexp_backward_gpu(const Tensor& grad_out, const Tensor&
         return grad_rel;
     }
     if (key_bound < rel_rows) grad_rel.narrow(0, key_bound, rel_rows - key_bound).zero_();
+    if (backward_by_src(fwd, kModeLogSumExp, g, o.data_ptr(), rel.data_ptr(), emb, grad_rel, key_bound,
+                        stream))
+        return grad_rel;
     const auto reference_error = [&]() {
         raise_lse_backward_index_error(s_idx, rel.size(0), d_idx, o.size(0), rel_rows);
     };

@@ -571,6 +571,101 @@ def test_backward_by_dst_with_plain_snapshot_tiles() -> None:
                                rtol=1e-4, atol=1e-6)
 
 
+def _injective_flat_src(rng, layout: str, n: int):
+    """(flat_src, rel_rows) of n edges, injective and not the identity."""
+
+    if layout == "callers":  # fused.py:183-190 for arity-2 predicates: position-major, flat = 2 atom + pos
+        a = np.arange(n // 2)
+        return np.concatenate([2 * a, 2 * a + 1]), n + 17
+    if layout == "gaps":  # arity 2 in a max-arity-3 row layout: every third row has no edge
+        a = np.arange(n // 2)
+        return np.concatenate([3 * a, 3 * a + 1]), 3 * (n // 2)
+    if layout == "partly_plain":  # the edge ids except one 4096-edge tile and the last edges
+        f = np.arange(n)
+        f[4096:2 * 4096] = f[4096:2 * 4096][rng.permutation(4096)]
+        f[-50:] = f[-50:][::-1]
+        return f, n
+    return rng.permutation(n), n + 17
+
+
+@pytest.mark.parametrize("layout", ["callers", "gaps", "partly_plain", "random"])
+@pytest.mark.parametrize("emb", [6, 32, 64])
+def test_backward_by_src_over_the_forward_plan(layout: str, emb: int) -> None:
+    """flat_src injective but not the identity: the fanin backward builds the
+    inverse map of flat_src from the forward plan's snapshot, without atomics,
+    reports no collision, and equals the oracle (sum: exact copies) and the
+    inverse-plan lane bit for bit; rows that no edge reads are zero.  A
+    flat_src that repeats an index reports collisions."""
+
+    from relmo_amd import capi
+
+    _log(f"backward by src layout={layout} emb={emb}")
+    rng = np.random.default_rng(50 + emb)
+    num_keys, n = 3000, 50_000
+    dst = _zipf_keys(rng, num_keys, n)
+    flat_src, rel_rows = _injective_flat_src(rng, layout, n)
+    assert np.unique(flat_src).size == n and flat_src.max() < rel_rows
+    rel = (2.0 * rng.standard_normal((rel_rows, emb))).astype(np.float32)
+    g = rng.standard_normal((num_keys, emb)).astype(np.float32)
+    bp = capi.csr_plan(_t(dst), num_keys, _t(flat_src), rel_rows, "dst_idx", "flat_src", True)
+    assert bp.plan.gather_identity == 0
+    got, coll = capi.plan_fanin_backward_by_src(bp, 0, _t(g), rel_rows)
+    assert coll == 0
+    assert np.array_equal(_np(got), oracle.fanin_reduce_sum_backward(g, flat_src, dst, rel_rows))
+    out = oracle.fanin_reduce_logsumexp(rel, flat_src, dst, num_keys)
+    got, coll = capi.plan_fanin_backward_by_src(bp, 1, _t(g), rel_rows, _t(out), _t(rel))
+    assert coll == 0
+    got = _np(got)
+    np.testing.assert_allclose(got, oracle.fanin_reduce_logsumexp_backward(g, rel, flat_src, dst, out, rel_rows),
+                               rtol=1e-4, atol=1e-6)
+    inv_lane = _np(capi.fanin_reduce_logsumexp_backward(_t(g), _t(rel), _t(flat_src), _t(dst), _t(out), rel_rows))
+    assert np.array_equal(got, inv_lane)
+    # one repeated index: counted as a collision
+    flat_dup = flat_src.copy()
+    flat_dup[5] = flat_dup[n - 3]
+    bp2 = capi.csr_plan(_t(dst), num_keys, _t(flat_dup), rel_rows, "dst_idx", "flat_src", True)
+    _, coll = capi.plan_fanin_backward_by_src(bp2, 0, _t(g), rel_rows)
+    assert coll > 0
+
+
+@pytest.mark.parametrize("layout", ["callers", "random", "repeats"])
+def test_facade_backward_with_injective_flat_src(layout: str, mp_env) -> None:
+    """Autograd through the facade with a flat_src that is not the identity:
+    the backward runs over the forward's plan (inverse map from its snapshot)
+    when flat_src is injective, and over its own CSR plan when it repeats; the
+    gradients equal the ops called without any cached plan and the oracle."""
+
+    from relmo_amd import mp
+
+    ns = torch.ops.relm_mp
+    rng = np.random.default_rng(42)
+    num_keys, n, emb = 2000, 40_000, 32
+    dst_np = _zipf_keys(rng, num_keys, n)
+    if layout == "repeats":
+        flat_np, rows = rng.integers(0, n, n), n
+    else:
+        flat_np, rows = _injective_flat_src(rng, layout, n)
+    dst, flat_src = _t(dst_np), _t(flat_np)
+    g = _t(rng.standard_normal((num_keys, emb)).astype(np.float32))
+    for mode in (0, 1):
+        rel = _t((2.0 * rng.standard_normal((rows, emb))).astype(np.float32)).requires_grad_(True)
+        ns.plan_cache_clear()
+        out = mp.fanin_reduce(rel, flat_src, dst, num_keys, mode)
+        (cached,) = torch.autograd.grad(out, rel, g)
+        ns.plan_cache_clear()
+        if mode == 0:
+            fresh = ns.fanin_reduce_sum_backward(g, flat_src, dst, rows)
+        else:
+            fresh = ns.fanin_reduce_logsumexp_backward(g, rel.detach(), flat_src, dst, out.detach(), rows)
+        assert torch.equal(cached, fresh), mode
+        if mode == 0:
+            want = oracle.fanin_reduce_sum_backward(_np(g), flat_np, dst_np, rows)
+        else:
+            want = oracle.fanin_reduce_logsumexp_backward(_np(g), _np(rel.detach()), flat_np, dst_np,
+                                                          _np(out.detach()), rows)
+        np.testing.assert_allclose(_np(cached), want, rtol=1e-4, atol=1e-6)
+
+
 def test_facade_backward_reuses_forward_plan(mp_env) -> None:
     """Autograd through the facade with flat_src = arange: the backward finds the
     forward's plan in the cache; results equal those computed without it."""

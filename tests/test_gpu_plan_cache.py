@@ -119,10 +119,13 @@ def test_content_hit_for_new_tensors_and_handoff(mp_env) -> None:
         d = _delta(before, _stats())
         _log(f"content cache step {step}: {d}")
         # the forward's CSR plan: built once, then served by content; the
-        # backward gets it from the autograd function and builds an inverse
-        # plan (flat_src is a permutation), served by content after step 0
-        if step > 0:
-            assert d["hits"] == 2 and d["misses"] == 0 and d["entries"] == 0, d
+        # backward gets it from the autograd function and (flat_src is a
+        # permutation) builds the inverse map of flat_src from that plan's
+        # snapshot - kept with the plan, so no plan of its own is looked up
+        if step == 0:
+            assert d["misses"] == 1 and d["entries"] == 1, d
+        else:
+            assert d["hits"] == 1 and d["misses"] == 0 and d["entries"] == 0, d
         outs.append((out.detach(), grad))
     for out, grad in outs[1:]:
         assert torch.equal(out, outs[0][0]) and torch.equal(grad, outs[0][1])
