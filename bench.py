@@ -141,14 +141,24 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         out = mp.fanin_reduce(rel, flat_src, next(shifted), K, mode)
         torch.autograd.grad(out, rel, grad_out)
 
-    # The callers' layout (fused.py:183-190): message e is read from rel row
-    # flat_src[e], an injective map that is not the identity (a seeded
-    # permutation here).  Plans rebuilt every step: the forward's CSR plan,
-    # and in the backward an inverse plan of flat_src (k_inv_build) for
-    # k_lse_bwd_inv / k_gather_inv over it.
+    # flat_src injective but not the identity, plans rebuilt every step: the
+    # forward's CSR plan, and in the backward the inverse map of flat_src,
+    # built from the forward plan's int32 snapshot (k_inv_scatter,
+    # k_inv_verify), for k_lse_bwd_inv / k_gather_inv over it.
+    #  * the callers' layout (fused.py:183-190): edges grouped by (predicate,
+    #    argument position), atoms in order within a group, flat_src =
+    #    (atom + predicate offset) * max_arity + position - here arity-2
+    #    predicates, E / 2 atoms, flat_src[k * E/2 + a] = 2a + k;
+    #  * a seeded random permutation: the worst case for both index maps.
+    flat_callers = callers_flat_src(torch, E, 2, dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     flat_perm = torch.randperm(E, device=dev, generator=gen)
+
+    def step_callers():
+        ns.plan_cache_clear()
+        out = mp.fanin_reduce(rel, flat_callers, dst, K, mode)
+        torch.autograd.grad(out, rel, grad_out)
 
     def step_permuted():
         ns.plan_cache_clear()
@@ -158,8 +168,9 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
     sync = torch.cuda.synchronize
     t_step = timed(step_uncached, steps, warmup, sync)
     t_bwd_step = statistics.fmean(a.elapsed_time(b) for a, b in bwd_events[-steps:]) / 1e3
+    t_callers = timed(step_callers, steps, warmup, sync)
     t_perm = timed(step_permuted, steps, warmup, sync)
-    del flat_perm
+    del flat_perm, flat_callers
     t_cached = timed(step_cached, steps, warmup, sync)
     stats0 = ns.plan_cache_stats()
     t_same = timed(step_same_topology, steps, warmup, sync)
@@ -201,8 +212,10 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
         "ms_step_same_topology_new_tensors": t_same * 1e3,
         "gbs_step_same_topology_new_tensors": gbs(b_fwd + b_bwd, t_same),
         "content_hits_same_topology": content_hits,
-        "ms_step_permuted_flat_src": t_perm * 1e3, "gbs_step_permuted_flat_src": gbs(b_fwd + b_bwd, t_perm),
-        "frac_step_permuted_flat_src": gbs(b_fwd + b_bwd, t_perm) / PEAK_HBM_GBS,
+        "ms_step_callers_flat_src": t_callers * 1e3, "gbs_step_callers_flat_src": gbs(b_fwd + b_bwd, t_callers),
+        "frac_step_callers_flat_src": gbs(b_fwd + b_bwd, t_callers) / PEAK_HBM_GBS,
+        "ms_step_random_flat_src": t_perm * 1e3, "gbs_step_random_flat_src": gbs(b_fwd + b_bwd, t_perm),
+        "frac_step_random_flat_src": gbs(b_fwd + b_bwd, t_perm) / PEAK_HBM_GBS,
         "ms_step_new_topology_cache_kept": t_new * 1e3,
         "gbs_step_new_topology_cache_kept": gbs(b_fwd + b_bwd, t_new),
         "misses_new_topology": stats1[3] - stats0[3],
@@ -219,10 +232,20 @@ def bench_c2(torch, mp, capi, syn, steps: int, warmup: int, mode: int) -> dict:
     return res
 
 
+def callers_flat_src(torch, num_edges: int, arity: int, dev):
+    """flat_src of the fused relation layer (fused.py:183-190) for predicates
+    of one arity: edges grouped by argument position, atoms in order within a
+    position, flat_src = atom * arity + position."""
+
+    atoms = num_edges // arity
+    a = torch.arange(atoms, device=dev, dtype=torch.int64)
+    return torch.cat([a * arity + k for k in range(arity)])
+
+
 def bench_c2_permuted(torch, mp, syn, steps: int, warmup: int, mode: int) -> dict:
-    """C2 with the callers' flat_src layout only (a seeded permutation, plans
-    rebuilt every step): the workload of ``--only c2perm``, for kernel traces
-    of that step alone."""
+    """C2 with the callers' flat_src layout only (callers_flat_src, arity 2;
+    plans rebuilt every step): the workload of ``--only c2perm``, for kernel
+    traces of that step alone."""
 
     dev = torch.device("cuda", 0)
     d = syn.c2_fanin(dev)
@@ -230,9 +253,7 @@ def bench_c2_permuted(torch, mp, syn, steps: int, warmup: int, mode: int) -> dic
     E, D = rel.shape
     ns = torch.ops.relm_mp
     rel.requires_grad_(True)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(1)
-    flat_perm = torch.randperm(E, device=dev, generator=gen)
+    flat_perm = callers_flat_src(torch, E, 2, dev)
     if mode == 1:
         nbytes = syn.bytes_fanin_fwd(E, D, K) + syn.bytes_fanin_lse_bwd(E, D, K, E)
     else:

@@ -475,8 +475,7 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->max_degree = plan->num_hubs = plan->num_chunks = plan->num_multi_hubs = -1;
     plan->num_items = plan->num_short = -1;
     const SortZero zero = sort_zero_region(sc.sort, num_edges);
-    const SortZero kzero = key_index_zero_region(sc.key_index, key_bound);
-    RELM_HIP(launch_status_init(l.status, s, zero.p, zero.n, kzero.p, kzero.n), "relm_mp status init");
+    RELM_HIP(launch_status_init(l.status, s, zero.p, zero.n), "relm_mp status init");
     // The validation result is final after the first sort pass: publish it
     // to the host, then enqueue the rest of the build.
     int32_t status_gen = 0;

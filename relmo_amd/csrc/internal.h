@@ -133,9 +133,6 @@ hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, in
 // item_first and item_short have item_capacity + 1 entries
 // (item_capacity_for(num_keys)).
 size_t key_index_words(int64_t num_keys);
-// The words of the key-index scratch that must be zero when launch_key_index
-// starts (chunk sums added with atomics).
-SortZero key_index_zero_region(uint32_t* scratch, int64_t num_keys);
 int64_t item_capacity_for(int64_t num_keys);
 hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted, int64_t num_keys,
                             uint32_t* scratch, int32_t* hub_key, int32_t* hub_chunk_base,

@@ -211,6 +211,53 @@ __global__ __launch_bounds__(kThreads) void k_inv_verify(const int32_t* __restri
 
 // ---- scan ----------------------------------------------------------------
 
+// Exclusive scan of every row of a [gridDim.x, len] array in place (one
+// workgroup per row, kScanTile values per step with a running carry);
+// tot[row] receives the row's sum.
+__global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict__ data,
+                                                            int64_t len,
+                                                            uint32_t* __restrict__ tot) {
+    __shared__ uint32_t tile[kScanTile];
+    __shared__ uint32_t lds[kScanThreads / kWave];
+    uint32_t* row = data + static_cast<int64_t>(blockIdx.x) * len;
+    uint32_t carry = 0;
+    for (int64_t base = 0; base < len; base += kScanTile) {
+        uint32_t in[kScanItems];
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
+            in[i] = p < len ? row[p] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) tile[i * kScanThreads + threadIdx.x] = in[i];
+        __syncthreads();
+        uint32_t v[kScanItems];
+        uint32_t sum = 0;
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            v[i] = tile[threadIdx.x * kScanItems + i];
+            sum += v[i];
+        }
+        uint32_t total;
+        const uint32_t incl = block_inclusive_scan<kScanThreads>(sum, lds, total);
+        uint32_t run = incl - sum + carry;
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            tile[threadIdx.x * kScanItems + i] = run;
+            run += v[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kScanItems; ++i) {
+            const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
+            if (p < len) row[p] = tile[i * kScanThreads + threadIdx.x];
+        }
+        carry += total;
+        __syncthreads();  // tile is rewritten by the next step
+    }
+    if (threadIdx.x == 0) tot[blockIdx.x] = carry;
+}
+
 // Exclusive scan over tiles of tile-major digit counts: hist[t * kSortBins + d]
 // becomes the number of keys with digit d in the tiles before t; tot[d] the
 // count over all tiles.  Workgroup (g, c) covers digits [32g, 32g + 32) of the
@@ -603,8 +650,8 @@ __global__ __launch_bounds__(kThreads) void k_offsets_from_sorted(const uint32_t
 //  * k_key_stats: per workgroup of kThreads keys the number of hubs (segments
 //    longer than kHubThreshold), their chunks, the hubs of more than one chunk
 //    and the hub messages;
-//  * k_key_write (its workgroup's prefix of these four rows from the chunk
-//    sums k_key_stats adds them to and the counts of its chunk before it): every hub gets its slot in key order, its chunk range and the
+//  * these four rows are scanned (k_scan_rows);
+//  * k_key_write: every hub gets its slot in key order, its chunk range and the
 //    chunk -> hub map; with S[k] = short messages before key k (= offsets[k]
 //    minus the hub messages before k) and the walk weight W[k] = k + S[k], the
 //    walk items, short_off = S and the short-segment gather copy.
@@ -629,27 +676,12 @@ __device__ __forceinline__ KeyFlags key_flags(const int32_t* __restrict__ offset
     return f;
 }
 
-constexpr int kKeyRows = 4;  // rows with prefixes: hubs, chunks, multi-chunk hubs, hub messages;
+constexpr int kKeyRows = 4;  // scanned rows: hubs, chunks, multi-chunk hubs, hub messages;
                              // a fifth row holds each workgroup's longest segment
-static_assert(kThreads / kWave == kKeyRows, "one wave per prefixed row in k_key_write");
-// Workgroups per chunk of the key-index row sums: k_key_stats adds its counts
-// to its chunk's sums with atomics (zeroed before the build), so k_key_write
-// finds the counts before its workgroup from the chunk sums before its chunk
-// and the workgroups of its own chunk before it - no separate scan pass.
-constexpr int64_t kKeyChunk = 16;
-
-__device__ __forceinline__ int64_t key_chunks(int64_t nblk) { return (nblk + kKeyChunk - 1) / kKeyChunk; }
-
-__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
 
 __global__ __launch_bounds__(kThreads) void k_key_stats(const int32_t* __restrict__ offsets,
                                                         int64_t num_keys, int64_t nblk,
                                                         uint32_t* __restrict__ counts,
-                                                        uint32_t* __restrict__ chunk_sum,
                                                         DevStatus* __restrict__ st) {
     __shared__ uint32_t lds[kThreads / kWave];
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -668,49 +700,25 @@ __global__ __launch_bounds__(kThreads) void k_key_stats(const int32_t* __restric
     }
     if (lane_id() == 0) wmax[threadIdx.x / kWave] = m;
     __syncthreads();
-    if (threadIdx.x < kKeyRows) {
-        const int r = static_cast<int>(threadIdx.x);
-        const uint32_t v = r == 0 ? th : (r == 1 ? tc : (r == 2 ? tm : te));
-        counts[r * (nblk + 1) + blockIdx.x] = v;
-        if (v != 0u) atomicAdd(chunk_sum + r * key_chunks(nblk) + blockIdx.x / kKeyChunk, v);
-    }
     if (threadIdx.x == 0) {
         uint32_t mm = 0;
         for (int w = 0; w < kThreads / kWave; ++w) mm = wmax[w] > mm ? wmax[w] : mm;
-        counts[kKeyRows * (nblk + 1) + blockIdx.x] = mm;
+        const int64_t stride = nblk + 1;
+        counts[blockIdx.x] = th;
+        counts[stride + blockIdx.x] = tc;
+        counts[2 * stride + blockIdx.x] = tm;
+        counts[3 * stride + blockIdx.x] = te;
+        counts[4 * stride + blockIdx.x] = mm;
+        if (blockIdx.x == 0) {
+            for (int r = 0; r < kKeyRows; ++r) counts[r * stride + nblk] = 0;
+        }
     }
     (void)st;
 }
 
-// Row w's count before this workgroup (pre[w]) and over all workgroups
-// (tot[w]), computed by wave w from the chunk sums and the counts of the
-// workgroups of its chunk before it.
-__device__ __forceinline__ void key_block_prefix(const uint32_t* __restrict__ counts,
-                                                 const uint32_t* __restrict__ chunk_sum,
-                                                 int64_t nblk, uint32_t* pre, uint32_t* tot) {
-    const int w = static_cast<int>(threadIdx.x) / kWave;
-    const int l = lane_id();
-    const int64_t nkc = key_chunks(nblk);
-    const int64_t b = blockIdx.x;
-    const int64_t cb = b / kKeyChunk;
-    uint32_t p = 0, t = 0;
-    for (int64_t c = l; c < nkc; c += kWave) {
-        const uint32_t v = chunk_sum[w * nkc + c];
-        t += v;
-        p += c < cb ? v : 0u;
-    }
-    for (int64_t j = cb * kKeyChunk + l; j < b; j += kWave) p += counts[w * (nblk + 1) + j];
-    p = wave_sum(p);
-    t = wave_sum(t);
-    if (l == 0) {
-        pre[w] = p;
-        tot[w] = t;
-    }
-}
-
 __global__ __launch_bounds__(kThreads) void k_key_write(
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_keys,
-    int64_t nblk, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ chunk_sum,
+    int64_t nblk, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ totals,
     int32_t* __restrict__ hub_key, int32_t* __restrict__ hub_chunk_base,
     int32_t* __restrict__ multi_hubs, int32_t* __restrict__ chunk_hub, int64_t hub_capacity,
     int64_t chunk_capacity, int32_t* __restrict__ item_first, int32_t* __restrict__ item_short,
@@ -720,8 +728,6 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     __shared__ int32_t blk_slot[kThreads];
     __shared__ int64_t blk_cbase[kThreads];
     __shared__ uint32_t blk_chunks[kThreads];
-    __shared__ uint32_t pre[kKeyRows], totals[kKeyRows];
-    key_block_prefix(counts, chunk_sum, nblk, pre, totals);
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
     const KeyFlags f = key_flags(offsets, k, num_keys);
     uint32_t th, tc, tm, te;
@@ -763,8 +769,8 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     // hub slot, chunk range; the workgroup fills the chunk -> hub map of its
     // hubs together (a hub can have hundreds of chunks)
     if (f.hub) {
-        const int64_t slot = static_cast<int64_t>(pre[0]) + ih - 1;
-        const int64_t cbase = static_cast<int64_t>(pre[1]) + ic - f.chunks;
+        const int64_t slot = static_cast<int64_t>(counts[blockIdx.x]) + ih - 1;
+        const int64_t cbase = static_cast<int64_t>(counts[stride + blockIdx.x]) + ic - f.chunks;
         blk_slot[ih - 1] = static_cast<int32_t>(slot);
         blk_cbase[ih - 1] = cbase;
         blk_chunks[ih - 1] = f.chunks;
@@ -772,7 +778,7 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
             hub_key[slot] = static_cast<int32_t>(k);
             hub_chunk_base[slot] = static_cast<int32_t>(cbase);
             if (f.multi) {
-                const int64_t mslot = static_cast<int64_t>(pre[2]) + im - 1;
+                const int64_t mslot = static_cast<int64_t>(counts[2 * stride + blockIdx.x]) + im - 1;
                 if (mslot >= 0 && mslot < hub_capacity) multi_hubs[mslot] = static_cast<int32_t>(slot);
             }
         }
@@ -788,7 +794,7 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     }
     // S[k]: short messages before k; W[k] = k + S[k]
     const bool live = k <= num_keys;
-    const int64_t hub_before = static_cast<int64_t>(pre[3]) + ie - f.hub_edges;
+    const int64_t hub_before = static_cast<int64_t>(counts[3 * stride + blockIdx.x]) + ie - f.hub_edges;
     const int64_t S = live ? static_cast<int64_t>(offsets[k]) - hub_before : 0;
     if (live) {
         const int64_t W = k + S;
@@ -1002,14 +1008,7 @@ hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, in
 
 size_t key_index_words(int64_t num_keys) {
     const int64_t nblk = (num_keys + 1 + kThreads - 1) / kThreads;
-    const int64_t nkc = (nblk + kKeyChunk - 1) / kKeyChunk;
-    // chunk sums (zeroed before the build), then the per-workgroup rows
-    return static_cast<size_t>(kKeyRows * nkc + (kKeyRows + 1) * (nblk + 1) + 64);
-}
-
-SortZero key_index_zero_region(uint32_t* scratch, int64_t num_keys) {
-    const int64_t nblk = (num_keys + 1 + kThreads - 1) / kThreads;
-    return {scratch, kKeyRows * ((nblk + kKeyChunk - 1) / kKeyChunk)};
+    return static_cast<size_t>((kKeyRows + 1) * (nblk + 1) + 64);
 }
 
 int64_t item_capacity_for(int64_t num_keys) {
@@ -1023,15 +1022,19 @@ hipError_t launch_key_index(const int32_t* offsets, const int32_t* gather_sorted
                             int64_t item_capacity, int32_t* short_off, int32_t* short_gather,
                             relm_mp_plan_counts* pc, DevStatus* st, hipStream_t s) {
     const int64_t nblk = (num_keys + 1 + kThreads - 1) / kThreads;
-    uint32_t* chunk_sum = scratch;
-    uint32_t* counts = scratch + key_index_zero_region(scratch, num_keys).n;
+    uint32_t* counts = scratch;
+    uint32_t* totals = scratch + (kKeyRows + 1) * (nblk + 1);
     hipLaunchKernelGGL(k_key_stats, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
-                       num_keys, nblk, counts, chunk_sum, st);
+                       num_keys, nblk, counts, st);
     hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_scan_rows, dim3(kKeyRows), dim3(kScanThreads), 0, s, counts, nblk + 1,
+                       totals);
+    err = hipGetLastError();
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_key_write, dim3(static_cast<unsigned>(nblk)), dim3(kThreads), 0, s, offsets,
                        gather_sorted, num_keys, nblk, static_cast<const uint32_t*>(counts),
-                       static_cast<const uint32_t*>(chunk_sum), hub_key, hub_chunk_base, multi_hubs,
+                       static_cast<const uint32_t*>(totals), hub_key, hub_chunk_base, multi_hubs,
                        chunk_hub, hub_capacity, chunk_capacity, item_first, item_short,
                        item_capacity, short_off, short_gather, pc, st);
     return hipGetLastError();
