@@ -142,10 +142,14 @@ struct PlanRef : torch::CustomClassHolder {
     // (flat_src), built by the first backward that needs it
     // (relm_mp_plan_fanin_backward_by_src) and kept for later backward calls
     // on the same stream with the same row count; inv_rows < 0: none.
+    // inv_collide_rows: the row count for which flat_src was found not to be
+    // injective (the plan's indices do not change, so neither does that
+    // answer); later backward calls go straight to the inverse plan.
     std::mutex inv_mu;
     Tensor inv_mem;
     int64_t inv_rows = -1;
     hipStream_t inv_stream = nullptr;
+    int64_t inv_collide_rows = -1;
 
     PlanRef() = default;
     PlanRef(const PlanRef&) = delete;
@@ -709,6 +713,8 @@ bool backward_by_src(const PlanPtr& fwd, int64_t mode, const Tensor& g, const vo
         return false;
     PlanRef& ref = *fwd;
     std::lock_guard<std::mutex> lock(ref.inv_mu);
+    if (ref.inv_collide_rows == rows)
+        return false;
     const bool ready = ref.inv_rows == rows && ref.inv_stream == stream && ref.inv_mem.defined();
     Tensor mem = ready ? ref.inv_mem : byte_buffer(relm_mp_inv_plan_bytes(rows, fwd->plan.num_edges, 0), g);
     int64_t collisions = 0;
@@ -721,6 +727,8 @@ bool backward_by_src(const PlanPtr& fwd, int64_t mode, const Tensor& g, const vo
         ref.inv_rows = rows;
         ref.inv_stream = stream;
     }
+    if (collisions != 0)
+        ref.inv_collide_rows = rows;
     return collisions == 0;
 }
 

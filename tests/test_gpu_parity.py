@@ -633,7 +633,8 @@ def test_facade_backward_with_injective_flat_src(layout: str, mp_env) -> None:
     """Autograd through the facade with a flat_src that is not the identity:
     the backward runs over the forward's plan (inverse map from its snapshot)
     when flat_src is injective, and over its own CSR plan when it repeats; the
-    gradients equal the ops called without any cached plan and the oracle."""
+    gradients equal those of a second step over the cached plan, the ops
+    called without any cached plan, and the oracle."""
 
     from relmo_amd import mp
 
@@ -652,6 +653,11 @@ def test_facade_backward_with_injective_flat_src(layout: str, mp_env) -> None:
         ns.plan_cache_clear()
         out = mp.fanin_reduce(rel, flat_src, dst, num_keys, mode)
         (cached,) = torch.autograd.grad(out, rel, g)
+        # a second step over the cached forward plan: the inverse map kept
+        # with it (injective) or its recorded collision (repeats)
+        out2 = mp.fanin_reduce(rel, flat_src, dst, num_keys, mode)
+        (again,) = torch.autograd.grad(out2, rel, g)
+        assert torch.equal(again, cached), mode
         ns.plan_cache_clear()
         if mode == 0:
             fresh = ns.fanin_reduce_sum_backward(g, flat_src, dst, rows)
