@@ -323,25 +323,27 @@ __device__ __forceinline__ void store_tile_counts(uint32_t* __restrict__ hist,
 
 // Tile digit histogram in LDS: kSubHists copies per wave (lane & 3), so that
 // lanes holding the same digit - frequent for hub keys - rarely hit the same
-// address; plain LDS atomics, no cross-lane matching.
+// address; plain LDS atomics, no cross-lane matching.  The copies lie
+// kSortBins + 1 words apart, so one digit of different copies falls in
+// different banks.
 constexpr int kSubHists = 4;
+constexpr int kHistStride = kSortBins + 1;
+constexpr int kHistWords = (kSortThreads / kWave) * kSubHists * kHistStride;
 
 __device__ __forceinline__ void hist_clear(uint32_t* h) {
-    for (int i = static_cast<int>(threadIdx.x); i < (kSortThreads / kWave) * kSubHists * kSortBins;
-         i += kSortThreads)
-        h[i] = 0;
+    for (int i = static_cast<int>(threadIdx.x); i < kHistWords; i += kSortThreads) h[i] = 0;
 }
 
 __device__ __forceinline__ void hist_add(uint32_t* h, uint32_t d) {
     const int copy = (static_cast<int>(threadIdx.x) / kWave) * kSubHists + (lane_id() & (kSubHists - 1));
-    atomicAdd(&h[copy * kSortBins + d], 1u);
+    atomicAdd(&h[copy * kHistStride + d], 1u);
 }
 
 // Sum of the copies for digit threadIdx.x (call after a barrier).
 __device__ __forceinline__ uint32_t hist_total(const uint32_t* h) {
     uint32_t t = 0;
 #pragma unroll
-    for (int c = 0; c < (kSortThreads / kWave) * kSubHists; ++c) t += h[c * kSortBins + threadIdx.x];
+    for (int c = 0; c < (kSortThreads / kWave) * kSubHists; ++c) t += h[c * kHistStride + threadIdx.x];
     return t;
 }
 
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
     int bits, int64_t key_bound, int64_t gather_bound, uint32_t* __restrict__ keys32,
     uint32_t* __restrict__ vals32, uint32_t* __restrict__ tile_plain, uint32_t* __restrict__ hist,
     uint32_t* __restrict__ chunk_sum, int64_t nblocks, DevStatus* __restrict__ st) {
-    __shared__ uint32_t h[(kSortThreads / kWave) * kSubHists * kSortBins];
+    __shared__ uint32_t h[kHistWords];
     hist_clear(h);
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
     const uint32_t dmask = (1u << bits) - 1u;
@@ -524,7 +526,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     constexpr int kPerWave = kSortTile / kWaves;
     __shared__ uint32_t wcnt[kWaves][kSortBins];
     __shared__ uint32_t dstart[kSortBins];
-    __shared__ uint32_t gbase[kSortBins];
+    __shared__ int32_t gdelta[kSortBins];  // global start of the digit minus its tile start
     __shared__ uint32_t scan_lds[kSortThreads / kWave];
     __shared__ uint32_t sk[kSortTile];
     __shared__ uint32_t sv[kSortTile];
@@ -586,7 +588,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     // digit in the tiles before this one (this tile's row of hist_scanned)
     uint32_t all;
     const uint32_t dincl = block_inclusive_scan<kSortThreads>(dt, scan_lds, all);
-    gbase[dd] = (dincl - dt) + tile_prefix;
+    gdelta[dd] = static_cast<int32_t>((dincl - dt) + tile_prefix) - static_cast<int32_t>(incl - run);
     __syncthreads();
 
     const int64_t rem = n - tile_base;
@@ -607,7 +609,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     for (int i = static_cast<int>(threadIdx.x); i < count; i += kSortThreads) {
         const uint32_t k = sk[i];
         const uint32_t d = (k >> shift) & dmask;
-        const int64_t op = static_cast<int64_t>(gbase[d]) + (i - static_cast<int64_t>(dstart[d]));
+        const int64_t op = static_cast<int64_t>(gdelta[d]) + i;
         if (op >= 0 && op < n) {
             keys_out[op] = k;
             vals_out[op] = sv[i];
