@@ -455,10 +455,13 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
 }
 
 // Per-tile digit histogram of the narrowed keys, written tile-major:
-// hist[tile * kSortBins + d] (one contiguous row per tile).  Lanes holding the same digit are matched and the
-// lowest of them adds their number to the wave's own histogram, so runs of
-// one key (hub messages, already grouped by the earlier passes) cost one LDS
-// update per wave instead of a chain of conflicting atomics.
+// hist[tile * kSortBins + d] (one contiguous row per tile).  Counting ignores
+// the order: each lane adds its keys with LDS atomics to one of kCountCopies
+// copies per wave (lane & 7; copies one word apart in banks), and a wave whose
+// active lanes all hold one digit - the runs of one key that hubs form once
+// the earlier passes have grouped the keys - adds their number once.
+constexpr int kCountCopies = 8;
+
 template <int BITS>
 __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* __restrict__ keys,
                                                                 int64_t n, int shift,
@@ -466,13 +469,16 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
                                                                 uint32_t* __restrict__ chunk_sum,
                                                                 int64_t nblocks) {
     constexpr int kWaves = kSortThreads / kWave;
-    __shared__ uint32_t h[kWaves * kSortBins];
-    for (int i = static_cast<int>(threadIdx.x); i < kWaves * kSortBins; i += kSortThreads) h[i] = 0;
+    constexpr int kDigits = 1 << BITS;
+    constexpr int kStride = kDigits + 1;
+    constexpr int kWords = kWaves * kCountCopies * kStride;
+    __shared__ uint32_t h[kWords];
+    for (int i = static_cast<int>(threadIdx.x); i < kWords; i += kSortThreads) h[i] = 0;
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
     constexpr uint32_t dmask = (1u << BITS) - 1u;
-    // Counting ignores the order, so a full tile is read as 16-byte loads
-    // (thread t holds elements 4 * (j * 256 + t) + {0..3}); a partial tile
-    // element by element, with the elements past n inactive.
+    // A full tile is read as 16-byte loads (thread t holds elements
+    // 4 * (j * 256 + t) + {0..3}); a partial tile element by element, with the
+    // elements past n inactive.
     uint32_t key[kSortItems];
     int valid = kSortItems;
     if (base + kSortTile <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0) {
@@ -495,19 +501,29 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
         }
     }
     __syncthreads();
-    uint32_t* wh = h + (static_cast<int>(threadIdx.x) / kWave) * kSortBins;
+    uint32_t* wh = h + (static_cast<int>(threadIdx.x) / kWave) * kCountCopies * kStride;
+    uint32_t* mine = wh + (lane_id() & (kCountCopies - 1)) * kStride;
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         // partial tiles: thread t's valid elements are its first `valid`
         const bool active = i < valid;
         const uint32_t d = (key[i] >> shift) & dmask;
-        const unsigned long long peers = match_digit<BITS>(d, __ballot(active));
-        if (active && (peers & lanemask_lt()) == 0) wh[d] += static_cast<uint32_t>(__popcll(peers));
+        const unsigned long long act = __ballot(active);
+        if (act == 0ull) continue;  // uniform over the wave
+        const uint32_t d0 = static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(d), __builtin_ctzll(act)));
+        if (__ballot(active && d != d0) == 0ull) {
+            if (lane_id() == 0) atomicAdd(&wh[d0], static_cast<uint32_t>(__popcll(act)));
+        } else if (active) {
+            atomicAdd(&mine[d], 1u);
+        }
     }
     __syncthreads();
     uint32_t t = 0;
+    if (static_cast<int>(threadIdx.x) < kDigits) {
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) t += h[w * kSortBins + threadIdx.x];
+        for (int c = 0; c < kWaves * kCountCopies; ++c) t += h[c * kStride + threadIdx.x];
+    }
     store_tile_counts(hist, chunk_sum, t);
 }
 
