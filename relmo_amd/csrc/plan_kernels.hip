@@ -527,23 +527,29 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
     store_tile_counts(hist, chunk_sum, t);
 }
 
-// Stable scatter of one tile.  Wave w owns tile positions [w*1024, (w+1)*1024)
-// in 16 rounds of 64, so the order (wave, round, lane) is the edge order; each
-// key's rank is counted in that order, the tile is staged in LDS in digit order
-// and written out in runs per digit.  In the first pass a tile flagged in
-// tile_plain takes the edge ids as its values.
+// Stable scatter of one tile by kDownThreads threads (eight waves: more waves
+// per CU than the 39 KB of LDS per workgroup would give four-wave workgroups).
+// Wave w owns tile positions [w * kPerWave, (w + 1) * kPerWave) in rounds of
+// 64, so the order (wave, round, lane) is the edge order; each key's rank is
+// counted in that order, the tile is staged in LDS in digit order and written
+// out in runs per digit.  In the first pass a tile flagged in tile_plain takes
+// the edge ids as its values.  Threads below kSortBins also own one digit each.
+constexpr int kDownThreads = 512;
+constexpr int kDownItems = kSortTile / kDownThreads;
+static_assert(kDownThreads >= kSortBins, "one thread per digit");
+
 template <int BITS>
-__global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
+__global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
     const uint32_t* __restrict__ tile_plain, int64_t n, int shift,
     const uint32_t* __restrict__ hist_scanned, const uint32_t* __restrict__ digit_tot,
     int64_t nblocks, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
-    constexpr int kWaves = kSortThreads / kWave;
+    constexpr int kWaves = kDownThreads / kWave;
     constexpr int kPerWave = kSortTile / kWaves;
     __shared__ uint32_t wcnt[kWaves][kSortBins];
     __shared__ uint32_t dstart[kSortBins];
     __shared__ int32_t gdelta[kSortBins];  // global start of the digit minus its tile start
-    __shared__ uint32_t scan_lds[kSortThreads / kWave];
+    __shared__ uint32_t scan_lds[kDownThreads / kWave];
     __shared__ uint32_t sk[kSortTile];
     __shared__ uint32_t sv[kSortTile];
 
@@ -552,19 +558,23 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     const int64_t tile = xcd_tile(blockIdx.x, nblocks);
     const int64_t tile_base = tile * kSortTile;
     constexpr uint32_t dmask = (1u << BITS) - 1u;
+    const int dd = static_cast<int>(threadIdx.x);  // the digit of threads below kSortBins
+    const bool owns_digit = dd < kSortBins;
     // this tile's start within each digit does not depend on the keys: fetch
     // it together with them
-    const uint32_t tile_prefix = hist_scanned[tile * kSortBins + threadIdx.x];
-    const uint32_t dt = digit_tot[threadIdx.x];
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) wcnt[w][threadIdx.x] = 0;
+    uint32_t tile_prefix = 0, dt = 0;
+    if (owns_digit) {
+        tile_prefix = hist_scanned[tile * kSortBins + dd];
+        dt = digit_tot[dd];
+    }
+    for (int i = dd; i < kWaves * kSortBins; i += kDownThreads) (&wcnt[0][0])[i] = 0;
     __syncthreads();
 
-    uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+    uint32_t key[kDownItems], val[kDownItems], rank[kDownItems];
     const bool plain = tile_plain != nullptr && tile_plain[tile] != 0u;
     const int64_t wave_base = tile_base + wave * kPerWave + lane;
 #pragma unroll
-    for (int r = 0; r < kSortItems; ++r) {
+    for (int r = 0; r < kDownItems; ++r) {
         const int64_t p = wave_base + r * kWave;
         uint32_t k = 0, v = 0;
         if (p < n) {
@@ -575,7 +585,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
         val[r] = v;
     }
 #pragma unroll
-    for (int r = 0; r < kSortItems; ++r) {
+    for (int r = 0; r < kDownItems; ++r) {
         const bool active = wave_base + r * kWave < n;
         const uint32_t d = (key[r] >> shift) & dmask;
         const unsigned long long peers = match_digit<BITS>(d, __ballot(active));
@@ -589,28 +599,31 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
     __syncthreads();
 
     // Per digit (one thread per digit): exclusive prefix over waves, tile total.
-    const int dd = static_cast<int>(threadIdx.x);
     uint32_t run = 0;
+    if (owns_digit) {
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        const uint32_t c = wcnt[w][dd];
-        wcnt[w][dd] = run;
-        run += c;
+        for (int w = 0; w < kWaves; ++w) {
+            const uint32_t c = wcnt[w][dd];
+            wcnt[w][dd] = run;
+            run += c;
+        }
     }
     uint32_t total;
-    const uint32_t incl = block_inclusive_scan<kSortThreads>(run, scan_lds, total);
-    dstart[dd] = incl - run;
+    const uint32_t incl = block_inclusive_scan<kDownThreads>(run, scan_lds, total);
     // global start of digit dd: all smaller digits of every tile, then this
     // digit in the tiles before this one (this tile's row of hist_scanned)
     uint32_t all;
-    const uint32_t dincl = block_inclusive_scan<kSortThreads>(dt, scan_lds, all);
-    gdelta[dd] = static_cast<int32_t>((dincl - dt) + tile_prefix) - static_cast<int32_t>(incl - run);
+    const uint32_t dincl = block_inclusive_scan<kDownThreads>(dt, scan_lds, all);
+    if (owns_digit) {
+        dstart[dd] = incl - run;
+        gdelta[dd] = static_cast<int32_t>((dincl - dt) + tile_prefix) - static_cast<int32_t>(incl - run);
+    }
     __syncthreads();
 
     const int64_t rem = n - tile_base;
     const int count = rem < kSortTile ? static_cast<int>(rem) : kSortTile;
 #pragma unroll
-    for (int r = 0; r < kSortItems; ++r) {
+    for (int r = 0; r < kDownItems; ++r) {
         const int local = wave * kPerWave + r * kWave + lane;
         if (local < count) {
             const uint32_t d = (key[r] >> shift) & dmask;
@@ -622,7 +635,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_downsweep(
         }
     }
     __syncthreads();
-    for (int i = static_cast<int>(threadIdx.x); i < count; i += kSortThreads) {
+    for (int i = static_cast<int>(threadIdx.x); i < count; i += kDownThreads) {
         const uint32_t k = sk[i];
         const uint32_t d = (k >> shift) & dmask;
         const int64_t op = static_cast<int64_t>(gdelta[d]) + i;
@@ -992,7 +1005,8 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         if (err != hipSuccess) return err;
         const uint32_t* plain = p == 0 ? static_cast<const uint32_t*>(buf.tile_plain) : nullptr;
         with_digit_bits(width, [&](auto bt) {
-            hipLaunchKernelGGL((k_radix_downsweep<decltype(bt)::value>), grid, block, 0, s, in_k, in_v,
+            hipLaunchKernelGGL((k_radix_downsweep<decltype(bt)::value>), grid, dim3(kDownThreads), 0, s,
+                               in_k, in_v,
                                plain, n, shift, static_cast<const uint32_t*>(buf.hist),
                                static_cast<const uint32_t*>(digit_tot), nblocks, out_k, out_v);
         });
