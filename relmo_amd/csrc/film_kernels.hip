@@ -33,25 +33,39 @@ struct FilmRanges {
     int num;
 };
 
-// Mish and its derivative through n = e^u (e^u + 2): tanh(softplus(u)) =
-// n / (n + 2), and d/du [u tanh(softplus(u))] = n / (n + 2) + 4 u e^u (1 +
-// e^u) / (n + 2)^2.  Above u = 20, tanh(softplus(u)) is 1 in fp32.  The
-// accurate expf and an IEEE division (the kernels are bound by memory): the
-// per-predicate sums of the backward add tens of thousands of these terms,
-// where the bias of approximate ones would show.
+// Mish and its derivative in the fp32 formulation of PyTorch's own Mish
+// kernels (torch.nn.functional.mish and its backward on ROCm):
+//   mish(u)         = u * tanh(log1p(exp(u)))
+//   dy * mish'(u)   = dy * (t + u * sigmoid(u) * (1 - t * t)),  t = tanh(log1p(exp(u))),
+// with the two multiply-adds of the derivative fused as torch's build fuses
+// them, the accurate expf / log1pf / tanhf and IEEE division.  Together with
+// the affine step b + g * (s + a) rounded as torch's addcmul rounds it, the
+// fused step computes exactly what torch's FiLM and Mish ops compute, bit for
+// bit (checked against them on the GPU).  The weight gradient of the Linear
+// before the FiLM step is a sum over all rows with large cancellation; its
+// rounding error moves by a factor of three with the last bit of a few rows'
+// gradients, so a different (even more accurate) formulation leaves the
+// models' gradients at a different fp32 error than the torch lane's.
+// At u >= 10 that formulation has t = 1 exactly (log1p(exp(u)) > 10, whose
+// tanh rounds to 1), so mish(u) = u and the gradient is dy; at u <= -104
+// exp(u) is 0 in fp32, so t = 0: mish(u) = u * 0 and the gradient dy * +0.  The shortcuts
+// skip the transcendental calls there and give the same bits (tested over
+// dense sweeps of both ranges against torch).
+constexpr float kMishOne = 10.0f;
+constexpr float kMishZero = -104.0f;
+
 __device__ __forceinline__ float mish(float u) {
-    if (u > 20.0f) return u;
-    const float e = expf(u);
-    const float n = e * (e + 2.0f);
-    return u * n / (n + 2.0f);
+    if (u >= kMishOne) return u;
+    if (u <= kMishZero) return u * 0.0f;
+    return u * tanhf(log1pf(expf(u)));
 }
 
-__device__ __forceinline__ float mish_grad(float u) {
-    if (u > 20.0f) return 1.0f;
-    const float e = expf(u);
-    const float n = e * (e + 2.0f);
-    const float r = 1.0f / (n + 2.0f);
-    return n * r + 4.0f * u * e * (1.0f + e) * r * r;
+__device__ __forceinline__ float mish_backward(float dy, float u) {
+    if (u >= kMishOne) return dy;
+    if (u <= kMishZero) return dy * 0.0f;  // fma(u * 0, 1, 0) = +0 in the full formula
+    const float sg = 1.0f / (1.0f + expf(-u));
+    const float t = tanhf(log1pf(expf(u)));
+    return dy * fmaf(u * sg, fmaf(-t, t, 1.0f), t);
 }
 
 template <int V>
@@ -163,7 +177,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_film_mish_backward(
 #pragma unroll
             for (int i = 0; i < V; ++i) {
                 const float tt = x.v[i] + a.v[i];
-                const float du = d.v[i] * mish_grad(b.v[i] + g.v[i] * tt);
+                const float du = mish_backward(d.v[i], b.v[i] + g.v[i] * tt);
                 o.v[i] = du * g.v[i];
                 sum_t[i] += static_cast<double>(du * tt);
                 sum_u[i] += static_cast<double>(du);

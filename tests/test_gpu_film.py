@@ -1,6 +1,6 @@
 """GPU tests of the fused FiLM step with Mish (torch.ops.relm_mp.film_mish and
 its backward; C ABI relm_mp_film_mish*): against the same function in float64
-through torch autograd."""
+through torch autograd, and bit for bit against torch's own fp32 ops."""
 
 from __future__ import annotations
 
@@ -75,6 +75,16 @@ def test_film_mish_against_float64(width, starts, with_add) -> None:
     if with_add:
         torch.testing.assert_close((gamma * db).double(), grads[3], rtol=1e-5, atol=1e-4)
 
+    # bit for bit what torch's own ops give in fp32 (addcmul, then Mish, per
+    # range, and autograd through them): the kernel uses their formulation
+    sl = s.clone().requires_grad_(True)
+    parts = [torch.nn.functional.mish(torch.addcmul(beta[r], gamma[r], v + add[r] if with_add else v))
+             for r, v in enumerate(torch.split(sl, [starts[r + 1] - starts[r] for r in range(k)]))]
+    y32 = torch.cat(parts)
+    (ds32,) = torch.autograd.grad(y32, sl, dy)
+    assert torch.equal(y, y32.detach())
+    assert torch.equal(ds, ds32)
+
     # the C ABI gives the same bits as the torch op
     assert torch.equal(capi.film_mish(s, starts, gamma, beta, add), y)
     ds2, partial = capi.film_mish_backward(dy, s, starts, gamma, beta, add)
@@ -86,6 +96,39 @@ def test_film_mish_against_float64(width, starts, with_add) -> None:
             assert partial.dtype == torch.float64
             assert torch.equal(partial[b0:b0 + nb, 1].sum(0).float(), db[r])
         b0 += nb
+
+
+@pytest.mark.parametrize("lo_bits,hi_bits,step", [
+    (0x41000000, 0x7F800000, 97),    # [8, inf): the saturated side (mish(u) = u from u = 10 on)
+    (0xC2A00000, 0xC3800000, 5),     # [-256, -80]: exp(u) denormal, then 0 (from u = -104 on)
+    (0xC0000000, 0xC2A00000, 41),    # [-80, -2]
+    (0x00000000, 0x41000000, 401),   # [0, 8)
+])
+def test_film_mish_bitwise_against_torch_over_float_ranges(lo_bits: int, hi_bits: int, step: int) -> None:
+    """Mish and its gradient on sweeps of fp32 values (every step-th bit
+    pattern of the range, with its ends and the infinities): the fused kernels
+    give torch's own fp32 results bit for bit, including past the thresholds
+    where they skip the transcendental calls."""
+
+    ops = torch.ops.relm_mp
+    bits = torch.arange(lo_bits, hi_bits, step, dtype=torch.int64, device=DEV)
+    bits = torch.cat([bits, torch.tensor([lo_bits, hi_bits - 1], device=DEV)])
+    u = bits.to(torch.int32).view(torch.float32)
+    u = torch.cat([u, torch.tensor([float("inf"), -float("inf")], device=DEV)])
+    n = u.numel() // 64 * 64
+    u = u[:n].view(-1, 64).contiguous()
+    one = torch.ones(1, 64, device=DEV)
+    zero = torch.zeros(1, 64, device=DEV)
+    dy = torch.randn(u.shape, device=DEV, generator=torch.Generator(device=DEV).manual_seed(7))
+    y = ops.film_mish(u, [0, u.size(0)], one, zero, None)
+    ds, _, _ = ops.film_mish_backward(dy, u, [0, u.size(0)], one, zero, None)
+    x = u.clone().requires_grad_(True)
+    y32 = torch.nn.functional.mish(torch.addcmul(zero[0], one[0], x))
+    (ds32,) = torch.autograd.grad(y32, x, dy)
+    same = (y == y32.detach()) | (torch.isnan(y) & torch.isnan(y32.detach()))
+    assert bool(same.all()), u[~same][:8].tolist()
+    same = (ds == ds32) | (torch.isnan(ds) & torch.isnan(ds32))
+    assert bool(same.all()), u[~same][:8].tolist()
 
 
 def test_film_mish_extremes_and_errors() -> None:
