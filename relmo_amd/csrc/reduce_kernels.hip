@@ -361,6 +361,28 @@ struct LseBwdOp {
 // ---- epilogues: applied to each key's result as it is stored ----------------
 
 // Stores the result as is.
+// Minimum waves per SIMD asked of the compiler for the walker and the hub
+// chunks (HIP's second launch bound), which caps their VGPRs: the fp32 sum and
+// logsumexp over dense rows fit 96 VGPRs in the walker (5 waves instead of 4 at
+// 116) and 80 in the hub chunks (6 instead of 5 at 93) without spilling; the
+// other ops (fp64, grouped rows, the logsumexp backward) would spill, and keep
+// the compiler's choice.
+template <class Op>
+struct WaveFloor {
+    static constexpr int walk = 1;
+    static constexpr int hub = 1;
+};
+template <int V, int U>
+struct WaveFloor<SumOp<float, V, U, DenseRows>> {
+    static constexpr int walk = 5;
+    static constexpr int hub = 6;
+};
+template <int V, int U>
+struct WaveFloor<LseOp<float, V, U>> {
+    static constexpr int walk = 5;
+    static constexpr int hub = 6;
+};
+
 struct NoEpilogue {
     template <typename T, int V>
     __device__ __forceinline__ Pack<T, V> operator()(int64_t, const Pack<T, V>& v, int64_t,
@@ -435,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void k_fill(T* __restrict__ p, int64_t n,
 // whose label differs from the next one stores its key's result - no
 // per-key loop, so the row groups of a wave stay in step.
 template <typename T, int V, int G, class Op, class Epi>
-__global__ __launch_bounds__(kThreads) void k_walk_items(
+__global__ __launch_bounds__(kThreads, WaveFloor<Op>::walk) void k_walk_items(
     const int32_t* __restrict__ short_off, const int32_t* __restrict__ short_gather_in,
     const int32_t* __restrict__ gather_sorted, const int32_t* __restrict__ item_first,
     const int32_t* __restrict__ item_short, const relm_mp_plan_counts* __restrict__ pc,
@@ -648,7 +670,7 @@ __device__ __forceinline__ int hub_slot(int p) { return p + (p >> 5); }
 // LDS with coalesced loads, row group g folds slice g of the chunk, the
 // slices are folded in order by group 0; a single-chunk hub is finished here.
 template <typename T, int V, int G, class Op, class Epi>
-__global__ __launch_bounds__(kThreads) void k_hub_chunks(
+__global__ __launch_bounds__(kThreads, WaveFloor<Op>::hub) void k_hub_chunks(
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ gs, int64_t num_edges,
     const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
     const int32_t* __restrict__ chunk_hub, const relm_mp_plan_counts* __restrict__ pc,
