@@ -15,6 +15,7 @@ import os
 import shlex
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent.parent
@@ -63,13 +64,15 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 def build_hip_lib(verbose: bool = False) -> Path:
     hipcc = str(ROCM / "bin" / "hipcc")
-    objs = []
     obj_dir = PKG_DIR / "_build"
     obj_dir.mkdir(exist_ok=True)
-    for src in HIP_SOURCES:
-        obj = obj_dir / (Path(src).stem + ".o")
-        _run([hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)], verbose)
-        objs.append(str(obj))
+    objs = [str(obj_dir / (Path(src).stem + ".o")) for src in HIP_SOURCES]
+    # one hipcc per source, run side by side (each is single-threaded)
+    jobs = max(1, min(len(HIP_SOURCES), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(lambda so: _run([hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+                                       str(CSRC / so[0]), "-o", so[1]], verbose),
+                      zip(HIP_SOURCES, objs)))
     tmp = HIP_LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-Wl,-soname,librelm_mp_hip.so", "-o", str(tmp)], verbose)
     os.replace(tmp, HIP_LIB)
