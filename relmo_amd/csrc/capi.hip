@@ -322,8 +322,6 @@ CsrScratch csr_scratch(void* mem, int64_t num_keys, int64_t num_edges) {
     const size_t n = static_cast<size_t>(num_edges);
     l.sort.keys_a = c.take<uint32_t>(n);
     l.sort.vals_a = c.take<uint32_t>(n);
-    l.sort.keys_b = c.take<uint32_t>(n);
-    l.sort.vals_b = c.take<uint32_t>(n);
     const size_t hist = sort_hist_words(num_edges);
     l.sort.hist = c.take<uint32_t>(hist);
     l.sort.keys_n = l.sort.vals_n = l.sort.tile_plain = nullptr;  // in the plan (csr_layout)

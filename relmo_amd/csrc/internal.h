@@ -95,15 +95,14 @@ hipError_t launch_inv_from_snapshot(const int32_t* snap, const uint32_t* plain, 
 // caller's int64 keys / gathers, validates them against the bounds (bad
 // entries are recorded in `st` and replaced by 0) and narrows them to 32 bit
 // into keys_n / vals_n in edge order (a plan keeps these as its snapshot);
-// the scatter passes ping-pong between the a and b buffers.
+// the scatter passes alternate between the a buffers and the output arrays
+// (the last pass writes the output).
 struct SortBuffers {
     uint32_t* keys_n;
     uint32_t* vals_n;
     uint32_t* tile_plain;  // sort_tiles(n): tiles whose values are the edge ids (vals_n not written)
     uint32_t* keys_a;
     uint32_t* vals_a;
-    uint32_t* keys_b;
-    uint32_t* vals_b;
     uint32_t* hist;        // sort_hist_words(n): per-tile digit counts, digit totals
 };
 int64_t sort_tiles(int64_t n);

@@ -970,16 +970,19 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
     const int64_t col_chunks = (nblocks + kColChunk - 1) / kColChunk;
     // per pass: the chunk sums (zeroed by launch_status_init; a single chunk
     // has no chunks before it and needs none)
-    // the narrowed input goes to the n buffers (the plan's snapshot); pass p
-    // writes a, b, a, ... and the last pass the plan arrays
+    // The narrowed input goes to the n buffers (the plan's snapshot).  Counted
+    // back from the last pass, which writes the plan arrays, the passes write
+    // a and the plan arrays in turn: an earlier pass's output in the plan
+    // arrays is overwritten two passes later, often while its lines are still
+    // in the memory-side cache, so they need not all be written back to HBM.
     const uint32_t* in_k = buf.keys_n;
     const uint32_t* in_v = buf.vals_n;
     int shift = 0;
     for (int p = 0; p < passes; ++p) {
         const int width = bits / passes + (p < bits % passes ? 1 : 0);
-        const bool last = p == passes - 1;
-        uint32_t* out_k = last ? keys_out : (p % 2 == 0 ? buf.keys_a : buf.keys_b);
-        uint32_t* out_v = last ? vals_out : (p % 2 == 0 ? buf.vals_a : buf.vals_b);
+        const bool to_plan = (passes - 1 - p) % 2 == 0;
+        uint32_t* out_k = to_plan ? keys_out : buf.keys_a;
+        uint32_t* out_v = to_plan ? vals_out : buf.vals_a;
         const dim3 grid(static_cast<unsigned>(nblocks)), block(kSortThreads);
         uint32_t* chunk_sum = col_chunks > 1 ? digit_tot + kSortBins + p * col_chunks * kSortBins : nullptr;
         if (p == 0) {
