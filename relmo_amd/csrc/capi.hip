@@ -917,7 +917,10 @@ int relm_mp_plan_fanin_backward_by_src(int dtype, const relm_mp_plan* dst_plan, 
     RELM_TRY(host_slot(&hs));
     RELM_TRY(no_pending(hs));
     RELM_HIP(launch_status_init(l.status, s), "relm_mp status init");
-    RELM_HIP(launch_fill_i32(l.inv, rel_rows, -1, s), "relm_mp fill");
+    // With as many rows as edges every entry of an injective map is written
+    // (and a map that is not injective is not used), and the check reads only
+    // entries that some edge of this call wrote: no initial fill.
+    if (rel_rows != fwd.num_edges) RELM_HIP(launch_fill_i32(l.inv, rel_rows, -1, s), "relm_mp fill");
     RELM_HIP(launch_inv_from_snapshot(fwd.snap_gathers, fwd.snap_gather_plain, fwd.num_edges, rel_rows,
                                       l.inv, l.status, s),
              "relm_mp inverse map kernels");

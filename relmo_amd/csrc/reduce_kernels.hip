@@ -1078,6 +1078,73 @@ __global__ __launch_bounds__(kThreads) void k_lse_bwd_inv(
     }
 }
 
+// Sum backward of fanin_reduce in edge order when the message rows are a
+// permutation of the edges (flat_src injective and rel_rows == num_edges, as a
+// count of the inverse map's lost edges - zero - has shown on the device):
+// edge e writes its own message row rows(e) whole, grad_rel[rows(e)] =
+// grad_out[dsts(e)], so no inverse map is read.  Both index arrays are a
+// forward plan's int32 snapshots; all loads of an iteration are issued without
+// a branch (an out-of-range index reads row 0 and stores nothing: the kernel
+// runs with at least one edge and one destination row).
+struct EdgeRow {
+    int64_t row;  // message row, or 0
+    int64_t d;    // destination row, or 0
+    bool ok;
+};
+
+template <int RU>
+__device__ __forceinline__ void edge_rows(EdgeRow (&r)[RU], int64_t e0, int64_t stride,
+                                          int64_t num_edges, const GathersSnap& rows,
+                                          int64_t num_rows, const GathersSnap& dsts,
+                                          int64_t num_dst) {
+    GathersSnap::Raw rr[RU], dr[RU];
+    int64_t e[RU];
+#pragma unroll
+    for (int j = 0; j < RU; ++j) {
+        e[j] = e0 + j * stride;
+        const int64_t ec = e[j] < num_edges ? e[j] : 0;
+        rr[j] = rows.fetch(ec);
+        dr[j] = dsts.fetch(ec);
+    }
+#pragma unroll
+    for (int j = 0; j < RU; ++j) {
+        const int64_t ec = e[j] < num_edges ? e[j] : 0;
+        const int64_t row = rows.value(ec, rr[j]);
+        const int64_t d = dsts.value(ec, dr[j]);
+        r[j].ok = e[j] < num_edges && static_cast<uint64_t>(row) < static_cast<uint64_t>(num_rows) &&
+                  static_cast<uint64_t>(d) < static_cast<uint64_t>(num_dst);
+        r[j].row = r[j].ok ? row : 0;
+        r[j].d = r[j].ok ? d : 0;
+    }
+}
+
+template <typename T, int V, int G>
+__global__ __launch_bounds__(kThreads) void k_gather_edges(const relm_mp_plan_counts* __restrict__ pc,
+                                                           int64_t num_edges, GathersSnap rows,
+                                                           int64_t num_rows, GathersSnap dsts,
+                                                           int64_t num_dst, const T* __restrict__ table,
+                                                           int64_t D, T* __restrict__ out) {
+    constexpr int R = kThreads / G;
+    constexpr int RU = gather_rows_in_flight<T, V>();
+    if (pc->collisions != 0) return;  // not a permutation: the caller takes another path
+    const int gl = static_cast<int>(threadIdx.x) & (G - 1);
+    const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
+    if (col >= D) return;
+    const int64_t chunk = static_cast<int64_t>(R) * RU;
+    const int64_t grp = threadIdx.x / G;
+    for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk + grp; e0 < num_edges;
+         e0 += static_cast<int64_t>(gridDim.x) * chunk) {
+        EdgeRow r[RU];
+        edge_rows<RU>(r, e0, R, num_edges, rows, num_rows, dsts, num_dst);
+        Pack<T, V> v[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) v[j] = pack_load<T, V>(table + row_offset(r[j].d, D) + col);
+#pragma unroll
+        for (int j = 0; j < RU; ++j)
+            if (r[j].ok) pack_store_stream<T, V>(out + row_offset(r[j].row, D) + col, v[j]);
+    }
+}
+
 // ---- host-side dispatch --------------------------------------------------
 
 struct Geometry {
@@ -1547,6 +1614,27 @@ int compute_logsumexp_backward(int dtype, const relm_mp_plan& plan, const int64_
                : lse_backward_t<float>(plan, gathers, grad_out, out, rel_flat, emb, grad_rel, scratch, s);
 }
 
+// The edge-order sum backward over a forward plan's snapshots
+// (k_gather_edges); `counts` carries the inverse map's lost-edge count.
+template <typename T>
+int sum_backward_edges_t(const relm_mp_plan& fwd, const relm_mp_plan_counts* counts,
+                         const void* grad_out_v, int64_t emb, void* grad_rel_v, hipStream_t s) {
+    const T* grad_out = static_cast<const T*>(grad_out_v);
+    T* grad_rel = static_cast<T*>(grad_rel_v);
+    const int64_t E = fwd.num_edges;
+    const GathersSnap rows{fwd.snap_gathers, fwd.snap_gather_plain};
+    const GathersSnap dsts{fwd.snap_keys, fwd.snap_key_plain};
+    const Geometry geo = choose_geometry<T>(emb, {grad_out, grad_rel});
+    return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
+        constexpr int V = decltype(vt)::value;
+        constexpr int G = decltype(gt)::value;
+        hipLaunchKernelGGL((k_gather_edges<T, V, G>), row_grid(E, G, geo.slices, gather_rows_in_flight<T, V>()),
+                           dim3(kThreads), 0, s, counts, E, rows, E, dsts, fwd.num_keys, grad_out, emb,
+                           grad_rel);
+        return hip_error(hipGetLastError(), "relm_mp edge-order sum backward kernel");
+    });
+}
+
 int compute_backward_by_src(int dtype, const relm_mp_plan& dst_plan, const relm_mp_plan& inv_plan,
                             int64_t mode, const void* grad_out, const void* out,
                             const void* rel_flat, int64_t emb, void* grad_rel, hipStream_t s) {
@@ -1554,8 +1642,16 @@ int compute_backward_by_src(int dtype, const relm_mp_plan& dst_plan, const relm_
     if (mode != RELM_MP_MODE_SUM && mode != RELM_MP_MODE_LOGSUMEXP)
         return set_error(RELM_MP_ERR_UNSUPPORTED_MODE,
                          "Unsupported fanin_reduce mode. Supported: 0=sum, 1=logsumexp.");
-    // rows in order through the inverse map; each row's destination from the
-    // forward plan's int32 snapshot of dst_idx
+    // Rows in order through the inverse map, each row's destination from the
+    // forward plan's int32 snapshot of dst_idx.  The sum backward with as many
+    // message rows as edges (a flat_src without repeats - the device skips the
+    // kernel otherwise - is then a permutation) runs in edge order instead, each
+    // edge writing its own row whole, with no map to read: C2 in the callers'
+    // layout 1.486 against 1.515 ms per step.  The logsumexp backward, which
+    // also reads every message row, keeps the rows in order: in edge order the
+    // callers' layout reads and writes every other row per sweep (1.802
+    // against 1.777 ms).
+    const bool by_edges = mode == RELM_MP_MODE_SUM && inv_plan.num_keys == dst_plan.num_edges;
     const relm_mp_plan* snap = &dst_plan;
     if (mode == RELM_MP_MODE_SUM) {
         // as the edge-order sum backward: grad_out and the destinations read
@@ -1574,6 +1670,10 @@ int compute_backward_by_src(int dtype, const relm_mp_plan& dst_plan, const relm_
             const int rc = hip_error(hipGetLastError(), "relm_mp prefetch kernel");
             if (rc != RELM_MP_OK) return rc;
         }
+        if (by_edges)
+            return dtype == RELM_MP_F64
+                       ? sum_backward_edges_t<double>(dst_plan, inv_plan.counts, grad_out, emb, grad_rel, s)
+                       : sum_backward_edges_t<float>(dst_plan, inv_plan.counts, grad_out, emb, grad_rel, s);
         return dtype == RELM_MP_F64
                    ? gather_last_t<double>(inv_plan, nullptr, grad_out, emb, grad_rel, 0, 0, s, snap, true)
                    : gather_last_t<float>(inv_plan, nullptr, grad_out, emb, grad_rel, 0, 0, s, snap, true);

@@ -574,9 +574,10 @@ def test_backward_by_dst_with_plain_snapshot_tiles() -> None:
 def _injective_flat_src(rng, layout: str, n: int):
     """(flat_src, rel_rows) of n edges, injective and not the identity."""
 
-    if layout == "callers":  # fused.py:183-190 for arity-2 predicates: position-major, flat = 2 atom + pos
+    if layout in ("callers", "callers_full"):  # fused.py:183-190, arity 2: position-major, flat = 2 atom + pos
         a = np.arange(n // 2)
-        return np.concatenate([2 * a, 2 * a + 1]), n + 17
+        # "callers_full": as many message rows as edges (a permutation: no map fill, edge-order sum)
+        return np.concatenate([2 * a, 2 * a + 1]), n + (17 if layout == "callers" else 0)
     if layout == "gaps":  # arity 2 in a max-arity-3 row layout: every third row has no edge
         a = np.arange(n // 2)
         return np.concatenate([3 * a, 3 * a + 1]), 3 * (n // 2)
@@ -585,17 +586,19 @@ def _injective_flat_src(rng, layout: str, n: int):
         f[4096:2 * 4096] = f[4096:2 * 4096][rng.permutation(4096)]
         f[-50:] = f[-50:][::-1]
         return f, n
-    return rng.permutation(n), n + 17
+    return rng.permutation(n), n + (17 if layout == "random" else 0)
 
 
-@pytest.mark.parametrize("layout", ["callers", "gaps", "partly_plain", "random"])
+@pytest.mark.parametrize("layout", ["callers", "callers_full", "gaps", "partly_plain", "random", "random_full"])
 @pytest.mark.parametrize("emb", [6, 32, 64])
 def test_backward_by_src_over_the_forward_plan(layout: str, emb: int) -> None:
     """flat_src injective but not the identity: the fanin backward builds the
     inverse map of flat_src from the forward plan's snapshot, without atomics,
     reports no collision, and equals the oracle (sum: exact copies) and the
-    inverse-plan lane bit for bit; rows that no edge reads are zero.  A
-    flat_src that repeats an index reports collisions."""
+    inverse-plan lane bit for bit; rows that no edge reads are zero.  With as
+    many rows as edges the map is built without its initial fill, and the sum
+    runs in edge order over the snapshots.  A flat_src that repeats an index
+    reports collisions."""
 
     from relmo_amd import capi
 
@@ -628,7 +631,7 @@ def test_backward_by_src_over_the_forward_plan(layout: str, emb: int) -> None:
     assert coll > 0
 
 
-@pytest.mark.parametrize("layout", ["callers", "random", "repeats"])
+@pytest.mark.parametrize("layout", ["callers", "callers_full", "random", "random_full", "repeats"])
 def test_facade_backward_with_injective_flat_src(layout: str, mp_env) -> None:
     """Autograd through the facade with a flat_src that is not the identity:
     the backward runs over the forward's plan (inverse map from its snapshot)
