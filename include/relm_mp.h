@@ -335,7 +335,10 @@ int relm_mp_plan_fanin_backward_by_dst(int dtype, const relm_mp_plan* dst_plan,
  * dst_plan->num_edges, 0) bytes.  map_ready != 0: inv_mem already holds the
  * map an earlier call built for this dst_plan and rel_rows with no collision
  * (that call's work on `stream` precedes this one); only the backward kernel is
- * launched, without waiting, and *collisions is 0.  No reference counterpart:
+ * launched, without waiting, and *collisions is 0.  With rel_rows ==
+ * num_edges the map is built without an initial fill (an injective flat_src
+ * writes every row) and the sum (mode 0) runs in edge order over the plan's
+ * snapshots, each edge writing its own row.  No reference counterpart:
  * it replaces the inverse-plan build of the backward ops (mp_ops.cpp:3224-3325
  * take flat_src and dst_idx afresh) for callers that hold the forward's plan. */
 int relm_mp_plan_fanin_backward_by_src(int dtype, const relm_mp_plan* dst_plan, int64_t mode,
