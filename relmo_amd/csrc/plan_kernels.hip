@@ -972,9 +972,9 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
     // has no chunks before it and needs none)
     // The narrowed input goes to the n buffers (the plan's snapshot).  Counted
     // back from the last pass, which writes the plan arrays, the passes write
-    // a and the plan arrays in turn: an earlier pass's output in the plan
-    // arrays is overwritten two passes later, often while its lines are still
-    // in the memory-side cache, so they need not all be written back to HBM.
+    // a and the plan arrays in turn (an earlier pass's output in the plan
+    // arrays is overwritten two passes later), so the sort needs one pair of
+    // scratch buffers.
     const uint32_t* in_k = buf.keys_n;
     const uint32_t* in_v = buf.vals_n;
     int shift = 0;
