@@ -377,6 +377,19 @@ int relm_mp_plan_segment_sum_scaled(int dtype, const relm_mp_plan* plan, const v
                                     const void* base, void* out, void* scratch,
                                     size_t scratch_bytes, relm_mp_stream_t stream);
 
+/* As relm_mp_plan_segment_sum_scaled with RELM_MP_DIV_NONE, but each gathered
+ * row g is divided by its own message count before it is added: out[k] =
+ * base[k] + sum over the segment of table[g] / max(1, msg_div_offsets[g + 1] -
+ * msg_div_offsets[g]), msg_div_offsets the offsets of a CSR plan keyed by the
+ * table's rows (valid for every gathered row).  The transposed mean of the LGAN
+ * aggregations in one pass (mp_ops.cpp:3548-3557: gathered rows divided by
+ * their counts, then index_add_), without the divided copy of the table that
+ * relm_mp_rows_scale would write; the same results bit for bit. */
+int relm_mp_plan_segment_sum_msgdiv(int dtype, const relm_mp_plan* plan, const void* table,
+                                    int64_t emb, const int32_t* msg_div_offsets, const void* base,
+                                    void* out, void* scratch, size_t scratch_bytes,
+                                    relm_mp_stream_t stream);
+
 /* ---- rows in groups (fanout straight into a wider input matrix) ----------- */
 
 /* Grouped row layout: row r of a [rows, emb] operand lies at element offset

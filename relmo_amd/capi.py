@@ -63,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "relm_mp_plan_match",
     "relm_mp_rows_scale",
     "relm_mp_plan_segment_sum_scaled",
+    "relm_mp_plan_segment_sum_msgdiv",
     "relm_mp_plan_gather_last_grouped",
     "relm_mp_plan_segment_sum_grouped",
     "relm_mp_film_mish",
@@ -175,6 +176,7 @@ _SIGNATURES = {
     "relm_mp_plan_match_workspace_size": (_sz, []),
     "relm_mp_rows_scale": (_int, [_int, _vp, _vp, _int, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "relm_mp_plan_segment_sum_scaled": (_int, [_int, _PP, _vp, _i64, _int, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "relm_mp_plan_segment_sum_msgdiv": (_int, [_int, _PP, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "relm_mp_plan_gather_last_grouped": (_int, [_int, _PP, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "relm_mp_plan_segment_sum_grouped": (
         _int, [_int, _PP, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
@@ -503,6 +505,23 @@ def plan_segment_sum_scaled(bp: BuiltPlan, table: torch.Tensor, div_kind: int = 
     check(
         lib().relm_mp_plan_segment_sum_scaled(
             _dtype(table), ctypes.byref(bp.plan), _ptr(table), emb, div_kind, _ptr(div_values),
+            _ptr(base), _ptr(out), _ptr(scratch), scratch.numel(), _stream(table),
+        )
+    )
+    return out
+
+
+def plan_segment_sum_msgdiv(bp: BuiltPlan, table: torch.Tensor, div_plan: BuiltPlan,
+                            base: torch.Tensor | None = None) -> torch.Tensor:
+    """``relm_mp_plan_segment_sum_msgdiv``: each gathered row divided by its count
+    in ``div_plan`` (a CSR plan keyed by the table's rows) before it is added."""
+    emb = table.size(1)
+    out = torch.empty(bp.plan.num_keys, emb, dtype=table.dtype, device=table.device)
+    n = lib().relm_mp_plan_compute_scratch_bytes(ctypes.byref(bp.plan), emb, _dtype(table), 0)
+    scratch = _bytes(n, table)
+    check(
+        lib().relm_mp_plan_segment_sum_msgdiv(
+            _dtype(table), ctypes.byref(bp.plan), _ptr(table), emb, div_plan.plan.offsets,
             _ptr(base), _ptr(out), _ptr(scratch), scratch.numel(), _stream(table),
         )
     )

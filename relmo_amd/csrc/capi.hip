@@ -854,6 +854,20 @@ int relm_mp_plan_segment_sum_scaled(int dtype, const relm_mp_plan* plan, const v
                                       scratch, scratch_bytes, static_cast<hipStream_t>(stream));
 }
 
+int relm_mp_plan_segment_sum_msgdiv(int dtype, const relm_mp_plan* plan, const void* table,
+                                    int64_t emb, const int32_t* msg_div_offsets, const void* base,
+                                    void* out, void* scratch, size_t scratch_bytes,
+                                    relm_mp_stream_t stream) {
+    RELM_TRY(check_dtype(dtype));
+    if (plan == nullptr) return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: plan is NULL");
+    if (emb < 0 || (msg_div_offsets == nullptr && plan->num_keys > 0 && plan->num_edges > 0))
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: bad divided sum arguments");
+    if (base != nullptr && base == out && plan->num_keys > 0 && emb > 0)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: base must not alias out");
+    return compute_segment_sum_msgdiv(dtype, *plan, table, emb, msg_div_offsets, base, out, scratch,
+                                      scratch_bytes, static_cast<hipStream_t>(stream));
+}
+
 int relm_mp_plan_logsumexp_backward(int dtype, const relm_mp_plan* plan, const int64_t* gathers,
                                     const void* grad_out, const void* out, const void* rel_flat,
                                     int64_t emb, void* grad_rel, void* scratch,

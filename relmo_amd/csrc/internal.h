@@ -201,6 +201,9 @@ int compute_segment_sum_scaled(int dtype, const relm_mp_plan& plan, const void* 
                                int64_t emb, int div_kind, const int64_t* div_values,
                                const void* base, void* out, void* scratch, size_t scratch_bytes,
                                hipStream_t s);
+int compute_segment_sum_msgdiv(int dtype, const relm_mp_plan& plan, const void* table, int64_t emb,
+                               const int32_t* msg_div_offsets, const void* base, void* out,
+                               void* scratch, size_t scratch_bytes, hipStream_t s);
 int compute_rows_scale(int dtype, const void* in, const int64_t* gather, int div_kind,
                        const int32_t* div_offsets, const int64_t* div_values, const void* base,
                        int64_t rows, int64_t emb, void* out, hipStream_t s);

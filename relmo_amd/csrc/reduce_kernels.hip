@@ -205,6 +205,36 @@ struct SumOp {
     __device__ __forceinline__ Partial partial() const { return {acc}; }
 };
 
+// Sum of table rows, each divided by its own row's message count before it
+// is added: row g contributes table[g] / d_g, d_g = max(1, div_offsets[g + 1] -
+// div_offsets[g]) (the offsets of a CSR plan keyed by the table's rows).  The
+// transposed mean of the LGAN aggregations, which divide every gathered
+// gradient row by its count and then add (mp_ops.cpp:3548-3557); the counts
+// are loaded with the rows, so no divided copy of the table is written.
+template <typename T, int V, int U>
+struct SumDivOp : SumOp<T, V, U> {
+    const int32_t* __restrict__ div_offsets;
+    T d[U];
+
+    __device__ __forceinline__ void load(const int32_t (&idx)[U], int cnt) {
+        SumOp<T, V, U>::load(idx, cnt);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int32_t n = div_offsets[idx[u] + 1] - div_offsets[idx[u]];
+            d[u] = n > 1 ? static_cast<T>(n) : T(1);
+        }
+    }
+    __device__ __forceinline__ void consume(int cnt) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) add(u, u < cnt);
+    }
+    __device__ __forceinline__ void add(int u, bool valid) {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+            this->acc.v[i] = valid ? this->acc.v[i] + this->x[u].v[i] / d[u] : this->acc.v[i];
+    }
+};
+
 // Logsumexp of table rows as a blocked max-then-sum: per batch the batch
 // maximum first, then exp(x - max) summed against the running maximum (s is
 // kept relative to m and rescaled when m grows).  Semantics of the reference's
@@ -1495,6 +1525,41 @@ int compute_segment_sum_scaled(int dtype, const relm_mp_plan& plan, const void* 
                                               scratch, s)
                : segment_sum_scaled_t<float>(plan, table, emb, div_kind, div_values, base, out,
                                              scratch, s);
+}
+
+template <typename T>
+int segment_sum_msgdiv_t(const relm_mp_plan& plan, const void* table_v, int64_t emb,
+                         const int32_t* msg_div_offsets, const void* base_v, void* out_v,
+                         void* scratch, hipStream_t s) {
+    const T* table = static_cast<const T*>(table_v);
+    const T* base = static_cast<const T*>(base_v);
+    T* out = static_cast<T*>(out_v);
+    T* partial = static_cast<T*>(scratch);
+    const Geometry geo = choose_geometry<T>(emb, {table, base, out, partial});
+    return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
+        constexpr int V = decltype(vt)::value;
+        constexpr int G = decltype(gt)::value;
+        constexpr int U = batch_rows<G>();
+        SumDivOp<T, V, U> op{};
+        op.table = table;
+        op.D = emb;
+        op.div_offsets = msg_div_offsets;
+        const ScaleEpilogue<T> epi{base, RELM_MP_DIV_NONE, plan.offsets, nullptr};
+        return run_csr<T, V, G>(plan, op, geo.slices, partial, out, s, epi);
+    });
+}
+
+int compute_segment_sum_msgdiv(int dtype, const relm_mp_plan& plan, const void* table, int64_t emb,
+                               const int32_t* msg_div_offsets, const void* base, void* out,
+                               void* scratch, size_t scratch_bytes, hipStream_t s) {
+    if (plan.num_keys == 0 || emb == 0) return RELM_MP_OK;
+    if (plan.kind != RELM_MP_PLAN_CSR)
+        return set_error(RELM_MP_ERR_INVALID_ARGUMENT, "relm_mp: divided sums need a CSR plan");
+    if (scratch_bytes < hub_partial_bytes(plan, emb, dtype, RELM_MP_MODE_SUM))
+        return set_error(RELM_MP_ERR_WORKSPACE, "relm_mp: hub scratch too small");
+    return dtype == RELM_MP_F64
+               ? segment_sum_msgdiv_t<double>(plan, table, emb, msg_div_offsets, base, out, scratch, s)
+               : segment_sum_msgdiv_t<float>(plan, table, emb, msg_div_offsets, base, out, scratch, s);
 }
 
 int compute_fill(int dtype, void* out, int64_t count, double value, hipStream_t s) {

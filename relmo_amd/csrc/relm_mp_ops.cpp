@@ -1435,7 +1435,8 @@ std::tuple<Tensor, Tensor, Tensor> fanin_pack_from_edges(
 // finished as they are stored (relm_mp_plan_segment_sum_scaled: division by
 // the count or arity, residual addition); the backward runs the transposed
 // sums over plans keyed by the sources, with the mean's per-message division
-// applied once per gradient row beforehand (relm_mp_rows_scale).  Other
+// applied to each gathered gradient row as it is loaded
+// (relm_mp_plan_segment_sum_msgdiv).  Other
 // tensors: the reference's tensor sequence.
 
 constexpr int64_t kModeMean = 2;
@@ -1532,18 +1533,18 @@ Tensor lgan_reverse_gpu(const Tensor& grad, const Tensor& s, const Tensor& t, in
                                     ptr_or_null(base), src_rows, D, out.data_ptr(), st));
         return out;
     }
-    Tensor table = grad;
-    if (mode == kModeMean) {
-        // message counts per grad row: the segment sizes of the forward's plan
-        PlanPtr fwd = csr_plan(t, grad.size(0), t_name, s, src_rows, s_name, true, st);
-        table = at::empty_like(grad);
-        raise_if(relm_mp_rows_scale(dt, grad.data_ptr(), nullptr, RELM_MP_DIV_SEGMENT,
-                                    fwd->plan.offsets, nullptr, nullptr, grad.size(0), D,
-                                    table.data_ptr(), st));
-    }
     PlanPtr gp = csr_plan(s, src_rows, s_name, t, grad.size(0), t_name, false, st);
     Tensor scratch = compute_scratch(gp->plan, D, dt, kModeSum, grad);
-    raise_if(relm_mp_plan_segment_sum_scaled(dt, &gp->plan, table.data_ptr(), D, RELM_MP_DIV_NONE,
+    if (mode == kModeMean) {
+        // each message's grad row divided by the messages into its row - the
+        // segment sizes of the forward's plan - as it is loaded
+        PlanPtr fwd = csr_plan(t, grad.size(0), t_name, s, src_rows, s_name, true, st);
+        raise_if(relm_mp_plan_segment_sum_msgdiv(dt, &gp->plan, grad.data_ptr(), D, fwd->plan.offsets,
+                                                 ptr_or_null(base), out.data_ptr(), scratch.data_ptr(),
+                                                 static_cast<size_t>(scratch.numel()), st));
+        return out;
+    }
+    raise_if(relm_mp_plan_segment_sum_scaled(dt, &gp->plan, grad.data_ptr(), D, RELM_MP_DIV_NONE,
                                              nullptr, ptr_or_null(base), out.data_ptr(),
                                              scratch.data_ptr(),
                                              static_cast<size_t>(scratch.numel()), st));

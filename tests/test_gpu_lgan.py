@@ -224,3 +224,43 @@ def test_lgan_random_shapes_match_oracle(ops, seed) -> None:
         want_g = lgan_oracle.lgan_pool_reduce_backward(*gr, s2r, arity, *edges, K, mode)
         np.testing.assert_allclose(grad.cpu().numpy(), want_g, rtol=1e-5 if dtype == np.float32 else 1e-12,
                                    atol=1e-5 if dtype == np.float32 else 1e-12)
+
+
+@pytest.mark.parametrize("emb,skew", [(64, False), (6, False), (32, True)])
+def test_divided_sum_equals_scaled_rows_then_sum(emb, skew) -> None:
+    """relm_mp_plan_segment_sum_msgdiv (each gathered row divided by its count as
+    it is loaded) equals the two-pass formulation it replaces - the rows divided
+    by relm_mp_rows_scale, then the plain segment sum - bit for bit, with a base
+    row added, over a skewed index set (hub chunks) and over uniform indices."""
+
+    from relmo_amd import capi
+
+    _log(f"divided sum emb={emb} skew={skew}")
+    rng = np.random.default_rng(7 + emb)
+    src_rows, tgt_rows, n = 3000, 2500, 60_000
+    if skew:
+        t = np.minimum(rng.pareto(0.6, n).astype(np.int64), tgt_rows - 1)
+        s = np.minimum(rng.pareto(0.6, n).astype(np.int64), src_rows - 1)
+    else:
+        t = rng.integers(0, tgt_rows, n)
+        s = rng.integers(0, src_rows, n)
+    tt, st = torch.from_numpy(t).to(DEV), torch.from_numpy(s).to(DEV)
+    grad = torch.from_numpy(rng.standard_normal((tgt_rows, emb)).astype(np.float32)).to(DEV)
+    base = torch.from_numpy(rng.standard_normal((src_rows, emb)).astype(np.float32)).to(DEV)
+    fwd = capi.csr_plan(tt, tgt_rows, st, src_rows)   # keyed by the table's rows: their counts
+    rev = capi.csr_plan(st, src_rows, tt, tgt_rows)   # the transposed sum
+    got = capi.plan_segment_sum_msgdiv(rev, grad, fwd, base)
+    scaled = capi.rows_scale(grad, tgt_rows, emb, grad, div_kind=capi.DIV_SEGMENT, div_offsets=fwd.offsets)
+    want = capi.plan_segment_sum_scaled(rev, scaled, 0, None, base)
+    assert torch.equal(got, want)
+    # float64 truth: within this module's 8 eps32 times the op on the magnitudes
+    # for the uniform sets (a count off by one there moves a term by ~4%); the
+    # skewed set sums ~2e4 messages into one row through 64-message sequential
+    # slices, so its bound is 1e-4 of the magnitudes
+    counts = np.maximum(np.bincount(t, minlength=tgt_rows), 1).astype(np.float64)
+    g64, b64 = grad.double().cpu().numpy(), base.double().cpu().numpy()
+    truth, mag = b64.copy(), np.abs(b64)
+    np.add.at(truth, s, g64[t] / counts[t][:, None])
+    np.add.at(mag, s, np.abs(g64[t]) / counts[t][:, None])
+    tol = 1e-4 if skew else 8 * np.finfo(np.float32).eps
+    assert np.all(np.abs(got.double().cpu().numpy() - truth) <= tol * mag)
