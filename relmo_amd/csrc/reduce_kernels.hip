@@ -999,39 +999,57 @@ __global__ __launch_bounds__(kThreads) void k_touch(const uint4* __restrict__ a,
 // j = gather[r] (or r), d_j = 1, max(1, segment size j of a CSR plan) or
 // max(1, (T)div_values[j]); `in` null reads zeros, `base` null adds nothing.
 // The division and the addition round separately, as the reference's
-// tensor expressions do.
+// tensor expressions do.  Each row group keeps gather_rows_in_flight<T, V>()
+// rows in flight: the gathered indices of its rows are loaded first, then
+// their divisors and rows, without a branch (a row past `rows` reads row 0 of
+// every array - the kernel runs only with rows > 0 - and stores nothing).
 template <typename T, int V, int G>
 __global__ __launch_bounds__(kThreads) void k_rows_scale(
     const T* in, const int64_t* __restrict__ gather, int div_kind,
     const int32_t* __restrict__ div_offsets, const int64_t* __restrict__ div_values,
     const T* base, int64_t rows, int64_t D, T* out) {
     constexpr int R = kThreads / G;
+    constexpr int RU = gather_rows_in_flight<T, V>();
     const int gl = static_cast<int>(threadIdx.x) & (G - 1);
     const int64_t col = static_cast<int64_t>(blockIdx.y) * (G * V) + static_cast<int64_t>(gl) * V;
     if (col >= D) return;
-    for (int64_t r = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / G; r < rows;
-         r += static_cast<int64_t>(gridDim.x) * R) {
-        const int64_t j = gather != nullptr ? gather[r] : r;
-        T d = T(1);
-        if (div_kind == RELM_MP_DIV_SEGMENT) {
-            const int32_t n = div_offsets[j + 1] - div_offsets[j];
-            d = n > 1 ? static_cast<T>(n) : T(1);
-        } else if (div_kind == RELM_MP_DIV_VALUES) {
-            const T v = static_cast<T>(div_values[j]);
-            d = v > T(1) ? v : T(1);
-        }
-        Pack<T, V> x = in != nullptr ? pack_load<T, V>(in + row_offset(j, D) + col)
-                                     : pack_fill<T, V>(T(0));
-        if (div_kind != RELM_MP_DIV_NONE) {
+    const int64_t chunk = static_cast<int64_t>(R) * RU;
+    for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * chunk + threadIdx.x / G; r0 < rows;
+         r0 += static_cast<int64_t>(gridDim.x) * chunk) {
+        int64_t r[RU], j[RU];
 #pragma unroll
-            for (int i = 0; i < V; ++i) x.v[i] = x.v[i] / d;
+        for (int u = 0; u < RU; ++u) {
+            r[u] = r0 + u * R;
+            const int64_t rc = r[u] < rows ? r[u] : 0;
+            j[u] = gather != nullptr ? gather[rc] : rc;
         }
-        if (base != nullptr) {
-            const Pack<T, V> b = pack_load<T, V>(base + r * D + col);
+        T d[RU];
+        Pack<T, V> x[RU], b[RU];
 #pragma unroll
-            for (int i = 0; i < V; ++i) x.v[i] = b.v[i] + x.v[i];
+        for (int u = 0; u < RU; ++u) {
+            d[u] = T(1);
+            if (div_kind == RELM_MP_DIV_SEGMENT) {
+                const int32_t n = div_offsets[j[u] + 1] - div_offsets[j[u]];
+                d[u] = n > 1 ? static_cast<T>(n) : T(1);
+            } else if (div_kind == RELM_MP_DIV_VALUES) {
+                const T v = static_cast<T>(div_values[j[u]]);
+                d[u] = v > T(1) ? v : T(1);
+            }
+            x[u] = in != nullptr ? pack_load<T, V>(in + row_offset(j[u], D) + col) : pack_fill<T, V>(T(0));
+            if (base != nullptr) b[u] = pack_load<T, V>(base + (r[u] < rows ? r[u] : 0) * D + col);
         }
-        pack_store<T, V>(out + r * D + col, x);
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            if (div_kind != RELM_MP_DIV_NONE) {
+#pragma unroll
+                for (int i = 0; i < V; ++i) x[u].v[i] = x[u].v[i] / d[u];
+            }
+            if (base != nullptr) {
+#pragma unroll
+                for (int i = 0; i < V; ++i) x[u].v[i] = b[u].v[i] + x[u].v[i];
+            }
+            if (r[u] < rows) pack_store<T, V>(out + r[u] * D + col, x[u]);
+        }
     }
 }
 
@@ -1587,7 +1605,8 @@ int rows_scale_t(const void* in_v, const int64_t* gather, int div_kind, const in
     return with_geometry<T>(geo, [&](auto vt, auto gt) -> int {
         constexpr int V = decltype(vt)::value;
         constexpr int G = decltype(gt)::value;
-        hipLaunchKernelGGL((k_rows_scale<T, V, G>), row_grid(rows, G, geo.slices), dim3(kThreads),
+        hipLaunchKernelGGL((k_rows_scale<T, V, G>), row_grid(rows, G, geo.slices, gather_rows_in_flight<T, V>()),
+                           dim3(kThreads),
                            0, s, in, gather, div_kind, div_offsets, div_values, base, rows, emb,
                            out);
         return hip_error(hipGetLastError(), "relm_mp row scale kernel");
