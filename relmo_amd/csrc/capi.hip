@@ -130,9 +130,17 @@ struct HostSlot {
     // statistics) to this slot's host status; returns its generation.
     hipError_t publish_status(const DevStatus* st, relm_mp_plan_counts* pc, hipStream_t s,
                               int32_t* gen) {
-        *gen = static_cast<int32_t>(static_cast<uint32_t>(status_issued) + 1u);
-        status_issued = *gen;
+        *gen = next_gen();
         return launch_status_publish(st, status_mapped, pc, status_gen_mapped, *gen, s);
+    }
+    // The target of a publication that a kernel of the caller's makes.
+    StatusPublish publish_target(const DevStatus* st, int32_t* gen) {
+        *gen = next_gen();
+        return StatusPublish{st, status_mapped, status_gen_mapped, *gen};
+    }
+    int32_t next_gen() {
+        status_issued = static_cast<int32_t>(static_cast<uint32_t>(status_issued) + 1u);
+        return status_issued;
     }
 };
 
@@ -474,21 +482,18 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->num_items = plan->num_short = -1;
     const SortZero zero = sort_zero_region(sc.sort, num_edges);
     RELM_HIP(launch_status_init(l.status, s, zero.p, zero.n), "relm_mp status init");
-    // The validation result is final after the first sort pass: publish it
-    // to the host, then enqueue the rest of the build.
+    // The validation result is final after the first sort pass: the pass
+    // behind it publishes it to the host, and the rest of the build is
+    // enqueued before the host waits for it.
     int32_t status_gen = 0;
-    auto mark_validation = [&]() -> hipError_t {
-        if (hs == nullptr) return hipSuccess;
-        return hs->publish_status(l.status, nullptr, s, &status_gen);
-    };
     if (num_edges > 0) {
+        const StatusPublish pub = hs != nullptr ? hs->publish_target(l.status, &status_gen) : StatusPublish{};
         RELM_HIP(sort_by_key(keys, key_bound, gathers, gather_bound, num_edges, sc.sort,
                              reinterpret_cast<uint32_t*>(l.keys_sorted),
-                             reinterpret_cast<uint32_t*>(l.gather_sorted), l.status, s,
-                             mark_validation),
+                             reinterpret_cast<uint32_t*>(l.gather_sorted), l.status, s, pub),
                  "relm_mp radix sort");
-    } else {
-        RELM_HIP(mark_validation(), "relm_mp status copy");
+    } else if (hs != nullptr) {
+        RELM_HIP(hs->publish_status(l.status, nullptr, s, &status_gen), "relm_mp status copy");
     }
     RELM_HIP(launch_offsets_from_sorted(reinterpret_cast<const uint32_t*>(l.keys_sorted), num_edges,
                                         key_bound, l.offsets, s),

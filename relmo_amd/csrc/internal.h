@@ -5,7 +5,6 @@
 
 #include <cstddef>
 #include <cstdint>
-#include <functional>
 #include <string>
 
 #include "relm_mp.h"
@@ -114,12 +113,20 @@ struct SortZero {
     int64_t n;
 };
 SortZero sort_zero_region(const SortBuffers& buf, int64_t n);
-// after_validation (may be null) is called once the first pass is enqueued:
-// from then on, in stream order, `st` holds the validation result.
+// Where a build publishes its validation status to the host (memory mapped
+// for the device; see launch_status_publish).  host == nullptr: nowhere.
+struct StatusPublish {
+    const DevStatus* st = nullptr;
+    DevStatus* host = nullptr;
+    int32_t* host_gen = nullptr;
+    int32_t gen = 0;
+};
+// The status `st` holds the validation result once the first pass has run;
+// the first pass's column scan publishes it as `pub` says.
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,
                        uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s,
-                       const std::function<hipError_t()>& after_validation);
+                       const StatusPublish& pub);
 
 hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
                                       int32_t* offsets, hipStream_t s);

@@ -65,10 +65,13 @@ __global__ void k_status_init(DevStatus* st, uint32_t* __restrict__ clear, int64
 
 // Copies the status to host memory mapped for the device (vector stores),
 // then stores `gen` behind it with a system-scope release: the host polls
-// *host_gen and reads the status once it equals gen.
-__global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __restrict__ host,
-                                 relm_mp_plan_counts* __restrict__ pc, int32_t* __restrict__ host_gen,
-                                 int32_t gen) {
+// *host_gen and reads the status once it equals gen.  Run by one workgroup
+// of a kernel that starts after every update of the status (a kernel
+// boundary behind them).
+__device__ __forceinline__ void publish_status(const DevStatus* __restrict__ st,
+                                               DevStatus* __restrict__ host,
+                                               relm_mp_plan_counts* __restrict__ pc,
+                                               int32_t* __restrict__ host_gen, int32_t gen) {
     constexpr int kWords = static_cast<int>(sizeof(DevStatus) / sizeof(unsigned long long));
     const int i = static_cast<int>(threadIdx.x);
     if (i < kWords)
@@ -81,6 +84,12 @@ __global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __
     __syncthreads();
     if (i == 0 && host_gen != nullptr)
         __hip_atomic_store(host_gen, gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__global__ void k_status_publish(const DevStatus* __restrict__ st, DevStatus* __restrict__ host,
+                                 relm_mp_plan_counts* __restrict__ pc, int32_t* __restrict__ host_gen,
+                                 int32_t gen) {
+    publish_status(st, host, pc, host_gen, gen);
 }
 
 // inv[k] = max e with keys[e] == k.  Every key and gathered index is checked;
@@ -275,7 +284,8 @@ constexpr int kColChunk = kColLanes * kColItems;      // tiles per workgroup
 __global__ __launch_bounds__(kScanThreads) void k_scan_cols(uint32_t* __restrict__ hist,
                                                             int64_t ntiles,
                                                             const uint32_t* __restrict__ chunk_sum,
-                                                            uint32_t* __restrict__ tot) {
+                                                            uint32_t* __restrict__ tot,
+                                                            StatusPublish pub) {
     __shared__ uint32_t part[kColLanes][kColDigits];
     __shared__ uint32_t prior[kColLanes][kColDigits];
     const int dl = static_cast<int>(threadIdx.x) % kColDigits;
@@ -307,6 +317,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_cols(uint32_t* __restrict
         before += v[i];
     }
     if (tl == kColLanes - 1 && c == static_cast<int64_t>(gridDim.y) - 1) tot[d] = before;
+    // The first pass's scan starts behind the validating pass: one workgroup
+    // publishes the validation status to the host (no kernel of its own).
+    if (pub.host != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
+        publish_status(pub.st, pub.host, nullptr, pub.host_gen, pub.gen);
 }
 
 // ---- radix sort ----------------------------------------------------------
@@ -959,7 +973,7 @@ void with_digit_bits(int bits, F&& f) {
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,
                        uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s,
-                       const std::function<hipError_t()>& after_validation) {
+                       const StatusPublish& pub) {
     if (n <= 0) return hipSuccess;
     int bits = 0;
     while (bits < 32 && (1ll << bits) < key_bound) ++bits;
@@ -997,13 +1011,10 @@ hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* ga
         }
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
-        if (p == 0 && after_validation) {
-            err = after_validation();
-            if (err != hipSuccess) return err;
-        }
         const dim3 cgrid(kSortBins / kColDigits, static_cast<unsigned>(col_chunks));
+        const StatusPublish none{};
         hipLaunchKernelGGL(k_scan_cols, cgrid, dim3(kScanThreads), 0, s, buf.hist, nblocks,
-                           static_cast<const uint32_t*>(chunk_sum), digit_tot);
+                           static_cast<const uint32_t*>(chunk_sum), digit_tot, p == 0 ? pub : none);
         err = hipGetLastError();
         if (err != hipSuccess) return err;
         const uint32_t* plain = p == 0 ? static_cast<const uint32_t*>(buf.tile_plain) : nullptr;
