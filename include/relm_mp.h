@@ -192,8 +192,9 @@ typedef struct relm_mp_plan {
     int32_t* inv;            /* inverse: [num_keys] largest edge id per key or -1;
                                 NULL = identity (key k <-> edge k for k < num_edges) */
     int32_t* offsets;        /* CSR: [num_keys + 1] segment offsets            */
-    int32_t* gather_sorted;  /* CSR: [num_edges] gathered row per edge, stable key order */
-    int32_t* keys_sorted;    /* CSR: [num_edges] key per edge, stable key order */
+    int32_t* gather_sorted;  /* CSR: [num_edges] gathered row per edge, stable key order
+                                (the keys in that order are not kept: key k holds
+                                positions offsets[k] .. offsets[k + 1] - 1) */
     int32_t* hub_key;        /* CSR: [num_hubs] key of each hub                */
     int32_t* hub_chunk_base; /* CSR: [num_hubs] first chunk of each hub        */
     int32_t* chunk_hub;      /* CSR: [num_chunks] hub of each chunk            */

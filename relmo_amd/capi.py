@@ -93,7 +93,6 @@ class Plan(ctypes.Structure):
         ("inv", ctypes.c_void_p),
         ("offsets", ctypes.c_void_p),
         ("gather_sorted", ctypes.c_void_p),
-        ("keys_sorted", ctypes.c_void_p),
         ("hub_key", ctypes.c_void_p),
         ("hub_chunk_base", ctypes.c_void_p),
         ("chunk_hub", ctypes.c_void_p),
@@ -405,7 +404,11 @@ class BuiltPlan:
 
     @property
     def keys_sorted(self) -> torch.Tensor:
-        return self._i32(self.plan.keys_sorted, self.plan.num_edges)
+        """The key of each position of ``gather_sorted``, expanded from the
+        offsets (plans keep no sorted keys)."""
+        off = self.offsets
+        keys = torch.arange(self.plan.num_keys, dtype=torch.int32, device=off.device)
+        return torch.repeat_interleave(keys, (off[1:] - off[:-1]).to(torch.int64))
 
     @property
     def item_first(self) -> torch.Tensor:

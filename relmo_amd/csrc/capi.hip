@@ -278,7 +278,6 @@ struct CsrLayout {
     relm_mp_plan_counts* counts;
     int32_t* offsets;
     int32_t* gather_sorted;
-    int32_t* keys_sorted;
     int32_t* hub_key;
     int32_t* hub_chunk_base;
     int32_t* chunk_hub;
@@ -301,7 +300,6 @@ CsrLayout csr_layout(void* mem, int64_t num_keys, int64_t num_edges) {
     l.counts = c.take<relm_mp_plan_counts>(1);
     l.offsets = c.take<int32_t>(static_cast<size_t>(num_keys) + 1);
     l.gather_sorted = c.take<int32_t>(static_cast<size_t>(num_edges));
-    l.keys_sorted = c.take<int32_t>(static_cast<size_t>(num_edges));
     l.hub_key = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.hub_chunk_base = c.take<int32_t>(static_cast<size_t>(max_hubs(num_edges)));
     l.chunk_hub = c.take<int32_t>(static_cast<size_t>(max_chunks(num_edges)));
@@ -464,7 +462,6 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     plan->num_gather = gathers != nullptr ? gather_bound : num_edges;
     plan->offsets = l.offsets;
     plan->gather_sorted = l.gather_sorted;
-    plan->keys_sorted = l.keys_sorted;
     plan->hub_key = l.hub_key;
     plan->hub_chunk_base = l.hub_chunk_base;
     plan->chunk_hub = l.chunk_hub;
@@ -488,16 +485,18 @@ int csr_build(const int64_t* keys, int64_t key_bound, const char* key_name, cons
     int32_t status_gen = 0;
     if (num_edges > 0) {
         const StatusPublish pub = hs != nullptr ? hs->publish_target(l.status, &status_gen) : StatusPublish{};
+        // short_gather is written by the key index after the sort: until
+        // then it holds the sort's intermediate keys
         RELM_HIP(sort_by_key(keys, key_bound, gathers, gather_bound, num_edges, sc.sort,
-                             reinterpret_cast<uint32_t*>(l.keys_sorted),
-                             reinterpret_cast<uint32_t*>(l.gather_sorted), l.status, s, pub),
+                             reinterpret_cast<uint32_t*>(l.short_gather),
+                             reinterpret_cast<uint32_t*>(l.gather_sorted), l.offsets, l.status, s,
+                             pub),
                  "relm_mp radix sort");
-    } else if (hs != nullptr) {
-        RELM_HIP(hs->publish_status(l.status, nullptr, s, &status_gen), "relm_mp status copy");
+    } else {
+        RELM_HIP(launch_fill_i32(l.offsets, key_bound + 1, 0, s), "relm_mp offsets fill");
+        if (hs != nullptr)
+            RELM_HIP(hs->publish_status(l.status, nullptr, s, &status_gen), "relm_mp status copy");
     }
-    RELM_HIP(launch_offsets_from_sorted(reinterpret_cast<const uint32_t*>(l.keys_sorted), num_edges,
-                                        key_bound, l.offsets, s),
-             "relm_mp offsets kernel");
     RELM_HIP(launch_key_index(l.offsets, l.gather_sorted, key_bound, sc.key_index, l.hub_key,
                               l.hub_chunk_base, l.multi_hubs, l.chunk_hub, max_hubs(num_edges),
                               max_chunks(num_edges), l.item_first, l.item_short, l.num_items,

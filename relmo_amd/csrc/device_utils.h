@@ -187,4 +187,28 @@ __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t x, uint32_t* l
     return x + pre;
 }
 
+// Exclusive maximum scan over a block of NT threads (NT a multiple of 64):
+// the maximum of x over the threads before this one, 0 for thread 0.  `lds`
+// holds NT/64 words.
+template <int NT>
+__device__ __forceinline__ uint32_t block_exclusive_max(uint32_t x, uint32_t* lds) {
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = lane_id();
+    uint32_t incl = x;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl = max(incl, y);
+    }
+    if (lane == kWave - 1) lds[wave] = incl;
+    uint32_t ex = __shfl_up(incl, 1, kWave);
+    if (lane == 0) ex = 0;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NT / kWave; ++w)
+        if (w < wave) ex = max(ex, lds[w]);
+    __syncthreads();
+    return ex;
+}
+
 }  // namespace relm_mp

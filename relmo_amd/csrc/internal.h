@@ -90,19 +90,21 @@ hipError_t launch_inv_from_snapshot(const int32_t* snap, const uint32_t* plain, 
                                     int64_t key_bound, int32_t* inv, DevStatus* st, hipStream_t s);
 
 
-// Stable LSD radix sort of (key, value) by key.  The first pass reads the
-// caller's int64 keys / gathers, validates them against the bounds (bad
-// entries are recorded in `st` and replaced by 0) and narrows them to 32 bit
-// into keys_n / vals_n in edge order (a plan keeps these as its snapshot);
-// the scatter passes alternate between the a buffers and the output arrays
-// (the last pass writes the output).
+// Stable LSD radix sort of (key, value) by key into CSR form.  The first pass
+// reads the caller's int64 keys / gathers, validates them against the bounds
+// (bad entries are recorded in `st` and replaced by 0) and narrows them to 32
+// bit into keys_n / vals_n in edge order (a plan keeps these as its snapshot);
+// the scatter passes alternate between the a buffers and (keys_tmp,
+// vals_out).  The last pass writes the values in key order to vals_out and,
+// instead of the sorted keys, offsets[k] = the first sorted position with key
+// >= k (key_bound + 1 entries, offsets[key_bound] = n).
 struct SortBuffers {
     uint32_t* keys_n;
     uint32_t* vals_n;
     uint32_t* tile_plain;  // sort_tiles(n): tiles whose values are the edge ids (vals_n not written)
     uint32_t* keys_a;
     uint32_t* vals_a;
-    uint32_t* hist;        // sort_hist_words(n): per-tile digit counts, digit totals
+    uint32_t* hist;        // sort_hist_words(n): per-tile digit counts and key maxima, totals
 };
 int64_t sort_tiles(int64_t n);
 size_t sort_hist_words(int64_t n);
@@ -123,13 +125,11 @@ struct StatusPublish {
 };
 // The status `st` holds the validation result once the first pass has run;
 // the first pass's column scan publishes it as `pub` says.
+// keys_tmp holds n words, free until the sort ends.
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,
-                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s,
-                       const StatusPublish& pub);
-
-hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
-                                      int32_t* offsets, hipStream_t s);
+                       uint32_t* keys_tmp, uint32_t* vals_out, int32_t* offsets, DevStatus* st,
+                       hipStream_t s, const StatusPublish& pub);
 // Per-key index of a CSR plan (deterministic, hubs in key order): hub list,
 // chunk ranges and chunk -> hub map, walk items (balanced by weight: 1 plus the
 // messages of a non-hub key), the short-segment index (short_off[k] = messages

@@ -548,16 +548,29 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
 // counted in that order, the tile is staged in LDS in digit order and written
 // out in runs per digit.  In the first pass a tile flagged in tile_plain takes
 // the edge ids as its values.  Threads below kSortBins also own one digit each.
+//
+// The last pass (LAST) writes the values and, in place of the sorted keys, the
+// CSR offsets: offsets[k] = the first sorted position with key >= k.  Its input
+// is sorted by the lower digits, so each digit's run within a tile is sorted by
+// the whole key, and the runs follow each other in the output in (digit, tile)
+// order.  An element whose key k exceeds the key p of the element before it in
+// its run writes offsets[p + 1 .. k] = its position, and the last element of
+// the output the offsets behind the largest key (= n).  For the first element
+// of each run the predecessor lies in another tile: the pass records the run's
+// first key and its last key + 1 (0: empty run; with the maximum per column
+// chunk in chunk_last) for k_run_heads.  Every offset has one writer.
 constexpr int kDownThreads = 512;
 constexpr int kDownItems = kSortTile / kDownThreads;
 static_assert(kDownThreads >= kSortBins, "one thread per digit");
 
-template <int BITS>
+template <int BITS, bool LAST>
 __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
     const uint32_t* __restrict__ tile_plain, int64_t n, int shift,
     const uint32_t* __restrict__ hist_scanned, const uint32_t* __restrict__ digit_tot,
-    int64_t nblocks, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
+    int64_t nblocks, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
+    int32_t* __restrict__ offsets, int64_t num_keys, uint32_t* __restrict__ run_first,
+    uint32_t* __restrict__ run_last, uint32_t* __restrict__ chunk_last) {
     constexpr int kWaves = kDownThreads / kWave;
     constexpr int kPerWave = kSortTile / kWaves;
     __shared__ uint32_t wcnt[kWaves][kSortBins];
@@ -649,43 +662,108 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
         }
     }
     __syncthreads();
+    if constexpr (LAST) {
+        if (owns_digit) {
+            const uint32_t first = dstart[dd];
+            const uint32_t last1 = run > 0 ? sk[first + run - 1] + 1u : 0u;
+            run_first[tile * kSortBins + dd] = run > 0 ? sk[first] : 0u;
+            run_last[tile * kSortBins + dd] = last1;
+            if (last1 != 0u) atomicMax(chunk_last + (tile / kColChunk) * kSortBins + dd, last1);
+        }
+    }
     for (int i = static_cast<int>(threadIdx.x); i < count; i += kDownThreads) {
         const uint32_t k = sk[i];
         const uint32_t d = (k >> shift) & dmask;
         const int64_t op = static_cast<int64_t>(gdelta[d]) + i;
         if (op >= 0 && op < n) {
-            keys_out[op] = k;
             vals_out[op] = sv[i];
+            if constexpr (!LAST) {
+                keys_out[op] = k;
+            } else {
+                if (i > 0) {
+                    const uint32_t pk = sk[i - 1];
+                    if (((pk >> shift) & dmask) == d)
+                        for (int64_t kk = static_cast<int64_t>(pk) + 1; kk <= static_cast<int64_t>(k); ++kk)
+                            offsets[kk] = static_cast<int32_t>(op);
+                }
+                if (op == n - 1)
+                    for (int64_t kk = static_cast<int64_t>(k) + 1; kk <= num_keys; ++kk)
+                        offsets[kk] = static_cast<int32_t>(n);
+            }
         }
     }
 }
 
-// offsets[k] = first sorted position with key >= k; offsets[num_keys] = n.
-__global__ __launch_bounds__(kThreads) void k_offsets_from_sorted(const uint32_t* __restrict__ ks,
-                                                                  int64_t n, int64_t num_keys,
-                                                                  int32_t* __restrict__ offsets) {
-    // thread t covers positions [4t, 4t + 4) (one 16-byte load) and writes
-    // offsets[k] = i for every key k in (ks[i - 1], ks[i]]; position n closes
-    // the keys after the last edge.
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; 4 * t <= n;
-         t += stride) {
-        const int64_t i0 = 4 * t;
-        int64_t cur[4];
-        if (i0 + 4 <= n) {
-            const uint4 v = *reinterpret_cast<const uint4*>(ks + i0);
-            cur[0] = v.x; cur[1] = v.y; cur[2] = v.z; cur[3] = v.w;
-        } else {
+// The offsets of the runs' first elements in the last pass (see
+// k_radix_downsweep): the key before the first element of run (tile t, digit
+// d) in the output is the largest key of the runs before it in (digit, tile)
+// order, so offsets[that key + 1 .. first key] = the run's output position.
+// Workgroup (g, c) walks digits [32g, 32g + 32) over the tile chunk c like
+// k_scan_cols, with the prefix maximum of the runs' last keys (+1) over the
+// tiles, the chunk maxima of the chunks before c, and the maximum over the
+// smaller digits; hist / digit_tot are the last pass's scanned counts.
+__global__ __launch_bounds__(kScanThreads) void k_run_heads(
+    const uint32_t* __restrict__ hist_scanned, const uint32_t* __restrict__ digit_tot,
+    const uint32_t* __restrict__ run_first, const uint32_t* __restrict__ run_last,
+    const uint32_t* __restrict__ chunk_last, int64_t ntiles, int64_t nchunks,
+    int32_t* __restrict__ offsets) {
+    static_assert(kScanThreads == kSortBins, "one thread per digit");
+    __shared__ uint32_t dlow[kSortBins];   // largest key + 1 of the smaller digits
+    __shared__ uint32_t dbase[kSortBins];  // first output position of each digit
+    __shared__ uint32_t part[kColLanes][kColDigits];
+    __shared__ uint32_t prior[kColLanes][kColDigits];
+    __shared__ uint32_t scan_lds[kScanThreads / kWave];
+    const int td = static_cast<int>(threadIdx.x);
+    // every load of a group issued before the first is used
+    uint32_t cm = 0;
+    for (int64_t c0 = 0; c0 < nchunks; c0 += 16) {
+        uint32_t m[16];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) cur[j] = i0 + j < n ? static_cast<int64_t>(ks[i0 + j]) : num_keys;
-        }
-        int64_t prev = i0 == 0 ? -1 : static_cast<int64_t>(ks[i0 - 1]);
+        for (int j = 0; j < 16; ++j) m[j] = c0 + j < nchunks ? chunk_last[(c0 + j) * kSortBins + td] : 0u;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (i0 + j > n) break;
-            const int64_t c = cur[j] > num_keys ? num_keys : cur[j];
-            for (int64_t k = prev + 1; k <= c; ++k) offsets[k] = static_cast<int32_t>(i0 + j);
-            prev = c > prev ? c : prev;
+        for (int j = 0; j < 16; ++j) cm = max(cm, m[j]);
+    }
+    const uint32_t tot_d = digit_tot[td];
+    const uint32_t below = block_exclusive_max<kScanThreads>(cm, scan_lds);
+    uint32_t all;
+    const uint32_t dincl = block_inclusive_scan<kScanThreads>(tot_d, scan_lds, all);
+    dlow[td] = below;
+    dbase[td] = dincl - tot_d;
+
+    const int dl = td % kColDigits;
+    const int tl = td / kColDigits;
+    const int64_t d = static_cast<int64_t>(blockIdx.x) * kColDigits + dl;
+    const int64_t c = blockIdx.y;
+    const int64_t t0 = c * kColChunk + static_cast<int64_t>(tl) * kColItems;
+    uint32_t v[kColItems], first[kColItems], pre[kColItems];
+    uint32_t lm = 0, pm = 0;
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) {
+        const bool in = t0 + i < ntiles;
+        const int64_t t = in ? t0 + i : 0;
+        v[i] = in ? run_last[t * kSortBins + d] : 0u;
+        first[i] = run_first[t * kSortBins + d];
+        pre[i] = hist_scanned[t * kSortBins + d];
+    }
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) lm = max(lm, v[i]);
+    for (int64_t cc = tl; cc < c; cc += kColLanes) pm = max(pm, chunk_last[cc * kSortBins + d]);
+    part[tl][dl] = lm;
+    prior[tl][dl] = pm;
+    __syncthreads();
+    uint32_t lo = dlow[d];
+#pragma unroll
+    for (int l = 0; l < kColLanes; ++l) {
+        if (l < tl) lo = max(lo, part[l][dl]);
+        lo = max(lo, prior[l][dl]);
+    }
+    const uint32_t base = dbase[d];
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) {
+        if (v[i] != 0u) {
+            const int32_t pos = static_cast<int32_t>(base + pre[i]);
+            for (int64_t kk = lo; kk <= static_cast<int64_t>(first[i]); ++kk) offsets[kk] = pos;
+            lo = max(lo, v[i]);
         }
     }
 }
@@ -932,22 +1010,37 @@ hipError_t launch_inv_build(const int64_t* keys, int64_t key_bound, const int64_
     return hipGetLastError();
 }
 
-SortZero sort_zero_region(const SortBuffers& buf, int64_t n) {
+// Layout of SortBuffers::hist, in rows of kSortBins words: the per-tile digit
+// counts (nblocks), the digit totals (1), the per-chunk digit sums of every
+// pass and the last pass's per-chunk maxima of its runs' last keys
+// ((kSortMaxPasses + 1) * chunks, zeroed together before the sort), then the
+// last pass's first and last keys of each tile's runs (nblocks each).
+struct HistLayout {
+    int64_t nblocks, chunks;
+    int64_t tot() const { return nblocks; }
+    int64_t chunk_sums(int p) const { return nblocks + 1 + p * chunks; }
+    int64_t chunk_last() const { return nblocks + 1 + kSortMaxPasses * chunks; }
+    int64_t run_first() const { return chunk_last() + chunks; }
+    int64_t run_last() const { return run_first() + nblocks; }
+    int64_t rows() const { return run_last() + nblocks; }
+};
+
+HistLayout hist_layout(int64_t n) {
     const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
-    const int64_t chunks = (nblocks + kColChunk - 1) / kColChunk;
-    if (n <= 0 || chunks <= 1) return {nullptr, 0};
-    return {buf.hist + static_cast<int64_t>(kSortBins) * (nblocks + 1),
-            static_cast<int64_t>(kSortBins) * kSortMaxPasses * chunks};
+    return {nblocks, (nblocks + kColChunk - 1) / kColChunk};
+}
+
+SortZero sort_zero_region(const SortBuffers& buf, int64_t n) {
+    const HistLayout hl = hist_layout(n);
+    if (n <= 0) return {nullptr, 0};
+    return {buf.hist + static_cast<int64_t>(kSortBins) * hl.chunk_sums(0),
+            static_cast<int64_t>(kSortBins) * (kSortMaxPasses + 1) * hl.chunks};
 }
 
 int64_t sort_tiles(int64_t n) { return std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile); }
 
 size_t sort_hist_words(int64_t n) {
-    const int64_t nblocks = std::max<int64_t>(1, (n + kSortTile - 1) / kSortTile);
-    const int64_t chunks = (nblocks + kColChunk - 1) / kColChunk;
-    // per-tile digit counts, the digit totals, the per-chunk digit sums of
-    // every pass (zeroed together before the sort)
-    return static_cast<size_t>(kSortBins) * static_cast<size_t>(nblocks + 1 + kSortMaxPasses * chunks);
+    return static_cast<size_t>(kSortBins) * static_cast<size_t>(hist_layout(n).rows());
 }
 
 namespace {
@@ -968,64 +1061,94 @@ void with_digit_bits(int bits, F&& f) {
     }
 }
 
+// Calls f(std::integral_constant<bool, flag>{}).
+template <class F>
+void with_flag(bool flag, F&& f) {
+    if (flag)
+        f(std::integral_constant<bool, true>{});
+    else
+        f(std::integral_constant<bool, false>{});
+}
+
 }  // namespace
 
 hipError_t sort_by_key(const int64_t* keys, int64_t key_bound, const int64_t* gathers,
                        int64_t gather_bound, int64_t n, const SortBuffers& buf,
-                       uint32_t* keys_out, uint32_t* vals_out, DevStatus* st, hipStream_t s,
-                       const StatusPublish& pub) {
+                       uint32_t* keys_tmp, uint32_t* vals_out, int32_t* offsets, DevStatus* st,
+                       hipStream_t s, const StatusPublish& pub) {
     if (n <= 0) return hipSuccess;
     int bits = 0;
     while (bits < 32 && (1ll << bits) < key_bound) ++bits;
     const int passes = std::max(1, (bits + 7) / 8);
-    const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
-    const int64_t hist_n = static_cast<int64_t>(kSortBins) * nblocks;
-    uint32_t* digit_tot = buf.hist + hist_n;
-    const int64_t col_chunks = (nblocks + kColChunk - 1) / kColChunk;
-    // per pass: the chunk sums (zeroed by launch_status_init; a single chunk
-    // has no chunks before it and needs none)
+    const HistLayout hl = hist_layout(n);
+    const int64_t nblocks = hl.nblocks;
+    uint32_t* const rows = buf.hist;
+    uint32_t* digit_tot = rows + kSortBins * hl.tot();
+    // per-chunk sums (zeroed by launch_status_init; a single chunk has no
+    // chunks before it and needs none)
+    const bool chunked = hl.chunks > 1;
+    uint32_t* chunk_last = rows + kSortBins * hl.chunk_last();
+    uint32_t* run_first = rows + kSortBins * hl.run_first();
+    uint32_t* run_last = rows + kSortBins * hl.run_last();
     // The narrowed input goes to the n buffers (the plan's snapshot).  Counted
-    // back from the last pass, which writes the plan arrays, the passes write
-    // a and the plan arrays in turn (an earlier pass's output in the plan
-    // arrays is overwritten two passes later), so the sort needs one pair of
-    // scratch buffers.
+    // back from the last pass, which writes the plan's values and offsets, the
+    // passes write keys_tmp / vals_out and the a buffers in turn (an earlier
+    // pass's values in vals_out are overwritten two passes later), so the sort
+    // needs one pair of scratch buffers.
     const uint32_t* in_k = buf.keys_n;
     const uint32_t* in_v = buf.vals_n;
     int shift = 0;
     for (int p = 0; p < passes; ++p) {
         const int width = bits / passes + (p < bits % passes ? 1 : 0);
+        const bool last = p == passes - 1;
         const bool to_plan = (passes - 1 - p) % 2 == 0;
-        uint32_t* out_k = to_plan ? keys_out : buf.keys_a;
+        uint32_t* out_k = last ? nullptr : to_plan ? keys_tmp : buf.keys_a;
         uint32_t* out_v = to_plan ? vals_out : buf.vals_a;
         const dim3 grid(static_cast<unsigned>(nblocks)), block(kSortThreads);
-        uint32_t* chunk_sum = col_chunks > 1 ? digit_tot + kSortBins + p * col_chunks * kSortBins : nullptr;
+        uint32_t* chunk_sum = chunked ? rows + kSortBins * hl.chunk_sums(p) : nullptr;
         if (p == 0) {
             hipLaunchKernelGGL(k_radix_narrow, grid, block, 0, s, keys, gathers, n, shift, width,
-                               key_bound, gather_bound, buf.keys_n, buf.vals_n, buf.tile_plain,
-                               buf.hist, chunk_sum, nblocks, st);
+                               key_bound, gather_bound, buf.keys_n, buf.vals_n, buf.tile_plain, rows,
+                               chunk_sum, nblocks, st);
         } else {
             with_digit_bits(width, [&](auto bt) {
-                hipLaunchKernelGGL((k_radix_upsweep<decltype(bt)::value>), grid, block, 0, s, in_k, n,
-                                   shift, buf.hist, chunk_sum, nblocks);
+                hipLaunchKernelGGL((k_radix_upsweep<decltype(bt)::value>), grid, block, 0, s, in_k,
+                                   n, shift, rows, chunk_sum, nblocks);
             });
         }
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
-        const dim3 cgrid(kSortBins / kColDigits, static_cast<unsigned>(col_chunks));
+        const dim3 cgrid(kSortBins / kColDigits, static_cast<unsigned>(hl.chunks));
         const StatusPublish none{};
-        hipLaunchKernelGGL(k_scan_cols, cgrid, dim3(kScanThreads), 0, s, buf.hist, nblocks,
+        hipLaunchKernelGGL(k_scan_cols, cgrid, dim3(kScanThreads), 0, s, rows, nblocks,
                            static_cast<const uint32_t*>(chunk_sum), digit_tot, p == 0 ? pub : none);
         err = hipGetLastError();
         if (err != hipSuccess) return err;
         const uint32_t* plain = p == 0 ? static_cast<const uint32_t*>(buf.tile_plain) : nullptr;
         with_digit_bits(width, [&](auto bt) {
-            hipLaunchKernelGGL((k_radix_downsweep<decltype(bt)::value>), grid, dim3(kDownThreads), 0, s,
-                               in_k, in_v,
-                               plain, n, shift, static_cast<const uint32_t*>(buf.hist),
-                               static_cast<const uint32_t*>(digit_tot), nblocks, out_k, out_v);
+            with_flag(last, [&](auto lt) {
+                hipLaunchKernelGGL((k_radix_downsweep<decltype(bt)::value, decltype(lt)::value>),
+                                   grid, dim3(kDownThreads), 0, s, in_k, in_v, plain, n, shift,
+                                   static_cast<const uint32_t*>(rows),
+                                   static_cast<const uint32_t*>(digit_tot), nblocks, out_k, out_v,
+                                   offsets, key_bound, run_first, run_last, chunk_last);
+            });
         });
         err = hipGetLastError();
         if (err != hipSuccess) return err;
+        if (last) {
+            // digit groups of kColDigits that hold digits of this pass
+            const dim3 hgrid(static_cast<unsigned>(((1 << width) + kColDigits - 1) / kColDigits),
+                             static_cast<unsigned>(hl.chunks));
+            hipLaunchKernelGGL(k_run_heads, hgrid, dim3(kScanThreads), 0, s,
+                               static_cast<const uint32_t*>(rows),
+                               static_cast<const uint32_t*>(digit_tot),
+                               static_cast<const uint32_t*>(run_first),
+                               static_cast<const uint32_t*>(run_last),
+                               static_cast<const uint32_t*>(chunk_last), nblocks, hl.chunks, offsets);
+            err = hipGetLastError();
+            if (err != hipSuccess) return err;
+        }
         in_k = out_k;
         in_v = out_v;
         shift += width;
@@ -1042,13 +1165,6 @@ hipError_t launch_inv_from_snapshot(const int32_t* snap, const uint32_t* plain, 
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_inv_verify, grid, dim3(kThreads), 0, s, snap, plain, n, key_bound,
                        static_cast<const int32_t*>(inv), st);
-    return hipGetLastError();
-}
-
-hipError_t launch_offsets_from_sorted(const uint32_t* keys_sorted, int64_t n, int64_t num_keys,
-                                      int32_t* offsets, hipStream_t s) {
-    hipLaunchKernelGGL(k_offsets_from_sorted, dim3(grid_1d(n / 4 + 1, kThreads)), dim3(kThreads), 0,
-                       s, keys_sorted, n, num_keys, offsets);
     return hipGetLastError();
 }
 
