@@ -573,7 +573,10 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
     uint32_t* __restrict__ run_last, uint32_t* __restrict__ chunk_last) {
     constexpr int kWaves = kDownThreads / kWave;
     constexpr int kPerWave = kSortTile / kWaves;
-    __shared__ uint32_t wcnt[kWaves][kSortBins];
+    constexpr int kDigits = 1 << BITS;
+    // per-wave counts of this pass's digits only: at 7 bits and less the
+    // tile's LDS (39 KB) leaves room for four workgroups per CU
+    __shared__ uint32_t wcnt[kWaves][kDigits];
     __shared__ uint32_t dstart[kSortBins];
     __shared__ int32_t gdelta[kSortBins];  // global start of the digit minus its tile start
     __shared__ uint32_t scan_lds[kDownThreads / kWave];
@@ -594,7 +597,7 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
         tile_prefix = hist_scanned[tile * kSortBins + dd];
         dt = digit_tot[dd];
     }
-    for (int i = dd; i < kWaves * kSortBins; i += kDownThreads) (&wcnt[0][0])[i] = 0;
+    for (int i = dd; i < kWaves * kDigits; i += kDownThreads) (&wcnt[0][0])[i] = 0;
     __syncthreads();
 
     uint32_t key[kDownItems], val[kDownItems], rank[kDownItems];
@@ -605,8 +608,8 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
         const int64_t p = wave_base + r * kWave;
         uint32_t k = 0, v = 0;
         if (p < n) {
-            k = keys[p];
-            v = plain ? static_cast<uint32_t>(p) : vals[p];
+            k = __builtin_nontemporal_load(keys + p);
+            v = plain ? static_cast<uint32_t>(p) : __builtin_nontemporal_load(vals + p);
         }
         key[r] = k;
         val[r] = v;
@@ -627,7 +630,7 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
 
     // Per digit (one thread per digit): exclusive prefix over waves, tile total.
     uint32_t run = 0;
-    if (owns_digit) {
+    if (dd < kDigits) {
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             const uint32_t c = wcnt[w][dd];
