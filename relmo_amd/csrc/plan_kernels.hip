@@ -674,25 +674,45 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
             if (last1 != 0u) atomicMax(chunk_last + (tile / kColChunk) * kSortBins + dd, last1);
         }
     }
-    for (int i = static_cast<int>(threadIdx.x); i < count; i += kDownThreads) {
-        const uint32_t k = sk[i];
+    // Element i of the staged tile goes to output position gdelta[d] + i.
+    auto put = [&](int i, uint32_t k, uint32_t v, uint32_t pk, int32_t gd) {
         const uint32_t d = (k >> shift) & dmask;
-        const int64_t op = static_cast<int64_t>(gdelta[d]) + i;
+        const int64_t op = static_cast<int64_t>(gd) + i;
         if (op >= 0 && op < n) {
-            vals_out[op] = sv[i];
+            vals_out[op] = v;
             if constexpr (!LAST) {
                 keys_out[op] = k;
             } else {
-                if (i > 0) {
-                    const uint32_t pk = sk[i - 1];
-                    if (((pk >> shift) & dmask) == d)
-                        for (int64_t kk = static_cast<int64_t>(pk) + 1; kk <= static_cast<int64_t>(k); ++kk)
-                            offsets[kk] = static_cast<int32_t>(op);
-                }
+                if (i > 0 && ((pk >> shift) & dmask) == d)
+                    for (int64_t kk = static_cast<int64_t>(pk) + 1; kk <= static_cast<int64_t>(k); ++kk)
+                        offsets[kk] = static_cast<int32_t>(op);
                 if (op == n - 1)
                     for (int64_t kk = static_cast<int64_t>(k) + 1; kk <= num_keys; ++kk)
                         offsets[kk] = static_cast<int32_t>(n);
             }
+        }
+    };
+    if (count == kSortTile) {
+        // a full tile: every LDS read of the thread's elements is issued
+        // before the first is used
+        uint32_t ks[kDownItems], vs[kDownItems], ps[kDownItems];
+        int32_t gd[kDownItems];
+#pragma unroll
+        for (int r = 0; r < kDownItems; ++r) {
+            const int i = static_cast<int>(threadIdx.x) + r * kDownThreads;
+            ks[r] = sk[i];
+            vs[r] = sv[i];
+            ps[r] = LAST && i > 0 ? sk[i - 1] : 0u;
+        }
+#pragma unroll
+        for (int r = 0; r < kDownItems; ++r) gd[r] = gdelta[(ks[r] >> shift) & dmask];
+#pragma unroll
+        for (int r = 0; r < kDownItems; ++r)
+            put(static_cast<int>(threadIdx.x) + r * kDownThreads, ks[r], vs[r], ps[r], gd[r]);
+    } else {
+        for (int i = static_cast<int>(threadIdx.x); i < count; i += kDownThreads) {
+            const uint32_t k = sk[i];
+            put(i, k, sv[i], LAST && i > 0 ? sk[i - 1] : 0u, gdelta[(k >> shift) & dmask]);
         }
     }
 }
