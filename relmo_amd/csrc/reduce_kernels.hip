@@ -797,8 +797,7 @@ __device__ __forceinline__ Partial fold_partials(const T* __restrict__ partial, 
 // order), so the result is deterministic.
 template <typename T, int V, int G, class Partial, class Epi>
 __global__ __launch_bounds__(kThreads) void k_hub_combine(
-    const int32_t* __restrict__ offsets, int64_t num_edges, int64_t D,
-    const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
+    int64_t D, const int32_t* __restrict__ hub_key, const int32_t* __restrict__ hub_chunk_base,
     const int32_t* __restrict__ multi_hubs, const relm_mp_plan_counts* __restrict__ pc,
     const T* __restrict__ partial, T* __restrict__ out, Epi epi) {
     constexpr int NG = kThreads / G;
@@ -815,11 +814,12 @@ __global__ __launch_bounds__(kThreads) void k_hub_combine(
         const int64_t h = multi_hubs[bi];
         const bool hok = h >= 0 && h < num_hubs;
         const int64_t key = hok ? hub_key[h] : 0;
-        const int64_t sb = hok ? clamp64(offsets[key], 0, num_edges) : 0;
-        const int64_t se = hok ? clamp64(offsets[key + 1], sb, num_edges) : 0;
-        int64_t nch = (se - sb + kChunkSize - 1) / kChunkSize;
+        // hub slots are in key order and so are their chunks: a hub's chunks
+        // end where the next hub's begin
         const int64_t base = hok ? hub_chunk_base[h] : 0;
-        if (base < 0 || base + nch > num_chunks) nch = 0;
+        const int64_t next = hok && h + 1 < num_hubs ? hub_chunk_base[h + 1] : num_chunks;
+        int64_t nch = next - base;
+        if (base < 0 || nch < 0 || next > num_chunks) nch = 0;
         const int64_t per = (nch + NG - 1) / NG;
         const int64_t lo = clamp64(grp * per, 0, nch);
         const int64_t hi = clamp64(lo + per, lo, nch);
@@ -1364,7 +1364,7 @@ int run_csr(const relm_mp_plan& plan, const Op& op, int64_t slices, T* partial, 
     const void* comb = reinterpret_cast<const void*>(&k_hub_combine<T, V, G, Partial, Epi>);
     hipLaunchKernelGGL((k_hub_combine<T, V, G, Partial, Epi>),
                        persistent_grid(comb, multi, 1, slices, 8), dim3(kThreads), 0, s,
-                       plan.offsets, plan.num_edges, op.D, plan.hub_key, plan.hub_chunk_base,
+                       op.D, plan.hub_key, plan.hub_chunk_base,
                        plan.multi_hubs, plan.counts, static_cast<const T*>(partial), out, epi);
     return hip_error(hipGetLastError(), "relm_mp hub combine kernel");
 }
