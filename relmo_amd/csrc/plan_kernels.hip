@@ -603,28 +603,51 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
     uint32_t key[kDownItems], val[kDownItems], rank[kDownItems];
     const bool plain = tile_plain != nullptr && tile_plain[tile] != 0u;
     const int64_t wave_base = tile_base + wave * kPerWave + lane;
+    // Every tile but a partial last one is full: its loads and ranks need no
+    // bounds (FULL), the last tile's go element by element.
+    auto load_and_rank = [&](auto full_t) {
+        constexpr bool FULL = decltype(full_t)::value;
+        if constexpr (FULL) {
+            const uint32_t* kp = keys + wave_base;
 #pragma unroll
-    for (int r = 0; r < kDownItems; ++r) {
-        const int64_t p = wave_base + r * kWave;
-        uint32_t k = 0, v = 0;
-        if (p < n) {
-            k = __builtin_nontemporal_load(keys + p);
-            v = plain ? static_cast<uint32_t>(p) : __builtin_nontemporal_load(vals + p);
+            for (int r = 0; r < kDownItems; ++r) key[r] = __builtin_nontemporal_load(kp + r * kWave);
+            if (plain) {
+#pragma unroll
+                for (int r = 0; r < kDownItems; ++r) val[r] = static_cast<uint32_t>(wave_base) + r * kWave;
+            } else {
+                const uint32_t* vp = vals + wave_base;
+#pragma unroll
+                for (int r = 0; r < kDownItems; ++r) val[r] = __builtin_nontemporal_load(vp + r * kWave);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < kDownItems; ++r) {
+                const int64_t p = wave_base + r * kWave;
+                uint32_t k = 0, v = 0;
+                if (p < n) {
+                    k = __builtin_nontemporal_load(keys + p);
+                    v = plain ? static_cast<uint32_t>(p) : __builtin_nontemporal_load(vals + p);
+                }
+                key[r] = k;
+                val[r] = v;
+            }
         }
-        key[r] = k;
-        val[r] = v;
-    }
 #pragma unroll
-    for (int r = 0; r < kDownItems; ++r) {
-        const bool active = wave_base + r * kWave < n;
-        const uint32_t d = (key[r] >> shift) & dmask;
-        const unsigned long long peers = match_digit<BITS>(d, __ballot(active));
-        const uint32_t below = __popcll(peers & lanemask_lt());
-        uint32_t before = 0;
-        if (active) before = wcnt[wave][d];
-        rank[r] = before + below;
-        if (active && below == 0) wcnt[wave][d] = before + __popcll(peers);
-    }
+        for (int r = 0; r < kDownItems; ++r) {
+            const bool active = FULL || wave_base + r * kWave < n;
+            const uint32_t d = (key[r] >> shift) & dmask;
+            const unsigned long long peers = match_digit<BITS>(d, FULL ? ~0ull : __ballot(active));
+            const uint32_t below = __popcll(peers & lanemask_lt());
+            uint32_t before = 0;
+            if (active) before = wcnt[wave][d];
+            rank[r] = before + below;
+            if (active && below == 0) wcnt[wave][d] = before + __popcll(peers);
+        }
+    };
+    if (tile_base + kSortTile <= n)
+        load_and_rank(std::integral_constant<bool, true>{});
+    else
+        load_and_rank(std::integral_constant<bool, false>{});
 
     __syncthreads();
 
