@@ -494,7 +494,8 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
     // 4 * (j * 256 + t) + {0..3}); a partial tile element by element, with the
     // elements past n inactive.
     uint32_t key[kSortItems];
-    int valid = kSortItems;
+    uint32_t* wh = h + (static_cast<int>(threadIdx.x) / kWave) * kCountCopies * kStride;
+    uint32_t* mine = wh + (lane_id() & (kCountCopies - 1)) * kStride;
     if (base + kSortTile <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0) {
 #pragma unroll
         for (int j = 0; j < kSortItems / 4; ++j) {
@@ -505,31 +506,41 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_upsweep(const uint32_t* 
             key[4 * j + 2] = v.z;
             key[4 * j + 3] = v.w;
         }
+        __syncthreads();
+        // a full tile: every lane holds kSortItems keys
+#pragma unroll
+        for (int i = 0; i < kSortItems; ++i) {
+            const uint32_t d = (key[i] >> shift) & dmask;
+            const uint32_t d0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(d)));
+            if (__ballot(d != d0) == 0ull) {
+                if (lane_id() == 0) atomicAdd(&wh[d0], static_cast<uint32_t>(kWave));
+            } else {
+                atomicAdd(&mine[d], 1u);
+            }
+        }
     } else {
-        valid = 0;
+        int valid = 0;
 #pragma unroll
         for (int i = 0; i < kSortItems; ++i) {
             const int64_t p = base + static_cast<int64_t>(i) * kSortThreads + threadIdx.x;
             key[i] = p < n ? keys[p] : 0u;
             valid += p < n ? 1 : 0;
         }
-    }
-    __syncthreads();
-    uint32_t* wh = h + (static_cast<int>(threadIdx.x) / kWave) * kCountCopies * kStride;
-    uint32_t* mine = wh + (lane_id() & (kCountCopies - 1)) * kStride;
+        __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        // partial tiles: thread t's valid elements are its first `valid`
-        const bool active = i < valid;
-        const uint32_t d = (key[i] >> shift) & dmask;
-        const unsigned long long act = __ballot(active);
-        if (act == 0ull) continue;  // uniform over the wave
-        const uint32_t d0 = static_cast<uint32_t>(
-            __builtin_amdgcn_readlane(static_cast<int>(d), __builtin_ctzll(act)));
-        if (__ballot(active && d != d0) == 0ull) {
-            if (lane_id() == 0) atomicAdd(&wh[d0], static_cast<uint32_t>(__popcll(act)));
-        } else if (active) {
-            atomicAdd(&mine[d], 1u);
+        for (int i = 0; i < kSortItems; ++i) {
+            // thread t's valid elements are its first `valid`
+            const bool active = i < valid;
+            const uint32_t d = (key[i] >> shift) & dmask;
+            const unsigned long long act = __ballot(active);
+            if (act == 0ull) continue;  // uniform over the wave
+            const uint32_t d0 = static_cast<uint32_t>(
+                __builtin_amdgcn_readlane(static_cast<int>(d), __builtin_ctzll(act)));
+            if (__ballot(active && d != d0) == 0ull) {
+                if (lane_id() == 0) atomicAdd(&wh[d0], static_cast<uint32_t>(__popcll(act)));
+            } else if (active) {
+                atomicAdd(&mine[d], 1u);
+            }
         }
     }
     __syncthreads();
@@ -675,15 +686,26 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
 
     const int64_t rem = n - tile_base;
     const int count = rem < kSortTile ? static_cast<int>(rem) : kSortTile;
+    if (count == kSortTile) {
+        // every element is staged; the mask keeps a position in the tile
 #pragma unroll
-    for (int r = 0; r < kDownItems; ++r) {
-        const int local = wave * kPerWave + r * kWave + lane;
-        if (local < count) {
+        for (int r = 0; r < kDownItems; ++r) {
             const uint32_t d = (key[r] >> shift) & dmask;
-            const uint32_t pos = dstart[d] + wcnt[wave][d] + rank[r];
-            if (pos < static_cast<uint32_t>(count)) {
-                sk[pos] = key[r];
-                sv[pos] = val[r];
+            const uint32_t pos = (dstart[d] + wcnt[wave][d] + rank[r]) & (kSortTile - 1);
+            sk[pos] = key[r];
+            sv[pos] = val[r];
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kDownItems; ++r) {
+            const int local = wave * kPerWave + r * kWave + lane;
+            if (local < count) {
+                const uint32_t d = (key[r] >> shift) & dmask;
+                const uint32_t pos = dstart[d] + wcnt[wave][d] + rank[r];
+                if (pos < static_cast<uint32_t>(count)) {
+                    sk[pos] = key[r];
+                    sv[pos] = val[r];
+                }
             }
         }
     }
@@ -701,7 +723,7 @@ __global__ __launch_bounds__(kDownThreads) void k_radix_downsweep(
     auto put = [&](int i, uint32_t k, uint32_t v, uint32_t pk, int32_t gd) {
         const uint32_t d = (k >> shift) & dmask;
         const int64_t op = static_cast<int64_t>(gd) + i;
-        if (op >= 0 && op < n) {
+        if (static_cast<uint64_t>(op) < static_cast<uint64_t>(n)) {
             vals_out[op] = v;
             if constexpr (!LAST) {
                 keys_out[op] = k;
