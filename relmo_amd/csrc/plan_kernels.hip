@@ -782,6 +782,21 @@ __global__ __launch_bounds__(kScanThreads) void k_run_heads(
     __shared__ uint32_t prior[kColLanes][kColDigits];
     __shared__ uint32_t scan_lds[kScanThreads / kWave];
     const int td = static_cast<int>(threadIdx.x);
+    const int dl = td % kColDigits;
+    const int tl = td / kColDigits;
+    const int64_t d = static_cast<int64_t>(blockIdx.x) * kColDigits + dl;
+    const int64_t c = blockIdx.y;
+    const int64_t t0 = c * kColChunk + static_cast<int64_t>(tl) * kColItems;
+    // this thread's column of runs: loaded before the scans below
+    uint32_t v[kColItems], first[kColItems], pre[kColItems];
+#pragma unroll
+    for (int i = 0; i < kColItems; ++i) {
+        const bool in = t0 + i < ntiles;
+        const int64_t t = in ? t0 + i : 0;
+        v[i] = in ? run_last[t * kSortBins + d] : 0u;
+        first[i] = run_first[t * kSortBins + d];
+        pre[i] = hist_scanned[t * kSortBins + d];
+    }
     // every load of a group issued before the first is used
     uint32_t cm = 0;
     for (int64_t c0 = 0; c0 < nchunks; c0 += 16) {
@@ -798,21 +813,7 @@ __global__ __launch_bounds__(kScanThreads) void k_run_heads(
     dlow[td] = below;
     dbase[td] = dincl - tot_d;
 
-    const int dl = td % kColDigits;
-    const int tl = td / kColDigits;
-    const int64_t d = static_cast<int64_t>(blockIdx.x) * kColDigits + dl;
-    const int64_t c = blockIdx.y;
-    const int64_t t0 = c * kColChunk + static_cast<int64_t>(tl) * kColItems;
-    uint32_t v[kColItems], first[kColItems], pre[kColItems];
     uint32_t lm = 0, pm = 0;
-#pragma unroll
-    for (int i = 0; i < kColItems; ++i) {
-        const bool in = t0 + i < ntiles;
-        const int64_t t = in ? t0 + i : 0;
-        v[i] = in ? run_last[t * kSortBins + d] : 0u;
-        first[i] = run_first[t * kSortBins + d];
-        pre[i] = hist_scanned[t * kSortBins + d];
-    }
 #pragma unroll
     for (int i = 0; i < kColItems; ++i) lm = max(lm, v[i]);
     for (int64_t cc = tl; cc < c; cc += kColLanes) pm = max(pm, chunk_last[cc * kSortBins + d]);
@@ -877,11 +878,12 @@ __global__ __launch_bounds__(kThreads) void k_key_stats(const int32_t* __restric
     __shared__ uint32_t lds[kThreads / kWave];
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
     const KeyFlags f = key_flags(offsets, k, num_keys);
-    uint32_t th, tc, tm, te;
-    block_inclusive_scan<kThreads>(f.hub, lds, th);
+    // hubs and multi-chunk hubs (at most kThreads each) in one scan
+    uint32_t thm, tc, te;
+    block_inclusive_scan<kThreads>(f.hub | f.multi << 16, lds, thm);
     block_inclusive_scan<kThreads>(f.chunks, lds, tc);
-    block_inclusive_scan<kThreads>(f.multi, lds, tm);
     block_inclusive_scan<kThreads>(f.hub_edges, lds, te);
+    const uint32_t th = thm & 0xFFFFu, tm = thm >> 16;
     __shared__ uint32_t wmax[kThreads / kWave];
     uint32_t m = f.deg > 0 ? static_cast<uint32_t>(f.deg) : 0u;
 #pragma unroll
@@ -920,13 +922,21 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     __shared__ int64_t blk_cbase[kThreads];
     __shared__ uint32_t blk_chunks[kThreads];
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    const KeyFlags f = key_flags(offsets, k, num_keys);
-    uint32_t th, tc, tm, te;
-    const uint32_t ih = block_inclusive_scan<kThreads>(f.hub, lds, th);
-    const uint32_t ic = block_inclusive_scan<kThreads>(f.chunks, lds, tc);
-    const uint32_t im = block_inclusive_scan<kThreads>(f.multi, lds, tm);
-    const uint32_t ie = block_inclusive_scan<kThreads>(f.hub_edges, lds, te);
     const int64_t stride = nblk + 1;
+    // the workgroup's prefixes of the scanned rows and the totals do not
+    // depend on this kernel's work: loaded with the offsets
+    const int64_t pre_hub = counts[blockIdx.x];
+    const int64_t pre_chunk = counts[stride + blockIdx.x];
+    const int64_t pre_multi = counts[2 * stride + blockIdx.x];
+    const int64_t pre_edges = counts[3 * stride + blockIdx.x];
+    const uint32_t total_hubs = totals[0];
+    const KeyFlags f = key_flags(offsets, k, num_keys);
+    // hubs and multi-chunk hubs (at most kThreads each) in one scan
+    uint32_t thm, tc, te;
+    const uint32_t ihm = block_inclusive_scan<kThreads>(f.hub | f.multi << 16, lds, thm);
+    const uint32_t ic = block_inclusive_scan<kThreads>(f.chunks, lds, tc);
+    const uint32_t ie = block_inclusive_scan<kThreads>(f.hub_edges, lds, te);
+    const uint32_t ih = ihm & 0xFFFFu, im = ihm >> 16, th = thm & 0xFFFFu;
     if (blockIdx.x == 0) {
         // totals (within the capacities the plan arrays were sized for) and
         // the longest segment into the plan's counts and the status
@@ -960,8 +970,8 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     // hub slot, chunk range; the workgroup fills the chunk -> hub map of its
     // hubs together (a hub can have hundreds of chunks)
     if (f.hub) {
-        const int64_t slot = static_cast<int64_t>(counts[blockIdx.x]) + ih - 1;
-        const int64_t cbase = static_cast<int64_t>(counts[stride + blockIdx.x]) + ic - f.chunks;
+        const int64_t slot = pre_hub + ih - 1;
+        const int64_t cbase = pre_chunk + ic - f.chunks;
         blk_slot[ih - 1] = static_cast<int32_t>(slot);
         blk_cbase[ih - 1] = cbase;
         blk_chunks[ih - 1] = f.chunks;
@@ -969,7 +979,7 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
             hub_key[slot] = static_cast<int32_t>(k);
             hub_chunk_base[slot] = static_cast<int32_t>(cbase);
             if (f.multi) {
-                const int64_t mslot = static_cast<int64_t>(counts[2 * stride + blockIdx.x]) + im - 1;
+                const int64_t mslot = pre_multi + im - 1;
                 if (mslot >= 0 && mslot < hub_capacity) multi_hubs[mslot] = static_cast<int32_t>(slot);
             }
         }
@@ -985,7 +995,7 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     }
     // S[k]: short messages before k; W[k] = k + S[k]
     const bool live = k <= num_keys;
-    const int64_t hub_before = static_cast<int64_t>(counts[3 * stride + blockIdx.x]) + ie - f.hub_edges;
+    const int64_t hub_before = pre_edges + ie - f.hub_edges;
     const int64_t S = live ? static_cast<int64_t>(offsets[k]) - hub_before : 0;
     if (live) {
         const int64_t W = k + S;
@@ -1015,7 +1025,7 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     // it).  The workgroup's keys own one contiguous range of short_gather;
     // its threads copy that range position by position (coalesced), each
     // finding its key among the workgroup's segment starts in LDS.
-    if (totals[0] == 0) return;  // uniform over the grid
+    if (total_hubs == 0) return;  // uniform over the grid
     __shared__ int32_t seg_start[kThreads + 1];
     __shared__ int32_t seg_src[kThreads];
     const bool short_key = live && k < num_keys && f.deg > 0 && f.deg <= kHubThreshold;
