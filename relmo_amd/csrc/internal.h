@@ -49,7 +49,7 @@ static_assert(kSnapTile == kSortTile, "the sort's first pass writes the snapshot
 
 // Scan geometry.
 constexpr int kScanThreads = 256;
-constexpr int kScanItems = 16;
+constexpr int kScanItems = 32;
 constexpr int kScanTile = kScanThreads * kScanItems;
 
 int set_error(int code, const std::string& msg);

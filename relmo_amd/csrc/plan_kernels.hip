@@ -223,10 +223,14 @@ __global__ __launch_bounds__(kThreads) void k_inv_verify(const int32_t* __restri
 // Exclusive scan of every row of a [gridDim.x, len] array in place (one
 // workgroup per row, kScanTile values per step with a running carry);
 // tot[row] receives the row's sum.
+// Thread t's kScanItems consecutive values lie kScanItems + 1 words apart in
+// LDS (padded rows: no two threads of a wave in one bank).
+constexpr int kScanPad = kScanItems + 1;
+
 __global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict__ data,
                                                             int64_t len,
                                                             uint32_t* __restrict__ tot) {
-    __shared__ uint32_t tile[kScanTile];
+    __shared__ uint32_t tile[kScanThreads * kScanPad];
     __shared__ uint32_t lds[kScanThreads / kWave];
     uint32_t* row = data + static_cast<int64_t>(blockIdx.x) * len;
     uint32_t carry = 0;
@@ -238,13 +242,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict
             in[i] = p < len ? row[p] : 0u;
         }
 #pragma unroll
-        for (int i = 0; i < kScanItems; ++i) tile[i * kScanThreads + threadIdx.x] = in[i];
+        for (int i = 0; i < kScanItems; ++i) {
+            const int e = i * kScanThreads + static_cast<int>(threadIdx.x);  // element of the tile
+            tile[(e / kScanItems) * kScanPad + e % kScanItems] = in[i];
+        }
         __syncthreads();
         uint32_t v[kScanItems];
         uint32_t sum = 0;
 #pragma unroll
         for (int i = 0; i < kScanItems; ++i) {
-            v[i] = tile[threadIdx.x * kScanItems + i];
+            v[i] = tile[threadIdx.x * kScanPad + i];
             sum += v[i];
         }
         uint32_t total;
@@ -252,14 +259,15 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_rows(uint32_t* __restrict
         uint32_t run = incl - sum + carry;
 #pragma unroll
         for (int i = 0; i < kScanItems; ++i) {
-            tile[threadIdx.x * kScanItems + i] = run;
+            tile[threadIdx.x * kScanPad + i] = run;
             run += v[i];
         }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < kScanItems; ++i) {
             const int64_t p = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
-            if (p < len) row[p] = tile[i * kScanThreads + threadIdx.x];
+            const int e = i * kScanThreads + static_cast<int>(threadIdx.x);
+            if (p < len) row[p] = tile[(e / kScanItems) * kScanPad + e % kScanItems];
         }
         carry += total;
         __syncthreads();  // tile is rewritten by the next step
