@@ -388,6 +388,14 @@ __device__ __forceinline__ uint32_t narrow_index(int64_t v, int64_t bound, int64
     return ok ? static_cast<uint32_t>(v) : 0u;
 }
 
+// The same check without the edge: `all_ok` clears on a bad index (whose edge
+// is then found again from memory, a path only invalid input takes).
+__device__ __forceinline__ uint32_t narrow_checked(int64_t v, int64_t bound, bool& all_ok) {
+    const bool ok = static_cast<uint64_t>(v) < static_cast<uint64_t>(bound);
+    all_ok = all_ok && ok;
+    return ok ? static_cast<uint32_t>(v) : 0u;
+}
+
 __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
     const int64_t* __restrict__ keys, const int64_t* __restrict__ gathers, int64_t n, int shift,
     int bits, int64_t key_bound, int64_t gather_bound, uint32_t* __restrict__ keys32,
@@ -408,12 +416,13 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
                       ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(gathers)) & 15u) == 0;
     constexpr int kPairs = kSortItems / 2;
     if (full) {
+        bool keys_ok = true, gathers_ok = true;
 #pragma unroll
         for (int i = 0; i < kPairs; ++i) {
             const int64_t p = base + 2 * (static_cast<int64_t>(i) * kSortThreads + threadIdx.x);
             const i64x2 k2 = __builtin_nontemporal_load(reinterpret_cast<const i64x2*>(keys + p));
-            key[2 * i] = narrow_index(k2.x, key_bound, p, bad_k);
-            key[2 * i + 1] = narrow_index(k2.y, key_bound, p + 1, bad_k);
+            key[2 * i] = narrow_checked(k2.x, key_bound, keys_ok);
+            key[2 * i + 1] = narrow_checked(k2.y, key_bound, keys_ok);
             val[2 * i] = val[2 * i + 1] = 0;
         }
         if (gathers != nullptr) {
@@ -422,9 +431,19 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_narrow(
                 const int64_t p = base + 2 * (static_cast<int64_t>(i) * kSortThreads + threadIdx.x);
                 const i64x2 g2 =
                     __builtin_nontemporal_load(reinterpret_cast<const i64x2*>(gathers + p));
-                val[2 * i] = narrow_index(g2.x, gather_bound, p, bad_g);
-                val[2 * i + 1] = narrow_index(g2.y, gather_bound, p + 1, bad_g);
+                val[2 * i] = narrow_checked(g2.x, gather_bound, gathers_ok);
+                val[2 * i + 1] = narrow_checked(g2.y, gather_bound, gathers_ok);
                 mismatch |= (g2.x != p) | (g2.y != p + 1);
+            }
+        }
+        // a bad index: the thread's smallest bad edge, from memory
+        if (!keys_ok || !gathers_ok) {
+            for (int i = 0; i < kPairs; ++i) {
+                const int64_t p = base + 2 * (static_cast<int64_t>(i) * kSortThreads + threadIdx.x);
+                for (int j = 0; j < 2; ++j) {
+                    if (!keys_ok) (void)narrow_index(keys[p + j], key_bound, p + j, bad_k);
+                    if (!gathers_ok) (void)narrow_index(gathers[p + j], gather_bound, p + j, bad_g);
+                }
             }
         }
     } else {

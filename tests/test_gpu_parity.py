@@ -252,6 +252,19 @@ def test_async_csr_plan_computes_before_its_counts_are_read(num_keys: int, num_e
     bad[num_edges // 2] = num_keys
     with pytest.raises((RuntimeError, ValueError), match=rf"key index out of bounds: {num_keys} not in"):
         capi.csr_plan(_t(bad), num_keys, None, num_edges, wait_counts=False)
+    # several bad indices in different sort tiles: the one of the smallest
+    # edge is reported, for the keys and for the gathered indices
+    if num_edges >= 3:
+        bad[num_edges // 3] = num_keys + 5
+        bad[num_edges - 1] = -2
+        with pytest.raises((RuntimeError, ValueError), match=rf"key index out of bounds: {num_keys + 5} not in"):
+            capi.csr_plan(_t(bad), num_keys, None, num_edges)
+        gathers = np.arange(num_edges, dtype=np.int64)
+        gathers[num_edges - 1] = num_edges + 9
+        gathers[num_edges // 2] = -1
+        gathers[num_edges // 3 + 1] = num_edges
+        with pytest.raises((RuntimeError, ValueError), match=rf"gather index out of bounds: {num_edges} not in"):
+            capi.csr_plan(kt, num_keys, _t(gathers), num_edges)
 
 
 @pytest.mark.parametrize("large", [True, False])
