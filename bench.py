@@ -6,7 +6,10 @@ backward through the public API (relmo_amd.mp + autograd) - 1,048,576
 objects, D = 32, 16,777,216 messages ~ N(0, 2^2), Zipf(1.1) destinations.
 One step = forward + backward over the whole batch, with the index plans
 rebuilt in every step (the plan cache is cleared first), so the figure covers
-the whole op call.  value = algorithmic bytes per step / time per step.
+the whole op call.  value = algorithmic bytes per step / time per step, in the
+steady state: the first 20-30 steps of a process run up to 2% slower (the
+same kernels take longer, the backward kernel included), so the default is
+30 untimed warmup steps before the timed ones.
 
 The JSON line also carries
   roofline      - the dominant kernel (logsumexp backward in edge order: flat_src
@@ -965,7 +968,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--only", choices=["c2", "c2sum", "c2perm", "c3", "c1", "c4", "c5", "pack", "lgan", "slots",
                                        "copy"],
                     default=None,
