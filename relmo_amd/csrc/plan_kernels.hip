@@ -1069,6 +1069,51 @@ __global__ __launch_bounds__(kThreads) void k_key_write(
     __syncthreads();
     const int nlive = static_cast<int>(last - static_cast<int64_t>(blockIdx.x) * kThreads + 1);
     const int total = seg_start[kThreads];
+    // Each position's key: up to kLabelCap positions labelled in LDS - every
+    // key with short messages marks its first position, a block-wide running
+    // maximum fills the rest; larger ranges search the segment starts.
+    constexpr int kLabelItems = 16;
+    constexpr int kLabelCap = kThreads * kLabelItems;
+    __shared__ uint16_t lbl[kLabelCap];
+    __shared__ uint32_t lbl_scan[kThreads / kWave];
+    if (total <= kLabelCap) {  // uniform: total is read from LDS
+        const int t0 = static_cast<int>(threadIdx.x) * kLabelItems;
+#pragma unroll
+        for (int i = 0; i < kLabelItems; ++i) lbl[t0 + i] = 0;
+        __syncthreads();
+        // keys with short messages start at distinct positions
+        if (short_key) lbl[S - base] = static_cast<uint16_t>(threadIdx.x);
+        __syncthreads();
+        uint32_t v[kLabelItems];
+        uint32_t run = 0;
+#pragma unroll
+        for (int i = 0; i < kLabelItems; ++i) {
+            v[i] = lbl[t0 + i];
+            run = max(run, v[i]);
+        }
+        uint32_t cur = block_exclusive_max<kThreads>(run, lbl_scan);
+#pragma unroll
+        for (int i = 0; i < kLabelItems; ++i) {
+            cur = max(cur, v[i]);
+            lbl[t0 + i] = static_cast<uint16_t>(cur);
+        }
+        __syncthreads();
+        int32_t val[kLabelItems];
+#pragma unroll
+        for (int i = 0; i < kLabelItems; ++i) {
+            const int j = static_cast<int>(threadIdx.x) + i * kThreads;
+            if (j < total) {
+                const int key = lbl[j];
+                val[i] = gs[static_cast<int64_t>(seg_src[key]) + (j - seg_start[key])];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kLabelItems; ++i) {
+            const int j = static_cast<int>(threadIdx.x) + i * kThreads;
+            if (j < total) short_gather[base + j] = val[i];
+        }
+        return;
+    }
     for (int j = static_cast<int>(threadIdx.x); j < total; j += kThreads) {
         // the last key whose start is <= j (a key of no short messages shares
         // its start with the next key, so the last such key has messages)
